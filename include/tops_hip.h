@@ -1,0 +1,95 @@
+/* tops-hip: C ABI of the MI355X (gfx950) GLA hot path.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t
+ * (passed as void*), enqueues its kernels on that stream and returns
+ * immediately.  Nothing here allocates, frees or synchronises, and no
+ * entry point keeps mutable global state beyond the thread-local error
+ * message, so calls are re-entrant.  Return value: TOPS_OK (0) or a
+ * negative TOPS_ERR_* code; tops_last_error() gives the message.
+ *
+ * Layouts follow the reference API: q, k [B,T,H,K]; v, o, do [B,T,H,V];
+ * per-channel log-gates g [B,T,H,K] (fp32); states [N,H,K,V] (fp32).
+ * Varlen packing (cu_seqlens != NULL) requires B == 1; N = number of
+ * sequences, otherwise N == B.  dtype selects the element type of
+ * q/k/v/o/do and their gradients: TOPS_F32 or TOPS_BF16.
+ *
+ * Each declaration names the reference interface it replaces
+ * (paths relative to the reference repository root).
+ */
+#ifndef TOPS_HIP_H_
+#define TOPS_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TOPS_F32 0
+#define TOPS_BF16 1
+
+#define TOPS_OK 0
+#define TOPS_ERR_NULL -1
+#define TOPS_ERR_SHAPE -2
+#define TOPS_ERR_DTYPE -3
+#define TOPS_ERR_LAUNCH -4
+#define TOPS_ERR_UNSUPPORTED -5
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char* tops_last_error(void);
+/* Library version string. */
+const char* tops_version(void);
+/* Internal: record an error message, return code. */
+int tops_set_error(int code, const char* msg);
+
+/* Bytes of the per-chunk state checkpoint buffer used between forward and
+ * backward: total_chunks * H * K * V * 4. */
+int64_t tops_gla_state_bytes(int total_chunks, int H, int K, int V);
+
+/* Host-side varlen chunk map.  Replaces tops.utils.prepare_chunk_indices
+ * (tops/utils.py:71-90) and the per-sequence chunk counts of
+ * tops/cpu/ops/gla/chunk.py:206-212.  Host pointers.
+ *   cu_seqlens [N+1]; chunk_offsets [N+1] (out; chunk_offsets[N] = total);
+ *   chunk_indices [capacity][2] (out, may be NULL): (sequence id, chunk id).
+ * Returns the total number of chunks, or a negative TOPS_ERR_* code
+ * (empty segments are rejected, as tops/cpu/ops/gla/chunk.py:686 does). */
+int tops_prepare_chunk_indices(const int32_t* cu_seqlens, int N, int C, int32_t* chunk_offsets,
+                               int32_t* chunk_indices, int capacity);
+
+/* Chunked GLA forward (C = 64 tiles).
+ * Replaces tops.ops.gla.chunk_gla_fwd (tops/ops/gla/chunk.py:1103-1199), i.e. the
+ * pallas_calls K1 chunk_cumsum (chunk.py:176), K7 chunk_fwd_h (ops/common/chunk_h.py:243),
+ * K2 fwd_intra_gk (chunk.py:420) and K3 fwd_o_gk (chunk.py:1383).
+ *   h0     [N,H,K,V] fp32 or NULL;  o [B,T,H,V] (dtype);  ht [N,H,K,V] fp32 or NULL
+ *   h_ckpt [total_chunks,H,K,V] fp32 or NULL: state before every chunk (for backward)
+ *   cu_seqlens [N+1] int32 or NULL; chunk_offsets [N+1] int32 (first global chunk of
+ *   each sequence; required with cu_seqlens when h_ckpt is given).
+ * Limits: K <= 128, K % 8 == 0, V % 8 == 0. */
+int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const float* g,
+                       const float* h0, void* o, float* ht, float* h_ckpt,
+                       const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                       int B, int T, int H, int K, int V, int N, int dtype, float scale,
+                       void* stream);
+
+/* Chunked GLA backward.  Replaces tops.ops.gla.chunk_gla_bwd / chunk_gla_bwd_with_pl
+ * (tops/ops/gla/chunk.py:832-1095): K8 chunk_bwd_dh (ops/common/chunk_h.py:864) and the
+ * fused K4 (chunk.py:1556), plus the oracle tops/cpu/ops/gla/chunk.py:469-640.
+ *   h_ckpt   [total_chunks,H,K,V] fp32 from tops_gla_chunk_fwd (state before each chunk)
+ *   dh_work  [total_chunks,H,K,V] fp32 scratch supplied by the caller
+ *   do_      [B,T,H,V] (dtype);  dht [N,H,K,V] fp32 or NULL
+ *   dq, dk [B,T,H,K] (dtype); dv [B,T,H,V] (dtype); dg [B,T,H,K] fp32; dh0 [N,H,K,V] fp32
+ *   or NULL.  chunk_map [total_chunks] int32: sequence id of each global chunk
+ *   (varlen only).  Same limits as the forward, plus V <= 128. */
+int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const float* g,
+                       const void* do_, const float* dht, const float* h_ckpt, float* dh_work,
+                       void* dq, void* dk, void* dv, float* dg, float* dh0,
+                       const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                       const int32_t* chunk_map, int total_chunks,
+                       int B, int T, int H, int K, int V, int N, int dtype, float scale,
+                       void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TOPS_HIP_H_ */

@@ -1,0 +1,97 @@
+"""ctypes binding of libtops_hip.so (the C ABI declared in include/tops_hip.h).
+
+The HIP library is the only compute path: if it is missing, every op raises
+instead of falling back to anything else.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libtops_hip.so")
+
+TOPS_F32 = 0
+TOPS_BF16 = 1
+
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int
+_f32 = ctypes.c_float
+
+# name -> argtypes (every entry point returns int)
+SIGNATURES = {
+    "tops_gla_chunk_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                           _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp],
+    "tops_gla_chunk_bwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                           _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32,
+                           _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp],
+    "tops_prepare_chunk_indices": [_vp, _i32, _i32, _vp, _vp, _i32],
+}
+
+_lib = None
+
+
+class TopsError(RuntimeError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    """Load the native library once; raise loudly when it is absent."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise TopsError(
+                f"tops-hip native library not found at {LIB_PATH}; build it with "
+                "`python pallas-kernel_amd/build.py` (hipcc, gfx950)")
+        L = ctypes.CDLL(LIB_PATH)
+        L.tops_last_error.restype = ctypes.c_char_p
+        L.tops_version.restype = ctypes.c_char_p
+        L.tops_gla_state_bytes.restype = ctypes.c_int64
+        L.tops_gla_state_bytes.argtypes = [_i32, _i32, _i32, _i32]
+        _lib = L
+    return _lib
+
+
+_bound = {}
+
+
+def _fn(name: str):
+    fn = _bound.get(name)
+    if fn is None:
+        fn = getattr(lib(), name)
+        fn.argtypes = SIGNATURES[name]
+        fn.restype = ctypes.c_int
+        _bound[name] = fn
+    return fn
+
+
+def call(name: str, *args) -> None:
+    rc = _fn(name)(*args)
+    if rc != 0:
+        msg = lib().tops_last_error().decode()
+        if rc == -2:
+            raise ValueError(f"{name}: {msg}")
+        raise TopsError(f"{name} failed ({rc}): {msg}")
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.bfloat16:
+        return TOPS_BF16
+    if dt == torch.float32:
+        return TOPS_F32
+    raise TypeError(f"tops-hip kernels take float32 or bfloat16 tensors, got {dt}")
+
+
+def require_cuda(*ts) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise TopsError("tops-hip ops take device (HIP) tensors; got a CPU tensor")

@@ -1,0 +1,10 @@
+"""tops.ops.gla on MI355X (mirrors tops/ops/gla/__init__.py:1-34)."""
+from .chunk import chunk_gla, chunk_gla_fwd, chunk_gla_bwd
+from .fused_chunk import fused_chunk_gla
+
+__all__ = [
+    "chunk_gla",
+    "chunk_gla_fwd",
+    "chunk_gla_bwd",
+    "fused_chunk_gla",
+]

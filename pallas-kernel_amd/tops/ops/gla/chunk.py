@@ -1,0 +1,196 @@
+"""Chunked GLA on MI355X: drop-in for tops.ops.gla.chunk (tops/ops/gla/chunk.py).
+
+`chunk_gla` keeps the reference signature (chunk.py:1207-1218) and is
+differentiable: a torch.autograd.Function wires the fused HIP backward, the
+MI355X counterpart of the custom_vjp the reference lacks for GLA.
+
+Tensors are PyTorch-ROCm device tensors in the reference layout:
+q, k [B,T,H,K]; v [B,T,H,V]; g [B,T,H,K] log-space gates; states [N,H,K,V].
+q/k/v are float32 or bfloat16 (computed with fp32 accumulation; bf16 MFMA
+operands split into hi+lo where a value is not bf16-exact), gates and states
+float32.  `chunk_size` is accepted for signature compatibility: the kernels
+always tile the sequence in chunks of 64, which gives the same result up to
+fp32 rounding for any requested chunk size.
+"""
+from __future__ import annotations
+
+import torch
+
+from ... import _native as N
+from ...utils import ChunkPlan, cdiv, CHUNK
+
+
+def _check(q, k, v, g, initial_state, cu_seqlens):
+    assert q.ndim == 4, f"q must be [B,T,H,K], got {tuple(q.shape)}"
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    assert k.shape == q.shape, f"k shape {tuple(k.shape)} != q shape {tuple(q.shape)}"
+    assert v.shape[:3] == (B, T, H), f"v shape {tuple(v.shape)} incompatible with q"
+    assert g is None or tuple(g.shape) == (B, T, H, K), f"g shape {tuple(g.shape)} != {(B, T, H, K)}"
+    assert q.dtype == k.dtype == v.dtype, "q, k, v must share a dtype"
+    if cu_seqlens is not None:
+        assert B == 1, f"B must be 1 for varlen, got {B}"
+    n = (len(cu_seqlens) - 1) if cu_seqlens is not None else B
+    if initial_state is not None:
+        assert tuple(initial_state.shape) == (n, H, K, V), (
+            f"initial_state shape {tuple(initial_state.shape)} != {(n, H, K, V)}")
+    if K > 128 or K % 8 or V % 8:
+        raise NotImplementedError(f"tops-hip chunk kernels need K <= 128 and K, V multiples of 8 "
+                                  f"(got K={K}, V={V})")
+    N.require_cuda(q, k, v, g, initial_state)
+
+
+def _fwd(q, k, v, g, h0, scale, output_final_state, plan: ChunkPlan, keep_states: bool):
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    o = torch.empty_like(v)
+    ht = torch.empty(plan.N, H, K, V, device=q.device, dtype=torch.float32) \
+        if output_final_state else None
+    hs = torch.empty(plan.total, H, K, V, device=q.device, dtype=torch.float32) \
+        if keep_states else None
+    N.call("tops_gla_chunk_fwd", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(g), N.ptr(h0), N.ptr(o),
+           N.ptr(ht), N.ptr(hs), N.ptr(plan.cu_dev), N.ptr(plan.offsets_dev),
+           B, T, H, K, V, plan.N, N.dtype_code(q.dtype), float(scale), N.stream())
+    return o, ht, hs
+
+
+def _bwd(q, k, v, g, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool):
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    if V > 128:
+        raise NotImplementedError("tops-hip chunk backward needs V <= 128")
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    dg = torch.empty(B, T, H, K, device=q.device, dtype=torch.float32)
+    dh0 = torch.empty(plan.N, H, K, V, device=q.device, dtype=torch.float32) if want_dh0 else None
+    dh_work = torch.empty_like(hs)
+    N.call("tops_gla_chunk_bwd", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(g), N.ptr(do), N.ptr(dht),
+           N.ptr(hs), N.ptr(dh_work), N.ptr(dq), N.ptr(dk), N.ptr(dv), N.ptr(dg), N.ptr(dh0),
+           N.ptr(plan.cu_dev), N.ptr(plan.offsets_dev), N.ptr(plan.chunk_map_dev), plan.total,
+           B, T, H, K, V, plan.N, N.dtype_code(q.dtype), float(scale), N.stream())
+    return dq, dk, dv, dg, dh0
+
+
+class _ChunkGLA(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, g, h0, scale, output_final_state, cu_seqlens):
+        q, k, v = (x.contiguous() for x in (q, k, v))
+        g32 = g.contiguous().to(torch.float32)
+        h032 = None if h0 is None else h0.contiguous().to(torch.float32)
+        plan = ChunkPlan(q.shape[0], q.shape[1], cu_seqlens, q.device)
+        train = any(ctx.needs_input_grad[:5])
+        o, ht, hs = _fwd(q, k, v, g32, h032, scale, output_final_state, plan, keep_states=train)
+        if train:
+            ctx.save_for_backward(q, k, v, g32, hs)
+            ctx.plan, ctx.scale = plan, scale
+            ctx.g_dtype = g.dtype
+            ctx.h0_info = None if h0 is None else h0.dtype
+        return o, ht
+
+    @staticmethod
+    def backward(ctx, do, dht):
+        q, k, v, g32, hs = ctx.saved_tensors
+        do = do.contiguous().to(q.dtype)
+        dht = None if dht is None else dht.contiguous().to(torch.float32)
+        want_dh0 = ctx.h0_info is not None
+        dq, dk, dv, dg, dh0 = _bwd(q, k, v, g32, do, dht, hs, ctx.scale, ctx.plan, want_dh0)
+        if dh0 is not None:
+            dh0 = dh0.to(ctx.h0_info)
+        return dq, dk, dv, dg.to(ctx.g_dtype), dh0, None, None, None
+
+
+def chunk_gla(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor | None = None,
+    g_gamma: torch.Tensor | None = None,
+    scale: float | None = None,
+    initial_state: torch.Tensor | None = None,
+    output_final_state: bool = False,
+    cu_seqlens=None,
+    chunk_size: int = 16,
+):
+    """Chunked GLA (tops/ops/gla/chunk.py:1207-1271).
+
+    Args follow the reference: g [B,T,H,K] per-step log gates, or g_gamma
+    (broadcastable to [B,T,H,K], used only when g is None), else no decay;
+    scale defaults to K^-0.5; initial_state [N,H,K,V]; cu_seqlens [N+1]
+    (host or device ints, B must be 1).
+    Returns (o [B,T,H,V] in q.dtype, final_state [N,H,K,V] fp32 or None).
+    """
+    assert chunk_size > 0, "chunk_size must be positive"
+    B, T, H, K = q.shape
+    if g is None:
+        if g_gamma is not None:
+            g = torch.as_tensor(g_gamma, device=q.device).to(torch.float32).expand(B, T, H, K)
+        else:
+            g = torch.zeros(B, T, H, K, device=q.device, dtype=torch.float32)
+    _check(q, k, v, g, initial_state, cu_seqlens)
+    if scale is None:
+        scale = K ** -0.5
+    o, ht = _ChunkGLA.apply(q, k, v, g, initial_state, float(scale), bool(output_final_state),
+                            cu_seqlens)
+    return o, (ht if output_final_state else None)
+
+
+def chunk_gla_fwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, output_final_state,
+                  cu_seqlens=None, chunk_size: int = 64):
+    """Forward orchestrator (tops/ops/gla/chunk.py:1103-1199).
+
+    Returns (g_cumsum, A, h, ht, o) like the reference.  The fused kernel never
+    materialises the gate cumsum or the intra-chunk matrix, so g_cumsum and A
+    are None (a supplied g_cumsum is not supported); h holds the state before
+    every 64-token chunk, [B, NT, H, K, V] fp32 ([1, total_chunks, ...] varlen).
+    """
+    if g_cumsum is not None:
+        raise NotImplementedError("tops-hip computes the gate cumsum inside the kernel; "
+                                  "pass raw gates g instead of g_cumsum")
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    if g is None:
+        g = (torch.as_tensor(g_gamma, device=q.device).to(torch.float32).expand(B, T, H, K)
+             if g_gamma is not None else torch.zeros(B, T, H, K, device=q.device))
+    _check(q, k, v, g, initial_state, cu_seqlens)
+    plan = ChunkPlan(B, T, cu_seqlens, q.device)
+    g32 = g.contiguous().to(torch.float32)
+    h0 = None if initial_state is None else initial_state.contiguous().to(torch.float32)
+    o, ht, hs = _fwd(q.contiguous(), k.contiguous(), v.contiguous(), g32, h0, scale,
+                     output_final_state, plan, keep_states=True)
+    h = hs.reshape(1 if plan.varlen else B, -1, H, K, V)
+    return None, None, h, ht, o
+
+
+def chunk_gla_bwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, h, A, do, dht,
+                  cu_seqlens=None, chunk_size: int = 64):
+    """Backward orchestrator (tops/ops/gla/chunk.py:832-997).
+
+    Returns (dq, dk, dv, dg, dh0).  `h` may be the state checkpoints returned by
+    chunk_gla_fwd; when None they are recomputed.  A / g_cumsum are not used
+    (the kernels recompute both).  A g_gamma caller gets dg sum-reduced to
+    g_gamma's shape (chunk.py:987-995).  dh0 is returned when initial_state or
+    dht is given (chunk.py:943)."""
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    g_orig = g
+    if g is None:
+        g = (torch.as_tensor(g_gamma, device=q.device).to(torch.float32).expand(B, T, H, K)
+             if g_gamma is not None else torch.zeros(B, T, H, K, device=q.device))
+    _check(q, k, v, g, initial_state, cu_seqlens)
+    plan = ChunkPlan(B, T, cu_seqlens, q.device)
+    q, k, v = (x.contiguous() for x in (q, k, v))
+    g32 = g.contiguous().to(torch.float32)
+    h0 = None if initial_state is None else initial_state.contiguous().to(torch.float32)
+    if h is None:
+        _, _, hs = _fwd(q, k, v, g32, h0, scale, False, plan, keep_states=True)
+    else:
+        hs = h.reshape(plan.total, H, K, V).contiguous().to(torch.float32)
+    want_dh0 = initial_state is not None or dht is not None
+    dq, dk, dv, dg, dh0 = _bwd(q, k, v, g32, do.contiguous().to(q.dtype),
+                               None if dht is None else dht.contiguous().to(torch.float32),
+                               hs, scale, plan, want_dh0)
+    if g_orig is None and g_gamma is not None:
+        gg = torch.as_tensor(g_gamma)
+        dg = dg.sum_to_size(*gg.shape) if gg.dim() > 0 else dg.sum()
+    return dq, dk, dv, dg, dh0

@@ -1,0 +1,30 @@
+"""Seeded synthetic inputs (NumPy PCG64, machine-independent)."""
+import numpy as np
+
+
+def logsigmoid(x):
+    return -np.logaddexp(0.0, -x)
+
+
+def gla_inputs(B, T, H, K, V, seed, gate_div=16.0, h0=False, N=None, dtype=np.float32,
+               grads=False):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    q = rng.standard_normal((B, T, H, K)).astype(np.float32)
+    k = rng.standard_normal((B, T, H, K)).astype(np.float32)
+    v = rng.standard_normal((B, T, H, V)).astype(np.float32)
+    g = (logsigmoid(rng.standard_normal((B, T, H, K))) / gate_div).astype(np.float32)
+    d = dict(q=q, k=k, v=v, g=g)
+    n0 = B if N is None else N
+    d["h0"] = (0.1 * rng.standard_normal((n0, H, K, V))).astype(np.float32) if h0 else None
+    if grads:
+        d["do"] = rng.standard_normal((B, T, H, V)).astype(np.float32)
+        d["dht"] = (0.1 * rng.standard_normal((n0, H, K, V))).astype(np.float32)
+    return d
+
+
+def bf16_round(x):
+    """Round-to-nearest-even float32 -> bfloat16 values, returned as float32."""
+    x = np.ascontiguousarray(x, np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
