@@ -1,0 +1,183 @@
+"""Headline benchmark: chunk_gla forward + backward at B=8, T=4096, H=16, K=V=128, bf16.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+One step = tops.ops.gla.chunk_gla forward (o, final state) plus its backward
+(dq, dk, dv, dg, dh0) through torch autograd, on synthetic inputs already resident
+in HBM (q, k, v, dO ~ N(0,1) bf16; g = logsigmoid(N(0,1))/16 fp32; h0, dht ~
+N(0, 0.1^2) fp32).  Prints ONE JSON line with the throughput (tokens/s, tokens =
+B*T per step), the roofline of the dominant kernel timed live with HIP events on
+the stream the kernels run on, and a CPU baseline: the float64 NumPy oracle on a
+bounded sample of the same workload on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "pallas-kernel_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+B, T, H, K, V, C = 8, 4096, 16, 128, 128, 64
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_BF16_PEAK_TFS = 2500.0    # MI355X dense bf16 MFMA
+METRIC = "chunk_gla fwd+bwd tokens/s (B8,T4096,H16,D128 bf16); % MFMA/HBM peak"
+
+# Algorithmic HBM bytes per launch of each kernel at this config (bf16 q/k/v/o/do and
+# their gradients, fp32 gates, gate gradient and states; nothing intermediate counted).
+_TH = B * T * H
+_S = B * H * K * V * 4
+KERNELS = {
+    # q, k, v, g read; o written; h0 read; ht written
+    "tops_gla_chunk_fwd": dict(kernel="gla_fwd_kernel",
+                               bytes=_TH * (2 * K + 2 * K + 2 * V + 4 * K + 2 * V) + 2 * _S),
+    # q, k, g, dO read; dv written; dht read; dh0 written
+    "tops_gla_chunk_bwd_dh": dict(kernel="gla_bwd_rev_kernel",
+                                  bytes=_TH * (2 * K + 2 * K + 4 * K + 2 * V + 2 * V) + 2 * _S),
+    # q, k, v, g, dO read; dq, dk, dg written
+    "tops_gla_chunk_bwd_dqkg": dict(kernel="gla_bwd_main_kernel",
+                                    bytes=_TH * (2 * K + 2 * K + 2 * V + 4 * K + 2 * V
+                                                 + 2 * K + 2 * K + 4 * K)),
+}
+# Whole-path minimum (each tensor read once per pass, written once): 2 323 644 416 B and
+# 294 912 flop per token-head (fwd 4KV+2CK+2CV, bwd twice that).
+PATH_BYTES = 2_323_644_416
+PATH_FLOPS = _TH * (3 * (4 * K * V + 2 * C * K + 2 * C * V))
+
+
+def make_inputs(device, seed=1003):
+    import torch
+    gen = torch.Generator(device=device).manual_seed(seed)
+
+    def n(*shape, std=1.0):
+        return torch.randn(*shape, generator=gen, device=device, dtype=torch.float32) * std
+
+    bf = torch.bfloat16
+    q = n(B, T, H, K).to(bf).requires_grad_()
+    k = n(B, T, H, K).to(bf).requires_grad_()
+    v = n(B, T, H, V).to(bf).requires_grad_()
+    g = (torch.nn.functional.logsigmoid(n(B, T, H, K)) / 16).requires_grad_()
+    h0 = n(B, H, K, V, std=0.1).requires_grad_()
+    do = n(B, T, H, V).to(bf)
+    dht = n(B, H, K, V, std=0.1)
+    return q, k, v, g, h0, do, dht
+
+
+def cpu_baseline(repeats=3, heads=4):
+    """The float64 oracle (a restatement of the reference's tops/cpu, test infrastructure)
+    on a bounded sample: B=1, T=4096, `heads` heads, K=V=128, forward + backward, one
+    thread.  Returns tokens/s scaled to the full 16-head config."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from oracle import gla as O
+    from _inputs import gla_inputs
+    d = gla_inputs(1, T, heads, K, V, seed=1003, gate_div=16.0, h0=True, grads=True)
+    times = []
+    with threadpool_limits(1):
+        for _ in range(repeats):
+            t0 = time.perf_counter()
+            O.chunk_gla(d["q"], d["k"], d["v"], d["g"], initial_state=d["h0"],
+                        output_final_state=True, chunk_size=C)
+            O.chunk_gla_bwd(d["q"], d["k"], d["v"], d["g"], K ** -0.5, d["h0"], d["do"], d["dht"],
+                            chunk_size=C)
+            times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": round(T * heads / H / med, 1), "unit": "tokens/s", "cores": 1,
+            "kind": "port",
+            "sample": f"float64 NumPy oracle, chunk_gla fwd+bwd on B=1,T={T},H={heads},K=V={K} "
+                      f"(1/{B * H // heads} of one step), median of {repeats}, 1 thread; "
+                      f"tokens/s scaled to H={H}"}
+
+
+def traffic_from_profiles(kernel):
+    """HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+    (calibrated against a copy kernel), if the committed summary holds the kernel."""
+    path = os.path.join(ROOT, "profiles", "traffic_chunk_gla_config3.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["kernels"][kernel]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the GLA hot path shards over (batch, head) "
+              "with no communication, so a multi-GPU figure adds nothing here; run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from tops import _native as NT
+    from tops.ops.gla import chunk_gla
+    dev = torch.device("cuda:0")
+    NT.lib()
+    q, k, v, g, h0, do, dht = make_inputs(dev)
+    ins = (q, k, v, g, h0)
+
+    def step():
+        o, ht = chunk_gla(q, k, v, g, initial_state=h0, output_final_state=True)
+        return torch.autograd.grad((o, ht), ins, (do, dht))
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    NT.enable_timing(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ev = NT.timing_events()
+    NT.enable_timing(False)
+    elapsed = t1 - t0
+    ms_step = elapsed * 1e3 / a.steps
+    value = B * T * a.steps / elapsed
+
+    kern = {}
+    for name, info in KERNELS.items():
+        ms = [e0.elapsed_time(e1) for e0, e1 in ev.get(name, [])]
+        if not ms:
+            continue
+        avg = sum(ms) / len(ms)
+        kern[name] = dict(kernel=info["kernel"], avg_ms=round(avg, 4), launches=len(ms),
+                          algo_bytes=info["bytes"],
+                          achieved_gbs=round(info["bytes"] / (avg * 1e-3) / 1e9, 1))
+    dom = max(kern, key=lambda n: kern[n]["avg_ms"])
+    dk = kern[dom]
+    roofline = {"bound": "hbm", "achieved": dk["achieved_gbs"], "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(dk["achieved_gbs"] / HBM_PEAK_GBS, 4),
+                "traffic": traffic_from_profiles(dk["kernel"]), "kernel": dk["kernel"],
+                "avg_ms": dk["avg_ms"], "algo_bytes_per_launch": dk["algo_bytes"]}
+    t_floor = PATH_BYTES / (HBM_PEAK_GBS * 1e9)
+    path = {"algo_bytes": PATH_BYTES, "algo_flops": PATH_FLOPS,
+            "hbm_floor_ms": round(t_floor * 1e3, 4),
+            "frac_of_roofline": round(t_floor / (ms_step * 1e-3), 4),
+            "mfma_frac": round(PATH_FLOPS / (ms_step * 1e-3) / (MFMA_BF16_PEAK_TFS * 1e12), 4)}
+    out = {"metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1,
+           "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_step, 4),
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+           "data": "synthetic",
+           "config": {"workload": "chunk_gla fwd+bwd (BASELINE config 3)", "B": B, "T": T,
+                      "H": H, "K": K, "V": V, "chunk": C, "h0": True, "dht": True},
+           "roofline": roofline, "path_roofline": path, "kernels": kern,
+           "cpu_baseline": None if a.no_cpu else cpu_baseline()}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

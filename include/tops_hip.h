@@ -88,6 +88,26 @@ int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const float*
                        int B, int T, int H, int K, int V, int N, int dtype, float scale,
                        void* stream);
 
+/* The two stages of tops_gla_chunk_bwd, callable separately (same arguments and limits).
+ * Stage 1 replaces K8 chunk_bwd_dh (tops/ops/common/chunk_h.py:790-878) together with the
+ * dv part of K4 (tops/ops/gla/chunk.py:1447-1509): a reverse sweep over the chunks of every
+ * (sequence, head) writing dh_work (dL/d(state after each chunk)), dv and dh0.
+ * Stage 2 replaces the dq/dk/dg part of K4 (chunk.py:1447-1581) and the oracle's
+ * chunk_gla_bwd_dqkg (tops/cpu/ops/gla/chunk.py:396-466): chunk-parallel, reading the
+ * forward checkpoints h_ckpt and the stage-1 dh_work. */
+int tops_gla_chunk_bwd_dh(const void* q, const void* k, const float* g, const void* do_,
+                          const float* dht, float* dh_work, void* dv, float* dh0,
+                          const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                          int B, int T, int H, int K, int V, int N, int dtype, float scale,
+                          void* stream);
+int tops_gla_chunk_bwd_dqkg(const void* q, const void* k, const void* v, const float* g,
+                            const void* do_, const float* h_ckpt, const float* dh_work,
+                            void* dq, void* dk, float* dg,
+                            const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                            const int32_t* chunk_map, int total_chunks,
+                            int B, int T, int H, int K, int V, int N, int dtype, float scale,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,6 +18,8 @@
 //        dk   = 2^(Gm-G)  (dA^T q~        + v (2^(Gamma-Gm) dh_c)^T)
 //        dg   = revcumsum_t(q dq - k dk) + 2^Gamma sum_v(h_c dh_c) + sum_t k dk_inter
 //    (the gate gradient of tops/cpu/ops/gla/chunk.py:396-466).
+#include <stdio.h>
+
 #include "tops_common.h"
 #include "tops_hip.h"
 
@@ -42,14 +44,6 @@ struct GlaBwdParams {
   const int* chunk_map;
   int total, B, T, H, K, V, N, NV;
   float scale;
-};
-
-// Cooperative load + in-chunk cumsum of the gates for a [C][KP] tile.
-// Every thread owns RPS rows x 2 columns; returns G (log2 units) in ga and
-// Gamma / Gm for the thread's two columns.  Writes sGam/sGm (KP) for all columns.
-template <int KP>
-struct GateTile {
-  static constexpr int NCP = KP / 2, NRS = 256 / NCP, RPS = kChunk / NRS;
 };
 
 template <typename TIn, int KP>
@@ -695,12 +689,16 @@ static hipError_t launch_main(const GlaBwdParams& p, hipStream_t s) {
 }
 
 template <typename TIn>
-static hipError_t launch_bwd(const GlaBwdParams& p, hipStream_t s) {
+static hipError_t launch_rev_t(const GlaBwdParams& p, hipStream_t s) {
+  const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
+  return kp == 32 ? launch_rev<TIn, 32>(p, s)
+       : kp == 64 ? launch_rev<TIn, 64>(p, s) : launch_rev<TIn, 128>(p, s);
+}
+
+template <typename TIn>
+static hipError_t launch_main_t(const GlaBwdParams& p, hipStream_t s) {
   const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
   const int vp = p.V <= 32 ? 32 : (p.V <= 64 ? 64 : 128);
-  hipError_t e = kp == 32 ? launch_rev<TIn, 32>(p, s)
-               : kp == 64 ? launch_rev<TIn, 64>(p, s) : launch_rev<TIn, 128>(p, s);
-  if (e != hipSuccess) return e;
 #define TOPS_MAIN(KPV, VPV) if (kp == KPV && vp == VPV) return launch_main<TIn, KPV, VPV>(p, s);
   TOPS_MAIN(32, 32) TOPS_MAIN(32, 64) TOPS_MAIN(32, 128)
   TOPS_MAIN(64, 32) TOPS_MAIN(64, 64) TOPS_MAIN(64, 128)
@@ -709,9 +707,84 @@ static hipError_t launch_bwd(const GlaBwdParams& p, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
+// Shape checks shared by the backward entry points; returns TOPS_OK or an error code.
+static int check_bwd(const char* who, int B, int T, int H, int K, int V, int N, int total_chunks,
+                     const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                     const int32_t* chunk_map, bool need_map, int dtype) {
+  char msg[160];
+  if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || N <= 0) {
+    snprintf(msg, sizeof(msg), "%s: non-positive dimension", who);
+    return tops_set_error(TOPS_ERR_SHAPE, msg);
+  }
+  if (K > 128 || V > 128 || (K % 8) || (V % 8)) {
+    snprintf(msg, sizeof(msg), "%s: need K, V <= 128 and multiples of 8", who);
+    return tops_set_error(TOPS_ERR_SHAPE, msg);
+  }
+  if (cu_seqlens && (B != 1 || !chunk_offsets || (need_map && !chunk_map))) {
+    snprintf(msg, sizeof(msg), "%s: varlen needs B == 1, chunk_offsets and chunk_map", who);
+    return tops_set_error(TOPS_ERR_SHAPE, msg);
+  }
+  if (!cu_seqlens && N != B) {
+    snprintf(msg, sizeof(msg), "%s: N must equal B", who);
+    return tops_set_error(TOPS_ERR_SHAPE, msg);
+  }
+  if (!cu_seqlens && need_map && total_chunks != B * ((T + kChunk - 1) / kChunk)) {
+    snprintf(msg, sizeof(msg), "%s: total_chunks must be B*ceil(T/64)", who);
+    return tops_set_error(TOPS_ERR_SHAPE, msg);
+  }
+  if (need_map && total_chunks <= 0) {
+    snprintf(msg, sizeof(msg), "%s: total_chunks must be positive", who);
+    return tops_set_error(TOPS_ERR_SHAPE, msg);
+  }
+  if (dtype != TOPS_BF16 && dtype != TOPS_F32) {
+    snprintf(msg, sizeof(msg), "%s: dtype must be TOPS_F32 or TOPS_BF16", who);
+    return tops_set_error(TOPS_ERR_DTYPE, msg);
+  }
+  return TOPS_OK;
+}
+
 }  // namespace tops
 
 using namespace tops;
+
+extern "C" int tops_gla_chunk_bwd_dh(const void* q, const void* k, const float* g,
+                                     const void* do_, const float* dht, float* dh_work, void* dv,
+                                     float* dh0, const int32_t* cu_seqlens,
+                                     const int32_t* chunk_offsets, int B, int T, int H, int K,
+                                     int V, int N, int dtype, float scale, void* stream) {
+  if (!q || !k || !g || !do_ || !dh_work || !dv)
+    return tops_set_error(TOPS_ERR_NULL, "gla_chunk_bwd_dh: null tensor");
+  int rc = check_bwd("gla_chunk_bwd_dh", B, T, H, K, V, N, 0, cu_seqlens, chunk_offsets, nullptr,
+                     false, dtype);
+  if (rc != TOPS_OK) return rc;
+  GlaBwdParams p{q, k, nullptr, g, do_, dht, nullptr, dh_work, nullptr, nullptr, dv, nullptr, dh0,
+                 cu_seqlens, chunk_offsets, nullptr, 0,
+                 B, T, H, K, V, N, (V + 63) / 64, scale};
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = dtype == TOPS_BF16 ? launch_rev_t<uint16_t>(p, s) : launch_rev_t<float>(p, s);
+  if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
+  return TOPS_OK;
+}
+
+extern "C" int tops_gla_chunk_bwd_dqkg(const void* q, const void* k, const void* v, const float* g,
+                                       const void* do_, const float* h_ckpt, const float* dh_work,
+                                       void* dq, void* dk, float* dg, const int32_t* cu_seqlens,
+                                       const int32_t* chunk_offsets, const int32_t* chunk_map,
+                                       int total_chunks, int B, int T, int H, int K, int V, int N,
+                                       int dtype, float scale, void* stream) {
+  if (!q || !k || !v || !g || !do_ || !h_ckpt || !dh_work || !dq || !dk || !dg)
+    return tops_set_error(TOPS_ERR_NULL, "gla_chunk_bwd_dqkg: null tensor");
+  int rc = check_bwd("gla_chunk_bwd_dqkg", B, T, H, K, V, N, total_chunks, cu_seqlens,
+                     chunk_offsets, chunk_map, true, dtype);
+  if (rc != TOPS_OK) return rc;
+  GlaBwdParams p{q, k, v, g, do_, nullptr, h_ckpt, const_cast<float*>(dh_work), dq, dk, nullptr,
+                 dg, nullptr, cu_seqlens, chunk_offsets, chunk_map, total_chunks,
+                 B, T, H, K, V, N, (V + 63) / 64, scale};
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = dtype == TOPS_BF16 ? launch_main_t<uint16_t>(p, s) : launch_main_t<float>(p, s);
+  if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
+  return TOPS_OK;
+}
 
 extern "C" int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const float* g,
                                   const void* do_, const float* dht, const float* h_ckpt,
@@ -720,24 +793,15 @@ extern "C" int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, c
                                   const int32_t* chunk_offsets, const int32_t* chunk_map,
                                   int total_chunks, int B, int T, int H, int K, int V, int N,
                                   int dtype, float scale, void* stream) {
-  if (!q || !k || !v || !g || !do_ || !h_ckpt || !dh_work || !dq || !dk || !dv || !dg)
+  if (!v || !h_ckpt || !dq || !dk || !dg)
     return tops_set_error(TOPS_ERR_NULL, "gla_chunk_bwd: null tensor");
-  if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || N <= 0 || total_chunks <= 0)
-    return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_bwd: non-positive dimension");
-  if (K > 128 || V > 128 || (K % 8) || (V % 8))
-    return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_bwd: need K, V <= 128 and multiples of 8");
-  if (cu_seqlens && (B != 1 || !chunk_offsets || !chunk_map))
-    return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_bwd: varlen needs B == 1, chunk_offsets, chunk_map");
-  if (!cu_seqlens && (N != B || total_chunks != B * ((T + kChunk - 1) / kChunk)))
-    return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_bwd: N must equal B and total_chunks B*ceil(T/64)");
-  GlaBwdParams p{q, k, v, g, do_, dht, h_ckpt, dh_work, dq, dk, dv, dg, dh0,
-                 cu_seqlens, chunk_offsets, chunk_map, total_chunks,
-                 B, T, H, K, V, N, (V + 63) / 64, scale};
-  hipStream_t s = (hipStream_t)stream;
-  hipError_t e;
-  if (dtype == TOPS_BF16) e = launch_bwd<uint16_t>(p, s);
-  else if (dtype == TOPS_F32) e = launch_bwd<float>(p, s);
-  else return tops_set_error(TOPS_ERR_DTYPE, "gla_chunk_bwd: dtype must be TOPS_F32 or TOPS_BF16");
-  if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
-  return TOPS_OK;
+  int rc = check_bwd("gla_chunk_bwd", B, T, H, K, V, N, total_chunks, cu_seqlens, chunk_offsets,
+                     chunk_map, true, dtype);
+  if (rc != TOPS_OK) return rc;
+  rc = tops_gla_chunk_bwd_dh(q, k, g, do_, dht, dh_work, dv, dh0, cu_seqlens, chunk_offsets,
+                             B, T, H, K, V, N, dtype, scale, stream);
+  if (rc != TOPS_OK) return rc;
+  return tops_gla_chunk_bwd_dqkg(q, k, v, g, do_, h_ckpt, dh_work, dq, dk, dg, cu_seqlens,
+                                 chunk_offsets, chunk_map, total_chunks, B, T, H, K, V, N, dtype,
+                                 scale, stream);
 }

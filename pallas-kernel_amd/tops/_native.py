@@ -26,6 +26,11 @@ SIGNATURES = {
     "tops_gla_chunk_bwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                            _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32,
                            _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp],
+    "tops_gla_chunk_bwd_dh": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                              _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp],
+    "tops_gla_chunk_bwd_dqkg": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                _vp, _vp, _vp, _i32,
+                                _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp],
     "tops_prepare_chunk_indices": [_vp, _i32, _i32, _vp, _vp, _i32],
 }
 
@@ -66,8 +71,31 @@ def _fn(name: str):
     return fn
 
 
+# Optional per-entry-point timing: when enabled, every call() is bracketed by a pair
+# of HIP events recorded on the stream the kernels are enqueued on.
+_timing = None
+
+
+def enable_timing(on: bool = True) -> None:
+    global _timing
+    _timing = {} if on else None
+
+
+def timing_events() -> dict:
+    """{entry point: [(start_event, end_event), ...]} recorded since enable_timing()."""
+    return {} if _timing is None else _timing
+
+
 def call(name: str, *args) -> None:
-    rc = _fn(name)(*args)
+    if _timing is not None:
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        rc = _fn(name)(*args)
+        ev1.record()
+        _timing.setdefault(name, []).append((ev0, ev1))
+    else:
+        rc = _fn(name)(*args)
     if rc != 0:
         msg = lib().tops_last_error().decode()
         if rc == -2:

@@ -65,10 +65,14 @@ def _bwd(q, k, v, g, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool):
     dg = torch.empty(B, T, H, K, device=q.device, dtype=torch.float32)
     dh0 = torch.empty(plan.N, H, K, V, device=q.device, dtype=torch.float32) if want_dh0 else None
     dh_work = torch.empty_like(hs)
-    N.call("tops_gla_chunk_bwd", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(g), N.ptr(do), N.ptr(dht),
-           N.ptr(hs), N.ptr(dh_work), N.ptr(dq), N.ptr(dk), N.ptr(dv), N.ptr(dg), N.ptr(dh0),
+    dt, st = N.dtype_code(q.dtype), N.stream()
+    N.call("tops_gla_chunk_bwd_dh", N.ptr(q), N.ptr(k), N.ptr(g), N.ptr(do), N.ptr(dht),
+           N.ptr(dh_work), N.ptr(dv), N.ptr(dh0), N.ptr(plan.cu_dev), N.ptr(plan.offsets_dev),
+           B, T, H, K, V, plan.N, dt, float(scale), st)
+    N.call("tops_gla_chunk_bwd_dqkg", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(g), N.ptr(do),
+           N.ptr(hs), N.ptr(dh_work), N.ptr(dq), N.ptr(dk), N.ptr(dg),
            N.ptr(plan.cu_dev), N.ptr(plan.offsets_dev), N.ptr(plan.chunk_map_dev), plan.total,
-           B, T, H, K, V, plan.N, N.dtype_code(q.dtype), float(scale), N.stream())
+           B, T, H, K, V, plan.N, dt, float(scale), st)
     return dq, dk, dv, dg, dh0
 
 
