@@ -1,0 +1,391 @@
+// GLA chunk sweeps for gfx950: the fused forward, and the reverse state-gradient sweep
+// of the backward.  One kernel template serves both directions.
+//
+// Forward (REV = false) replaces the reference's K1 chunk_local_cumsum_vector
+// (tops/ops/gla/chunk.py:55-198), K7 chunk_fwd_h (tops/ops/common/chunk_h.py:22-272),
+// K2 chunk_gla_fwd_intra_gk (tops/ops/gla/chunk.py:351-438) and K3 chunk_gla_fwd_o_gk
+// (chunk.py:1279-1440).  Reverse (REV = true) replaces K8 chunk_bwd_dh
+// (tops/ops/common/chunk_h.py:685-878) plus the dv part of K4 (chunk.py:1447-1509),
+// following the oracle tops/cpu/ops/gla/chunk.py:310-354, 387-427.
+//
+// One workgroup (4 wave64) owns one (sequence, head, 64-wide V tile) and walks the
+// sequence chunk by chunk (C = 64), forwards or backwards.  A K x 64 fp32 state S lives
+// in MFMA accumulators for the whole walk.  Per chunk, with G the in-chunk inclusive
+// gate cumsum (log2 units), Gamma = G[last], Gm = Gamma / 2, q~ = q 2^(G-Gm),
+// k~ = k 2^(Gm-G):
+//
+//   forward:  S = h (state before the chunk), Y = v
+//     o^T   = (scale 2^Gm S)^T q~^T + v^T M^T,   M[i][j] = scale q~_i.k~_j  (j <= i)
+//     S     = 2^Gamma S + 2^(Gamma-Gm) (k~^T v)
+//   reverse:  S = dh (gradient w.r.t. the state after the chunk), Y = dO
+//     dv^T  = (2^(Gamma-Gm) S)^T k~^T + dO^T M,  (M as above, contracted over i >= j)
+//     S     = 2^Gamma S + scale 2^Gm (q~^T dO)
+//
+// i.e. out^T = (alpha S)^T X~^T + Y^T D with (X~, Z~) = (q~, k~) forward and (k~, q~)
+// reverse, D[p][r] = scale Z~_p.X~_r on the causal side, and S = 2^Gamma S + beta Z~^T Y.
+// The midpoint Gm bounds every exponent by |Gamma|/2, the stabilisation of
+// tops/ops/gla/chunk.py:371-375.
+//
+// Every workgroup also writes S at the start of each chunk to `ckpt` when given (the
+// forward's state checkpoints, or the reverse sweep's dh per chunk).
+//
+// Pipelining: the raw q/k/g/Y of chunk c+1 are loaded into registers while chunk c is
+// computed; a full chunk takes a branch-free path (masked rows read a clamped in-bounds
+// address and are zeroed).  Two barriers per chunk.
+#include "gla_sweep.h"
+#include "tops_common.h"
+#include "tops_hip.h"
+
+namespace tops {
+
+
+template <typename TIn, int KP, bool REV>
+__global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
+  constexpr int C = kChunk, BV = 64;
+  constexpr int NQ = KP / 4;             // column quads of a [C][KP] tile
+  constexpr int NSEG = 256 / NQ;         // row segments
+  constexpr int RPT = C / NSEG;          // rows per thread (2, 4, 8)
+  constexpr bool SIN = !In<TIn>::kExactBf16;
+  constexpr int LQ = KP + 8, LT = C + 8, LH = KP + 8;
+  constexpr int NHT = (KP / 16) * (BV / 16) / 4;  // state tiles per wave
+  constexpr int NM = NHT >= 4 ? NHT / 4 : 1;      // distinct K blocks per wave
+  constexpr int ES = sizeof(TIn);
+  static_assert(RPT == 2 || RPT == 4 || RPT == 8, "KP must be 32, 64 or 128");
+  typedef Words<TIn> Wd;
+
+  __shared__ __attribute__((aligned(16))) uint16_t sX[2 * C * LQ];
+  __shared__ __attribute__((aligned(16))) uint16_t sZ[2 * C * LQ];
+  __shared__ __attribute__((aligned(16))) uint16_t sZT[2 * KP * LT];
+  __shared__ __attribute__((aligned(16))) uint16_t sYT[(SIN ? 2 : 1) * BV * LT];
+  __shared__ __attribute__((aligned(16))) uint16_t sHT[2 * BV * LH];
+  __shared__ __attribute__((aligned(16))) float sTot[NSEG * KP];
+
+  const Plane PX{sX, sX + C * LQ, LQ};
+  const Plane PZ{sZ, sZ + C * LQ, LQ};
+  const Plane PZt{sZT, sZT + KP * LT, LT};
+  const Plane PYt{sYT, SIN ? sYT + BV * LT : sYT, LT};
+  const Plane PHt{sHT, sHT + BV * LH, LH};
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int wg = xcd_remap(blockIdx.x, gridDim.x, p.NV);
+  const int vt = wg % p.NV;
+  const int hh = (wg / p.NV) % p.H;
+  const int n = wg / (p.NV * p.H);
+  const int H = p.H, K = p.K, V = p.V;
+  const float scale = p.scale;
+
+  int L, row0, cbase;
+  if (p.cu_seqlens) {
+    row0 = p.cu_seqlens[n];
+    L = p.cu_seqlens[n + 1] - row0;
+    cbase = p.chunk_offsets ? p.chunk_offsets[n] : 0;
+  } else {
+    row0 = n * p.T;
+    L = p.T;
+    cbase = n * cdiv(p.T, C);
+  }
+  const int NTs = cdiv(L, C);
+  const long long rows_total = (long long)p.B * p.T;   // rows of the [B*T, H, .] tensors
+
+  // ---- staging coordinates and per-thread byte offsets within a chunk
+  const int cq = tid % NQ, seg = tid / NQ;
+  const int c0 = 4 * cq, r0 = seg * RPT;
+  const bool colok = c0 < K;
+  const int yc = tid & 31, yseg = tid >> 5;     // Y: 2 columns x 8 rows per thread
+  const int yv = vt * BV + 2 * yc;
+  const bool ycolok = yv < V;
+  const uint32_t rowK = (uint32_t)(H * K), rowV = (uint32_t)(H * V);
+  const uint32_t offQ = colok ? ((uint32_t)r0 * rowK + c0) * ES : kOOB;        // q, k
+  const uint32_t offG = colok ? ((uint32_t)r0 * rowK + c0) * 4u : kOOB;        // g
+  const uint32_t offY = ycolok ? ((uint32_t)(yseg * 8) * rowV + yv) * ES : kOOB;
+
+  // ---- state tiles: tile i of this wave -> (m, nn)
+  f32x4 S[NHT];
+#pragma unroll
+  for (int i = 0; i < NHT; ++i) {
+    const int t = wave * NHT + i, m = t / (BV / 16), nn = t % (BV / 16);
+    const int vv = vt * BV + 16 * nn + l16;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int kr = 16 * m + 4 * lg + r;
+      float x = 0.f;
+      if (p.s0 && kr < K && vv < V) x = p.s0[((size_t)(n * H + hh) * K + kr) * V + vv];
+      S[i][r] = x;
+    }
+  }
+
+  // ---- raw chunk registers (prefetch target)
+  typename Wd::W4 rq[RPT], rk[RPT];
+  uint4 rg[RPT];
+  typename Wd::W2 ry[8];
+  auto load_chunk = [&](int c) {
+    const int t0 = c * C;
+    const int nval = min(C, L - t0);
+    const size_t e0 = (size_t)(row0 + t0) * H + hh;     // first row of the chunk, this head
+    const long long rem = (rows_total - (row0 + t0)) * (long long)H;
+    const rsrc_t Rq = make_rsrc((const TIn*)p.q + e0 * K, rem * K * ES);
+    const rsrc_t Rk = make_rsrc((const TIn*)p.k + e0 * K, rem * K * ES);
+    const rsrc_t Rg = make_rsrc(p.g + e0 * K, rem * K * 4);
+    const rsrc_t Ry = make_rsrc((const TIn*)p.y + e0 * V, rem * V * ES);
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const bool ok = r0 + i < nval;
+      rq[i] = Wd::ld4(Rq, ok ? offQ : kOOB, i * rowK * ES);
+      rk[i] = Wd::ld4(Rk, ok ? offQ : kOOB, i * rowK * ES);
+      rg[i] = bld128(Rg, ok ? offG : kOOB, i * rowK * 4);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const bool ok = yseg * 8 + i < nval;
+      ry[i] = Wd::ld2(Ry, ok ? offY : kOOB, i * rowV * ES);
+    }
+  };
+
+  const int cfirst = REV ? NTs - 1 : 0;
+  load_chunk(cfirst);
+
+  for (int it = 0; it < NTs; ++it) {
+    const int c = REV ? NTs - 1 - it : it;
+    const int t0 = c * C;
+    const int nval = min(C, L - t0);
+
+    // ---------------- gate cumsum: thread-local rows, then segment totals via LDS
+    float G[RPT][4];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      float x[4];
+      unpack4(rg[i], x);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) G[i][j] = x[j] * kLog2e + (i > 0 ? G[i - 1][j] : 0.f);
+    }
+    *(float4*)(sTot + seg * KP + c0) = make_float4(G[RPT - 1][0], G[RPT - 1][1], G[RPT - 1][2], G[RPT - 1][3]);
+    __syncthreads();  // B1: totals visible; every wave is done with the previous chunk's planes
+
+    float pre[4] = {0.f, 0.f, 0.f, 0.f}, gam[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NSEG; ++s) {
+      const float4 t = *(const float4*)(sTot + s * KP + c0);
+      if (s < seg) { pre[0] += t.x; pre[1] += t.y; pre[2] += t.z; pre[3] += t.w; }
+      gam[0] += t.x; gam[1] += t.y; gam[2] += t.z; gam[3] += t.w;
+    }
+    // Gamma of this lane's state rows kr = 16 m + 4 lg + r
+    float sgam[NM][4];
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi) {
+      const int m = (wave * NHT) / (BV / 16) + mi;
+      sgam[mi][0] = sgam[mi][1] = sgam[mi][2] = sgam[mi][3] = 0.f;
+#pragma unroll
+      for (int s = 0; s < NSEG; ++s) {
+        const float4 t = *(const float4*)(sTot + s * KP + 16 * m + 4 * lg);
+        sgam[mi][0] += t.x; sgam[mi][1] += t.y; sgam[mi][2] += t.z; sgam[mi][3] += t.w;
+      }
+    }
+
+    // ---------------- state -> H^T plane (alpha S); checkpoint of S
+    const rsrc_t Rck = make_rsrc(p.ckpt ? p.ckpt + ((size_t)(cbase + c) * H + hh) * K * V : nullptr,
+                                 p.ckpt ? (long long)K * V * 4 : 0);
+#pragma unroll
+    for (int i = 0; i < NHT; ++i) {
+      const int t = wave * NHT + i, m = t / (BV / 16), nn = t % (BV / 16);
+      const int mi = (NHT >= 4) ? i / 4 : 0;
+      const int kr = 16 * m + 4 * lg;
+      float x[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float gm = 0.5f * sgam[mi][r];
+        const float alpha = REV ? fast_exp2(sgam[mi][r] - gm) : scale * fast_exp2(gm);
+        x[r] = alpha * S[i][r];
+      }
+      put_n<true, 4>(PHt, 16 * nn + l16, kr, x);
+      if (p.ckpt) {
+        const int vv = vt * BV + 16 * nn + l16;
+        const uint32_t vo = (vv < V) ? ((uint32_t)kr * V + vv) * 4u : kOOB;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          bst32(Rck, __float_as_uint(S[i][r]), (kr + r < K) ? vo : kOOB, (uint32_t)(r * V * 4));
+      }
+    }
+
+    // ---------------- gated operands for the staging rows
+    {
+      float gm[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) gm[j] = 0.5f * gam[j];
+      float zt[4][RPT];
+#pragma unroll
+      for (int i = 0; i < RPT; ++i) {
+        float qv[4], kv[4], xq[4], xk[4];
+        unpack4(rq[i], qv);
+        unpack4(rk[i], kv);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float Gv = G[i][j] + pre[j];
+          xq[j] = qv[j] * fast_exp2(Gv - gm[j]);
+          xk[j] = kv[j] * fast_exp2(gm[j] - Gv);
+        }
+        const float* xx = REV ? xk : xq;
+        const float* zz = REV ? xq : xk;
+        put_n<true, 4>(PX, r0 + i, c0, xx);
+        put_n<true, 4>(PZ, r0 + i, c0, zz);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) zt[j][i] = zz[j];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) put_n<true, RPT>(PZt, c0 + j, r0, zt[j]);
+      float ya[8], yb[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) unpack2(ry[i], ya[i], yb[i]);
+      put_n<SIN, 8>(PYt, 2 * yc, yseg * 8, ya);
+      put_n<SIN, 8>(PYt, 2 * yc + 1, yseg * 8, yb);
+    }
+    __syncthreads();  // B2: all planes visible
+
+    // ---------------- prefetch the next chunk while this one is computed
+    if (it + 1 < NTs) load_chunk(REV ? c - 1 : c + 1);
+
+    // ---------------- output block R = wave: out^T tiles (nn, R)
+    {
+      const int R = wave;
+      bf16x8 xh[KP / 32], xl[KP / 32];
+#pragma unroll
+      for (int kc = 0; kc < KP / 32; ++kc) {
+        xh[kc] = PX.hi8(16 * R + l16, 32 * kc + 8 * lg);
+        xl[kc] = PX.lo8(16 * R + l16, 32 * kc + 8 * lg);
+      }
+      // D tiles (P, R) on the causal side: lane holds D[16P+4lg+r][16R+l16]
+      uint2 dh[4], dl[4];
+#pragma unroll
+      for (int P = 0; P < 4; ++P) {
+        dh[P] = make_uint2(0u, 0u);
+        dl[P] = make_uint2(0u, 0u);
+        const bool live = REV ? (P >= R) : (P <= R);
+        if (live) {
+          f32x4 t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kc = 0; kc < KP / 32; ++kc)
+            t = mma<true, true>(t, PZ.hi8(16 * P + l16, 32 * kc + 8 * lg),
+                                PZ.lo8(16 * P + l16, 32 * kc + 8 * lg), xh[kc], xl[kc]);
+          const int rr = 16 * R + l16;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int pp = 16 * P + 4 * lg + r;
+            const bool keep = REV ? (pp >= rr) : (pp <= rr);
+            t[r] = keep ? t[r] * scale : 0.f;
+          }
+          acc_to_bf16x4(t, dh[P], dl[P]);
+        }
+      }
+      // lane writes out[token 16R + l16][v = 16 nn + 4 lg + 0..3]
+      const int tok = 16 * R + l16;
+      const size_t eo = (size_t)(row0 + t0) * H + hh;
+      const rsrc_t Ro = make_rsrc((TIn*)p.out + eo * V,
+                                  (rows_total - (row0 + t0)) * (long long)H * V * ES);
+      const uint32_t oo = (tok < nval) ? ((uint32_t)tok * rowV + vt * BV + 4 * lg) * ES : kOOB;
+#pragma unroll
+      for (int nn = 0; nn < BV / 16; ++nn) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < KP / 32; ++kc)
+          acc = mma<true, true>(acc, PHt.hi8(16 * nn + l16, 32 * kc + 8 * lg),
+                                PHt.lo8(16 * nn + l16, 32 * kc + 8 * lg), xh[kc], xl[kc]);
+        // out^T += Y^T D  (contraction over p, two 16-blocks per MFMA)
+#pragma unroll
+        for (int Pp = 0; Pp < 2; ++Pp) {
+          const int P0 = 2 * Pp, P1 = 2 * Pp + 1;
+          const bool live = REV ? (P1 >= R) : (P0 <= R);
+          if (live) {
+            const bf16x8 ah = PYt.hi44(16 * nn + l16, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg);
+            bf16x8 al = ah;
+            if constexpr (SIN) al = PYt.lo44(16 * nn + l16, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg);
+            acc = mma<SIN, true>(acc, ah, al, cat44(dh[P0], dh[P1]), cat44(dl[P0], dl[P1]));
+          }
+        }
+        const int v0 = vt * BV + 16 * nn + 4 * lg;
+        Wd::st4(Ro, acc, v0 < V ? oo : kOOB, (uint32_t)(16 * nn * ES));
+      }
+    }
+
+    // ---------------- state update: S = 2^Gamma S + beta (Z~^T Y)
+#pragma unroll
+    for (int i = 0; i < NHT; ++i) {
+      const int t = wave * NHT + i, m = t / (BV / 16), nn = t % (BV / 16);
+      const int mi = (NHT >= 4) ? i / 4 : 0;
+      f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kc = 0; kc < C / 32; ++kc) {
+        const bf16x8 bh = PYt.hi8(16 * nn + l16, 32 * kc + 8 * lg);
+        bf16x8 bl = bh;
+        if constexpr (SIN) bl = PYt.lo8(16 * nn + l16, 32 * kc + 8 * lg);
+        d = mma<true, SIN>(d, PZt.hi8(16 * m + l16, 32 * kc + 8 * lg),
+                           PZt.lo8(16 * m + l16, 32 * kc + 8 * lg), bh, bl);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float ga = sgam[mi][r], gmv = 0.5f * ga;
+        const float beta = REV ? scale * fast_exp2(gmv) : fast_exp2(ga - gmv);
+        S[i][r] = fast_exp2(ga) * S[i][r] + beta * d[r];
+      }
+    }
+  }
+
+  if (p.s_fin) {
+#pragma unroll
+    for (int i = 0; i < NHT; ++i) {
+      const int t = wave * NHT + i, m = t / (BV / 16), nn = t % (BV / 16);
+      const int vv = vt * BV + 16 * nn + l16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kr = 16 * m + 4 * lg + r;
+        if (kr < K && vv < V) p.s_fin[((size_t)(n * H + hh) * K + kr) * V + vv] = S[i][r];
+      }
+    }
+  }
+}
+
+template <typename TIn, bool REV>
+hipError_t launch_gla_sweep(const SweepParams& p, hipStream_t s) {
+  const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
+  dim3 grid(p.NV * p.H * p.N);
+  if (kp == 32) hipLaunchKernelGGL((gla_sweep_kernel<TIn, 32, REV>), grid, dim3(256), 0, s, p);
+  else if (kp == 64) hipLaunchKernelGGL((gla_sweep_kernel<TIn, 64, REV>), grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((gla_sweep_kernel<TIn, 128, REV>), grid, dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+template hipError_t launch_gla_sweep<uint16_t, false>(const SweepParams&, hipStream_t);
+template hipError_t launch_gla_sweep<uint16_t, true>(const SweepParams&, hipStream_t);
+template hipError_t launch_gla_sweep<float, false>(const SweepParams&, hipStream_t);
+template hipError_t launch_gla_sweep<float, true>(const SweepParams&, hipStream_t);
+
+}  // namespace tops
+
+using namespace tops;
+
+extern "C" int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const float* g,
+                                  const float* h0, void* o, float* ht, float* h_ckpt,
+                                  const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                                  int B, int T, int H, int K, int V, int N, int dtype,
+                                  float scale, void* stream) {
+  if (!q || !k || !v || !g || !o) return tops_set_error(TOPS_ERR_NULL, "gla_chunk_fwd: null tensor");
+  if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || N <= 0)
+    return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd: non-positive dimension");
+  if (K > 128 || (K % 8) || (V % 8))
+    return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd: need K <= 128, K % 8 == 0, V % 8 == 0");
+  if (cu_seqlens && B != 1) return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd: varlen needs B == 1");
+  if ((long long)kChunk * H * (K > V ? K : V) * 4 >= (1LL << 31))
+    return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd: H * max(K, V) too large for 32-bit chunk offsets");
+  if (!cu_seqlens && N != B) return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd: N must equal B");
+  if (h_ckpt && cu_seqlens && !chunk_offsets)
+    return tops_set_error(TOPS_ERR_NULL, "gla_chunk_fwd: varlen checkpoints need chunk_offsets");
+  SweepParams p{q, k, g, v, h0, o, ht, h_ckpt, cu_seqlens, chunk_offsets,
+                B, T, H, K, V, N, (V + 63) / 64, scale};
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e;
+  if (dtype == TOPS_BF16) e = launch_gla_sweep<uint16_t, false>(p, s);
+  else if (dtype == TOPS_F32) e = launch_gla_sweep<float, false>(p, s);
+  else return tops_set_error(TOPS_ERR_DTYPE, "gla_chunk_fwd: dtype must be TOPS_F32 or TOPS_BF16");
+  if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
+  return TOPS_OK;
+}

@@ -156,6 +156,44 @@ __device__ __forceinline__ bf16x8 cat44(const uint2& x, const uint2& y) {
 
 __device__ __forceinline__ int cdiv(int a, int b) { return (a + b - 1) / b; }
 
+// ---------------------------------------------------------------- buffer resources
+// Raw (stride 0) buffer descriptors: 32-bit byte offsets from an SGPR base, and the
+// hardware range check returns 0 for a load (drops a store) whose offset is at or past
+// num_records.  Masked elements use kOOB, which is past any num_records set here
+// (num_records is capped at 2^31 - 1).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kOOB = 0x80000000u;
+constexpr int kRsrcFlags = 0x00020000;  // gfx9 family: raw untyped dword access
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, long long bytes) {
+  const int n = bytes > 0x7fffffffLL ? 0x7fffffff : (int)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, kRsrcFlags);
+}
+__device__ __forceinline__ uint32_t bld32(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+}
+__device__ __forceinline__ uint2 bld64(rsrc_t r, uint32_t voff, uint32_t soff) {
+  auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0);
+  return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ uint4 bld128(rsrc_t r, uint32_t voff, uint32_t soff) {
+  auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void bst32(rsrc_t r, uint32_t x, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b32(x, r, (int)voff, (int)soff, 0);
+}
+__device__ __forceinline__ void bst64(rsrc_t r, uint2 x, uint32_t voff, uint32_t soff) {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  u32x2 v = {x.x, x.y};
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, (int)voff, (int)soff, 0);
+}
+__device__ __forceinline__ void bst128(rsrc_t r, uint4 x, uint32_t voff, uint32_t soff) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 v = {x.x, x.y, x.z, x.w};
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)voff, (int)soff, 0);
+}
+
 // Map a linear workgroup id so that `group` consecutive logical ids land on
 // the same XCD (dispatch round-robins workgroups over the 8 XCDs): logical
 // ids that share data (e.g. the V tiles of one head) then share an L2.
@@ -168,6 +206,72 @@ __device__ __forceinline__ int xcd_remap(int wg, int nwg, int group) {
   int blk = slot / group, sub = slot % group;
   (void)per_xcd;
   return (blk * kXcd + xcd) * group + sub;
+}
+
+// ---------------------------------------------------------------- shared helpers
+// Raw input words -> floats (bf16 bits or fp32)
+__device__ __forceinline__ void unpack4(const uint2& u, float* x) {
+  x[0] = __uint_as_float(u.x << 16);
+  x[1] = __uint_as_float(u.x & 0xffff0000u);
+  x[2] = __uint_as_float(u.y << 16);
+  x[3] = __uint_as_float(u.y & 0xffff0000u);
+}
+__device__ __forceinline__ void unpack4(const uint4& u, float* x) {
+  x[0] = __uint_as_float(u.x); x[1] = __uint_as_float(u.y);
+  x[2] = __uint_as_float(u.z); x[3] = __uint_as_float(u.w);
+}
+__device__ __forceinline__ void unpack2(const uint32_t& u, float& a, float& b) {
+  a = __uint_as_float(u << 16);
+  b = __uint_as_float(u & 0xffff0000u);
+}
+__device__ __forceinline__ void unpack2(const uint2& u, float& a, float& b) {
+  a = __uint_as_float(u.x);
+  b = __uint_as_float(u.y);
+}
+// Word types: 4 and 2 consecutive elements of TIn
+template <typename TIn> struct Words;
+template <> struct Words<uint16_t> {
+  typedef uint2 W4;
+  typedef uint32_t W2;
+  __device__ __forceinline__ static W4 ld4(rsrc_t r, uint32_t v, uint32_t s) { return bld64(r, v, s); }
+  __device__ __forceinline__ static W2 ld2(rsrc_t r, uint32_t v, uint32_t s) { return bld32(r, v, s); }
+  __device__ __forceinline__ static void st4(rsrc_t r, const f32x4& x, uint32_t v, uint32_t s) {
+    bst64(r, make_uint2(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])), v, s);
+  }
+};
+template <> struct Words<float> {
+  typedef uint4 W4;
+  typedef uint2 W2;
+  __device__ __forceinline__ static W4 ld4(rsrc_t r, uint32_t v, uint32_t s) { return bld128(r, v, s); }
+  __device__ __forceinline__ static W2 ld2(rsrc_t r, uint32_t v, uint32_t s) { return bld64(r, v, s); }
+  __device__ __forceinline__ static void st4(rsrc_t r, const f32x4& x, uint32_t v, uint32_t s) {
+    bst128(r, make_uint4(__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]),
+                         __float_as_uint(x[3])), v, s);
+  }
+};
+
+// write n (2, 4 or 8) consecutive contraction values of one plane row, hi (and lo)
+template <bool SPLIT, int NE>
+__device__ __forceinline__ void put_n(const Plane& P, int r, int c, const float* x) {
+  uint32_t h[NE / 2], l[NE / 2];
+#pragma unroll
+  for (int i = 0; i < NE / 2; ++i) {
+    if constexpr (SPLIT) split_bf16x2(x[2 * i], x[2 * i + 1], h[i], l[i]);
+    else h[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+  }
+  uint16_t* ph = P.hi + r * P.ld + c;
+  uint16_t* pl = P.lo + r * P.ld + c;
+  if constexpr (NE == 2) {
+    *(uint32_t*)ph = h[0];
+    if constexpr (SPLIT) *(uint32_t*)pl = l[0];
+  } else if constexpr (NE == 4) {
+    *(uint2*)ph = make_uint2(h[0], h[1]);
+    if constexpr (SPLIT) *(uint2*)pl = make_uint2(l[0], l[1]);
+  } else {
+    static_assert(NE == 8, "2, 4 or 8 elements");
+    *(uint4*)ph = make_uint4(h[0], h[1], h[2], h[3]);
+    if constexpr (SPLIT) *(uint4*)pl = make_uint4(l[0], l[1], l[2], l[3]);
+  }
 }
 
 }  // namespace tops
