@@ -108,6 +108,31 @@ int tops_gla_chunk_bwd_dqkg(const void* q, const void* k, const void* v, const f
                             int B, int T, int H, int K, int V, int N, int dtype, float scale,
                             void* stream);
 
+/* Simple GLA: one log-gate per (token, head) -- g [B,T,H] fp32 -- or a constant per-head
+ * log-decay g_gamma [H] fp32; pass exactly one.  The state recurrence is GLA's with the
+ * gate shared by all K channels.  Replaces tops.ops.simple_gla.chunk_simple_gla_fwd /
+ * _varlen (tops/ops/simple_gla/chunk.py:464-577; K9 ops/common/chunk_h.py:887-962,
+ * K10 ops/common/chunk_o.py:119-185) and the oracle tops/cpu/ops/simple_gla/chunk.py:53-129.
+ * Other arguments as tops_gla_chunk_fwd. */
+int tops_simple_gla_chunk_fwd(const void* q, const void* k, const void* v, const float* g,
+                              const float* g_gamma, const float* h0, void* o, float* ht,
+                              float* h_ckpt, const int32_t* cu_seqlens,
+                              const int32_t* chunk_offsets, int B, int T, int H, int K, int V,
+                              int N, int dtype, float scale, void* stream);
+
+/* Simple GLA backward: dq, dk, dv, dh0 and, for a per-token g, dg [B,T,H] fp32 (the gate
+ * gradient summed over the K channels; dg is ignored with g_gamma).  Replaces
+ * tops.ops.simple_gla.chunk_simple_gla_bwd (tops/ops/simple_gla/chunk.py:579-674; K11
+ * ops/common/chunk_o.py:277-366) and the oracle tops/cpu/ops/simple_gla/chunk.py:668-788.
+ * Arguments as tops_gla_chunk_bwd. */
+int tops_simple_gla_chunk_bwd(const void* q, const void* k, const void* v, const float* g,
+                              const float* g_gamma, const void* do_, const float* dht,
+                              const float* h_ckpt, float* dh_work, void* dq, void* dk, void* dv,
+                              float* dg, float* dh0, const int32_t* cu_seqlens,
+                              const int32_t* chunk_offsets, const int32_t* chunk_map,
+                              int total_chunks, int B, int T, int H, int K, int V, int N,
+                              int dtype, float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

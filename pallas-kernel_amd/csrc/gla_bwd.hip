@@ -58,23 +58,51 @@ static int check_bwd(const char* who, int B, int T, int H, int K, int V, int N, 
 
 using namespace tops;
 
-extern "C" int tops_gla_chunk_bwd_dh(const void* q, const void* k, const float* g,
-                                     const void* do_, const float* dht, float* dh_work, void* dv,
-                                     float* dh0, const int32_t* cu_seqlens,
-                                     const int32_t* chunk_offsets, int B, int T, int H, int K,
-                                     int V, int N, int dtype, float scale, void* stream) {
+static int bwd_dh_impl(const void* q, const void* k, const float* g, const void* do_,
+                       const float* dht, float* dh_work, void* dv, float* dh0,
+                       const int32_t* cu_seqlens, const int32_t* chunk_offsets, int B, int T, int H,
+                       int K, int V, int N, int dtype, float scale, int gate_mode, void* stream) {
   if (!q || !k || !g || !do_ || !dh_work || !dv)
     return tops_set_error(TOPS_ERR_NULL, "gla_chunk_bwd_dh: null tensor");
   int rc = check_bwd("gla_chunk_bwd_dh", B, T, H, K, V, N, 0, cu_seqlens, chunk_offsets, nullptr,
                      false, dtype);
   if (rc != TOPS_OK) return rc;
   SweepParams p{q, k, g, do_, dht, dv, dh0, dh_work, cu_seqlens, chunk_offsets,
-                B, T, H, K, V, N, (V + 63) / 64, scale};
+                B, T, H, K, V, N, (V + 63) / 64, scale, gate_mode};
   hipStream_t s = (hipStream_t)stream;
   hipError_t e = dtype == TOPS_BF16 ? launch_gla_sweep<uint16_t, true>(p, s)
                                     : launch_gla_sweep<float, true>(p, s);
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   return TOPS_OK;
+}
+
+static int bwd_dqkg_impl(const void* q, const void* k, const void* v, const float* g,
+                         const void* do_, const float* h_ckpt, const float* dh_work, void* dq,
+                         void* dk, float* dg, const int32_t* cu_seqlens,
+                         const int32_t* chunk_offsets, const int32_t* chunk_map, int total_chunks,
+                         int B, int T, int H, int K, int V, int N, int dtype, float scale,
+                         int gate_mode, void* stream) {
+  if (!q || !k || !v || !g || !do_ || !h_ckpt || !dh_work || !dq || !dk ||
+      (gate_mode != kGateGamma && !dg))
+    return tops_set_error(TOPS_ERR_NULL, "gla_chunk_bwd_dqkg: null tensor");
+  int rc = check_bwd("gla_chunk_bwd_dqkg", B, T, H, K, V, N, total_chunks, cu_seqlens,
+                     chunk_offsets, chunk_map, true, dtype);
+  if (rc != TOPS_OK) return rc;
+  DqkgParams p{q, k, v, g, do_, h_ckpt, dh_work, dq, dk, dg, cu_seqlens, chunk_offsets, chunk_map,
+               total_chunks, B, T, H, K, V, N, scale, gate_mode};
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = dtype == TOPS_BF16 ? launch_gla_dqkg<uint16_t>(p, s) : launch_gla_dqkg<float>(p, s);
+  if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
+  return TOPS_OK;
+}
+
+extern "C" int tops_gla_chunk_bwd_dh(const void* q, const void* k, const float* g,
+                                     const void* do_, const float* dht, float* dh_work, void* dv,
+                                     float* dh0, const int32_t* cu_seqlens,
+                                     const int32_t* chunk_offsets, int B, int T, int H, int K,
+                                     int V, int N, int dtype, float scale, void* stream) {
+  return bwd_dh_impl(q, k, g, do_, dht, dh_work, dv, dh0, cu_seqlens, chunk_offsets, B, T, H, K, V,
+                     N, dtype, scale, kGateK, stream);
 }
 
 extern "C" int tops_gla_chunk_bwd_dqkg(const void* q, const void* k, const void* v, const float* g,
@@ -83,17 +111,8 @@ extern "C" int tops_gla_chunk_bwd_dqkg(const void* q, const void* k, const void*
                                        const int32_t* chunk_offsets, const int32_t* chunk_map,
                                        int total_chunks, int B, int T, int H, int K, int V, int N,
                                        int dtype, float scale, void* stream) {
-  if (!q || !k || !v || !g || !do_ || !h_ckpt || !dh_work || !dq || !dk || !dg)
-    return tops_set_error(TOPS_ERR_NULL, "gla_chunk_bwd_dqkg: null tensor");
-  int rc = check_bwd("gla_chunk_bwd_dqkg", B, T, H, K, V, N, total_chunks, cu_seqlens,
-                     chunk_offsets, chunk_map, true, dtype);
-  if (rc != TOPS_OK) return rc;
-  DqkgParams p{q, k, v, g, do_, h_ckpt, dh_work, dq, dk, dg, cu_seqlens, chunk_offsets, chunk_map,
-               total_chunks, B, T, H, K, V, N, scale};
-  hipStream_t s = (hipStream_t)stream;
-  hipError_t e = dtype == TOPS_BF16 ? launch_gla_dqkg<uint16_t>(p, s) : launch_gla_dqkg<float>(p, s);
-  if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
-  return TOPS_OK;
+  return bwd_dqkg_impl(q, k, v, g, do_, h_ckpt, dh_work, dq, dk, dg, cu_seqlens, chunk_offsets,
+                       chunk_map, total_chunks, B, T, H, K, V, N, dtype, scale, kGateK, stream);
 }
 
 extern "C" int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, const float* g,
@@ -103,15 +122,29 @@ extern "C" int tops_gla_chunk_bwd(const void* q, const void* k, const void* v, c
                                   const int32_t* chunk_offsets, const int32_t* chunk_map,
                                   int total_chunks, int B, int T, int H, int K, int V, int N,
                                   int dtype, float scale, void* stream) {
-  if (!v || !h_ckpt || !dq || !dk || !dg)
-    return tops_set_error(TOPS_ERR_NULL, "gla_chunk_bwd: null tensor");
-  int rc = check_bwd("gla_chunk_bwd", B, T, H, K, V, N, total_chunks, cu_seqlens, chunk_offsets,
-                     chunk_map, true, dtype);
+  int rc = bwd_dh_impl(q, k, g, do_, dht, dh_work, dv, dh0, cu_seqlens, chunk_offsets, B, T, H, K,
+                       V, N, dtype, scale, kGateK, stream);
   if (rc != TOPS_OK) return rc;
-  rc = tops_gla_chunk_bwd_dh(q, k, g, do_, dht, dh_work, dv, dh0, cu_seqlens, chunk_offsets,
-                             B, T, H, K, V, N, dtype, scale, stream);
+  return bwd_dqkg_impl(q, k, v, g, do_, h_ckpt, dh_work, dq, dk, dg, cu_seqlens, chunk_offsets,
+                       chunk_map, total_chunks, B, T, H, K, V, N, dtype, scale, kGateK, stream);
+}
+
+extern "C" int tops_simple_gla_chunk_bwd(const void* q, const void* k, const void* v,
+                                         const float* g, const float* g_gamma, const void* do_,
+                                         const float* dht, const float* h_ckpt, float* dh_work,
+                                         void* dq, void* dk, void* dv, float* dg, float* dh0,
+                                         const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                                         const int32_t* chunk_map, int total_chunks, int B, int T,
+                                         int H, int K, int V, int N, int dtype, float scale,
+                                         void* stream) {
+  if ((g == nullptr) == (g_gamma == nullptr))
+    return tops_set_error(TOPS_ERR_NULL, "simple_gla_chunk_bwd: pass exactly one of g, g_gamma");
+  const int mode = g ? kGateS : kGateGamma;
+  const float* gp = g ? g : g_gamma;
+  int rc = bwd_dh_impl(q, k, gp, do_, dht, dh_work, dv, dh0, cu_seqlens, chunk_offsets, B, T, H, K,
+                       V, N, dtype, scale, mode, stream);
   if (rc != TOPS_OK) return rc;
-  return tops_gla_chunk_bwd_dqkg(q, k, v, g, do_, h_ckpt, dh_work, dq, dk, dg, cu_seqlens,
-                                 chunk_offsets, chunk_map, total_chunks, B, T, H, K, V, N, dtype,
-                                 scale, stream);
+  return bwd_dqkg_impl(q, k, v, gp, do_, h_ckpt, dh_work, dq, dk, g ? dg : nullptr, cu_seqlens,
+                       chunk_offsets, chunk_map, total_chunks, B, T, H, K, V, N, dtype, scale, mode,
+                       stream);
 }

@@ -56,6 +56,7 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
   __shared__ __attribute__((aligned(16))) float sZk[2 * KH];
   __shared__ __attribute__((aligned(16))) float sHdh[KH];
   __shared__ __attribute__((aligned(16))) float sBlk[KH];
+  __shared__ __attribute__((aligned(16))) float sDgS[2 * C];   // kGateS: per channel-block token sums
 
   const Plane Pv{sV, SIN ? sV + C * LV : sV, LV};
   const Plane Pd{sD, SIN ? sD + C * LV : sD, LV};
@@ -92,7 +93,9 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
   const uint32_t rowK = (uint32_t)(H * K), rowV = (uint32_t)(H * V);
   const rsrc_t Rq = make_rsrc((const TIn*)p.q + e0 * K, remr * K * ES);
   const rsrc_t Rk = make_rsrc((const TIn*)p.k + e0 * K, remr * K * ES);
-  const rsrc_t Rg = make_rsrc(p.g + e0 * K, remr * K * 4);
+  const int gmode = p.gate_mode;
+  const rsrc_t Rg = make_rsrc(gmode == kGateK ? p.g + e0 * K : p.g + e0, remr * (gmode == kGateK ? K : 1) * 4);
+  const float gam_h = gmode == kGateGamma ? p.g[hh] : 0.f;
 
   // ---------------- v / dO planes ([C][V], V contiguous)
   {
@@ -143,7 +146,9 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
         rq[i] = (off & 1u) ? __uint_as_float(wq & 0xffff0000u) : __uint_as_float(wq << 16);
         rk[i] = (off & 1u) ? __uint_as_float(wk & 0xffff0000u) : __uint_as_float(wk << 16);
       }
-      rg[i] = __uint_as_float(bld32(Rg, v_ ? off * 4u : kOOB, 0));
+      // one unconditional load whatever the gate mode (gamma loads nothing: out of range)
+      const uint32_t go = gmode == kGateK ? off * 4u : (gmode == kGateS ? (uint32_t)r * H * 4u : kOOB);
+      rg[i] = __uint_as_float(bld32(Rg, v_ ? go : kOOB, 0));
     }
   };
   load_pass(0);
@@ -202,7 +207,9 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
   const rsrc_t Rdh = make_rsrc(p.dhs + ((size_t)gc * H + hh) * K * V, (long long)K * V * 4);
   const rsrc_t Rdq = make_rsrc((TIn*)p.dq + e0 * K, remr * K * ES);
   const rsrc_t Rdk = make_rsrc((TIn*)p.dk + e0 * K, remr * K * ES);
-  const rsrc_t Rdg = make_rsrc(p.dg + e0 * K, remr * K * 4);
+  const rsrc_t Rdg = make_rsrc(p.dg ? (gmode == kGateS ? p.dg + e0 : p.dg + e0 * K) : nullptr,
+                               p.dg ? remr * (gmode == kGateS ? 1 : K) * 4 : 0);
+  if (tid < 2 * C) sDgS[tid] = 0.f;
 
 #pragma unroll 1
   for (int ps = 0; ps < NPS; ++ps) {
@@ -210,7 +217,10 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
     // ---- gate cumsum of the pass (thread: channel ch, rows 8sg..8sg+7)
     float G[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) G[i] = rg[i] * kLog2e + (i > 0 ? G[i - 1] : 0.f);
+    for (int i = 0; i < 8; ++i) {
+      const float x = gmode == kGateGamma ? ((cb + ch < K && 8 * sg + i < nval) ? gam_h : 0.f) : rg[i];
+      G[i] = x * kLog2e + (i > 0 ? G[i - 1] : 0.f);
+    }
     __syncthreads();  // the previous pass is done with every LDS array
     sTot[sg * KH + ch] = G[7];
     __syncthreads();
@@ -386,14 +396,36 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
       add[r] = fast_exp2(sGam[cl + r]) * sHdh[cl + r] + sZk[cl + r] + sZk[KH + cl + r];
       if (rh == 0) add[r] += sBlk[cl + r];
     }
+    if (gmode == kGateK) {
 #pragma unroll
-    for (int a = 0; a < 2; ++a) {
-      const int tok = 16 * (2 * rh + a) + l16;
-      const bool ok = chok && tok < nval;
-      const uint32_t off = (uint32_t)tok * rowK + kc;
-      bst128(Rdg, make_uint4(__float_as_uint(dgr[a][0] + add[0]), __float_as_uint(dgr[a][1] + add[1]),
-                             __float_as_uint(dgr[a][2] + add[2]), __float_as_uint(dgr[a][3] + add[3])),
-             ok ? off * 4u : kOOB, 0);
+      for (int a = 0; a < 2; ++a) {
+        const int tok = 16 * (2 * rh + a) + l16;
+        const bool ok = chok && tok < nval;
+        const uint32_t off = (uint32_t)tok * rowK + kc;
+        bst128(Rdg, make_uint4(__float_as_uint(dgr[a][0] + add[0]), __float_as_uint(dgr[a][1] + add[1]),
+                               __float_as_uint(dgr[a][2] + add[2]), __float_as_uint(dgr[a][3] + add[3])),
+               ok ? off * 4u : kOOB, 0);
+      }
+    } else if (gmode == kGateS) {
+      // one gate per token: sum the per-channel gradients over this wave's 16 channels
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        float x = 0.f;
+        if (chok) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) x += dgr[a][r] + add[r];
+        }
+        x += __shfl_xor(x, 16, 64);
+        x += __shfl_xor(x, 32, 64);
+        if (lg == 0) sDgS[kb * C + 16 * (2 * rh + a) + l16] += x;
+      }
+    }
+  }
+  if (gmode == kGateS && p.dg) {
+    __syncthreads();
+    if (tid < C) {
+      const float x = sDgS[tid] + sDgS[C + tid];
+      bst32(Rdg, __float_as_uint(x), tid < nval ? (uint32_t)tid * H * 4u : kOOB, 0);
     }
   }
 }

@@ -4,6 +4,12 @@
 
 namespace tops {
 
+// Gate modes of the chunk kernels (runtime, wave-uniform):
+//   kGateK     g is [B,T,H,K] per-channel log-gates (GLA)
+//   kGateS     g is [B,T,H] one log-gate per (token, head), shared by all K channels
+//   kGateGamma g is gamma[H], a constant log-decay per head (simple GLA g_gamma)
+enum { kGateK = 0, kGateS = 1, kGateGamma = 2 };
+
 struct SweepParams {
   const void* q;
   const void* k;
@@ -17,6 +23,7 @@ struct SweepParams {
   const int* chunk_offsets;
   int B, T, H, K, V, N, NV;
   float scale;
+  int gate_mode;
 };
 
 // TIn = uint16_t (bf16 bits) or float; REV = reverse (state-gradient) sweep.
@@ -33,12 +40,13 @@ struct DqkgParams {
   const float* dhs;      // [total, H, K, V] gradient w.r.t. the state after each chunk
   void* dq;
   void* dk;
-  float* dg;
+  float* dg;             // [B,T,H,K] (kGateK), [B,T,H] (kGateS) or NULL
   const int* cu_seqlens;
   const int* chunk_offsets;
   const int* chunk_map;
   int total, B, T, H, K, V, N;
   float scale;
+  int gate_mode;
 };
 
 template <typename TIn>

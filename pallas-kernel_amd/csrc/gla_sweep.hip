@@ -100,6 +100,13 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
   const uint32_t offQ = colok ? ((uint32_t)r0 * rowK + c0) * ES : kOOB;        // q, k
   const uint32_t offG = colok ? ((uint32_t)r0 * rowK + c0) * 4u : kOOB;        // g
   const uint32_t offY = ycolok ? ((uint32_t)(yseg * 8) * rowV + yv) * ES : kOOB;
+  // gate load: per-channel [.., K] float4, or the per-(token, head) scalar read as the first
+  // word of a 16-byte load; the gamma mode loads nothing (out of range -> 0)
+  const int gmode = p.gate_mode;
+  const bool gk_mode = gmode == kGateK;
+  const uint32_t offGm = gk_mode ? offG : (gmode == kGateS ? (uint32_t)r0 * H * 4u : kOOB);
+  const uint32_t gstride = gk_mode ? rowK * 4 : (uint32_t)H * 4;
+  const float gam_h = gmode == kGateGamma ? p.g[hh] : 0.f;
 
   // ---- state tiles: tile i of this wave -> (m, nn)
   f32x4 S[NHT];
@@ -127,14 +134,16 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
     const long long rem = (rows_total - (row0 + t0)) * (long long)H;
     const rsrc_t Rq = make_rsrc((const TIn*)p.q + e0 * K, rem * K * ES);
     const rsrc_t Rk = make_rsrc((const TIn*)p.k + e0 * K, rem * K * ES);
-    const rsrc_t Rg = make_rsrc(p.g + e0 * K, rem * K * 4);
+    const rsrc_t Rg = make_rsrc(gk_mode ? p.g + e0 * K : p.g + e0, rem * (gk_mode ? K : 1) * 4);
     const rsrc_t Ry = make_rsrc((const TIn*)p.y + e0 * V, rem * V * ES);
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
       const bool ok = r0 + i < nval;
       rq[i] = Wd::ld4(Rq, ok ? offQ : kOOB, i * rowK * ES);
       rk[i] = Wd::ld4(Rk, ok ? offQ : kOOB, i * rowK * ES);
-      rg[i] = bld128(Rg, ok ? offG : kOOB, i * rowK * 4);
+      // one unconditional load whatever the gate mode (the mode's transform is applied
+      // when the chunk is consumed, so the prefetch never waits)
+      rg[i] = bld128(Rg, ok ? offGm : kOOB, i * gstride);
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -157,6 +166,10 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
     for (int i = 0; i < RPT; ++i) {
       float x[4];
       unpack4(rg[i], x);
+      if (!gk_mode) {
+        const float s1 = gmode == kGateS ? x[0] : (r0 + i < nval ? gam_h : 0.f);
+        x[0] = x[1] = x[2] = x[3] = s1;
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) G[i][j] = x[j] * kLog2e + (i > 0 ? G[i - 1][j] : 0.f);
     }
@@ -363,11 +376,11 @@ template hipError_t launch_gla_sweep<float, true>(const SweepParams&, hipStream_
 
 using namespace tops;
 
-extern "C" int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const float* g,
-                                  const float* h0, void* o, float* ht, float* h_ckpt,
-                                  const int32_t* cu_seqlens, const int32_t* chunk_offsets,
-                                  int B, int T, int H, int K, int V, int N, int dtype,
-                                  float scale, void* stream) {
+static int chunk_fwd_impl(const void* q, const void* k, const void* v, const float* g,
+                          const float* h0, void* o, float* ht, float* h_ckpt,
+                          const int32_t* cu_seqlens, const int32_t* chunk_offsets, int B, int T,
+                          int H, int K, int V, int N, int dtype, float scale, int gate_mode,
+                          void* stream) {
   if (!q || !k || !v || !g || !o) return tops_set_error(TOPS_ERR_NULL, "gla_chunk_fwd: null tensor");
   if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || N <= 0)
     return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd: non-positive dimension");
@@ -380,7 +393,7 @@ extern "C" int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, c
   if (h_ckpt && cu_seqlens && !chunk_offsets)
     return tops_set_error(TOPS_ERR_NULL, "gla_chunk_fwd: varlen checkpoints need chunk_offsets");
   SweepParams p{q, k, g, v, h0, o, ht, h_ckpt, cu_seqlens, chunk_offsets,
-                B, T, H, K, V, N, (V + 63) / 64, scale};
+                B, T, H, K, V, N, (V + 63) / 64, scale, gate_mode};
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
   if (dtype == TOPS_BF16) e = launch_gla_sweep<uint16_t, false>(p, s);
@@ -388,4 +401,25 @@ extern "C" int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, c
   else return tops_set_error(TOPS_ERR_DTYPE, "gla_chunk_fwd: dtype must be TOPS_F32 or TOPS_BF16");
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   return TOPS_OK;
+}
+
+extern "C" int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, const float* g,
+                                  const float* h0, void* o, float* ht, float* h_ckpt,
+                                  const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                                  int B, int T, int H, int K, int V, int N, int dtype,
+                                  float scale, void* stream) {
+  return chunk_fwd_impl(q, k, v, g, h0, o, ht, h_ckpt, cu_seqlens, chunk_offsets, B, T, H, K, V, N,
+                        dtype, scale, kGateK, stream);
+}
+
+extern "C" int tops_simple_gla_chunk_fwd(const void* q, const void* k, const void* v,
+                                         const float* g, const float* g_gamma, const float* h0,
+                                         void* o, float* ht, float* h_ckpt,
+                                         const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                                         int B, int T, int H, int K, int V, int N, int dtype,
+                                         float scale, void* stream) {
+  if ((g == nullptr) == (g_gamma == nullptr))
+    return tops_set_error(TOPS_ERR_NULL, "simple_gla_chunk_fwd: pass exactly one of g, g_gamma");
+  return chunk_fwd_impl(q, k, v, g ? g : g_gamma, h0, o, ht, h_ckpt, cu_seqlens, chunk_offsets, B, T,
+                        H, K, V, N, dtype, scale, g ? kGateS : kGateGamma, stream);
 }

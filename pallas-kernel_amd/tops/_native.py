@@ -31,6 +31,8 @@ SIGNATURES = {
     "tops_gla_chunk_bwd_dqkg": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                 _vp, _vp, _vp, _i32,
                                 _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp],
+    "tops_simple_gla_chunk_fwd": [_vp] * 11 + [_i32] * 7 + [_f32, _vp],
+    "tops_simple_gla_chunk_bwd": [_vp] * 17 + [_i32] * 8 + [_f32, _vp],
     "tops_prepare_chunk_indices": [_vp, _i32, _i32, _vp, _vp, _i32],
 }
 

@@ -16,64 +16,22 @@ from __future__ import annotations
 
 import torch
 
-from ... import _native as N
-from ...utils import ChunkPlan, cdiv, CHUNK
+from ...utils import ChunkPlan
+from .._chunk_core import GATE_K, check_qkv, chunk_fwd as _core_fwd, chunk_bwd as _core_bwd
 
 
 def _check(q, k, v, g, initial_state, cu_seqlens):
-    assert q.ndim == 4, f"q must be [B,T,H,K], got {tuple(q.shape)}"
+    check_qkv(q, k, v, initial_state, cu_seqlens)
     B, T, H, K = q.shape
-    V = v.shape[-1]
-    assert k.shape == q.shape, f"k shape {tuple(k.shape)} != q shape {tuple(q.shape)}"
-    assert v.shape[:3] == (B, T, H), f"v shape {tuple(v.shape)} incompatible with q"
     assert g is None or tuple(g.shape) == (B, T, H, K), f"g shape {tuple(g.shape)} != {(B, T, H, K)}"
-    assert q.dtype == k.dtype == v.dtype, "q, k, v must share a dtype"
-    if cu_seqlens is not None:
-        assert B == 1, f"B must be 1 for varlen, got {B}"
-    n = (len(cu_seqlens) - 1) if cu_seqlens is not None else B
-    if initial_state is not None:
-        assert tuple(initial_state.shape) == (n, H, K, V), (
-            f"initial_state shape {tuple(initial_state.shape)} != {(n, H, K, V)}")
-    if K > 128 or K % 8 or V % 8:
-        raise NotImplementedError(f"tops-hip chunk kernels need K <= 128 and K, V multiples of 8 "
-                                  f"(got K={K}, V={V})")
-    N.require_cuda(q, k, v, g, initial_state)
 
 
 def _fwd(q, k, v, g, h0, scale, output_final_state, plan: ChunkPlan, keep_states: bool):
-    B, T, H, K = q.shape
-    V = v.shape[-1]
-    o = torch.empty_like(v)
-    ht = torch.empty(plan.N, H, K, V, device=q.device, dtype=torch.float32) \
-        if output_final_state else None
-    hs = torch.empty(plan.total, H, K, V, device=q.device, dtype=torch.float32) \
-        if keep_states else None
-    N.call("tops_gla_chunk_fwd", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(g), N.ptr(h0), N.ptr(o),
-           N.ptr(ht), N.ptr(hs), N.ptr(plan.cu_dev), N.ptr(plan.offsets_dev),
-           B, T, H, K, V, plan.N, N.dtype_code(q.dtype), float(scale), N.stream())
-    return o, ht, hs
+    return _core_fwd(q, k, v, (GATE_K, g), h0, scale, output_final_state, plan, keep_states)
 
 
 def _bwd(q, k, v, g, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool):
-    B, T, H, K = q.shape
-    V = v.shape[-1]
-    if V > 128:
-        raise NotImplementedError("tops-hip chunk backward needs V <= 128")
-    dq = torch.empty_like(q)
-    dk = torch.empty_like(k)
-    dv = torch.empty_like(v)
-    dg = torch.empty(B, T, H, K, device=q.device, dtype=torch.float32)
-    dh0 = torch.empty(plan.N, H, K, V, device=q.device, dtype=torch.float32) if want_dh0 else None
-    dh_work = torch.empty_like(hs)
-    dt, st = N.dtype_code(q.dtype), N.stream()
-    N.call("tops_gla_chunk_bwd_dh", N.ptr(q), N.ptr(k), N.ptr(g), N.ptr(do), N.ptr(dht),
-           N.ptr(dh_work), N.ptr(dv), N.ptr(dh0), N.ptr(plan.cu_dev), N.ptr(plan.offsets_dev),
-           B, T, H, K, V, plan.N, dt, float(scale), st)
-    N.call("tops_gla_chunk_bwd_dqkg", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(g), N.ptr(do),
-           N.ptr(hs), N.ptr(dh_work), N.ptr(dq), N.ptr(dk), N.ptr(dg),
-           N.ptr(plan.cu_dev), N.ptr(plan.offsets_dev), N.ptr(plan.chunk_map_dev), plan.total,
-           B, T, H, K, V, plan.N, dt, float(scale), st)
-    return dq, dk, dv, dg, dh0
+    return _core_bwd(q, k, v, (GATE_K, g), do, dht, hs, scale, plan, want_dh0)
 
 
 class _ChunkGLA(torch.autograd.Function):
@@ -104,6 +62,15 @@ class _ChunkGLA(torch.autograd.Function):
         return dq, dk, dv, dg.to(ctx.g_dtype), dh0, None, None, None
 
 
+def _gate_or_default(q, g, g_gamma):
+    B, T, H, K = q.shape
+    if g is not None:
+        return g
+    if g_gamma is not None:
+        return torch.as_tensor(g_gamma, device=q.device).to(torch.float32).expand(B, T, H, K)
+    return torch.zeros(B, T, H, K, device=q.device, dtype=torch.float32)
+
+
 def chunk_gla(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -125,12 +92,8 @@ def chunk_gla(
     Returns (o [B,T,H,V] in q.dtype, final_state [N,H,K,V] fp32 or None).
     """
     assert chunk_size > 0, "chunk_size must be positive"
-    B, T, H, K = q.shape
-    if g is None:
-        if g_gamma is not None:
-            g = torch.as_tensor(g_gamma, device=q.device).to(torch.float32).expand(B, T, H, K)
-        else:
-            g = torch.zeros(B, T, H, K, device=q.device, dtype=torch.float32)
+    K = q.shape[-1]
+    g = _gate_or_default(q, g, g_gamma)
     _check(q, k, v, g, initial_state, cu_seqlens)
     if scale is None:
         scale = K ** -0.5
@@ -153,9 +116,7 @@ def chunk_gla_fwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, output_fi
                                   "pass raw gates g instead of g_cumsum")
     B, T, H, K = q.shape
     V = v.shape[-1]
-    if g is None:
-        g = (torch.as_tensor(g_gamma, device=q.device).to(torch.float32).expand(B, T, H, K)
-             if g_gamma is not None else torch.zeros(B, T, H, K, device=q.device))
+    g = _gate_or_default(q, g, g_gamma)
     _check(q, k, v, g, initial_state, cu_seqlens)
     plan = ChunkPlan(B, T, cu_seqlens, q.device)
     g32 = g.contiguous().to(torch.float32)
@@ -178,9 +139,7 @@ def chunk_gla_bwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, h, A, do,
     B, T, H, K = q.shape
     V = v.shape[-1]
     g_orig = g
-    if g is None:
-        g = (torch.as_tensor(g_gamma, device=q.device).to(torch.float32).expand(B, T, H, K)
-             if g_gamma is not None else torch.zeros(B, T, H, K, device=q.device))
+    g = _gate_or_default(q, g, g_gamma)
     _check(q, k, v, g, initial_state, cu_seqlens)
     plan = ChunkPlan(B, T, cu_seqlens, q.device)
     q, k, v = (x.contiguous() for x in (q, k, v))

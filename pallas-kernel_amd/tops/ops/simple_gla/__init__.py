@@ -1,0 +1,51 @@
+"""tops.ops.simple_gla on MI355X (mirrors tops/ops/simple_gla/__init__.py:1-239)."""
+from __future__ import annotations
+
+from .chunk import (chunk_simple_gla, chunk_simple_gla_bwd, chunk_simple_gla_fwd,
+                    chunk_simple_gla_fwd_varlen)
+from .fused_chunk import fused_chunk_simple_gla, fused_chunk_simple_gla_bwd, fused_chunk_simple_gla_fwd
+
+
+def simple_gla(q, k, v, *args, g=None, g_gamma=None, scale=None, initial_state=None,
+               output_final_state=False, chunk_size=64, reverse=False, cu_seqlens_cpu=None,
+               mode="chunk", **kwargs):
+    """Unified simple-GLA entry point (tops/ops/simple_gla/__init__.py:15-158), with the
+    reference's argument checks and ValueErrors per mode."""
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    assert tuple(k.shape) == (B, T, H, K), f"k shape {tuple(k.shape)} != {(B, T, H, K)}"
+    assert tuple(v.shape) == (B, T, H, V), f"v shape {tuple(v.shape)} != {(B, T, H, V)}"
+    assert g is None or tuple(g.shape) == (B, T, H), f"g shape {tuple(g.shape)} != {(B, T, H)}"
+    assert g_gamma is None or tuple(g_gamma.shape) == (H,), f"g_gamma shape must be ({H},)"
+    if mode in ("chunk", "fused_chunk"):
+        if g is not None:
+            raise ValueError(f"mode={mode!r} does not support per-token gate `g`; "
+                             "use 'fused_recurrent' or 'naive' instead")
+        if reverse:
+            raise ValueError(f"mode={mode!r} does not support `reverse`")
+        if cu_seqlens_cpu is not None:
+            raise ValueError(f"mode={mode!r} does not support `cu_seqlens`")
+        assert g_gamma is not None, f"mode={mode!r} requires g_gamma"
+        fn = chunk_simple_gla if mode == "chunk" else fused_chunk_simple_gla
+        return fn(q, k, v, g_gamma, initial_state=initial_state, scale=scale,
+                  output_final_state=output_final_state, chunk_size=chunk_size)
+    if mode in ("fused_recurrent", "naive"):
+        from .fused_recurrent import fused_recurrent_simple_gla
+        return fused_recurrent_simple_gla(q, k, v, g=g, g_gamma=g_gamma, scale=scale,
+                                          initial_state=initial_state,
+                                          output_final_state=output_final_state, reverse=reverse,
+                                          cu_seqlens=cu_seqlens_cpu)
+    raise ValueError(f"Unknown mode {mode!r}; expected one of "
+                     "'chunk', 'fused_chunk', 'fused_recurrent', 'naive'")
+
+
+__all__ = [
+    "simple_gla",
+    "chunk_simple_gla",
+    "chunk_simple_gla_fwd",
+    "chunk_simple_gla_fwd_varlen",
+    "chunk_simple_gla_bwd",
+    "fused_chunk_simple_gla",
+    "fused_chunk_simple_gla_fwd",
+    "fused_chunk_simple_gla_bwd",
+]

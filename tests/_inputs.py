@@ -28,3 +28,27 @@ def bf16_round(x):
     u = x.view(np.uint32).astype(np.uint64)
     u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
     return u.astype(np.uint32).view(np.float32)
+
+
+def simple_gla_inputs(B, T, H, K, V, seed, gate_div=1.0, h0=False, N=None, grads=False):
+    """Seeded simple-GLA inputs: q, k, v ~ N(0,1); g = logsigmoid(N(0,1))/gate_div [B,T,H];
+    g_gamma = -|N(0,1)|/8 [H]."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    d = dict(q=rng.standard_normal((B, T, H, K)).astype(np.float32),
+             k=rng.standard_normal((B, T, H, K)).astype(np.float32),
+             v=rng.standard_normal((B, T, H, V)).astype(np.float32),
+             g=(logsigmoid(rng.standard_normal((B, T, H))) / gate_div).astype(np.float32),
+             g_gamma=(-np.abs(rng.standard_normal(H)) / 8).astype(np.float32))
+    n0 = B if N is None else N
+    d["h0"] = (0.1 * rng.standard_normal((n0, H, K, V))).astype(np.float32) if h0 else None
+    if grads:
+        d["do"] = rng.standard_normal((B, T, H, V)).astype(np.float32)
+        d["dht"] = (0.1 * rng.standard_normal((n0, H, K, V))).astype(np.float32)
+    return d
+
+
+def varlen_cu(T_total, N, seed):
+    """cu_seqlens [N+1] with seeded uniform-random cut points (generally not chunk-aligned)."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    cuts = np.sort(rng.choice(np.arange(1, T_total), N - 1, replace=False))
+    return [0] + [int(c) for c in cuts] + [T_total]
