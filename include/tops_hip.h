@@ -133,6 +133,37 @@ int tops_simple_gla_chunk_bwd(const void* q, const void* k, const void* v, const
                               int total_chunks, int B, int T, int H, int K, int V, int N,
                               int dtype, float scale, void* stream);
 
+/* Fused recurrent GLA forward: the per-token recurrence
+ *   h_t = h_{t-1} * exp(gk_t)[:,None] * exp(gv_t)[None,:] + k_t v_t^T,  o_t = h_t^T (scale q_t)
+ * over each sequence (reverse != 0: from its last token to its first).  Replaces
+ * tops.ops.gla.fused_recurrent_gla_fwd (tops/ops/gla/fused_recurrent.py:236-431, K5 :140-228)
+ * and the oracle tops/cpu/ops/gla/fused_recurrent.py:51-167, 362-422.
+ *   gk [B,T,H,K] fp32 or NULL; gv [B,T,H,V] fp32 or NULL; h0 [N,H,K,V] fp32 or NULL
+ *   o [B,T,H,V] (dtype); o32 [B,T,H,V] fp32 copy of o or NULL; ht [N,H,K,V] fp32 or NULL
+ * Limits: K <= 128, K % 4 == 0. */
+int tops_gla_fused_recurrent_fwd(const void* q, const void* k, const void* v, const float* gk,
+                                 const float* gv, const float* h0, void* o, float* o32, float* ht,
+                                 const int32_t* cu_seqlens, int B, int T, int H, int K, int V,
+                                 int N, int dtype, float scale, int reverse, void* stream);
+
+/* Bytes of the workspace tops_gla_fused_recurrent_bwd needs (with_gv: a gv gate is used). */
+int64_t tops_gla_fused_recurrent_bwd_workspace(int B, int T, int H, int K, int V, int N,
+                                               int with_gv);
+
+/* Fused recurrent GLA backward: dq, dk, dv (dtype), dgk [B,T,H,K] / dgv [B,T,H,V] fp32 (when
+ * gk / gv are given; dgv needs the forward output o32 in fp32) and dh0 [N,H,K,V] fp32 or NULL.
+ * A forward replay gives dq and the final state, a reverse pass dk, dv and dh0, and the gate
+ * gradients are suffix sums of (q dq - k dk) / (o dO - v dv) plus the h_T * dht boundary
+ * term.  Replaces tops.ops.gla.fused_recurrent_gla_bwd (tops/ops/gla/fused_recurrent.py:
+ * 881-958; K6 :496-619; _compute_gate_grads :800-878) and the oracle
+ * tops/cpu/ops/gla/fused_recurrent.py:171-358.  workspace: see the size query above. */
+int tops_gla_fused_recurrent_bwd(const void* q, const void* k, const void* v, const float* gk,
+                                 const float* gv, const float* o32, const void* do_,
+                                 const float* dht, const float* h0, void* dq, void* dk, void* dv,
+                                 float* dgk, float* dgv, float* dh0, float* workspace,
+                                 const int32_t* cu_seqlens, int B, int T, int H, int K, int V,
+                                 int N, int dtype, float scale, int reverse, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

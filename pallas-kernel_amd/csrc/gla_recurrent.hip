@@ -1,0 +1,498 @@
+// Fused recurrent GLA for gfx950: the per-token recurrence, forward and backward.
+//
+// Replaces the reference's K5 _fused_recurrent_gla_fwd_kernel
+// (tops/ops/gla/fused_recurrent.py:140-372), K6 _fused_recurrent_gla_bwd_kernel (:496-750)
+// and _compute_gate_grads (:800-878), following the oracle
+// tops/cpu/ops/gla/fused_recurrent.py:51-358:
+//     h_t = h_{t-1} * exp(gk_t)[:, None] * exp(gv_t)[None, :] + k_t v_t^T
+//     o_t = h_t^T (scale q_t)
+// over t = bos..eos-1, or eos-1..bos with `reverse`, per sequence (varlen) and head.
+//
+// One workgroup (4 wave64) owns one (sequence, head, 32-wide V tile).  Thread (grp, col)
+// holds state rows grp*RG .. grp*RG + RG - 1 of column col in registers (RG = KP / 8).
+// Tokens are processed in blocks of 16: the block's q (pre-scaled), k, exp(gk), v and
+// exp(gv) are staged in LDS (the next block is prefetched into registers meanwhile), every
+// thread advances its rows token by token reading broadcast LDS values, and the
+// reductions over K (o, dv) are done once per block through LDS.  Reductions over V
+// within the tile (dq, dk) use a 32-lane reduce-scatter; the V tiles' partial sums are
+// added by the finishing kernel, which also forms the gate gradients as suffix sums.
+#include <stdio.h>
+
+#include "tops_common.h"
+#include "tops_hip.h"
+
+namespace tops {
+
+struct FrParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const float* gk;      // [B,T,H,K] or NULL
+  const float* gv;      // [B,T,H,V] or NULL
+  const float* s0;      // h0 (forward / replay) [N,H,K,V] or NULL
+  const float* dht;     // [N,H,K,V] or NULL (backward)
+  const void* dout;     // dO [B,T,H,V] (backward)
+  void* o;              // o [B,T,H,V] in the input dtype (forward)
+  float* o32;           // o in fp32 (forward, optional)
+  float* s_fin;         // ht (forward) / dh0 (backward) or NULL
+  float* h_fin;         // final state of the replay (backward) [N,H,K,V]
+  float* dq_part;       // [NV, B*T*H*K] fp32 (backward)
+  float* dk_part;       // [NV, B*T*H*K] fp32 (backward)
+  void* dv;             // [B,T,H,V] (backward)
+  float* dv32;          // fp32 copy of dv for the gv gradient, or NULL (backward)
+  const int* cu_seqlens;
+  int B, T, H, K, V, N, NV;
+  float scale;
+  int reverse;
+};
+
+constexpr int kFrBV = 32;   // V tile
+constexpr int kFrTB = 16;   // tokens per block
+
+__device__ __forceinline__ float ld_elem(const uint16_t* p, size_t i) { return bf16_to_f32(p[i]); }
+__device__ __forceinline__ float ld_elem(const float* p, size_t i) { return p[i]; }
+__device__ __forceinline__ void st_elem(uint16_t* p, size_t i, float x) { p[i] = f32_to_bf16(x); }
+__device__ __forceinline__ void st_elem(float* p, size_t i, float x) { p[i] = x; }
+
+// Sum of v[0..NR-1] over the 32 lanes of a half-wave, reduce-scattered (v is clobbered):
+// returns the total of row `row` (lanes 2j and 2j+1 of the half-wave get row j for
+// NR = 16; lanes 4j..4j+3 for NR = 8; lanes 8j..8j+7 for NR = 4).  NR in {4, 8, 16}.
+template <int NR>
+__device__ __forceinline__ float rs32(float (&v)[NR], int lane32, int& row) {
+  int n = NR, base = 0;
+#pragma unroll
+  for (int off = 16; off >= 1; off >>= 1) {
+    if (n > 1) {
+      const int h = n / 2;
+      const bool upper = (lane32 & off) != 0;
+#pragma unroll
+      for (int i = 0; i < NR / 2; ++i) {
+        if (i < h) {
+          const float mine = upper ? v[i + h] : v[i];
+          const float other = upper ? v[i] : v[i + h];
+          v[i] = mine + __shfl_xor(other, off, 64);
+        }
+      }
+      if (upper) base += h;
+      n = h;
+    } else {
+      v[0] += __shfl_xor(v[0], off, 64);
+    }
+  }
+  row = base;
+  return v[0];
+}
+
+template <typename TIn, int KP, bool BWD>
+__global__ __launch_bounds__(256) void fr_kernel(FrParams p) {
+  constexpr int BV = kFrBV, TB = kFrTB, RG = KP / 8;
+  constexpr int NE = TB * KP / 256;   // staged [TB][KP] elements per thread
+  __shared__ __attribute__((aligned(16))) float sq[TB][KP];
+  __shared__ __attribute__((aligned(16))) float sk[TB][KP];
+  __shared__ __attribute__((aligned(16))) float sd[TB][KP];
+  __shared__ float sv[TB][BV];
+  __shared__ float sgv[TB][BV];
+  __shared__ float sdo[TB][BV];
+  __shared__ float sred[8][TB][BV];
+  __shared__ __attribute__((aligned(16))) float sdqk[TB][KP];
+
+  const int tid = threadIdx.x;
+  const int col = tid & 31, grp = tid >> 5, lane32 = tid & 31;
+  const int r0 = grp * RG;
+  const int wg = blockIdx.x;
+  const int vt = wg % p.NV;
+  const int hh = (wg / p.NV) % p.H;
+  const int n = wg / (p.NV * p.H);
+  const int H = p.H, K = p.K, V = p.V;
+  const int vc = vt * BV + col;
+  const bool colok = vc < V;
+
+  int bos, L;
+  if (p.cu_seqlens) {
+    bos = p.cu_seqlens[n];
+    L = p.cu_seqlens[n + 1] - bos;
+  } else {
+    bos = n * p.T;
+    L = p.T;
+  }
+  const int nblk = cdiv(L, TB);
+  const TIn* q = (const TIn*)p.q;
+  const TIn* kk = (const TIn*)p.k;
+  const TIn* v = (const TIn*)p.v;
+  const TIn* dout = (const TIn*)p.dout;
+  const size_t sbase = ((size_t)n * H + hh) * K * V;
+
+  // time index of the j-th token of block b in processing order
+  auto tok = [&](int b, int j) { return p.reverse ? bos + L - 1 - (b * TB + j) : bos + b * TB + j; };
+
+  // ---- raw block registers (prefetch)
+  float rq[NE], rk[NE], rg[NE], rv[2], rgv[2], rdo[2];
+  auto load_block = [&](int b) {
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      const int e = tid + 256 * i, j = e / KP, row = e % KP;
+      const bool ok = (b * TB + j < L) && row < K;
+      const size_t off = ((size_t)(ok ? tok(b, j) : bos) * H + hh) * K + (ok ? row : 0);
+      rq[i] = ok ? ld_elem(q, off) : 0.f;
+      rk[i] = ok ? ld_elem(kk, off) : 0.f;
+      rg[i] = (ok && p.gk) ? p.gk[off] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + 256 * i, j = e / BV, c = e % BV, vv = vt * BV + c;
+      const bool ok = (b * TB + j < L) && vv < V;
+      const size_t off = ((size_t)(ok ? tok(b, j) : bos) * H + hh) * V + (ok ? vv : 0);
+      rv[i] = ok ? ld_elem(v, off) : 0.f;
+      rgv[i] = (ok && p.gv) ? p.gv[off] : 0.f;
+      if constexpr (BWD) rdo[i] = ok ? ld_elem(dout, off) : 0.f;
+    }
+  };
+  auto stage_block = [&]() {
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      const int e = tid + 256 * i, j = e / KP, row = e % KP;
+      sq[j][row] = rq[i] * p.scale;
+      sk[j][row] = rk[i];
+      sd[j][row] = fast_exp2(rg[i] * kLog2e);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + 256 * i, j = e / BV, c = e % BV;
+      sv[j][c] = rv[i];
+      sgv[j][c] = fast_exp2(rgv[i] * kLog2e);
+      if constexpr (BWD) sdo[j][c] = rdo[i];
+    }
+  };
+
+  // ================= forward (or the backward's replay pass)
+  float h[RG];
+#pragma unroll
+  for (int r = 0; r < RG; ++r) {
+    const int kr = r0 + r;
+    h[r] = (p.s0 && kr < K && colok) ? p.s0[sbase + (size_t)kr * V + vc] : 0.f;
+  }
+  load_block(0);
+  for (int b = 0; b < nblk; ++b) {
+    stage_block();
+    __syncthreads();
+    if (b + 1 < nblk) load_block(b + 1);
+#pragma unroll
+    for (int j = 0; j < TB; ++j) {
+      const float vj = sv[j][col], gvj = sgv[j][col];
+      float acc = 0.f;
+      float pr[RG];
+#pragma unroll
+      for (int r4 = 0; r4 < RG; r4 += 4) {
+        const float4 d4 = *(const float4*)&sd[j][r0 + r4];
+        const float4 k4 = *(const float4*)&sk[j][r0 + r4];
+        const float4 q4 = *(const float4*)&sq[j][r0 + r4];
+        const float dd[4] = {d4.x, d4.y, d4.z, d4.w}, ks[4] = {k4.x, k4.y, k4.z, k4.w};
+        const float qs[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          h[r4 + u] = h[r4 + u] * (dd[u] * gvj) + ks[u] * vj;
+          acc += h[r4 + u] * qs[u];
+        }
+      }
+      if constexpr (BWD) {
+        // dq_t[k] = scale sum_v h_t[k][v] dO_t[v] over this tile's columns
+        const float dj = sdo[j][col] * p.scale;
+#pragma unroll
+        for (int r = 0; r < RG; ++r) pr[r] = h[r] * dj;
+        int row;
+        const float s = rs32<RG>(pr, lane32, row);
+        if ((lane32 & ((32 / RG) - 1)) == 0) sdqk[j][r0 + row] = s;
+      } else {
+        sred[grp][j][col] = acc;
+      }
+    }
+    __syncthreads();
+    if constexpr (!BWD) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int e = tid + 256 * i, j = e / BV, c = e % BV, vv = vt * BV + c;
+        float s = 0.f;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) s += sred[g][j][c];
+        if (b * TB + j < L && vv < V) {
+          const size_t off = ((size_t)tok(b, j) * H + hh) * V + vv;
+          st_elem((TIn*)p.o, off, s);
+          if (p.o32) p.o32[off] = s;
+        }
+      }
+    } else {
+      // dq partial of this V tile
+#pragma unroll
+      for (int i = 0; i < NE; ++i) {
+        const int e = tid + 256 * i, j = e / KP, row = e % KP;
+        if (b * TB + j < L && row < K)
+          p.dq_part[(size_t)vt * ((size_t)p.B * p.T * H * K) + ((size_t)tok(b, j) * H + hh) * K + row] = sdqk[j][row];
+      }
+    }
+    __syncthreads();
+  }
+  if (!BWD && p.s_fin) {
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {
+      const int kr = r0 + r;
+      if (kr < K && colok) p.s_fin[sbase + (size_t)kr * V + vc] = h[r];
+    }
+  }
+  if constexpr (BWD) {
+    if (p.h_fin) {
+#pragma unroll
+      for (int r = 0; r < RG; ++r) {
+        const int kr = r0 + r;
+        if (kr < K && colok) p.h_fin[sbase + (size_t)kr * V + vc] = h[r];
+      }
+    }
+    // ================= backward: reverse of the processing order
+    float dh[RG];
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {
+      const int kr = r0 + r;
+      dh[r] = (p.dht && kr < K && colok) ? p.dht[sbase + (size_t)kr * V + vc] : 0.f;
+    }
+    load_block(nblk - 1);
+    for (int b = nblk - 1; b >= 0; --b) {
+      stage_block();
+      __syncthreads();
+      if (b > 0) load_block(b - 1);
+#pragma unroll 2
+      for (int jj = 0; jj < TB; ++jj) {
+        const int j = TB - 1 - jj;
+        const float vj = sv[j][col], gvj = sgv[j][col], dj = sdo[j][col];
+        float acc = 0.f, pr[RG];
+#pragma unroll
+        for (int r4 = 0; r4 < RG; r4 += 4) {
+          const float4 k4 = *(const float4*)&sk[j][r0 + r4];
+          const float4 q4 = *(const float4*)&sq[j][r0 + r4];
+          const float ks[4] = {k4.x, k4.y, k4.z, k4.w}, qs[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            dh[r4 + u] += qs[u] * dj;                 // dh += (scale q) dO^T
+            pr[r4 + u] = dh[r4 + u] * vj;             // dk_t = dh v_t
+            acc += dh[r4 + u] * ks[u];                // dv_t = dh^T k_t
+          }
+        }
+        int row;
+        const float s = rs32<RG>(pr, lane32, row);
+        if ((lane32 & ((32 / RG) - 1)) == 0) sdqk[j][r0 + row] = s;
+        sred[grp][j][col] = acc;
+#pragma unroll
+        for (int r4 = 0; r4 < RG; r4 += 4) {
+          const float4 d4 = *(const float4*)&sd[j][r0 + r4];
+          const float dd[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) dh[r4 + u] *= dd[u] * gvj;
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int e = tid + 256 * i, j = e / BV, c = e % BV, vv = vt * BV + c;
+        float s = 0.f;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) s += sred[g][j][c];
+        if (b * TB + j < L && vv < V) {
+          const size_t off = ((size_t)tok(b, j) * H + hh) * V + vv;
+          st_elem((TIn*)p.dv, off, s);
+          if (p.dv32) p.dv32[off] = s;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < NE; ++i) {
+        const int e = tid + 256 * i, j = e / KP, row = e % KP;
+        if (b * TB + j < L && row < K)
+          p.dk_part[(size_t)vt * ((size_t)p.B * p.T * H * K) + ((size_t)tok(b, j) * H + hh) * K + row] = sdqk[j][row];
+      }
+      __syncthreads();
+    }
+    if (p.s_fin) {
+#pragma unroll
+      for (int r = 0; r < RG; ++r) {
+        const int kr = r0 + r;
+        if (kr < K && colok) p.s_fin[sbase + (size_t)kr * V + vc] = dh[r];
+      }
+    }
+  }
+}
+
+// Finishing kernel of the backward: one workgroup per (sequence, head).  Threads
+// 0..K-1 sum the V-tile partials of dq and dk (written in the input dtype) and form
+// dgk_t = sum over later-processed tokens s >= t of (q dq - k dk)_s + sum_v(h_T dht);
+// threads 128..128+V-1 form dgv_t = sum_{s >= t} (o dO - v dv)_s + sum_k(h_T dht).
+struct FrFinishParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const float* o32;
+  const void* dout;
+  const float* dv32;
+  const float* dht;
+  const float* h_fin;
+  const float* dq_part;
+  const float* dk_part;
+  void* dq;
+  void* dk;
+  float* dgk;
+  float* dgv;
+  const int* cu_seqlens;
+  int B, T, H, K, V, N, NV;
+  int reverse;
+};
+
+template <typename TIn>
+__global__ __launch_bounds__(256) void fr_finish_kernel(FrFinishParams p) {
+  const int tid = threadIdx.x;
+  const int hh = blockIdx.x % p.H, n = blockIdx.x / p.H;
+  const int H = p.H, K = p.K, V = p.V;
+  int bos, L;
+  if (p.cu_seqlens) {
+    bos = p.cu_seqlens[n];
+    L = p.cu_seqlens[n + 1] - bos;
+  } else {
+    bos = n * p.T;
+    L = p.T;
+  }
+  const size_t sbase = ((size_t)n * H + hh) * K * V;
+  const size_t plane = (size_t)p.B * p.T * H * K;
+  if (tid < 128) {
+    const int kr = tid;
+    if (kr >= K) return;
+    float bnd = 0.f;
+    if (p.dgk && p.dht) {
+      for (int vv = 0; vv < V; ++vv) bnd += p.h_fin[sbase + (size_t)kr * V + vv] * p.dht[sbase + (size_t)kr * V + vv];
+    }
+    float run = 0.f;
+    for (int s = L - 1; s >= 0; --s) {          // s: position in processing order
+      const int t = p.reverse ? bos + L - 1 - s : bos + s;
+      const size_t off = ((size_t)t * H + hh) * K + kr;
+      float dq = 0.f, dk = 0.f;
+      for (int i = 0; i < p.NV; ++i) {
+        dq += p.dq_part[i * plane + off];
+        dk += p.dk_part[i * plane + off];
+      }
+      st_elem((TIn*)p.dq, off, dq);
+      st_elem((TIn*)p.dk, off, dk);
+      if (p.dgk) {
+        run += ld_elem((const TIn*)p.q, off) * dq - ld_elem((const TIn*)p.k, off) * dk;
+        p.dgk[off] = run + bnd;
+      }
+    }
+  } else {
+    if (!p.dgv) return;
+    for (int vv = tid - 128; vv < V; vv += 128) {
+    float bnd = 0.f;
+    if (p.dht) {
+      for (int kr = 0; kr < K; ++kr) bnd += p.h_fin[sbase + (size_t)kr * V + vv] * p.dht[sbase + (size_t)kr * V + vv];
+    }
+    float run = 0.f;
+    for (int s = L - 1; s >= 0; --s) {
+      const int t = p.reverse ? bos + L - 1 - s : bos + s;
+      const size_t off = ((size_t)t * H + hh) * V + vv;
+      run += p.o32[off] * ld_elem((const TIn*)p.dout, off) - ld_elem((const TIn*)p.v, off) * p.dv32[off];
+      p.dgv[off] = run + bnd;
+    }
+    }
+  }
+}
+
+template <typename TIn, bool BWD>
+static hipError_t launch_fr(const FrParams& p, hipStream_t s) {
+  const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
+  dim3 grid(p.NV * p.H * p.N);
+  if (kp == 32) hipLaunchKernelGGL((fr_kernel<TIn, 32, BWD>), grid, dim3(256), 0, s, p);
+  else if (kp == 64) hipLaunchKernelGGL((fr_kernel<TIn, 64, BWD>), grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((fr_kernel<TIn, 128, BWD>), grid, dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+static int fr_check(const char* who, int B, int T, int H, int K, int V, int N,
+                    const int32_t* cu_seqlens, int dtype) {
+  char msg[160];
+  if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || N <= 0) {
+    snprintf(msg, sizeof(msg), "%s: non-positive dimension", who);
+    return tops_set_error(TOPS_ERR_SHAPE, msg);
+  }
+  if (K > 128 || (K % 4)) {
+    snprintf(msg, sizeof(msg), "%s: need K <= 128 and K % 4 == 0", who);
+    return tops_set_error(TOPS_ERR_SHAPE, msg);
+  }
+  if (cu_seqlens && B != 1) {
+    snprintf(msg, sizeof(msg), "%s: varlen needs B == 1", who);
+    return tops_set_error(TOPS_ERR_SHAPE, msg);
+  }
+  if (!cu_seqlens && N != B) {
+    snprintf(msg, sizeof(msg), "%s: N must equal B", who);
+    return tops_set_error(TOPS_ERR_SHAPE, msg);
+  }
+  if (dtype != TOPS_BF16 && dtype != TOPS_F32) {
+    snprintf(msg, sizeof(msg), "%s: dtype must be TOPS_F32 or TOPS_BF16", who);
+    return tops_set_error(TOPS_ERR_DTYPE, msg);
+  }
+  return TOPS_OK;
+}
+
+}  // namespace tops
+
+using namespace tops;
+
+extern "C" int64_t tops_gla_fused_recurrent_bwd_workspace(int B, int T, int H, int K, int V, int N,
+                                                         int with_gv) {
+  const int64_t NV = (V + kFrBV - 1) / kFrBV;
+  return (2 * NV * (int64_t)B * T * H * K + (int64_t)N * H * K * V +
+          (with_gv ? (int64_t)B * T * H * V : 0)) * 4;
+}
+
+extern "C" int tops_gla_fused_recurrent_fwd(const void* q, const void* k, const void* v,
+                                            const float* gk, const float* gv, const float* h0,
+                                            void* o, float* o32, float* ht,
+                                            const int32_t* cu_seqlens, int B, int T, int H, int K,
+                                            int V, int N, int dtype, float scale, int reverse,
+                                            void* stream) {
+  if (!q || !k || !v || !o) return tops_set_error(TOPS_ERR_NULL, "gla_fused_recurrent_fwd: null tensor");
+  int rc = fr_check("gla_fused_recurrent_fwd", B, T, H, K, V, N, cu_seqlens, dtype);
+  if (rc != TOPS_OK) return rc;
+  FrParams p{q, k, v, gk, gv, h0, nullptr, nullptr, o, o32, ht, nullptr, nullptr, nullptr, nullptr,
+             nullptr, cu_seqlens, B, T, H, K, V, N, (V + kFrBV - 1) / kFrBV, scale, reverse ? 1 : 0};
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = dtype == TOPS_BF16 ? launch_fr<uint16_t, false>(p, s) : launch_fr<float, false>(p, s);
+  if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
+  return TOPS_OK;
+}
+
+extern "C" int tops_gla_fused_recurrent_bwd(const void* q, const void* k, const void* v,
+                                            const float* gk, const float* gv, const float* o32,
+                                            const void* do_, const float* dht, const float* h0,
+                                            void* dq, void* dk, void* dv, float* dgk, float* dgv,
+                                            float* dh0, float* workspace,
+                                            const int32_t* cu_seqlens, int B, int T, int H, int K,
+                                            int V, int N, int dtype, float scale, int reverse,
+                                            void* stream) {
+  if (!q || !k || !v || !do_ || !dq || !dk || !dv || !workspace)
+    return tops_set_error(TOPS_ERR_NULL, "gla_fused_recurrent_bwd: null tensor");
+  if ((gk && !dgk) || (gv && (!dgv || !o32)))
+    return tops_set_error(TOPS_ERR_NULL, "gla_fused_recurrent_bwd: gate gradients need dgk / dgv (and o)");
+  int rc = fr_check("gla_fused_recurrent_bwd", B, T, H, K, V, N, cu_seqlens, dtype);
+  if (rc != TOPS_OK) return rc;
+  const int NV = (V + kFrBV - 1) / kFrBV;
+  float* dq_part = workspace;
+  float* dk_part = dq_part + (size_t)NV * B * T * H * K;
+  float* h_fin = dk_part + (size_t)NV * B * T * H * K;
+  float* dv32 = gv ? h_fin + (size_t)N * H * K * V : nullptr;
+  FrParams p{q, k, v, gk, gv, h0, dht, do_, nullptr, nullptr, dh0, h_fin, dq_part, dk_part, dv, dv32,
+             cu_seqlens, B, T, H, K, V, N, NV, scale, reverse ? 1 : 0};
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = dtype == TOPS_BF16 ? launch_fr<uint16_t, true>(p, s) : launch_fr<float, true>(p, s);
+  if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
+  FrFinishParams f{q, k, v, o32, do_, dv32, dht, h_fin, dq_part, dk_part, dq, dk, gk ? dgk : nullptr,
+                   gv ? dgv : nullptr, cu_seqlens, B, T, H, K, V, N, NV, reverse ? 1 : 0};
+  if (dtype == TOPS_BF16)
+    hipLaunchKernelGGL((fr_finish_kernel<uint16_t>), dim3(H * N), dim3(256), 0, s, f);
+  else
+    hipLaunchKernelGGL((fr_finish_kernel<float>), dim3(H * N), dim3(256), 0, s, f);
+  e = hipGetLastError();
+  if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
+  return TOPS_OK;
+}

@@ -33,6 +33,8 @@ SIGNATURES = {
                                 _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp],
     "tops_simple_gla_chunk_fwd": [_vp] * 11 + [_i32] * 7 + [_f32, _vp],
     "tops_simple_gla_chunk_bwd": [_vp] * 17 + [_i32] * 8 + [_f32, _vp],
+    "tops_gla_fused_recurrent_fwd": [_vp] * 10 + [_i32] * 7 + [_f32, _i32, _vp],
+    "tops_gla_fused_recurrent_bwd": [_vp] * 17 + [_i32] * 7 + [_f32, _i32, _vp],
     "tops_prepare_chunk_indices": [_vp, _i32, _i32, _vp, _vp, _i32],
 }
 
@@ -56,6 +58,8 @@ def lib() -> ctypes.CDLL:
         L.tops_version.restype = ctypes.c_char_p
         L.tops_gla_state_bytes.restype = ctypes.c_int64
         L.tops_gla_state_bytes.argtypes = [_i32, _i32, _i32, _i32]
+        L.tops_gla_fused_recurrent_bwd_workspace.restype = ctypes.c_int64
+        L.tops_gla_fused_recurrent_bwd_workspace.argtypes = [_i32] * 7
         _lib = L
     return _lib
 

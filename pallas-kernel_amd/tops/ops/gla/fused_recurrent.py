@@ -1,0 +1,146 @@
+"""Fused recurrent GLA on MI355X: drop-in for tops.ops.gla.fused_recurrent
+(tops/ops/gla/fused_recurrent.py) with the dtype contract of the reference's CPU tier
+(tops/cpu/ops/gla/fused_recurrent.py:6-28, 362-422): o in q.dtype, ht fp32.
+
+    h_t = h_{t-1} * exp(gk_t)[:, None] * exp(gv_t)[None, :] + k_t v_t^T
+    o_t = h_t^T (scale * q_t)
+
+`fused_recurrent_gla` is differentiable (torch.autograd.Function over the HIP backward:
+forward replay, reverse pass and gate-gradient suffix sums), covering gk, gv, reverse,
+initial_state and cu_seqlens.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from ... import _native as N
+
+
+def _cu_dev(cu_seqlens, device):
+    if cu_seqlens is None:
+        return None
+    if isinstance(cu_seqlens, torch.Tensor):
+        return cu_seqlens.to(device=device, dtype=torch.int32).contiguous()
+    return torch.from_numpy(np.ascontiguousarray(np.asarray(cu_seqlens, np.int32))).to(device)
+
+
+def _check(q, k, v, gk, gv, initial_state, cu_seqlens):
+    assert q.ndim == 4, f"q must be [B,T,H,K], got {tuple(q.shape)}"
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    n = len(cu_seqlens) - 1 if cu_seqlens is not None else B
+    assert tuple(k.shape) == (B, T, H, K), f"k shape {tuple(k.shape)} != expected {(B, T, H, K)}"
+    assert v.ndim == 4 and tuple(v.shape[:3]) == (B, T, H), f"v shape {tuple(v.shape)} incompatible with q"
+    assert gk is None or tuple(gk.shape) == (B, T, H, K), f"gk shape {tuple(gk.shape)} != expected {(B, T, H, K)}"
+    assert gv is None or tuple(gv.shape) == (B, T, H, V), f"gv shape {tuple(gv.shape)} != expected {(B, T, H, V)}"
+    assert initial_state is None or tuple(initial_state.shape) == (n, H, K, V), (
+        f"initial_state shape {tuple(initial_state.shape)} != expected {(n, H, K, V)}")
+    assert cu_seqlens is None or B == 1, f"cu_seqlens requires B=1, got B={B}"
+    assert q.dtype == k.dtype == v.dtype, "q, k, v must share a dtype"
+    if K > 128 or K % 4:
+        raise NotImplementedError(f"tops-hip fused recurrent kernels need K <= 128, K % 4 == 0 (got K={K})")
+    N.require_cuda(q, k, v, gk, gv, initial_state)
+    return B, T, H, K, V, n
+
+
+def _f32(x):
+    return None if x is None else x.contiguous().to(torch.float32)
+
+
+def _fwd(q, k, v, gk32, gv32, h032, scale, output_final_state, reverse, cu, n, want_o32):
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    o = torch.empty_like(v)
+    o32 = torch.empty(B, T, H, V, device=q.device, dtype=torch.float32) if want_o32 else None
+    ht = torch.empty(n, H, K, V, device=q.device, dtype=torch.float32) if output_final_state else None
+    N.call("tops_gla_fused_recurrent_fwd", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gk32), N.ptr(gv32),
+           N.ptr(h032), N.ptr(o), N.ptr(o32), N.ptr(ht), N.ptr(cu), B, T, H, K, V, n,
+           N.dtype_code(q.dtype), float(scale), int(bool(reverse)), N.stream())
+    return o, o32, ht
+
+
+def _bwd(q, k, v, gk32, gv32, o32, do, dht32, h032, scale, reverse, cu, n):
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dgk = torch.empty(B, T, H, K, device=q.device, dtype=torch.float32) if gk32 is not None else None
+    dgv = torch.empty(B, T, H, V, device=q.device, dtype=torch.float32) if gv32 is not None else None
+    dh0 = torch.empty(n, H, K, V, device=q.device, dtype=torch.float32) if h032 is not None else None
+    ws_bytes = N.lib().tops_gla_fused_recurrent_bwd_workspace(B, T, H, K, V, n,
+                                                              int(gv32 is not None))
+    ws = torch.empty((ws_bytes + 3) // 4, device=q.device, dtype=torch.float32)
+    N.call("tops_gla_fused_recurrent_bwd", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gk32), N.ptr(gv32),
+           N.ptr(o32), N.ptr(do), N.ptr(dht32), N.ptr(h032), N.ptr(dq), N.ptr(dk), N.ptr(dv),
+           N.ptr(dgk), N.ptr(dgv), N.ptr(dh0), N.ptr(ws), N.ptr(cu), B, T, H, K, V, n,
+           N.dtype_code(q.dtype), float(scale), int(bool(reverse)), N.stream())
+    return dq, dk, dv, dgk, dgv, dh0
+
+
+class _FusedRecurrentGLA(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, gk, gv, h0, scale, output_final_state, reverse, cu_seqlens):
+        q, k, v = (x.contiguous() for x in (q, k, v))
+        gk32, gv32, h032 = _f32(gk), _f32(gv), _f32(h0)
+        cu = _cu_dev(cu_seqlens, q.device)
+        n = len(cu_seqlens) - 1 if cu_seqlens is not None else q.shape[0]
+        train = any(ctx.needs_input_grad[:6])
+        o, o32, ht = _fwd(q, k, v, gk32, gv32, h032, scale, output_final_state, reverse, cu, n,
+                          want_o32=train and gv is not None)
+        if train:
+            ctx.save_for_backward(q, k, v, gk32, gv32, h032, o32)
+            ctx.meta = (scale, reverse, cu, n)
+            ctx.dtypes = tuple(None if x is None else x.dtype for x in (gk, gv, h0))
+        return o, ht
+
+    @staticmethod
+    def backward(ctx, do, dht):
+        q, k, v, gk32, gv32, h032, o32 = ctx.saved_tensors
+        scale, reverse, cu, n = ctx.meta
+        dq, dk, dv, dgk, dgv, dh0 = _bwd(q, k, v, gk32, gv32, o32, do.contiguous().to(q.dtype),
+                                         _f32(dht), h032, scale, reverse, cu, n)
+        gdt, vdt, hdt = ctx.dtypes
+        dgk = None if dgk is None else dgk.to(gdt)
+        dgv = None if dgv is None else dgv.to(vdt)
+        dh0 = None if dh0 is None else dh0.to(hdt)
+        return dq, dk, dv, dgk, dgv, dh0, None, None, None, None
+
+
+def fused_recurrent_gla(q, k, v, gk=None, gv=None, scale=None, initial_state=None,
+                        output_final_state=False, reverse=False, cu_seqlens=None):
+    """tops/ops/gla/fused_recurrent.py:439-482 (CPU dtype contract: o in q.dtype).
+    Returns (o [B,T,H,V], ht [N,H,K,V] fp32 or None)."""
+    _check(q, k, v, gk, gv, initial_state, cu_seqlens)
+    if scale is None:
+        scale = q.shape[-1] ** -0.5
+    o, ht = _FusedRecurrentGLA.apply(q, k, v, gk, gv, initial_state, float(scale),
+                                     bool(output_final_state), bool(reverse), cu_seqlens)
+    return o, (ht if output_final_state else None)
+
+
+def fused_recurrent_gla_fwd(q, k, v, gk=None, gv=None, scale=None, initial_state=None,
+                            output_final_state=False, reverse=False, cu_seqlens=None):
+    """tops/ops/gla/fused_recurrent.py:380-431.  Returns (o, ht), o in q.dtype."""
+    B, T, H, K, V, n = _check(q, k, v, gk, gv, initial_state, cu_seqlens)
+    if scale is None:
+        scale = K ** -0.5
+    o, _, ht = _fwd(q.contiguous(), k.contiguous(), v.contiguous(), _f32(gk), _f32(gv),
+                    _f32(initial_state), scale, output_final_state, reverse,
+                    _cu_dev(cu_seqlens, q.device), n, want_o32=False)
+    return o, ht
+
+
+def fused_recurrent_gla_bwd(q, k, v, gk=None, gv=None, o=None, do=None, dht=None, scale=None,
+                            initial_state=None, reverse=False, cu_seqlens=None):
+    """tops/ops/gla/fused_recurrent.py:881-958.  Returns (dq, dk, dv, dgk, dgv, dh0):
+    dq/dk/dv in the input dtype, dgk/dgv fp32 (None without the gate), dh0 fp32 (None
+    without initial_state).  `o` (the forward output) is required when gv is given."""
+    B, T, H, K, V, n = _check(q, k, v, gk, gv, initial_state, cu_seqlens)
+    assert do is not None and tuple(do.shape) == (B, T, H, V)
+    assert dht is None or tuple(dht.shape) == (n, H, K, V)
+    assert gv is None or o is not None, "o (forward output) is required when gv is used"
+    if scale is None:
+        scale = K ** -0.5
+    return _bwd(q.contiguous(), k.contiguous(), v.contiguous(), _f32(gk), _f32(gv), _f32(o),
+                do.contiguous().to(q.dtype), _f32(dht), _f32(initial_state), scale, reverse,
+                _cu_dev(cu_seqlens, q.device), n)
