@@ -96,6 +96,63 @@ def cpu_baseline(repeats=3, heads=4):
                       f"tokens/s scaled to H={H}"}
 
 
+def _time(fn, iters, warmup=2):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / iters
+
+
+def secondary(dev, iters=10):
+    """The other BASELINE configs that fit one GPU, measured the same way (inputs resident,
+    synchronise around the timed iterations): config 2 (fused_recurrent_gla forward) and
+    config 4 (simple GLA, varlen, forward + backward)."""
+    import torch
+    import numpy as np
+    from tops.ops.gla import fused_recurrent_gla
+    from tops.ops.simple_gla import chunk_simple_gla
+    out = []
+    gen = torch.Generator(device=dev).manual_seed(1002)
+    bf = torch.bfloat16
+    # config 2: B16 T2048 H8 K=V=128, bf16 q/k/v, fp32 gk and h0; o + final state
+    B2, T2, H2, D2 = 16, 2048, 8, 128
+    q, k, v = (torch.randn(B2, T2, H2, D2, device=dev, generator=gen).to(bf) for _ in range(3))
+    gk = torch.nn.functional.logsigmoid(torch.randn(B2, T2, H2, D2, device=dev, generator=gen)) / 16
+    h0 = torch.randn(B2, H2, D2, D2, device=dev, generator=gen) * 0.1
+    with torch.no_grad():
+        sec = _time(lambda: fused_recurrent_gla(q, k, v, gk, initial_state=h0,
+                                                output_final_state=True), iters)
+    algo = 419_430_400
+    out.append({"config": "BASELINE config 2: fused_recurrent_gla fwd B16 T2048 H8 K=V=128 bf16",
+                "tokens_per_s": round(B2 * T2 / sec, 1), "ms": round(sec * 1e3, 4),
+                "algo_bytes": algo, "hbm_gbs": round(algo / sec / 1e9, 1),
+                "hbm_frac": round(algo / sec / 1e9 / HBM_PEAK_GBS, 4)})
+    del q, k, v, gk, h0
+    # config 4: simple GLA, T_total 16384 in 8 seeded varlen sequences, H32 K=V=128, bf16
+    T4, H4 = 16384, 32
+    rng = np.random.Generator(np.random.PCG64(1004))
+    cu = [0] + sorted(int(c) for c in rng.choice(np.arange(1, T4), 7, replace=False)) + [T4]
+    q, k, v = (torch.randn(1, T4, H4, D2, device=dev, generator=gen).to(bf).requires_grad_()
+               for _ in range(3))
+    g = torch.nn.functional.logsigmoid(torch.randn(1, T4, H4, device=dev, generator=gen)).requires_grad_()
+    do = torch.randn(1, T4, H4, D2, device=dev, generator=gen).to(bf)
+
+    def step4():
+        o, _ = chunk_simple_gla(q, k, v, None, g=g, cu_seqlens=cu)
+        return torch.autograd.grad(o, (q, k, v, g), do)
+    sec = _time(step4, iters)
+    out.append({"config": "BASELINE config 4: chunk_simple_gla fwd+bwd, varlen T16384 (8 seqs) "
+                          "H32 K=V=128 bf16, per-token g",
+                "tokens_per_s": round(T4 / sec, 1), "ms": round(sec * 1e3, 4),
+                "hbm_floor_ms": round(1.483e9 / (HBM_PEAK_GBS * 1e9) * 1e3, 4)})
+    return out
+
+
 def traffic_from_profiles(kernel):
     """HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
     (calibrated against a copy kernel), if the committed summary holds the kernel."""
@@ -113,6 +170,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-secondary", action="store_true", help="skip the config 2 / 4 lines")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the GLA hot path shards over (batch, head) "
@@ -175,6 +233,7 @@ def main():
            "config": {"workload": "chunk_gla fwd+bwd (BASELINE config 3)", "B": B, "T": T,
                       "H": H, "K": K, "V": V, "chunk": C, "h0": True, "dht": True},
            "roofline": roofline, "path_roofline": path, "kernels": kern,
+           "secondary": None if a.no_secondary else secondary(dev),
            "cpu_baseline": None if a.no_cpu else cpu_baseline()}
     print(json.dumps(out), flush=True)
 

@@ -5,9 +5,14 @@
     h_t = h_{t-1} * exp(gk_t)[:, None] * exp(gv_t)[None, :] + k_t v_t^T
     o_t = h_t^T (scale * q_t)
 
-`fused_recurrent_gla` is differentiable (torch.autograd.Function over the HIP backward:
-forward replay, reverse pass and gate-gradient suffix sums), covering gk, gv, reverse,
-initial_state and cu_seqlens.
+`fused_recurrent_gla` is differentiable, covering gk, gv, reverse, initial_state and
+cu_seqlens.  Two HIP implementations of the same recurrence are used:
+  * without gv and in forward time order (the common case, and BASELINE config 2) the
+    recurrence is computed chunkwise on MFMA by the chunk kernels (gla_sweep.hip,
+    gla_dqkg.hip) -- the same sums, grouped by 64-token chunks;
+  * with gv or reverse=True, the per-token kernels of gla_recurrent.hip (state in
+    registers, one token at a time) run the forward, a replay + reverse backward and the
+    gate-gradient suffix sums.
 """
 from __future__ import annotations
 
@@ -106,13 +111,22 @@ class _FusedRecurrentGLA(torch.autograd.Function):
         return dq, dk, dv, dgk, dgv, dh0, None, None, None, None
 
 
+def _chunked(gv, reverse, K, V):
+    """Whether the chunk (MFMA) kernels compute this call."""
+    return gv is None and not reverse and K % 8 == 0 and V % 8 == 0 and V <= 128
+
+
 def fused_recurrent_gla(q, k, v, gk=None, gv=None, scale=None, initial_state=None,
                         output_final_state=False, reverse=False, cu_seqlens=None):
     """tops/ops/gla/fused_recurrent.py:439-482 (CPU dtype contract: o in q.dtype).
     Returns (o [B,T,H,V], ht [N,H,K,V] fp32 or None)."""
-    _check(q, k, v, gk, gv, initial_state, cu_seqlens)
+    B, T, H, K, V, n = _check(q, k, v, gk, gv, initial_state, cu_seqlens)
     if scale is None:
         scale = q.shape[-1] ** -0.5
+    if _chunked(gv, reverse, K, V):
+        from .chunk import chunk_gla
+        return chunk_gla(q, k, v, gk, scale=scale, initial_state=initial_state,
+                         output_final_state=output_final_state, cu_seqlens=cu_seqlens)
     o, ht = _FusedRecurrentGLA.apply(q, k, v, gk, gv, initial_state, float(scale),
                                      bool(output_final_state), bool(reverse), cu_seqlens)
     return o, (ht if output_final_state else None)
@@ -124,6 +138,10 @@ def fused_recurrent_gla_fwd(q, k, v, gk=None, gv=None, scale=None, initial_state
     B, T, H, K, V, n = _check(q, k, v, gk, gv, initial_state, cu_seqlens)
     if scale is None:
         scale = K ** -0.5
+    if _chunked(gv, reverse, K, V):
+        from .chunk import chunk_gla
+        return chunk_gla(q, k, v, gk, scale=scale, initial_state=initial_state,
+                         output_final_state=output_final_state, cu_seqlens=cu_seqlens)
     o, _, ht = _fwd(q.contiguous(), k.contiguous(), v.contiguous(), _f32(gk), _f32(gv),
                     _f32(initial_state), scale, output_final_state, reverse,
                     _cu_dev(cu_seqlens, q.device), n, want_o32=False)
@@ -141,6 +159,12 @@ def fused_recurrent_gla_bwd(q, k, v, gk=None, gv=None, o=None, do=None, dht=None
     assert gv is None or o is not None, "o (forward output) is required when gv is used"
     if scale is None:
         scale = K ** -0.5
+    if _chunked(gv, reverse, K, V):
+        from .chunk import chunk_gla_bwd
+        dq, dk, dv, dg, dh0 = chunk_gla_bwd(q, k, v, gk, None, None, scale, initial_state, None,
+                                            None, do, dht, cu_seqlens=cu_seqlens)
+        return dq, dk, dv, (dg if gk is not None else None), None, \
+            (dh0 if initial_state is not None else None)
     return _bwd(q.contiguous(), k.contiguous(), v.contiguous(), _f32(gk), _f32(gv), _f32(o),
                 do.contiguous().to(q.dtype), _f32(dht), _f32(initial_state), scale, reverse,
                 _cu_dev(cu_seqlens, q.device), n)

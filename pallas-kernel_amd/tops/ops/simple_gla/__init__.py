@@ -4,6 +4,7 @@ from __future__ import annotations
 from .chunk import (chunk_simple_gla, chunk_simple_gla_bwd, chunk_simple_gla_fwd,
                     chunk_simple_gla_fwd_varlen)
 from .fused_chunk import fused_chunk_simple_gla, fused_chunk_simple_gla_bwd, fused_chunk_simple_gla_fwd
+from .fused_recurrent import fused_recurrent_simple_gla
 
 
 def simple_gla(q, k, v, *args, g=None, g_gamma=None, scale=None, initial_state=None,
@@ -30,7 +31,6 @@ def simple_gla(q, k, v, *args, g=None, g_gamma=None, scale=None, initial_state=N
         return fn(q, k, v, g_gamma, initial_state=initial_state, scale=scale,
                   output_final_state=output_final_state, chunk_size=chunk_size)
     if mode in ("fused_recurrent", "naive"):
-        from .fused_recurrent import fused_recurrent_simple_gla
         return fused_recurrent_simple_gla(q, k, v, g=g, g_gamma=g_gamma, scale=scale,
                                           initial_state=initial_state,
                                           output_final_state=output_final_state, reverse=reverse,
@@ -48,4 +48,16 @@ __all__ = [
     "fused_chunk_simple_gla",
     "fused_chunk_simple_gla_fwd",
     "fused_chunk_simple_gla_bwd",
+    "fused_recurrent_simple_gla",
+    "simple_gla_naive",
 ]
+
+
+def simple_gla_naive(q, k, v, g=None, g_gamma=None, scale=None, initial_state=None,
+                     output_final_state=False, chunk_size=64, cu_seqlens_cpu=None):
+    """The reference's pure-JAX testing form (tops/ops/simple_gla/naive.py); here the
+    per-token recurrence on the HIP fused_recurrent kernels (same equations)."""
+    return fused_recurrent_simple_gla(q, k, v, g=g, g_gamma=g_gamma, scale=scale,
+                                      initial_state=initial_state,
+                                      output_final_state=output_final_state,
+                                      cu_seqlens=cu_seqlens_cpu)

@@ -1,0 +1,33 @@
+"""fused_recurrent_simple_gla on MI355X (tops/ops/simple_gla/fused_recurrent.py:146-240).
+
+The per-token simple-GLA recurrence h_t = h_{t-1} exp(g_t + g_gamma) + k_t v_t^T,
+o_t = h_t^T (scale q_t) is GLA's with the gate shared by all K channels, so it runs on
+tops.ops.gla.fused_recurrent_gla with the gate expanded over K.  The expansion is a
+broadcast view inside the autograd graph: the gradients w.r.t. g [B,T,H] and g_gamma [H]
+come back summed over the broadcast axes, which is the gradient of the reference's
+lax.scan (g and g_gamma may be combined, as in tops/cpu/ops/simple_gla/naive.py:113-125).
+"""
+from __future__ import annotations
+
+import torch
+
+from ..gla.fused_recurrent import fused_recurrent_gla
+
+
+def fused_recurrent_simple_gla(q, k, v, g=None, g_gamma=None, scale=None, initial_state=None,
+                               output_final_state=False, reverse=False, cu_seqlens=None):
+    """Returns (o [B,T,H,V] in q.dtype, final_state [N,H,K,V] fp32 or None)."""
+    B, T, H, K = q.shape
+    assert g is None or tuple(g.shape) == (B, T, H), f"g shape {tuple(g.shape)} != {(B, T, H)}"
+    assert g_gamma is None or tuple(g_gamma.shape) == (H,), f"g_gamma shape must be ({H},)"
+    gk = None
+    if g is not None:
+        gk = g.to(torch.float32)[..., None]
+    if g_gamma is not None:
+        gg = torch.as_tensor(g_gamma, device=q.device).to(torch.float32)[None, None, :, None]
+        gk = gg if gk is None else gk + gg
+    if gk is not None:
+        gk = gk.expand(B, T, H, K)
+    return fused_recurrent_gla(q, k, v, gk, None, scale=scale, initial_state=initial_state,
+                               output_final_state=output_final_state, reverse=reverse,
+                               cu_seqlens=cu_seqlens)

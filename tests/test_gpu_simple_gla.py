@@ -96,3 +96,32 @@ def test_dispatcher_modes(cuda_device):
     o2, _ = simple_gla(q, k, v, g_gamma=gg, mode="fused_chunk")
     o3, _ = chunk_simple_gla(q, k, v, gg)
     assert torch.equal(o1, o3) and torch.equal(o2, o3)
+
+
+@pytest.mark.parametrize("gates", ["g", "gamma", "both"])
+@pytest.mark.parametrize("reverse", [False, True])
+def test_fused_recurrent_simple_gla(gates, reverse, cuda_device):
+    """simple_gla(mode='fused_recurrent') vs the naive oracle (tops/cpu/ops/simple_gla/naive.py),
+    and its gradients vs the chunk oracle's (per-token g) on the time-flipped sequence."""
+    from tops.ops.simple_gla import simple_gla
+    B, T, H, K, V = 2, 50, 2, 32, 32
+    d = simple_gla_inputs(B, T, H, K, V, seed=17, h0=True, grads=True)
+    g = to_dev(d["g"], torch.float32, cuda_device).requires_grad_() if gates != "gamma" else None
+    gg = to_dev(d["g_gamma"], torch.float32, cuda_device).requires_grad_() if gates != "g" else None
+    q, k, v = (to_dev(d[x], torch.float32, cuda_device).requires_grad_() for x in "qkv")
+    h0 = to_dev(d["h0"], torch.float32, cuda_device)
+    o, ht = simple_gla(q, k, v, g=g, g_gamma=gg, initial_state=h0, output_final_state=True,
+                       reverse=reverse, mode="fused_recurrent")
+    fl = (lambda x: np.ascontiguousarray(x[:, ::-1])) if reverse else (lambda x: x)
+    gs = None if gates == "gamma" else d["g"]
+    gam = None if gates == "g" else d["g_gamma"]
+    ro, rht = S.naive_simple_gla(fl(d["q"]), fl(d["k"]), fl(d["v"]), g=None if gs is None else fl(gs),
+                                 g_gamma=gam, initial_state=d["h0"], output_final_state=True)
+    assert rel(host(o), fl(ro)) < 1e-4 and rel(host(ht), rht) < 1e-4
+    if gates == "g":
+        torch.autograd.backward((o, ht), (to_dev(d["do"], torch.float32, cuda_device),
+                                          to_dev(d["dht"], torch.float32, cuda_device)))
+        r = S.chunk_simple_gla_bwd(fl(d["q"]), fl(d["k"]), fl(d["v"]), fl(d["g"]), None, d["h0"],
+                                   fl(d["do"]), d["dht"], K ** -0.5)
+        for got, ref in zip((q.grad, k.grad, v.grad, g.grad), r[:4]):
+            assert rel(host(got), fl(ref)) < 1e-4
