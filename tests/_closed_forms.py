@@ -78,3 +78,38 @@ def rel(a, b):
     b = np.asarray(b, np.float64)
     den = np.linalg.norm(b.ravel())
     return np.linalg.norm((a - b).ravel()) / (den if den > 0 else 1.0)
+
+
+def kda_naive_torch(q, k, v, g, beta, h0=None, scale=None):
+    """Per-token gated delta rule in torch (differentiable), written from the recurrence
+    S' = S diag(exp g_t); S = S' + beta_t k_t (v_t - S'^T k_t)^T; o_t = S^T (scale q_t)."""
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    if scale is None:
+        scale = K ** -0.5
+    S = torch.zeros(B, H, K, V, dtype=q.dtype) if h0 is None else h0
+    outs = []
+    for t in range(T):
+        S = S * torch.exp(g[:, t])[..., None]
+        pred = torch.einsum("bhk,bhkv->bhv", k[:, t], S)
+        S = S + torch.einsum("bhk,bhv->bhkv", beta[:, t][..., None] * k[:, t], v[:, t] - pred)
+        outs.append(torch.einsum("bhk,bhkv->bhv", q[:, t] * scale, S))
+    return torch.stack(outs, 1), S
+
+
+def kda_grads(q, k, v, g, beta, h0, do, dht, scale=None):
+    """o, ht and the gradients of sum(o*do) + sum(ht*dht) through kda_naive_torch (fp64)."""
+    t = {n: torch.tensor(np.asarray(x, np.float64), requires_grad=True)
+         for n, x in dict(q=q, k=k, v=v, g=g, beta=beta).items()}
+    h0t = None if h0 is None else torch.tensor(np.asarray(h0, np.float64), requires_grad=True)
+    o, ht = kda_naive_torch(t["q"], t["k"], t["v"], t["g"], t["beta"], h0t, scale)
+    loss = (o * torch.tensor(np.asarray(do, np.float64))).sum()
+    if dht is not None:
+        loss = loss + (ht * torch.tensor(np.asarray(dht, np.float64))).sum()
+    loss.backward()
+    out = dict(o=o.detach().numpy(), ht=ht.detach().numpy())
+    for n in ("q", "k", "v", "g", "beta"):
+        out["d" + n] = t[n].grad.numpy()
+    if h0t is not None:
+        out["dh0"] = h0t.grad.numpy()
+    return out
