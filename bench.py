@@ -41,7 +41,7 @@ KERNELS = {
     "tops_gla_chunk_bwd_dh": dict(kernel="gla_sweep_kernel<rev>",
                                   bytes=_TH * (2 * K + 2 * K + 4 * K + 2 * V + 2 * V) + 2 * _S),
     # q, k, v, g, dO read; dq, dk, dg written
-    "tops_gla_chunk_bwd_dqkg": dict(kernel="gla_bwd_main_kernel",
+    "tops_gla_chunk_bwd_dqkg": dict(kernel="gla_dqkg_kernel",
                                     bytes=_TH * (2 * K + 2 * K + 2 * V + 4 * K + 2 * V
                                                  + 2 * K + 2 * K + 4 * K)),
 }
@@ -108,18 +108,28 @@ def _time(fn, iters, warmup=2):
     return (time.perf_counter() - t0) / iters
 
 
-def secondary(dev, iters=10):
+def secondary(dev, iters=10, configs=(2, 4, 5)):
     """The other BASELINE configs that fit one GPU, measured the same way (inputs resident,
-    synchronise around the timed iterations): config 2 (fused_recurrent_gla forward) and
-    config 4 (simple GLA, varlen, forward + backward)."""
+    synchronise around the timed iterations): config 2 (fused_recurrent_gla forward),
+    config 4 (simple GLA, varlen, forward + backward) and config 5 (KDA, forward +
+    backward)."""
     import torch
-    import numpy as np
-    from tops.ops.gla import fused_recurrent_gla
-    from tops.ops.simple_gla import chunk_simple_gla
     out = []
     gen = torch.Generator(device=dev).manual_seed(1002)
+    if 2 in configs:
+        out.append(_config2(dev, gen, iters))
+    if 4 in configs:
+        out.append(_config4(dev, gen, iters))
+    if 5 in configs:
+        out.append(_config5(dev, gen, iters))
+    return out
+
+
+def _config2(dev, gen, iters):
+    """config 2: B16 T2048 H8 K=V=128, bf16 q/k/v, fp32 gk and h0; o + final state."""
+    import torch
+    from tops.ops.gla import fused_recurrent_gla
     bf = torch.bfloat16
-    # config 2: B16 T2048 H8 K=V=128, bf16 q/k/v, fp32 gk and h0; o + final state
     B2, T2, H2, D2 = 16, 2048, 8, 128
     q, k, v = (torch.randn(B2, T2, H2, D2, device=dev, generator=gen).to(bf) for _ in range(3))
     gk = torch.nn.functional.logsigmoid(torch.randn(B2, T2, H2, D2, device=dev, generator=gen)) / 16
@@ -128,13 +138,19 @@ def secondary(dev, iters=10):
         sec = _time(lambda: fused_recurrent_gla(q, k, v, gk, initial_state=h0,
                                                 output_final_state=True), iters)
     algo = 419_430_400
-    out.append({"config": "BASELINE config 2: fused_recurrent_gla fwd B16 T2048 H8 K=V=128 bf16",
-                "tokens_per_s": round(B2 * T2 / sec, 1), "ms": round(sec * 1e3, 4),
-                "algo_bytes": algo, "hbm_gbs": round(algo / sec / 1e9, 1),
-                "hbm_frac": round(algo / sec / 1e9 / HBM_PEAK_GBS, 4)})
-    del q, k, v, gk, h0
-    # config 4: simple GLA, T_total 16384 in 8 seeded varlen sequences, H32 K=V=128, bf16
-    T4, H4 = 16384, 32
+    return {"config": "BASELINE config 2: fused_recurrent_gla fwd B16 T2048 H8 K=V=128 bf16",
+            "tokens_per_s": round(B2 * T2 / sec, 1), "ms": round(sec * 1e3, 4),
+            "algo_bytes": algo, "hbm_gbs": round(algo / sec / 1e9, 1),
+            "hbm_frac": round(algo / sec / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def _config4(dev, gen, iters):
+    """config 4: simple GLA, T_total 16384 in 8 seeded varlen sequences, H32 K=V=128, bf16."""
+    import numpy as np
+    import torch
+    from tops.ops.simple_gla import chunk_simple_gla
+    bf = torch.bfloat16
+    T4, H4, D2 = 16384, 32, 128
     rng = np.random.Generator(np.random.PCG64(1004))
     cu = [0] + sorted(int(c) for c in rng.choice(np.arange(1, T4), 7, replace=False)) + [T4]
     q, k, v = (torch.randn(1, T4, H4, D2, device=dev, generator=gen).to(bf).requires_grad_()
@@ -146,11 +162,40 @@ def secondary(dev, iters=10):
         o, _ = chunk_simple_gla(q, k, v, None, g=g, cu_seqlens=cu)
         return torch.autograd.grad(o, (q, k, v, g), do)
     sec = _time(step4, iters)
-    out.append({"config": "BASELINE config 4: chunk_simple_gla fwd+bwd, varlen T16384 (8 seqs) "
-                          "H32 K=V=128 bf16, per-token g",
-                "tokens_per_s": round(T4 / sec, 1), "ms": round(sec * 1e3, 4),
-                "hbm_floor_ms": round(1.483e9 / (HBM_PEAK_GBS * 1e9) * 1e3, 4)})
-    return out
+    return {"config": "BASELINE config 4: chunk_simple_gla fwd+bwd, varlen T16384 (8 seqs) "
+                      "H32 K=V=128 bf16, per-token g",
+            "tokens_per_s": round(T4 / sec, 1), "ms": round(sec * 1e3, 4),
+            "hbm_floor_ms": round(1.483e9 / (HBM_PEAK_GBS * 1e9) * 1e3, 4)}
+
+
+def _config5(dev, gen, iters):
+    """config 5: KDA B4 T8192 H32 K=V=128; q, k L2-normalised, bf16 q/k/v, fp32 g, beta."""
+    import torch
+    from tops.ops.kda import chunk_kda
+    bf = torch.bfloat16
+    B5, T5, H5, D2 = 4, 8192, 32, 128
+
+    def l2n(x):
+        return x / torch.sqrt((x * x).sum(-1, keepdim=True) + 1e-6)
+    q, k = (l2n(torch.randn(B5, T5, H5, D2, device=dev, generator=gen)).to(bf).requires_grad_()
+            for _ in range(2))
+    v = torch.randn(B5, T5, H5, D2, device=dev, generator=gen).to(bf).requires_grad_()
+    beta = torch.sigmoid(torch.randn(B5, T5, H5, device=dev, generator=gen)).requires_grad_()
+    g = (torch.nn.functional.logsigmoid(torch.randn(B5, T5, H5, D2, device=dev, generator=gen))
+         / 16).requires_grad_()
+    do = torch.randn(B5, T5, H5, D2, device=dev, generator=gen).to(bf)
+
+    def step5():
+        o, _ = chunk_kda(q, k, v, g, beta)
+        return torch.autograd.grad(o, (q, k, v, g, beta), do)
+    sec = _time(step5, iters)
+    # input/output floor: fwd reads q, k, v (bf16), g (fp32), writes o; bwd reads q, k, v, g, dO,
+    # writes dq, dk, dv (bf16), dg (fp32); beta / dbeta
+    n5 = B5 * T5 * H5 * D2
+    io5 = n5 * (2 * 3 + 4 + 2) + n5 * (2 * 4 + 4 + 2 * 3 + 4) + B5 * T5 * H5 * 4 * 3
+    return {"config": "BASELINE config 5: chunk_kda fwd+bwd B4 T8192 H32 K=V=128 bf16",
+            "tokens_per_s": round(B5 * T5 / sec, 1), "ms": round(sec * 1e3, 4),
+            "io_bytes": io5, "hbm_floor_ms": round(io5 / (HBM_PEAK_GBS * 1e9) * 1e3, 4)}
 
 
 def traffic_from_profiles(kernel):
@@ -170,8 +215,12 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-secondary", action="store_true", help="skip the config 2 / 4 lines")
+    ap.add_argument("--no-secondary", action="store_true", help="skip the config 2 / 4 / 5 lines")
+    ap.add_argument("--configs", default="2,4,5", help="secondary configs to measure")
+    ap.add_argument("--only-secondary", action="store_true",
+                    help="measure only the secondary configs (for profiling them alone)")
     a = ap.parse_args()
+    configs = tuple(int(x) for x in a.configs.split(",") if x)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the GLA hot path shards over (batch, head) "
               "with no communication, so a multi-GPU figure adds nothing here; run with --gpus 1",
@@ -183,6 +232,9 @@ def main():
     from tops.ops.gla import chunk_gla
     dev = torch.device("cuda:0")
     NT.lib()
+    if a.only_secondary:
+        print(json.dumps({"secondary": secondary(dev, iters=a.steps, configs=configs)}), flush=True)
+        return
     q, k, v, g, h0, do, dht = make_inputs(dev)
     ins = (q, k, v, g, h0)
 
@@ -233,7 +285,7 @@ def main():
            "config": {"workload": "chunk_gla fwd+bwd (BASELINE config 3)", "B": B, "T": T,
                       "H": H, "K": K, "V": V, "chunk": C, "h0": True, "dht": True},
            "roofline": roofline, "path_roofline": path, "kernels": kern,
-           "secondary": None if a.no_secondary else secondary(dev),
+           "secondary": None if a.no_secondary else secondary(dev, configs=configs),
            "cpu_baseline": None if a.no_cpu else cpu_baseline()}
     print(json.dumps(out), flush=True)
 

@@ -164,6 +164,43 @@ int tops_gla_fused_recurrent_bwd(const void* q, const void* k, const void* v, co
                                  const int32_t* cu_seqlens, int B, int T, int H, int K, int V,
                                  int N, int dtype, float scale, int reverse, void* stream);
 
+/* Chunked KDA forward (gated delta rule with per-channel gates, C = 64 tiles).
+ * Replaces tops.ops.kda.chunk_kda_fwd (tops/ops/kda/chunk.py:25-190): the gate
+ * cumsum (tops/ops/kda/gate.py:19-51), the intra-chunk WY solve
+ * kda_intra_chunk_fwd (tops/ops/kda/chunk_intra.py:168-274), the delta-rule
+ * state pass chunk_gated_delta_rule_fwd_h (tops/ops/common/chunk_delta_h.py:848-979)
+ * and the output kernel chunk_gla_fwd_o_gk (tops/ops/gla/chunk.py:1383-1440).
+ *   g [B,T,H,K] natural-log gates, beta [B,T,H] (fp32); h0, ht [N,H,K,V] or NULL.
+ *   Workspace (fp32, written): u [B,T,H,V], w [B,T,H,K].
+ *   Saved for the backward (fp32, may be NULL for inference): tt [total,H,64,64]
+ *   (T = (I + Akk)^-1 transposed per chunk), v_new [B,T,H,V], h_ckpt [total,H,K,V]
+ *   (state before each chunk).
+ *   chunk_offsets / chunk_map as for tops_gla_chunk_bwd (both required for varlen);
+ *   total_chunks = B*ceil(T/64) or the varlen total.  K, V <= 128. */
+int tops_kda_chunk_fwd(const void* q, const void* k, const void* v, const float* g,
+                       const float* beta, const float* h0, void* o, float* ht, float* u, float* w,
+                       float* tt, float* v_new, float* h_ckpt, const int32_t* cu_seqlens,
+                       const int32_t* chunk_offsets, const int32_t* chunk_map, int total_chunks,
+                       int B, int T, int H, int K, int V, int N, int dtype, float scale,
+                       void* stream);
+
+/* Chunked KDA backward.  Replaces tops.ops.kda.chunk_bwd.chunk_kda_bwd
+ * (tops/ops/kda/chunk_bwd.py:655-832: the dAv, dhu, WY/dqkg and intra stages)
+ * from the tensors saved by tops_kda_chunk_fwd (w, tt, v_new, h_ckpt).
+ *   do [B,T,H,V] (dtype); dht [N,H,K,V] or NULL.
+ *   Workspace (fp32, written): dh_work [total,H,K,V] (dS per chunk),
+ *   dvn_work [total,H,V,64] (dv_new transposed per chunk), dk_work, dg_work [B,T,H,K].
+ *   Outputs: dq, dk [B,T,H,K] and dv [B,T,H,V] (dtype); dbeta [B,T,H], dg [B,T,H,K]
+ *   (w.r.t. the natural-log gates) fp32; dh0 [N,H,K,V] fp32 or NULL. */
+int tops_kda_chunk_bwd(const void* q, const void* k, const void* v, const float* g,
+                       const float* beta, const float* w, const float* tt, const float* v_new,
+                       const float* h_ckpt, const void* do_, const float* dht, float* dh_work,
+                       float* dvn_work, float* dk_work, float* dg_work, void* dq, void* dk, void* dv,
+                       float* dbeta, float* dg, float* dh0, const int32_t* cu_seqlens,
+                       const int32_t* chunk_offsets, const int32_t* chunk_map, int total_chunks,
+                       int B, int T, int H, int K, int V, int N, int dtype, float scale,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

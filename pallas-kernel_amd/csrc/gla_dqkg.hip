@@ -28,24 +28,31 @@
 
 namespace tops {
 
-template <typename TIn, int KP, int VP>
+template <typename TIn, typename TV, int KP, int VP>
 __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
   constexpr int C = kChunk;
   constexpr int KH = 32;                       // channels per pass
   constexpr int NPS = KP / KH;                 // passes
   constexpr int VC = VP / 32;
   constexpr bool SIN = !In<TIn>::kExactBf16;
+  constexpr bool SINV = !In<TV>::kExactBf16;
   constexpr int NPL = SIN ? 2 : 1;
+  constexpr int NPLV = SINV ? 2 : 1;
   constexpr int ES = sizeof(TIn);
+  constexpr int ESV = sizeof(TV);
   constexpr int LV = VP + 8, LT = C + 8, LG = KH + 4;
-  constexpr int EP = 16 / ES;                  // elements per 16-byte piece of v / dO
+  constexpr int EP = 16 / ES;                  // elements per 16-byte piece of dO
   constexpr int NPC = VP / EP;                 // pieces per row
   constexpr int NPT = C * NPC / 256;           // pieces per thread
+  constexpr int EPV = 16 / ESV;                // the same for v
+  constexpr int NPCV = VP / EPV;
+  constexpr int NPTV = C * NPCV / 256;
   static_assert(NPT >= 1 && C * NPC % 256 == 0, "VP must be 32, 64 or 128");
+  static_assert(NPTV >= 1 && C * NPCV % 256 == 0, "VP must be 32, 64 or 128");
   static_assert(KP % KH == 0, "KP must be 32, 64 or 128");
   typedef Words<TIn> Wd;
 
-  __shared__ __attribute__((aligned(16))) uint16_t sV[NPL * C * LV];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[NPLV * C * LV];
   __shared__ __attribute__((aligned(16))) uint16_t sD[NPL * C * LV];
   __shared__ __attribute__((aligned(16))) uint16_t sQT[2 * KH * LT];
   __shared__ __attribute__((aligned(16))) uint16_t sKT[2 * KH * LT];
@@ -58,7 +65,7 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
   __shared__ __attribute__((aligned(16))) float sBlk[KH];
   __shared__ __attribute__((aligned(16))) float sDgS[2 * C];   // kGateS: per channel-block token sums
 
-  const Plane Pv{sV, SIN ? sV + C * LV : sV, LV};
+  const Plane Pv{sV, SINV ? sV + C * LV : sV, LV};
   const Plane Pd{sD, SIN ? sD + C * LV : sD, LV};
   const Plane Pqt{sQT, sQT + KH * LT, LT};
   const Plane Pkt{sKT, sKT + KH * LT, LT};
@@ -99,27 +106,38 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
 
   // ---------------- v / dO planes ([C][V], V contiguous)
   {
-    const rsrc_t Rv = make_rsrc((const TIn*)p.v + e0 * V, remr * V * ES);
+    const rsrc_t Rv = make_rsrc((const TV*)p.v + e0 * V, remr * V * ESV);
     const rsrc_t Rd = make_rsrc((const TIn*)p.dout + e0 * V, remr * V * ES);
-    uint4 pv[NPT], pd[NPT];
+    uint4 pv[NPTV], pd[NPT];
+#pragma unroll
+    for (int i = 0; i < NPTV; ++i) {
+      const int pc = tid + 256 * i, row = pc / NPCV, col = (pc % NPCV) * EPV;
+      pv[i] = bld128(Rv, (row < nval && col < V) ? ((uint32_t)row * rowV + col) * ESV : kOOB, 0);
+    }
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
       const int pc = tid + 256 * i, row = pc / NPC, col = (pc % NPC) * EP;
-      const uint32_t o = (row < nval && col < V) ? ((uint32_t)row * rowV + col) * ES : kOOB;
-      pv[i] = bld128(Rv, o, 0);
-      pd[i] = bld128(Rd, o, 0);
+      pd[i] = bld128(Rd, (row < nval && col < V) ? ((uint32_t)row * rowV + col) * ES : kOOB, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < NPTV; ++i) {
+      const int pc = tid + 256 * i, row = pc / NPCV, col = (pc % NPCV) * EPV;
+      if constexpr (!SINV) {
+        *(uint4*)(Pv.hi + row * LV + col) = pv[i];
+      } else {
+        float a[4];
+        unpack4(pv[i], a);
+        put_n<true, 4>(Pv, row, col, a);
+      }
     }
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
       const int pc = tid + 256 * i, row = pc / NPC, col = (pc % NPC) * EP;
       if constexpr (!SIN) {
-        *(uint4*)(Pv.hi + row * LV + col) = pv[i];
         *(uint4*)(Pd.hi + row * LV + col) = pd[i];
       } else {
-        float a[4], b[4];
-        unpack4(pv[i], a);
+        float b[4];
         unpack4(pd[i], b);
-        put_n<true, 4>(Pv, row, col, a);
         put_n<true, 4>(Pd, row, col, b);
       }
     }
@@ -171,11 +189,9 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
           const bf16x8 ah = Pv.hi8(16 * J + l16, 32 * vc + 8 * lg);
           const bf16x8 bh = Pd.hi8(16 * B2 + l16, 32 * vc + 8 * lg);
           bf16x8 al = ah, bl = bh;
-          if constexpr (SIN) {
-            al = Pv.lo8(16 * J + l16, 32 * vc + 8 * lg);
-            bl = Pd.lo8(16 * B2 + l16, 32 * vc + 8 * lg);
-          }
-          t = mma<SIN, SIN>(t, ah, al, bh, bl);
+          if constexpr (SINV) al = Pv.lo8(16 * J + l16, 32 * vc + 8 * lg);
+          if constexpr (SIN) bl = Pd.lo8(16 * B2 + l16, 32 * vc + 8 * lg);
+          t = mma<SINV, SIN>(t, ah, al, bh, bl);
         }
         const int i = 16 * B2 + l16;
 #pragma unroll
@@ -189,11 +205,9 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
           const bf16x8 ah = Pd.hi8(16 * J + l16, 32 * vc + 8 * lg);
           const bf16x8 bh = Pv.hi8(16 * B2 + l16, 32 * vc + 8 * lg);
           bf16x8 al = ah, bl = bh;
-          if constexpr (SIN) {
-            al = Pd.lo8(16 * J + l16, 32 * vc + 8 * lg);
-            bl = Pv.lo8(16 * B2 + l16, 32 * vc + 8 * lg);
-          }
-          t = mma<SIN, SIN>(t, ah, al, bh, bl);
+          if constexpr (SIN) al = Pd.lo8(16 * J + l16, 32 * vc + 8 * lg);
+          if constexpr (SINV) bl = Pv.lo8(16 * B2 + l16, 32 * vc + 8 * lg);
+          t = mma<SIN, SINV>(t, ah, al, bh, bl);
         }
         const int j = 16 * B2 + l16;
 #pragma unroll
@@ -207,6 +221,8 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
   const rsrc_t Rdh = make_rsrc(p.dhs + ((size_t)gc * H + hh) * K * V, (long long)K * V * 4);
   const rsrc_t Rdq = make_rsrc((TIn*)p.dq + e0 * K, remr * K * ES);
   const rsrc_t Rdk = make_rsrc((TIn*)p.dk + e0 * K, remr * K * ES);
+  const rsrc_t Rdka = make_rsrc(p.dk_add ? p.dk_add + e0 * K : nullptr, p.dk_add ? remr * K * 4 : 0);
+  const rsrc_t Rdga = make_rsrc(p.dg_add ? p.dg_add + e0 * K : nullptr, p.dg_add ? remr * K * 4 : 0);
   const rsrc_t Rdg = make_rsrc(p.dg ? (gmode == kGateS ? p.dg + e0 : p.dg + e0 * K) : nullptr,
                                p.dg ? remr * (gmode == kGateS ? 1 : K) * 4 : 0);
   if (tid < 2 * C) sDgS[tid] = 0.f;
@@ -288,12 +304,10 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
         const bf16x8 doh = Pd.hi8(16 * B2 + l16, v0);
         const bf16x8 vh = Pv.hi8(16 * B2 + l16, v0);
         bf16x8 dol = doh, vl = vh;
-        if constexpr (SIN) {
-          dol = Pd.lo8(16 * B2 + l16, v0);
-          vl = Pv.lo8(16 * B2 + l16, v0);
-        }
+        if constexpr (SIN) dol = Pd.lo8(16 * B2 + l16, v0);
+        if constexpr (SINV) vl = Pv.lo8(16 * B2 + l16, v0);
         X[a] = mma<true, SIN>(X[a], Ah, Al, doh, dol);
-        Wt[a] = mma<true, SIN>(Wt[a], Dh, Dl, vh, vl);
+        Wt[a] = mma<true, SINV>(Wt[a], Dh, Dl, vh, vl);
       }
     }
     // ---- sum_t k~ W_inter (this wave's tokens) and sum_v h dh (token-half-0 waves)
@@ -368,6 +382,12 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
         dkv[r] = fast_exp2(gmr[r] - gr[r]) * Wt[a][r];
         dgr[a][r] = qv[r] * dqv[r] - kv[r] * dkv[r];
       }
+      if (p.dk_add) {
+        float ka[4];
+        unpack4(bld128(Rdka, ok ? off * 4u : kOOB, 0), ka);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dkv[r] += ka[r];
+      }
       Wd::st4(Rdq, dqv, ok ? off * ES : kOOB, 0);
       Wd::st4(Rdk, dkv, ok ? off * ES : kOOB, 0);
     }
@@ -402,8 +422,10 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
         const int tok = 16 * (2 * rh + a) + l16;
         const bool ok = chok && tok < nval;
         const uint32_t off = (uint32_t)tok * rowK + kc;
-        bst128(Rdg, make_uint4(__float_as_uint(dgr[a][0] + add[0]), __float_as_uint(dgr[a][1] + add[1]),
-                               __float_as_uint(dgr[a][2] + add[2]), __float_as_uint(dgr[a][3] + add[3])),
+        float ga[4] = {0.f, 0.f, 0.f, 0.f};
+        if (p.dg_add) unpack4(bld128(Rdga, ok ? off * 4u : kOOB, 0), ga);
+        bst128(Rdg, make_uint4(__float_as_uint(dgr[a][0] + add[0] + ga[0]), __float_as_uint(dgr[a][1] + add[1] + ga[1]),
+                               __float_as_uint(dgr[a][2] + add[2] + ga[2]), __float_as_uint(dgr[a][3] + add[3] + ga[3])),
                ok ? off * 4u : kOOB, 0);
       }
     } else if (gmode == kGateS) {
@@ -430,13 +452,13 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
   }
 }
 
-template <typename TIn>
+template <typename TIn, typename TV>
 hipError_t launch_gla_dqkg(const DqkgParams& p, hipStream_t s) {
   const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
   const int vp = p.V <= 32 ? 32 : (p.V <= 64 ? 64 : 128);
   dim3 grid(p.total * p.H), block(256);
 #define TOPS_DQKG(KPV, VPV) \
-  if (kp == KPV && vp == VPV) { hipLaunchKernelGGL((gla_dqkg_kernel<TIn, KPV, VPV>), grid, block, 0, s, p); return hipGetLastError(); }
+  if (kp == KPV && vp == VPV) { hipLaunchKernelGGL((gla_dqkg_kernel<TIn, TV, KPV, VPV>), grid, block, 0, s, p); return hipGetLastError(); }
   TOPS_DQKG(32, 32) TOPS_DQKG(32, 64) TOPS_DQKG(32, 128)
   TOPS_DQKG(64, 32) TOPS_DQKG(64, 64) TOPS_DQKG(64, 128)
   TOPS_DQKG(128, 32) TOPS_DQKG(128, 64) TOPS_DQKG(128, 128)
@@ -444,7 +466,8 @@ hipError_t launch_gla_dqkg(const DqkgParams& p, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
-template hipError_t launch_gla_dqkg<uint16_t>(const DqkgParams&, hipStream_t);
-template hipError_t launch_gla_dqkg<float>(const DqkgParams&, hipStream_t);
+template hipError_t launch_gla_dqkg<uint16_t, uint16_t>(const DqkgParams&, hipStream_t);
+template hipError_t launch_gla_dqkg<float, float>(const DqkgParams&, hipStream_t);
+template hipError_t launch_gla_dqkg<uint16_t, float>(const DqkgParams&, hipStream_t);
 
 }  // namespace tops

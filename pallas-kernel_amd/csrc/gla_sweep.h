@@ -24,10 +24,16 @@ struct SweepParams {
   int B, T, H, K, V, N, NV;
   float scale;
   int gate_mode;
+  // KDA (delta rule) sweeps only:
+  const float* u;        // forward: u = T (beta v) [B,T,H,V]
+  const float* w;        // w = T (beta 2^G k) [B,T,H,K]
+  float* y32;            // forward: v_new [B,T,H,V] or NULL; reverse: dv_new per chunk,
+                         // transposed, [total,H,V,C]
 };
 
-// TIn = uint16_t (bf16 bits) or float; REV = reverse (state-gradient) sweep.
-template <typename TIn, bool REV>
+// TIn = uint16_t (bf16 bits) or float; REV = reverse (state-gradient) sweep;
+// DELTA = the KDA delta-rule sweep (v_new = u - w S replaces v).
+template <typename TIn, bool REV, bool DELTA = false>
 hipError_t launch_gla_sweep(const SweepParams& p, hipStream_t s);
 
 struct DqkgParams {
@@ -47,9 +53,13 @@ struct DqkgParams {
   int total, B, T, H, K, V, N;
   float scale;
   int gate_mode;
+  // optional fp32 terms added to dk and dg ([B,T,H,K]; the KDA WY part), or NULL
+  const float* dk_add;
+  const float* dg_add;
 };
 
-template <typename TIn>
+// TV = type of v (the KDA backward passes fp32 v_new with bf16 q / k / dO)
+template <typename TIn, typename TV = TIn>
 hipError_t launch_gla_dqkg(const DqkgParams& p, hipStream_t s);
 
 }  // namespace tops

@@ -39,13 +39,16 @@
 namespace tops {
 
 
-template <typename TIn, int KP, bool REV>
+template <typename TIn, int KP, bool REV, bool DELTA>
 __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
   constexpr int C = kChunk, BV = 64;
   constexpr int NQ = KP / 4;             // column quads of a [C][KP] tile
   constexpr int NSEG = 256 / NQ;         // row segments
   constexpr int RPT = C / NSEG;          // rows per thread (2, 4, 8)
   constexpr bool SIN = !In<TIn>::kExactBf16;
+  constexpr bool FWD_DELTA = DELTA && !REV;
+  constexpr bool REV_DELTA = DELTA && REV;
+  constexpr bool SY = SIN || FWD_DELTA;  // the Y plane carries a lo half (fp32 Y, or v_new)
   constexpr int LQ = KP + 8, LT = C + 8, LH = KP + 8;
   constexpr int NHT = (KP / 16) * (BV / 16) / 4;  // state tiles per wave
   constexpr int NM = NHT >= 4 ? NHT / 4 : 1;      // distinct K blocks per wave
@@ -56,15 +59,21 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t sX[2 * C * LQ];
   __shared__ __attribute__((aligned(16))) uint16_t sZ[2 * C * LQ];
   __shared__ __attribute__((aligned(16))) uint16_t sZT[2 * KP * LT];
-  __shared__ __attribute__((aligned(16))) uint16_t sYT[(SIN ? 2 : 1) * BV * LT];
-  __shared__ __attribute__((aligned(16))) uint16_t sHT[2 * BV * LH];
+  __shared__ __attribute__((aligned(16))) uint16_t sYT[(SY ? 2 : 1) * BV * LT];
+  // (the reverse delta rule reuses sHT for the [BV][LT] dv_new^T plane: size for both)
+  constexpr int NHTS = 2 * BV * (REV_DELTA && LT > LH ? LT : LH);
+  __shared__ __attribute__((aligned(16))) uint16_t sHT[NHTS];
   __shared__ __attribute__((aligned(16))) float sTot[NSEG * KP];
 
   const Plane PX{sX, sX + C * LQ, LQ};
   const Plane PZ{sZ, sZ + C * LQ, LQ};
   const Plane PZt{sZT, sZT + KP * LT, LT};
-  const Plane PYt{sYT, SIN ? sYT + BV * LT : sYT, LT};
+  const Plane PYt{sYT, SY ? sYT + BV * LT : sYT, LT};
   const Plane PHt{sHT, sHT + BV * LH, LH};
+  // reverse delta rule: once the output pass is done, w^T [K][C] reuses sZT and
+  // dv_new^T [BV][C] reuses sHT
+  const Plane PWt{sZT, sZT + KP * LT, LT};
+  const Plane PDt{sHT, sHT + BV * LT, LT};
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
@@ -98,7 +107,7 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
   const bool ycolok = yv < V;
   const uint32_t rowK = (uint32_t)(H * K), rowV = (uint32_t)(H * V);
   const uint32_t offQ = colok ? ((uint32_t)r0 * rowK + c0) * ES : kOOB;        // q, k
-  const uint32_t offG = colok ? ((uint32_t)r0 * rowK + c0) * 4u : kOOB;        // g
+  const uint32_t offG = colok ? ((uint32_t)r0 * rowK + c0) * 4u : kOOB;        // g, w
   const uint32_t offY = ycolok ? ((uint32_t)(yseg * 8) * rowV + yv) * ES : kOOB;
   // gate load: per-channel [.., K] float4, or the per-(token, head) scalar read as the first
   // word of a 16-byte load; the gamma mode loads nothing (out of range -> 0)
@@ -135,7 +144,6 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
     const rsrc_t Rq = make_rsrc((const TIn*)p.q + e0 * K, rem * K * ES);
     const rsrc_t Rk = make_rsrc((const TIn*)p.k + e0 * K, rem * K * ES);
     const rsrc_t Rg = make_rsrc(gk_mode ? p.g + e0 * K : p.g + e0, rem * (gk_mode ? K : 1) * 4);
-    const rsrc_t Ry = make_rsrc((const TIn*)p.y + e0 * V, rem * V * ES);
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
       const bool ok = r0 + i < nval;
@@ -145,10 +153,13 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
       // when the chunk is consumed, so the prefetch never waits)
       rg[i] = bld128(Rg, ok ? offGm : kOOB, i * gstride);
     }
+    if constexpr (!FWD_DELTA) {
+      const rsrc_t Ry = make_rsrc((const TIn*)p.y + e0 * V, rem * V * ES);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const bool ok = yseg * 8 + i < nval;
-      ry[i] = Wd::ld2(Ry, ok ? offY : kOOB, i * rowV * ES);
+      for (int i = 0; i < 8; ++i) {
+        const bool ok = yseg * 8 + i < nval;
+        ry[i] = Wd::ld2(Ry, ok ? offY : kOOB, i * rowV * ES);
+      }
     }
   };
 
@@ -159,6 +170,35 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
     const int c = REV ? NTs - 1 - it : it;
     const int t0 = c * C;
     const int nval = min(C, L - t0);
+
+    // ---------------- delta rule: w rows of this thread (and u in the MFMA result
+    // layout for the forward), loaded now and consumed after barrier B2
+    float4 rw[RPT];
+    float ru[BV / 16][4];
+    if constexpr (DELTA) {
+      const size_t e0 = (size_t)(row0 + t0) * H + hh;
+      const long long rem = (rows_total - (row0 + t0)) * (long long)H;
+      const rsrc_t Rw = make_rsrc(p.w + e0 * K, rem * K * 4);
+#pragma unroll
+      for (int i = 0; i < RPT; ++i) {
+        const uint4 x = bld128(Rw, r0 + i < nval ? offG : kOOB, i * rowK * 4);
+        rw[i] = make_float4(__uint_as_float(x.x), __uint_as_float(x.y), __uint_as_float(x.z),
+                            __uint_as_float(x.w));
+      }
+      if constexpr (FWD_DELTA) {
+        const rsrc_t Ru = make_rsrc(p.u + e0 * V, rem * V * 4);
+#pragma unroll
+        for (int nn = 0; nn < BV / 16; ++nn) {
+          const int vv = vt * BV + 16 * nn + l16;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int tok = 16 * wave + 4 * lg + r;
+            ru[nn][r] = __uint_as_float(
+                bld32(Ru, (tok < nval && vv < V) ? ((uint32_t)tok * rowV + vv) * 4u : kOOB, 0));
+          }
+        }
+      }
+    }
 
     // ---------------- gate cumsum: thread-local rows, then segment totals via LDS
     float G[RPT][4];
@@ -208,7 +248,7 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float gm = 0.5f * sgam[mi][r];
-        const float alpha = REV ? fast_exp2(sgam[mi][r] - gm) : scale * fast_exp2(gm);
+        const float alpha = REV ? fast_exp2(sgam[mi][r] - gm) : (DELTA ? 1.f : scale) * fast_exp2(gm);
         x[r] = alpha * S[i][r];
       }
       put_n<true, 4>(PHt, 16 * nn + l16, kr, x);
@@ -222,10 +262,10 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
     }
 
     // ---------------- gated operands for the staging rows
-    {
-      float gm[4];
+    float gm[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) gm[j] = 0.5f * gam[j];
+    for (int j = 0; j < 4; ++j) gm[j] = 0.5f * gam[j];
+    {
       float zt[4][RPT];
 #pragma unroll
       for (int i = 0; i < RPT; ++i) {
@@ -235,7 +275,7 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const float Gv = G[i][j] + pre[j];
-          xq[j] = qv[j] * fast_exp2(Gv - gm[j]);
+          xq[j] = (FWD_DELTA ? scale : 1.f) * qv[j] * fast_exp2(Gv - gm[j]);
           xk[j] = kv[j] * fast_exp2(gm[j] - Gv);
         }
         const float* xx = REV ? xk : xq;
@@ -247,50 +287,151 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) put_n<true, RPT>(PZt, c0 + j, r0, zt[j]);
-      float ya[8], yb[8];
+      if constexpr (!FWD_DELTA) {
+        float ya[8], yb[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) unpack2(ry[i], ya[i], yb[i]);
-      put_n<SIN, 8>(PYt, 2 * yc, yseg * 8, ya);
-      put_n<SIN, 8>(PYt, 2 * yc + 1, yseg * 8, yb);
+        for (int i = 0; i < 8; ++i) unpack2(ry[i], ya[i], yb[i]);
+        put_n<SY, 8>(PYt, 2 * yc, yseg * 8, ya);
+        put_n<SY, 8>(PYt, 2 * yc + 1, yseg * 8, yb);
+      }
     }
     __syncthreads();  // B2: all planes visible
 
     // ---------------- prefetch the next chunk while this one is computed
     if (it + 1 < NTs) load_chunk(REV ? c - 1 : c + 1);
 
-    // ---------------- output block R = wave: out^T tiles (nn, R)
-    {
-      const int R = wave;
-      bf16x8 xh[KP / 32], xl[KP / 32];
+    // ---------------- reverse delta rule: first half of the state update (Z~^T Y)
+    f32x4 d1[NHT];
+    if constexpr (REV_DELTA) {
 #pragma unroll
-      for (int kc = 0; kc < KP / 32; ++kc) {
-        xh[kc] = PX.hi8(16 * R + l16, 32 * kc + 8 * lg);
-        xl[kc] = PX.lo8(16 * R + l16, 32 * kc + 8 * lg);
-      }
-      // D tiles (P, R) on the causal side: lane holds D[16P+4lg+r][16R+l16]
-      uint2 dh[4], dl[4];
+      for (int i = 0; i < NHT; ++i) {
+        const int t = wave * NHT + i, m = t / (BV / 16), nn = t % (BV / 16);
+        d1[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int P = 0; P < 4; ++P) {
-        dh[P] = make_uint2(0u, 0u);
-        dl[P] = make_uint2(0u, 0u);
-        const bool live = REV ? (P >= R) : (P <= R);
-        if (live) {
-          f32x4 t = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int kc = 0; kc < KP / 32; ++kc)
-            t = mma<true, true>(t, PZ.hi8(16 * P + l16, 32 * kc + 8 * lg),
-                                PZ.lo8(16 * P + l16, 32 * kc + 8 * lg), xh[kc], xl[kc]);
-          const int rr = 16 * R + l16;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int pp = 16 * P + 4 * lg + r;
-            const bool keep = REV ? (pp >= rr) : (pp <= rr);
-            t[r] = keep ? t[r] * scale : 0.f;
-          }
-          acc_to_bf16x4(t, dh[P], dl[P]);
+        for (int kc = 0; kc < C / 32; ++kc) {
+          const bf16x8 bh = PYt.hi8(16 * nn + l16, 32 * kc + 8 * lg);
+          bf16x8 bl = bh;
+          if constexpr (SY) bl = PYt.lo8(16 * nn + l16, 32 * kc + 8 * lg);
+          d1[i] = mma<true, SY>(d1[i], PZt.hi8(16 * m + l16, 32 * kc + 8 * lg),
+                                PZt.lo8(16 * m + l16, 32 * kc + 8 * lg), bh, bl);
         }
       }
-      // lane writes out[token 16R + l16][v = 16 nn + 4 lg + 0..3]
+    }
+
+    // ---------------- output block R = wave
+    const int R = wave;
+    bf16x8 xh[KP / 32], xl[KP / 32];
+#pragma unroll
+    for (int kc = 0; kc < KP / 32; ++kc) {
+      xh[kc] = PX.hi8(16 * R + l16, 32 * kc + 8 * lg);
+      xl[kc] = PX.lo8(16 * R + l16, 32 * kc + 8 * lg);
+    }
+    // D tiles (P, R) on the causal side: lane holds D[16P+4lg+r][16R+l16]
+    const float dsc = FWD_DELTA ? 1.f : scale;   // the delta forward folds scale into X
+    uint2 dh[4], dl[4];
+#pragma unroll
+    for (int P = 0; P < 4; ++P) {
+      dh[P] = make_uint2(0u, 0u);
+      dl[P] = make_uint2(0u, 0u);
+      const bool live = REV ? (P >= R) : (P <= R);
+      if (live) {
+        f32x4 t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < KP / 32; ++kc)
+          t = mma<true, true>(t, PZ.hi8(16 * P + l16, 32 * kc + 8 * lg),
+                              PZ.lo8(16 * P + l16, 32 * kc + 8 * lg), xh[kc], xl[kc]);
+        const int rr = 16 * R + l16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int pp = 16 * P + 4 * lg + r;
+          const bool keep = REV ? (pp >= rr) : (pp <= rr);
+          t[r] = keep ? t[r] * dsc : 0.f;
+        }
+        acc_to_bf16x4(t, dh[P], dl[P]);
+      }
+    }
+
+    if constexpr (FWD_DELTA) {
+      // v_new = u - w S for this wave's tokens.  Rows 16R.. of X are read only by this
+      // wave (above), so they now take w 2^-Gm, the A operand against H^T = 2^Gm S.
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int i = 0; i < RPT; ++i) {
+        float x[4] = {rw[i].x, rw[i].y, rw[i].z, rw[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] *= fast_exp2(-gm[j]);
+        put_n<true, 4>(PX, r0 + i, c0, x);
+      }
+      asm volatile("" ::: "memory");
+      const size_t e0 = (size_t)(row0 + t0) * H + hh;
+      const rsrc_t Rvn = make_rsrc(p.y32 ? p.y32 + e0 * V : nullptr,
+                                   p.y32 ? (rows_total - (row0 + t0)) * (long long)H * V * 4 : 0);
+#pragma unroll
+      for (int nn = 0; nn < BV / 16; ++nn) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < KP / 32; ++kc)
+          acc = mma<true, true>(acc, PX.hi8(16 * R + l16, 32 * kc + 8 * lg), PX.lo8(16 * R + l16, 32 * kc + 8 * lg),
+                                PHt.hi8(16 * nn + l16, 32 * kc + 8 * lg), PHt.lo8(16 * nn + l16, 32 * kc + 8 * lg));
+        // lane holds (token 16R + 4lg + r, column 16nn + l16)
+        float vn[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) vn[r] = ru[nn][r] - acc[r];
+        put_n<true, 4>(PYt, 16 * nn + l16, 16 * R + 4 * lg, vn);
+        const int vv = vt * BV + 16 * nn + l16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tok = 16 * R + 4 * lg + r;
+          bst32(Rvn, __float_as_uint(vn[r]), (tok < nval && vv < V) ? ((uint32_t)tok * rowV + vv) * 4u : kOOB, 0);
+        }
+      }
+      __syncthreads();  // B3: v_new^T plane complete
+    }
+
+    if constexpr (REV_DELTA) {
+      // dv_new = k~ (alpha dS) + D^T dO, token-major: lane holds (token 16R + 4lg + r,
+      // column 16nn + l16); stored transposed per chunk ([V][C]) and kept for the update
+      f32x4 dvn[BV / 16];
+      const rsrc_t Rd = make_rsrc(p.y32 + ((size_t)(cbase + c) * H + hh) * V * C, (long long)V * C * 4);
+#pragma unroll
+      for (int nn = 0; nn < BV / 16; ++nn) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < KP / 32; ++kc)
+          acc = mma<true, true>(acc, xh[kc], xl[kc], PHt.hi8(16 * nn + l16, 32 * kc + 8 * lg),
+                                PHt.lo8(16 * nn + l16, 32 * kc + 8 * lg));
+#pragma unroll
+        for (int Pp = 0; Pp < 2; ++Pp) {
+          const int P0 = 2 * Pp, P1 = 2 * Pp + 1;
+          if (P1 >= R) {
+            const bf16x8 bh = PYt.hi44(16 * nn + l16, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg);
+            bf16x8 bl = bh;
+            if constexpr (SY) bl = PYt.lo44(16 * nn + l16, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg);
+            acc = mma<true, SY>(acc, cat44(dh[P0], dh[P1]), cat44(dl[P0], dl[P1]), bh, bl);
+          }
+        }
+        dvn[nn] = acc;
+        const int vv = vt * BV + 16 * nn + l16;
+        bst128(Rd, make_uint4(__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]),
+                              __float_as_uint(acc[3])),
+               vv < V ? ((uint32_t)vv * C + 16 * R + 4 * lg) * 4u : kOOB, 0);
+      }
+      __syncthreads();  // B3: every wave is done with X, Z, Z^T, Y^T and H^T
+#pragma unroll
+      for (int nn = 0; nn < BV / 16; ++nn) {
+        const float x[4] = {dvn[nn][0], dvn[nn][1], dvn[nn][2], dvn[nn][3]};
+        put_n<true, 4>(PDt, 16 * nn + l16, 16 * R + 4 * lg, x);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float x[RPT];
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) x[i] = j == 0 ? rw[i].x : (j == 1 ? rw[i].y : (j == 2 ? rw[i].z : rw[i].w));
+        put_n<true, RPT>(PWt, c0 + j, r0, x);
+      }
+      __syncthreads();  // B4: w^T and dv_new^T planes visible
+    } else {
+      // out^T tiles (nn, R); lane writes out[token 16R + l16][v = 16 nn + 4 lg + 0..3]
       const int tok = 16 * R + l16;
       const size_t eo = (size_t)(row0 + t0) * H + hh;
       const rsrc_t Ro = make_rsrc((TIn*)p.out + eo * V,
@@ -311,8 +452,8 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
           if (live) {
             const bf16x8 ah = PYt.hi44(16 * nn + l16, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg);
             bf16x8 al = ah;
-            if constexpr (SIN) al = PYt.lo44(16 * nn + l16, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg);
-            acc = mma<SIN, true>(acc, ah, al, cat44(dh[P0], dh[P1]), cat44(dl[P0], dl[P1]));
+            if constexpr (SY) al = PYt.lo44(16 * nn + l16, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg);
+            acc = mma<SY, true>(acc, ah, al, cat44(dh[P0], dh[P1]), cat44(dl[P0], dl[P1]));
           }
         }
         const int v0 = vt * BV + 16 * nn + 4 * lg;
@@ -320,25 +461,33 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
       }
     }
 
-    // ---------------- state update: S = 2^Gamma S + beta (Z~^T Y)
+    // ---------------- state update: S = 2^Gamma S + beta (Z~^T Y) [- w^T dv_new]
 #pragma unroll
     for (int i = 0; i < NHT; ++i) {
       const int t = wave * NHT + i, m = t / (BV / 16), nn = t % (BV / 16);
       const int mi = (NHT >= 4) ? i / 4 : 0;
       f32x4 d = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (REV_DELTA) {
 #pragma unroll
-      for (int kc = 0; kc < C / 32; ++kc) {
-        const bf16x8 bh = PYt.hi8(16 * nn + l16, 32 * kc + 8 * lg);
-        bf16x8 bl = bh;
-        if constexpr (SIN) bl = PYt.lo8(16 * nn + l16, 32 * kc + 8 * lg);
-        d = mma<true, SIN>(d, PZt.hi8(16 * m + l16, 32 * kc + 8 * lg),
-                           PZt.lo8(16 * m + l16, 32 * kc + 8 * lg), bh, bl);
+        for (int kc = 0; kc < C / 32; ++kc)
+          d = mma<true, true>(d, PWt.hi8(16 * m + l16, 32 * kc + 8 * lg), PWt.lo8(16 * m + l16, 32 * kc + 8 * lg),
+                              PDt.hi8(16 * nn + l16, 32 * kc + 8 * lg), PDt.lo8(16 * nn + l16, 32 * kc + 8 * lg));
+      } else {
+#pragma unroll
+        for (int kc = 0; kc < C / 32; ++kc) {
+          const bf16x8 bh = PYt.hi8(16 * nn + l16, 32 * kc + 8 * lg);
+          bf16x8 bl = bh;
+          if constexpr (SY) bl = PYt.lo8(16 * nn + l16, 32 * kc + 8 * lg);
+          d = mma<true, SY>(d, PZt.hi8(16 * m + l16, 32 * kc + 8 * lg),
+                            PZt.lo8(16 * m + l16, 32 * kc + 8 * lg), bh, bl);
+        }
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float ga = sgam[mi][r], gmv = 0.5f * ga;
         const float beta = REV ? scale * fast_exp2(gmv) : fast_exp2(ga - gmv);
-        S[i][r] = fast_exp2(ga) * S[i][r] + beta * d[r];
+        if constexpr (REV_DELTA) S[i][r] = fast_exp2(ga) * S[i][r] + beta * d1[i][r] - d[r];
+        else S[i][r] = fast_exp2(ga) * S[i][r] + beta * d[r];
       }
     }
   }
@@ -357,20 +506,24 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
   }
 }
 
-template <typename TIn, bool REV>
+template <typename TIn, bool REV, bool DELTA>
 hipError_t launch_gla_sweep(const SweepParams& p, hipStream_t s) {
   const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
   dim3 grid(p.NV * p.H * p.N);
-  if (kp == 32) hipLaunchKernelGGL((gla_sweep_kernel<TIn, 32, REV>), grid, dim3(256), 0, s, p);
-  else if (kp == 64) hipLaunchKernelGGL((gla_sweep_kernel<TIn, 64, REV>), grid, dim3(256), 0, s, p);
-  else hipLaunchKernelGGL((gla_sweep_kernel<TIn, 128, REV>), grid, dim3(256), 0, s, p);
+  if (kp == 32) hipLaunchKernelGGL((gla_sweep_kernel<TIn, 32, REV, DELTA>), grid, dim3(256), 0, s, p);
+  else if (kp == 64) hipLaunchKernelGGL((gla_sweep_kernel<TIn, 64, REV, DELTA>), grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((gla_sweep_kernel<TIn, 128, REV, DELTA>), grid, dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
-template hipError_t launch_gla_sweep<uint16_t, false>(const SweepParams&, hipStream_t);
-template hipError_t launch_gla_sweep<uint16_t, true>(const SweepParams&, hipStream_t);
-template hipError_t launch_gla_sweep<float, false>(const SweepParams&, hipStream_t);
-template hipError_t launch_gla_sweep<float, true>(const SweepParams&, hipStream_t);
+template hipError_t launch_gla_sweep<uint16_t, false, false>(const SweepParams&, hipStream_t);
+template hipError_t launch_gla_sweep<uint16_t, true, false>(const SweepParams&, hipStream_t);
+template hipError_t launch_gla_sweep<float, false, false>(const SweepParams&, hipStream_t);
+template hipError_t launch_gla_sweep<float, true, false>(const SweepParams&, hipStream_t);
+template hipError_t launch_gla_sweep<uint16_t, false, true>(const SweepParams&, hipStream_t);
+template hipError_t launch_gla_sweep<uint16_t, true, true>(const SweepParams&, hipStream_t);
+template hipError_t launch_gla_sweep<float, false, true>(const SweepParams&, hipStream_t);
+template hipError_t launch_gla_sweep<float, true, true>(const SweepParams&, hipStream_t);
 
 }  // namespace tops
 

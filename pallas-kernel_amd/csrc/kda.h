@@ -1,0 +1,49 @@
+// Internal interfaces of the KDA chunk kernels (kda_prep.hip, kda_wy.hip; the state sweeps
+// are the DELTA instances of gla_sweep.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+
+namespace tops {
+
+// Chunk-parallel forward preparation (one workgroup per (chunk, head)).
+struct KdaPrepParams {
+  const void* k;
+  const void* v;
+  const float* g;          // [B,T,H,K] natural-log gates
+  const float* beta;       // [B,T,H]
+  float* u;                // [B,T,H,V]  T (beta v)
+  float* w;                // [B,T,H,K]  T (beta 2^G k)
+  float* tt;               // [total,H,C,C]  T transposed (row i holds column i of T), or NULL
+  const int* cu_seqlens;
+  const int* chunk_offsets;
+  const int* chunk_map;
+  int total, B, T, H, K, V, N;
+};
+
+template <typename TIn>
+hipError_t launch_kda_prep(const KdaPrepParams& p, hipStream_t s);
+
+// Chunk-parallel WY backward (one workgroup per (chunk, head)).
+struct KdaWyParams {
+  const void* k;
+  const void* v;
+  const float* g;          // [B,T,H,K]
+  const float* beta;       // [B,T,H]
+  const float* tt;         // [total,H,C,C]  T transposed
+  const float* dvnt;       // [total,H,V,C]  dv_new transposed per chunk
+  const float* vnew;       // [B,T,H,V]
+  const float* hs;         // [total,H,K,V]  state before each chunk
+  void* dv;                // [B,T,H,V]  (TIn)
+  float* dbeta;            // [B,T,H]
+  float* dk_wy;            // [B,T,H,K]  WY part of dk
+  float* dg_wy;            // [B,T,H,K]  WY part of dg (reverse in-chunk cumsum applied)
+  const int* cu_seqlens;
+  const int* chunk_offsets;
+  const int* chunk_map;
+  int total, B, T, H, K, V, N;
+};
+
+template <typename TIn>
+hipError_t launch_kda_wy(const KdaWyParams& p, hipStream_t s);
+
+}  // namespace tops

@@ -1,0 +1,377 @@
+// KDA backward, WY stage, for gfx950: gradients that flow through u = T (beta v),
+// w = T (beta 2^G k) and Akk.
+//
+// Replaces the WY part of the reference's fused K18 (_chunk_kda_bwd_wy_dqkg_fused_kernel,
+// tops/ops/kda/chunk_bwd.py:19-141) and the Akk part of K17 (kda_intra_chunk_bwd_kernel,
+// tops/ops/kda/chunk_intra.py:283-383), following the oracle
+// tops/cpu/ops/kda/chunk_bwd.py:525-668 (wy_fast.py for the WY backward).
+//
+// One workgroup (4 wave64) per (chunk, head).  With dv_new the gradient w.r.t.
+// v_new = u - w S (S the state before the chunk), the WY backward collapses to
+//     P    = T^T dv_new                      (dL/d(beta v))
+//     dbk  = -P S^T                          (dL/d(beta 2^G k))
+//     dAkk = -P v_new^T, strictly lower      (since v_new = T (beta v - beta 2^G k S))
+// and then
+//     dv    = beta P
+//     dbeta = sum_v v P + sum_d 2^G k dbk + sum_d k Y1
+//     dk    = beta 2^G dbk + beta Y1 + Y2
+//     dG    = beta 2^G k dbk + beta k Y1 - k Y2          (w.r.t. the natural-log cumsum)
+// with Y1[i] = 2^(G_i - Gm) sum_j dAkk[i][j] k~_j (k~ = k 2^(Gm - G)) and
+//      Y2[j] = 2^(Gm - G_j) sum_i beta_i dAkk[i][j] k^_i (k^ = k 2^(G - Gm)).
+// dg_wy is the reverse in-chunk cumsum of dG.  The GLA-shaped terms (through o and the
+// state update) are added by the dq / dk / dg kernel, which reads dk_wy and dg_wy.
+//
+// Wave R owns token block R (16 tokens).  P goes through LDS (bf16 hi/lo); the dAkk tiles
+// stay in registers for the channel passes (32 channels each: gated k^T planes, gate
+// cumsum).  The inputs T^T [C][C] and dv_new^T [V][C] are stored transposed per chunk,
+// so MFMA operands load straight from global memory.
+#include "kda.h"
+#include "tops_common.h"
+
+namespace tops {
+
+__device__ __forceinline__ void load_split8(rsrc_t r, uint32_t off, bf16x8& h, bf16x8& l) {
+  float a[4], b[4];
+  unpack4(bld128(r, off, 0), a);
+  unpack4(bld128(r, off == kOOB ? kOOB : off + 16u, 0), b);
+  uint32_t hh[4], ll[4];
+  split_bf16x2(a[0], a[1], hh[0], ll[0]);
+  split_bf16x2(a[2], a[3], hh[1], ll[1]);
+  split_bf16x2(b[0], b[1], hh[2], ll[2]);
+  split_bf16x2(b[2], b[3], hh[3], ll[3]);
+  h = __builtin_bit_cast(bf16x8, make_uint4(hh[0], hh[1], hh[2], hh[3]));
+  l = __builtin_bit_cast(bf16x8, make_uint4(ll[0], ll[1], ll[2], ll[3]));
+}
+
+template <typename TIn, int KP, int VP>
+__global__ __launch_bounds__(256, 2) void kda_wy_kernel(KdaWyParams p) {
+  constexpr int C = kChunk;
+  constexpr int KH = 32;                 // channels per pass
+  constexpr int NPS = KP / KH;
+  constexpr int VC = VP / 32;
+  constexpr int ES = sizeof(TIn);
+  constexpr int LP = VP + 8, LT = C + 8, LG = KH + 4;
+  static_assert(KP % KH == 0 && VP % 32 == 0, "KP, VP must be 32, 64 or 128");
+  typedef Words<TIn> Wd;
+
+  __shared__ __attribute__((aligned(16))) uint16_t sP[2 * C * LP];
+  __shared__ __attribute__((aligned(16))) uint16_t sK1t[2 * KH * LT];
+  __shared__ __attribute__((aligned(16))) uint16_t sK2t[2 * KH * LT];
+  __shared__ __attribute__((aligned(16))) float sG[C * LG];
+  __shared__ __attribute__((aligned(16))) float sTot[8 * KH];
+  __shared__ __attribute__((aligned(16))) float sGm[KH];
+  __shared__ __attribute__((aligned(16))) float sBlk[4 * KH];
+  __shared__ float sBeta[C];
+  __shared__ float sDb[C];
+
+  const Plane PP{sP, sP + C * LP, LP};
+  const Plane PK1t{sK1t, sK1t + KH * LT, LT};
+  const Plane PK2t{sK2t, sK2t + KH * LT, LT};
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int R = __builtin_amdgcn_readfirstlane(tid >> 6);   // token block of this wave
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int hh = blockIdx.x % p.H;
+  const int gc = blockIdx.x / p.H;
+  const int H = p.H, K = p.K, V = p.V;
+
+  int c, L, row0;
+  if (p.cu_seqlens) {
+    const int n = p.chunk_map[gc];
+    c = gc - p.chunk_offsets[n];
+    row0 = p.cu_seqlens[n];
+    L = p.cu_seqlens[n + 1] - row0;
+  } else {
+    const int nt = cdiv(p.T, C);
+    const int n = gc / nt;
+    c = gc % nt;
+    row0 = n * p.T;
+    L = p.T;
+  }
+  const int t0 = c * C;
+  const int nval = min(C, L - t0);
+  const long long rows_total = (long long)p.B * p.T;
+  const size_t e0 = (size_t)(row0 + t0) * H + hh;
+  const long long remr = (rows_total - (row0 + t0)) * (long long)H;
+  const uint32_t rowK = (uint32_t)(H * K), rowV = (uint32_t)(H * V);
+  const rsrc_t Rk = make_rsrc((const TIn*)p.k + e0 * K, remr * K * ES);
+  const rsrc_t Rg = make_rsrc(p.g + e0 * K, remr * K * 4);
+  const rsrc_t Rv = make_rsrc((const TIn*)p.v + e0 * V, remr * V * ES);
+  const rsrc_t Rvn = make_rsrc(p.vnew + e0 * V, remr * V * 4);
+  const rsrc_t Rb = make_rsrc(p.beta + e0, remr * 4);
+  const rsrc_t Rtt = make_rsrc(p.tt + ((size_t)gc * H + hh) * C * C, (long long)C * C * 4);
+  const rsrc_t Rdvt = make_rsrc(p.dvnt + ((size_t)gc * H + hh) * V * C, (long long)V * C * 4);
+  const rsrc_t Rh = make_rsrc(p.hs + ((size_t)gc * H + hh) * K * V, (long long)K * V * 4);
+
+  if (tid < C) sBeta[tid] = __uint_as_float(bld32(Rb, tid < nval ? (uint32_t)tid * H * 4u : kOOB, 0));
+
+  // ---------------- P^T tiles of token block R: P[i][v] = sum_i' T[i'][i] dv_new[i'][v]
+  {
+    const int i = 16 * R + l16;
+    bf16x8 th[2], tl[2];
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) load_split8(Rtt, ((uint32_t)i * C + 32 * kc + 8 * lg) * 4u, th[kc], tl[kc]);
+    const float bi = __uint_as_float(bld32(Rb, i < nval ? (uint32_t)i * H * 4u : kOOB, 0));
+    const rsrc_t Rdv = make_rsrc((TIn*)p.dv + e0 * V, remr * V * ES);
+    float dbv = 0.f;
+#pragma unroll
+    for (int vb = 0; vb < VP / 16; ++vb) {
+      const int v = 16 * vb + l16;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        if (kc == 1 || R < 2) {           // T[i'][i] = 0 for i' < i
+          bf16x8 ah, al;
+          load_split8(Rdvt, v < V ? ((uint32_t)v * C + 32 * kc + 8 * lg) * 4u : kOOB, ah, al);
+          acc = mma<true, true>(acc, ah, al, th[kc], tl[kc]);
+        }
+      }
+      // lane holds P[i][16vb + 4lg + r]
+      const float x[4] = {acc[0], acc[1], acc[2], acc[3]};
+      put_n<true, 4>(PP, i, 16 * vb + 4 * lg, x);
+      const int col = 16 * vb + 4 * lg;
+      const uint32_t off = (i < nval && col < V) ? ((uint32_t)i * rowV + col) * ES : kOOB;
+      float vv[4];
+      unpack4(Wd::ld4(Rv, off, 0), vv);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dbv += vv[r] * acc[r];
+      Wd::st4(Rdv, f32x4{bi * acc[0], bi * acc[1], bi * acc[2], bi * acc[3]}, off, 0);
+    }
+    dbv += __shfl_xor(dbv, 16, 64);
+    dbv += __shfl_xor(dbv, 32, 64);
+    if (lg == 0) sDb[i] = dbv;
+  }
+  __syncthreads();  // P plane, beta visible
+
+  // ---------------- dAkk tiles (registers, all passes)
+  // dar[J] (J <= R): lane holds dAkk[16R + l16][16J + 4lg + r]          (A operand, rows i)
+  // dac[I] (I >= R): lane holds beta_i dAkk[16I + 4lg + r][16R + l16]   (A operand, rows j)
+  uint2 darh[4], darl[4], dach[4], dacl[4];
+  {
+    bf16x8 pRh[VC], pRl[VC];
+#pragma unroll
+    for (int vc = 0; vc < VC; ++vc) {
+      pRh[vc] = PP.hi8(16 * R + l16, 32 * vc + 8 * lg);
+      pRl[vc] = PP.lo8(16 * R + l16, 32 * vc + 8 * lg);
+    }
+#pragma unroll
+    for (int J = 0; J < 4; ++J) {
+      darh[J] = darl[J] = dach[J] = dacl[J] = make_uint2(0u, 0u);
+      if (J <= R) {
+        f32x4 t = {0.f, 0.f, 0.f, 0.f};
+        const int j = 16 * J + l16;
+#pragma unroll
+        for (int vc = 0; vc < VC; ++vc) {
+          const int v0 = 32 * vc + 8 * lg;
+          bf16x8 ah, al;
+          load_split8(Rvn, (j < nval && v0 < V) ? ((uint32_t)j * rowV + v0) * 4u : kOOB, ah, al);
+          t = mma<true, true>(t, ah, al, pRh[vc], pRl[vc]);
+        }
+        // t = sum_v vn[j][v] P[i][v] at (j = 16J + 4lg + r, i = 16R + l16)
+        const int i = 16 * R + l16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) t[r] = (i > 16 * J + 4 * lg + r) ? -t[r] : 0.f;
+        acc_to_bf16x4(t, darh[J], darl[J]);
+      }
+    }
+    // B operand rows j of block R (v_new), shared by every dac tile
+    bf16x8 vRh[VC], vRl[VC];
+#pragma unroll
+    for (int vc = 0; vc < VC; ++vc) {
+      const int j = 16 * R + l16, v0 = 32 * vc + 8 * lg;
+      load_split8(Rvn, (j < nval && v0 < V) ? ((uint32_t)j * rowV + v0) * 4u : kOOB, vRh[vc], vRl[vc]);
+    }
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      if (I >= R) {
+        f32x4 t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int vc = 0; vc < VC; ++vc)
+          t = mma<true, true>(t, PP.hi8(16 * I + l16, 32 * vc + 8 * lg), PP.lo8(16 * I + l16, 32 * vc + 8 * lg),
+                              vRh[vc], vRl[vc]);
+        // t = sum_v P[i][v] vn[j][v] at (i = 16I + 4lg + r, j = 16R + l16)
+        const int j = 16 * R + l16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = 16 * I + 4 * lg + r;
+          t[r] = i > j ? -sBeta[i] * t[r] : 0.f;
+        }
+        acc_to_bf16x4(t, dach[I], dacl[I]);
+      }
+    }
+  }
+
+  // ---------------- channel passes
+  const rsrc_t Rdk = make_rsrc(p.dk_wy + e0 * K, remr * K * 4);
+  const rsrc_t Rdg = make_rsrc(p.dg_wy + e0 * K, remr * K * 4);
+  const int ch = tid & 31, sg = tid >> 5;
+  float dbk_acc[4] = {0.f, 0.f, 0.f, 0.f};   // per token 16R + 4lg + r: sum_d (2^G k dbk + k Y1)
+#pragma unroll 1
+  for (int ps = 0; ps < NPS; ++ps) {
+    const int cb = ps * KH;
+    // ---- staging: thread = (channel ch, rows 8sg..8sg+7)
+    {
+      const int kc = cb + ch;
+      float G[8], kv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int r = 8 * sg + i;
+        const bool ok = kc < K && r < nval;
+        const uint32_t off = (uint32_t)r * rowK + kc;
+        if constexpr (ES == 4) {
+          kv[i] = __uint_as_float(bld32(Rk, ok ? off * 4u : kOOB, 0));
+        } else {
+          const uint32_t wd = bld32(Rk, ok ? (off & ~1u) * 2u : kOOB, 0);
+          kv[i] = (off & 1u) ? __uint_as_float(wd & 0xffff0000u) : __uint_as_float(wd << 16);
+        }
+        const float x = __uint_as_float(bld32(Rg, ok ? off * 4u : kOOB, 0));
+        G[i] = x * kLog2e + (i > 0 ? G[i - 1] : 0.f);
+      }
+      __syncthreads();  // the previous pass is done with every pass array
+      sTot[sg * KH + ch] = G[7];
+      __syncthreads();
+      float pre = 0.f, gam = 0.f;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const float t = sTot[s * KH + ch];
+        if (s < sg) pre += t;
+        gam += t;
+      }
+      const float gmv = 0.5f * gam;
+      if (sg == 0) sGm[ch] = gmv;
+      float k1[8], k2[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        G[i] += pre;
+        sG[(8 * sg + i) * LG + ch] = G[i];
+        k1[i] = kv[i] * fast_exp2(G[i] - gmv);
+        k2[i] = kv[i] * fast_exp2(gmv - G[i]);
+      }
+      put_n<true, 8>(PK1t, ch, 8 * sg, k1);
+      put_n<true, 8>(PK2t, ch, 8 * sg, k2);
+    }
+    __syncthreads();  // pass planes, sG, sGm visible
+
+    float dgr[2][4];
+    float dkr[2][4];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const int kl = 16 * kb + l16;        // channel in the pass of this lane's result column
+      const int kk = cb + kl;
+      // dbk: -sum_v P[j][v] S[kk][v]
+      f32x4 db = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int vc = 0; vc < VC; ++vc) {
+        const int v0 = 32 * vc + 8 * lg;
+        bf16x8 bh, bl;
+        load_split8(Rh, (kk < K && v0 < V) ? ((uint32_t)kk * V + v0) * 4u : kOOB, bh, bl);
+        db = mma<true, true>(db, PP.hi8(16 * R + l16, v0), PP.lo8(16 * R + l16, v0), bh, bl);
+      }
+      // Y1 (rows i of block R) and Y2 (rows j of block R), contraction over tokens
+      f32x4 y1 = {0.f, 0.f, 0.f, 0.f}, y2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int Pp = 0; Pp < 2; ++Pp) {
+        const int P0 = 2 * Pp, P1 = 2 * Pp + 1;
+        if (P0 <= R)
+          y1 = mma<true, true>(y1, cat44(darh[P0], darh[P1]), cat44(darl[P0], darl[P1]),
+                               PK2t.hi44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
+                               PK2t.lo44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg));
+        if (P1 >= R)
+          y2 = mma<true, true>(y2, cat44(dach[P0], dach[P1]), cat44(dacl[P0], dacl[P1]),
+                               PK1t.hi44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
+                               PK1t.lo44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg));
+      }
+      // epilogue: lane holds (token 16R + 4lg + r, channel kk)
+      const float gmv = sGm[kl];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * R + 4 * lg + r;
+        const bool ok = kk < K && t < nval;
+        const uint32_t off = (uint32_t)t * rowK + kk;
+        float kv;
+        if constexpr (ES == 4) {
+          kv = __uint_as_float(bld32(Rk, ok ? off * 4u : kOOB, 0));
+        } else {
+          const uint32_t wd = bld32(Rk, ok ? (off & ~1u) * 2u : kOOB, 0);
+          kv = (off & 1u) ? __uint_as_float(wd & 0xffff0000u) : __uint_as_float(wd << 16);
+        }
+        const float Gt = sG[t * LG + kl];
+        const float e = fast_exp2(Gt);
+        const float b = sBeta[t];
+        const float dbkv = -db[r];
+        const float Y1 = y1[r] * fast_exp2(Gt - gmv);
+        const float Y2 = y2[r] * fast_exp2(gmv - Gt);
+        dkr[kb][r] = b * e * dbkv + b * Y1 + Y2;
+        dgr[kb][r] = b * e * kv * dbkv + b * kv * Y1 - kv * Y2;
+        dbk_acc[r] += e * kv * dbkv + kv * Y1;
+      }
+    }
+    // reverse in-chunk cumsum of dG: within the lane (r), over the 4 lane groups, then
+    // over the token blocks of later waves
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      dgr[kb][2] += dgr[kb][3];
+      dgr[kb][1] += dgr[kb][2];
+      dgr[kb][0] += dgr[kb][1];
+      const float tot = dgr[kb][0];
+      const float t1 = __shfl(tot, (lane & 15) + 16, 64);
+      const float t2 = __shfl(tot, (lane & 15) + 32, 64);
+      const float t3 = __shfl(tot, (lane & 15) + 48, 64);
+      const float add = (lg < 1 ? t1 : 0.f) + (lg < 2 ? t2 : 0.f) + (lg < 3 ? t3 : 0.f);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dgr[kb][r] += add;
+      if (lg == 0) sBlk[R * KH + 16 * kb + l16] = dgr[kb][0];   // block total
+    }
+    __syncthreads();  // block totals visible
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const int kl = 16 * kb + l16, kk = cb + kl;
+      float add = 0.f;
+#pragma unroll
+      for (int R2 = 1; R2 < 4; ++R2)
+        if (R2 > R) add += sBlk[R2 * KH + kl];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * R + 4 * lg + r;
+        const uint32_t off = (kk < K && t < nval) ? ((uint32_t)t * rowK + kk) * 4u : kOOB;
+        bst32(Rdg, __float_as_uint(dgr[kb][r] + add), off, 0);
+        bst32(Rdk, __float_as_uint(dkr[kb][r]), off, 0);
+      }
+    }
+  }
+
+  // ---------------- dbeta: channel sums over the 16 lanes of a group, plus sum_v v P
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) dbk_acc[r] += __shfl_xor(dbk_acc[r], o, 64);
+  }
+  if (l16 == 0) {
+    float* db = p.dbeta;
+    const rsrc_t Rdb = make_rsrc(db + e0, remr * 4);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 16 * R + 4 * lg + r;
+      bst32(Rdb, __float_as_uint(dbk_acc[r] + sDb[t]), t < nval ? (uint32_t)t * H * 4u : kOOB, 0);
+    }
+  }
+}
+
+template <typename TIn>
+hipError_t launch_kda_wy(const KdaWyParams& p, hipStream_t s) {
+  const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
+  const int vp = p.V <= 32 ? 32 : (p.V <= 64 ? 64 : 128);
+  dim3 grid(p.total * p.H), block(256);
+#define TOPS_KWY(KPV, VPV) \
+  if (kp == KPV && vp == VPV) { hipLaunchKernelGGL((kda_wy_kernel<TIn, KPV, VPV>), grid, block, 0, s, p); return hipGetLastError(); }
+  TOPS_KWY(32, 32) TOPS_KWY(32, 64) TOPS_KWY(32, 128)
+  TOPS_KWY(64, 32) TOPS_KWY(64, 64) TOPS_KWY(64, 128)
+  TOPS_KWY(128, 32) TOPS_KWY(128, 64) TOPS_KWY(128, 128)
+#undef TOPS_KWY
+  return hipErrorInvalidValue;
+}
+
+template hipError_t launch_kda_wy<uint16_t>(const KdaWyParams&, hipStream_t);
+template hipError_t launch_kda_wy<float>(const KdaWyParams&, hipStream_t);
+
+}  // namespace tops

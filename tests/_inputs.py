@@ -54,7 +54,7 @@ def varlen_cu(T_total, N, seed):
     return [0] + [int(c) for c in cuts] + [T_total]
 
 
-def kda_inputs(B, T, H, K, V, seed, gate_div=16.0, h0=False, grads=False):
+def kda_inputs(B, T, H, K, V, seed, gate_div=16.0, h0=False, grads=False, N=None):
     """BASELINE config-5 style KDA inputs: q, k ~ N(0,1) L2-normalised over K per (b,t,h)
     as x / sqrt(sum x^2 + 1e-6) (tops/cpu/ops/kda/fused_recurrent.py:14-18); v ~ N(0,1);
     beta = sigmoid(N(0,1)) [B,T,H]; g = logsigmoid(N(0,1)) / gate_div [B,T,H,K]."""
@@ -67,8 +67,9 @@ def kda_inputs(B, T, H, K, V, seed, gate_div=16.0, h0=False, grads=False):
              v=rng.standard_normal((B, T, H, V)).astype(np.float32),
              beta=(1.0 / (1.0 + np.exp(-rng.standard_normal((B, T, H))))).astype(np.float32),
              g=(logsigmoid(rng.standard_normal((B, T, H, K))) / gate_div).astype(np.float32))
-    d["h0"] = (0.1 * rng.standard_normal((B, H, K, V))).astype(np.float32) if h0 else None
+    n = B if N is None else N
+    d["h0"] = (0.1 * rng.standard_normal((n, H, K, V))).astype(np.float32) if h0 else None
     if grads:
         d["do"] = rng.standard_normal((B, T, H, V)).astype(np.float32)
-        d["dht"] = (0.1 * rng.standard_normal((B, H, K, V))).astype(np.float32)
+        d["dht"] = (0.1 * rng.standard_normal((n, H, K, V))).astype(np.float32)
     return d
