@@ -219,6 +219,9 @@ def main():
     ap.add_argument("--configs", default="2,4,5", help="secondary configs to measure")
     ap.add_argument("--only-secondary", action="store_true",
                     help="measure only the secondary configs (for profiling them alone)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="after the timed steps, copy a 1 GiB fp32 buffer 3 times: the known-size "
+                         "kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE")
     a = ap.parse_args()
     configs = tuple(int(x) for x in a.configs.split(",") if x)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -254,6 +257,13 @@ def main():
     t1 = time.perf_counter()
     ev = NT.timing_events()
     NT.enable_timing(False)
+    if a.copy_calibration:
+        src = torch.zeros(1 << 28, device=dev, dtype=torch.float32)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     elapsed = t1 - t0
     ms_step = elapsed * 1e3 / a.steps
     value = B * T * a.steps / elapsed
