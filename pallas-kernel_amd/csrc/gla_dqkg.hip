@@ -23,6 +23,8 @@
 // result layout: the reverse token cumsum of dg is a 16-lane shuffle scan plus a
 // cross-wave block total.  LDS holds the v / dO planes, the pass's gated q~^T / k~^T
 // planes and its fp32 gate cumsum: < 70 KB, so two workgroups share a CU.
+#include <type_traits>
+
 #include "gla_sweep.h"
 #include "tops_common.h"
 
@@ -63,7 +65,10 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
   __shared__ __attribute__((aligned(16))) float sZk[2 * KH];
   __shared__ __attribute__((aligned(16))) float sHdh[KH];
   __shared__ __attribute__((aligned(16))) float sBlk[KH];
-  __shared__ __attribute__((aligned(16))) float sDgS[2 * C];   // kGateS: per channel-block token sums
+  // kGateS: per channel-block token sums (the fp32-v instantiation serves only kGateK, and
+  // dropping this keeps it under 80 KB of LDS: two workgroups per CU)
+  constexpr bool kScalarGate = std::is_same<TIn, TV>::value;
+  __shared__ __attribute__((aligned(16))) float sDgS[kScalarGate ? 2 * C : 1];
 
   const Plane Pv{sV, SINV ? sV + C * LV : sV, LV};
   const Plane Pd{sD, SIN ? sD + C * LV : sD, LV};
@@ -225,11 +230,22 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
   const rsrc_t Rdga = make_rsrc(p.dg_add ? p.dg_add + e0 * K : nullptr, p.dg_add ? remr * K * 4 : 0);
   const rsrc_t Rdg = make_rsrc(p.dg ? (gmode == kGateS ? p.dg + e0 : p.dg + e0 * K) : nullptr,
                                p.dg ? remr * (gmode == kGateS ? 1 : K) * 4 : 0);
-  if (tid < 2 * C) sDgS[tid] = 0.f;
+  if (kScalarGate && tid < 2 * C) sDgS[tid] = 0.f;
 
 #pragma unroll 1
   for (int ps = 0; ps < NPS; ++ps) {
     const int cb = ps * KH;
+    // ---- this pass's h rows, issued before the staging so their latency overlaps it
+    const int kl = 16 * kb + l16;          // channel of this lane's A-operand row (in pass)
+    const int kk = cb + kl;
+    uint4 hraw[VC][2];
+#pragma unroll
+    for (int vc = 0; vc < VC; ++vc) {
+      const int v0 = 32 * vc + 8 * lg;
+      const uint32_t o = (kk < K && v0 < V) ? ((uint32_t)kk * V + v0) * 4u : kOOB;
+      hraw[vc][0] = bld128(Rh, o, 0);
+      hraw[vc][1] = bld128(Rh, o, 16);
+    }
     // ---- gate cumsum of the pass (thread: channel ch, rows 8sg..8sg+7)
     float G[8];
 #pragma unroll
@@ -268,8 +284,6 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
     __syncthreads();  // planes, sG, sGm, sGam visible
 
     // ---- inter-chunk: X^T += (alpha h) dO^T, W^T += (beta dh) v^T
-    const int kl = 16 * kb + l16;          // channel of this lane's A-operand row (in pass)
-    const int kk = cb + kl;
     const float al = scale * fast_exp2(sGm[kl]);
     const float be = fast_exp2(sGam[kl] - sGm[kl]);
     f32x4 X[2], Wt[2];
@@ -280,8 +294,8 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
       const int v0 = 32 * vc + 8 * lg;
       const uint32_t o = (kk < K && v0 < V) ? ((uint32_t)kk * V + v0) * 4u : kOOB;
       float hv[8], dv[8];
-      unpack4(bld128(Rh, o, 0), hv);
-      unpack4(bld128(Rh, o, 16), hv + 4);
+      unpack4(hraw[vc][0], hv);
+      unpack4(hraw[vc][1], hv + 4);
       unpack4(bld128(Rdh, o, 0), dv);
       unpack4(bld128(Rdh, o, 16), dv + 4);
       if (rh == 0) {
@@ -370,17 +384,28 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
       const int tok = 16 * (2 * rh + a) + l16;
       const bool ok = chok && tok < nval;
       const uint32_t off = (uint32_t)tok * rowK + kc;
-      float qv[4], kv[4];
-      unpack4(Wd::ld4(Rq, ok ? off * ES : kOOB, 0), qv);
-      unpack4(Wd::ld4(Rk, ok ? off * ES : kOOB, 0), kv);
       const float4 g4 = *(const float4*)(sG + tok * LG + cl);
       const float gr[4] = {g4.x, g4.y, g4.z, g4.w};
+      // fp32 inputs re-read q, k (exact); bf16 inputs use q dq - k dk = q~ X - k~ W with
+      // q~ / k~ read back from the pass planes (hi + lo: 2^-17 relative, far below bf16)
+      float qv[4], kv[4];
+      if constexpr (SIN) {
+        unpack4(Wd::ld4(Rq, ok ? off * ES : kOOB, 0), qv);
+        unpack4(Wd::ld4(Rk, ok ? off * ES : kOOB, 0), kv);
+      }
       f32x4 dqv, dkv;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         dqv[r] = fast_exp2(gr[r] - gmr[r]) * X[a][r];
         dkv[r] = fast_exp2(gmr[r] - gr[r]) * Wt[a][r];
-        dgr[a][r] = qv[r] * dqv[r] - kv[r] * dkv[r];
+        if constexpr (SIN) {
+          dgr[a][r] = qv[r] * dqv[r] - kv[r] * dkv[r];
+        } else {
+          const int pi = (cl + r) * LT + tok;
+          const float qt = bf16_to_f32(Pqt.hi[pi]) + bf16_to_f32(Pqt.lo[pi]);
+          const float kt = bf16_to_f32(Pkt.hi[pi]) + bf16_to_f32(Pkt.lo[pi]);
+          dgr[a][r] = qt * X[a][r] - kt * Wt[a][r];
+        }
       }
       if (p.dk_add) {
         float ka[4];
@@ -428,7 +453,7 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
                                __float_as_uint(dgr[a][2] + add[2] + ga[2]), __float_as_uint(dgr[a][3] + add[3] + ga[3])),
                ok ? off * 4u : kOOB, 0);
       }
-    } else if (gmode == kGateS) {
+    } else if (kScalarGate && gmode == kGateS) {
       // one gate per token: sum the per-channel gradients over this wave's 16 channels
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
@@ -443,7 +468,7 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
       }
     }
   }
-  if (gmode == kGateS && p.dg) {
+  if (kScalarGate && gmode == kGateS && p.dg) {
     __syncthreads();
     if (tid < C) {
       const float x = sDgS[tid] + sDgS[C + tid];
