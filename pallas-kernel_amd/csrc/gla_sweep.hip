@@ -8,11 +8,11 @@
 // (tops/ops/common/chunk_h.py:685-878) plus the dv part of K4 (chunk.py:1447-1509),
 // following the oracle tops/cpu/ops/gla/chunk.py:310-354, 387-427.
 //
-// One workgroup (4 wave64) owns one (sequence, head, 64-wide V tile) and walks the
-// sequence chunk by chunk (C = 64), forwards or backwards.  A K x 64 fp32 state S lives
-// in MFMA accumulators for the whole walk.  Per chunk, with G the in-chunk inclusive
-// gate cumsum (log2 units), Gamma = G[last], Gm = Gamma / 2, q~ = q 2^(G-Gm),
-// k~ = k 2^(Gm-G):
+// One workgroup (8 wave64, two per SIMD) owns one (sequence, head, 64-wide V tile) and
+// walks the sequence chunk by chunk (C = 64), forwards or backwards.  A K x 64 fp32 state S
+// lives in MFMA accumulators for the whole walk (4 tiles per wave at K = 128).  Per chunk,
+// with G the in-chunk inclusive gate cumsum (log2 units), Gamma = G[last], Gm = Gamma / 2,
+// q~ = q 2^(G-Gm), k~ = k 2^(Gm-G):
 //
 //   forward:  S = h (state before the chunk), Y = v
 //     o^T   = (scale 2^Gm S)^T q~^T + v^T M^T,   M[i][j] = scale q~_i.k~_j  (j <= i)
@@ -24,14 +24,21 @@
 // i.e. out^T = (alpha S)^T X~^T + Y^T D with (X~, Z~) = (q~, k~) forward and (k~, q~)
 // reverse, D[p][r] = scale Z~_p.X~_r on the causal side, and S = 2^Gamma S + beta Z~^T Y.
 // The midpoint Gm bounds every exponent by |Gamma|/2, the stabilisation of
-// tops/ops/gla/chunk.py:371-375.
+// tops/ops/gla/chunk.py:371-375.  Wave w computes the output tiles of token block w / 2 and
+// column tiles 2 (w % 2), 2 (w % 2) + 1 (the two waves of a token block both compute its
+// intra-chunk D tiles: MFMA has the headroom, a split would cost a barrier).
+//
+// DELTA (the KDA delta rule): forward, Y = v_new = u - w S is computed per chunk before the
+// output and the state update (w 2^-Gm is read from HBM as the MFMA A operand against
+// H^T = 2^Gm S); reverse, the state update gains - w^T dv_new, and dv_new is written
+// transposed per chunk for the WY backward.
 //
 // Every workgroup also writes S at the start of each chunk to `ckpt` when given (the
 // forward's state checkpoints, or the reverse sweep's dh per chunk).
 //
 // Pipelining: the raw q/k/g/Y of chunk c+1 are loaded into registers while chunk c is
-// computed; a full chunk takes a branch-free path (masked rows read a clamped in-bounds
-// address and are zeroed).  Two barriers per chunk.
+// computed; a full chunk takes a branch-free path (masked rows read out of range and are
+// zeroed by the buffer range check).  Two barriers per chunk (three or four with DELTA).
 #include "gla_sweep.h"
 #include "tops_common.h"
 #include "tops_hip.h"
@@ -40,20 +47,24 @@ namespace tops {
 
 
 template <typename TIn, int KP, bool REV, bool DELTA>
-__global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
+__global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
+  constexpr int NW = 8;                  // wave64s per workgroup
+  constexpr int NTH = 64 * NW;
   constexpr int C = kChunk, BV = 64;
   constexpr int NQ = KP / 4;             // column quads of a [C][KP] tile
-  constexpr int NSEG = 256 / NQ;         // row segments
-  constexpr int RPT = C / NSEG;          // rows per thread (2, 4, 8)
+  constexpr int NSEG = NTH / NQ;         // row segments
+  constexpr int RPT = C / NSEG;          // rows per thread (4, 2, 1)
+  constexpr int GPW = 64 / NQ;           // row segments per wave (2, 4, 8)
   constexpr bool SIN = !In<TIn>::kExactBf16;
   constexpr bool FWD_DELTA = DELTA && !REV;
   constexpr bool REV_DELTA = DELTA && REV;
   constexpr bool SY = SIN || FWD_DELTA;  // the Y plane carries a lo half (fp32 Y, or v_new)
   constexpr int LQ = KP + 8, LT = C + 8, LH = KP + 8;
-  constexpr int NHT = (KP / 16) * (BV / 16) / 4;  // state tiles per wave
-  constexpr int NM = NHT >= 4 ? NHT / 4 : 1;      // distinct K blocks per wave
+  constexpr int NHT = (KP / 16) * (BV / 16) / NW;  // state tiles per wave (4, 2, 1), one K block
   constexpr int ES = sizeof(TIn);
-  static_assert(RPT == 2 || RPT == 4 || RPT == 8, "KP must be 32, 64 or 128");
+  constexpr int YR = C * BV / (2 * NTH);           // Y rows per thread (2 columns each)
+  static_assert(RPT == 1 || RPT == 2 || RPT == 4, "KP must be 32, 64 or 128");
+  static_assert(YR == 4, "Y staging assumes 4 rows x 2 columns per thread");
   typedef Words<TIn> Wd;
 
   __shared__ __attribute__((aligned(16))) uint16_t sX[2 * C * LQ];
@@ -63,7 +74,10 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
   // (the reverse delta rule reuses sHT for the [BV][LT] dv_new^T plane: size for both)
   constexpr int NHTS = 2 * BV * (REV_DELTA && LT > LH ? LT : LH);
   __shared__ __attribute__((aligned(16))) uint16_t sHT[NHTS];
-  __shared__ __attribute__((aligned(16))) float sTot[NSEG * KP];
+  __shared__ __attribute__((aligned(16))) float sTot[NW * KP];   // per-wave gate totals
+  // Gamma / 2 of channel c sits in the padding columns of the X hi plane (row c / 4, word c % 4):
+  // no MFMA fragment or staging write touches columns >= KP
+  auto gm_at = [&](int c4) { return (float*)(sX + (c4 >> 2) * LQ + KP); };
 
   const Plane PX{sX, sX + C * LQ, LQ};
   const Plane PZ{sZ, sZ + C * LQ, LQ};
@@ -78,6 +92,9 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int l16 = lane & 15, lg = lane >> 4;
+  const int R = wave >> 1;               // token block of this wave's output tiles
+  const int nh = wave & 1;               // output column tiles nn = 2 nh, 2 nh + 1
+  const int msb = (wave * NHT) / (BV / 16);   // K block of this wave's state tiles
   const int wg = xcd_remap(blockIdx.x, gridDim.x, p.NV);
   const int vt = wg % p.NV;
   const int hh = (wg / p.NV) % p.H;
@@ -101,14 +118,15 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
   // ---- staging coordinates and per-thread byte offsets within a chunk
   const int cq = tid % NQ, seg = tid / NQ;
   const int c0 = 4 * cq, r0 = seg * RPT;
+  const int sw = lane / NQ;              // row segment within the wave
   const bool colok = c0 < K;
-  const int yc = tid & 31, yseg = tid >> 5;     // Y: 2 columns x 8 rows per thread
+  const int yc = tid & 31, yseg = tid >> 5;     // Y: 2 columns x 4 rows per thread
   const int yv = vt * BV + 2 * yc;
   const bool ycolok = yv < V;
   const uint32_t rowK = (uint32_t)(H * K), rowV = (uint32_t)(H * V);
   const uint32_t offQ = colok ? ((uint32_t)r0 * rowK + c0) * ES : kOOB;        // q, k
   const uint32_t offG = colok ? ((uint32_t)r0 * rowK + c0) * 4u : kOOB;        // g, w
-  const uint32_t offY = ycolok ? ((uint32_t)(yseg * 8) * rowV + yv) * ES : kOOB;
+  const uint32_t offY = ycolok ? ((uint32_t)(yseg * YR) * rowV + yv) * ES : kOOB;
   // gate load: per-channel [.., K] float4, or the per-(token, head) scalar read as the first
   // word of a 16-byte load; the gamma mode loads nothing (out of range -> 0)
   const int gmode = p.gate_mode;
@@ -117,15 +135,15 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
   const uint32_t gstride = gk_mode ? rowK * 4 : (uint32_t)H * 4;
   const float gam_h = gmode == kGateGamma ? p.g[hh] : 0.f;
 
-  // ---- state tiles: tile i of this wave -> (m, nn)
+  // ---- state tiles: tile i of this wave -> (msb, nn)
   f32x4 S[NHT];
 #pragma unroll
   for (int i = 0; i < NHT; ++i) {
-    const int t = wave * NHT + i, m = t / (BV / 16), nn = t % (BV / 16);
+    const int nn = (wave * NHT + i) % (BV / 16);
     const int vv = vt * BV + 16 * nn + l16;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int kr = 16 * m + 4 * lg + r;
+      const int kr = 16 * msb + 4 * lg + r;
       float x = 0.f;
       if (p.s0 && kr < K && vv < V) x = p.s0[((size_t)(n * H + hh) * K + kr) * V + vv];
       S[i][r] = x;
@@ -135,7 +153,7 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
   // ---- raw chunk registers (prefetch target)
   typename Wd::W4 rq[RPT], rk[RPT];
   uint4 rg[RPT];
-  typename Wd::W2 ry[8];
+  typename Wd::W2 ry[YR];
   auto load_chunk = [&](int c) {
     const int t0 = c * C;
     const int nval = min(C, L - t0);
@@ -156,8 +174,8 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
     if constexpr (!FWD_DELTA) {
       const rsrc_t Ry = make_rsrc((const TIn*)p.y + e0 * V, rem * V * ES);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const bool ok = yseg * 8 + i < nval;
+      for (int i = 0; i < YR; ++i) {
+        const bool ok = yseg * YR + i < nval;
         ry[i] = Wd::ld2(Ry, ok ? offY : kOOB, i * rowV * ES);
       }
     }
@@ -171,11 +189,9 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
     const int t0 = c * C;
     const int nval = min(C, L - t0);
 
-    // ---------------- delta rule: w rows of this thread (and u in the MFMA result
-    // layout for the forward), loaded now and consumed after barrier B2
+    // ---------------- reverse delta rule: w rows of this thread, consumed after barrier B3
     float4 rw[RPT];
-    float ru[BV / 16][4];
-    if constexpr (DELTA) {
+    if constexpr (REV_DELTA) {
       const size_t e0 = (size_t)(row0 + t0) * H + hh;
       const long long rem = (rows_total - (row0 + t0)) * (long long)H;
       const rsrc_t Rw = make_rsrc(p.w + e0 * K, rem * K * 4);
@@ -185,22 +201,10 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
         rw[i] = make_float4(__uint_as_float(x.x), __uint_as_float(x.y), __uint_as_float(x.z),
                             __uint_as_float(x.w));
       }
-      if constexpr (FWD_DELTA) {
-        const rsrc_t Ru = make_rsrc(p.u + e0 * V, rem * V * 4);
-#pragma unroll
-        for (int nn = 0; nn < BV / 16; ++nn) {
-          const int vv = vt * BV + 16 * nn + l16;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int tok = 16 * wave + 4 * lg + r;
-            ru[nn][r] = __uint_as_float(
-                bld32(Ru, (tok < nval && vv < V) ? ((uint32_t)tok * rowV + vv) * 4u : kOOB, 0));
-          }
-        }
-      }
     }
 
-    // ---------------- gate cumsum: thread-local rows, then segment totals via LDS
+    // ---------------- gate cumsum: thread rows, a shuffle scan over the wave's row
+    // segments, then per-wave totals through LDS
     float G[RPT][4];
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
@@ -213,27 +217,48 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) G[i][j] = x[j] * kLog2e + (i > 0 ? G[i - 1][j] : 0.f);
     }
-    *(float4*)(sTot + seg * KP + c0) = make_float4(G[RPT - 1][0], G[RPT - 1][1], G[RPT - 1][2], G[RPT - 1][3]);
+    float pre[4], gam[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float t = G[RPT - 1][j];
+      float x = t;
+#pragma unroll
+      for (int d = NQ; d < 64; d <<= 1) {
+        const float y = __shfl_up(x, d, 64);
+        if (lane >= d) x += y;
+      }
+      pre[j] = x - t;                    // segments before this one, within the wave
+      gam[j] = x;                        // inclusive; the last segment holds the wave total
+    }
+    if (sw == GPW - 1) *(float4*)(sTot + wave * KP + c0) = make_float4(gam[0], gam[1], gam[2], gam[3]);
     __syncthreads();  // B1: totals visible; every wave is done with the previous chunk's planes
 
-    float pre[4] = {0.f, 0.f, 0.f, 0.f}, gam[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < NSEG; ++s) {
-      const float4 t = *(const float4*)(sTot + s * KP + c0);
-      if (s < seg) { pre[0] += t.x; pre[1] += t.y; pre[2] += t.z; pre[3] += t.w; }
+    for (int j = 0; j < 4; ++j) gam[j] = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < NW; ++w2) {
+      const float4 t = *(const float4*)(sTot + w2 * KP + c0);
+      if (w2 < wave) { pre[0] += t.x; pre[1] += t.y; pre[2] += t.z; pre[3] += t.w; }
       gam[0] += t.x; gam[1] += t.y; gam[2] += t.z; gam[3] += t.w;
     }
-    // Gamma of this lane's state rows kr = 16 m + 4 lg + r
-    float sgam[NM][4];
+    float gm[4];
 #pragma unroll
-    for (int mi = 0; mi < NM; ++mi) {
-      const int m = (wave * NHT) / (BV / 16) + mi;
-      sgam[mi][0] = sgam[mi][1] = sgam[mi][2] = sgam[mi][3] = 0.f;
+    for (int j = 0; j < 4; ++j) gm[j] = 0.5f * gam[j];
+    if (seg == 0) *(float4*)gm_at(c0) = make_float4(gm[0], gm[1], gm[2], gm[3]);
+    // Gamma of this lane's state rows kr = 16 msb + 4 lg + r
+    float sgam[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < NSEG; ++s) {
-        const float4 t = *(const float4*)(sTot + s * KP + 16 * m + 4 * lg);
-        sgam[mi][0] += t.x; sgam[mi][1] += t.y; sgam[mi][2] += t.z; sgam[mi][3] += t.w;
-      }
+    for (int w2 = 0; w2 < NW; ++w2) {
+      const float4 t = *(const float4*)(sTot + w2 * KP + 16 * msb + 4 * lg);
+      sgam[0] += t.x; sgam[1] += t.y; sgam[2] += t.z; sgam[3] += t.w;
+    }
+    float sga[4], sal[4], sbe[4];        // 2^Gamma, alpha (H^T scaling), beta (update scaling)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float g2 = 0.5f * sgam[r];
+      sga[r] = fast_exp2(sgam[r]);
+      sal[r] = REV ? fast_exp2(sgam[r] - g2) : (DELTA ? 1.f : scale) * fast_exp2(g2);
+      sbe[r] = REV ? scale * fast_exp2(g2) : fast_exp2(sgam[r] - g2);
     }
 
     // ---------------- state -> H^T plane (alpha S); checkpoint of S
@@ -241,16 +266,11 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
                                  p.ckpt ? (long long)K * V * 4 : 0);
 #pragma unroll
     for (int i = 0; i < NHT; ++i) {
-      const int t = wave * NHT + i, m = t / (BV / 16), nn = t % (BV / 16);
-      const int mi = (NHT >= 4) ? i / 4 : 0;
-      const int kr = 16 * m + 4 * lg;
+      const int nn = (wave * NHT + i) % (BV / 16);
+      const int kr = 16 * msb + 4 * lg;
       float x[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float gm = 0.5f * sgam[mi][r];
-        const float alpha = REV ? fast_exp2(sgam[mi][r] - gm) : (DELTA ? 1.f : scale) * fast_exp2(gm);
-        x[r] = alpha * S[i][r];
-      }
+      for (int r = 0; r < 4; ++r) x[r] = sal[r] * S[i][r];
       put_n<true, 4>(PHt, 16 * nn + l16, kr, x);
       if (p.ckpt) {
         const int vv = vt * BV + 16 * nn + l16;
@@ -262,9 +282,6 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
     }
 
     // ---------------- gated operands for the staging rows
-    float gm[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) gm[j] = 0.5f * gam[j];
     {
       float zt[4][RPT];
 #pragma unroll
@@ -288,11 +305,11 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) put_n<true, RPT>(PZt, c0 + j, r0, zt[j]);
       if constexpr (!FWD_DELTA) {
-        float ya[8], yb[8];
+        float ya[YR], yb[YR];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) unpack2(ry[i], ya[i], yb[i]);
-        put_n<SY, 8>(PYt, 2 * yc, yseg * 8, ya);
-        put_n<SY, 8>(PYt, 2 * yc + 1, yseg * 8, yb);
+        for (int i = 0; i < YR; ++i) unpack2(ry[i], ya[i], yb[i]);
+        put_n<SY, YR>(PYt, 2 * yc, yseg * YR, ya);
+        put_n<SY, YR>(PYt, 2 * yc + 1, yseg * YR, yb);
       }
     }
     __syncthreads();  // B2: all planes visible
@@ -305,21 +322,20 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
     if constexpr (REV_DELTA) {
 #pragma unroll
       for (int i = 0; i < NHT; ++i) {
-        const int t = wave * NHT + i, m = t / (BV / 16), nn = t % (BV / 16);
+        const int nn = (wave * NHT + i) % (BV / 16);
         d1[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kc = 0; kc < C / 32; ++kc) {
           const bf16x8 bh = PYt.hi8(16 * nn + l16, 32 * kc + 8 * lg);
           bf16x8 bl = bh;
           if constexpr (SY) bl = PYt.lo8(16 * nn + l16, 32 * kc + 8 * lg);
-          d1[i] = mma<true, SY>(d1[i], PZt.hi8(16 * m + l16, 32 * kc + 8 * lg),
-                                PZt.lo8(16 * m + l16, 32 * kc + 8 * lg), bh, bl);
+          d1[i] = mma<true, SY>(d1[i], PZt.hi8(16 * msb + l16, 32 * kc + 8 * lg),
+                                PZt.lo8(16 * msb + l16, 32 * kc + 8 * lg), bh, bl);
         }
       }
     }
 
-    // ---------------- output block R = wave
-    const int R = wave;
+    // ---------------- output block: token block R, column tiles 2 nh, 2 nh + 1
     bf16x8 xh[KP / 32], xl[KP / 32];
 #pragma unroll
     for (int kc = 0; kc < KP / 32; ++kc) {
@@ -352,38 +368,50 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
     }
 
     if constexpr (FWD_DELTA) {
-      // v_new = u - w S for this wave's tokens.  Rows 16R.. of X are read only by this
-      // wave (above), so they now take w 2^-Gm, the A operand against H^T = 2^Gm S.
-      asm volatile("" ::: "memory");
-#pragma unroll
-      for (int i = 0; i < RPT; ++i) {
-        float x[4] = {rw[i].x, rw[i].y, rw[i].z, rw[i].w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) x[j] *= fast_exp2(-gm[j]);
-        put_n<true, 4>(PX, r0 + i, c0, x);
-      }
-      asm volatile("" ::: "memory");
+      // v_new = u - w S for (token block R, column tiles 2nh, 2nh+1).  The A operand
+      // w 2^-Gm is read straight from HBM in the MFMA row layout (against H^T = 2^Gm S).
       const size_t e0 = (size_t)(row0 + t0) * H + hh;
-      const rsrc_t Rvn = make_rsrc(p.y32 ? p.y32 + e0 * V : nullptr,
-                                   p.y32 ? (rows_total - (row0 + t0)) * (long long)H * V * 4 : 0);
+      const long long rem = (rows_total - (row0 + t0)) * (long long)H;
+      const rsrc_t Rw = make_rsrc(p.w + e0 * K, rem * K * 4);
+      const rsrc_t Ru = make_rsrc(p.u + e0 * V, rem * V * 4);
+      const rsrc_t Rvn = make_rsrc(p.y32 ? p.y32 + e0 * V : nullptr, p.y32 ? rem * V * 4 : 0);
+      const int trow = 16 * R + l16;
+      bf16x8 wh[KP / 32], wl[KP / 32];
 #pragma unroll
-      for (int nn = 0; nn < BV / 16; ++nn) {
+      for (int kc = 0; kc < KP / 32; ++kc) {
+        const int k0 = 32 * kc + 8 * lg;
+        const uint32_t o = (trow < nval && k0 < K) ? ((uint32_t)trow * rowK + k0) * 4u : kOOB;
+        float a[8];
+        unpack4(bld128(Rw, o, 0), a);
+        unpack4(bld128(Rw, o == kOOB ? kOOB : o + 16u, 0), a + 4);
+        const float4 g0 = *(const float4*)gm_at(k0), g1 = *(const float4*)gm_at(k0 + 4);
+        const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+        uint32_t h4[4], l4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          split_bf16x2(a[2 * e] * fast_exp2(-gg[2 * e]), a[2 * e + 1] * fast_exp2(-gg[2 * e + 1]), h4[e], l4[e]);
+        wh[kc] = __builtin_bit_cast(bf16x8, make_uint4(h4[0], h4[1], h4[2], h4[3]));
+        wl[kc] = __builtin_bit_cast(bf16x8, make_uint4(l4[0], l4[1], l4[2], l4[3]));
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int nn = 2 * nh + j;
+        const int vv = vt * BV + 16 * nn + l16;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kc = 0; kc < KP / 32; ++kc)
-          acc = mma<true, true>(acc, PX.hi8(16 * R + l16, 32 * kc + 8 * lg), PX.lo8(16 * R + l16, 32 * kc + 8 * lg),
-                                PHt.hi8(16 * nn + l16, 32 * kc + 8 * lg), PHt.lo8(16 * nn + l16, 32 * kc + 8 * lg));
+          acc = mma<true, true>(acc, wh[kc], wl[kc], PHt.hi8(16 * nn + l16, 32 * kc + 8 * lg),
+                                PHt.lo8(16 * nn + l16, 32 * kc + 8 * lg));
         // lane holds (token 16R + 4lg + r, column 16nn + l16)
         float vn[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) vn[r] = ru[nn][r] - acc[r];
-        put_n<true, 4>(PYt, 16 * nn + l16, 16 * R + 4 * lg, vn);
-        const int vv = vt * BV + 16 * nn + l16;
-#pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int tok = 16 * R + 4 * lg + r;
-          bst32(Rvn, __float_as_uint(vn[r]), (tok < nval && vv < V) ? ((uint32_t)tok * rowV + vv) * 4u : kOOB, 0);
+          const uint32_t o = (tok < nval && vv < V) ? ((uint32_t)tok * rowV + vv) * 4u : kOOB;
+          vn[r] = __uint_as_float(bld32(Ru, o, 0)) - acc[r];
+          bst32(Rvn, __float_as_uint(vn[r]), o, 0);
         }
+        put_n<true, 4>(PYt, 16 * nn + l16, 16 * R + 4 * lg, vn);
       }
       __syncthreads();  // B3: v_new^T plane complete
     }
@@ -391,10 +419,11 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
     if constexpr (REV_DELTA) {
       // dv_new = k~ (alpha dS) + D^T dO, token-major: lane holds (token 16R + 4lg + r,
       // column 16nn + l16); stored transposed per chunk ([V][C]) and kept for the update
-      f32x4 dvn[BV / 16];
+      f32x4 dvn[2];
       const rsrc_t Rd = make_rsrc(p.y32 + ((size_t)(cbase + c) * H + hh) * V * C, (long long)V * C * 4);
 #pragma unroll
-      for (int nn = 0; nn < BV / 16; ++nn) {
+      for (int j = 0; j < 2; ++j) {
+        const int nn = 2 * nh + j;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kc = 0; kc < KP / 32; ++kc)
@@ -410,7 +439,7 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
             acc = mma<true, SY>(acc, cat44(dh[P0], dh[P1]), cat44(dl[P0], dl[P1]), bh, bl);
           }
         }
-        dvn[nn] = acc;
+        dvn[j] = acc;
         const int vv = vt * BV + 16 * nn + l16;
         bst128(Rd, make_uint4(__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]),
                               __float_as_uint(acc[3])),
@@ -418,9 +447,9 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
       }
       __syncthreads();  // B3: every wave is done with X, Z, Z^T, Y^T and H^T
 #pragma unroll
-      for (int nn = 0; nn < BV / 16; ++nn) {
-        const float x[4] = {dvn[nn][0], dvn[nn][1], dvn[nn][2], dvn[nn][3]};
-        put_n<true, 4>(PDt, 16 * nn + l16, 16 * R + 4 * lg, x);
+      for (int j = 0; j < 2; ++j) {
+        const float x[4] = {dvn[j][0], dvn[j][1], dvn[j][2], dvn[j][3]};
+        put_n<true, 4>(PDt, 16 * (2 * nh + j) + l16, 16 * R + 4 * lg, x);
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -438,7 +467,8 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
                                   (rows_total - (row0 + t0)) * (long long)H * V * ES);
       const uint32_t oo = (tok < nval) ? ((uint32_t)tok * rowV + vt * BV + 4 * lg) * ES : kOOB;
 #pragma unroll
-      for (int nn = 0; nn < BV / 16; ++nn) {
+      for (int j = 0; j < 2; ++j) {
+        const int nn = 2 * nh + j;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kc = 0; kc < KP / 32; ++kc)
@@ -464,13 +494,12 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
     // ---------------- state update: S = 2^Gamma S + beta (Z~^T Y) [- w^T dv_new]
 #pragma unroll
     for (int i = 0; i < NHT; ++i) {
-      const int t = wave * NHT + i, m = t / (BV / 16), nn = t % (BV / 16);
-      const int mi = (NHT >= 4) ? i / 4 : 0;
+      const int nn = (wave * NHT + i) % (BV / 16);
       f32x4 d = {0.f, 0.f, 0.f, 0.f};
       if constexpr (REV_DELTA) {
 #pragma unroll
         for (int kc = 0; kc < C / 32; ++kc)
-          d = mma<true, true>(d, PWt.hi8(16 * m + l16, 32 * kc + 8 * lg), PWt.lo8(16 * m + l16, 32 * kc + 8 * lg),
+          d = mma<true, true>(d, PWt.hi8(16 * msb + l16, 32 * kc + 8 * lg), PWt.lo8(16 * msb + l16, 32 * kc + 8 * lg),
                               PDt.hi8(16 * nn + l16, 32 * kc + 8 * lg), PDt.lo8(16 * nn + l16, 32 * kc + 8 * lg));
       } else {
 #pragma unroll
@@ -478,16 +507,14 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
           const bf16x8 bh = PYt.hi8(16 * nn + l16, 32 * kc + 8 * lg);
           bf16x8 bl = bh;
           if constexpr (SY) bl = PYt.lo8(16 * nn + l16, 32 * kc + 8 * lg);
-          d = mma<true, SY>(d, PZt.hi8(16 * m + l16, 32 * kc + 8 * lg),
-                            PZt.lo8(16 * m + l16, 32 * kc + 8 * lg), bh, bl);
+          d = mma<true, SY>(d, PZt.hi8(16 * msb + l16, 32 * kc + 8 * lg),
+                            PZt.lo8(16 * msb + l16, 32 * kc + 8 * lg), bh, bl);
         }
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float ga = sgam[mi][r], gmv = 0.5f * ga;
-        const float beta = REV ? scale * fast_exp2(gmv) : fast_exp2(ga - gmv);
-        if constexpr (REV_DELTA) S[i][r] = fast_exp2(ga) * S[i][r] + beta * d1[i][r] - d[r];
-        else S[i][r] = fast_exp2(ga) * S[i][r] + beta * d[r];
+        if constexpr (REV_DELTA) S[i][r] = sga[r] * S[i][r] + sbe[r] * d1[i][r] - d[r];
+        else S[i][r] = sga[r] * S[i][r] + sbe[r] * d[r];
       }
     }
   }
@@ -495,11 +522,11 @@ __global__ __launch_bounds__(256) void gla_sweep_kernel(SweepParams p) {
   if (p.s_fin) {
 #pragma unroll
     for (int i = 0; i < NHT; ++i) {
-      const int t = wave * NHT + i, m = t / (BV / 16), nn = t % (BV / 16);
+      const int nn = (wave * NHT + i) % (BV / 16);
       const int vv = vt * BV + 16 * nn + l16;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int kr = 16 * m + 4 * lg + r;
+        const int kr = 16 * msb + 4 * lg + r;
         if (kr < K && vv < V) p.s_fin[((size_t)(n * H + hh) * K + kr) * V + vv] = S[i][r];
       }
     }
@@ -510,9 +537,9 @@ template <typename TIn, bool REV, bool DELTA>
 hipError_t launch_gla_sweep(const SweepParams& p, hipStream_t s) {
   const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
   dim3 grid(p.NV * p.H * p.N);
-  if (kp == 32) hipLaunchKernelGGL((gla_sweep_kernel<TIn, 32, REV, DELTA>), grid, dim3(256), 0, s, p);
-  else if (kp == 64) hipLaunchKernelGGL((gla_sweep_kernel<TIn, 64, REV, DELTA>), grid, dim3(256), 0, s, p);
-  else hipLaunchKernelGGL((gla_sweep_kernel<TIn, 128, REV, DELTA>), grid, dim3(256), 0, s, p);
+  if (kp == 32) hipLaunchKernelGGL((gla_sweep_kernel<TIn, 32, REV, DELTA>), grid, dim3(512), 0, s, p);
+  else if (kp == 64) hipLaunchKernelGGL((gla_sweep_kernel<TIn, 64, REV, DELTA>), grid, dim3(512), 0, s, p);
+  else hipLaunchKernelGGL((gla_sweep_kernel<TIn, 128, REV, DELTA>), grid, dim3(512), 0, s, p);
   return hipGetLastError();
 }
 

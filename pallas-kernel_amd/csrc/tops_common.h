@@ -250,27 +250,35 @@ template <> struct Words<float> {
   }
 };
 
-// write n (2, 4 or 8) consecutive contraction values of one plane row, hi (and lo)
+// write n (1, 2, 4 or 8) consecutive contraction values of one plane row, hi (and lo)
 template <bool SPLIT, int NE>
 __device__ __forceinline__ void put_n(const Plane& P, int r, int c, const float* x) {
-  uint32_t h[NE / 2], l[NE / 2];
-#pragma unroll
-  for (int i = 0; i < NE / 2; ++i) {
-    if constexpr (SPLIT) split_bf16x2(x[2 * i], x[2 * i + 1], h[i], l[i]);
-    else h[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
-  }
-  uint16_t* ph = P.hi + r * P.ld + c;
-  uint16_t* pl = P.lo + r * P.ld + c;
-  if constexpr (NE == 2) {
-    *(uint32_t*)ph = h[0];
-    if constexpr (SPLIT) *(uint32_t*)pl = l[0];
-  } else if constexpr (NE == 4) {
-    *(uint2*)ph = make_uint2(h[0], h[1]);
-    if constexpr (SPLIT) *(uint2*)pl = make_uint2(l[0], l[1]);
+  if constexpr (NE == 1) {
+    uint32_t h, l;
+    if constexpr (SPLIT) split_bf16x2(x[0], 0.f, h, l);
+    else h = pack_bf16x2(x[0], 0.f);
+    P.hi[r * P.ld + c] = (uint16_t)(h & 0xffffu);
+    if constexpr (SPLIT) P.lo[r * P.ld + c] = (uint16_t)(l & 0xffffu);
   } else {
-    static_assert(NE == 8, "2, 4 or 8 elements");
-    *(uint4*)ph = make_uint4(h[0], h[1], h[2], h[3]);
-    if constexpr (SPLIT) *(uint4*)pl = make_uint4(l[0], l[1], l[2], l[3]);
+    uint32_t h[NE / 2], l[NE / 2];
+#pragma unroll
+    for (int i = 0; i < NE / 2; ++i) {
+      if constexpr (SPLIT) split_bf16x2(x[2 * i], x[2 * i + 1], h[i], l[i]);
+      else h[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+    }
+    uint16_t* ph = P.hi + r * P.ld + c;
+    uint16_t* pl = P.lo + r * P.ld + c;
+    if constexpr (NE == 2) {
+      *(uint32_t*)ph = h[0];
+      if constexpr (SPLIT) *(uint32_t*)pl = l[0];
+    } else if constexpr (NE == 4) {
+      *(uint2*)ph = make_uint2(h[0], h[1]);
+      if constexpr (SPLIT) *(uint2*)pl = make_uint2(l[0], l[1]);
+    } else {
+      static_assert(NE == 8, "1, 2, 4 or 8 elements");
+      *(uint4*)ph = make_uint4(h[0], h[1], h[2], h[3]);
+      if constexpr (SPLIT) *(uint4*)pl = make_uint4(l[0], l[1], l[2], l[3]);
+    }
   }
 }
 
