@@ -150,11 +150,16 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     }
   }
 
-  // ---- raw chunk registers (prefetch target)
-  typename Wd::W4 rq[RPT], rk[RPT];
-  uint4 rg[RPT];
-  typename Wd::W2 ry[YR];
-  auto load_chunk = [&](int c) {
+  // ---- raw chunk registers (prefetch targets): PF sets, the chunk PF steps ahead is
+  // loaded into the set just consumed
+  constexpr int PF = (DELTA || SIN) ? 1 : 2;   // two sets fit the register budget for bf16
+  struct Raw {
+    typename Wd::W4 rq[RPT], rk[RPT];
+    uint4 rg[RPT];
+    typename Wd::W2 ry[YR];
+  };
+  Raw rsA, rsB;
+  auto load_chunk = [&](int c, Raw& rs) {
     const int t0 = c * C;
     const int nval = min(C, L - t0);
     const size_t e0 = (size_t)(row0 + t0) * H + hh;     // first row of the chunk, this head
@@ -165,27 +170,30 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
       const bool ok = r0 + i < nval;
-      rq[i] = Wd::ld4(Rq, ok ? offQ : kOOB, i * rowK * ES);
-      rk[i] = Wd::ld4(Rk, ok ? offQ : kOOB, i * rowK * ES);
+      rs.rq[i] = Wd::ld4(Rq, ok ? offQ : kOOB, i * rowK * ES);
+      rs.rk[i] = Wd::ld4(Rk, ok ? offQ : kOOB, i * rowK * ES);
       // one unconditional load whatever the gate mode (the mode's transform is applied
       // when the chunk is consumed, so the prefetch never waits)
-      rg[i] = bld128(Rg, ok ? offGm : kOOB, i * gstride);
+      rs.rg[i] = bld128(Rg, ok ? offGm : kOOB, i * gstride);
     }
     if constexpr (!FWD_DELTA) {
       const rsrc_t Ry = make_rsrc((const TIn*)p.y + e0 * V, rem * V * ES);
 #pragma unroll
       for (int i = 0; i < YR; ++i) {
         const bool ok = yseg * YR + i < nval;
-        ry[i] = Wd::ld2(Ry, ok ? offY : kOOB, i * rowV * ES);
+        rs.ry[i] = Wd::ld2(Ry, ok ? offY : kOOB, i * rowV * ES);
       }
     }
   };
 
-  const int cfirst = REV ? NTs - 1 : 0;
-  load_chunk(cfirst);
+  auto cidx = [&](int it) { return REV ? NTs - 1 - it : it; };
+  load_chunk(cidx(0), rsA);
+  if constexpr (PF == 2) {
+    if (NTs > 1) load_chunk(cidx(1), rsB);
+  }
 
-  for (int it = 0; it < NTs; ++it) {
-    const int c = REV ? NTs - 1 - it : it;
+  auto body = [&](int it, Raw& rs) {
+    const int c = cidx(it);
     const int t0 = c * C;
     const int nval = min(C, L - t0);
 
@@ -209,7 +217,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
       float x[4];
-      unpack4(rg[i], x);
+      unpack4(rs.rg[i], x);
       if (!gk_mode) {
         const float s1 = gmode == kGateS ? x[0] : (r0 + i < nval ? gam_h : 0.f);
         x[0] = x[1] = x[2] = x[3] = s1;
@@ -287,8 +295,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 #pragma unroll
       for (int i = 0; i < RPT; ++i) {
         float qv[4], kv[4], xq[4], xk[4];
-        unpack4(rq[i], qv);
-        unpack4(rk[i], kv);
+        unpack4(rs.rq[i], qv);
+        unpack4(rs.rk[i], kv);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const float Gv = G[i][j] + pre[j];
@@ -307,15 +315,15 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       if constexpr (!FWD_DELTA) {
         float ya[YR], yb[YR];
 #pragma unroll
-        for (int i = 0; i < YR; ++i) unpack2(ry[i], ya[i], yb[i]);
+        for (int i = 0; i < YR; ++i) unpack2(rs.ry[i], ya[i], yb[i]);
         put_n<SY, YR>(PYt, 2 * yc, yseg * YR, ya);
         put_n<SY, YR>(PYt, 2 * yc + 1, yseg * YR, yb);
       }
     }
     __syncthreads();  // B2: all planes visible
 
-    // ---------------- prefetch the next chunk while this one is computed
-    if (it + 1 < NTs) load_chunk(REV ? c - 1 : c + 1);
+    // ---------------- prefetch the chunk PF steps ahead while this one is computed
+    if (it + PF < NTs) load_chunk(cidx(it + PF), rs);
 
     // ---------------- reverse delta rule: first half of the state update (Z~^T Y)
     f32x4 d1[NHT];
@@ -517,6 +525,15 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
         else S[i][r] = sga[r] * S[i][r] + sbe[r] * d[r];
       }
     }
+  };
+
+  if constexpr (PF == 2) {
+    for (int it = 0; it < NTs; it += 2) {
+      body(it, rsA);
+      if (it + 1 < NTs) body(it + 1, rsB);
+    }
+  } else {
+    for (int it = 0; it < NTs; ++it) body(it, rsA);
   }
 
   if (p.s_fin) {
