@@ -197,6 +197,37 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     const int t0 = c * C;
     const int nval = min(C, L - t0);
 
+    // ---------------- forward delta rule: w rows of this wave's token block (MFMA row layout)
+    // and u in the result layout, issued now so their latency overlaps the staging
+    // (bf16 only: the fp32 instantiation has no register room and loads them after B2)
+    constexpr bool HOIST = FWD_DELTA && !SIN;
+    uint4 wraw[KP / 32][2];
+    float ur[2][4];
+    auto load_wu = [&]() {
+      const size_t e0 = (size_t)(row0 + t0) * H + hh;
+      const long long rem = (rows_total - (row0 + t0)) * (long long)H;
+      const rsrc_t Rw = make_rsrc(p.w + e0 * K, rem * K * 4);
+      const rsrc_t Ru = make_rsrc(p.u + e0 * V, rem * V * 4);
+      const int trow = 16 * R + l16;
+#pragma unroll
+      for (int kc = 0; kc < KP / 32; ++kc) {
+        const int k0 = 32 * kc + 8 * lg;
+        const uint32_t o = (trow < nval && k0 < K) ? ((uint32_t)trow * rowK + k0) * 4u : kOOB;
+        wraw[kc][0] = bld128(Rw, o, 0);
+        wraw[kc][1] = bld128(Rw, o == kOOB ? kOOB : o + 16u, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int vv = vt * BV + 16 * (2 * nh + j) + l16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tok = 16 * R + 4 * lg + r;
+          ur[j][r] = __uint_as_float(bld32(Ru, (tok < nval && vv < V) ? ((uint32_t)tok * rowV + vv) * 4u : kOOB, 0));
+        }
+      }
+    };
+    if constexpr (HOIST) load_wu();
+
     // ---------------- reverse delta rule: w rows of this thread, consumed after barrier B3
     float4 rw[RPT];
     if constexpr (REV_DELTA) {
@@ -380,18 +411,23 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       // w 2^-Gm is read straight from HBM in the MFMA row layout (against H^T = 2^Gm S).
       const size_t e0 = (size_t)(row0 + t0) * H + hh;
       const long long rem = (rows_total - (row0 + t0)) * (long long)H;
+      const rsrc_t Rvn = make_rsrc(p.y32 ? p.y32 + e0 * V : nullptr, p.y32 ? rem * V * 4 : 0);
       const rsrc_t Rw = make_rsrc(p.w + e0 * K, rem * K * 4);
       const rsrc_t Ru = make_rsrc(p.u + e0 * V, rem * V * 4);
-      const rsrc_t Rvn = make_rsrc(p.y32 ? p.y32 + e0 * V : nullptr, p.y32 ? rem * V * 4 : 0);
-      const int trow = 16 * R + l16;
       bf16x8 wh[KP / 32], wl[KP / 32];
 #pragma unroll
       for (int kc = 0; kc < KP / 32; ++kc) {
         const int k0 = 32 * kc + 8 * lg;
-        const uint32_t o = (trow < nval && k0 < K) ? ((uint32_t)trow * rowK + k0) * 4u : kOOB;
         float a[8];
-        unpack4(bld128(Rw, o, 0), a);
-        unpack4(bld128(Rw, o == kOOB ? kOOB : o + 16u, 0), a + 4);
+        if constexpr (HOIST) {
+          unpack4(wraw[kc][0], a);
+          unpack4(wraw[kc][1], a + 4);
+        } else {
+          const int trow = 16 * R + l16;
+          const uint32_t o = (trow < nval && k0 < K) ? ((uint32_t)trow * rowK + k0) * 4u : kOOB;
+          unpack4(bld128(Rw, o, 0), a);
+          unpack4(bld128(Rw, o == kOOB ? kOOB : o + 16u, 0), a + 4);
+        }
         const float4 g0 = *(const float4*)gm_at(k0), g1 = *(const float4*)gm_at(k0 + 4);
         const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
         uint32_t h4[4], l4[4];
@@ -416,7 +452,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
         for (int r = 0; r < 4; ++r) {
           const int tok = 16 * R + 4 * lg + r;
           const uint32_t o = (tok < nval && vv < V) ? ((uint32_t)tok * rowV + vv) * 4u : kOOB;
-          vn[r] = __uint_as_float(bld32(Ru, o, 0)) - acc[r];
+          vn[r] = (HOIST ? ur[j][r] : __uint_as_float(bld32(Ru, o, 0))) - acc[r];
           bst32(Rvn, __float_as_uint(vn[r]), o, 0);
         }
         put_n<true, 4>(PYt, 16 * nn + l16, 16 * R + 4 * lg, vn);
