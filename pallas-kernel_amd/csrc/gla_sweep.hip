@@ -98,7 +98,25 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   const int wg = xcd_remap(blockIdx.x, gridDim.x, p.NV);
   const int vt = wg % p.NV;
   const int hh = (wg / p.NV) % p.H;
-  const int n = wg / (p.NV * p.H);
+  int n = wg / (p.NV * p.H);
+  if (p.cu_seqlens && p.N > 1 && p.N <= 256) {
+    // Varlen: dispatch sequences longest first (LPT), so the workgroups that share a CU
+    // balance; slot r takes the sequence of rank r in descending length (ties by index).
+    const int slot = n;
+    if (tid < p.N) {
+      const int li = p.cu_seqlens[tid + 1] - p.cu_seqlens[tid];
+      int rank = 0;
+      for (int j = 0; j < p.N; ++j) {
+        const int lj = p.cu_seqlens[j + 1] - p.cu_seqlens[j];
+        rank += (lj > li) || (lj == li && j < tid);
+      }
+      if (rank == slot) *(int*)sTot = tid;
+    }
+    __syncthreads();
+    n = *(const int*)sTot;
+    __syncthreads();  // sTot is reused by the chunk loop
+  }
+  n = __builtin_amdgcn_readfirstlane(n);
   const int H = p.H, K = p.K, V = p.V;
   const float scale = p.scale;
 
