@@ -49,6 +49,7 @@ __global__ __launch_bounds__(256, 2) void kda_wy_kernel(KdaWyParams p) {
   constexpr int KH = 32;                 // channels per pass
   constexpr int NPS = KP / KH;
   constexpr int VC = VP / 32;
+  constexpr int NVB = VP / 16;           // 16-wide V blocks
   constexpr int ES = sizeof(TIn);
   constexpr int LP = VP + 8, LT = C + 8, LG = KH + 4;
   static_assert(KP % KH == 0 && VP % 32 == 0, "KP, VP must be 32, 64 or 128");
@@ -60,16 +61,18 @@ __global__ __launch_bounds__(256, 2) void kda_wy_kernel(KdaWyParams p) {
   __shared__ __attribute__((aligned(16))) float sG[C * LG];
   __shared__ __attribute__((aligned(16))) float sTot[8 * KH];
   __shared__ __attribute__((aligned(16))) float sGm[KH];
-  __shared__ __attribute__((aligned(16))) float sBlk[4 * KH];
+  __shared__ __attribute__((aligned(16))) float sBlk[2 * 16];     // per channel half: tokens 32..63 total
   __shared__ float sBeta[C];
-  __shared__ float sDb[C];
+  __shared__ float sDbv[4 * C];         // per wave: sum_v v P over its V blocks
+  __shared__ float sDbk[2 * C];         // per channel half: sum_d (2^G k dbk + k Y1)
 
   const Plane PP{sP, sP + C * LP, LP};
   const Plane PK1t{sK1t, sK1t + KH * LT, LT};
   const Plane PK2t{sK2t, sK2t + KH * LT, LT};
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int R = __builtin_amdgcn_readfirstlane(tid >> 6);   // token block of this wave
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kb = wave & 1, tp = wave >> 1;   // channel half of a pass, token-block pair
   const int l16 = lane & 15, lg = lane >> 4;
   const int hh = blockIdx.x % p.H;
   const int gc = blockIdx.x / p.H;
@@ -104,111 +107,127 @@ __global__ __launch_bounds__(256, 2) void kda_wy_kernel(KdaWyParams p) {
   const rsrc_t Rh = make_rsrc(p.hs + ((size_t)gc * H + hh) * K * V, (long long)K * V * 4);
 
   if (tid < C) sBeta[tid] = __uint_as_float(bld32(Rb, tid < nval ? (uint32_t)tid * H * 4u : kOOB, 0));
+  __syncthreads();  // beta visible
 
-  // ---------------- P^T tiles of token block R: P[i][v] = sum_i' T[i'][i] dv_new[i'][v]
+  // ---------------- P = T^T dv_new: wave w takes the V blocks vb = w, w + 4, ..; tile (vb, I)
+  // computed transposed, lane holds P[16I + l16][16vb + 4lg + r]
   {
-    const int i = 16 * R + l16;
-    bf16x8 th[2], tl[2];
-#pragma unroll
-    for (int kc = 0; kc < 2; ++kc) load_split8(Rtt, ((uint32_t)i * C + 32 * kc + 8 * lg) * 4u, th[kc], tl[kc]);
-    const float bi = __uint_as_float(bld32(Rb, i < nval ? (uint32_t)i * H * 4u : kOOB, 0));
     const rsrc_t Rdv = make_rsrc((TIn*)p.dv + e0 * V, remr * V * ES);
-    float dbv = 0.f;
-#pragma unroll
-    for (int vb = 0; vb < VP / 16; ++vb) {
+    float dbv[4] = {0.f, 0.f, 0.f, 0.f};        // per token block I: sum_v v P (this lane's v's)
+    for (int vb = wave; vb < NVB; vb += 4) {
       const int v = 16 * vb + l16;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      bf16x8 ah[2], al[2];
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc) {
-        if (kc == 1 || R < 2) {           // T[i'][i] = 0 for i' < i
-          bf16x8 ah, al;
-          load_split8(Rdvt, v < V ? ((uint32_t)v * C + 32 * kc + 8 * lg) * 4u : kOOB, ah, al);
-          acc = mma<true, true>(acc, ah, al, th[kc], tl[kc]);
+      for (int kc = 0; kc < 2; ++kc)
+        load_split8(Rdvt, v < V ? ((uint32_t)v * C + 32 * kc + 8 * lg) * 4u : kOOB, ah[kc], al[kc]);
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        const int i = 16 * I + l16;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+          if (kc == 1 || I < 2) {           // T[i'][i] = 0 for i' < i
+            bf16x8 th, tl;
+            load_split8(Rtt, ((uint32_t)i * C + 32 * kc + 8 * lg) * 4u, th, tl);
+            acc = mma<true, true>(acc, ah[kc], al[kc], th, tl);
+          }
         }
+        const float x[4] = {acc[0], acc[1], acc[2], acc[3]};
+        put_n<true, 4>(PP, i, 16 * vb + 4 * lg, x);
+        const int col = 16 * vb + 4 * lg;
+        const uint32_t off = (i < nval && col < V) ? ((uint32_t)i * rowV + col) * ES : kOOB;
+        float vv[4];
+        unpack4(Wd::ld4(Rv, off, 0), vv);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dbv[I] += vv[r] * acc[r];
+        const float bi = sBeta[i];
+        Wd::st4(Rdv, f32x4{bi * acc[0], bi * acc[1], bi * acc[2], bi * acc[3]}, off, 0);
       }
-      // lane holds P[i][16vb + 4lg + r]
-      const float x[4] = {acc[0], acc[1], acc[2], acc[3]};
-      put_n<true, 4>(PP, i, 16 * vb + 4 * lg, x);
-      const int col = 16 * vb + 4 * lg;
-      const uint32_t off = (i < nval && col < V) ? ((uint32_t)i * rowV + col) * ES : kOOB;
-      float vv[4];
-      unpack4(Wd::ld4(Rv, off, 0), vv);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) dbv += vv[r] * acc[r];
-      Wd::st4(Rdv, f32x4{bi * acc[0], bi * acc[1], bi * acc[2], bi * acc[3]}, off, 0);
-    }
-    dbv += __shfl_xor(dbv, 16, 64);
-    dbv += __shfl_xor(dbv, 32, 64);
-    if (lg == 0) sDb[i] = dbv;
-  }
-  __syncthreads();  // P plane, beta visible
-
-  // ---------------- dAkk tiles (registers, all passes)
-  // dar[J] (J <= R): lane holds dAkk[16R + l16][16J + 4lg + r]          (A operand, rows i)
-  // dac[I] (I >= R): lane holds beta_i dAkk[16I + 4lg + r][16R + l16]   (A operand, rows j)
-  uint2 darh[4], darl[4], dach[4], dacl[4];
-  {
-    bf16x8 pRh[VC], pRl[VC];
-#pragma unroll
-    for (int vc = 0; vc < VC; ++vc) {
-      pRh[vc] = PP.hi8(16 * R + l16, 32 * vc + 8 * lg);
-      pRl[vc] = PP.lo8(16 * R + l16, 32 * vc + 8 * lg);
-    }
-#pragma unroll
-    for (int J = 0; J < 4; ++J) {
-      darh[J] = darl[J] = dach[J] = dacl[J] = make_uint2(0u, 0u);
-      if (J <= R) {
-        f32x4 t = {0.f, 0.f, 0.f, 0.f};
-        const int j = 16 * J + l16;
-#pragma unroll
-        for (int vc = 0; vc < VC; ++vc) {
-          const int v0 = 32 * vc + 8 * lg;
-          bf16x8 ah, al;
-          load_split8(Rvn, (j < nval && v0 < V) ? ((uint32_t)j * rowV + v0) * 4u : kOOB, ah, al);
-          t = mma<true, true>(t, ah, al, pRh[vc], pRl[vc]);
-        }
-        // t = sum_v vn[j][v] P[i][v] at (j = 16J + 4lg + r, i = 16R + l16)
-        const int i = 16 * R + l16;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) t[r] = (i > 16 * J + 4 * lg + r) ? -t[r] : 0.f;
-        acc_to_bf16x4(t, darh[J], darl[J]);
-      }
-    }
-    // B operand rows j of block R (v_new), shared by every dac tile
-    bf16x8 vRh[VC], vRl[VC];
-#pragma unroll
-    for (int vc = 0; vc < VC; ++vc) {
-      const int j = 16 * R + l16, v0 = 32 * vc + 8 * lg;
-      load_split8(Rvn, (j < nval && v0 < V) ? ((uint32_t)j * rowV + v0) * 4u : kOOB, vRh[vc], vRl[vc]);
     }
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
-      if (I >= R) {
-        f32x4 t = {0.f, 0.f, 0.f, 0.f};
+      float x = dbv[I];
+      x += __shfl_xor(x, 16, 64);
+      x += __shfl_xor(x, 32, 64);
+      if (lg == 0) sDbv[wave * C + 16 * I + l16] = x;
+    }
+  }
+  __syncthreads();  // P plane visible
+
+  // ---------------- dAkk tiles (registers, all passes) for the token blocks t = 2tp + a
+  // dar[a][J] (J <= t): lane holds dAkk[16t + l16][16J + 4lg + r]          (A operand, rows i)
+  // dac[a][I] (I >= t): lane holds beta_i dAkk[16I + 4lg + r][16t + l16]   (A operand, rows j)
+  uint2 darh[2][4], darl[2][4], dach[2][4], dacl[2][4];
+  {
 #pragma unroll
-        for (int vc = 0; vc < VC; ++vc)
-          t = mma<true, true>(t, PP.hi8(16 * I + l16, 32 * vc + 8 * lg), PP.lo8(16 * I + l16, 32 * vc + 8 * lg),
-                              vRh[vc], vRl[vc]);
-        // t = sum_v P[i][v] vn[j][v] at (i = 16I + 4lg + r, j = 16R + l16)
-        const int j = 16 * R + l16;
+    for (int a = 0; a < 2; ++a) {
+      const int t = 2 * tp + a;
+      bf16x8 pth[VC], ptl[VC], vth[VC], vtl[VC];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = 16 * I + 4 * lg + r;
-          t[r] = i > j ? -sBeta[i] * t[r] : 0.f;
+      for (int vc = 0; vc < VC; ++vc) {
+        pth[vc] = PP.hi8(16 * t + l16, 32 * vc + 8 * lg);
+        ptl[vc] = PP.lo8(16 * t + l16, 32 * vc + 8 * lg);
+        const int j = 16 * t + l16, v0 = 32 * vc + 8 * lg;
+        load_split8(Rvn, (j < nval && v0 < V) ? ((uint32_t)j * rowV + v0) * 4u : kOOB, vth[vc], vtl[vc]);
+      }
+#pragma unroll
+      for (int J = 0; J < 4; ++J) {
+        darh[a][J] = darl[a][J] = dach[a][J] = dacl[a][J] = make_uint2(0u, 0u);
+        if (J <= t) {
+          f32x4 s = {0.f, 0.f, 0.f, 0.f};
+          const int j = 16 * J + l16;
+#pragma unroll
+          for (int vc = 0; vc < VC; ++vc) {
+            const int v0 = 32 * vc + 8 * lg;
+            bf16x8 ah, al;
+            if (J == t) { ah = vth[vc]; al = vtl[vc]; }
+            else load_split8(Rvn, (j < nval && v0 < V) ? ((uint32_t)j * rowV + v0) * 4u : kOOB, ah, al);
+            s = mma<true, true>(s, ah, al, pth[vc], ptl[vc]);
+          }
+          // s = sum_v vn[j][v] P[i][v] at (j = 16J + 4lg + r, i = 16t + l16)
+          const int i = 16 * t + l16;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s[r] = (i > 16 * J + 4 * lg + r) ? -s[r] : 0.f;
+          acc_to_bf16x4(s, darh[a][J], darl[a][J]);
         }
-        acc_to_bf16x4(t, dach[I], dacl[I]);
+        if (J >= t) {
+          f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int vc = 0; vc < VC; ++vc)
+            s = mma<true, true>(s, PP.hi8(16 * J + l16, 32 * vc + 8 * lg), PP.lo8(16 * J + l16, 32 * vc + 8 * lg),
+                                vth[vc], vtl[vc]);
+          // s = sum_v P[i][v] vn[j][v] at (i = 16J + 4lg + r, j = 16t + l16)
+          const int j = 16 * t + l16;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int i = 16 * J + 4 * lg + r;
+            s[r] = i > j ? -sBeta[i] * s[r] : 0.f;
+          }
+          acc_to_bf16x4(s, dach[a][J], dacl[a][J]);
+        }
       }
     }
   }
 
-  // ---------------- channel passes
+  // ---------------- channel passes: wave (kb, tp) -> channels cb + 16kb.., tokens of blocks 2tp, 2tp+1
   const rsrc_t Rdk = make_rsrc(p.dk_wy + e0 * K, remr * K * 4);
   const rsrc_t Rdg = make_rsrc(p.dg_wy + e0 * K, remr * K * 4);
   const int ch = tid & 31, sg = tid >> 5;
-  float dbk_acc[4] = {0.f, 0.f, 0.f, 0.f};   // per token 16R + 4lg + r: sum_d (2^G k dbk + k Y1)
+  float dbk_acc[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};   // per (a, r): sum over channels
 #pragma unroll 1
   for (int ps = 0; ps < NPS; ++ps) {
     const int cb = ps * KH;
+    const int kl = 16 * kb + l16;        // channel in the pass of this lane's result column
+    const int kk = cb + kl;
+    // this pass's S rows kk (B operand of dbk), issued before the staging
+    uint4 sraw[VC][2];
+#pragma unroll
+    for (int vc = 0; vc < VC; ++vc) {
+      const int v0 = 32 * vc + 8 * lg;
+      const uint32_t o = (kk < K && v0 < V) ? ((uint32_t)kk * V + v0) * 4u : kOOB;
+      sraw[vc][0] = bld128(Rh, o, 0);
+      sraw[vc][1] = bld128(Rh, o == kOOB ? kOOB : o + 16u, 0);
+    }
     // ---- staging: thread = (channel ch, rows 8sg..8sg+7)
     {
       const int kc = cb + ch;
@@ -227,8 +246,7 @@ __global__ __launch_bounds__(256, 2) void kda_wy_kernel(KdaWyParams p) {
         const float x = __uint_as_float(bld32(Rg, ok ? off * 4u : kOOB, 0));
         G[i] = x * kLog2e + (i > 0 ? G[i - 1] : 0.f);
       }
-      __syncthreads();  // the previous pass is done with every pass array
-      sTot[sg * KH + ch] = G[7];
+      sTot[sg * KH + ch] = G[7];          // sTot is last read before the previous pass's planes barrier
       __syncthreads();
       float pre = 0.f, gam = 0.f;
 #pragma unroll
@@ -252,42 +270,51 @@ __global__ __launch_bounds__(256, 2) void kda_wy_kernel(KdaWyParams p) {
     }
     __syncthreads();  // pass planes, sG, sGm visible
 
-    float dgr[2][4];
-    float dkr[2][4];
+    bf16x8 bh[VC], bl[VC];              // S rows kk, split once for both token blocks
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const int kl = 16 * kb + l16;        // channel in the pass of this lane's result column
-      const int kk = cb + kl;
+    for (int vc = 0; vc < VC; ++vc) {
+      float a[4], b[4];
+      unpack4(sraw[vc][0], a);
+      unpack4(sraw[vc][1], b);
+      uint32_t h4[4], l4[4];
+      split_bf16x2(a[0], a[1], h4[0], l4[0]);
+      split_bf16x2(a[2], a[3], h4[1], l4[1]);
+      split_bf16x2(b[0], b[1], h4[2], l4[2]);
+      split_bf16x2(b[2], b[3], h4[3], l4[3]);
+      bh[vc] = __builtin_bit_cast(bf16x8, make_uint4(h4[0], h4[1], h4[2], h4[3]));
+      bl[vc] = __builtin_bit_cast(bf16x8, make_uint4(l4[0], l4[1], l4[2], l4[3]));
+    }
+    const float gmv = sGm[kl];
+    float dgr[2][4], dkr[2][4];
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      const int t = 2 * tp + a;
       // dbk: -sum_v P[j][v] S[kk][v]
       f32x4 db = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int vc = 0; vc < VC; ++vc) {
-        const int v0 = 32 * vc + 8 * lg;
-        bf16x8 bh, bl;
-        load_split8(Rh, (kk < K && v0 < V) ? ((uint32_t)kk * V + v0) * 4u : kOOB, bh, bl);
-        db = mma<true, true>(db, PP.hi8(16 * R + l16, v0), PP.lo8(16 * R + l16, v0), bh, bl);
-      }
-      // Y1 (rows i of block R) and Y2 (rows j of block R), contraction over tokens
+      for (int vc = 0; vc < VC; ++vc)
+        db = mma<true, true>(db, PP.hi8(16 * t + l16, 32 * vc + 8 * lg), PP.lo8(16 * t + l16, 32 * vc + 8 * lg),
+                             bh[vc], bl[vc]);
+      // Y1 (rows i of block t) and Y2 (rows j of block t), contraction over tokens
       f32x4 y1 = {0.f, 0.f, 0.f, 0.f}, y2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int Pp = 0; Pp < 2; ++Pp) {
         const int P0 = 2 * Pp, P1 = 2 * Pp + 1;
-        if (P0 <= R)
-          y1 = mma<true, true>(y1, cat44(darh[P0], darh[P1]), cat44(darl[P0], darl[P1]),
+        if (P0 <= t)
+          y1 = mma<true, true>(y1, cat44(darh[a][P0], darh[a][P1]), cat44(darl[a][P0], darl[a][P1]),
                                PK2t.hi44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
                                PK2t.lo44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg));
-        if (P1 >= R)
-          y2 = mma<true, true>(y2, cat44(dach[P0], dach[P1]), cat44(dacl[P0], dacl[P1]),
+        if (P1 >= t)
+          y2 = mma<true, true>(y2, cat44(dach[a][P0], dach[a][P1]), cat44(dacl[a][P0], dacl[a][P1]),
                                PK1t.hi44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
                                PK1t.lo44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg));
       }
-      // epilogue: lane holds (token 16R + 4lg + r, channel kk)
-      const float gmv = sGm[kl];
+      // epilogue: lane holds (token 16t + 4lg + r, channel kk)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int t = 16 * R + 4 * lg + r;
-        const bool ok = kk < K && t < nval;
-        const uint32_t off = (uint32_t)t * rowK + kk;
+        const int tok = 16 * t + 4 * lg + r;
+        const bool ok = kk < K && tok < nval;
+        const uint32_t off = (uint32_t)tok * rowK + kk;
         float kv;
         if constexpr (ES == 4) {
           kv = __uint_as_float(bld32(Rk, ok ? off * 4u : kOOB, 0));
@@ -295,65 +322,74 @@ __global__ __launch_bounds__(256, 2) void kda_wy_kernel(KdaWyParams p) {
           const uint32_t wd = bld32(Rk, ok ? (off & ~1u) * 2u : kOOB, 0);
           kv = (off & 1u) ? __uint_as_float(wd & 0xffff0000u) : __uint_as_float(wd << 16);
         }
-        const float Gt = sG[t * LG + kl];
+        const float Gt = sG[tok * LG + kl];
         const float e = fast_exp2(Gt);
-        const float b = sBeta[t];
+        const float b = sBeta[tok];
         const float dbkv = -db[r];
         const float Y1 = y1[r] * fast_exp2(Gt - gmv);
         const float Y2 = y2[r] * fast_exp2(gmv - Gt);
-        dkr[kb][r] = b * e * dbkv + b * Y1 + Y2;
-        dgr[kb][r] = b * e * kv * dbkv + b * kv * Y1 - kv * Y2;
-        dbk_acc[r] += e * kv * dbkv + kv * Y1;
+        dkr[a][r] = b * e * dbkv + b * Y1 + Y2;
+        dgr[a][r] = b * e * kv * dbkv + b * kv * Y1 - kv * Y2;
+        dbk_acc[a][r] += e * kv * dbkv + kv * Y1;
       }
     }
-    // reverse in-chunk cumsum of dG: within the lane (r), over the 4 lane groups, then
-    // over the token blocks of later waves
+    // reverse in-chunk cumsum of dG over this wave's 32 tokens (in-lane, lane groups, block
+    // 2tp+1 into 2tp), then tokens 32..63 into the first token pair through LDS
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      dgr[kb][2] += dgr[kb][3];
-      dgr[kb][1] += dgr[kb][2];
-      dgr[kb][0] += dgr[kb][1];
-      const float tot = dgr[kb][0];
-      const float t1 = __shfl(tot, (lane & 15) + 16, 64);
-      const float t2 = __shfl(tot, (lane & 15) + 32, 64);
-      const float t3 = __shfl(tot, (lane & 15) + 48, 64);
+    for (int a = 0; a < 2; ++a) {
+      dgr[a][2] += dgr[a][3];
+      dgr[a][1] += dgr[a][2];
+      dgr[a][0] += dgr[a][1];
+      const float tot = dgr[a][0];
+      const float t1 = __shfl(tot, l16 + 16, 64);
+      const float t2 = __shfl(tot, l16 + 32, 64);
+      const float t3 = __shfl(tot, l16 + 48, 64);
       const float add = (lg < 1 ? t1 : 0.f) + (lg < 2 ? t2 : 0.f) + (lg < 3 ? t3 : 0.f);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) dgr[kb][r] += add;
-      if (lg == 0) sBlk[R * KH + 16 * kb + l16] = dgr[kb][0];   // block total
+      for (int r = 0; r < 4; ++r) dgr[a][r] += add;
     }
+    {
+      const float blk1 = __shfl(dgr[1][0], l16, 64);       // total of block 2tp + 1
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dgr[0][r] += blk1;
+    }
+    if (tp == 1 && lg == 0) sBlk[kb * 16 + l16] = dgr[0][0];   // total of tokens 32..63
     __syncthreads();  // block totals visible
+    const float add = tp == 0 ? sBlk[kb * 16 + l16] : 0.f;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const int kl = 16 * kb + l16, kk = cb + kl;
-      float add = 0.f;
-#pragma unroll
-      for (int R2 = 1; R2 < 4; ++R2)
-        if (R2 > R) add += sBlk[R2 * KH + kl];
+    for (int a = 0; a < 2; ++a) {
+      const int t = 2 * tp + a;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int t = 16 * R + 4 * lg + r;
-        const uint32_t off = (kk < K && t < nval) ? ((uint32_t)t * rowK + kk) * 4u : kOOB;
-        bst32(Rdg, __float_as_uint(dgr[kb][r] + add), off, 0);
-        bst32(Rdk, __float_as_uint(dkr[kb][r]), off, 0);
+        const int tok = 16 * t + 4 * lg + r;
+        const uint32_t off = (kk < K && tok < nval) ? ((uint32_t)tok * rowK + kk) * 4u : kOOB;
+        bst32(Rdg, __float_as_uint(dgr[a][r] + add), off, 0);
+        bst32(Rdk, __float_as_uint(dkr[a][r]), off, 0);
       }
     }
   }
 
-  // ---------------- dbeta: channel sums over the 16 lanes of a group, plus sum_v v P
+  // ---------------- dbeta: channel sums (16 lanes, two channel halves), plus sum_v v P
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) dbk_acc[r] += __shfl_xor(dbk_acc[r], o, 64);
-  }
-  if (l16 == 0) {
-    float* db = p.dbeta;
-    const rsrc_t Rdb = make_rsrc(db + e0, remr * 4);
+  for (int a = 0; a < 2; ++a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int t = 16 * R + 4 * lg + r;
-      bst32(Rdb, __float_as_uint(dbk_acc[r] + sDb[t]), t < nval ? (uint32_t)t * H * 4u : kOOB, 0);
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) dbk_acc[a][r] += __shfl_xor(dbk_acc[a][r], o, 64);
     }
+  }
+  if (l16 == 0) {
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sDbk[kb * C + 16 * (2 * tp + a) + 4 * lg + r] = dbk_acc[a][r];
+    }
+  }
+  __syncthreads();
+  if (tid < C) {
+    const float x = sDbk[tid] + sDbk[C + tid] + sDbv[tid] + sDbv[C + tid] + sDbv[2 * C + tid] + sDbv[3 * C + tid];
+    const rsrc_t Rdb = make_rsrc(p.dbeta + e0, remr * 4);
+    bst32(Rdb, __float_as_uint(x), tid < nval ? (uint32_t)tid * H * 4u : kOOB, 0);
   }
 }
 
