@@ -15,7 +15,9 @@
 // substitution, then the off-diagonal blocks follow level by level,
 // T[I][J] = -T[I][I] sum_{J <= k < I} Akk[I][k] T[k][J].
 // Outputs: u [B,T,H,V], w [B,T,H,K] (fp32, read by the state sweep) and, for the
-// backward, T transposed per chunk [total,H,C,C] (row i holds column i of T).
+// backward, T transposed per chunk [total,H,C,C] (row i holds column i of T).  The Akk and
+// u / w products run in passes of 64 channels (columns) so the workgroup needs < 80 KB of
+// LDS and two share a CU: one's serial triangular solve overlaps the other's products.
 #include "kda.h"
 #include "tops_common.h"
 #include "tops_hip.h"
@@ -28,17 +30,22 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(KdaPrepParams p) {
   constexpr int NQ = KP / 4, NSEG = 256 / NQ, RPT = C / NSEG;        // k / g staging
   constexpr int NQV = VP / 4, NSEGV = 256 / NQV, RPTV = C / NSEGV;   // v staging
   constexpr int ES = sizeof(TIn);
-  constexpr int LQ = KP + 8;   // row-major gated-k planes [C][LQ]
+  constexpr int KH2 = KP < 64 ? KP : 64;   // channels per Akk / w pass
+  constexpr int VH2 = VP < 64 ? VP : 64;   // columns per u pass
+  constexpr int NKP = KP / KH2, NVP = VP / VH2;
+  constexpr int NUW = NKP > NVP ? NKP : NVP;
+  constexpr int LQ = KH2 + 8;  // row-major gated-k planes [C][LQ]
   constexpr int LT = C + 8;    // transposed planes [channel][LT]
   constexpr int LA = C + 4;    // fp32 [C][LA]
   static_assert(RPT == 2 || RPT == 4 || RPT == 8, "KP must be 32, 64 or 128");
   static_assert(RPTV == 2 || RPTV == 4 || RPTV == 8, "VP must be 32, 64 or 128");
   typedef Words<TIn> Wd;
 
-  // Region R1: K1 | K2 (row-major, hi+lo) for the Akk product, then BKt | BVt
-  // (transposed beta 2^G k and beta v, hi+lo) for the u / w products.
+  // Region R1: K1 | K2 (row-major, hi+lo, one channel pass) for the Akk product, then
+  // BKt | BVt (transposed beta 2^G k and beta v, hi+lo, one pass) for the u / w products.
+  // Passes of 64 channels / columns keep the workgroup under 80 KB: two per CU.
   constexpr int R1A = 4 * C * LQ;
-  constexpr int R1B = 2 * KP * LT + 2 * VP * LT;
+  constexpr int R1B = 2 * KH2 * LT + 2 * VH2 * LT;
   constexpr int R1 = R1A > R1B ? R1A : R1B;
   __shared__ __attribute__((aligned(16))) uint16_t sR1[R1];
   __shared__ __attribute__((aligned(16))) float sA[C * LA];     // Akk (strictly lower)
@@ -49,8 +56,8 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(KdaPrepParams p) {
 
   const Plane PK1{sR1, sR1 + C * LQ, LQ};
   const Plane PK2{sR1 + 2 * C * LQ, sR1 + 3 * C * LQ, LQ};
-  const Plane PBK{sR1, sR1 + KP * LT, LT};
-  const Plane PBV{sR1 + 2 * KP * LT, sR1 + 2 * KP * LT + VP * LT, LT};
+  const Plane PBK{sR1, sR1 + KH2 * LT, LT};
+  const Plane PBV{sR1 + 2 * KH2 * LT, sR1 + 2 * KH2 * LT + VH2 * LT, LT};
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -130,57 +137,87 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(KdaPrepParams p) {
     for (int j = 0; j < 4; ++j) gm[j] = 0.5f * gam[j];
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
-      float x1[4], x2[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        G[i][j] += pre[j];
-        x1[j] = kv[i][j] * fast_exp2(G[i][j] - gm[j]);
-        x2[j] = kv[i][j] * fast_exp2(gm[j] - G[i][j]);
-      }
-      put_n<true, 4>(PK1, r0 + i, c0, x1);
-      put_n<true, 4>(PK2, r0 + i, c0, x2);
+      for (int j = 0; j < 4; ++j) G[i][j] += pre[j];
     }
   }
-  __syncthreads();  // K1 / K2, beta and the zeroed T visible
 
-  // ---------------- Akk: the 10 lower 16x16 tiles, dealt round-robin over the waves
-  for (int t = wave; t < 10; t += 4) {
-    const int I = t >= 6 ? 3 : (t >= 3 ? 2 : (t >= 1 ? 1 : 0));
-    const int J = t - I * (I + 1) / 2;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  // ---------------- Akk: the 10 lower 16x16 tiles, dealt round-robin over the waves,
+  // accumulated over channel passes of KH2
+  f32x4 akk[3];
 #pragma unroll
-    for (int kc = 0; kc < KP / 32; ++kc)
-      acc = mma<true, true>(acc, PK1.hi8(16 * I + l16, 32 * kc + 8 * lg), PK1.lo8(16 * I + l16, 32 * kc + 8 * lg),
-                            PK2.hi8(16 * J + l16, 32 * kc + 8 * lg), PK2.lo8(16 * J + l16, 32 * kc + 8 * lg));
-    const int j = 16 * J + l16;
+  for (int ti = 0; ti < 3; ++ti) akk[ti] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = 16 * I + 4 * lg + r;
-      sA[i * LA + j] = i > j ? sBeta[i] * acc[r] : 0.f;
+  for (int hp = 0; hp < NKP; ++hp) {
+    if (hp > 0) __syncthreads();  // the previous pass is done with K1 / K2
+    if (c0 >= hp * KH2 && c0 < (hp + 1) * KH2) {
+#pragma unroll
+      for (int i = 0; i < RPT; ++i) {
+        float x1[4], x2[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          x1[j] = kv[i][j] * fast_exp2(G[i][j] - gm[j]);
+          x2[j] = kv[i][j] * fast_exp2(gm[j] - G[i][j]);
+        }
+        put_n<true, 4>(PK1, r0 + i, c0 - hp * KH2, x1);
+        put_n<true, 4>(PK2, r0 + i, c0 - hp * KH2, x2);
+      }
+    }
+    __syncthreads();  // K1 / K2 of the pass (and, first time, beta and the zeroed T) visible
+#pragma unroll
+    for (int ti = 0; ti < 3; ++ti) {
+      const int t = wave + 4 * ti;
+      if (t < 10) {
+        const int I = t >= 6 ? 3 : (t >= 3 ? 2 : (t >= 1 ? 1 : 0));
+        const int J = t - I * (I + 1) / 2;
+#pragma unroll
+        for (int kc = 0; kc < KH2 / 32; ++kc)
+          akk[ti] = mma<true, true>(akk[ti], PK1.hi8(16 * I + l16, 32 * kc + 8 * lg), PK1.lo8(16 * I + l16, 32 * kc + 8 * lg),
+                                    PK2.hi8(16 * J + l16, 32 * kc + 8 * lg), PK2.lo8(16 * J + l16, 32 * kc + 8 * lg));
+      }
+    }
+  }
+#pragma unroll
+  for (int ti = 0; ti < 3; ++ti) {
+    const int t = wave + 4 * ti;
+    if (t < 10) {
+      const int I = t >= 6 ? 3 : (t >= 3 ? 2 : (t >= 1 ? 1 : 0));
+      const int J = t - I * (I + 1) / 2;
+      const int j = 16 * J + l16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * I + 4 * lg + r;
+        sA[i * LA + j] = i > j ? sBeta[i] * akk[ti][r] : 0.f;
+      }
     }
   }
   __syncthreads();  // Akk complete; K1 / K2 are dead
 
-  // ---------------- BKt = (beta 2^G k)^T, BVt = (beta v)^T into region R1
-  {
+  // ---------------- BKt = (beta 2^G k)^T, BVt = (beta v)^T of u / w pass up into region R1
+  auto write_bkbv = [&](int up) {
+    if (up < NKP && c0 >= up * KH2 && c0 < (up + 1) * KH2) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float x[RPT];
+      for (int j = 0; j < 4; ++j) {
+        float x[RPT];
 #pragma unroll
-      for (int i = 0; i < RPT; ++i) x[i] = sBeta[r0 + i] * fast_exp2(G[i][j]) * kv[i][j];
-      put_n<true, RPT>(PBK, c0 + j, r0, x);
+        for (int i = 0; i < RPT; ++i) x[i] = sBeta[r0 + i] * fast_exp2(G[i][j]) * kv[i][j];
+        put_n<true, RPT>(PBK, c0 - up * KH2 + j, r0, x);
+      }
     }
-    float vv[RPTV][4];
+    if (up < NVP && vc0 >= up * VH2 && vc0 < (up + 1) * VH2) {
+      float vv[RPTV][4];
 #pragma unroll
-    for (int i = 0; i < RPTV; ++i) unpack4(rv[i], vv[i]);
+      for (int i = 0; i < RPTV; ++i) unpack4(rv[i], vv[i]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float x[RPTV];
+      for (int j = 0; j < 4; ++j) {
+        float x[RPTV];
 #pragma unroll
-      for (int i = 0; i < RPTV; ++i) x[i] = sBeta[rv0 + i] * vv[i][j];
-      put_n<true, RPTV>(PBV, vc0 + j, rv0, x);
+        for (int i = 0; i < RPTV; ++i) x[i] = sBeta[rv0 + i] * vv[i][j];
+        put_n<true, RPTV>(PBV, vc0 - up * VH2 + j, rv0, x);
+      }
     }
-  }
+  };
+  write_bkbv(0);
 
   // ---------------- diagonal blocks of T: wave b inverts I + Akk[b][b] (lane = column)
   {
@@ -258,30 +295,42 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(KdaPrepParams p) {
     const rsrc_t Ru = make_rsrc(p.u + e0 * V, remr * V * 4);
     const rsrc_t Rw = make_rsrc(p.w + e0 * K, remr * K * 4);
 #pragma unroll
-    for (int vb = 0; vb < VP / 16; ++vb) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int up = 0; up < NUW; ++up) {
+      if (up > 0) {
+        __syncthreads();  // the previous pass is done with BKt / BVt
+        write_bkbv(up);
+        __syncthreads();
+      }
+      if (up < NVP) {
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc)
-        if (kc < nkc)
-          acc = mma<true, true>(acc, PBV.hi8(16 * vb + l16, 32 * kc + 8 * lg),
-                                PBV.lo8(16 * vb + l16, 32 * kc + 8 * lg), th[kc], tl[kc]);
-      const int col = 16 * vb + 4 * lg;
-      bst128(Ru, make_uint4(__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]),
-                            __float_as_uint(acc[3])),
-             (tok_ok && col < V) ? ((uint32_t)tok * rowV + col) * 4u : kOOB, 0);
-    }
+        for (int vb = 0; vb < VH2 / 16; ++vb) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kb = 0; kb < KP / 16; ++kb) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+          for (int kc = 0; kc < 2; ++kc)
+            if (kc < nkc)
+              acc = mma<true, true>(acc, PBV.hi8(16 * vb + l16, 32 * kc + 8 * lg),
+                                    PBV.lo8(16 * vb + l16, 32 * kc + 8 * lg), th[kc], tl[kc]);
+          const int col = up * VH2 + 16 * vb + 4 * lg;
+          bst128(Ru, make_uint4(__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]),
+                                __float_as_uint(acc[3])),
+                 (tok_ok && col < V) ? ((uint32_t)tok * rowV + col) * 4u : kOOB, 0);
+        }
+      }
+      if (up < NKP) {
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc)
-        if (kc < nkc)
-          acc = mma<true, true>(acc, PBK.hi8(16 * kb + l16, 32 * kc + 8 * lg),
-                                PBK.lo8(16 * kb + l16, 32 * kc + 8 * lg), th[kc], tl[kc]);
-      const int col = 16 * kb + 4 * lg;
-      bst128(Rw, make_uint4(__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]),
-                            __float_as_uint(acc[3])),
-             (tok_ok && col < K) ? ((uint32_t)tok * rowK + col) * 4u : kOOB, 0);
+        for (int kb = 0; kb < KH2 / 16; ++kb) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kc = 0; kc < 2; ++kc)
+            if (kc < nkc)
+              acc = mma<true, true>(acc, PBK.hi8(16 * kb + l16, 32 * kc + 8 * lg),
+                                    PBK.lo8(16 * kb + l16, 32 * kc + 8 * lg), th[kc], tl[kc]);
+          const int col = up * KH2 + 16 * kb + 4 * lg;
+          bst128(Rw, make_uint4(__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]),
+                                __float_as_uint(acc[3])),
+                 (tok_ok && col < K) ? ((uint32_t)tok * rowK + col) * 4u : kOOB, 0);
+        }
+      }
     }
   }
 
