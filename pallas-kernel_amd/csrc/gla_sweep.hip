@@ -54,7 +54,12 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   constexpr int NQ = KP / 4;             // column quads of a [C][KP] tile
   constexpr int NSEG = NTH / NQ;         // row segments
   constexpr int RPT = C / NSEG;          // rows per thread (4, 2, 1)
-  constexpr int GPW = 64 / NQ;           // row segments per wave (2, 4, 8)
+  // staging thread mapping: a 32-lane half-wave covers CQL column quads x SGL row segments,
+  // which keeps the row-major and the transposed plane writes (nearly) free of bank conflicts
+  constexpr int CQL = 8, SGL = 32 / CQL;  // 8 column quads x 4 row segments per half-wave
+  constexpr int NCQH = NQ / CQL;         // half-waves across the columns
+  constexpr int NSGH = NSEG / SGL;       // segment groups (half-waves down the rows)
+  static_assert(NQ % CQL == 0, "KP must be a multiple of 32");
   constexpr bool SIN = !In<TIn>::kExactBf16;
   constexpr bool FWD_DELTA = DELTA && !REV;
   constexpr bool REV_DELTA = DELTA && REV;
@@ -74,7 +79,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   // (the reverse delta rule reuses sHT for the [BV][LT] dv_new^T plane: size for both)
   constexpr int NHTS = 2 * BV * (REV_DELTA && LT > LH ? LT : LH);
   __shared__ __attribute__((aligned(16))) uint16_t sHT[NHTS];
-  __shared__ __attribute__((aligned(16))) float sTot[NW * KP];   // per-wave gate totals
+  __shared__ __attribute__((aligned(16))) float sTot[NSGH * KP]; // gate totals per segment group
   // Gamma / 2 of channel c sits in the padding columns of the X hi plane (row c / 4, word c % 4):
   // no MFMA fragment or staging write touches columns >= KP
   auto gm_at = [&](int c4) { return (float*)(sX + (c4 >> 2) * LQ + KP); };
@@ -134,11 +139,14 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   const long long rows_total = (long long)p.B * p.T;   // rows of the [B*T, H, .] tensors
 
   // ---- staging coordinates and per-thread byte offsets within a chunk
-  const int cq = tid % NQ, seg = tid / NQ;
+  const int hw = tid >> 5;               // half-wave
+  const int sgl = (lane & 31) / CQL;     // row segment within the half-wave
+  const int sgh = hw / NCQH;             // segment group
+  const int cq = (lane & 31) % CQL + CQL * (hw % NCQH), seg = sgl + SGL * sgh;
   const int c0 = 4 * cq, r0 = seg * RPT;
-  const int sw = lane / NQ;              // row segment within the wave
   const bool colok = c0 < K;
-  const int yc = tid & 31, yseg = tid >> 5;     // Y: 2 columns x 4 rows per thread
+  // Y: 2 columns x 4 rows per thread; a half-wave covers 8 column pairs x 4 row groups
+  const int yc = (lane & 7) + 8 * (hw & 3), yseg = ((lane >> 3) & 3) + 4 * (hw >> 2);
   const int yv = vt * BV + 2 * yc;
   const bool ycolok = yv < V;
   const uint32_t rowK = (uint32_t)(H * K), rowV = (uint32_t)(H * V);
@@ -260,8 +268,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       }
     }
 
-    // ---------------- gate cumsum: thread rows, a shuffle scan over the wave's row
-    // segments, then per-wave totals through LDS
+    // ---------------- gate cumsum: thread rows, a shuffle scan over the half-wave's row
+    // segments, then segment-group totals through LDS
     float G[RPT][4];
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
@@ -280,22 +288,22 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       const float t = G[RPT - 1][j];
       float x = t;
 #pragma unroll
-      for (int d = NQ; d < 64; d <<= 1) {
+      for (int d = CQL; d < 32; d <<= 1) {
         const float y = __shfl_up(x, d, 64);
-        if (lane >= d) x += y;
+        if ((lane & 31) >= d) x += y;
       }
-      pre[j] = x - t;                    // segments before this one, within the wave
-      gam[j] = x;                        // inclusive; the last segment holds the wave total
+      pre[j] = x - t;                    // segments before this one, within the half-wave
+      gam[j] = x;                        // inclusive; the last segment holds the group total
     }
-    if (sw == GPW - 1) *(float4*)(sTot + wave * KP + c0) = make_float4(gam[0], gam[1], gam[2], gam[3]);
+    if (sgl == SGL - 1) *(float4*)(sTot + sgh * KP + c0) = make_float4(gam[0], gam[1], gam[2], gam[3]);
     __syncthreads();  // B1: totals visible; every wave is done with the previous chunk's planes
 
 #pragma unroll
     for (int j = 0; j < 4; ++j) gam[j] = 0.f;
 #pragma unroll
-    for (int w2 = 0; w2 < NW; ++w2) {
-      const float4 t = *(const float4*)(sTot + w2 * KP + c0);
-      if (w2 < wave) { pre[0] += t.x; pre[1] += t.y; pre[2] += t.z; pre[3] += t.w; }
+    for (int s2 = 0; s2 < NSGH; ++s2) {
+      const float4 t = *(const float4*)(sTot + s2 * KP + c0);
+      if (s2 < sgh) { pre[0] += t.x; pre[1] += t.y; pre[2] += t.z; pre[3] += t.w; }
       gam[0] += t.x; gam[1] += t.y; gam[2] += t.z; gam[3] += t.w;
     }
     float gm[4];
@@ -305,8 +313,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     // Gamma of this lane's state rows kr = 16 msb + 4 lg + r
     float sgam[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int w2 = 0; w2 < NW; ++w2) {
-      const float4 t = *(const float4*)(sTot + w2 * KP + 16 * msb + 4 * lg);
+    for (int s2 = 0; s2 < NSGH; ++s2) {
+      const float4 t = *(const float4*)(sTot + s2 * KP + 16 * msb + 4 * lg);
       sgam[0] += t.x; sgam[1] += t.y; sgam[2] += t.z; sgam[3] += t.w;
     }
     float sga[4], sal[4], sbe[4];        // 2^Gamma, alpha (H^T scaling), beta (update scaling)
