@@ -253,7 +253,8 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
       const float x = gmode == kGateGamma ? ((cb + ch < K && 8 * sg + i < nval) ? gam_h : 0.f) : rg[i];
       G[i] = x * kLog2e + (i > 0 ? G[i - 1] : 0.f);
     }
-    __syncthreads();  // the previous pass is done with every LDS array
+    // (no barrier before this write: sTot is last read before the previous pass's planes
+    // barrier, and everything read after its final barrier is rewritten only after the next one)
     sTot[sg * KH + ch] = G[7];
     __syncthreads();
     float pre = 0.f, gam = 0.f;

@@ -91,12 +91,17 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(KdaPrepParams p) {
   const rsrc_t Rb = make_rsrc(p.beta + e0, remr * 4);
 
   // ---------------- loads: k / g rows r0.. (4 channels), v rows rv0.. (4 columns), beta
-  const int cq = tid % NQ, seg = tid / NQ;
+  // a 32-lane half-wave covers 8 channel quads x 4 row segments: the row-major K1 / K2 writes
+  // and the transposed BKt writes then (nearly) avoid LDS bank conflicts
+  constexpr int CQL = NQ < 8 ? NQ : 8, SGL = 32 / CQL, NCQH = NQ / CQL;
+  const int hw = tid >> 5;
+  const int cq = (lane & 31) % CQL + CQL * (hw % NCQH), seg = (lane & 31) / CQL + SGL * (hw / NCQH);
   const int c0 = 4 * cq, r0 = seg * RPT;
   const bool colok = c0 < K;
   const uint32_t offK = colok ? ((uint32_t)r0 * rowK + c0) * ES : kOOB;
   const uint32_t offG = colok ? ((uint32_t)r0 * rowK + c0) * 4u : kOOB;
-  const int cv = tid % NQV, sv = tid / NQV;
+  constexpr int CQLV = NQV < 8 ? NQV : 8, SGLV = 32 / CQLV, NCQHV = NQV / CQLV;
+  const int cv = (lane & 31) % CQLV + CQLV * (hw % NCQHV), sv = (lane & 31) / CQLV + SGLV * (hw / NCQHV);
   const int vc0 = 4 * cv, rv0 = sv * RPTV;
   const uint32_t offV = vc0 < V ? ((uint32_t)rv0 * rowV + vc0) * ES : kOOB;
   typename Wd::W4 rk[RPT], rv[RPTV];
