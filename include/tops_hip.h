@@ -133,6 +133,51 @@ int tops_simple_gla_chunk_bwd(const void* q, const void* k, const void* v, const
                               int total_chunks, int B, int T, int H, int K, int V, int N,
                               int dtype, float scale, void* stream);
 
+/* The two stages of tops_simple_gla_chunk_bwd, callable separately (arguments as there):
+ * the reverse sweep writing dh_work, dv and dh0 (chunk_bwd_dh, tops/ops/common/chunk_h.py:
+ * 790-878, as called at tops/ops/simple_gla/chunk.py:653) and the chunk-parallel
+ * dq / dk / dg stage (K11, tops/ops/common/chunk_o.py:277-366). */
+int tops_simple_gla_chunk_bwd_dh(const void* q, const void* k, const float* g,
+                                 const float* g_gamma, const void* do_, const float* dht,
+                                 float* dh_work, void* dv, float* dh0, const int32_t* cu_seqlens,
+                                 const int32_t* chunk_offsets, int B, int T, int H, int K, int V,
+                                 int N, int dtype, float scale, void* stream);
+int tops_simple_gla_chunk_bwd_dqkg(const void* q, const void* k, const void* v, const float* g,
+                                   const float* g_gamma, const void* do_, const float* h_ckpt,
+                                   const float* dh_work, void* dq, void* dk, float* dg,
+                                   const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                                   const int32_t* chunk_map, int total_chunks, int B, int T,
+                                   int H, int K, int V, int N, int dtype, float scale,
+                                   void* stream);
+
+/* Sequence-parallel sweeps (long or few sequences on one device).  The caller cuts each
+ * sequence at chunk boundaries into segments, listed in token order as a varlen layout over
+ * the same tokens (cu_seqlens of the segments, B == 1), and runs:
+ *   1. tops_chunk_state_pass over a list of N segments, segment i = rows
+ *      [seg_start[i], seg_end[i]): its end state from a zero state, s_loc [N,H,K,V] fp32,
+ *      and its summed log2 gates, dec [N,H,K] fp32.  reverse != 0: the state-gradient
+ *      sweep, z = q, y = dO; else z = k, y = v.  Only the segments that pass a state on
+ *      are needed: all but the last of a sequence (forward) or all but the first (reverse).
+ *   2. tops_chunk_state_combine: real sequence n owns the segments
+ *      [seg_first[n], seg_first[n+1]) and the state-pass entries
+ *      [st_first[n], st_first[n+1]) (one fewer, same token order).  Writes every segment's
+ *      incoming state init [Nseg,H,K,V] from s_in (h0, or dht when reverse, of the real
+ *      sequences, [Nreal,H,K,V], or NULL for zero).
+ *   3. the usual chunk sweep over the segments with h0 (dht) = init and chunk_offsets = each
+ *      segment's first global chunk; its final states per segment give ht (last segment of
+ *      each sequence) and dh0 (first segment).
+ * No counterpart in the reference, whose K7/K8 state kernels sweep every sequence serially
+ * (tops/ops/common/chunk_h.py:160-238, 685-878); results equal those of tops_gla_chunk_fwd
+ * and tops_gla_chunk_bwd_dh up to fp32 rounding.  gate_mode: 0 = per-channel g [B,T,H,K],
+ * 1 = per-token g [B,T,H], 2 = g_gamma [H].  T = rows of the token-major tensors. */
+int tops_chunk_state_pass(const void* z, const void* y, const float* g, int gate_mode,
+                          float* s_loc, float* dec, const int32_t* seg_start,
+                          const int32_t* seg_end, int T, int H, int K, int V, int N, int dtype,
+                          float scale, int reverse, void* stream);
+int tops_chunk_state_combine(const float* s_loc, const float* dec, const float* s_in,
+                             float* init, const int32_t* seg_first, const int32_t* st_first,
+                             int Nreal, int H, int K, int V, int reverse, void* stream);
+
 /* Fused recurrent GLA forward: the per-token recurrence
  *   h_t = h_{t-1} * exp(gk_t)[:,None] * exp(gv_t)[None,:] + k_t v_t^T,  o_t = h_t^T (scale q_t)
  * over each sequence (reverse != 0: from its last token to its first).  Replaces

@@ -148,3 +148,32 @@ extern "C" int tops_simple_gla_chunk_bwd(const void* q, const void* k, const voi
                        chunk_offsets, chunk_map, total_chunks, B, T, H, K, V, N, dtype, scale, mode,
                        stream);
 }
+
+extern "C" int tops_simple_gla_chunk_bwd_dh(const void* q, const void* k, const float* g,
+                                            const float* g_gamma, const void* do_,
+                                            const float* dht, float* dh_work, void* dv,
+                                            float* dh0, const int32_t* cu_seqlens,
+                                            const int32_t* chunk_offsets, int B, int T, int H,
+                                            int K, int V, int N, int dtype, float scale,
+                                            void* stream) {
+  if ((g == nullptr) == (g_gamma == nullptr))
+    return tops_set_error(TOPS_ERR_NULL, "simple_gla_chunk_bwd_dh: pass exactly one of g, g_gamma");
+  return bwd_dh_impl(q, k, g ? g : g_gamma, do_, dht, dh_work, dv, dh0, cu_seqlens, chunk_offsets,
+                     B, T, H, K, V, N, dtype, scale, g ? kGateS : kGateGamma, stream);
+}
+
+extern "C" int tops_simple_gla_chunk_bwd_dqkg(const void* q, const void* k, const void* v,
+                                              const float* g, const float* g_gamma,
+                                              const void* do_, const float* h_ckpt,
+                                              const float* dh_work, void* dq, void* dk, float* dg,
+                                              const int32_t* cu_seqlens,
+                                              const int32_t* chunk_offsets,
+                                              const int32_t* chunk_map, int total_chunks, int B,
+                                              int T, int H, int K, int V, int N, int dtype,
+                                              float scale, void* stream) {
+  if ((g == nullptr) == (g_gamma == nullptr))
+    return tops_set_error(TOPS_ERR_NULL, "simple_gla_chunk_bwd_dqkg: pass exactly one of g, g_gamma");
+  return bwd_dqkg_impl(q, k, v, g ? g : g_gamma, do_, h_ckpt, dh_work, dq, dk, g ? dg : nullptr,
+                       cu_seqlens, chunk_offsets, chunk_map, total_chunks, B, T, H, K, V, N, dtype,
+                       scale, g ? kGateS : kGateGamma, stream);
+}

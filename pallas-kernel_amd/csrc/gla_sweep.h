@@ -29,12 +29,21 @@ struct SweepParams {
   const float* w;        // w = T (beta 2^G k) [B,T,H,K]
   float* y32;            // forward: v_new [B,T,H,V] or NULL; reverse: dv_new per chunk,
                          // transposed, [total,H,V,C]
+  // state-only pass (sequence-parallel segments):
+  float* dec_fin;        // [N,H,K] sum of the log2 gates over the sequence, or NULL
+  const int* seg_end;    // [N] end row of sequence n (its start is cu_seqlens[n]), or NULL:
+                         // sequence n then ends where n + 1 starts
 };
 
 // TIn = uint16_t (bf16 bits) or float; REV = reverse (state-gradient) sweep;
 // DELTA = the KDA delta-rule sweep (v_new = u - w S replaces v).
 template <typename TIn, bool REV, bool DELTA = false>
 hipError_t launch_gla_sweep(const SweepParams& p, hipStream_t s);
+
+// State-only sweep: the end state s_fin of every sequence (from s0, usually zero) and the
+// decay sums dec_fin; no output, no checkpoints.
+template <typename TIn, bool REV>
+hipError_t launch_gla_state_pass(const SweepParams& p, hipStream_t s);
 
 struct DqkgParams {
   const void* q;

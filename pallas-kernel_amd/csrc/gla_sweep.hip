@@ -46,7 +46,7 @@
 namespace tops {
 
 
-template <typename TIn, int KP, bool REV, bool DELTA>
+template <typename TIn, int KP, bool REV, bool DELTA, bool ST>
 __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   constexpr int NW = 8;                  // wave64s per workgroup
   constexpr int NTH = 64 * NW;
@@ -104,15 +104,18 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   const int vt = wg % p.NV;
   const int hh = (wg / p.NV) % p.H;
   int n = wg / (p.NV * p.H);
+  // sequence j covers rows [cu_seqlens[j], end of j): the next start, or seg_end[j] when the
+  // sequences are a list of disjoint segments
+  auto seq_end = [&](int j) { return p.seg_end ? p.seg_end[j] : p.cu_seqlens[j + 1]; };
   if (p.cu_seqlens && p.N > 1 && p.N <= 256) {
     // Varlen: dispatch sequences longest first (LPT), so the workgroups that share a CU
     // balance; slot r takes the sequence of rank r in descending length (ties by index).
     const int slot = n;
     if (tid < p.N) {
-      const int li = p.cu_seqlens[tid + 1] - p.cu_seqlens[tid];
+      const int li = seq_end(tid) - p.cu_seqlens[tid];
       int rank = 0;
       for (int j = 0; j < p.N; ++j) {
-        const int lj = p.cu_seqlens[j + 1] - p.cu_seqlens[j];
+        const int lj = seq_end(j) - p.cu_seqlens[j];
         rank += (lj > li) || (lj == li && j < tid);
       }
       if (rank == slot) *(int*)sTot = tid;
@@ -128,7 +131,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   int L, row0, cbase;
   if (p.cu_seqlens) {
     row0 = p.cu_seqlens[n];
-    L = p.cu_seqlens[n + 1] - row0;
+    L = seq_end(n) - row0;
     cbase = p.chunk_offsets ? p.chunk_offsets[n] : 0;
   } else {
     row0 = n * p.T;
@@ -213,6 +216,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   };
 
   auto cidx = [&](int it) { return REV ? NTs - 1 - it : it; };
+  float dsum[4] = {0.f, 0.f, 0.f, 0.f};   // state-only pass: sum of Gamma of this lane's rows
   load_chunk(cidx(0), rsA);
   if constexpr (PF == 2) {
     if (NTs > 1) load_chunk(cidx(1), rsB);
@@ -309,7 +313,9 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     float gm[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) gm[j] = 0.5f * gam[j];
-    if (seg == 0) *(float4*)gm_at(c0) = make_float4(gm[0], gm[1], gm[2], gm[3]);
+    if constexpr (FWD_DELTA) {
+      if (seg == 0) *(float4*)gm_at(c0) = make_float4(gm[0], gm[1], gm[2], gm[3]);
+    }
     // Gamma of this lane's state rows kr = 16 msb + 4 lg + r
     float sgam[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -327,22 +333,27 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     }
 
     // ---------------- state -> H^T plane (alpha S); checkpoint of S
-    const rsrc_t Rck = make_rsrc(p.ckpt ? p.ckpt + ((size_t)(cbase + c) * H + hh) * K * V : nullptr,
-                                 p.ckpt ? (long long)K * V * 4 : 0);
+    if constexpr (ST) {
 #pragma unroll
-    for (int i = 0; i < NHT; ++i) {
-      const int nn = (wave * NHT + i) % (BV / 16);
-      const int kr = 16 * msb + 4 * lg;
-      float x[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) x[r] = sal[r] * S[i][r];
-      put_n<true, 4>(PHt, 16 * nn + l16, kr, x);
-      if (p.ckpt) {
-        const int vv = vt * BV + 16 * nn + l16;
-        const uint32_t vo = (vv < V) ? ((uint32_t)kr * V + vv) * 4u : kOOB;
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          bst32(Rck, __float_as_uint(S[i][r]), (kr + r < K) ? vo : kOOB, (uint32_t)(r * V * 4));
+      for (int r = 0; r < 4; ++r) dsum[r] += sgam[r];
+    } else {
+      const rsrc_t Rck = make_rsrc(p.ckpt ? p.ckpt + ((size_t)(cbase + c) * H + hh) * K * V : nullptr,
+                                   p.ckpt ? (long long)K * V * 4 : 0);
+  #pragma unroll
+      for (int i = 0; i < NHT; ++i) {
+        const int nn = (wave * NHT + i) % (BV / 16);
+        const int kr = 16 * msb + 4 * lg;
+        float x[4];
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) x[r] = sal[r] * S[i][r];
+        put_n<true, 4>(PHt, 16 * nn + l16, kr, x);
+        if (p.ckpt) {
+          const int vv = vt * BV + 16 * nn + l16;
+          const uint32_t vo = (vv < V) ? ((uint32_t)kr * V + vv) * 4u : kOOB;
+  #pragma unroll
+          for (int r = 0; r < 4; ++r)
+            bst32(Rck, __float_as_uint(S[i][r]), (kr + r < K) ? vo : kOOB, (uint32_t)(r * V * 4));
+        }
       }
     }
 
@@ -362,8 +373,10 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
         }
         const float* xx = REV ? xk : xq;
         const float* zz = REV ? xq : xk;
-        put_n<true, 4>(PX, r0 + i, c0, xx);
-        put_n<true, 4>(PZ, r0 + i, c0, zz);
+        if constexpr (!ST) {
+          put_n<true, 4>(PX, r0 + i, c0, xx);
+          put_n<true, 4>(PZ, r0 + i, c0, zz);
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) zt[j][i] = zz[j];
       }
@@ -401,6 +414,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     }
 
     // ---------------- output block: token block R, column tiles 2 nh, 2 nh + 1
+    if constexpr (!ST) {
     bf16x8 xh[KP / 32], xl[KP / 32];
 #pragma unroll
     for (int kc = 0; kc < KP / 32; ++kc) {
@@ -561,6 +575,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       }
     }
 
+    }  // !ST
+
     // ---------------- state update: S = 2^Gamma S + beta (Z~^T Y) [- w^T dv_new]
 #pragma unroll
     for (int i = 0; i < NHT; ++i) {
@@ -598,6 +614,16 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     for (int it = 0; it < NTs; ++it) body(it, rsA);
   }
 
+  if constexpr (ST) {
+    // one lane per K row (first wave of each K block, first column group, V tile 0)
+    if (p.dec_fin && vt == 0 && ((wave * NHT) % (BV / 16)) == 0 && l16 == 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kr = 16 * msb + 4 * lg + r;
+        if (kr < K) p.dec_fin[(size_t)(n * H + hh) * K + kr] = dsum[r];
+      }
+    }
+  }
   if (p.s_fin) {
 #pragma unroll
     for (int i = 0; i < NHT; ++i) {
@@ -616,11 +642,26 @@ template <typename TIn, bool REV, bool DELTA>
 hipError_t launch_gla_sweep(const SweepParams& p, hipStream_t s) {
   const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
   dim3 grid(p.NV * p.H * p.N);
-  if (kp == 32) hipLaunchKernelGGL((gla_sweep_kernel<TIn, 32, REV, DELTA>), grid, dim3(512), 0, s, p);
-  else if (kp == 64) hipLaunchKernelGGL((gla_sweep_kernel<TIn, 64, REV, DELTA>), grid, dim3(512), 0, s, p);
-  else hipLaunchKernelGGL((gla_sweep_kernel<TIn, 128, REV, DELTA>), grid, dim3(512), 0, s, p);
+  if (kp == 32) hipLaunchKernelGGL((gla_sweep_kernel<TIn, 32, REV, DELTA, false>), grid, dim3(512), 0, s, p);
+  else if (kp == 64) hipLaunchKernelGGL((gla_sweep_kernel<TIn, 64, REV, DELTA, false>), grid, dim3(512), 0, s, p);
+  else hipLaunchKernelGGL((gla_sweep_kernel<TIn, 128, REV, DELTA, false>), grid, dim3(512), 0, s, p);
   return hipGetLastError();
 }
+
+template <typename TIn, bool REV>
+hipError_t launch_gla_state_pass(const SweepParams& p, hipStream_t s) {
+  const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
+  dim3 grid(p.NV * p.H * p.N);
+  if (kp == 32) hipLaunchKernelGGL((gla_sweep_kernel<TIn, 32, REV, false, true>), grid, dim3(512), 0, s, p);
+  else if (kp == 64) hipLaunchKernelGGL((gla_sweep_kernel<TIn, 64, REV, false, true>), grid, dim3(512), 0, s, p);
+  else hipLaunchKernelGGL((gla_sweep_kernel<TIn, 128, REV, false, true>), grid, dim3(512), 0, s, p);
+  return hipGetLastError();
+}
+
+template hipError_t launch_gla_state_pass<uint16_t, false>(const SweepParams&, hipStream_t);
+template hipError_t launch_gla_state_pass<uint16_t, true>(const SweepParams&, hipStream_t);
+template hipError_t launch_gla_state_pass<float, false>(const SweepParams&, hipStream_t);
+template hipError_t launch_gla_state_pass<float, true>(const SweepParams&, hipStream_t);
 
 template hipError_t launch_gla_sweep<uint16_t, false, false>(const SweepParams&, hipStream_t);
 template hipError_t launch_gla_sweep<uint16_t, true, false>(const SweepParams&, hipStream_t);

@@ -29,24 +29,67 @@ def check_qkv(q, k, v, initial_state, cu_seqlens):
     N.require_cuda(q, k, v, initial_state)
 
 
+_GATE_CODE = {GATE_K: 0, GATE_S: 1, GATE_GAMMA: 2}
+
+
+def _gate_ptrs(gate):
+    """(g, g_gamma) pointer pair of the simple-GLA entry points."""
+    mode, gt = gate
+    return (N.ptr(gt) if mode == GATE_S else None, N.ptr(gt) if mode == GATE_GAMMA else None)
+
+
+def _segment_states(z, y, gate, s_in, scale, sp, reverse: bool):
+    """Incoming state of every segment of a sequence-parallel sweep: the state pass over the
+    segments that hand a state on, then the scan over each sequence's segments."""
+    B, T, H, K = z.shape
+    V = y.shape[-1]
+    mode, gt = gate
+    dev = z.device
+    s_loc = dec = None
+    if sp.n_state:
+        s_loc = torch.empty(sp.n_state, H, K, V, device=dev, dtype=torch.float32)
+        dec = torch.empty(sp.n_state, H, K, device=dev, dtype=torch.float32)
+        start, end = (sp.rev_start_dev, sp.rev_end_dev) if reverse else \
+            (sp.fwd_start_dev, sp.fwd_end_dev)
+        N.call("tops_chunk_state_pass", N.ptr(z), N.ptr(y), N.ptr(gt), _GATE_CODE[mode],
+               N.ptr(s_loc), N.ptr(dec), N.ptr(start), N.ptr(end), B * T, H, K, V, sp.n_state,
+               N.dtype_code(z.dtype), float(scale), int(reverse), N.stream())
+    init = torch.empty(sp.Nv, H, K, V, device=dev, dtype=torch.float32)
+    N.call("tops_chunk_state_combine", N.ptr(s_loc), N.ptr(dec), N.ptr(s_in), N.ptr(init),
+           N.ptr(sp.seg_first_dev), N.ptr(sp.st_first_dev), len(sp.seg_first) - 1, H, K, V,
+           int(reverse), N.stream())
+    return init
+
+
 def chunk_fwd(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, keep_states: bool):
-    """Run the forward chunk sweep.  gate = (mode, fp32 tensor).  Returns (o, ht, h_ckpt)."""
+    """Run the forward chunk sweep.  gate = (mode, fp32 tensor).  Returns (o, ht, h_ckpt).
+    Long or few sequences sweep as concurrent segments (plan.segments)."""
     B, T, H, K = q.shape
     V = v.shape[-1]
     mode, gt = gate
     o = torch.empty_like(v)
-    ht = torch.empty(plan.N, H, K, V, device=q.device, dtype=torch.float32) \
-        if output_final_state else None
     hs = torch.empty(plan.total, H, K, V, device=q.device, dtype=torch.float32) \
         if keep_states else None
-    tail = (N.ptr(h0), N.ptr(o), N.ptr(ht), N.ptr(hs), N.ptr(plan.cu_dev), N.ptr(plan.offsets_dev),
-            B, T, H, K, V, plan.N, N.dtype_code(q.dtype), float(scale), N.stream())
+    sp = plan.segments(H, V)
+    if sp is None:
+        ht = torch.empty(plan.N, H, K, V, device=q.device, dtype=torch.float32) \
+            if output_final_state else None
+        s0, fin, cu, offs, Bx, Tx, Nx = h0, ht, plan.cu_dev, plan.offsets_dev, B, T, plan.N
+    else:
+        s0 = _segment_states(k, v, gate, h0, scale, sp, reverse=False)
+        fin = torch.empty(sp.Nv, H, K, V, device=q.device, dtype=torch.float32) \
+            if output_final_state else None
+        cu, offs, Bx, Tx, Nx = sp.cu_dev, sp.offsets_dev, 1, B * T, sp.Nv
+    tail = (N.ptr(s0), N.ptr(o), N.ptr(fin), N.ptr(hs), N.ptr(cu), N.ptr(offs),
+            Bx, Tx, H, K, V, Nx, N.dtype_code(q.dtype), float(scale), N.stream())
     if mode == GATE_K:
         N.call("tops_gla_chunk_fwd", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gt), *tail)
     else:
-        N.call("tops_simple_gla_chunk_fwd", N.ptr(q), N.ptr(k), N.ptr(v),
-               N.ptr(gt) if mode == GATE_S else None, N.ptr(gt) if mode == GATE_GAMMA else None,
+        N.call("tops_simple_gla_chunk_fwd", N.ptr(q), N.ptr(k), N.ptr(v), *_gate_ptrs(gate),
                *tail)
+    ht = fin
+    if sp is not None and fin is not None:
+        ht = fin.index_select(0, sp.last_dev)
     return o, ht, hs
 
 
@@ -67,21 +110,31 @@ def chunk_bwd(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool
         dg = torch.empty(B, T, H, K, device=q.device, dtype=torch.float32)
     elif mode == GATE_S:
         dg = torch.empty(B, T, H, device=q.device, dtype=torch.float32)
-    dh0 = torch.empty(plan.N, H, K, V, device=q.device, dtype=torch.float32) if want_dh0 else None
     dh_work = torch.empty_like(hs)
     dt, st = N.dtype_code(q.dtype), N.stream()
-    if mode == GATE_K:
-        N.call("tops_gla_chunk_bwd_dh", N.ptr(q), N.ptr(k), N.ptr(gt), N.ptr(do), N.ptr(dht),
-               N.ptr(dh_work), N.ptr(dv), N.ptr(dh0), N.ptr(plan.cu_dev), N.ptr(plan.offsets_dev),
-               B, T, H, K, V, plan.N, dt, float(scale), st)
-        N.call("tops_gla_chunk_bwd_dqkg", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gt), N.ptr(do),
-               N.ptr(hs), N.ptr(dh_work), N.ptr(dq), N.ptr(dk), N.ptr(dg),
-               N.ptr(plan.cu_dev), N.ptr(plan.offsets_dev), N.ptr(plan.chunk_map_dev), plan.total,
-               B, T, H, K, V, plan.N, dt, float(scale), st)
+    sp = plan.segments(H, V)
+    if sp is None:
+        dh0 = torch.empty(plan.N, H, K, V, device=q.device, dtype=torch.float32) \
+            if want_dh0 else None
+        s0, fin, cu, offs, Bx, Tx, Nx = dht, dh0, plan.cu_dev, plan.offsets_dev, B, T, plan.N
     else:
-        N.call("tops_simple_gla_chunk_bwd", N.ptr(q), N.ptr(k), N.ptr(v),
-               N.ptr(gt) if mode == GATE_S else None, N.ptr(gt) if mode == GATE_GAMMA else None,
-               N.ptr(do), N.ptr(dht), N.ptr(hs), N.ptr(dh_work), N.ptr(dq), N.ptr(dk), N.ptr(dv),
-               N.ptr(dg), N.ptr(dh0), N.ptr(plan.cu_dev), N.ptr(plan.offsets_dev),
-               N.ptr(plan.chunk_map_dev), plan.total, B, T, H, K, V, plan.N, dt, float(scale), st)
+        s0 = _segment_states(q, do, gate, dht, scale, sp, reverse=True)
+        fin = torch.empty(sp.Nv, H, K, V, device=q.device, dtype=torch.float32) \
+            if want_dh0 else None
+        cu, offs, Bx, Tx, Nx = sp.cu_dev, sp.offsets_dev, 1, B * T, sp.Nv
+    dh_args = (N.ptr(do), N.ptr(s0), N.ptr(dh_work), N.ptr(dv), N.ptr(fin), N.ptr(cu), N.ptr(offs),
+               Bx, Tx, H, K, V, Nx, dt, float(scale), st)
+    dqkg_tail = (N.ptr(do), N.ptr(hs), N.ptr(dh_work), N.ptr(dq), N.ptr(dk), N.ptr(dg),
+                 N.ptr(plan.cu_dev), N.ptr(plan.offsets_dev), N.ptr(plan.chunk_map_dev),
+                 plan.total, B, T, H, K, V, plan.N, dt, float(scale), st)
+    if mode == GATE_K:
+        N.call("tops_gla_chunk_bwd_dh", N.ptr(q), N.ptr(k), N.ptr(gt), *dh_args)
+        N.call("tops_gla_chunk_bwd_dqkg", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gt), *dqkg_tail)
+    else:
+        N.call("tops_simple_gla_chunk_bwd_dh", N.ptr(q), N.ptr(k), *_gate_ptrs(gate), *dh_args)
+        N.call("tops_simple_gla_chunk_bwd_dqkg", N.ptr(q), N.ptr(k), N.ptr(v), *_gate_ptrs(gate),
+               *dqkg_tail)
+    dh0 = fin
+    if sp is not None and fin is not None:
+        dh0 = fin.index_select(0, sp.first_dev)
     return dq, dk, dv, dg, dh0

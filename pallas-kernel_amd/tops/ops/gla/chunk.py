@@ -40,7 +40,7 @@ class _ChunkGLA(torch.autograd.Function):
         q, k, v = (x.contiguous() for x in (q, k, v))
         g32 = g.contiguous().to(torch.float32)
         h032 = None if h0 is None else h0.contiguous().to(torch.float32)
-        plan = ChunkPlan(q.shape[0], q.shape[1], cu_seqlens, q.device)
+        plan = ChunkPlan.get(q.shape[0], q.shape[1], cu_seqlens, q.device)
         train = any(ctx.needs_input_grad[:5])
         o, ht, hs = _fwd(q, k, v, g32, h032, scale, output_final_state, plan, keep_states=train)
         if train:
@@ -118,7 +118,7 @@ def chunk_gla_fwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, output_fi
     V = v.shape[-1]
     g = _gate_or_default(q, g, g_gamma)
     _check(q, k, v, g, initial_state, cu_seqlens)
-    plan = ChunkPlan(B, T, cu_seqlens, q.device)
+    plan = ChunkPlan.get(B, T, cu_seqlens, q.device)
     g32 = g.contiguous().to(torch.float32)
     h0 = None if initial_state is None else initial_state.contiguous().to(torch.float32)
     o, ht, hs = _fwd(q.contiguous(), k.contiguous(), v.contiguous(), g32, h0, scale,
@@ -141,7 +141,7 @@ def chunk_gla_bwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, h, A, do,
     g_orig = g
     g = _gate_or_default(q, g, g_gamma)
     _check(q, k, v, g, initial_state, cu_seqlens)
-    plan = ChunkPlan(B, T, cu_seqlens, q.device)
+    plan = ChunkPlan.get(B, T, cu_seqlens, q.device)
     q, k, v = (x.contiguous() for x in (q, k, v))
     g32 = g.contiguous().to(torch.float32)
     h0 = None if initial_state is None else initial_state.contiguous().to(torch.float32)

@@ -88,7 +88,7 @@ class _ChunkKDA(torch.autograd.Function):
         g32 = g.contiguous().to(torch.float32)
         b32 = beta.contiguous().to(torch.float32)
         h032 = None if h0 is None else h0.contiguous().to(torch.float32)
-        plan = ChunkPlan(q.shape[0], q.shape[1], cu_seqlens, q.device)
+        plan = ChunkPlan.get(q.shape[0], q.shape[1], cu_seqlens, q.device)
         train = any(ctx.needs_input_grad[:5]) or (h0 is not None and ctx.needs_input_grad[6])
         o, ht, saved = _fwd(q, k, v, g32, b32, h032, scale, output_final_state, plan, keep=train)
         if train:
@@ -157,7 +157,7 @@ def chunk_kda_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
     g32 = g.contiguous().to(torch.float32)
     b32 = beta.contiguous().to(torch.float32)
     h0 = None if initial_state is None else initial_state.contiguous().to(torch.float32)
-    plan = ChunkPlan(q.shape[0], q.shape[1], cu_seqlens, q.device)
+    plan = ChunkPlan.get(q.shape[0], q.shape[1], cu_seqlens, q.device)
     with torch.no_grad():
         o, ht, (w, tt, vn, hs) = _fwd(q, k, v, g32, b32, h0, scale, output_final_state, plan,
                                       keep=True)

@@ -46,7 +46,7 @@ class _ChunkSimpleGLA(torch.autograd.Function):
         q, k, v = (x.contiguous() for x in (q, k, v))
         g32 = gt.detach().contiguous().to(torch.float32)
         h032 = None if h0 is None else h0.contiguous().to(torch.float32)
-        plan = ChunkPlan(q.shape[0], q.shape[1], cu_seqlens, q.device)
+        plan = ChunkPlan.get(q.shape[0], q.shape[1], cu_seqlens, q.device)
         train = any(ctx.needs_input_grad[:5])
         o, ht, hs = _core_fwd(q, k, v, (mode, g32), h032, scale, output_final_state, plan,
                               keep_states=train)
@@ -109,7 +109,7 @@ def chunk_simple_gla_fwd(q, k, v, g=None, g_gamma=None, scale=None, initial_stat
     check_qkv(q, k, v, initial_state, cu_seqlens)
     if scale is None:
         scale = q.shape[-1] ** -0.5
-    plan = ChunkPlan(q.shape[0], q.shape[1], cu_seqlens, q.device)
+    plan = ChunkPlan.get(q.shape[0], q.shape[1], cu_seqlens, q.device)
     h0 = None if initial_state is None else initial_state.contiguous().to(torch.float32)
     o, ht, _ = _core_fwd(q.contiguous(), k.contiguous(), v.contiguous(),
                          (mode, gt.contiguous().to(torch.float32)), h0, scale,
@@ -138,7 +138,7 @@ def chunk_simple_gla_bwd(q, k, v, do, *, g=None, g_gamma=None, scale=None, h0=No
     check_qkv(q, k, v, h0, cu_seqlens)
     if scale is None:
         scale = q.shape[-1] ** -0.5
-    plan = ChunkPlan(q.shape[0], q.shape[1], cu_seqlens, q.device)
+    plan = ChunkPlan.get(q.shape[0], q.shape[1], cu_seqlens, q.device)
     q, k, v = (x.contiguous() for x in (q, k, v))
     g32 = gt.contiguous().to(torch.float32)
     h032 = None if h0 is None else h0.contiguous().to(torch.float32)

@@ -1,6 +1,8 @@
 """Host-side helpers mirroring tops/utils.py (varlen chunk maps, ceil-div)."""
 from __future__ import annotations
 
+from collections import OrderedDict
+
 import numpy as np
 import torch
 
@@ -41,8 +43,46 @@ def prepare_chunk_indices(cu_seqlens, chunk_size: int) -> np.ndarray:
     return idx[:total].copy()
 
 
+def _upload(a: np.ndarray, device) -> torch.Tensor:
+    """One int32 host array to the device; staged through pinned memory so the copy is
+    queued on the current stream instead of draining it."""
+    t = torch.from_numpy(np.ascontiguousarray(a, np.int32))
+    if torch.device(device).type == "cuda":
+        return t.pin_memory().to(device, non_blocking=True)
+    return t.to(device)
+
+
+def _split_views(t: torch.Tensor, sizes):
+    out, o = [], 0
+    for n in sizes:
+        out.append(t[o:o + n])
+        o += n
+    return out
+
+
+_PLANS: "OrderedDict" = OrderedDict()
+_PLANS_MAX = 32
+
+
 class ChunkPlan:
-    """Chunk bookkeeping of one call: sequences, global chunk offsets, device maps."""
+    """Chunk bookkeeping of one call: sequences, global chunk offsets, device maps (one
+    device array, uploaded once)."""
+
+    @classmethod
+    def get(cls, B: int, T: int, cu_seqlens, device, C: int = CHUNK) -> "ChunkPlan":
+        """The plan for these sizes / sequence boundaries, reused across calls (the maps
+        depend only on the boundaries)."""
+        cu = None if cu_seqlens is None else _host_cu(cu_seqlens)
+        key = (B, T, C, str(torch.device(device)), None if cu is None else cu.tobytes())
+        plan = _PLANS.get(key)
+        if plan is None:
+            plan = cls(B, T, cu, device, C)
+            _PLANS[key] = plan
+            if len(_PLANS) > _PLANS_MAX:
+                _PLANS.popitem(last=False)
+        else:
+            _PLANS.move_to_end(key)
+        return plan
 
     def __init__(self, B: int, T: int, cu_seqlens, device, C: int = CHUNK):
         self.C = C
@@ -54,10 +94,119 @@ class ChunkPlan:
             self.total = idx.shape[0]
             offs = np.zeros(self.N + 1, np.int32)
             np.cumsum(np.bincount(idx[:, 0], minlength=self.N), out=offs[1:])
-            self.cu_dev = torch.from_numpy(cu).to(device)
-            self.offsets_dev = torch.from_numpy(offs).to(device)
-            self.chunk_map_dev = torch.from_numpy(np.ascontiguousarray(idx[:, 0])).to(device)
+            dev = _upload(np.concatenate([cu, offs, idx[:, 0]]), device)
+            self.cu_dev, self.offsets_dev, self.chunk_map_dev = _split_views(
+                dev, (self.N + 1, self.N + 1, self.total))
         else:
             self.N = B
             self.total = B * cdiv(T, C)
             self.cu_dev = self.offsets_dev = self.chunk_map_dev = None
+            cu = np.arange(B + 1, dtype=np.int32) * T
+        self.cu_host = cu
+        self.device = device
+        self._seg = {}
+
+    def segments(self, H: int, V: int):
+        """The sequence-parallel split of this call for H heads and V columns (a SegPlan),
+        or None when every sequence sweeps whole."""
+        key = (H, V, _SPLIT["mode"])
+        if key not in self._seg:
+            self._seg[key] = SegPlan.build(self, H, V)
+        return self._seg[key]
+
+
+# Sequence-parallel sweeps.  A sweep runs one workgroup per (sequence, head, 64-column
+# V tile) and walks that sequence's chunks in order, so a call whose sequences are few or
+# unequal leaves CUs idle while its longest sequence finishes.  Such sequences are cut
+# at chunk boundaries into segments that sweep concurrently (tops_chunk_state_pass /
+# tops_chunk_state_combine in include/tops_hip.h).
+_SPLIT = {"mode": None}   # None: automatic; 0: never split; k > 0: segments of k chunks
+MIN_SEG_CHUNKS = 8        # shortest segment worth its state pass
+SPLIT_SLACK = 1.25        # split a sequence only when it is this much above the target
+
+
+def set_sequence_split(mode=None) -> None:
+    """None: split long sequences when the CUs would otherwise idle (default); 0: never;
+    an integer k > 0: cut every sequence into ceil(chunks / k) near-equal segments."""
+    if mode is not None and (not isinstance(mode, int) or mode < 0):
+        raise ValueError("set_sequence_split takes None or an integer >= 0")
+    _SPLIT["mode"] = mode
+
+
+def _device_cus(device) -> int:
+    return int(torch.cuda.get_device_properties(device).multi_processor_count)
+
+
+class SegPlan:
+    """Segments of the sequences of one ChunkPlan, in token order (host arrays and their
+    device copies):
+      cu_dev [Nv+1]        segment boundaries (a varlen layout over the same tokens)
+      offsets_dev [Nv+1]   first global chunk of each segment (the plan's chunk numbering)
+      seg_first_dev [N+1]  segments of real sequence n: [seg_first[n], seg_first[n+1])
+      st_first_dev [N+1]   its state-pass entries (one fewer than its segments)
+      fwd_start/fwd_end    rows of the segments that pass a state forward (all but the last
+                           of a sequence), rev_start/rev_end the same for the reverse sweep
+      last_dev, first_dev  [N] last / first segment of every real sequence"""
+
+    @staticmethod
+    def split_counts(chunks: np.ndarray, slots: int, mode) -> np.ndarray:
+        """Segments per sequence.  Automatic: aim at total/slots chunks per segment (at least
+        MIN_SEG_CHUNKS) and split only sequences above SPLIT_SLACK times that."""
+        if mode == 0:
+            return np.ones_like(chunks)
+        if mode is not None:
+            return np.maximum(1, -(-chunks // mode))
+        target = max(-(-int(chunks.sum()) // max(slots, 1)), MIN_SEG_CHUNKS)
+        m = -(-chunks // target)
+        return np.where(chunks > SPLIT_SLACK * target, m, 1)
+
+    @classmethod
+    def build(cls, plan: "ChunkPlan", H: int, V: int):
+        cu = plan.cu_host.astype(np.int64)
+        lens = cu[1:] - cu[:-1]
+        C = plan.C
+        chunks = -(-lens // C)
+        mode = _SPLIT["mode"]
+        slots = 1
+        if mode is None:
+            slots = _device_cus(plan.device) // max(H * cdiv(V, 64), 1)
+        m = cls.split_counts(chunks, slots, mode)
+        if int(m.max()) <= 1:
+            return None
+        return cls(cu, chunks, m, C, plan.device)
+
+    def __init__(self, cu, chunks, m, C, device):
+        coff = np.concatenate([[0], np.cumsum(chunks)])
+        starts, offs, seg_first = [], [], [0]
+        fwd, rev, st_first = [], [], [0]
+        for n in range(len(chunks)):
+            base, rem = divmod(int(chunks[n]), int(m[n]))
+            sizes = [base + (1 if j < rem else 0) for j in range(int(m[n]))]
+            c0 = 0
+            bounds = []
+            for sz in sizes:
+                bounds.append(int(cu[n]) + C * c0)
+                offs.append(int(coff[n]) + c0)
+                c0 += sz
+            bounds.append(int(cu[n + 1]))
+            starts.extend(bounds[:-1])
+            seg_first.append(seg_first[-1] + len(sizes))
+            st_first.append(st_first[-1] + len(sizes) - 1)
+            for j in range(len(sizes) - 1):
+                fwd.append((bounds[j], bounds[j + 1]))
+                rev.append((bounds[j + 1], bounds[j + 2]))
+        self.Nv = len(starts)
+        self.n_state = len(fwd)
+        cu_v = np.array(starts + [int(cu[-1])], np.int32)
+        offs_v = np.array(offs + [int(coff[-1])], np.int32)
+        sf = np.array(seg_first, np.int32)
+        self.seg_first = sf
+        self.cu_host = cu_v
+        fw = np.array(fwd, np.int32).reshape(-1, 2)
+        rv = np.array(rev, np.int32).reshape(-1, 2)
+        parts = [cu_v, offs_v, sf, np.array(st_first, np.int32), fw[:, 0], fw[:, 1], rv[:, 0],
+                 rv[:, 1], sf[:-1], sf[1:] - 1]
+        (self.cu_dev, self.offsets_dev, self.seg_first_dev, self.st_first_dev,
+         self.fwd_start_dev, self.fwd_end_dev, self.rev_start_dev, self.rev_end_dev,
+         self.first_dev, self.last_dev) = _split_views(
+            _upload(np.concatenate(parts), device), [len(x) for x in parts])
