@@ -238,7 +238,7 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
     // ---- this pass's h rows, issued before the staging so their latency overlaps it
     const int kl = 16 * kb + l16;          // channel of this lane's A-operand row (in pass)
     const int kk = cb + kl;
-    uint4 hraw[VC][2];
+    uint4 hraw[VC][2], draw[VC][2];
 #pragma unroll
     for (int vc = 0; vc < VC; ++vc) {
       const int v0 = 32 * vc + 8 * lg;
@@ -282,6 +282,14 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
       put_n<true, 8>(Pkt, ch, 8 * sg, kt);
     }
     if (ps + 1 < NPS) load_pass(ps + 1);
+    // this pass's dh rows, in flight across the barrier
+#pragma unroll
+    for (int vc = 0; vc < VC; ++vc) {
+      const int v0 = 32 * vc + 8 * lg;
+      const uint32_t o = (kk < K && v0 < V) ? ((uint32_t)kk * V + v0) * 4u : kOOB;
+      draw[vc][0] = bld128(Rdh, o, 0);
+      draw[vc][1] = bld128(Rdh, o, 16);
+    }
     __syncthreads();  // planes, sG, sGm, sGam visible
 
     // ---- inter-chunk: X^T += (alpha h) dO^T, W^T += (beta dh) v^T
@@ -293,12 +301,11 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
 #pragma unroll
     for (int vc = 0; vc < VC; ++vc) {
       const int v0 = 32 * vc + 8 * lg;
-      const uint32_t o = (kk < K && v0 < V) ? ((uint32_t)kk * V + v0) * 4u : kOOB;
       float hv[8], dv[8];
       unpack4(hraw[vc][0], hv);
       unpack4(hraw[vc][1], hv + 4);
-      unpack4(bld128(Rdh, o, 0), dv);
-      unpack4(bld128(Rdh, o, 16), dv + 4);
+      unpack4(draw[vc][0], dv);
+      unpack4(draw[vc][1], dv + 4);
       if (rh == 0) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) hd += hv[e] * dv[e];
