@@ -416,7 +416,7 @@ static int fr_check(const char* who, int B, int T, int H, int K, int V, int N,
     return tops_set_error(TOPS_ERR_SHAPE, msg);
   }
   if (K > 128 || (K % 4)) {
-    snprintf(msg, sizeof(msg), "%s: need K <= 128 and K % 4 == 0", who);
+    snprintf(msg, sizeof(msg), "%s: need K <= 128 and K %% 4 == 0", who);
     return tops_set_error(TOPS_ERR_SHAPE, msg);
   }
   if (cu_seqlens && B != 1) {
