@@ -80,6 +80,13 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   constexpr int NHTS = 2 * BV * (REV_DELTA && LT > LH ? LT : LH);
   __shared__ __attribute__((aligned(16))) uint16_t sHT[NHTS];
   __shared__ __attribute__((aligned(16))) float sTot[NSGH * KP]; // gate totals per segment group
+  // Causal D tiles of the chunk shared through LDS (bf16 hi/lo per lane, 10 tiles x 1 KB):
+  // each tile is computed once instead of once per column-tile wave, and the work is spread
+  // evenly over the waves.  Only where the 160 KB budget allows (not the delta sweeps).
+  constexpr int LDS_BASE = 2 * (2 * C * LQ) * 2 + 2 * KP * LT * 2 + (SY ? 2 : 1) * BV * LT * 2 +
+                           NHTS * 2 + NSGH * KP * 4;
+  constexpr bool SHARED_D = !DELTA && !ST && LDS_BASE + 10 * 64 * 16 <= 160 * 1024;
+  __shared__ __attribute__((aligned(16))) uint4 sDt[SHARED_D ? 10 * 64 : 1];
   // Gamma / 2 of channel c sits in the padding columns of the X hi plane (row c / 4, word c % 4):
   // no MFMA fragment or staging write touches columns >= KP
   auto gm_at = [&](int c4) { return (float*)(sX + (c4 >> 2) * LQ + KP); };
@@ -180,8 +187,10 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   }
 
   // ---- raw chunk registers (prefetch targets): PF sets, the chunk PF steps ahead is
-  // loaded into the set just consumed
-  constexpr int PF = (DELTA || SIN) ? 1 : 2;   // two sets fit the register budget for bf16
+  // loaded into the set just consumed.  One set is issued a whole chunk ahead (after B2),
+  // which covers the load latency; the second set pays off only for the instances whose
+  // output block keeps fewer registers live (bf16 without shared D tiles).
+  constexpr int PF = (DELTA || SIN || SHARED_D) ? 1 : 2;
   struct Raw {
     typename Wd::W4 rq[RPT], rk[RPT];
     uint4 rg[RPT];
@@ -339,18 +348,18 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     } else {
       const rsrc_t Rck = make_rsrc(p.ckpt ? p.ckpt + ((size_t)(cbase + c) * H + hh) * K * V : nullptr,
                                    p.ckpt ? (long long)K * V * 4 : 0);
-  #pragma unroll
+#pragma unroll
       for (int i = 0; i < NHT; ++i) {
         const int nn = (wave * NHT + i) % (BV / 16);
         const int kr = 16 * msb + 4 * lg;
         float x[4];
-  #pragma unroll
+#pragma unroll
         for (int r = 0; r < 4; ++r) x[r] = sal[r] * S[i][r];
         put_n<true, 4>(PHt, 16 * nn + l16, kr, x);
         if (p.ckpt) {
           const int vv = vt * BV + 16 * nn + l16;
           const uint32_t vo = (vv < V) ? ((uint32_t)kr * V + vv) * 4u : kOOB;
-  #pragma unroll
+#pragma unroll
           for (int r = 0; r < 4; ++r)
             bst32(Rck, __float_as_uint(S[i][r]), (kr + r < K) ? vo : kOOB, (uint32_t)(r * V * 4));
         }
@@ -413,17 +422,144 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       }
     }
 
+    // ---------------- state update: S = 2^Gamma S + beta (Z~^T Y) [- w^T dv_new]
+    auto state_update = [&]() {
+      // (shared-D build) every fragment first, then the NHT independent accumulation chains
+      // interleaved term by term, so neither LDS latency nor MFMA dependencies serialise
+      f32x4 dsu[NHT];
+      if constexpr (SHARED_D) {
+        bf16x8 zh[C / 32], zl[C / 32], yh[NHT][C / 32], yl[NHT][C / 32];
+#pragma unroll
+        for (int kc = 0; kc < C / 32; ++kc) {
+          zh[kc] = PZt.hi8(16 * msb + l16, 32 * kc + 8 * lg);
+          zl[kc] = PZt.lo8(16 * msb + l16, 32 * kc + 8 * lg);
+#pragma unroll
+          for (int i = 0; i < NHT; ++i) {
+            const int nn = (wave * NHT + i) % (BV / 16);
+            yh[i][kc] = PYt.hi8(16 * nn + l16, 32 * kc + 8 * lg);
+            if constexpr (SY) yl[i][kc] = PYt.lo8(16 * nn + l16, 32 * kc + 8 * lg);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < NHT; ++i) dsu[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < C / 32; ++kc) {
+#pragma unroll
+          for (int i = 0; i < NHT; ++i) dsu[i] = mfma(zl[kc], yh[i][kc], dsu[i]);
+          if constexpr (SY) {
+#pragma unroll
+            for (int i = 0; i < NHT; ++i) dsu[i] = mfma(zh[kc], yl[i][kc], dsu[i]);
+          }
+#pragma unroll
+          for (int i = 0; i < NHT; ++i) dsu[i] = mfma(zh[kc], yh[i][kc], dsu[i]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < NHT; ++i) {
+        const int nn = (wave * NHT + i) % (BV / 16);
+        f32x4 d = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (REV_DELTA) {
+#pragma unroll
+          for (int kc = 0; kc < C / 32; ++kc)
+            d = mma<true, true>(d, PWt.hi8(16 * msb + l16, 32 * kc + 8 * lg), PWt.lo8(16 * msb + l16, 32 * kc + 8 * lg),
+                                PDt.hi8(16 * nn + l16, 32 * kc + 8 * lg), PDt.lo8(16 * nn + l16, 32 * kc + 8 * lg));
+        } else if constexpr (!SHARED_D) {
+#pragma unroll
+          for (int kc = 0; kc < C / 32; ++kc) {
+            const bf16x8 bh = PYt.hi8(16 * nn + l16, 32 * kc + 8 * lg);
+            bf16x8 bl = bh;
+            if constexpr (SY) bl = PYt.lo8(16 * nn + l16, 32 * kc + 8 * lg);
+            d = mma<true, SY>(d, PZt.hi8(16 * msb + l16, 32 * kc + 8 * lg),
+                              PZt.lo8(16 * msb + l16, 32 * kc + 8 * lg), bh, bl);
+          }
+        } else {
+          d = dsu[i];
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if constexpr (REV_DELTA) S[i][r] = sga[r] * S[i][r] + sbe[r] * d1[i][r] - d[r];
+          else S[i][r] = sga[r] * S[i][r] + sbe[r] * d[r];
+        }
+      }
+    };
+
     // ---------------- output block: token block R, column tiles 2 nh, 2 nh + 1
     if constexpr (!ST) {
+    // X rows of this wave's token block (with shared D tiles: loaded after B3, so they do not
+    // hold registers through the D tiles and the state update)
     bf16x8 xh[KP / 32], xl[KP / 32];
+    auto load_x = [&]() {
 #pragma unroll
-    for (int kc = 0; kc < KP / 32; ++kc) {
-      xh[kc] = PX.hi8(16 * R + l16, 32 * kc + 8 * lg);
-      xl[kc] = PX.lo8(16 * R + l16, 32 * kc + 8 * lg);
-    }
+      for (int kc = 0; kc < KP / 32; ++kc) {
+        xh[kc] = PX.hi8(16 * R + l16, 32 * kc + 8 * lg);
+        xl[kc] = PX.lo8(16 * R + l16, 32 * kc + 8 * lg);
+      }
+    };
+    if constexpr (!SHARED_D) load_x();
     // D tiles (P, R) on the causal side: lane holds D[16P+4lg+r][16R+l16]
     const float dsc = FWD_DELTA ? 1.f : scale;   // the delta forward folds scale into X
     uint2 dh[4], dl[4];
+    if constexpr (SHARED_D) {
+      // tile t = Rc (Rc + 1) / 2 + Pc with Pc <= Rc in causal order (Rc = R, Pc = P forward;
+      // 3 - R, 3 - P reverse); wave w computes tiles w and w + 8
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int t = wave + 8 * u;
+        if (t < 10) {
+          const int Rc = t >= 6 ? 3 : (t >= 3 ? 2 : (t >= 1 ? 1 : 0));
+          const int Pc = t - Rc * (Rc + 1) / 2;
+          const int Rt = REV ? 3 - Rc : Rc, Pt = REV ? 3 - Pc : Pc;
+          // three independent chains (lo.hi, hi.lo, hi.hi); the fragments of step kc + 1 are
+          // read before the products of step kc
+          f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0, a2 = a0;
+          bf16x8 fz[2][2], fx[2][2];
+          auto ld = [&](int kc, int b) {
+            fz[b][0] = PZ.hi8(16 * Pt + l16, 32 * kc + 8 * lg);
+            fz[b][1] = PZ.lo8(16 * Pt + l16, 32 * kc + 8 * lg);
+            fx[b][0] = PX.hi8(16 * Rt + l16, 32 * kc + 8 * lg);
+            fx[b][1] = PX.lo8(16 * Rt + l16, 32 * kc + 8 * lg);
+          };
+          ld(0, 0);
+#pragma unroll
+          for (int kc = 0; kc < KP / 32; ++kc) {
+            const int b = kc & 1;
+            if (kc + 1 < KP / 32) ld(kc + 1, b ^ 1);
+            a0 = mfma(fz[b][1], fx[b][0], a0);
+            a1 = mfma(fz[b][0], fx[b][1], a1);
+            a2 = mfma(fz[b][0], fx[b][0], a2);
+          }
+          f32x4 acc;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[r] = (a0[r] + a1[r]) + a2[r];
+          const int rr = 16 * Rt + l16;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int pp = 16 * Pt + 4 * lg + r;
+            const bool keep = REV ? (pp >= rr) : (pp <= rr);
+            acc[r] = keep ? acc[r] * dsc : 0.f;
+          }
+          uint2 th, tl;
+          acc_to_bf16x4(acc, th, tl);
+          sDt[t * 64 + lane] = make_uint4(th.x, th.y, tl.x, tl.y);
+        }
+      }
+      // the state update reads only the Z^T / Y^T planes: it fills the wait for the D tiles
+      state_update();
+      __syncthreads();  // B3: D tiles visible
+      load_x();
+#pragma unroll
+      for (int P = 0; P < 4; ++P) {
+        dh[P] = make_uint2(0u, 0u);
+        dl[P] = make_uint2(0u, 0u);
+        const bool live = REV ? (P >= R) : (P <= R);
+        if (live) {
+          const int Rc = REV ? 3 - R : R, Pc = REV ? 3 - P : P;
+          const uint4 x = sDt[(Rc * (Rc + 1) / 2 + Pc) * 64 + lane];
+          dh[P] = make_uint2(x.x, x.y);
+          dl[P] = make_uint2(x.z, x.w);
+        }
+      }
+    } else {
 #pragma unroll
     for (int P = 0; P < 4; ++P) {
       dh[P] = make_uint2(0u, 0u);
@@ -445,6 +581,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
         acc_to_bf16x4(t, dh[P], dl[P]);
       }
     }
+    }  // SHARED_D
 
     if constexpr (FWD_DELTA) {
       // v_new = u - w S for (token block R, column tiles 2nh, 2nh+1).  The A operand
@@ -577,32 +714,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 
     }  // !ST
 
-    // ---------------- state update: S = 2^Gamma S + beta (Z~^T Y) [- w^T dv_new]
-#pragma unroll
-    for (int i = 0; i < NHT; ++i) {
-      const int nn = (wave * NHT + i) % (BV / 16);
-      f32x4 d = {0.f, 0.f, 0.f, 0.f};
-      if constexpr (REV_DELTA) {
-#pragma unroll
-        for (int kc = 0; kc < C / 32; ++kc)
-          d = mma<true, true>(d, PWt.hi8(16 * msb + l16, 32 * kc + 8 * lg), PWt.lo8(16 * msb + l16, 32 * kc + 8 * lg),
-                              PDt.hi8(16 * nn + l16, 32 * kc + 8 * lg), PDt.lo8(16 * nn + l16, 32 * kc + 8 * lg));
-      } else {
-#pragma unroll
-        for (int kc = 0; kc < C / 32; ++kc) {
-          const bf16x8 bh = PYt.hi8(16 * nn + l16, 32 * kc + 8 * lg);
-          bf16x8 bl = bh;
-          if constexpr (SY) bl = PYt.lo8(16 * nn + l16, 32 * kc + 8 * lg);
-          d = mma<true, SY>(d, PZt.hi8(16 * msb + l16, 32 * kc + 8 * lg),
-                            PZt.lo8(16 * msb + l16, 32 * kc + 8 * lg), bh, bl);
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if constexpr (REV_DELTA) S[i][r] = sga[r] * S[i][r] + sbe[r] * d1[i][r] - d[r];
-        else S[i][r] = sga[r] * S[i][r] + sbe[r] * d[r];
-      }
-    }
+    if constexpr (!SHARED_D) state_update();
   };
 
   if constexpr (PF == 2) {
