@@ -366,9 +366,11 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       }
     }
 
-    // ---------------- gated operands for the staging rows
+    // ---------------- gated operands for the staging rows.  Z~ is split into bf16 hi / lo once;
+    // the transposed plane reuses those halves, regrouped per channel with byte permutes.
     {
       float zt[4][RPT];
+      uint32_t zh[RPT][2], zl[RPT][2];
 #pragma unroll
       for (int i = 0; i < RPT; ++i) {
         float qv[4], kv[4], xq[4], xk[4];
@@ -382,15 +384,41 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
         }
         const float* xx = REV ? xk : xq;
         const float* zz = REV ? xq : xk;
+        if constexpr (!ST) put_n<true, 4>(PX, r0 + i, c0, xx);
+        split_bf16x2(zz[0], zz[1], zh[i][0], zl[i][0]);
+        split_bf16x2(zz[2], zz[3], zh[i][1], zl[i][1]);
         if constexpr (!ST) {
-          put_n<true, 4>(PX, r0 + i, c0, xx);
-          put_n<true, 4>(PZ, r0 + i, c0, zz);
+          *(uint2*)(PZ.hi + (r0 + i) * PZ.ld + c0) = make_uint2(zh[i][0], zh[i][1]);
+          *(uint2*)(PZ.lo + (r0 + i) * PZ.ld + c0) = make_uint2(zl[i][0], zl[i][1]);
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) zt[j][i] = zz[j];
       }
+      if constexpr (RPT >= 2) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) put_n<true, RPT>(PZt, c0 + j, r0, zt[j]);
+        for (int j = 0; j < 4; ++j) {
+          // channel j of rows (2m, 2m + 1): the low (j even) or high (j odd) bf16 of each word
+          const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+          uint32_t th[RPT / 2], tl[RPT / 2];
+#pragma unroll
+          for (int m = 0; m < RPT / 2; ++m) {
+            th[m] = __builtin_amdgcn_perm(zh[2 * m + 1][j >> 1], zh[2 * m][j >> 1], sel);
+            tl[m] = __builtin_amdgcn_perm(zl[2 * m + 1][j >> 1], zl[2 * m][j >> 1], sel);
+          }
+          uint16_t* ph = PZt.hi + (c0 + j) * PZt.ld + r0;
+          uint16_t* pl = PZt.lo + (c0 + j) * PZt.ld + r0;
+          if constexpr (RPT == 4) {
+            *(uint2*)ph = make_uint2(th[0], th[1]);
+            *(uint2*)pl = make_uint2(tl[0], tl[1]);
+          } else {
+            *(uint32_t*)ph = th[0];
+            *(uint32_t*)pl = tl[0];
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) put_n<true, RPT>(PZt, c0 + j, r0, zt[j]);
+      }
       if constexpr (!FWD_DELTA) {
         float ya[YR], yb[YR];
 #pragma unroll
