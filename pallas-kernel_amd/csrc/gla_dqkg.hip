@@ -151,9 +151,14 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
   // ---------------- staging of a pass: thread = (channel ch, 8-row segment sg)
   const int ch = tid & 31, sg = tid >> 5;
   float rq[8], rk[8], rg[8];
+  // gate element (row r, channel kc): per-channel [.., K], per-token [.., 1], or none (gamma)
+  const bool gk_mode = gmode == kGateK;
+  const uint32_t gstr = gk_mode ? rowK * 4u : (uint32_t)H * 4u;
+  const bool gload = gmode != kGateGamma;
   auto load_pass = [&](int ps) {
     const int kc = ps * KH + ch;
     const bool ok = kc < K;
+    const uint32_t gcol = gk_mode ? (uint32_t)kc * 4u : 0u;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int r = 8 * sg + i;
@@ -170,8 +175,7 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
         rk[i] = (off & 1u) ? __uint_as_float(wk & 0xffff0000u) : __uint_as_float(wk << 16);
       }
       // one unconditional load whatever the gate mode (gamma loads nothing: out of range)
-      const uint32_t go = gmode == kGateK ? off * 4u : (gmode == kGateS ? (uint32_t)r * H * 4u : kOOB);
-      rg[i] = __uint_as_float(bld32(Rg, v_ ? go : kOOB, 0));
+      rg[i] = __uint_as_float(bld32(Rg, (v_ && gload) ? (uint32_t)r * gstr + gcol : kOOB, 0));
     }
   };
   load_pass(0);
