@@ -110,38 +110,88 @@ __global__ __launch_bounds__(256, 2) void kda_wy_kernel(KdaWyParams p) {
   __syncthreads();  // beta visible
 
   // ---------------- P = T^T dv_new: wave w takes the V blocks vb = w, w + 4, ..; tile (vb, I)
-  // computed transposed, lane holds P[16I + l16][16vb + 4lg + r]
+  // computed transposed, lane holds P[16I + l16][16vb + 4lg + r].  Every global operand of
+  // the phase (dv_new^T and T^T fragments, v rows) is requested before the first product.
   {
+    constexpr int NVW = (NVB + 3) / 4;          // V blocks per wave
     const rsrc_t Rdv = make_rsrc((TIn*)p.dv + e0 * V, remr * V * ES);
-    float dbv[4] = {0.f, 0.f, 0.f, 0.f};        // per token block I: sum_v v P (this lane's v's)
-    for (int vb = wave; vb < NVB; vb += 4) {
-      const int v = 16 * vb + l16;
-      bf16x8 ah[2], al[2];
+    uint4 draw[NVW][2][2], traw[4][2][2];
+    typename Wd::W4 vraw[NVW][4];
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc)
-        load_split8(Rdvt, v < V ? ((uint32_t)v * C + 32 * kc + 8 * lg) * 4u : kOOB, ah[kc], al[kc]);
+    for (int u = 0; u < NVW; ++u) {
+      const int vb = wave + 4 * u;
+      const int v = 16 * vb + l16;
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        const uint32_t o = (vb < NVB && v < V) ? ((uint32_t)v * C + 32 * kc + 8 * lg) * 4u : kOOB;
+        draw[u][kc][0] = bld128(Rdvt, o, 0);
+        draw[u][kc][1] = bld128(Rdvt, o == kOOB ? kOOB : o + 16u, 0);
+      }
+    }
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        if (kc == 1 || I < 2) {                 // T[i'][i] = 0 for i' < i
+          const uint32_t o = ((uint32_t)(16 * I + l16) * C + 32 * kc + 8 * lg) * 4u;
+          traw[I][kc][0] = bld128(Rtt, o, 0);
+          traw[I][kc][1] = bld128(Rtt, o + 16u, 0);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < NVW; ++u) {
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
-        const int i = 16 * I + l16;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        const int vb = wave + 4 * u, i = 16 * I + l16, col = 16 * vb + 4 * lg;
+        vraw[u][I] = Wd::ld4(Rv, (vb < NVB && i < nval && col < V) ? ((uint32_t)i * rowV + col) * ES : kOOB, 0);
+      }
+    }
+    auto split16 = [](const uint4 (&r)[2], bf16x8& h, bf16x8& l) {
+      float a[4], b[4];
+      unpack4(r[0], a);
+      unpack4(r[1], b);
+      uint32_t hh[4], ll[4];
+      split_bf16x2(a[0], a[1], hh[0], ll[0]);
+      split_bf16x2(a[2], a[3], hh[1], ll[1]);
+      split_bf16x2(b[0], b[1], hh[2], ll[2]);
+      split_bf16x2(b[2], b[3], hh[3], ll[3]);
+      h = __builtin_bit_cast(bf16x8, make_uint4(hh[0], hh[1], hh[2], hh[3]));
+      l = __builtin_bit_cast(bf16x8, make_uint4(ll[0], ll[1], ll[2], ll[3]));
+    };
+    bf16x8 th[4][2], tl[4][2];
 #pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {
-          if (kc == 1 || I < 2) {           // T[i'][i] = 0 for i' < i
-            bf16x8 th, tl;
-            load_split8(Rtt, ((uint32_t)i * C + 32 * kc + 8 * lg) * 4u, th, tl);
-            acc = mma<true, true>(acc, ah[kc], al[kc], th, tl);
-          }
+    for (int I = 0; I < 4; ++I) {
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc)
+        if (kc == 1 || I < 2) split16(traw[I][kc], th[I][kc], tl[I][kc]);
+    }
+    float dbv[4] = {0.f, 0.f, 0.f, 0.f};        // per token block I: sum_v v P (this lane's v's)
+#pragma unroll
+    for (int u = 0; u < NVW; ++u) {
+      const int vb = wave + 4 * u;
+      if (vb < NVB) {
+        bf16x8 ah[2], al[2];
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) split16(draw[u][kc], ah[kc], al[kc]);
+#pragma unroll
+        for (int I = 0; I < 4; ++I) {
+          const int i = 16 * I + l16;
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kc = 0; kc < 2; ++kc)
+            if (kc == 1 || I < 2) acc = mma<true, true>(acc, ah[kc], al[kc], th[I][kc], tl[I][kc]);
+          const float x[4] = {acc[0], acc[1], acc[2], acc[3]};
+          put_n<true, 4>(PP, i, 16 * vb + 4 * lg, x);
+          const int col = 16 * vb + 4 * lg;
+          const uint32_t off = (i < nval && col < V) ? ((uint32_t)i * rowV + col) * ES : kOOB;
+          float vv[4];
+          unpack4(vraw[u][I], vv);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) dbv[I] += vv[r] * acc[r];
+          const float bi = sBeta[i];
+          Wd::st4(Rdv, f32x4{bi * acc[0], bi * acc[1], bi * acc[2], bi * acc[3]}, off, 0);
         }
-        const float x[4] = {acc[0], acc[1], acc[2], acc[3]};
-        put_n<true, 4>(PP, i, 16 * vb + 4 * lg, x);
-        const int col = 16 * vb + 4 * lg;
-        const uint32_t off = (i < nval && col < V) ? ((uint32_t)i * rowV + col) * ES : kOOB;
-        float vv[4];
-        unpack4(Wd::ld4(Rv, off, 0), vv);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dbv[I] += vv[r] * acc[r];
-        const float bi = sBeta[i];
-        Wd::st4(Rdv, f32x4{bi * acc[0], bi * acc[1], bi * acc[2], bi * acc[3]}, off, 0);
       }
     }
 #pragma unroll
@@ -159,29 +209,71 @@ __global__ __launch_bounds__(256, 2) void kda_wy_kernel(KdaWyParams p) {
   // dac[a][I] (I >= t): lane holds beta_i dAkk[16I + 4lg + r][16t + l16]   (A operand, rows j)
   uint2 darh[2][4], darl[2][4], dach[2][4], dacl[2][4];
   {
+    // v_new rows of the wave's two token blocks, requested together; the lower half of the
+    // chunk (blocks 0, 1) is handed to the upper waves through LDS (the pass planes' space,
+    // unused until the channel passes), so no wave reads a row block from HBM twice
+    uint4 oraw[2][VC][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      const int j = 16 * (2 * tp + a) + l16;
+#pragma unroll
+      for (int vc = 0; vc < VC; ++vc) {
+        const int v0 = 32 * vc + 8 * lg;
+        const uint32_t o = (j < nval && v0 < V) ? ((uint32_t)j * rowV + v0) * 4u : kOOB;
+        oraw[a][vc][0] = bld128(Rvn, o, 0);
+        oraw[a][vc][1] = bld128(Rvn, o == kOOB ? kOOB : o + 16u, 0);
+      }
+    }
+    bf16x8 vth[2][VC], vtl[2][VC];
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+#pragma unroll
+      for (int vc = 0; vc < VC; ++vc) {
+        float x[4], y[4];
+        unpack4(oraw[a][vc][0], x);
+        unpack4(oraw[a][vc][1], y);
+        uint32_t hh[4], ll[4];
+        split_bf16x2(x[0], x[1], hh[0], ll[0]);
+        split_bf16x2(x[2], x[3], hh[1], ll[1]);
+        split_bf16x2(y[0], y[1], hh[2], ll[2]);
+        split_bf16x2(y[2], y[3], hh[3], ll[3]);
+        vth[a][vc] = __builtin_bit_cast(bf16x8, make_uint4(hh[0], hh[1], hh[2], hh[3]));
+        vtl[a][vc] = __builtin_bit_cast(bf16x8, make_uint4(ll[0], ll[1], ll[2], ll[3]));
+      }
+    }
+    static_assert(32 * LP * 2 <= 2 * KH * LT * 2, "rows 0..31 must fit the pass planes");
+    const Plane PL{sK1t, sK2t, LP};             // v_new rows 0..31, hi / lo
+    if (tp == 0 && kb == 0) {
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+#pragma unroll
+        for (int vc = 0; vc < VC; ++vc) {
+          *(bf16x8*)(PL.hi + (16 * a + l16) * LP + 32 * vc + 8 * lg) = vth[a][vc];
+          *(bf16x8*)(PL.lo + (16 * a + l16) * LP + 32 * vc + 8 * lg) = vtl[a][vc];
+        }
+      }
+    }
+    __syncthreads();  // rows 0..31 visible
 #pragma unroll
     for (int a = 0; a < 2; ++a) {
       const int t = 2 * tp + a;
-      bf16x8 pth[VC], ptl[VC], vth[VC], vtl[VC];
+      bf16x8 pth[VC], ptl[VC];
 #pragma unroll
       for (int vc = 0; vc < VC; ++vc) {
         pth[vc] = PP.hi8(16 * t + l16, 32 * vc + 8 * lg);
         ptl[vc] = PP.lo8(16 * t + l16, 32 * vc + 8 * lg);
-        const int j = 16 * t + l16, v0 = 32 * vc + 8 * lg;
-        load_split8(Rvn, (j < nval && v0 < V) ? ((uint32_t)j * rowV + v0) * 4u : kOOB, vth[vc], vtl[vc]);
       }
 #pragma unroll
       for (int J = 0; J < 4; ++J) {
         darh[a][J] = darl[a][J] = dach[a][J] = dacl[a][J] = make_uint2(0u, 0u);
         if (J <= t) {
           f32x4 s = {0.f, 0.f, 0.f, 0.f};
-          const int j = 16 * J + l16;
 #pragma unroll
           for (int vc = 0; vc < VC; ++vc) {
-            const int v0 = 32 * vc + 8 * lg;
             bf16x8 ah, al;
-            if (J == t) { ah = vth[vc]; al = vtl[vc]; }
-            else load_split8(Rvn, (j < nval && v0 < V) ? ((uint32_t)j * rowV + v0) * 4u : kOOB, ah, al);
+            if (J == t) { ah = vth[a][vc]; al = vtl[a][vc]; }
+            else if (J == 2 * tp) { ah = vth[0][vc]; al = vtl[0][vc]; }
+            else { ah = PL.hi8(16 * J + l16, 32 * vc + 8 * lg); al = PL.lo8(16 * J + l16, 32 * vc + 8 * lg); }
             s = mma<true, true>(s, ah, al, pth[vc], ptl[vc]);
           }
           // s = sum_v vn[j][v] P[i][v] at (j = 16J + 4lg + r, i = 16t + l16)
@@ -195,7 +287,7 @@ __global__ __launch_bounds__(256, 2) void kda_wy_kernel(KdaWyParams p) {
 #pragma unroll
           for (int vc = 0; vc < VC; ++vc)
             s = mma<true, true>(s, PP.hi8(16 * J + l16, 32 * vc + 8 * lg), PP.lo8(16 * J + l16, 32 * vc + 8 * lg),
-                                vth[vc], vtl[vc]);
+                                vth[a][vc], vtl[a][vc]);
           // s = sum_v P[i][v] vn[j][v] at (i = 16J + 4lg + r, j = 16t + l16)
           const int j = 16 * t + l16;
 #pragma unroll
