@@ -250,6 +250,20 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
       hraw[vc][0] = bld128(Rh, o, 0);
       hraw[vc][1] = bld128(Rh, o, 16);
     }
+    // ---- the pass's WY parts of dk / dg (fp32-v instantiation only, the one the KDA
+    // backward uses): requested now, added in the epilogue
+    constexpr bool kEarlyAdd = !kScalarGate;
+    uint4 kadd[2], gadd[2];
+    if constexpr (kEarlyAdd) {
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const int tok = 16 * (2 * rh + a) + l16;
+        const int kc = cb + 16 * kb + 4 * lg;
+        const uint32_t o = (kc < K && tok < nval) ? ((uint32_t)tok * rowK + kc) * 4u : kOOB;
+        kadd[a] = bld128(Rdka, o, 0);
+        gadd[a] = bld128(Rdga, o, 0);
+      }
+    }
     // ---- gate cumsum of the pass (thread: channel ch, rows 8sg..8sg+7)
     float G[8];
 #pragma unroll
@@ -419,9 +433,10 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
           dgr[a][r] = qt * X[a][r] - kt * Wt[a][r];
         }
       }
-      if (p.dk_add) {
+      if (kEarlyAdd || p.dk_add) {
         float ka[4];
-        unpack4(bld128(Rdka, ok ? off * 4u : kOOB, 0), ka);
+        if constexpr (kEarlyAdd) unpack4(kadd[a], ka);
+        else unpack4(bld128(Rdka, ok ? off * 4u : kOOB, 0), ka);
 #pragma unroll
         for (int r = 0; r < 4; ++r) dkv[r] += ka[r];
       }
@@ -460,7 +475,8 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
         const bool ok = chok && tok < nval;
         const uint32_t off = (uint32_t)tok * rowK + kc;
         float ga[4] = {0.f, 0.f, 0.f, 0.f};
-        if (p.dg_add) unpack4(bld128(Rdga, ok ? off * 4u : kOOB, 0), ga);
+        if constexpr (kEarlyAdd) unpack4(gadd[a], ga);
+        else if (p.dg_add) unpack4(bld128(Rdga, ok ? off * 4u : kOOB, 0), ga);
         bst128(Rdg, make_uint4(__float_as_uint(dgr[a][0] + add[0] + ga[0]), __float_as_uint(dgr[a][1] + add[1] + ga[1]),
                                __float_as_uint(dgr[a][2] + add[2] + ga[2]), __float_as_uint(dgr[a][3] + add[3] + ga[3])),
                ok ? off * 4u : kOOB, 0);
