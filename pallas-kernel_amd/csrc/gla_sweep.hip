@@ -527,54 +527,45 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     // D tiles (P, R) on the causal side: lane holds D[16P+4lg+r][16R+l16]
     const float dsc = FWD_DELTA ? 1.f : scale;   // the delta forward folds scale into X
     uint2 dh[4], dl[4];
-    if constexpr (SHARED_D) {
-      // tile t = Rc (Rc + 1) / 2 + Pc with Pc <= Rc in causal order (Rc = R, Pc = P forward;
-      // 3 - R, 3 - P reverse); wave w computes tiles w and w + 8
+    // causal D tile t = Rc (Rc + 1) / 2 + Pc, Pc <= Rc (Rc = R, Pc = P forward; 3 - R, 3 - P
+    // reverse), packed bf16 hi / lo per lane; three independent MFMA chains (lo.hi, hi.lo,
+    // hi.hi), the fragments of step kc + 1 read before the products of step kc
+    auto dtile = [&](int t) -> uint4 {
+      const int Rc = t >= 6 ? 3 : (t >= 3 ? 2 : (t >= 1 ? 1 : 0));
+      const int Pc = t - Rc * (Rc + 1) / 2;
+      const int Rt = REV ? 3 - Rc : Rc, Pt = REV ? 3 - Pc : Pc;
+      f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0, a2 = a0;
+      bf16x8 fz[2][2], fx[2][2];
+      auto ld = [&](int kc, int b) {
+        fz[b][0] = PZ.hi8(16 * Pt + l16, 32 * kc + 8 * lg);
+        fz[b][1] = PZ.lo8(16 * Pt + l16, 32 * kc + 8 * lg);
+        fx[b][0] = PX.hi8(16 * Rt + l16, 32 * kc + 8 * lg);
+        fx[b][1] = PX.lo8(16 * Rt + l16, 32 * kc + 8 * lg);
+      };
+      ld(0, 0);
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int t = wave + 8 * u;
-        if (t < 10) {
-          const int Rc = t >= 6 ? 3 : (t >= 3 ? 2 : (t >= 1 ? 1 : 0));
-          const int Pc = t - Rc * (Rc + 1) / 2;
-          const int Rt = REV ? 3 - Rc : Rc, Pt = REV ? 3 - Pc : Pc;
-          // three independent chains (lo.hi, hi.lo, hi.hi); the fragments of step kc + 1 are
-          // read before the products of step kc
-          f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0, a2 = a0;
-          bf16x8 fz[2][2], fx[2][2];
-          auto ld = [&](int kc, int b) {
-            fz[b][0] = PZ.hi8(16 * Pt + l16, 32 * kc + 8 * lg);
-            fz[b][1] = PZ.lo8(16 * Pt + l16, 32 * kc + 8 * lg);
-            fx[b][0] = PX.hi8(16 * Rt + l16, 32 * kc + 8 * lg);
-            fx[b][1] = PX.lo8(16 * Rt + l16, 32 * kc + 8 * lg);
-          };
-          ld(0, 0);
-#pragma unroll
-          for (int kc = 0; kc < KP / 32; ++kc) {
-            const int b = kc & 1;
-            if (kc + 1 < KP / 32) ld(kc + 1, b ^ 1);
-            a0 = mfma(fz[b][1], fx[b][0], a0);
-            a1 = mfma(fz[b][0], fx[b][1], a1);
-            a2 = mfma(fz[b][0], fx[b][0], a2);
-          }
-          f32x4 acc;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[r] = (a0[r] + a1[r]) + a2[r];
-          const int rr = 16 * Rt + l16;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int pp = 16 * Pt + 4 * lg + r;
-            const bool keep = REV ? (pp >= rr) : (pp <= rr);
-            acc[r] = keep ? acc[r] * dsc : 0.f;
-          }
-          uint2 th, tl;
-          acc_to_bf16x4(acc, th, tl);
-          sDt[t * 64 + lane] = make_uint4(th.x, th.y, tl.x, tl.y);
-        }
+      for (int kc = 0; kc < KP / 32; ++kc) {
+        const int b = kc & 1;
+        if (kc + 1 < KP / 32) ld(kc + 1, b ^ 1);
+        a0 = mfma(fz[b][1], fx[b][0], a0);
+        a1 = mfma(fz[b][0], fx[b][1], a1);
+        a2 = mfma(fz[b][0], fx[b][0], a2);
       }
-      // the state update reads only the Z^T / Y^T planes: it fills the wait for the D tiles
-      state_update();
-      __syncthreads();  // B3: D tiles visible
-      load_x();
+      f32x4 acc;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = (a0[r] + a1[r]) + a2[r];
+      const int rr = 16 * Rt + l16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int pp = 16 * Pt + 4 * lg + r;
+        const bool keep = REV ? (pp >= rr) : (pp <= rr);
+        acc[r] = keep ? acc[r] * dsc : 0.f;
+      }
+      uint2 th, tl;
+      acc_to_bf16x4(acc, th, tl);
+      return make_uint4(th.x, th.y, tl.x, tl.y);
+    };
+    auto read_d = [&](const uint4* base) {
 #pragma unroll
       for (int P = 0; P < 4; ++P) {
         dh[P] = make_uint2(0u, 0u);
@@ -582,10 +573,32 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
         const bool live = REV ? (P >= R) : (P <= R);
         if (live) {
           const int Rc = REV ? 3 - R : R, Pc = REV ? 3 - P : P;
-          const uint4 x = sDt[(Rc * (Rc + 1) / 2 + Pc) * 64 + lane];
+          const uint4 x = base[(Rc * (Rc + 1) / 2 + Pc) * 64 + lane];
           dh[P] = make_uint2(x.x, x.y);
           dl[P] = make_uint2(x.z, x.w);
         }
+      }
+    };
+    // forward delta rule (no LDS left for the shared tiles): the D tiles are computed now, in
+    // the same even split (wave w: tiles w, w + 8), and handed over through the Z plane once
+    // the v_new phase below has passed B3 (Z is not read after the D tiles)
+    uint4 dz[2];
+    if constexpr (SHARED_D) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int t = wave + 8 * u;
+        if (t < 10) sDt[t * 64 + lane] = dtile(t);
+      }
+      // the state update reads only the Z^T / Y^T planes: it fills the wait for the D tiles
+      state_update();
+      __syncthreads();  // B3: D tiles visible
+      load_x();
+      read_d(sDt);
+    } else if constexpr (FWD_DELTA) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int t = wave + 8 * u;
+        if (t < 10) dz[u] = dtile(t);
       }
     } else {
 #pragma unroll
@@ -662,7 +675,15 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
         }
         put_n<true, 4>(PYt, 16 * nn + l16, 16 * R + 4 * lg, vn);
       }
-      __syncthreads();  // B3: v_new^T plane complete
+      __syncthreads();  // B3: v_new^T plane complete; no wave reads the Z plane any more
+      uint4* zD = (uint4*)sZ;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int t = wave + 8 * u;
+        if (t < 10) zD[t * 64 + lane] = dz[u];
+      }
+      __syncthreads();  // B3b: D tiles visible
+      read_d(zD);
     }
 
     if constexpr (REV_DELTA) {
