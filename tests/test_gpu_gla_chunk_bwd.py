@@ -119,3 +119,28 @@ def test_g_gamma_gradient_reduces(cuda_device):
     assert rel(host(o), ro) < 1e-4
     ref = O.chunk_gla_bwd(d["q"], d["k"], d["v"], gfull, K ** -0.5, None, d["do"], None)
     assert rel(host(gg.grad), ref[3].sum(axis=(0, 1))) < 1e-4
+
+
+def test_many_sequences(cuda_device):
+    """300 varlen sequences of 1..40 tokens (more than the sweeps' in-kernel longest-first
+    ranking covers): forward and backward against the oracle."""
+    from tops.ops.gla import chunk_gla
+    rng = np.random.default_rng(300)
+    lens = rng.integers(1, 41, size=300)
+    cu = [0] + [int(x) for x in np.cumsum(lens)]
+    B, T, H, K, V = 1, cu[-1], 1, 32, 32
+    d = gla_inputs(B, T, H, K, V, 300, gate_div=4.0, h0=True, N=300, grads=True)
+    q, k, v = (to_dev(d[x], torch.float32, cuda_device).requires_grad_() for x in "qkv")
+    g = to_dev(d["g"], torch.float32, cuda_device).requires_grad_()
+    h0 = to_dev(d["h0"], torch.float32, cuda_device).requires_grad_()
+    o, ht = chunk_gla(q, k, v, g, initial_state=h0, output_final_state=True, cu_seqlens=cu)
+    torch.autograd.backward((o, ht), (to_dev(d["do"], torch.float32, cuda_device),
+                                      to_dev(d["dht"], torch.float32, cuda_device)))
+    ro, rht = O.chunk_gla(d["q"], d["k"], d["v"], d["g"], initial_state=d["h0"],
+                          output_final_state=True, cu_seqlens=cu)
+    ref = O.chunk_gla_bwd(d["q"], d["k"], d["v"], d["g"], K ** -0.5, d["h0"], d["do"], d["dht"],
+                          chunk_size=64, cu_seqlens=cu)
+    got = [o, ht, q.grad, k.grad, v.grad, g.grad, h0.grad]
+    want = [ro, rht] + list(ref)
+    for name, a, b in zip(("o", "ht", "dq", "dk", "dv", "dg", "dh0"), got, want):
+        assert rel(host(a), b) < 1e-4, name

@@ -153,3 +153,17 @@ def test_automatic_split_of_one_long_sequence(cuda_device, split_mode):
         e = rel(got[x], ref[x])
         print(f"{x}={e:.2e}", end=" ")
         assert e < 2e-3, (x, e)
+
+
+def test_more_segments_than_the_dispatch_ranking(cuda_device, split_mode):
+    """301 one-chunk segments of one sequence: the segment sweep runs with more sequences
+    than its in-kernel longest-first ranking covers (256) and the combine scans 300 states."""
+    B, T, H, K, V = 1, 64 * 300 + 17, 1, 32, 32
+    split_mode(1)
+    d = gla_inputs(B, T, H, K, V, seed=301, gate_div=64.0, h0=True, grads=True)
+    got = _gla(d, None, torch.float32, cuda_device)
+    ref = _gla_oracle(d, None, torch.float32, None)
+    for x in got:
+        e = rel(got[x], ref[x])
+        print(f"{x}={e:.2e}", end=" ")
+        assert e < 1e-4, (x, e)
