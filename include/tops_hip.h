@@ -152,17 +152,19 @@ int tops_simple_gla_chunk_bwd_dqkg(const void* q, const void* k, const void* v, 
 
 /* Sequence-parallel sweeps (long or few sequences on one device).  The caller cuts each
  * sequence at chunk boundaries into segments, listed in token order as a varlen layout over
- * the same tokens (cu_seqlens of the segments, B == 1), and runs:
- *   1. tops_chunk_state_pass over a list of N segments, segment i = rows
- *      [seg_start[i], seg_end[i]): its end state from a zero state, s_loc [N,H,K,V] fp32,
- *      and its summed log2 gates, dec [N,H,K] fp32.  reverse != 0: the state-gradient
- *      sweep, z = q, y = dO; else z = k, y = v.  Only the segments that pass a state on
- *      are needed: all but the last of a sequence (forward) or all but the first (reverse).
+ * the same tokens (cu_seqlens of the segments, B == 1), and runs per sweep direction:
+ *   1. tops_chunk_state_pass over a list of N pieces, piece i = rows [seg_start[i],
+ *      seg_end[i]) (chunk-aligned except at a sequence end): its end state from a zero
+ *      state, s_loc [N,H,K,V] fp32, and its summed log2 gates, dec [N,H,K] fp32.
+ *      reverse != 0: the state-gradient sweep, z = q, y = dO; else z = k, y = v.  The pieces
+ *      cover every segment that hands a state on (all but the last of a sequence forward,
+ *      all but the first in reverse), possibly cut finer than the segments so the pass
+ *      itself fills the device.
  *   2. tops_chunk_state_combine: real sequence n owns the segments
- *      [seg_first[n], seg_first[n+1]) and the state-pass entries
- *      [st_first[n], st_first[n+1]) (one fewer, same token order).  Writes every segment's
- *      incoming state init [Nseg,H,K,V] from s_in (h0, or dht when reverse, of the real
- *      sequences, [Nreal,H,K,V], or NULL for zero).
+ *      [seg_first[n], seg_first[n+1]) and the pieces [st_first[n], st_first[n+1]), stored in
+ *      sweep order; after piece e the running state enters segment st_dst[e] (-1: none).
+ *      Writes every segment's incoming state init [Nseg,H,K,V] from s_in (h0, or dht when
+ *      reverse, of the real sequences, [Nreal,H,K,V], or NULL for zero).
  *   3. the usual chunk sweep over the segments with h0 (dht) = init and chunk_offsets = each
  *      segment's first global chunk; its final states per segment give ht (last segment of
  *      each sequence) and dh0 (first segment).
@@ -176,7 +178,8 @@ int tops_chunk_state_pass(const void* z, const void* y, const float* g, int gate
                           float scale, int reverse, void* stream);
 int tops_chunk_state_combine(const float* s_loc, const float* dec, const float* s_in,
                              float* init, const int32_t* seg_first, const int32_t* st_first,
-                             int Nreal, int H, int K, int V, int reverse, void* stream);
+                             const int32_t* st_dst, int Nreal, int H, int K, int V, int reverse,
+                             void* stream);
 
 /* Fused recurrent GLA forward: the per-token recurrence
  *   h_t = h_{t-1} * exp(gk_t)[:,None] * exp(gv_t)[None,:] + k_t v_t^T,  o_t = h_t^T (scale q_t)

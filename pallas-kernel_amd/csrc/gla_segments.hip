@@ -15,15 +15,17 @@
 
 namespace tops {
 
-// One thread per (sequence, head, K row, 4 V columns): walks the segments of its sequence in
-// sweep order and writes each segment's incoming state.  Sequence n owns the segments
-// [seg_first[n], seg_first[n+1]) of the full list and, for all of them but the last in sweep
-// order, the state-pass results [st_first[n], st_first[n+1]) in the same token order.
+// One thread per (sequence, head, K row, 4 V columns): walks the state-pass entries of its
+// sequence in sweep order, carrying the state across them, and writes the incoming state of
+// every segment.  Sequence n owns the segments [seg_first[n], seg_first[n+1]) of the full list
+// and the entries [st_first[n], st_first[n+1]) (stored in sweep order); after entry e the
+// running state enters segment st_dst[e] (or no segment: -1, when the entry ends inside one).
 __global__ void __launch_bounds__(256)
 state_combine_kernel(const float* __restrict__ s_loc, const float* __restrict__ dec,
                      const float* __restrict__ s_in, float* __restrict__ init,
                      const int32_t* __restrict__ seg_first, const int32_t* __restrict__ st_first,
-                     int Nreal, int H, int K, int V, int reverse) {
+                     const int32_t* __restrict__ st_dst, int Nreal, int H, int K, int V,
+                     int reverse) {
   const int V4 = V >> 2;
   const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   const long long per_seq = (long long)H * K * V4;
@@ -35,21 +37,17 @@ state_combine_kernel(const float* __restrict__ s_loc, const float* __restrict__ 
   const size_t hkv = (size_t)hk * V + 4 * v4;            // offset inside one [H,K,V] state
   const size_t st = (size_t)H * K * V;
   float4 S = s_in ? *(const float4*)(s_in + (size_t)n * st + hkv) : make_float4(0.f, 0.f, 0.f, 0.f);
-  const int j0 = seg_first[n], m = seg_first[n + 1] - j0, e0 = st_first[n];
-  for (int i = 0; i < m; ++i) {
-    // i-th segment in sweep order; its state-pass entry (token order, the first segment in
-    // sweep order has none)
-    const int j = reverse ? m - 1 - i : i;
-    *(float4*)(init + (size_t)(j0 + j) * st + hkv) = S;
-    if (i + 1 < m) {
-      const int e = e0 + (reverse ? j - 1 : j);
-      const float a = exp2f(dec[(size_t)e * H * K + hk]);
-      const float4 l = *(const float4*)(s_loc + (size_t)e * st + hkv);
-      S.x = a * S.x + l.x;
-      S.y = a * S.y + l.y;
-      S.z = a * S.z + l.z;
-      S.w = a * S.w + l.w;
-    }
+  const int j_first = reverse ? seg_first[n + 1] - 1 : seg_first[n];
+  *(float4*)(init + (size_t)j_first * st + hkv) = S;
+  for (int e = st_first[n]; e < st_first[n + 1]; ++e) {
+    const float a = exp2f(dec[(size_t)e * H * K + hk]);
+    const float4 l = *(const float4*)(s_loc + (size_t)e * st + hkv);
+    S.x = a * S.x + l.x;
+    S.y = a * S.y + l.y;
+    S.z = a * S.z + l.z;
+    S.w = a * S.w + l.w;
+    const int j = st_dst[e];
+    if (j >= 0) *(float4*)(init + (size_t)j * st + hkv) = S;
   }
 }
 
@@ -90,9 +88,10 @@ extern "C" int tops_chunk_state_pass(const void* z, const void* y, const float* 
 
 extern "C" int tops_chunk_state_combine(const float* s_loc, const float* dec, const float* s_in,
                                         float* init, const int32_t* seg_first,
-                                        const int32_t* st_first, int Nreal, int H, int K, int V,
-                                        int reverse, void* stream) {
-  if (!init || !seg_first || !st_first)
+                                        const int32_t* st_first, const int32_t* st_dst,
+                                        int Nreal, int H, int K, int V, int reverse,
+                                        void* stream) {
+  if (!init || !seg_first || !st_first || !st_dst)
     return tops_set_error(TOPS_ERR_NULL, "chunk_state_combine: null tensor");
   if (Nreal <= 0 || H <= 0 || K <= 0 || V <= 0 || (V % 4))
     return tops_set_error(TOPS_ERR_SHAPE, "chunk_state_combine: need positive sizes, V % 4 == 0");
@@ -100,8 +99,8 @@ extern "C" int tops_chunk_state_combine(const float* s_loc, const float* dec, co
   const long long blocks = (n + 255) / 256;
   if (blocks > 0x7fffffffLL) return tops_set_error(TOPS_ERR_SHAPE, "chunk_state_combine: too large");
   hipLaunchKernelGGL(state_combine_kernel, dim3((unsigned)blocks), dim3(256), 0,
-                     (hipStream_t)stream, s_loc, dec, s_in, init, seg_first, st_first, Nreal, H, K,
-                     V, reverse);
+                     (hipStream_t)stream, s_loc, dec, s_in, init, seg_first, st_first, st_dst,
+                     Nreal, H, K, V, reverse);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   return TOPS_OK;

@@ -41,7 +41,7 @@ SIGNATURES = {
     "tops_simple_gla_chunk_bwd_dh": [_vp] * 11 + [_i32] * 7 + [_f32, _vp],
     "tops_simple_gla_chunk_bwd_dqkg": [_vp] * 14 + [_i32] * 8 + [_f32, _vp],
     "tops_chunk_state_pass": [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp] + [_i32] * 6 + [_f32, _i32, _vp],
-    "tops_chunk_state_combine": [_vp] * 6 + [_i32] * 5 + [_vp],
+    "tops_chunk_state_combine": [_vp] * 7 + [_i32] * 5 + [_vp],
 }
 
 _lib = None

@@ -40,24 +40,23 @@ def _gate_ptrs(gate):
 
 def _segment_states(z, y, gate, s_in, scale, sp, reverse: bool):
     """Incoming state of every segment of a sequence-parallel sweep: the state pass over the
-    segments that hand a state on, then the scan over each sequence's segments."""
+    pieces that hand a state on, then the scan over each sequence's pieces."""
     B, T, H, K = z.shape
     V = y.shape[-1]
     mode, gt = gate
     dev = z.device
+    pc = sp.rev if reverse else sp.fwd
     s_loc = dec = None
-    if sp.n_state:
-        s_loc = torch.empty(sp.n_state, H, K, V, device=dev, dtype=torch.float32)
-        dec = torch.empty(sp.n_state, H, K, device=dev, dtype=torch.float32)
-        start, end = (sp.rev_start_dev, sp.rev_end_dev) if reverse else \
-            (sp.fwd_start_dev, sp.fwd_end_dev)
+    if pc.n:
+        s_loc = torch.empty(pc.n, H, K, V, device=dev, dtype=torch.float32)
+        dec = torch.empty(pc.n, H, K, device=dev, dtype=torch.float32)
         N.call("tops_chunk_state_pass", N.ptr(z), N.ptr(y), N.ptr(gt), _GATE_CODE[mode],
-               N.ptr(s_loc), N.ptr(dec), N.ptr(start), N.ptr(end), B * T, H, K, V, sp.n_state,
-               N.dtype_code(z.dtype), float(scale), int(reverse), N.stream())
+               N.ptr(s_loc), N.ptr(dec), N.ptr(pc.start_dev), N.ptr(pc.end_dev), B * T, H, K, V,
+               pc.n, N.dtype_code(z.dtype), float(scale), int(reverse), N.stream())
     init = torch.empty(sp.Nv, H, K, V, device=dev, dtype=torch.float32)
     N.call("tops_chunk_state_combine", N.ptr(s_loc), N.ptr(dec), N.ptr(s_in), N.ptr(init),
-           N.ptr(sp.seg_first_dev), N.ptr(sp.st_first_dev), len(sp.seg_first) - 1, H, K, V,
-           int(reverse), N.stream())
+           N.ptr(sp.seg_first_dev), N.ptr(pc.first_dev), N.ptr(pc.dst_dev),
+           len(sp.seg_first) - 1, H, K, V, int(reverse), N.stream())
     return init
 
 

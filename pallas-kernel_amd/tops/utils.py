@@ -122,6 +122,7 @@ class ChunkPlan:
 # tops_chunk_state_combine in include/tops_hip.h).
 _SPLIT = {"mode": None}   # None: automatic; 0: never split; k > 0: segments of k chunks
 MIN_SEG_CHUNKS = 8        # shortest segment worth its state pass
+MIN_PIECE_CHUNKS = 4      # shortest state-pass piece
 SPLIT_SLACK = 1.25        # split a sequence only when it is this much above the target
 
 
@@ -138,15 +139,23 @@ def _device_cus(device) -> int:
 
 
 class SegPlan:
-    """Segments of the sequences of one ChunkPlan, in token order (host arrays and their
-    device copies):
+    """Segments of the sequences of one ChunkPlan, in token order, and the state-pass pieces
+    of both sweep directions (host arrays and their device copies):
       cu_dev [Nv+1]        segment boundaries (a varlen layout over the same tokens)
       offsets_dev [Nv+1]   first global chunk of each segment (the plan's chunk numbering)
       seg_first_dev [N+1]  segments of real sequence n: [seg_first[n], seg_first[n+1])
-      st_first_dev [N+1]   its state-pass entries (one fewer than its segments)
-      fwd_start/fwd_end    rows of the segments that pass a state forward (all but the last
-                           of a sequence), rev_start/rev_end the same for the reverse sweep
-      last_dev, first_dev  [N] last / first segment of every real sequence"""
+      last_dev, first_dev  [N] last / first segment of every real sequence
+      fwd / rev            a Pieces: the rows each state-pass workgroup sweeps, grouped per
+                           sequence in sweep order, and the segment each piece hands into
+    A piece is a segment that hands a state on (all but the last of a sequence forward, all
+    but the first in reverse), cut into ``sub``-chunk parts when the pass alone would leave
+    the device idle."""
+
+    class Pieces:
+        def __init__(self, start, end, first, dst):
+            self.n = len(start)
+            self.start, self.end = np.array(start, np.int32), np.array(end, np.int32)
+            self.first, self.dst = np.array(first, np.int32), np.array(dst, np.int32)
 
     @staticmethod
     def split_counts(chunks: np.ndarray, slots: int, mode) -> np.ndarray:
@@ -160,6 +169,12 @@ class SegPlan:
         m = -(-chunks // target)
         return np.where(chunks > SPLIT_SLACK * target, m, 1)
 
+    @staticmethod
+    def piece_chunks(state_chunks: int, wgs_per_piece: int, cus: int) -> int:
+        """Piece length (chunks) so that the state pass is about one round of workgroups on
+        `cus` CUs (one state-pass workgroup per CU), at least MIN_PIECE_CHUNKS."""
+        return max(-(-state_chunks * wgs_per_piece // max(cus, 1)), MIN_PIECE_CHUNKS)
+
     @classmethod
     def build(cls, plan: "ChunkPlan", H: int, V: int):
         cu = plan.cu_host.astype(np.int64)
@@ -167,46 +182,85 @@ class SegPlan:
         C = plan.C
         chunks = -(-lens // C)
         mode = _SPLIT["mode"]
-        slots = 1
-        if mode is None:
-            slots = _device_cus(plan.device) // max(H * cdiv(V, 64), 1)
+        if mode == 0:
+            return None
+        per = max(H * cdiv(V, 64), 1)
+        cus = _device_cus(plan.device)
+        slots = cus // per if mode is None else 1
         m = cls.split_counts(chunks, slots, mode)
         if int(m.max()) <= 1:
             return None
-        return cls(cu, chunks, m, C, plan.device)
+        return cls(cu, chunks, m, C, plan.device, per=per, cus=cus)
 
-    def __init__(self, cu, chunks, m, C, device):
+    @staticmethod
+    def _cut(lo_chunk: int, n_chunks: int, sub: int):
+        """[lo, hi) chunk ranges of near-equal parts of at most about `sub` chunks."""
+        k = max(1, -(-n_chunks // sub))
+        base, rem = divmod(n_chunks, k)
+        out, c = [], lo_chunk
+        for i in range(k):
+            sz = base + (1 if i < rem else 0)
+            out.append((c, c + sz))
+            c += sz
+        return out
+
+    def __init__(self, cu, chunks, m, C, device, per=None, cus=None):
         coff = np.concatenate([[0], np.cumsum(chunks)])
         starts, offs, seg_first = [], [], [0]
-        fwd, rev, st_first = [], [], [0]
+        seq_bounds = []                       # per sequence: segment boundaries in chunks
         for n in range(len(chunks)):
             base, rem = divmod(int(chunks[n]), int(m[n]))
             sizes = [base + (1 if j < rem else 0) for j in range(int(m[n]))]
-            c0 = 0
-            bounds = []
+            cb = [0]
             for sz in sizes:
-                bounds.append(int(cu[n]) + C * c0)
-                offs.append(int(coff[n]) + c0)
-                c0 += sz
-            bounds.append(int(cu[n + 1]))
-            starts.extend(bounds[:-1])
+                cb.append(cb[-1] + sz)
+            seq_bounds.append(cb)
+            for j in range(len(sizes)):
+                starts.append(int(cu[n]) + C * cb[j])
+                offs.append(int(coff[n]) + cb[j])
             seg_first.append(seg_first[-1] + len(sizes))
-            st_first.append(st_first[-1] + len(sizes) - 1)
-            for j in range(len(sizes) - 1):
-                fwd.append((bounds[j], bounds[j + 1]))
-                rev.append((bounds[j + 1], bounds[j + 2]))
+        # piece length: one round of state-pass workgroups (pieces = segments when unknown)
+        state_chunks = sum(cb[-1] - (cb[-1] - cb[-2]) for cb in seq_bounds if len(cb) > 2)
+        sub = self.piece_chunks(state_chunks, per, cus) if per and cus else None
+
+        def row(n, c):                        # token row of chunk boundary c of sequence n
+            return min(int(cu[n]) + C * c, int(cu[n + 1]))
+
+        fwd = ([], [], [0], [])
+        rev = ([], [], [0], [])
+        for n, cb in enumerate(seq_bounds):
+            j0, ms = seg_first[n], len(cb) - 1
+            # forward: segments 0..ms-2, token order; the piece ending at boundary j + 1
+            # hands into segment j + 1
+            for j in range(ms - 1):
+                parts = self._cut(cb[j], cb[j + 1] - cb[j], sub or (cb[j + 1] - cb[j]))
+                for i, (a, b) in enumerate(parts):
+                    fwd[0].append(row(n, a))
+                    fwd[1].append(row(n, b))
+                    fwd[3].append(j0 + j + 1 if i == len(parts) - 1 else -1)
+            fwd[2].append(len(fwd[0]))
+            # reverse: segments ms-1..1, from the end of the sequence; the piece starting at
+            # boundary j hands into segment j - 1
+            for j in range(ms - 1, 0, -1):
+                parts = self._cut(cb[j], cb[j + 1] - cb[j], sub or (cb[j + 1] - cb[j]))
+                for i, (a, b) in enumerate(reversed(parts)):
+                    rev[0].append(row(n, a))
+                    rev[1].append(row(n, b))
+                    rev[3].append(j0 + j - 1 if i == len(parts) - 1 else -1)
+            rev[2].append(len(rev[0]))
+        self.sub = sub
+        self.fwd = self.Pieces(*fwd)
+        self.rev = self.Pieces(*rev)
         self.Nv = len(starts)
-        self.n_state = len(fwd)
         cu_v = np.array(starts + [int(cu[-1])], np.int32)
         offs_v = np.array(offs + [int(coff[-1])], np.int32)
         sf = np.array(seg_first, np.int32)
         self.seg_first = sf
         self.cu_host = cu_v
-        fw = np.array(fwd, np.int32).reshape(-1, 2)
-        rv = np.array(rev, np.int32).reshape(-1, 2)
-        parts = [cu_v, offs_v, sf, np.array(st_first, np.int32), fw[:, 0], fw[:, 1], rv[:, 0],
-                 rv[:, 1], sf[:-1], sf[1:] - 1]
-        (self.cu_dev, self.offsets_dev, self.seg_first_dev, self.st_first_dev,
-         self.fwd_start_dev, self.fwd_end_dev, self.rev_start_dev, self.rev_end_dev,
-         self.first_dev, self.last_dev) = _split_views(
-            _upload(np.concatenate(parts), device), [len(x) for x in parts])
+        parts = [cu_v, offs_v, sf, sf[:-1], sf[1:] - 1]
+        for pc in (self.fwd, self.rev):
+            parts += [pc.start, pc.end, pc.first, pc.dst]
+        views = _split_views(_upload(np.concatenate(parts), device), [len(x) for x in parts])
+        (self.cu_dev, self.offsets_dev, self.seg_first_dev, self.first_dev, self.last_dev) = views[:5]
+        for pc, v in ((self.fwd, views[5:9]), (self.rev, views[9:13])):
+            pc.start_dev, pc.end_dev, pc.first_dev, pc.dst_dev = v

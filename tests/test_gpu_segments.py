@@ -74,7 +74,7 @@ def test_chunk_gla_segments(cfg, dtype, cuda_device, split_mode):
     d = gla_inputs(B, T, H, K, V, seed=T + H, gate_div=64.0, h0=True, N=n, grads=True)
     split_mode(cfg["split"])
     sp = ChunkPlan(B, T, cu, cuda_device).segments(H, V)
-    assert sp is not None and sp.n_state > 0
+    assert sp is not None and sp.fwd.n > 0 and sp.rev.n > 0
     got = _gla(d, cu, dtype, cuda_device, cfg.get("scale"))
     split_mode(0)
     whole = _gla(d, cu, dtype, cuda_device, cfg.get("scale"))
