@@ -249,6 +249,58 @@ int tops_kda_chunk_bwd(const void* q, const void* k, const void* v, const float*
                        int B, int T, int H, int K, int V, int N, int dtype, float scale,
                        void* stream);
 
+/* KDA gate activation modes. */
+#define TOPS_KDA_GATE_NONE 0        /* gate already activated (cumsum only) */
+#define TOPS_KDA_GATE_SOFTPLUS 1    /* y = -exp(A_log[h]) * softplus(g + dt_bias[h, k]) */
+#define TOPS_KDA_GATE_LOWER_BOUND 2 /* y = lower_bound * sigmoid(exp(A_log[h]) * (g + dt_bias[h, k])) */
+
+/* KDA gate activation, y [rows,H,K] fp32 from the raw gate g [rows,H,K] (dtype g_dtype,
+ * rows = B*T).  A_log [A_heads] fp32 (A_heads divides H; head h reads A_log[h / (H/A_heads)]);
+ * dt_bias [bias_heads*K] fp32 or NULL, bias_heads = A_heads or H.  K % 4 == 0.
+ * gate_mode: TOPS_KDA_GATE_SOFTPLUS or TOPS_KDA_GATE_LOWER_BOUND.
+ * Replaces fused_kda_gate / kda_gate_fwd / naive_kda_gate / naive_kda_lowerbound_gate
+ * (tops/cpu/ops/kda/gate.py:60-115, 161-176) and the head broadcast of
+ * _expand_headwise_params (tops/cpu/ops/kda/gate.py:20-57). */
+int tops_kda_gate_fwd(const void* g, int g_dtype, const float* A_log, const float* dt_bias,
+                      float* y, int rows, int H, int K, int A_heads, int bias_heads,
+                      int gate_mode, float lower_bound, void* stream);
+
+/* Chunk-local cumulative sum of (optionally activated) gates, out [B,T,H,K] fp32:
+ * out[t] = scale * sum over the tokens of t's chunk up to t of act(g).  Chunks of
+ * chunk_size tokens tile each sequence from its start (varlen: cu_seqlens / chunk_offsets /
+ * chunk_map of that chunk size, as for tops_gla_chunk_bwd; total_chunks = B*ceil(T/C) or
+ * the varlen total).  gate_mode TOPS_KDA_GATE_NONE with scale = 1/ln 2 replaces
+ * tops.ops.kda.gate.kda_gate_chunk_cumsum (tops/ops/kda/gate.py:19-51); the activated modes
+ * replace the FLA-form kda_gate_chunk_cumsum (tops/cpu/ops/kda/gate.py:179-204). */
+int tops_kda_gate_chunk_cumsum(const void* g, int g_dtype, const float* A_log,
+                               const float* dt_bias, float* out, const int32_t* cu_seqlens,
+                               const int32_t* chunk_offsets, const int32_t* chunk_map,
+                               int total_chunks, int B, int T, int H, int K, int A_heads,
+                               int bias_heads, int chunk_size, int gate_mode, float lower_bound,
+                               float scale, void* stream);
+
+/* Floats of the workspace tops_kda_gate_bwd needs (per-workgroup partials). */
+int64_t tops_kda_gate_bwd_workspace(int rows, int H, int K);
+
+/* KDA gate backward: dg [rows,H,K] (g_dtype), dA [A_heads] and dbias [bias_heads*K] (fp32)
+ * from dyg [rows,H,K] fp32.  dA / dbias are summed over tokens and over the heads that share
+ * a parameter row, in a fixed order (deterministic).  Replaces tops.ops.kda.gate.kda_gate_bwd
+ * (tops/ops/kda/gate.py:54-119) and the autodiff backward of tops/cpu/ops/kda/gate.py:117-158. */
+int tops_kda_gate_bwd(const void* g, int g_dtype, const float* A_log, const float* dt_bias,
+                      const float* dyg, void* dg, float* dA, float* dbias, float* workspace,
+                      int64_t workspace_floats, int rows, int H, int K, int A_heads,
+                      int bias_heads, int gate_mode, float lower_bound, void* stream);
+
+/* Row L2 normalisation y = x / sqrt(sum x^2 + 1e-6) over the last axis (D <= 256),
+ * y fp32 [rows,D].  Replaces _l2_normalize_last_dim (tops/cpu/ops/kda/fused_recurrent.py:14-18)
+ * of fused_recurrent_kda(use_qk_l2norm_in_kernel=True). */
+int tops_l2norm_fwd(const void* x, int x_dtype, float* y, int rows, int D, void* stream);
+
+/* Its backward: dx = r (dy - y (y . dy)), r = 1 / sqrt(sum x^2 + 1e-6); dy fp32, dx in
+ * x_dtype.  (The reference differentiates _l2_normalize_last_dim by autodiff.) */
+int tops_l2norm_bwd(const void* x, int x_dtype, const float* dy, void* dx, int rows, int D,
+                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

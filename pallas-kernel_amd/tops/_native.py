@@ -18,6 +18,7 @@ TOPS_BF16 = 1
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int
 _f32 = ctypes.c_float
+_i64 = ctypes.c_int64
 
 # name -> argtypes (every entry point returns int)
 SIGNATURES = {
@@ -42,6 +43,11 @@ SIGNATURES = {
     "tops_simple_gla_chunk_bwd_dqkg": [_vp] * 14 + [_i32] * 8 + [_f32, _vp],
     "tops_chunk_state_pass": [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp] + [_i32] * 6 + [_f32, _i32, _vp],
     "tops_chunk_state_combine": [_vp] * 7 + [_i32] * 5 + [_vp],
+    "tops_kda_gate_fwd": [_vp, _i32, _vp, _vp, _vp] + [_i32] * 6 + [_f32, _vp],
+    "tops_kda_gate_chunk_cumsum": [_vp, _i32] + [_vp] * 6 + [_i32] * 9 + [_f32, _f32, _vp],
+    "tops_kda_gate_bwd": [_vp, _i32] + [_vp] * 7 + [_i64] + [_i32] * 6 + [_f32, _vp],
+    "tops_l2norm_fwd": [_vp, _i32, _vp, _i32, _i32, _vp],
+    "tops_l2norm_bwd": [_vp, _i32, _vp, _vp, _i32, _i32, _vp],
 }
 
 _lib = None
@@ -66,6 +72,8 @@ def lib() -> ctypes.CDLL:
         L.tops_gla_state_bytes.argtypes = [_i32, _i32, _i32, _i32]
         L.tops_gla_fused_recurrent_bwd_workspace.restype = ctypes.c_int64
         L.tops_gla_fused_recurrent_bwd_workspace.argtypes = [_i32] * 7
+        L.tops_kda_gate_bwd_workspace.restype = ctypes.c_int64
+        L.tops_kda_gate_bwd_workspace.argtypes = [_i32] * 3
         _lib = L
     return _lib
 

@@ -21,8 +21,6 @@ the same result up to fp32 rounding.
 """
 from __future__ import annotations
 
-import math
-
 import torch
 
 from ... import _native as N
@@ -110,35 +108,53 @@ class _ChunkKDA(torch.autograd.Function):
         return dq, dk, dv, dg.to(g_dt), dbeta.to(b_dt), None, dh0, None, None
 
 
+def _prologue(q, k, v, g, A_log, dt_bias, use_gate_in_kernel, lower_bound,
+              use_qk_l2norm_in_kernel):
+    """The FLA-side options of KDA applied ahead of the kernels: q / k L2 normalisation
+    (float32 out, so v runs in float32 with them) and the in-kernel gate activation;
+    both stay differentiable (dq, dk chain through the normalisation; dg, dA_log and
+    dt_bias through the gate, as tops/cpu/ops/kda/chunk_bwd.py:617-668 does for the gate)."""
+    if use_qk_l2norm_in_kernel:
+        from .l2norm import l2norm
+        q, k = l2norm(q), l2norm(k)
+        v = v.to(torch.float32)
+    if use_gate_in_kernel:
+        from .gate import fused_kda_gate
+        if A_log is None:
+            raise AssertionError("A_log is required when use_gate_in_kernel=True")
+        g = fused_kda_gate(g, A_log, dt_bias=dt_bias, lower_bound=lower_bound)
+    return q, k, v, g
+
+
 def chunk_kda(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
               beta: torch.Tensor, scale: float | None = None,
               initial_state: torch.Tensor | None = None, output_final_state: bool = False,
-              cu_seqlens=None, chunk_size: int = 64):
+              cu_seqlens=None, chunk_size: int = 64, *, A_log: torch.Tensor | None = None,
+              dt_bias: torch.Tensor | None = None, use_gate_in_kernel: bool = False,
+              lower_bound: float | None = None, use_qk_l2norm_in_kernel: bool = False):
     """Chunked KDA, forward + backward (tops/ops/kda/chunk.py:193-217).
 
     q, k [B,T,H,K]; v [B,T,H,V]; g [B,T,H,K] natural-log gates; beta [B,T,H];
-    initial_state [N,H,K,V].  Returns (o [B,T,H,V], final_state [N,H,K,V] or None)."""
+    initial_state [N,H,K,V].  Returns (o [B,T,H,V] in v.dtype, final_state [N,H,K,V] or
+    None).  The keyword-only options are FLA's: with use_gate_in_kernel, g holds raw gates
+    activated by A_log / dt_bias / lower_bound (tops/cpu/ops/kda/gate.py); with
+    use_qk_l2norm_in_kernel, q and k are L2-normalised first."""
+    out_dtype = v.dtype
+    q, k, v, g = _prologue(q, k, v, g, A_log, dt_bias, use_gate_in_kernel, lower_bound,
+                           use_qk_l2norm_in_kernel)
     _check(q, k, v, g, beta, initial_state, cu_seqlens)
     if scale is None:
         scale = q.shape[-1] ** -0.5
-    return _ChunkKDA.apply(q, k, v, g, beta, float(scale), initial_state, bool(output_final_state),
-                           cu_seqlens)
+    o, ht = _ChunkKDA.apply(q, k, v, g, beta, float(scale), initial_state,
+                            bool(output_final_state), cu_seqlens)
+    return o.to(out_dtype), ht
 
 
 def _g_cumsum_log2(g: torch.Tensor, cu_seqlens) -> torch.Tensor:
     """Chunk-local cumsum of g / ln 2 (the reference's kda_gate_chunk_cumsum output,
-    tops/ops/kda/gate.py:19-51): differences of one float64 running sum."""
-    T = g.shape[1]
-    pos = torch.arange(T, device=g.device)
-    if cu_seqlens is None:
-        start = (pos // CHUNK) * CHUNK
-    else:
-        cu = torch.as_tensor(cu_seqlens, device=g.device).to(torch.long)
-        s0 = cu[torch.searchsorted(cu[1:], pos, right=True)]
-        start = s0 + ((pos - s0) // CHUNK) * CHUNK
-    c = (g.to(torch.float64) / math.log(2.0)).cumsum(1)
-    c = torch.cat([torch.zeros_like(c[:, :1]), c], 1)
-    return (c[:, pos + 1] - c[:, start]).to(torch.float32)
+    tops/ops/kda/gate.py:19-51), on tops_kda_gate_chunk_cumsum."""
+    from .gate import kda_gate_chunk_cumsum
+    return kda_gate_chunk_cumsum(g, CHUNK, cu_seqlens)
 
 
 def chunk_kda_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
