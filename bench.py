@@ -122,7 +122,80 @@ def secondary(dev, iters=10, configs=(2, 4, 5)):
         out.append(_config4(dev, gen, iters))
     if 5 in configs:
         out.append(_config5(dev, gen, iters))
+    if 6 in configs:
+        out.append(_neighbours(dev, gen, iters))
     return out
+
+
+def _neighbours(dev, gen, iters):
+    """The kernels either side of the op, each timed per launch with HIP events on the stream
+    it runs on, against its algorithmic HBM bytes: the KDA gate (forward, backward, log2
+    chunk cumsum) and the q / k L2 norm at config 5's shape, FusedRMSNormGated on the GLA
+    output and ShortConvolution (W = 4) on a projection at config 3's layer shape."""
+    import torch
+    from tops import _native as NT
+    from tops.modules import rms_norm_gated, short_conv
+    from tops.ops.kda import fused_kda_gate, kda_gate_chunk_cumsum, l2norm
+    f32, bf = torch.float32, torch.bfloat16
+    B5, T5, H5, D = 4, 8192, 32, 128
+    n5 = B5 * T5 * H5 * D
+    g = torch.randn(B5, T5, H5, D, device=dev, generator=gen).requires_grad_()
+    A = torch.log(torch.rand(H5, device=dev, generator=gen) * 3 + 1).requires_grad_()
+    bias = torch.randn(H5 * D, device=dev, generator=gen).requires_grad_()
+    dyg = torch.randn(B5, T5, H5, D, device=dev, generator=gen)
+    gl = torch.nn.functional.logsigmoid(torch.randn(B5, T5, H5, D, device=dev, generator=gen))
+    q = torch.randn(B5, T5, H5, D, device=dev, generator=gen).to(bf).requires_grad_()
+    dq = torch.randn(B5, T5, H5, D, device=dev, generator=gen)
+    n3 = B * T * H * V
+    o = torch.randn(B, T, H, V, device=dev, generator=gen).to(bf).requires_grad_()
+    og = torch.randn(B, T, H, V, device=dev, generator=gen).to(bf).requires_grad_()
+    w = torch.ones(V, device=dev, requires_grad=True)
+    do = torch.randn(B, T, H, V, device=dev, generator=gen).to(bf)
+    Dh = H * K
+    x = torch.randn(B, T, Dh, device=dev, generator=gen).to(bf).requires_grad_()
+    cw = (torch.randn(Dh, 1, 4, device=dev, generator=gen) / 2).requires_grad_()
+    cb = torch.randn(Dh, device=dev, generator=gen).requires_grad_()
+    dy = torch.randn(B, T, Dh, device=dev, generator=gen)
+    nc = B * T * Dh
+    algo = {  # entry point -> (algorithmic bytes per launch, shape)
+        "tops_kda_gate_fwd": (n5 * 8, "g f32 [4,8192,32,128] -> y f32"),
+        "tops_kda_gate_bwd": (n5 * 12, "g, dyg f32 -> dg f32 (+ dA, dbias)"),
+        "tops_kda_gate_chunk_cumsum": (n5 * 8, "g f32 -> log2 chunk cumsum f32"),
+        "tops_l2norm_fwd": (n5 * 6, "q bf16 [4,8192,32,128] -> f32"),
+        "tops_l2norm_bwd": (n5 * 8, "q bf16, dy f32 -> dq bf16"),
+        "tops_rmsnorm_gated_fwd": (n3 * 6, "o, g bf16 [8,4096,16,128] -> bf16"),
+        "tops_rmsnorm_gated_bwd": (n3 * 10, "o, g, dy bf16 -> do, dg bf16 (+ dw)"),
+        "tops_short_conv_fwd": (nc * 6, "x bf16 [8,4096,2048], W=4 -> y f32"),
+        "tops_short_conv_bwd": (nc * 8, "x bf16, dy f32 -> dx bf16 (+ dw, db)"),
+    }
+
+    def run():
+        y = fused_kda_gate(g, A, dt_bias=bias)
+        torch.autograd.grad(y, (g, A, bias), dyg)
+        kda_gate_chunk_cumsum(gl, 64)
+        torch.autograd.grad(l2norm(q), q, dq)
+        torch.autograd.grad(rms_norm_gated(o, og, w), (o, og, w), do)
+        yc, _ = short_conv(x, cw, cb, "silu")
+        torch.autograd.grad(yc, (x, cw, cb), dy)
+    run()
+    torch.cuda.synchronize()
+    NT.enable_timing(True)
+    for _ in range(iters):
+        run()
+    torch.cuda.synchronize()
+    ev = NT.timing_events()
+    NT.enable_timing(False)
+    rows = []
+    for name, (nbytes, shape) in algo.items():
+        ms = [e0.elapsed_time(e1) for e0, e1 in ev.get(name, [])]
+        if not ms:
+            continue
+        avg = sum(ms) / len(ms)
+        gbs = nbytes / (avg * 1e-3) / 1e9
+        rows.append({"entry": name, "shape": shape, "avg_ms": round(avg, 4), "launches": len(ms),
+                     "algo_bytes": nbytes, "hbm_gbs": round(gbs, 1),
+                     "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
+    return {"config": "layer-side and KDA gate kernels (HBM-bound streams)", "kernels": rows}
 
 
 def _config2(dev, gen, iters):
@@ -216,7 +289,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the config 2 / 4 / 5 lines")
-    ap.add_argument("--configs", default="2,4,5", help="secondary configs to measure")
+    ap.add_argument("--configs", default="2,4,5,6",
+                    help="secondary configs to measure (6: the gate / norm / conv kernels)")
     ap.add_argument("--only-secondary", action="store_true",
                     help="measure only the secondary configs (for profiling them alone)")
     ap.add_argument("--copy-calibration", action="store_true",

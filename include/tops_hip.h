@@ -301,6 +301,56 @@ int tops_l2norm_fwd(const void* x, int x_dtype, float* y, int rows, int D, void*
 int tops_l2norm_bwd(const void* x, int x_dtype, const float* dy, void* dx, int rows, int D,
                     void* stream);
 
+/* RMSNorm with an optional SiLU gate, y [rows,D] in x_dtype:
+ *   y = x * rsqrt(mean(x^2) + eps) * weight * silu(g), computed in fp32.
+ * g [rows,D] (g_dtype) or NULL (plain RMSNorm); weight [D] fp32 or NULL (no affine).
+ * D <= 2048.  Replaces FusedRMSNormGated.__call__ (tops/modules/fused_norm_gate.py:28-37)
+ * and RMSNorm.__call__ (tops/modules/layernorm.py:28-35). */
+int tops_rmsnorm_gated_fwd(const void* x, int x_dtype, const void* g, int g_dtype,
+                           const float* weight, void* y, int rows, int D, float eps,
+                           void* stream);
+
+/* Floats of the workspace tops_rmsnorm_gated_bwd needs when weight != NULL. */
+int64_t tops_rmsnorm_gated_bwd_workspace(int rows, int D);
+
+/* Its backward: dx (x_dtype), dg (g_dtype, when g != NULL) and dweight [D] fp32 (when
+ * weight != NULL; per-workgroup partials added in a fixed order) from dy (x_dtype).
+ * The reference differentiates the modules above by autodiff. */
+int tops_rmsnorm_gated_bwd(const void* x, int x_dtype, const void* g, int g_dtype,
+                           const float* weight, const void* dy, void* dx, void* dg,
+                           float* dweight, float* workspace, int64_t workspace_floats, int rows,
+                           int D, float eps, void* stream);
+
+/* Causal depthwise convolution over time, y [B,T,D] (y_dtype):
+ *   y[t, d] = act(sum_j x[t - W + 1 + j, d] * weight[d, j] + bias[d]),
+ * zero left padding per sequence (varlen: cu_seqlens [N+1], B == 1).  weight [D,W] fp32
+ * (the [D,1,W] depthwise kernel), bias [D] fp32 or NULL, 1 <= W <= 8, activation 0 (none)
+ * or 1 (SiLU).  final_state [N,D,W] (x_dtype) or NULL: the last W inputs of each sequence,
+ * zero left-padded.  Replaces ShortConvolution._causal_conv1d and the final-state window of
+ * ShortConvolution.__call__ (tops/modules/convolution.py:44-80, 128-173). */
+int tops_short_conv_fwd(const void* x, int x_dtype, const float* weight, const float* bias,
+                        void* y, int y_dtype, void* final_state, const int32_t* cu_seqlens,
+                        int B, int T, int D, int W, int N, int activation, void* stream);
+
+/* Floats of the workspace tops_short_conv_bwd needs. */
+int64_t tops_short_conv_bwd_workspace(int B, int T, int D, int W);
+
+/* Its backward: dx [B,T,D] (x_dtype), dweight [D,W] and dbias [D] (fp32; dbias may be NULL)
+ * from dy (dy_dtype).  Deterministic (fixed-order partial sums).  The reference
+ * differentiates ShortConvolution by autodiff. */
+int tops_short_conv_bwd(const void* x, int x_dtype, const float* weight, const float* bias,
+                        const void* dy, int dy_dtype, void* dx, float* dweight, float* dbias,
+                        float* workspace, int64_t workspace_floats, const int32_t* cu_seqlens,
+                        int B, int T, int D, int W, int N, int activation, void* stream);
+
+/* One decode step for N sequences: cache_out [N,D,W] fp32 = cache_in rolled by one along W
+ * with x [N,D] appended (cache_out may alias cache_in), y [N,D] = act(sum_j cache_out[.., j]
+ * * weight[d, j] + bias); without a cache (cache_in NULL) y = act(x * weight[d, W-1] + bias).
+ * Replaces ShortConvolution.step (tops/modules/convolution.py:82-126). */
+int tops_short_conv_step(const void* x, int x_dtype, const float* cache_in, float* cache_out,
+                         const float* weight, const float* bias, void* y, int y_dtype, int N,
+                         int D, int W, int activation, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -20,6 +20,7 @@
 #include <math.h>
 #include <stdio.h>
 
+#include "stream_ops.h"
 #include "tops_common.h"
 #include "tops_hip.h"
 
@@ -34,60 +35,63 @@ struct GateArgs {
   float lb;
 };
 
-__device__ __forceinline__ float softplus_f(float x) {
-  return fmaxf(x, 0.f) + log1pf(expf(-fabsf(x)));
+// softplus and sigmoid from one e = exp(-|x|) (no overflow for any x):
+//   softplus(x) = max(x, 0) + log1p(e),  sigmoid(x) = (x >= 0 ? 1 : e) / (1 + e).
+// log1p(e), 0 <= e <= 1, by Kahan's correction log(u) * e / (u - 1) with u = fl(1 + e): exact
+// to a few ulp given an accurate log2 (the hardware log2 / reciprocal here, 1 ulp each).
+__device__ __forceinline__ float rcp_f(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float log1p_unit(float e) {
+  const float u = 1.f + e;
+  const float d = u - 1.f;
+  return d == 0.f ? e : log2f(u) * kLn2 * (e * rcp_f(d));
 }
-__device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
+__device__ __forceinline__ float softplus_f(float x) {
+  return fmaxf(x, 0.f) + log1p_unit(expf(-fabsf(x)));
+}
+__device__ __forceinline__ float sigmoid_f(float x) {
+  const float e = expf(-fabsf(x));
+  const float r = rcp_f(1.f + e);
+  return x >= 0.f ? r : e * r;
+}
+__device__ __forceinline__ void softplus_sigmoid(float x, float& sp, float& sg) {
+  const float e = expf(-fabsf(x));
+  const float r = rcp_f(1.f + e);
+  sp = fmaxf(x, 0.f) + log1p_unit(e);
+  sg = x >= 0.f ? r : e * r;
+}
 
 // activated gate of one element; eA = exp(A_log[h]), x = g + bias
 __device__ __forceinline__ float gate_act(float x, float eA, int mode, float lb) {
   return mode == TOPS_KDA_GATE_LOWER_BOUND ? lb * sigmoid_f(eA * x) : -eA * softplus_f(x);
 }
 
-template <typename TIn> struct Vec4;
-template <> struct Vec4<float> {
-  __device__ __forceinline__ static void ld(const float* p, float* v) {
-    float4 u = *(const float4*)p;
-    v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
-  }
-  __device__ __forceinline__ static void st(float* p, const float* v) {
-    *(float4*)p = make_float4(v[0], v[1], v[2], v[3]);
-  }
-};
-template <> struct Vec4<uint16_t> {
-  __device__ __forceinline__ static void ld(const uint16_t* p, float* v) {
-    uint2 u = *(const uint2*)p;
-    v[0] = __uint_as_float(u.x << 16); v[1] = __uint_as_float(u.x & 0xffff0000u);
-    v[2] = __uint_as_float(u.y << 16); v[3] = __uint_as_float(u.y & 0xffff0000u);
-  }
-  __device__ __forceinline__ static void st(uint16_t* p, const float* v) {
-    *(uint2*)p = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-  }
-};
-
 // ---------------------------------------------------------------- forward
-// 4 consecutive columns per thread (K % 4 == 0, so the 4 share a head)
+// grid (tiles of 1024 columns, row blocks): 4 consecutive columns per thread (K % 4 == 0, so
+// the 4 share a head), rows of the block four at a time with the loads issued first
 template <typename TIn>
 __global__ void __launch_bounds__(256) kda_gate_fwd_kernel(const TIn* __restrict__ g,
                                                            float* __restrict__ y, GateArgs a,
-                                                           long long n4) {
+                                                           int rows, int per) {
   const int HK = a.H * a.K;
-  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n4;
-       i += (long long)gridDim.x * 256) {
-    const long long e = i * 4;
-    const int col = (int)(e % HK);
-    const int h = col / a.K;
-    const float eA = expf(a.A_log[h / a.rep_a]);
-    float v[4];
-    Vec4<TIn>::ld(g + e, v);
-    if (a.bias) {
-      const float* b = a.bias + (h / a.rep_b) * a.K + (col - h * a.K);
+  const int col = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (col >= HK) return;
+  const int h = col / a.K;
+  const float eA = expf(a.A_log[h / a.rep_a]);
+  float b[4] = {0.f, 0.f, 0.f, 0.f};
+  if (a.bias) V4<float>::ld(a.bias + (h / a.rep_b) * a.K + (col - h * a.K), b);
+  const int r0 = blockIdx.y * per, r1 = min(r0 + per, rows);
+  for (int r = r0; r < r1; r += 4) {
+    float v[4][4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] += b[j];
+    for (int u = 0; u < 4; ++u)
+      if (r + u < r1) V4<TIn>::ld(g + (long long)(r + u) * HK + col, v[u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (r + u >= r1) break;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[u][j] = gate_act(v[u][j] + b[j], eA, a.mode, a.lb);
+      V4<float>::st(y + (long long)(r + u) * HK + col, v[u]);
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = gate_act(v[j], eA, a.mode, a.lb);
-    Vec4<float>::st(y + e, v);
   }
 }
 
@@ -134,60 +138,70 @@ __global__ void __launch_bounds__(256) kda_gate_cumsum_kernel(
 }
 
 // ---------------------------------------------------------------- backward
-// grid (column tiles of 256, row blocks).  Each thread owns one (head, column) over the
-// block's rows: writes dg and one partial of dA (per element: dyg * y, or dg * x for the
-// lower bound) and of dbias (dg).
+// grid (tiles of 1024 columns, row blocks).  Each thread owns 4 columns of one head over
+// the block's rows: writes dg and one partial per column of dA (per element: dyg * y, or
+// dg * x for the lower bound) and of dbias (dg), laid out [row block][2 * H * K].
 template <typename TIn>
 __global__ void __launch_bounds__(256) kda_gate_bwd_kernel(
     const TIn* __restrict__ g, const float* __restrict__ dyg, TIn* __restrict__ dg,
-    float* __restrict__ part_a, float* __restrict__ part_b, GateArgs a, int rows,
-    int rows_per_blk) {
+    float* __restrict__ part, GateArgs a, int rows, int per) {
   const int HK = a.H * a.K;
-  const int col = blockIdx.x * 256 + threadIdx.x;
+  const int col = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (col >= HK) return;
   const int rb = blockIdx.y;
-  const int r0 = rb * rows_per_blk;
-  const int r1 = min(r0 + rows_per_blk, rows);
+  const int r0 = rb * per, r1 = min(r0 + per, rows);
   const int h = col / a.K;
   const float eA = expf(a.A_log[h / a.rep_a]);
-  const float bias = a.bias ? a.bias[(h / a.rep_b) * a.K + (col - h * a.K)] : 0.f;
-  float sa = 0.f, sb = 0.f;
-#pragma unroll 4
-  for (int r = r0; r < r1; ++r) {
-    const long long off = (long long)r * HK + col;
-    const float x = In<TIn>::ld(g + off) + bias;
-    const float dy = dyg[off];
-    float d;
-    if (a.mode == TOPS_KDA_GATE_LOWER_BOUND) {
-      const float s = sigmoid_f(eA * x);
-      d = dy * (a.lb * s * (1.f - s)) * eA;
-      sa += d * x;
-    } else {
-      d = -eA * (dy * sigmoid_f(x));
-      sa += dy * (-eA * softplus_f(x));
+  float b[4] = {0.f, 0.f, 0.f, 0.f};
+  if (a.bias) V4<float>::ld(a.bias + (h / a.rep_b) * a.K + (col - h * a.K), b);
+  float sa[4] = {0.f, 0.f, 0.f, 0.f}, sb[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int r = r0; r < r1; r += 4) {
+    float x[4][4], dy[4][4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (r + u < r1) {
+        V4<TIn>::ld(g + (long long)(r + u) * HK + col, x[u]);
+        V4<float>::ld(dyg + (long long)(r + u) * HK + col, dy[u]);
+      }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (r + u >= r1) break;
+      float d[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float xv = x[u][j] + b[j];
+        if (a.mode == TOPS_KDA_GATE_LOWER_BOUND) {
+          const float s = sigmoid_f(eA * xv);
+          d[j] = dy[u][j] * (a.lb * s * (1.f - s)) * eA;
+          sa[j] += d[j] * xv;
+        } else {
+          float sp, sg;
+          softplus_sigmoid(xv, sp, sg);
+          d[j] = -eA * (dy[u][j] * sg);
+          sa[j] += dy[u][j] * (-eA * sp);
+        }
+        sb[j] += d[j];
+      }
+      V4<TIn>::st(dg + (long long)(r + u) * HK + col, d);
     }
-    sb += d;
-    In<TIn>::st(dg + off, d);
   }
-  part_a[(long long)rb * HK + col] = sa;
-  part_b[(long long)rb * HK + col] = sb;
+  float* pp = part + (long long)rb * 2 * HK;
+  V4<float>::st(pp + col, sa);
+  V4<float>::st(pp + HK + col, sb);
 }
 
-// blocks [0, A_heads): dA[ha] = sum over its heads, columns and row blocks (fixed-order tree
-// over the workgroup); blocks after: dbias[hb * K + k], one thread each.
-__global__ void __launch_bounds__(256) kda_gate_bwd_reduce_kernel(
-    const float* __restrict__ part_a, const float* __restrict__ part_b, int nrb, GateArgs a,
-    int A_heads, int bias_heads, float* __restrict__ dA, float* __restrict__ dbias) {
-  const int HK = a.H * a.K;
+// tot_a / tot_b [H * K]: the partials summed over row blocks.  Blocks [0, A_heads):
+// dA[ha] = sum over its heads' columns (fixed-order tree); blocks after: dbias[hb * K + k],
+// one thread each, summing the heads that share the row.
+__global__ void __launch_bounds__(256) kda_gate_fold_kernel(
+    const float* __restrict__ tot_a, const float* __restrict__ tot_b, GateArgs a, int A_heads,
+    int bias_heads, float* __restrict__ dA, float* __restrict__ dbias) {
   const int tid = threadIdx.x;
   if ((int)blockIdx.x < A_heads) {
     __shared__ float red[256];
     const int ha = blockIdx.x;
     float s = 0.f;
-    for (int j = tid; j < a.rep_a * a.K; j += 256) {
-      const int col = ha * a.rep_a * a.K + j;  // heads ha*rep_a .. are contiguous columns
-      for (int r = 0; r < nrb; ++r) s += part_a[(long long)r * HK + col];
-    }
+    for (int j = tid; j < a.rep_a * a.K; j += 256) s += tot_a[ha * a.rep_a * a.K + j];
     red[tid] = s;
     __syncthreads();
     for (int w = 128; w > 0; w >>= 1) {
@@ -201,10 +215,7 @@ __global__ void __launch_bounds__(256) kda_gate_bwd_reduce_kernel(
   if (!dbias || idx >= bias_heads * a.K) return;
   const int hb = idx / a.K, k = idx - hb * a.K;
   float s = 0.f;
-  for (int i = 0; i < a.rep_b; ++i) {
-    const int col = (hb * a.rep_b + i) * a.K + k;
-    for (int r = 0; r < nrb; ++r) s += part_b[(long long)r * HK + col];
-  }
+  for (int i = 0; i < a.rep_b; ++i) s += tot_b[(hb * a.rep_b + i) * a.K + k];
   dbias[idx] = s;
 }
 
@@ -270,6 +281,78 @@ __global__ void __launch_bounds__(256) l2norm_bwd_kernel(const TIn* __restrict__
   }
 }
 
+// vector path (D % 8 == 0, 64 <= D <= 512): LPR lanes per row, 8 consecutive elements per
+// lane, 64 / LPR rows per wave, two row groups per iteration in the forward
+template <typename TIn, int LPR>
+__global__ void __launch_bounds__(256) l2norm_fwd_v8(const TIn* __restrict__ x,
+                                                     float* __restrict__ y, int rows, int D) {
+  constexpr int RPW = 64 / LPR;
+  const int lane = threadIdx.x & 63, sub = lane % LPR, slot = lane / LPR;
+  const int nw = gridDim.x * 4;
+  const bool col_ok = sub < (D >> 3);
+  for (int rg = blockIdx.x * 4 + (threadIdx.x >> 6); rg * RPW < rows; rg += 2 * nw) {
+    float v[2][8];
+    bool ok[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int row = (rg + u * nw) * RPW + slot;
+      ok[u] = row < rows && col_ok;
+      if (ok[u]) V8<TIn>::ld(x + (long long)row * D + sub * 8, v[u]);
+      else
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[u][e] = 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += v[u][e] * v[u][e];
+      const float den = sqrtf(group_sum<LPR>(ss) + 1e-6f);
+      if (!ok[u]) continue;
+      const int row = (rg + u * nw) * RPW + slot;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[u][e] = v[u][e] / den;
+      V8<float>::st(y + (long long)row * D + sub * 8, v[u]);
+    }
+  }
+}
+
+template <typename TIn, int LPR>
+__global__ void __launch_bounds__(256) l2norm_bwd_v8(const TIn* __restrict__ x,
+                                                     const float* __restrict__ dy,
+                                                     TIn* __restrict__ dx, int rows, int D) {
+  constexpr int RPW = 64 / LPR;
+  const int lane = threadIdx.x & 63, sub = lane % LPR, slot = lane / LPR;
+  const int nw = gridDim.x * 4;
+  const bool col_ok = sub < (D >> 3);
+  for (int rg = blockIdx.x * 4 + (threadIdx.x >> 6); rg * RPW < rows; rg += nw) {
+    const int row = rg * RPW + slot;
+    const bool ok = row < rows && col_ok;
+    const long long base = (long long)row * D + sub * 8;
+    float v[8], w[8];
+    if (ok) {
+      V8<TIn>::ld(x + base, v);
+      V8<float>::ld(dy + base, w);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = w[e] = 0.f;
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+    const float r = 1.f / sqrtf(group_sum<LPR>(ss) + 1e-6f);
+    float sd = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sd += (v[e] * r) * w[e];
+    sd = group_sum<LPR>(sd);
+    if (!ok) continue;
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = r * (w[e] - (v[e] * r) * sd);
+    V8<TIn>::st(dx + base, o);
+  }
+}
+
 }  // namespace tops
 
 using namespace tops;
@@ -321,9 +404,18 @@ static int gate_check(const char* who, const void* g, int g_dtype, const float* 
   return TOPS_OK;
 }
 
-static int grid_of(long long n, int per_block, int cap) {
-  long long b = (n + per_block - 1) / per_block;
-  return (int)(b < 1 ? 1 : (b > cap ? cap : b));
+// row blocks over (tiles of 1024 columns x row blocks): about `target` workgroups, at most
+// 4096 row blocks, runs of whole rows
+static void row_split(int rows, int HK, int target, int& nrb, int& per) {
+  const int tiles = (HK / 4 + 255) / 256;
+  nrb = (target + tiles - 1) / tiles;
+  if (nrb > rows) nrb = rows;
+  if (nrb > 4096) nrb = 4096;
+  if (nrb < 1) nrb = 1;
+  per = (rows + nrb - 1) / nrb;
+  if (per < 1) per = 1;
+  nrb = (rows + per - 1) / per;
+  if (nrb < 1) nrb = 1;
 }
 
 extern "C" int tops_kda_gate_fwd(const void* g, int g_dtype, const float* A_log,
@@ -336,14 +428,16 @@ extern "C" int tops_kda_gate_fwd(const void* g, int g_dtype, const float* A_log,
   if (rc != TOPS_OK) return rc;
   if (!y) return tops_set_error(TOPS_ERR_NULL, "kda_gate_fwd: null output");
   a.lb = lower_bound;
-  const long long n4 = (long long)rows * H * K / 4;
-  if (n4 == 0) return TOPS_OK;
+  if (rows == 0) return TOPS_OK;
   hipStream_t s = (hipStream_t)stream;
-  const int grid = grid_of(n4, 256, 256 * 32);
+  const int HK = H * K;
+  int nrb, per;
+  row_split(rows, HK, 8192, nrb, per);
+  dim3 grid((HK / 4 + 255) / 256, nrb);
   if (g_dtype == TOPS_BF16)
-    kda_gate_fwd_kernel<uint16_t><<<grid, 256, 0, s>>>((const uint16_t*)g, y, a, n4);
+    kda_gate_fwd_kernel<uint16_t><<<grid, 256, 0, s>>>((const uint16_t*)g, y, a, rows, per);
   else
-    kda_gate_fwd_kernel<float><<<grid, 256, 0, s>>>((const float*)g, y, a, n4);
+    kda_gate_fwd_kernel<float><<<grid, 256, 0, s>>>((const float*)g, y, a, rows, per);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? TOPS_OK : tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
 }
@@ -387,23 +481,21 @@ extern "C" int tops_kda_gate_chunk_cumsum(const void* g, int g_dtype, const floa
   return e == hipSuccess ? TOPS_OK : tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
 }
 
-// row blocks of the backward: about 2048 workgroups in all
-static void gate_bwd_split(int rows, int H, int K, int& nrb, int& per) {
-  const int tiles = (H * K + 255) / 256;
-  nrb = (2048 + tiles - 1) / tiles;
-  if (nrb > rows) nrb = rows;
-  if (nrb < 1) nrb = 1;
-  per = (rows + nrb - 1) / nrb;
-  if (per < 1) per = 1;
-  nrb = (rows + per - 1) / per;
-  if (nrb < 1) nrb = 1;
+// backward workspace: partials [nrb][2 * H * K], the column sum's scratch, totals [2 * H * K]
+static void gate_bwd_layout(int rows, int H, int K, int& nrb, int& per, int64_t& n_part,
+                            int64_t& n_total) {
+  const int HK = H * K;
+  row_split(rows > 0 ? rows : 1, HK, 2048, nrb, per);
+  n_part = (int64_t)nrb * 2 * HK;
+  n_total = n_part + colsum_scratch_floats(nrb, 2 * HK) + 2LL * HK;
 }
 
 extern "C" int64_t tops_kda_gate_bwd_workspace(int rows, int H, int K) {
-  if (rows < 0 || H <= 0 || K <= 0) return TOPS_ERR_SHAPE;
+  if (rows < 0 || H <= 0 || K <= 0 || (long long)H * K >= (1LL << 30)) return TOPS_ERR_SHAPE;
   int nrb, per;
-  gate_bwd_split(rows, H, K, nrb, per);
-  return 2LL * nrb * H * K;
+  int64_t n_part, n_total;
+  gate_bwd_layout(rows, H, K, nrb, per, n_part, n_total);
+  return n_total;
 }
 
 extern "C" int tops_kda_gate_bwd(const void* g, int g_dtype, const float* A_log,
@@ -419,35 +511,63 @@ extern "C" int tops_kda_gate_bwd(const void* g, int g_dtype, const float* A_log,
     return tops_set_error(TOPS_ERR_NULL, "kda_gate_bwd: null tensor");
   a.lb = lower_bound;
   int nrb, per;
-  gate_bwd_split(rows, H, K, nrb, per);
-  const long long HK = (long long)H * K;
-  if (workspace_floats < 2LL * nrb * HK)
+  int64_t n_part, n_total;
+  gate_bwd_layout(rows, H, K, nrb, per, n_part, n_total);
+  if (workspace_floats < n_total)
     return tops_set_error(TOPS_ERR_SHAPE, "kda_gate_bwd: workspace smaller than tops_kda_gate_bwd_workspace()");
   hipStream_t s = (hipStream_t)stream;
-  float* part_a = workspace;
-  float* part_b = workspace + (long long)nrb * HK;
-  const int tiles = (int)((HK + 255) / 256);
+  const int HK = H * K;
+  float* part = workspace;
+  float* tot = workspace + n_total - 2LL * HK;
+  hipError_t e = hipSuccess;
   if (rows > 0) {
-    dim3 grid(tiles, nrb);
+    dim3 grid((HK / 4 + 255) / 256, nrb);
     if (g_dtype == TOPS_BF16)
       kda_gate_bwd_kernel<uint16_t><<<grid, 256, 0, s>>>((const uint16_t*)g, dyg, (uint16_t*)dg,
-                                                          part_a, part_b, a, rows, per);
+                                                          part, a, rows, per);
     else
-      kda_gate_bwd_kernel<float><<<grid, 256, 0, s>>>((const float*)g, dyg, (float*)dg, part_a,
-                                                       part_b, a, rows, per);
-  } else {
-    nrb = 0;  // no tokens: dA and dbias are zero
+      kda_gate_bwd_kernel<float><<<grid, 256, 0, s>>>((const float*)g, dyg, (float*)dg, part, a,
+                                                       rows, per);
+    e = hipGetLastError();
+    if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   }
+  // no tokens: zero partial rows, so dA and dbias come out zero
+  e = launch_colsum(part, rows > 0 ? nrb : 0, 2 * HK, HK, tot, tot + HK, s);
+  if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   const int nb = dt_bias ? bias_heads : 0;
   const int grid2 = A_heads + (nb * K + 255) / 256;
-  kda_gate_bwd_reduce_kernel<<<grid2, 256, 0, s>>>(part_a, part_b, nrb, a, A_heads, nb,
-                                                   dA, dt_bias ? dbias : nullptr);
-  hipError_t e = hipGetLastError();
+  kda_gate_fold_kernel<<<grid2, 256, 0, s>>>(tot, tot + HK, a, A_heads, nb, dA,
+                                             dt_bias ? dbias : nullptr);
+  e = hipGetLastError();
   return e == hipSuccess ? TOPS_OK : tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
+}
+
+// L2 norm: vector path for D % 8 == 0, 64 <= D <= 512 (LPR = D / 8 rounded up to a power of
+// two); other D one wave per row
+static int l2_lpr(int D) {
+  if (D % 8 || D < 64 || D > 512) return 0;
+  int l = 8;
+  while (l < D / 8) l <<= 1;
+  return l;
 }
 
 template <int NV>
 static hipError_t l2_fwd(const void* x, int dt, float* y, int rows, int D, hipStream_t s) {
+  if (const int lpr = l2_lpr(D)) {
+    const long long groups = ((long long)rows + 64 / lpr - 1) / (64 / lpr);
+    long long gl = (groups + 7) / 8;
+    const int grid = (int)(gl > 16384 ? 16384 : (gl < 1 ? 1 : gl));
+#define TOPS_L2F(L)                                                                        \
+  (dt == TOPS_BF16                                                                         \
+       ? (l2norm_fwd_v8<uint16_t, L><<<grid, 256, 0, s>>>((const uint16_t*)x, y, rows, D)) \
+       : (l2norm_fwd_v8<float, L><<<grid, 256, 0, s>>>((const float*)x, y, rows, D)))
+    if (lpr == 8) TOPS_L2F(8);
+    else if (lpr == 16) TOPS_L2F(16);
+    else if (lpr == 32) TOPS_L2F(32);
+    else TOPS_L2F(64);
+#undef TOPS_L2F
+    return hipGetLastError();
+  }
   const int grid = (rows + 3) / 4;
   if (dt == TOPS_BF16)
     l2norm_fwd_kernel<uint16_t, NV><<<grid, 256, 0, s>>>((const uint16_t*)x, y, rows, D);
@@ -459,6 +579,22 @@ static hipError_t l2_fwd(const void* x, int dt, float* y, int rows, int D, hipSt
 template <int NV>
 static hipError_t l2_bwd(const void* x, int dt, const float* dy, void* dx, int rows, int D,
                          hipStream_t s) {
+  if (const int lpr = l2_lpr(D)) {
+    const long long groups = ((long long)rows + 64 / lpr - 1) / (64 / lpr);
+    long long gl = (groups + 3) / 4;
+    const int grid = (int)(gl > 16384 ? 16384 : (gl < 1 ? 1 : gl));
+#define TOPS_L2B(L)                                                                          \
+  (dt == TOPS_BF16 ? (l2norm_bwd_v8<uint16_t, L><<<grid, 256, 0, s>>>(                       \
+                         (const uint16_t*)x, dy, (uint16_t*)dx, rows, D))                    \
+                   : (l2norm_bwd_v8<float, L><<<grid, 256, 0, s>>>((const float*)x, dy,      \
+                                                                   (float*)dx, rows, D)))
+    if (lpr == 8) TOPS_L2B(8);
+    else if (lpr == 16) TOPS_L2B(16);
+    else if (lpr == 32) TOPS_L2B(32);
+    else TOPS_L2B(64);
+#undef TOPS_L2B
+    return hipGetLastError();
+  }
   const int grid = (rows + 3) / 4;
   if (dt == TOPS_BF16)
     l2norm_bwd_kernel<uint16_t, NV><<<grid, 256, 0, s>>>((const uint16_t*)x, dy, (uint16_t*)dx,

@@ -48,6 +48,12 @@ SIGNATURES = {
     "tops_kda_gate_bwd": [_vp, _i32] + [_vp] * 7 + [_i64] + [_i32] * 6 + [_f32, _vp],
     "tops_l2norm_fwd": [_vp, _i32, _vp, _i32, _i32, _vp],
     "tops_l2norm_bwd": [_vp, _i32, _vp, _vp, _i32, _i32, _vp],
+    "tops_rmsnorm_gated_fwd": [_vp, _i32, _vp, _i32, _vp, _vp, _i32, _i32, _f32, _vp],
+    "tops_rmsnorm_gated_bwd": [_vp, _i32, _vp, _i32] + [_vp] * 6 + [_i64, _i32, _i32, _f32, _vp],
+    "tops_short_conv_fwd": [_vp, _i32, _vp, _vp, _vp, _i32, _vp, _vp] + [_i32] * 6 + [_vp],
+    "tops_short_conv_bwd": [_vp, _i32, _vp, _vp, _vp, _i32] + [_vp] * 4 + [_i64, _vp]
+                           + [_i32] * 6 + [_vp],
+    "tops_short_conv_step": [_vp, _i32, _vp, _vp, _vp, _vp, _vp] + [_i32] * 5 + [_vp],
 }
 
 _lib = None
@@ -74,6 +80,10 @@ def lib() -> ctypes.CDLL:
         L.tops_gla_fused_recurrent_bwd_workspace.argtypes = [_i32] * 7
         L.tops_kda_gate_bwd_workspace.restype = ctypes.c_int64
         L.tops_kda_gate_bwd_workspace.argtypes = [_i32] * 3
+        L.tops_rmsnorm_gated_bwd_workspace.restype = ctypes.c_int64
+        L.tops_rmsnorm_gated_bwd_workspace.argtypes = [_i32] * 2
+        L.tops_short_conv_bwd_workspace.restype = ctypes.c_int64
+        L.tops_short_conv_bwd_workspace.argtypes = [_i32] * 4
         _lib = L
     return _lib
 
