@@ -351,6 +351,87 @@ int tops_short_conv_step(const void* x, int x_dtype, const float* cache_in, floa
                          const float* weight, const float* bias, void* y, int y_dtype, int N,
                          int D, int W, int activation, void* stream);
 
+/* ---- Stage functions of chunked GLA (csrc/gla_stages.hip) --------------------------------
+ * Each computes one intermediate of the chunk algorithm on its own, in fp32, for callers
+ * that drive the stages separately (the fused chunk entry points above never write these
+ * intermediates).  Layout [B,T,H,D] with T % chunk_size == 0, chunk_size 16, 32, 64 or 128;
+ * q/k/v/do in `dtype` (TOPS_F32 / TOPS_BF16), gates, A, states and gradients fp32; K and V
+ * positive multiples of 16.  Chunks are those of the flattened [B*T] token axis, which is
+ * also the layout of a varlen batch whose cu_seqlens are multiples of chunk_size. */
+
+/* Chunk-local cumsum of g ([B,T,H,S], or [B,H,T,S] when head_first): inclusive prefix sum
+ * (suffix sum when reverse) inside each chunk, times scale (pass 1 for none).  g and out
+ * each TOPS_F32 or TOPS_BF16; chunk_size any power of two; T need not be a multiple of it.
+ * Varlen (B == 1): cu_seqlens [N+1], chunk_offsets [N+1], chunk_map [total_chunks] as for
+ * tops_gla_chunk_bwd.  Replaces chunk_local_cumsum_vector (tops/ops/gla/chunk.py:110-198,
+ * K1 :55-107; tops/ops/common/cumsum.py:472-540). */
+int tops_chunk_local_cumsum(const void* g, int g_dtype, void* out, int out_dtype,
+                            const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                            const int32_t* chunk_map, int total_chunks, int B, int T, int H,
+                            int S, int chunk_size, int head_first, int reverse, float scale,
+                            void* stream);
+
+/* Inter-chunk state recurrence over x [B,T,H,K], y [B,T,H,V] with optional chunk-local gate
+ * cumsums gk [B,T,H,K], g [B,T,H] and per-head constant g_gamma [H] (log decay; the gate of
+ * row t of a chunk is gk + g + g_gamma * (t + 1)).
+ *   reverse == 0 (x = k, y = v): states[c / every] = state before chunk c (c % every == 0),
+ *     then S = S * exp(G_last) + (x * exp(G_last - G))^T y; s0 = h0, s_final = ht.
+ *     Replaces chunk_fwd_h_ref / chunk_fwd_h_kernel (tops/ops/common/chunk_h.py:100-489,
+ *     K7 :22-92; tops/ops/gla/chunk.py:206-292).
+ *   reverse == 1 (x = q, y = do): states[c] = gradient w.r.t. the state after chunk c, then
+ *     dS = dS * exp(G_last) + (x * scale * exp(G))^T y; s0 = dht, s_final = dh0.  Replaces
+ *     chunk_bwd_dh_ref / chunk_bwd_dh_kernel (chunk_h.py:575-884).
+ * states [B, NT/every, H, K, V] in states_dtype; s0, s_final [N,H,K,V] fp32 or NULL.
+ * cu_seqlens [N+1] (B == 1, every == 1): non-decreasing multiples of chunk_size from 0 to T.
+ * K <= 256. */
+int tops_chunk_state_recurrence(const void* x, const void* y, int dtype, const float* gk,
+                                const float* g, const float* g_gamma, const float* s0,
+                                void* states, int states_dtype, float* s_final,
+                                const int32_t* cu_seqlens, int B, int T, int H, int K, int V,
+                                int N, int chunk_size, int every, int reverse, float scale,
+                                void* stream);
+
+/* A [B,T,H,C] fp32 = scale * (q e^{g - gm}) (k e^{gm - g})^T per chunk, full square, gm the
+ * mean of the chunk's first and last gate rows.  Replaces chunk_gla_fwd_intra_gk
+ * (tops/ops/gla/chunk.py:390-438, K2 :351-387) and its ref (:300-343). */
+int tops_gla_stage_attn(const void* q, const void* k, int dtype, const float* g, float* A,
+                           int B, int T, int H, int K, int chunk_size, float scale,
+                           void* stream);
+
+/* o [B,T,H,V] (dtype) = scale * (q e^{g - gm}) (h_c e^{gm}) + tril(A) v per chunk, with
+ * h [B,NT,H,K,V] fp32 and exp2 instead of exp when use_exp2.  Replaces chunk_gla_fwd_o_gk
+ * (tops/ops/gla/chunk.py:1411-1440, K3 :1279-1335) and its ref (:446-501). */
+int tops_gla_stage_o(const void* q, const void* v, int dtype, const float* g, const float* A,
+                     const float* h, void* o, int B, int T, int H, int K, int V, int chunk_size,
+                     float scale, int use_exp2, void* stream);
+
+/* dA [B,T,H,C] (dA_dtype) = scale * tril(do v^T) per chunk.  Replaces chunk_gla_bwd_dA_ref
+ * (tops/ops/gla/chunk.py:509-549). */
+int tops_gla_stage_dattn(const void* v, const void* do_, int dtype, void* dA, int dA_dtype, int B,
+                      int T, int H, int V, int chunk_size, float scale, void* stream);
+
+/* dv [B,T,H,V] fp32 = tril(A)^T do + (k e^{g_last - g}) dh_c per chunk, dh [B,NT,H,K,V].
+ * Replaces chunk_gla_bwd_dv_ref (tops/ops/gla/chunk.py:552-605). */
+int tops_gla_stage_dv(const void* k, const void* do_, int dtype, const float* g, const float* A,
+                      const float* dh, float* dv, int B, int T, int H, int K, int V,
+                      int chunk_size, void* stream);
+
+/* dq = e^{g - gm} dA (k e^{gm - g}), dk = e^{gm - g} dA^T (q e^{g - gm}) per chunk, dA used as
+ * given (no mask); dq, dk [B,T,H,K] fp32.  Replaces chunk_gla_bwd_dqk_intra_ref
+ * (tops/ops/gla/chunk.py:608-662). */
+int tops_gla_stage_dqk_intra(const void* q, const void* k, int dtype, const float* g,
+                             const float* dA, float* dq, float* dk, int B, int T, int H, int K,
+                             int chunk_size, void* stream);
+
+/* dq_out = dq + scale e^{g} (do h_c^T), dk_out = dk + e^{g_last - g} (v dh_c^T),
+ * dg = reverse-cumsum over the chunk of (q dq_out - k dk_out) + e^{g_last} sum_v(h_c dh_c)
+ * + sum over the chunk of the inter dk times k; all [B,T,H,K] fp32.  Replaces
+ * chunk_gla_bwd_dqkg_ref (tops/ops/gla/chunk.py:665-760). */
+int tops_gla_stage_dqkg(const void* q, const void* k, const void* v, const void* do_, int dtype,
+                        const float* g, const float* h, const float* dh, const float* dq,
+                        const float* dk, float* dq_out, float* dk_out, float* dg, int B, int T,
+                        int H, int K, int V, int chunk_size, float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -3,7 +3,8 @@
 Restates:
   * tops/utils.py:63-90            prepare_lens / prepare_chunk_indices
   * tops/cpu/ops/common/utils.py   cdiv, pad_to_multiple, read_chunk
-  * tops/cpu/ops/common/chunk_o.py:18-112   chunk_local_cumsum
+  * tops/cpu/ops/common/chunk_o.py:18-112   chunk_local_cumsum, chunk_local_cumsum_segments
+    (the latter also tops/ops/gla/chunk.py:55-107: varlen restarts, short last chunks)
   * tops/cpu/ops/common/chunk_h.py:31-226   chunk_fwd_h   (gk and scalar-g gates)
   * tops/cpu/ops/common/chunk_h.py:229-427  chunk_bwd_dh  (gk and scalar-g gates)
 
@@ -69,6 +70,34 @@ def chunk_local_cumsum(g: np.ndarray, C: int, reverse: bool = False) -> np.ndarr
     if reverse:
         x = np.flip(x, axis=2)
     return np.ascontiguousarray(x.reshape(g.shape))
+
+
+def chunk_local_cumsum_segments(g, C: int, reverse: bool = False, cu_seqlens=None,
+                                head_first: bool = False, scale=None) -> np.ndarray:
+    """Chunk-local cumsum where chunks restart at every sequence start and the last chunk of
+    a sequence may be short; then * scale.
+
+    tops/cpu/ops/common/chunk_o.py:22-112 (packed-layout branch) and the accelerator kernel
+    tops/ops/gla/chunk.py:55-107 (valid-length masking).  g: [B,T,H,S] ([B,H,T,S] when
+    head_first); cu_seqlens [N+1] with B == 1, else each batch row is one sequence.
+    """
+    g = f64(g)
+    x = np.swapaxes(g, 1, 2) if head_first else g
+    out = np.zeros_like(x)
+    T = x.shape[1]
+    bounds = [(0, T)] if cu_seqlens is None else list(zip(cu_seqlens[:-1], cu_seqlens[1:]))
+    for b in range(x.shape[0]):
+        for s0, s1 in bounds:
+            for c0 in range(int(s0), int(s1), C):
+                c1 = min(c0 + C, int(s1))
+                blk = x[b, c0:c1]
+                if reverse:
+                    out[b, c0:c1] = np.flip(np.cumsum(np.flip(blk, 0), 0), 0)
+                else:
+                    out[b, c0:c1] = np.cumsum(blk, 0)
+    if scale is not None:
+        out = out * scale
+    return np.ascontiguousarray(np.swapaxes(out, 1, 2) if head_first else out)
 
 
 def chunk_fwd_h(k, v, *, gk=None, g=None, h0=None, C: int = 64):

@@ -54,6 +54,15 @@ SIGNATURES = {
     "tops_short_conv_bwd": [_vp, _i32, _vp, _vp, _vp, _i32] + [_vp] * 4 + [_i64, _vp]
                            + [_i32] * 6 + [_vp],
     "tops_short_conv_step": [_vp, _i32, _vp, _vp, _vp, _vp, _vp] + [_i32] * 5 + [_vp],
+    "tops_chunk_local_cumsum": [_vp, _i32, _vp, _i32, _vp, _vp, _vp] + [_i32] * 8 + [_f32, _vp],
+    "tops_chunk_state_recurrence": [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp]
+                                   + [_i32] * 9 + [_f32, _vp],
+    "tops_gla_stage_attn": [_vp, _vp, _i32, _vp, _vp] + [_i32] * 5 + [_f32, _vp],
+    "tops_gla_stage_o": [_vp, _vp, _i32, _vp, _vp, _vp, _vp] + [_i32] * 6 + [_f32, _i32, _vp],
+    "tops_gla_stage_dattn": [_vp, _vp, _i32, _vp, _i32] + [_i32] * 5 + [_f32, _vp],
+    "tops_gla_stage_dv": [_vp, _vp, _i32, _vp, _vp, _vp, _vp] + [_i32] * 6 + [_vp],
+    "tops_gla_stage_dqk_intra": [_vp, _vp, _i32, _vp, _vp, _vp, _vp] + [_i32] * 5 + [_vp],
+    "tops_gla_stage_dqkg": [_vp, _vp, _vp, _vp, _i32] + [_vp] * 8 + [_i32] * 6 + [_f32, _vp],
 }
 
 _lib = None

@@ -1,6 +1,8 @@
 """tops.ops.simple_gla on MI355X (mirrors tops/ops/simple_gla/__init__.py:1-239)."""
 from __future__ import annotations
 
+import enum
+
 from .chunk import (chunk_simple_gla, chunk_simple_gla_bwd, chunk_simple_gla_fwd,
                     chunk_simple_gla_fwd_varlen)
 from .fused_chunk import fused_chunk_simple_gla, fused_chunk_simple_gla_bwd, fused_chunk_simple_gla_fwd
@@ -50,14 +52,61 @@ __all__ = [
     "fused_chunk_simple_gla_bwd",
     "fused_recurrent_simple_gla",
     "simple_gla_naive",
+    "SimpleGLAKernelMode",
+    "simple_gla_fwd",
+    "simple_gla_bwd",
 ]
 
 
 def simple_gla_naive(q, k, v, g=None, g_gamma=None, scale=None, initial_state=None,
                      output_final_state=False, chunk_size=64, cu_seqlens_cpu=None):
-    """The reference's pure-JAX testing form (tops/ops/simple_gla/naive.py); here the
-    per-token recurrence on the HIP fused_recurrent kernels (same equations)."""
-    return fused_recurrent_simple_gla(q, k, v, g=g, g_gamma=g_gamma, scale=scale,
-                                      initial_state=initial_state,
-                                      output_final_state=output_final_state,
-                                      cu_seqlens=cu_seqlens_cpu)
+    """The reference's pure-JAX testing form (tops/ops/simple_gla/naive.py:5-100); here the
+    per-token recurrence on the HIP fused_recurrent kernels (same equations).  Returns
+    (o [B,T,H,V] float32, final state float32 or None) as the reference does."""
+    o, ht = fused_recurrent_simple_gla(q, k, v, g=g, g_gamma=g_gamma, scale=scale,
+                                       initial_state=initial_state,
+                                       output_final_state=output_final_state,
+                                       cu_seqlens=cu_seqlens_cpu)
+    return o.float(), ht
+
+
+class SimpleGLAKernelMode(enum.Enum):
+    """Kernel family for simple_gla_fwd / simple_gla_bwd (tops/ops/simple_gla/__init__.py:160-164);
+    both run the same HIP chunk sweep here."""
+    CHUNK = "chunk"
+    FUSED_CHUNK = "fused_chunk"
+
+
+def simple_gla_fwd(q, k, v, *, g=None, g_gamma=None, scale=None, h0=None, use_ht=False,
+                   cu_seqlens_cpu=None, cu_seqlens_dev=None, chunk_size=64,
+                   mode=SimpleGLAKernelMode.FUSED_CHUNK):
+    """tops/ops/simple_gla/__init__.py:167-201: forward by kernel mode (a device cu_seqlens
+    selects the varlen forward).  Returns (o, ht)."""
+    if mode not in (SimpleGLAKernelMode.CHUNK, SimpleGLAKernelMode.FUSED_CHUNK) \
+            and cu_seqlens_dev is None:
+        raise Exception(f"mode {mode} not support")
+    if cu_seqlens_dev is not None:
+        fn = chunk_simple_gla_fwd_varlen
+    elif mode == SimpleGLAKernelMode.CHUNK:
+        fn = chunk_simple_gla_fwd
+    else:
+        fn = fused_chunk_simple_gla_fwd
+    return fn(q, k, v, g=g, g_gamma=g_gamma, scale=scale, h0=h0, use_ht=use_ht,
+              cu_seqlens_cpu=cu_seqlens_cpu, cu_seqlens_dev=cu_seqlens_dev,
+              chunk_size=chunk_size)
+
+
+def simple_gla_bwd(q, k, v, do, *, g=None, g_gamma=None, scale=None, h0=None, dht=None,
+                   cu_seqlens_cpu=None, cu_seqlens_dev=None, chunk_size=64,
+                   mode=SimpleGLAKernelMode.FUSED_CHUNK):
+    """tops/ops/simple_gla/__init__.py:204-239: backward by kernel mode.  Returns
+    (dq, dk, dv, dh0)."""
+    if mode == SimpleGLAKernelMode.CHUNK:
+        fn = chunk_simple_gla_bwd
+    elif mode == SimpleGLAKernelMode.FUSED_CHUNK:
+        fn = fused_chunk_simple_gla_bwd
+    else:
+        raise Exception(f"mode {mode} not support")
+    return fn(q, k, v, do, g=g, g_gamma=g_gamma, scale=scale, h0=h0, dht=dht,
+              cu_seqlens_cpu=cu_seqlens_cpu, cu_seqlens_dev=cu_seqlens_dev,
+              chunk_size=chunk_size)

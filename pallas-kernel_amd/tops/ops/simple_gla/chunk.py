@@ -101,10 +101,30 @@ def chunk_simple_gla(
     return o, (ht if output_final_state else None)
 
 
+def _alias(new, old, name_new, name_old):
+    if old is not None:
+        if new is not None and new is not old:
+            raise ValueError(f"pass either {name_new} or {name_old}, not both")
+        return old
+    return new
+
+
 def chunk_simple_gla_fwd(q, k, v, g=None, g_gamma=None, scale=None, initial_state=None,
-                         output_final_state=False, chunk_size: int = 64, cu_seqlens=None):
+                         output_final_state=False, chunk_size: int = 64, cu_seqlens=None, *,
+                         h0=None, use_ht=None, cu_seqlens_cpu=None, cu_seqlens_dev=None,
+                         interpret=None):
     """Forward orchestrator (tops/cpu/ops/simple_gla/chunk.py:53-129; Pallas
-    tops/ops/simple_gla/chunk.py:464-521).  Returns (o, ht)."""
+    tops/ops/simple_gla/chunk.py:464-521).  Returns (o, ht).
+
+    Takes both the CPU-reference keywords (initial_state, output_final_state, cu_seqlens)
+    and the accelerator ones (h0, use_ht, cu_seqlens_cpu / cu_seqlens_dev; interpret is
+    ignored)."""
+    del interpret
+    initial_state = _alias(initial_state, h0, "initial_state", "h0")
+    if use_ht is not None:
+        output_final_state = bool(use_ht)
+    cu_seqlens = _alias(cu_seqlens, cu_seqlens_cpu if cu_seqlens_cpu is not None else cu_seqlens_dev,
+                        "cu_seqlens", "cu_seqlens_cpu")
     mode, gt = _gate(q, g, g_gamma)
     check_qkv(q, k, v, initial_state, cu_seqlens)
     if scale is None:
@@ -118,9 +138,17 @@ def chunk_simple_gla_fwd(q, k, v, g=None, g_gamma=None, scale=None, initial_stat
 
 
 def chunk_simple_gla_fwd_varlen(q, k, v, g=None, g_gamma=None, scale=None, initial_state=None,
-                                output_final_state=False, cu_seqlens=None, chunk_size: int = 64):
+                                output_final_state=False, cu_seqlens=None, chunk_size: int = 64,
+                                *, h0=None, use_ht=None, cu_seqlens_cpu=None, cu_seqlens_dev=None,
+                                interpret=None):
     """Varlen forward (tops/ops/simple_gla/chunk.py:522-577): the same kernels with a
-    cu_seqlens chunk map."""
+    cu_seqlens chunk map (keywords as chunk_simple_gla_fwd)."""
+    del interpret
+    initial_state = _alias(initial_state, h0, "initial_state", "h0")
+    if use_ht is not None:
+        output_final_state = bool(use_ht)
+    cu_seqlens = _alias(cu_seqlens, cu_seqlens_cpu if cu_seqlens_cpu is not None else cu_seqlens_dev,
+                        "cu_seqlens", "cu_seqlens_cpu")
     assert cu_seqlens is not None, "chunk_simple_gla_fwd_varlen needs cu_seqlens"
     return chunk_simple_gla_fwd(q, k, v, g=g, g_gamma=g_gamma, scale=scale,
                                 initial_state=initial_state, output_final_state=output_final_state,
@@ -128,12 +156,22 @@ def chunk_simple_gla_fwd_varlen(q, k, v, g=None, g_gamma=None, scale=None, initi
 
 
 def chunk_simple_gla_bwd(q, k, v, do, *, g=None, g_gamma=None, scale=None, h0=None, dht=None,
-                         cu_seqlens=None, chunk_size: int = 64):
-    """Backward orchestrator (tops/ops/simple_gla/chunk.py:579-674 keyword form; gate
-    options of tops/cpu/ops/simple_gla/chunk.py:668-788).
+                         cu_seqlens=None, chunk_size: int = 64, cu_seqlens_cpu=None,
+                         cu_seqlens_dev=None, interpret=None):
+    """Backward orchestrator (tops/ops/simple_gla/chunk.py:579-674 keyword form).
 
-    Returns (dq, dk, dv, dg, dh0): dg is [B,T,H] fp32 for a per-token g, None for
-    g_gamma; dh0 is returned when h0 is given."""
+    Returns (dq, dk, dv, dh0) as the reference does for g_gamma (dh0 when h0 is given,
+    else None).  The reference rejects a per-token g here; this backend also accepts one
+    (gate options of tops/cpu/ops/simple_gla/chunk.py:668-788) and then returns
+    (dq, dk, dv, dh0, dg) with dg [B,T,H] fp32."""
+    del interpret
+    cu_seqlens = _alias(cu_seqlens, cu_seqlens_cpu if cu_seqlens_cpu is not None else cu_seqlens_dev,
+                        "cu_seqlens", "cu_seqlens_cpu")
+    dq, dk, dv, dg, dh0 = _bwd_all(q, k, v, do, g, g_gamma, scale, h0, dht, cu_seqlens)
+    return (dq, dk, dv, dh0) if g is None else (dq, dk, dv, dh0, dg)
+
+
+def _bwd_all(q, k, v, do, g, g_gamma, scale, h0, dht, cu_seqlens):
     mode, gt = _gate(q, g, g_gamma)
     check_qkv(q, k, v, h0, cu_seqlens)
     if scale is None:

@@ -1,0 +1,52 @@
+"""Host-side checks of the stage / export surface (CPU, no kernel calls): the names each
+package exports at the reference's import paths and the argument errors raised before
+any device work."""
+import pytest
+import torch
+
+
+def test_gla_exports_match_reference_names():
+    import tops.ops.gla as G
+    # tops/ops/gla/__init__.py:19-35
+    names = ["naive_recurrent_gla", "chunk_gla", "chunk_local_cumsum", "chunk_fwd_h",
+             "chunk_gla_fwd_intra_gk", "chunk_gla_fwd_o_gk", "chunk_gla_fwd",
+             "chunk_gla_bwd_dA_ref", "chunk_gla_bwd_dv_ref", "chunk_gla_bwd_dqk_intra_ref",
+             "chunk_gla_bwd_dqkg_ref", "chunk_gla_bwd", "fused_chunk_gla",
+             "fused_recurrent_gla", "fused_recurrent_gla_bwd"]
+    for n in names:
+        assert n in G.__all__ and callable(getattr(G, n)), n
+
+
+def test_simple_gla_and_ops_exports():
+    import importlib
+    import tops.ops as OPS
+    # tops.ops re-exports the simple_gla function under the subpackage's name (as the
+    # reference does), so fetch the subpackage itself from the import system
+    S = importlib.import_module("tops.ops.simple_gla")
+    assert OPS.__all__ == ["chunk_kda", "chunk_kda_fwd", "fused_recurrent_kda", "simple_gla"]
+    for n in ("simple_gla", "chunk_simple_gla", "chunk_simple_gla_fwd",
+              "chunk_simple_gla_fwd_varlen", "chunk_simple_gla_bwd", "fused_chunk_simple_gla",
+              "fused_chunk_simple_gla_fwd", "fused_chunk_simple_gla_bwd",
+              "fused_recurrent_simple_gla", "simple_gla_naive", "SimpleGLAKernelMode",
+              "simple_gla_fwd", "simple_gla_bwd"):
+        assert hasattr(S, n), n
+    assert [m.value for m in S.SimpleGLAKernelMode] == ["chunk", "fused_chunk"]
+
+
+def test_common_exports():
+    from tops.ops.common import chunk_h, cumsum
+    for n in ("chunk_fwd_h_ref", "chunk_fwd_h_kernel", "chunk_bwd_dh_ref", "chunk_bwd_dh_kernel"):
+        assert callable(getattr(chunk_h, n))
+    assert callable(cumsum.chunk_local_cumsum_vector)
+
+
+def test_argument_errors_before_device_work():
+    from tops.ops.common.cumsum import chunk_local_cumsum_vector
+    from tops.ops.simple_gla import simple_gla_bwd
+    g = torch.zeros(1, 8, 1, 4)
+    with pytest.raises(AssertionError, match="power of 2"):
+        chunk_local_cumsum_vector(g, 12)
+    with pytest.raises(AssertionError, match="4-D"):
+        chunk_local_cumsum_vector(torch.zeros(8, 4), 8)
+    with pytest.raises(Exception, match="not support"):
+        simple_gla_bwd(g, g, g, g, g_gamma=torch.zeros(1), mode="bogus")
