@@ -432,6 +432,19 @@ int tops_gla_stage_dqkg(const void* q, const void* k, const void* v, const void*
                         const float* dk, float* dq_out, float* dk_out, float* dg, int B, int T,
                         int H, int K, int V, int chunk_size, float scale, void* stream);
 
+/* KDA intra-chunk backward through Aqk and Akk, with E_ij = 2^{g_i - g_j} per channel (g the
+ * chunk-local gate cumsum in log2 units) and dAqk, dAkk [B,T,H,C] used on i >= j:
+ *   dq_i = sum_j dAqk_ij k_j E_ij;  row_i = sum_j dAkk_ij k_j E_ij;  db_i = row_i . k_i;
+ *   dk = beta_i row_i + sum_i dAqk_ij q_i E_ij + sum_i beta_i dAkk_ij k_i E_ij (column sums);
+ *   dg_i = q_i dq_i + k_i beta_i row_i - k_i (column sums)  (no ln 2 factor, as the reference).
+ * Writes the intra parts only: dq, dk, dg [B,T,H,K] and db [B,T,H] fp32; beta fp32 [B,T,H].
+ * chunk_size 16, 32 or 64.  Replaces chunk_kda_bwd_intra (tops/ops/kda/chunk_intra.py:477-574,
+ * K17 :283-386; CPU tier tops/cpu/ops/kda/chunk_intra.py:16-200). */
+int tops_kda_stage_intra_bwd(const void* q, const void* k, int dtype, const float* g,
+                             const float* beta, const float* dAqk, const float* dAkk, float* dq,
+                             float* dk, float* db, float* dg, int B, int T, int H, int K,
+                             int chunk_size, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

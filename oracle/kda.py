@@ -203,3 +203,30 @@ def chunk_kda_bwd(q, k, v, g, beta, scale, initial_state, do, dht, chunk_size=64
         P.update(dS=dSs, dv_new=dvn)
         return tuple(out), P
     return tuple(out)
+
+
+def chunk_kda_bwd_intra(q, k, g, beta, dAqk, dAkk, C=64):
+    """Intra-chunk backward through Aqk and Akk (tops/ops/kda/chunk_intra.py:283-386 and
+    :477-574; tops/cpu/ops/kda/chunk_intra.py:16-200).  g is the chunk-local cumsum in log2
+    units, Aqk_ij = sum_d q_id k_jd 2^(g_id - g_jd), Akk_ij = beta_i sum_d k_id k_jd
+    2^(g_id - g_jd); both upstream gradients are used on i >= j (the accelerator kernel's
+    mask).  Returns the intra parts (dq, dk, db, dg); dg is taken w.r.t. g as if the
+    exponentials were natural (no ln 2 factor), as the reference does."""
+    q, k, g, beta, dAqk, dAkk = map(f64, (q, k, g, beta, dAqk, dAkk))
+    B, T, H, K = q.shape
+    NT = T // C
+    qc, kc, gc = (x.reshape(B, NT, C, H, K) for x in (q, k, g))
+    bc = beta.reshape(B, NT, C, H)
+    m = np.tril(np.ones((C, C), bool))[None, None, :, None, :]
+    aq = np.where(m, dAqk.reshape(B, NT, C, H, C), 0.0)
+    ak = np.where(m, dAkk.reshape(B, NT, C, H, C), 0.0)
+    E = np.exp2(gc[:, :, :, None] - gc[:, :, None, :])            # [B,NT,i,j,H,K]
+    dq = np.einsum("bnihj,bnjhk,bnijhk->bnihk", aq, kc, E)
+    row = np.einsum("bnihj,bnjhk,bnijhk->bnihk", ak, kc, E)
+    db = np.sum(row * kc, axis=-1)
+    dkrow = bc[..., None] * row
+    dkcol = np.einsum("bnihj,bnihk,bnijhk->bnjhk", aq, qc, E) \
+        + np.einsum("bnihj,bnih,bnihk,bnijhk->bnjhk", ak, bc, kc, E)
+    dg = qc * dq + kc * dkrow - kc * dkcol
+    return (dq.reshape(B, T, H, K), (dkrow + dkcol).reshape(B, T, H, K), db.reshape(B, T, H),
+            dg.reshape(B, T, H, K))

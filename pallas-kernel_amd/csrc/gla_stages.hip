@@ -684,6 +684,117 @@ __global__ void __launch_bounds__(NTH) dqkg_kernel(
   }
 }
 
+// KDA intra-chunk backward (tops/ops/kda/chunk_intra.py:283-386 kernel, :477-574 wrapper):
+// with E_ij = 2^{g_i - g_j} per channel (g: chunk-local cumsum in log2 units),
+//   dq_i  = sum_{j<=i} dAqk_ij k_j E_ij,            dk_j += sum_{i>=j} dAqk_ij q_i E_ij
+//   row_i = sum_{j<=i} dAkk_ij k_j E_ij,  db_i = row_i . k_i,  dk_i += beta_i row_i
+//   dk_j += sum_{i>=j} beta_i dAkk_ij k_i E_ij
+//   dg_i  = q_i dq_i + k_i beta_i row_i - k_i (dk_i from the two column sums)
+// (the reference's gradients w.r.t. g carry no ln 2 factor).  One workgroup per (chunk, head)
+// walks K in slices of 64; E is split as 2^{g_i - gm} 2^{gm - g_j} with gm the mean of the
+// chunk's first and last gate rows.  Writes the intra parts only, fp32; C <= 64.
+template <typename TIn>
+__global__ void __launch_bounds__(NTH) kda_intra_bwd_kernel(
+    const TIn* __restrict__ q, const TIn* __restrict__ k, const float* __restrict__ g,
+    const float* __restrict__ beta, const float* __restrict__ dAqk,
+    const float* __restrict__ dAkk, float* __restrict__ dq, float* __restrict__ dk,
+    float* __restrict__ db, float* __restrict__ dg, int H, int K, int C) {
+  __shared__ float aq[64 * LD], ak[64 * LD], qp[64 * LD], kp[64 * LD], kn[64 * LD];
+  __shared__ float gm_s[SL], be_s[64], dbw[4][64];
+  const Geo e(H, K, 0, C);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 15, qq = lane >> 4;
+  const int MR = C / 16, lda = C + 4;
+  for (int idx = tid; idx < C * C; idx += NTH) {
+    const int i = idx / C, j = idx - i * C;
+    const bool ok = j <= i;
+    aq[i * lda + j] = ok ? dAqk[e.aof(i, j)] : 0.f;
+    ak[i * lda + j] = ok ? dAkk[e.aof(i, j)] : 0.f;
+  }
+  if (tid < C) be_s[tid] = beta[(e.tok0 + tid) * H + e.h];
+  float dbl[4][4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dbl[m][i] = 0.f;
+  for (int k0 = 0; k0 < K; k0 += SL) {
+    const int kw = min(SL, K - k0);
+    const bool active = 16 * w < kw;
+    if (tid < kw) gm_s[tid] = 0.5f * (g[e.kof(0, k0 + tid)] + g[e.kof(C - 1, k0 + tid)]);
+    __syncthreads();
+    for (int idx = tid; idx < C * SL; idx += NTH) {
+      const int i = idx >> 6, c = idx & 63;
+      float a = 0.f, b = 0.f, d = 0.f;
+      if (c < kw) {
+        const long long of = e.kof(i, k0 + c);
+        const float t = g[of] - gm_s[c];
+        const float ep = exp2f(t), en = exp2f(-t);
+        const float kv = ldx(k, of);
+        a = ldx(q, of) * ep;
+        b = kv * ep;
+        d = kv * en;
+      }
+      qp[i * LD + c] = a;
+      kp[i * LD + c] = b;
+      kn[i * LD + c] = d;
+    }
+    __syncthreads();
+    if (active) {
+      f32x4 p1[4], p2[4], p3[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) p1[m] = p2[m] = p3[m] = zero4();
+      for (int s = 0; s < C / 4; ++s) {
+        const int jr = 4 * s + qq;
+        const float bn = kn[jr * LD + 16 * w + r];
+        const float bq = qp[jr * LD + 16 * w + r];
+        const float bk = kp[jr * LD + 16 * w + r];
+        const float bej = be_s[jr];
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          if (m < MR) {
+            p1[m] = mf4(aq[(16 * m + r) * lda + jr], bn, p1[m]);
+            p2[m] = mf4(ak[(16 * m + r) * lda + jr], bn, p2[m]);
+            p3[m] = mf4(aq[jr * lda + 16 * m + r], bq, p3[m]);
+            p3[m] = mf4(ak[jr * lda + 16 * m + r] * bej, bk, p3[m]);
+          }
+      }
+      const int ch = k0 + 16 * w + r;
+      const float gm = gm_s[16 * w + r];
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        if (m < MR) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int row = 16 * m + 4 * qq + i;
+            const long long of = e.kof(row, ch);
+            const float t = g[of] - gm;
+            const float ep = exp2f(t), en = exp2f(-t);
+            const float qv = ldx(q, of), kv = ldx(k, of);
+            const float dqv = p1[m][i] * ep, rowv = p2[m][i] * ep;
+            const float dkrow = be_s[row] * rowv, dkcol = p3[m][i] * en;
+            dq[of] = dqv;
+            dk[of] = dkrow + dkcol;
+            dg[of] = qv * dqv + kv * dkrow - kv * dkcol;
+            dbl[m][i] += rowv * kv;
+          }
+        }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = dbl[m][i];
+      v += __shfl_xor(v, 1, 64);
+      v += __shfl_xor(v, 2, 64);
+      v += __shfl_xor(v, 4, 64);
+      v += __shfl_xor(v, 8, 64);
+      if (r == 0 && m < MR) dbw[w][16 * m + 4 * qq + i] = v;
+    }
+  __syncthreads();
+  if (tid < C) db[(e.tok0 + tid) * H + e.h] = dbw[0][tid] + dbw[1][tid] + dbw[2][tid] + dbw[3][tid];
+}
+
 bool chunk_ok(int C) { return C == 16 || C == 32 || C == 64 || C == 128; }
 
 int launch_status() {
@@ -937,5 +1048,30 @@ extern "C" int tops_gla_stage_dqkg(const void* q, const void* k, const void* v, 
                                                (const uint16_t*)v, (const uint16_t*)do_, g, h,
                                                dh, dq, dk, dq_out, dk_out, dg, H, K, V,
                                                chunk_size, scale);
+  return launch_status();
+}
+
+extern "C" int tops_kda_stage_intra_bwd(const void* q, const void* k, int dtype, const float* g,
+                                        const float* beta, const float* dAqk, const float* dAkk,
+                                        float* dq, float* dk, float* db, float* dg, int B, int T,
+                                        int H, int K, int chunk_size, void* stream) {
+  const char* fn = "kda_stage_intra_bwd";
+  if (!q || !k || !g || !beta || !dAqk || !dAkk || !dq || !dk || !db || !dg)
+    return tops_set_error(TOPS_ERR_NULL, "kda_stage_intra_bwd: null tensor");
+  STAGE_TRY(stage_check(fn, B, T, H, chunk_size, dtype));
+  STAGE_TRY(dim16(fn, "K", K));
+  if (chunk_size > 64)
+    return tops_set_error(TOPS_ERR_UNSUPPORTED, "kda_stage_intra_bwd: chunk_size must be 16, 32 or 64");
+  if (T == 0) return TOPS_OK;
+  const int grid = B * (T / chunk_size) * H;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == TOPS_F32)
+    kda_intra_bwd_kernel<float><<<grid, NTH, 0, s>>>((const float*)q, (const float*)k, g, beta,
+                                                     dAqk, dAkk, dq, dk, db, dg, H, K,
+                                                     chunk_size);
+  else
+    kda_intra_bwd_kernel<uint16_t><<<grid, NTH, 0, s>>>((const uint16_t*)q, (const uint16_t*)k, g,
+                                                        beta, dAqk, dAkk, dq, dk, db, dg, H, K,
+                                                        chunk_size);
   return launch_status();
 }

@@ -63,6 +63,7 @@ SIGNATURES = {
     "tops_gla_stage_dv": [_vp, _vp, _i32, _vp, _vp, _vp, _vp] + [_i32] * 6 + [_vp],
     "tops_gla_stage_dqk_intra": [_vp, _vp, _i32, _vp, _vp, _vp, _vp] + [_i32] * 5 + [_vp],
     "tops_gla_stage_dqkg": [_vp, _vp, _vp, _vp, _i32] + [_vp] * 8 + [_i32] * 6 + [_f32, _vp],
+    "tops_kda_stage_intra_bwd": [_vp, _vp, _i32] + [_vp] * 8 + [_i32] * 5 + [_vp],
 }
 
 _lib = None

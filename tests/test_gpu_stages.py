@@ -338,3 +338,56 @@ def test_stages_compose_to_chunk_gla(dt, cuda_device):
         print("vs chunk_gla: " + " ".join(f"{n}={e:.2e}" for n, e in errs.items()))
         for n, e in errs.items():
             assert e < 1e-4, (n, e)
+
+
+# tests/ops/kda/test_chunk_kda_tpu.py:31-52 (shapes as NT chunks of C)
+KDA_INTRA = [
+    dict(B=2, H=4, NT=2, C=16, K=32), dict(B=1, H=2, NT=4, C=16, K=16),
+    dict(B=2, H=4, NT=1, C=32, K=16), dict(B=1, H=2, NT=2, C=64, K=32),
+    dict(B=1, H=2, NT=2, C=16, K=64), dict(B=1, H=2, NT=2, C=16, K=128),
+    dict(B=2, H=1, NT=2, C=16, K=32), dict(B=1, H=1, NT=4, C=32, K=64),
+    dict(B=1, H=2, NT=3, C=16, K=32), dict(B=2, H=4, NT=5, C=16, K=16),
+    dict(B=1, H=2, NT=7, C=32, K=32), dict(B=4, H=4, NT=2, C=16, K=32),
+    dict(B=8, H=2, NT=2, C=16, K=16), dict(B=2, H=8, NT=4, C=16, K=16),
+    dict(B=1, H=4, NT=8, C=16, K=16), dict(B=1, H=4, NT=16, C=64, K=128),
+    dict(B=1, H=2, NT=3, C=64, K=80),
+]
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("c", KDA_INTRA, ids=lambda c: "B{B}-H{H}-NT{NT}-C{C}-K{K}".format(**c))
+def test_chunk_kda_bwd_intra(c, dt, cuda_device):
+    from tops.ops.kda import chunk_kda_bwd_intra
+    from oracle import kda as KO
+    B, H, NT, C, K = (c[x] for x in ("B", "H", "NT", "C", "K"))
+    T = NT * C
+    print(f"kda intra bwd B={B} H={H} T={T} C={C} K={K} {dt}", flush=True)
+    rng = np.random.default_rng(B * 1000 + H * 100 + NT * 10 + K)
+    q, k = (rng.standard_normal((B, T, H, K)).astype(np.float32) * 0.5 for _ in range(2))
+    g = (OC.chunk_local_cumsum(-np.abs(rng.standard_normal((B, T, H, K))) * 0.1, C)
+         / np.log(2.0)).astype(np.float32)
+    beta = (1 / (1 + np.exp(-rng.standard_normal((B, T, H))))).astype(np.float32)
+    tri = np.tril(np.ones((C, C)))[None, None, :, None, :]
+    stri = np.tril(np.ones((C, C)), -1)[None, None, :, None, :]
+    dAqk = (rng.standard_normal((B, NT, C, H, C)) * tri).reshape(B, T, H, C).astype(np.float32)
+    dAkk = (rng.standard_normal((B, NT, C, H, C)) * stri).reshape(B, T, H, C).astype(np.float32)
+    inc = [rng.standard_normal(s).astype(np.float32) for s in ((B, T, H, K), (B, T, H, K),
+                                                                (B, T, H), (B, T, H, K))]
+    f = lambda x: to_dev(x, torch.float32, cuda_device)
+    sq, sk = seen(q, dt), seen(k, dt)
+    rq, rk, rb, rg = KO.chunk_kda_bwd_intra(sq, sk, g, beta, dAqk, dAkk, C)
+    # standalone: outputs in q's dtype
+    out = chunk_kda_bwd_intra(to_dev(q, dt, cuda_device), to_dev(k, dt, cuda_device), f(g), f(beta),
+                              f(dAqk), f(dAkk), chunk_size=C)
+    assert all(o.dtype == dt for o in out)
+    errs = {n: rel(host(o), r) for n, o, r in zip(("dq", "dk", "db", "dg"), out, (rq, rk, rb, rg))}
+    # accumulating into fp32 incoming gradients
+    out2 = chunk_kda_bwd_intra(to_dev(q, dt, cuda_device), to_dev(k, dt, cuda_device), f(g), f(beta),
+                               f(dAqk), f(dAkk), *(f(x) for x in inc), chunk_size=C)
+    for n, o, r, x in zip(("dq", "dk", "db", "dg"), out2, (rq, rk, rb, rg), inc):
+        assert o.dtype == torch.float32
+        errs[n + "+in"] = rel(host(o), r + x)
+    print(" ".join(f"{n}={e:.2e}" for n, e in errs.items()))
+    for n, e in errs.items():
+        lim = F32 if ("+in" in n or dt == torch.float32) else BF
+        assert e < lim, (n, e)

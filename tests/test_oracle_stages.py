@@ -75,3 +75,36 @@ def test_scalar_gate_equals_broadcast_channel_gate():
     ramp = np.broadcast_to(gam, (B, T, H))
     np.testing.assert_allclose(OC.chunk_local_cumsum(ramp, C).reshape(B, T // C, C, H)[:, 0, :, 1],
                                np.outer(np.ones(B), (np.arange(C) + 1) * gam[1]), rtol=1e-13)
+
+
+def test_kda_bwd_intra_against_autograd():
+    """chunk_kda_bwd_intra = the float64 autograd of L = sum(dAqk * Aqk) + sum(dAkk * Akk)
+    (with the i >= j masks), dg scaled by 1 / ln 2 (the reference drops that factor)."""
+    import torch
+    from oracle import kda as KO
+    rng = np.random.default_rng(5)
+    B, T, H, K, C = 1, 32, 2, 8, 16
+    q, k = rng.standard_normal((2, B, T, H, K)) * 0.5
+    g = OC.chunk_local_cumsum(-np.abs(rng.standard_normal((B, T, H, K))) * 0.3, C)
+    beta = 1 / (1 + np.exp(-rng.standard_normal((B, T, H))))
+    dAqk, dAkk = rng.standard_normal((2, B, T, H, C))
+    tq, tk, tg, tb = (torch.tensor(x, requires_grad=True) for x in (q, k, g, beta))
+    NT = T // C
+    mask = torch.tril(torch.ones(C, C, dtype=torch.bool))[None, None, :, None, :]
+    q5, k5, g5 = (x.reshape(B, NT, C, H, K) for x in (tq, tk, tg))
+    b5 = tb.reshape(B, NT, C, H)
+    E = torch.exp2(g5[:, :, :, None] - g5[:, :, None, :])
+    Aqk = torch.einsum("bnihk,bnjhk,bnijhk->bnihj", q5, k5, E)
+    Akk = b5[..., None] * torch.einsum("bnihk,bnjhk,bnijhk->bnihj", k5, k5, E)
+    uq = torch.tensor(dAqk).reshape(B, NT, C, H, C)
+    uk = torch.tensor(dAkk).reshape(B, NT, C, H, C)
+    L = (torch.where(mask, uq, 0.0) * Aqk).sum() + (torch.where(mask, uk, 0.0) * Akk).sum()
+    gq, gk_, gg, gb = torch.autograd.grad(L, (tq, tk, tg, tb))
+    dq, dk, db, dg = KO.chunk_kda_bwd_intra(q, k, g, beta, dAqk, dAkk, C)
+    np.testing.assert_allclose(dq, gq.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dk, gk_.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(db, gb.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dg, gg.numpy() / np.log(2.0), rtol=1e-10, atol=1e-12)
+    # a planted mistake (beta on the column instead of the row) is caught
+    bad = KO.chunk_kda_bwd_intra(q, k, g, np.roll(beta, 1, axis=1), dAqk, dAkk, C)[1]
+    assert np.abs(bad - gk_.numpy()).max() > 1e-3

@@ -33,6 +33,12 @@ def test_simple_gla_and_ops_exports():
     assert [m.value for m in S.SimpleGLAKernelMode] == ["chunk", "fused_chunk"]
 
 
+def test_kda_exports_match_reference_names():
+    import tops.ops.kda as KD
+    for n in ("chunk_kda", "chunk_kda_fwd", "fused_recurrent_kda", "chunk_kda_bwd_intra"):
+        assert n in KD.__all__ and callable(getattr(KD, n)), n
+
+
 def test_common_exports():
     from tops.ops.common import chunk_h, cumsum
     for n in ("chunk_fwd_h_ref", "chunk_fwd_h_kernel", "chunk_bwd_dh_ref", "chunk_bwd_dh_kernel"):
