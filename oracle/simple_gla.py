@@ -215,3 +215,29 @@ def naive_simple_gla(q, k, v, g=None, g_gamma=None, scale=None, initial_state=No
             o[b, t] = np.einsum("hkv,hk->hv", h, q[b, t] * scale)
         hts.append(h)
     return o, (np.stack(hts) if output_final_state else None)
+
+
+def chunk_bwd_dqkwg_raw_dg(q, k, v, h, do, dh, g_cumsum, scale, C):
+    """The raw per-position gate gradient of tops/ops/common/chunk_o.py:780-835 (per-token g):
+    sum over channels of q dq_gate - k dk_gate, plus the row sums minus the column sums of
+    ds2 = causal(do v^T e^{g_i - g_j}) scale * (q k^T), and the chunk-end term
+    e^{g_last} sum(h dh) + sum(dk_gate k) added at each chunk's last position; not
+    reverse-cumsummed.  g_cumsum [B,T,H]; h, dh [B,NT,H,K,V]."""
+    q, k, v, h, do, dh, g = map(f64, (q, k, v, h, do, dh, g_cumsum))
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    NT = T // C
+    qc, kc = (x.reshape(B, NT, C, H, K) for x in (q, k))
+    vc, dc = (x.reshape(B, NT, C, H, V) for x in (v, do))
+    gc = g.reshape(B, NT, C, H)
+    gl = gc[:, :, -1]                                              # [B,NT,H]
+    dq_gate = np.einsum("bnchv,bnhkv->bnchk", dc, h) * np.exp(gc)[..., None] * scale
+    dk_gate = np.einsum("bnchv,bnhkv->bnchk", vc, dh) * np.exp(gl[:, :, None] - gc)[..., None]
+    last = np.exp(gl) * np.einsum("bnhkv,bnhkv->bnh", h, dh) + np.einsum("bnchk,bnchk->bnh", dk_gate, kc)
+    m = np.tril(np.ones((C, C), bool))[None, None, :, :, None]
+    ds = np.einsum("bnihv,bnjhv->bnijh", dc, vc) * np.exp(gc[:, :, :, None] - gc[:, :, None, :])
+    ds2 = np.where(m, ds, 0.0) * scale * np.einsum("bnihk,bnjhk->bnijh", qc, kc)
+    raw = (np.sum(dq_gate * qc, -1) - np.sum(kc * dk_gate, -1)
+           + ds2.sum(axis=3) - ds2.sum(axis=2))
+    raw[:, :, -1] += last
+    return raw.reshape(B, T, H)

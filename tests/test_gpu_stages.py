@@ -391,3 +391,77 @@ def test_chunk_kda_bwd_intra(c, dt, cuda_device):
     for n, e in errs.items():
         lim = F32 if ("+in" in n or dt == torch.float32) else BF
         assert e < lim, (n, e)
+
+
+SIMPLE_CASES = [
+    dict(B=2, T=128, H=2, K=64, V=64, C=32, gate="g"),
+    dict(B=1, T=256, H=4, K=128, V=128, C=64, gate="g_gamma"),
+    dict(B=2, T=128, H=2, K=128, V=64, C=64, gate="both"),
+    dict(B=1, T=64, H=2, K=32, V=48, C=16, gate="none"),
+]
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("c", SIMPLE_CASES, ids=lambda c: "{gate}-B{B}-T{T}-K{K}-V{V}-C{C}".format(**c))
+def test_simple_gla_common_stages(c, dt, cuda_device):
+    """tops.ops.common.chunk_o / fused_chunk: the scalar-gate stages against the GLA oracle
+    stages on the gate broadcast over K (and the raw-dg oracle)."""
+    from tops.ops.common import (chunk_bwd_dqkwg, chunk_bwd_dv, chunk_fwd_o,
+                                 chunk_simple_gla_bwd_o_pl, fused_chunk_fwd)
+    from oracle import simple_gla as SO
+    B, T, H, K, V, C = (c[x] for x in ("B", "T", "H", "K", "V", "C"))
+    NT = T // C
+    print(f"simple stages {c} {dt}", flush=True)
+    rng = np.random.default_rng(T + K + V + C + len(c["gate"]))
+    q, k = (rng.standard_normal((B, T, H, K)).astype(np.float32) for _ in range(2))
+    v, do = (rng.standard_normal((B, T, H, V)).astype(np.float32) for _ in range(2))
+    hs, dh = rng.standard_normal((2, B, NT, H, K, V)) * 0.3
+    h0 = rng.standard_normal((B, H, K, V)) * 0.3
+    g = OC.chunk_local_cumsum(-np.abs(rng.standard_normal((B, T, H))) * 0.1, C) \
+        if c["gate"] in ("g", "both") else None
+    gam = -np.linspace(0.01, 0.1, H) if c["gate"] in ("g_gamma", "both") else None
+    G = np.zeros((B, T, H))
+    if g is not None:
+        G = G + g
+    if gam is not None:
+        G = G + ((np.arange(T) % C + 1)[:, None] * gam[None, :])[None]
+    Gk = np.repeat(G[..., None], K, axis=-1)
+    scale = K ** -0.5
+    d = lambda x: to_dev(x, dt, cuda_device)
+    f = lambda x: None if x is None else to_dev(x, torch.float32, cuda_device)
+    sq, sk, sv, sdo = (seen(x, dt) for x in (q, k, v, do))
+    A = O.causal_mask_A(O.chunk_gla_fwd_intra_gk(sq, sk, Gk, scale, C), C)
+    errs = {}
+    o = chunk_fwd_o(d(q), d(k), d(v), f(hs), g=f(g), g_gamma=f(gam), scale=scale, chunk_size=C)
+    assert o.dtype == dt
+    errs["o"] = (rel(host(o), O.chunk_gla_fwd_o_gk(sq, sv, Gk, A, hs, scale, C)), _lim(dt))
+    dv = chunk_bwd_dv(d(q), d(k), d(do), f(dh), g=f(g), g_gamma=f(gam), scale=scale, chunk_size=C)
+    errs["dv"] = (rel(host(dv), O.chunk_gla_bwd_dv(sk, Gk, A, sdo, dh, C)), _lim(dt))
+    dq, dk, dw, dg = chunk_bwd_dqkwg(d(q), d(k), d(v), f(hs), d(do), f(dh), g=f(g), g_gamma=f(gam),
+                                     scale=scale, chunk_size=C, w=d(k), dv=d(do))
+    dA = O.chunk_gla_bwd_dA(sv, sdo, scale, C)
+    rqi, rki = O.chunk_gla_bwd_dqk_intra(sq, sk, Gk, dA, C)
+    rq, rk, _ = O.chunk_gla_bwd_dqkg(sq, sk, sv, hs, Gk, sdo, dh, rqi, rki, scale, C)
+    errs["dq"] = (rel(host(dq), rq), F32)
+    errs["dk"] = (rel(host(dk), rk), F32)
+    rdw = -np.einsum("bnchv,bnhkv->bnchk", sdo.reshape(B, NT, C, H, V), hs).reshape(B, T, H, K)
+    errs["dw"] = (rel(host(dw), rdw), _lim(dt))
+    if g is None:
+        assert dg is None
+    else:
+        rdg = SO.chunk_bwd_dqkwg_raw_dg(sq, sk, sv, hs, sdo, dh, G, scale, C)
+        errs["dg"] = (rel(host(dg), rdg), 1e-4)
+    if gam is not None and g is None:
+        pq, pk, pv = chunk_simple_gla_bwd_o_pl(d(q), d(k), d(v), f(gam), f(hs), d(do), f(dh),
+                                               scale, C)
+        assert pq.dtype == dt and pv.dtype == dt
+        errs["pl_dq"] = (rel(host(pq), rq), _lim(dt))
+        errs["pl_dv"] = (rel(host(pv), O.chunk_gla_bwd_dv(sk, Gk, A, sdo, dh, C)), _lim(dt))
+    o2, ht = fused_chunk_fwd(d(q), d(k), d(v), g=f(g), g_gamma=f(gam), h0=f(h0), scale=scale,
+                             use_ht=True, chunk_size=C)
+    rh, rht = OC.chunk_fwd_h(sk, sv, gk=Gk, h0=h0, C=C)
+    errs["fused_o"] = (rel(host(o2), O.chunk_gla_fwd_o_gk(sq, sv, Gk, A, rh, scale, C)), _lim(dt))
+    errs["fused_ht"] = (rel(host(ht), rht), F32)
+    print(" ".join(f"{n}={e:.2e}" for n, (e, _) in errs.items()))
+    for n, (e, lim) in errs.items():
+        assert e < lim, (n, e)

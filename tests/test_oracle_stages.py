@@ -108,3 +108,24 @@ def test_kda_bwd_intra_against_autograd():
     # a planted mistake (beta on the column instead of the row) is caught
     bad = KO.chunk_kda_bwd_intra(q, k, g, np.roll(beta, 1, axis=1), dAqk, dAkk, C)[1]
     assert np.abs(bad - gk_.numpy()).max() > 1e-3
+
+
+def test_simple_gla_raw_dg_reverse_cumsum_is_the_gla_gate_gradient():
+    """Reverse-cumsumming the raw per-position dg of chunk_bwd_dqkwg inside each chunk gives
+    the GLA gate gradient (autograd-pinned oracle) of the same gate broadcast over K, summed
+    over the channels."""
+    from oracle import gla as O
+    from oracle import simple_gla as SO
+    rng = np.random.default_rng(21)
+    B, T, H, K, V, C = 1, 64, 2, 8, 4, 16
+    q, k = rng.standard_normal((2, B, T, H, K))
+    v, do = rng.standard_normal((2, B, T, H, V))
+    h, dh = rng.standard_normal((2, B, T // C, H, K, V)) * 0.3
+    g = OC.chunk_local_cumsum(-np.abs(rng.standard_normal((B, T, H))) * 0.2, C)
+    G = np.repeat(g[..., None], K, axis=-1)
+    dA = O.chunk_gla_bwd_dA(v, do, 0.5, C)
+    dqi, dki = O.chunk_gla_bwd_dqk_intra(q, k, G, dA, C)
+    _, _, dgc = O.chunk_gla_bwd_dqkg(q, k, v, h, G, do, dh, dqi, dki, 0.5, C)
+    raw = SO.chunk_bwd_dqkwg_raw_dg(q, k, v, h, do, dh, g, 0.5, C)
+    rc = OC.chunk_local_cumsum(raw, C, reverse=True)
+    np.testing.assert_allclose(rc, dgc.sum(-1), rtol=1e-10, atol=1e-10)
