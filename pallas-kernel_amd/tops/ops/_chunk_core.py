@@ -10,7 +10,20 @@ from ..utils import ChunkPlan
 GATE_K, GATE_S, GATE_GAMMA = "k", "s", "gamma"
 
 
-def check_qkv(q, k, v, initial_state, cu_seqlens):
+def tiling(K: int, V: int, tile_v: bool):
+    """Split of K (and V when tile_v) into equal slices of at most 128, multiples of 8, for
+    the kernels' K <= 128 (backward: V <= 128) limit: (nK, K slice, nV, V slice)."""
+    nk = -(-K // 128)
+    nv = -(-V // 128) if tile_v else 1
+    if K % nk or (K // nk) % 8 or V % nv or (V // nv) % 8:
+        raise NotImplementedError(f"tops-hip chunk kernels need K and V that split into equal "
+                                  f"slices of at most 128, multiples of 8 (got K={K}, V={V})")
+    return nk, K // nk, nv, V // nv
+
+
+def check_qkv(q, k, v, initial_state, cu_seqlens, split_ok: bool = False):
+    """Shape / dtype checks.  split_ok: the op is linear in its K and V slices (GLA, simple
+    GLA), so K, V > 128 run as slices (tiling); otherwise (delta rule) K <= 128."""
     assert q.ndim == 4, f"q must be [B,T,H,K], got {tuple(q.shape)}"
     B, T, H, K = q.shape
     V = v.shape[-1]
@@ -23,7 +36,9 @@ def check_qkv(q, k, v, initial_state, cu_seqlens):
     if initial_state is not None:
         assert tuple(initial_state.shape) == (n, H, K, V), (
             f"initial_state shape {tuple(initial_state.shape)} != {(n, H, K, V)}")
-    if K > 128 or K % 8 or V % 8:
+    if split_ok:
+        tiling(K, V, True)
+    elif K > 128 or K % 8 or V % 8:
         raise NotImplementedError(f"tops-hip chunk kernels need K <= 128 and K, V multiples of 8 "
                                   f"(got K={K}, V={V})")
     N.require_cuda(q, k, v, initial_state)
@@ -60,8 +75,8 @@ def _segment_states(z, y, gate, s_in, scale, sp, reverse: bool):
     return init
 
 
-def chunk_fwd(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, keep_states: bool):
-    """Run the forward chunk sweep.  gate = (mode, fp32 tensor).  Returns (o, ht, h_ckpt).
+def _fwd_tile(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, keep_states: bool):
+    """Run the forward chunk sweep on one tile (K <= 128).  gate = (mode, fp32 tensor).  Returns (o, ht, h_ckpt).
     Long or few sequences sweep as concurrent segments (plan.segments)."""
     B, T, H, K = q.shape
     V = v.shape[-1]
@@ -92,8 +107,8 @@ def chunk_fwd(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, kee
     return o, ht, hs
 
 
-def chunk_bwd(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool):
-    """Run the backward (reverse sweep + chunk-parallel dq/dk/dg).
+def _bwd_tile(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool):
+    """Run the backward (reverse sweep + chunk-parallel dq/dk/dg) on one tile (K, V <= 128).
     Returns (dq, dk, dv, dg, dh0); dg is [B,T,H,K] for GATE_K, [B,T,H] for GATE_S and None
     for GATE_GAMMA."""
     B, T, H, K = q.shape
@@ -137,3 +152,110 @@ def chunk_bwd(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool
     if sp is not None and fin is not None:
         dh0 = fin.index_select(0, sp.first_dev)
     return dq, dk, dv, dg, dh0
+
+
+_KERNEL_DTYPES = (torch.float32, torch.bfloat16)
+
+
+def _direct(q, K, V, tile_v):
+    return q.dtype in _KERNEL_DTYPES and K <= 128 and (V <= 128 or not tile_v)
+
+
+def _k_gate(gate, ks):
+    mode, gt = gate
+    return (mode, gt[..., ks].contiguous()) if mode == GATE_K else gate
+
+
+def chunk_fwd(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, keep_states: bool):
+    """Forward of GLA / simple GLA.  Returns (o, ht, h_ckpt).
+
+    K > 128 (and V > 128 when states are kept for the backward) runs as equal slices: the
+    recurrence is separate per state entry, so the output is the sum of the K slices'
+    outputs and the V slices are independent.  Such calls, and dtypes the kernels do not
+    take (fp16), compute in fp32 and cast o back; h_ckpt then holds the slices' checkpoints
+    as [slices, chunks, H, K/nK, V/nV]."""
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    if _direct(q, K, V, keep_states):
+        return _fwd_tile(q, k, v, gate, h0, scale, output_final_state, plan, keep_states)
+    nk, Kp, nv, Vp = tiling(K, V, keep_states)
+    f32 = torch.float32
+    qf, kf, vf = (x.to(f32) for x in (q, k, v))
+    o = torch.zeros(B, T, H, V, device=q.device, dtype=f32)
+    ht = torch.empty(plan.N, H, K, V, device=q.device, dtype=f32) if output_final_state else None
+    hs = torch.empty(nk * nv, plan.total, H, Kp, Vp, device=q.device, dtype=f32) \
+        if keep_states else None
+    for a in range(nk):
+        ks = slice(a * Kp, (a + 1) * Kp)
+        qa, ka, ga = qf[..., ks].contiguous(), kf[..., ks].contiguous(), _k_gate(gate, ks)
+        for b in range(nv):
+            vs = slice(b * Vp, (b + 1) * Vp)
+            h0ab = None if h0 is None else h0[:, :, ks, vs].contiguous()
+            oab, htab, hsab = _fwd_tile(qa, ka, vf[..., vs].contiguous(), ga, h0ab, scale,
+                                        output_final_state, plan, keep_states)
+            o[..., vs] += oab
+            if ht is not None:
+                ht[:, :, ks, vs] = htab
+            if hs is not None:
+                hs[a * nv + b] = hsab
+    return o.to(v.dtype), ht, hs
+
+
+def chunk_bwd(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool):
+    """Backward of GLA / simple GLA.  Returns (dq, dk, dv, dg, dh0); dg is [B,T,H,K] for
+    GATE_K, [B,T,H] for GATE_S and None for GATE_GAMMA.  Sliced as chunk_fwd: dq, dk and a
+    per-channel dg are the sums over the V slices, dv (and a scalar-gate dg) the sums over
+    the K slices."""
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    if _direct(q, K, V, True) and hs.dim() == 4:
+        return _bwd_tile(q, k, v, gate, do, dht, hs, scale, plan, want_dh0)
+    nk, Kp, nv, Vp = tiling(K, V, True)
+    f32 = torch.float32
+    qf, kf, vf, dof = (x.to(f32) for x in (q, k, v, do))
+    mode = gate[0]
+    dq = torch.zeros(B, T, H, K, device=q.device, dtype=f32)
+    dk = torch.zeros_like(dq)
+    dv = torch.zeros(B, T, H, V, device=q.device, dtype=f32)
+    dg = torch.zeros_like(dq) if mode == GATE_K else \
+        torch.zeros(B, T, H, device=q.device, dtype=f32) if mode == GATE_S else None
+    dh0 = torch.empty(plan.N, H, K, V, device=q.device, dtype=f32) if want_dh0 else None
+    for a in range(nk):
+        ks = slice(a * Kp, (a + 1) * Kp)
+        qa, ka, ga = qf[..., ks].contiguous(), kf[..., ks].contiguous(), _k_gate(gate, ks)
+        for b in range(nv):
+            vs = slice(b * Vp, (b + 1) * Vp)
+            dhtab = None if dht is None else dht[:, :, ks, vs].contiguous()
+            dqa, dka, dvb, dga, dh0ab = _bwd_tile(qa, ka, vf[..., vs].contiguous(), ga,
+                                                   dof[..., vs].contiguous(), dhtab, hs[a * nv + b],
+                                                   scale, plan, want_dh0)
+            dq[..., ks] += dqa
+            dk[..., ks] += dka
+            dv[..., vs] += dvb
+            if mode == GATE_K:
+                dg[..., ks] += dga
+            elif mode == GATE_S:
+                dg += dga
+            if dh0 is not None:
+                dh0[:, :, ks, vs] = dh0ab
+    return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg, dh0
+
+
+def states_full(hs, K: int, V: int):
+    """Checkpoints [chunks, H, K, V] from chunk_fwd's h_ckpt (whole or sliced)."""
+    if hs.dim() == 4:
+        return hs
+    nk, Kp, nv, Vp = tiling(K, V, True)
+    n, H = hs.shape[1], hs.shape[2]
+    return hs.reshape(nk, nv, n, H, Kp, Vp).permute(2, 3, 0, 4, 1, 5).reshape(n, H, K, V)
+
+
+def states_for_bwd(hs, q, V: int):
+    """chunk_bwd's h_ckpt layout for whole checkpoints [chunks, H, K, V]."""
+    K = q.shape[-1]
+    if _direct(q, K, V, True):
+        return hs
+    nk, Kp, nv, Vp = tiling(K, V, True)
+    n, H = hs.shape[0], hs.shape[1]
+    return hs.reshape(n, H, nk, Kp, nv, Vp).permute(2, 4, 0, 1, 3, 5).reshape(nk * nv, n, H, Kp, Vp) \
+        .contiguous()

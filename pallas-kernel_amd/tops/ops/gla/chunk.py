@@ -17,11 +17,12 @@ from __future__ import annotations
 import torch
 
 from ...utils import ChunkPlan
-from .._chunk_core import GATE_K, check_qkv, chunk_fwd as _core_fwd, chunk_bwd as _core_bwd
+from .._chunk_core import (GATE_K, check_qkv, chunk_fwd as _core_fwd, chunk_bwd as _core_bwd,
+                           states_for_bwd, states_full)
 
 
 def _check(q, k, v, g, initial_state, cu_seqlens):
-    check_qkv(q, k, v, initial_state, cu_seqlens)
+    check_qkv(q, k, v, initial_state, cu_seqlens, split_ok=True)
     B, T, H, K = q.shape
     assert g is None or tuple(g.shape) == (B, T, H, K), f"g shape {tuple(g.shape)} != {(B, T, H, K)}"
 
@@ -123,7 +124,7 @@ def chunk_gla_fwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, output_fi
     h0 = None if initial_state is None else initial_state.contiguous().to(torch.float32)
     o, ht, hs = _fwd(q.contiguous(), k.contiguous(), v.contiguous(), g32, h0, scale,
                      output_final_state, plan, keep_states=True)
-    h = hs.reshape(1 if plan.varlen else B, -1, H, K, V)
+    h = states_full(hs, K, V).reshape(1 if plan.varlen else B, -1, H, K, V)
     return None, None, h, ht, o
 
 
@@ -148,7 +149,7 @@ def chunk_gla_bwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, h, A, do,
     if h is None:
         _, _, hs = _fwd(q, k, v, g32, h0, scale, False, plan, keep_states=True)
     else:
-        hs = h.reshape(plan.total, H, K, V).contiguous().to(torch.float32)
+        hs = states_for_bwd(h.reshape(plan.total, H, K, V).contiguous().to(torch.float32), q, V)
     want_dh0 = initial_state is not None or dht is not None
     dq, dk, dv, dg, dh0 = _bwd(q, k, v, g32, do.contiguous().to(q.dtype),
                                None if dht is None else dht.contiguous().to(torch.float32),

@@ -93,7 +93,7 @@ def chunk_simple_gla(
     Returns (o [B,T,H,V] in q.dtype, final_state [N,H,K,V] fp32 or None)."""
     assert chunk_size > 0, "chunk_size must be positive"
     mode, gt = _gate(q, g, g_gamma)
-    check_qkv(q, k, v, initial_state, cu_seqlens)
+    check_qkv(q, k, v, initial_state, cu_seqlens, split_ok=True)
     if scale is None:
         scale = q.shape[-1] ** -0.5
     o, ht = _ChunkSimpleGLA.apply(q, k, v, gt, initial_state, mode, float(scale),
@@ -126,7 +126,7 @@ def chunk_simple_gla_fwd(q, k, v, g=None, g_gamma=None, scale=None, initial_stat
     cu_seqlens = _alias(cu_seqlens, cu_seqlens_cpu if cu_seqlens_cpu is not None else cu_seqlens_dev,
                         "cu_seqlens", "cu_seqlens_cpu")
     mode, gt = _gate(q, g, g_gamma)
-    check_qkv(q, k, v, initial_state, cu_seqlens)
+    check_qkv(q, k, v, initial_state, cu_seqlens, split_ok=True)
     if scale is None:
         scale = q.shape[-1] ** -0.5
     plan = ChunkPlan.get(q.shape[0], q.shape[1], cu_seqlens, q.device)
@@ -173,7 +173,7 @@ def chunk_simple_gla_bwd(q, k, v, do, *, g=None, g_gamma=None, scale=None, h0=No
 
 def _bwd_all(q, k, v, do, g, g_gamma, scale, h0, dht, cu_seqlens):
     mode, gt = _gate(q, g, g_gamma)
-    check_qkv(q, k, v, h0, cu_seqlens)
+    check_qkv(q, k, v, h0, cu_seqlens, split_ok=True)
     if scale is None:
         scale = q.shape[-1] ** -0.5
     plan = ChunkPlan.get(q.shape[0], q.shape[1], cu_seqlens, q.device)

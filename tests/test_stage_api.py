@@ -56,3 +56,19 @@ def test_argument_errors_before_device_work():
         chunk_local_cumsum_vector(torch.zeros(8, 4), 8)
     with pytest.raises(Exception, match="not support"):
         simple_gla_bwd(g, g, g, g, g_gamma=torch.zeros(1), mode="bogus")
+
+
+def test_tiling_and_checkpoint_layouts():
+    """The K / V slicing of the chunk core and its checkpoint layouts (host only)."""
+    from tops.ops._chunk_core import states_for_bwd, states_full, tiling
+    assert tiling(256, 128, True) == (2, 128, 1, 128)
+    assert tiling(192, 256, True) == (2, 96, 2, 128)
+    assert tiling(64, 512, False) == (1, 64, 1, 512)
+    with pytest.raises(NotImplementedError):
+        tiling(200, 64, True)                   # 2 slices of 100: not a multiple of 8
+    hs = torch.randn(3, 2, 256, 192)
+    q = torch.zeros(1, 1, 2, 256)
+    tiles = states_for_bwd(hs, q, 192)
+    assert tiles.shape == (4, 3, 2, 128, 96)
+    assert torch.equal(tiles[1], hs[:, :, :128, 96:])
+    assert torch.equal(states_full(tiles, 256, 192), hs)
