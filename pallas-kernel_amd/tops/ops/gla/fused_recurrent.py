@@ -30,7 +30,7 @@ def _cu_dev(cu_seqlens, device):
     return torch.from_numpy(np.ascontiguousarray(np.asarray(cu_seqlens, np.int32))).to(device)
 
 
-def _check(q, k, v, gk, gv, initial_state, cu_seqlens):
+def _check(q, k, v, gk, gv, initial_state, cu_seqlens, wide_ok: bool = False):
     assert q.ndim == 4, f"q must be [B,T,H,K], got {tuple(q.shape)}"
     B, T, H, K = q.shape
     V = v.shape[-1]
@@ -43,10 +43,41 @@ def _check(q, k, v, gk, gv, initial_state, cu_seqlens):
         f"initial_state shape {tuple(initial_state.shape)} != expected {(n, H, K, V)}")
     assert cu_seqlens is None or B == 1, f"cu_seqlens requires B=1, got B={B}"
     assert q.dtype == k.dtype == v.dtype, "q, k, v must share a dtype"
-    if K > 128 or K % 4:
+    if (K > 128 and not wide_ok) or K % 4:
         raise NotImplementedError(f"tops-hip fused recurrent kernels need K <= 128, K % 4 == 0 (got K={K})")
     N.require_cuda(q, k, v, gk, gv, initial_state)
     return B, T, H, K, V, n
+
+
+def _k_slices(K: int):
+    """Equal K slices of at most 128, multiples of 4 (None when K does not split so)."""
+    n = -(-K // 128)
+    return None if K % n or (K // n) % 4 else [slice(i * (K // n), (i + 1) * (K // n))
+                                              for i in range(n)]
+
+
+def _sliced(q, k, v, gk, gv, scale, initial_state, output_final_state, reverse, cu_seqlens):
+    """fused_recurrent_gla for K > 128 or fp16 inputs, in fp32: every state entry has its own
+    recurrence, so the output is the sum of the K slices' outputs and the final state their
+    concatenation; autograd runs through the same slicing."""
+    K = q.shape[-1]
+    ks = _k_slices(K) if K > 128 else [slice(0, K)]
+    if ks is None:
+        raise NotImplementedError(f"tops-hip fused recurrent kernels need K <= 128 or K in equal "
+                                  f"slices of at most 128, multiples of 4 (got K={K})")
+    f32 = torch.float32
+    qf, kf, vf = (x.to(f32) for x in (q, k, v))
+    o, hts = None, []
+    for sl in ks:
+        h0s = None if initial_state is None else initial_state[:, :, sl]
+        os_, hs_ = _FusedRecurrentGLA.apply(qf[..., sl], kf[..., sl], vf,
+                                            None if gk is None else gk[..., sl], gv, h0s,
+                                            float(scale), bool(output_final_state), bool(reverse),
+                                            cu_seqlens)
+        o = os_ if o is None else o + os_
+        hts.append(hs_)
+    ht = torch.cat(hts, dim=2) if output_final_state else None
+    return o.to(q.dtype), ht
 
 
 def _f32(x):
@@ -120,9 +151,13 @@ def fused_recurrent_gla(q, k, v, gk=None, gv=None, scale=None, initial_state=Non
                         output_final_state=False, reverse=False, cu_seqlens=None):
     """tops/ops/gla/fused_recurrent.py:439-482 (CPU dtype contract: o in q.dtype).
     Returns (o [B,T,H,V], ht [N,H,K,V] fp32 or None)."""
-    B, T, H, K, V, n = _check(q, k, v, gk, gv, initial_state, cu_seqlens)
+    B, T, H, K, V, n = _check(q, k, v, gk, gv, initial_state, cu_seqlens, wide_ok=True)
+    wide = K > 128 or q.dtype not in (torch.float32, torch.bfloat16)
     if scale is None:
-        scale = q.shape[-1] ** -0.5
+        scale = K ** -0.5
+    if wide and not _chunked(gv, reverse, K, V):
+        return _sliced(q, k, v, gk, gv, scale, initial_state, output_final_state, reverse,
+                       cu_seqlens)
     if _chunked(gv, reverse, K, V):
         from .chunk import chunk_gla
         return chunk_gla(q, k, v, gk, scale=scale, initial_state=initial_state,

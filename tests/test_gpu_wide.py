@@ -138,3 +138,44 @@ def test_chunk_simple_gla_sliced_and_fp16(c, dt, cuda_device):
     print(" ".join(f"{n_}={e:.2e}" for n_, e in errs.items()))
     for n_, e in errs.items():
         assert e < _lim(dt), (n_, e)
+
+
+FR = [
+    dict(B=1, T=40, H=2, K=256, V=64, gv=True, reverse=False),
+    dict(B=2, T=33, H=1, K=192, V=32, gv=False, reverse=True),
+    dict(B=1, T=50, H=2, K=256, V=64, gv=False, reverse=False),
+]
+
+
+@pytest.mark.parametrize("dt", DTS, ids=IDS)
+@pytest.mark.parametrize("c", FR, ids=lambda c: "B{B}-T{T}-K{K}-V{V}-gv{gv}-rev{reverse}".format(**c))
+def test_fused_recurrent_gla_wide_and_fp16(c, dt, cuda_device):
+    from tops.ops.gla import fused_recurrent_gla
+    B, T, H, K, V = (c[x] for x in "BTHKV")
+    print(f"fused_recurrent {c} {dt}", flush=True)
+    d = gla_inputs(B, T, H, K, V, seed=T * K, h0=True, grads=True)
+    rng = np.random.default_rng(T)
+    gvn = (np.log(1 / (1 + np.exp(-rng.standard_normal((B, T, H, V))))) / 16).astype(np.float32) \
+        if c["gv"] else None
+    q, k, v = (to_dev(d[x], dt, cuda_device).requires_grad_() for x in "qkv")
+    gk = to_dev(d["g"], torch.float32, cuda_device).requires_grad_()
+    gv = None if gvn is None else to_dev(gvn, torch.float32, cuda_device).requires_grad_()
+    h0 = to_dev(d["h0"], torch.float32, cuda_device).requires_grad_()
+    o, ht = fused_recurrent_gla(q, k, v, gk, gv, initial_state=h0, output_final_state=True,
+                                reverse=c["reverse"])
+    assert o.dtype == dt and ht.shape == (B, H, K, V)
+    do = to_dev(d["do"], dt, cuda_device)
+    torch.autograd.backward((o, ht), (do, to_dev(d["dht"], torch.float32, cuda_device)))
+    sq, sk, sv, sdo = (_seen(d[x], dt) for x in ("q", "k", "v", "do"))
+    ro, rht = O.fused_recurrent_gla(sq, sk, sv, d["g"], gvn, K ** -0.5, d["h0"], True,
+                                    reverse=c["reverse"])
+    r = O.fused_recurrent_bwd(sq, sk, sv, d["g"], gvn, ro, sdo, d["dht"], K ** -0.5, d["h0"],
+                              reverse=c["reverse"])
+    errs = dict(o=rel(host(o), ro), ht=rel(host(ht), rht), dq=rel(host(q.grad), r[0]),
+                dk=rel(host(k.grad), r[1]), dv=rel(host(v.grad), r[2]), dgk=rel(host(gk.grad), r[3]),
+                dh0=rel(host(h0.grad), r[5]))
+    if gv is not None:
+        errs["dgv"] = rel(host(gv.grad), r[4])
+    print(" ".join(f"{n_}={e:.2e}" for n_, e in errs.items()))
+    for n_, e in errs.items():
+        assert e < _lim(dt), (n_, e)
