@@ -465,3 +465,44 @@ def test_simple_gla_common_stages(c, dt, cuda_device):
     print(" ".join(f"{n}={e:.2e}" for n, (e, _) in errs.items()))
     for n, (e, lim) in errs.items():
         assert e < lim, (n, e)
+
+
+@pytest.mark.parametrize("case", [dict(T=256, cu=None, h0=True), dict(T=300, cu=[0, 100, 300], h0=True),
+                                  dict(T=128, cu=None, h0=False, C=32)],
+                         ids=["fixed", "varlen", "C32-noh0"])
+def test_chunk_kda_bwd_functional(case, cuda_device):
+    """tops.ops.kda.chunk_bwd.chunk_kda_bwd (the reference's functional backward on the log2
+    gate cumsum) = chunk_kda's autograd, with dg in log2 units (ln 2 times the natural-log
+    gradient), as the reference's custom_vjp relates them (tops/ops/kda/chunk.py:230-252)."""
+    from tops.ops.kda import chunk_kda
+    from tops.ops.kda.chunk_bwd import chunk_kda_bwd
+    from tops.ops.common.cumsum import chunk_local_cumsum_vector
+    T, cu = case["T"], case["cu"]
+    B, H, K, V = 1, 2, 64, 64
+    C = case.get("C", 64)
+    gen = torch.Generator(device=cuda_device).manual_seed(T)
+    r = lambda *s: torch.randn(*s, device=cuda_device, generator=gen)
+    l2 = lambda x: x / x.norm(dim=-1, keepdim=True)
+    q, k = l2(r(B, T, H, K)), l2(r(B, T, H, K))
+    v = r(B, T, H, V)
+    g = torch.nn.functional.logsigmoid(r(B, T, H, K)) / 8
+    beta = torch.sigmoid(r(B, T, H))
+    n = 1 if cu is None else len(cu) - 1
+    h0 = r(n, H, K, V) * 0.1 if case["h0"] else None
+    do, dht = r(B, T, H, V), r(n, H, K, V) * 0.1
+    ins = [x.clone().requires_grad_() for x in (q, k, v, g, beta)]
+    hin = None if h0 is None else h0.clone().requires_grad_()
+    o, ht = chunk_kda(*ins, initial_state=hin, output_final_state=True, cu_seqlens=cu)
+    grads = torch.autograd.grad((o, ht), ins + ([hin] if hin is not None else []), (do, dht))
+    g2 = chunk_local_cumsum_vector(g, C, scale=1 / np.log(2.0), cu_seqlens=cu)
+    dq, dk, dv, db, dg, dh0, dA, dbias = chunk_kda_bwd(q, k, v, beta, None, None, K ** -0.5, h0, do,
+                                                       dht, g=g2, cu_seqlens=cu, chunk_size=C)
+    assert dA is None and dbias is None and (dh0 is None) == (h0 is None)
+    errs = dict(dq=rel(host(dq), host(grads[0])), dk=rel(host(dk), host(grads[1])),
+                dv=rel(host(dv), host(grads[2])), dg=rel(host(dg), host(grads[3]) * np.log(2.0)),
+                db=rel(host(db), host(grads[4])))
+    if h0 is not None:
+        errs["dh0"] = rel(host(dh0), host(grads[5]))
+    print(" ".join(f"{n_}={e:.2e}" for n_, e in errs.items()))
+    for n_, e in errs.items():
+        assert e < 1e-4, (n_, e)
