@@ -264,3 +264,76 @@ class SegPlan:
         (self.cu_dev, self.offsets_dev, self.seg_first_dev, self.first_dev, self.last_dev) = views[:5]
         for pc, v in ((self.fwd, views[5:9]), (self.rev, views[9:13])):
             pc.start_dev, pc.end_dev, pc.first_dev, pc.dst_dev = v
+
+
+# ---- small helpers of tops/utils.py:7-140, on torch tensors (and NumPy arrays) ----
+
+def next_power_of_2(n: int) -> int:
+    """Smallest power of 2 >= n (tops/utils.py:7-17)."""
+    return 1 if n <= 1 else 1 << (int(n) - 1).bit_length()
+
+
+def align_up(x: int, align: int) -> int:
+    """x rounded up to a multiple of align (tops/utils.py:29-31)."""
+    return cdiv(x, align) * align
+
+
+def pad_to_multiple(x, multiple, axis, val):
+    """Pad x at the end of each `axis` to a multiple of `multiple` with `val`
+    (tops/utils.py:34-60); ints or equal-length lists."""
+    multiple = [multiple] if isinstance(multiple, int) else list(multiple)
+    axis = [axis] if isinstance(axis, int) else list(axis)
+    assert len(multiple) == len(axis), (
+        f"Length of multiple {len(multiple)} must match length of axis {len(axis)}")
+    widths = [(0, 0)] * x.ndim
+    for ax, mu in zip(axis, multiple):
+        rem = x.shape[ax] % mu
+        if rem:
+            widths[ax] = (0, mu - rem)
+    if isinstance(x, np.ndarray):
+        return np.pad(x, widths, constant_values=val)
+    if not isinstance(x, torch.Tensor):
+        raise NotImplementedError(f"pad_to_multiple is not implemented for type {type(x)}")
+    flat = [p for w in reversed(widths) for p in w]
+    return torch.nn.functional.pad(x, flat, value=val)
+
+
+def assert_shape(x, expected_shape, name="tensor"):
+    """Assert that x (or every tensor of a list / tuple) has expected_shape
+    (tops/utils.py:111-124)."""
+    exp = tuple(expected_shape)
+    if isinstance(x, (list, tuple)):
+        named = isinstance(name, (list, tuple)) and len(name) == len(x)
+        for i, t in enumerate(x):
+            n = name[i] if named else f"{name}_{i}"
+            assert tuple(t.shape) == exp, f"[{n}] Expected shape {exp}, got {tuple(t.shape)}"
+    else:
+        assert tuple(x.shape) == exp, f"[{name}] Expected shape {exp}, got {tuple(x.shape)}"
+
+
+def assert_shape_or_none(x, expected_shape, name="tensor"):
+    """assert_shape skipping None entries (tops/utils.py:92-109)."""
+    if x is None:
+        return
+    if isinstance(x, (list, tuple)):
+        named = isinstance(name, (list, tuple)) and len(name) == len(x)
+        keep = [(name[i] if named else f"{name}_{i}", t) for i, t in enumerate(x) if t is not None]
+        for n, t in keep:
+            assert_shape(t, expected_shape, n)
+    else:
+        assert_shape(x, expected_shape, name)
+
+
+def export_public(current_globals) -> list:
+    """Public names a module defines itself (no leading underscore, not imported, not a
+    module) (tops/utils.py:126-140)."""
+    import types
+    mod = current_globals.get("__name__")
+    out = []
+    for n, obj in current_globals.items():
+        if n.startswith("_") or isinstance(obj, types.ModuleType):
+            continue
+        if hasattr(obj, "__module__") and obj.__module__ != mod:
+            continue
+        out.append(n)
+    return out

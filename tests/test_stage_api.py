@@ -72,3 +72,19 @@ def test_tiling_and_checkpoint_layouts():
     assert tiles.shape == (4, 3, 2, 128, 96)
     assert torch.equal(tiles[1], hs[:, :, :128, 96:])
     assert torch.equal(states_full(tiles, 256, 192), hs)
+
+
+def test_reference_utils_helpers():
+    import numpy as np
+    from tops.utils import (align_up, assert_shape, assert_shape_or_none, next_power_of_2,
+                            pad_to_multiple)
+    assert [next_power_of_2(n) for n in (1, 2, 3, 64, 65)] == [1, 2, 4, 64, 128]
+    assert align_up(65, 64) == 128 and align_up(64, 64) == 64
+    t = torch.ones(2, 5, 3)
+    p = pad_to_multiple(t, [4, 2], [1, 2], 0.0)
+    assert p.shape == (2, 8, 4) and float(p.sum()) == 30.0
+    assert pad_to_multiple(np.ones((3, 2)), 4, 0, -1).shape == (4, 2)
+    assert_shape([t, t], (2, 5, 3), ("a", "b"))
+    assert_shape_or_none([t, None], (2, 5, 3))
+    with pytest.raises(AssertionError, match=r"\[x\]"):
+        assert_shape(t, (2, 5), "x")
