@@ -32,11 +32,15 @@ def simple_gla(q, k, v, *args, g=None, g_gamma=None, scale=None, initial_state=N
         fn = chunk_simple_gla if mode == "chunk" else fused_chunk_simple_gla
         return fn(q, k, v, g_gamma, initial_state=initial_state, scale=scale,
                   output_final_state=output_final_state, chunk_size=chunk_size)
-    if mode in ("fused_recurrent", "naive"):
+    if mode == "fused_recurrent":
         return fused_recurrent_simple_gla(q, k, v, g=g, g_gamma=g_gamma, scale=scale,
                                           initial_state=initial_state,
                                           output_final_state=output_final_state, reverse=reverse,
                                           cu_seqlens=cu_seqlens_cpu)
+    if mode == "naive":
+        return simple_gla_naive(q, k, v, g=g, g_gamma=g_gamma, scale=scale,
+                                initial_state=initial_state, output_final_state=output_final_state,
+                                chunk_size=chunk_size, cu_seqlens_cpu=cu_seqlens_cpu)
     raise ValueError(f"Unknown mode {mode!r}; expected one of "
                      "'chunk', 'fused_chunk', 'fused_recurrent', 'naive'")
 
@@ -63,11 +67,12 @@ def simple_gla_naive(q, k, v, g=None, g_gamma=None, scale=None, initial_state=No
     """The reference's pure-JAX testing form (tops/ops/simple_gla/naive.py:5-100); here the
     per-token recurrence on the HIP fused_recurrent kernels (same equations).  Returns
     (o [B,T,H,V] float32, final state float32 or None) as the reference does."""
+    q, k, v = (x.float() for x in (q, k, v))      # the reference computes in fp32 throughout
     o, ht = fused_recurrent_simple_gla(q, k, v, g=g, g_gamma=g_gamma, scale=scale,
                                        initial_state=initial_state,
                                        output_final_state=output_final_state,
                                        cu_seqlens=cu_seqlens_cpu)
-    return o.float(), ht
+    return o, ht
 
 
 class SimpleGLAKernelMode(enum.Enum):

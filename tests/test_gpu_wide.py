@@ -179,3 +179,19 @@ def test_fused_recurrent_gla_wide_and_fp16(c, dt, cuda_device):
     print(" ".join(f"{n_}={e:.2e}" for n_, e in errs.items()))
     for n_, e in errs.items():
         assert e < _lim(dt), (n_, e)
+
+
+def test_simple_gla_naive_mode_returns_float32(cuda_device):
+    """simple_gla(mode='naive') goes through simple_gla_naive, whose output is float32 as the
+    reference's (tops/ops/simple_gla/__init__.py:144-155, naive.py:69-100)."""
+    from tops.ops.simple_gla import simple_gla
+    d = simple_gla_inputs(1, 33, 2, 32, 16, seed=3, h0=True)
+    q, k, v = (to_dev(d[x], torch.bfloat16, cuda_device) for x in "qkv")
+    g = to_dev(d["g"], torch.float32, cuda_device)
+    o, ht = simple_gla(q, k, v, g=g, initial_state=to_dev(d["h0"], torch.float32, cuda_device),
+                       output_final_state=True, mode="naive")
+    assert o.dtype == torch.float32 and ht.dtype == torch.float32
+    sq, sk, sv = (_seen(d[x], torch.bfloat16) for x in "qkv")
+    ro, rht = S.naive_simple_gla(sq, sk, sv, g=d["g"], initial_state=d["h0"],
+                                 output_final_state=True)
+    assert rel(host(o), ro) < 1e-4 and rel(host(ht), rht) < 1e-4
