@@ -45,6 +45,8 @@ CUMSUM_CASES = [
     dict(B=8, T=1024, H=64, K=128, C=64, hf=True),
     dict(B=1, T=2048, H=64, K=128, C=128, cu=[0, 512, 888, 2048]),
     dict(B=2, T=100, H=3, K=1, C=16, ind=torch.bfloat16),
+    dict(B=1, T=50, H=2, K=64, C=16, hf=True, reverse=True, cu=[0, 20, 50]),
+    dict(B=1, T=0, H=2, K=8, C=16),
 ]
 
 
