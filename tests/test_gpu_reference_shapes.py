@@ -1,0 +1,139 @@
+"""The reference's own chunk_gla test shapes (tests/ops/gla/test_pallas_chunk_gla.py:26-86
+and test_pallas_chunk_gla_g_gamma.py:60-74), run through tops.ops.gla.chunk_gla (forward
+and autograd backward) on MI355X against the float64 oracle: tiny and ragged T, T = 1,
+K / V from 8 to 128, custom scale, h0, chunk-aligned and chunk-crossing varlen, and the
+three g_gamma forms (scalar, per head (1,1,H,1), per head and channel (1,1,H,K)) whose
+gradient is the broadcast gate's gradient summed to g_gamma's shape.
+Tolerances (relative L2): fp32 1e-4, bf16 2e-3.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gla as O
+from _gpu import to_dev, seen, host, rel
+from _inputs import gla_inputs
+
+pytestmark = pytest.mark.gpu
+
+REF = [
+    dict(B=2, T=32, H=4, K=32, V=64), dict(B=2, T=32, H=4, K=32, V=64, h0=True),
+    dict(B=1, T=128, H=2, K=64, V=128), dict(B=2, T=32, H=1, K=32, V=64),
+    dict(B=2, T=32, H=4, K=16, V=128), dict(B=2, T=32, H=4, K=128, V=16),
+    dict(B=1, T=1, H=2, K=32, V=64), dict(B=1, T=3, H=2, K=32, V=64),
+    dict(B=2, T=37, H=4, K=16, V=32), dict(B=1, T=50, H=2, K=32, V=64),
+    dict(B=1, T=100, H=2, K=32, V=64, h0=True), dict(B=8, T=32, H=4, K=32, V=64),
+    dict(B=1, T=64, H=16, K=32, V=64), dict(B=2, T=32, H=2, K=8, V=16),
+    dict(B=2, T=32, H=2, K=8, V=16, h0=True), dict(B=1, T=16, H=1, K=16, V=16),
+    dict(B=4, T=64, H=8, K=32, V=64), dict(B=2, T=48, H=4, K=32, V=32),
+    dict(B=2, T=32, H=4, K=32, V=64, scale=0.1),
+    dict(B=1, T=32, H=4, K=32, V=64, cu=[0, 16, 32]),
+    dict(B=1, T=96, H=4, K=32, V=64, cu=[0, 32, 64, 96]),
+    dict(B=1, T=48, H=4, K=32, V=64, cu=[0, 16, 48]),
+    dict(B=1, T=64, H=2, K=16, V=32, cu=[0, 16, 48, 64]),
+    dict(B=1, T=32, H=4, K=32, V=64, cu=[0, 16, 32], h0=True),
+    dict(B=1, T=48, H=4, K=32, V=64, cu=[0, 16, 48], h0=True),
+    dict(B=1, T=64, H=2, K=16, V=32, cu=[0, 16, 32, 48, 64]),
+    dict(B=1, T=80, H=2, K=32, V=64, cu=[0, 16, 80]),
+    dict(B=1, T=64, H=2, K=32, V=64, cu=[0, 48, 64]),
+    dict(B=1, T=96, H=2, K=16, V=32, cu=[0, 16, 32, 48, 64, 80, 96]),
+    dict(B=1, T=64, H=4, K=32, V=64, cu=[0, 64]),
+    dict(B=2, T=32, H=4, K=32, V=64, scale=0.1, h0=True),
+    dict(B=1, T=32, H=4, K=32, V=64, scale=0.1, cu=[0, 16, 32]),
+    dict(B=1, T=256, H=2, K=32, V=64), dict(B=1, T=512, H=2, K=32, V=64),
+    dict(B=1, T=1024, H=2, K=32, V=64), dict(B=1, T=256, H=2, K=32, V=64, h0=True),
+    dict(B=1, T=512, H=2, K=32, V=64, h0=True), dict(B=1, T=256, H=2, K=32, V=64, scale=0.1),
+    dict(B=1, T=512, H=2, K=32, V=64, scale=0.01),
+    dict(B=1, T=256, H=2, K=32, V=64, cu=[0, 128, 256]),
+]
+
+
+def _rid(c):
+    s = "B{B}-T{T}-H{H}-K{K}-V{V}".format(**c)
+    for key in ("h0", "scale", "cu"):
+        if key in c:
+            s += f"-{key}" + (str(c[key]) if key == "scale" else "")
+    return s
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("c", REF, ids=_rid)
+def test_reference_chunk_gla_shapes(c, dt, cuda_device):
+    from tops.ops.gla import chunk_gla
+    B, T, H, K, V = (c[x] for x in "BTHKV")
+    cu = c.get("cu")
+    n = B if cu is None else len(cu) - 1
+    scale = c.get("scale", K ** -0.5)
+    print(f"ref shape {_rid(c)} {dt}", flush=True)
+    d = gla_inputs(B, T, H, K, V, seed=B * 1000 + T + K + V, gate_div=4.0, h0=c.get("h0", False),
+                   N=n, grads=True)
+    q, k, v = (to_dev(d[x], dt, cuda_device).requires_grad_() for x in "qkv")
+    g = to_dev(d["g"], torch.float32, cuda_device).requires_grad_()
+    h0 = to_dev(d["h0"], torch.float32, cuda_device)
+    if h0 is not None:
+        h0.requires_grad_()
+    o, ht = chunk_gla(q, k, v, g, scale=scale, initial_state=h0, output_final_state=True,
+                      cu_seqlens=cu)
+    torch.autograd.backward((o, ht), (to_dev(d["do"], dt, cuda_device),
+                                      to_dev(d["dht"], torch.float32, cuda_device)))
+    sq, sk, sv, sdo = (seen(d[x], dt) for x in ("q", "k", "v", "do"))
+    ro, rht = O.chunk_gla(sq, sk, sv, d["g"], scale, d["h0"], True, cu_seqlens=cu)
+    rq, rk, rv, rg, rh0 = O.chunk_gla_bwd(sq, sk, sv, d["g"], scale, d["h0"], sdo, d["dht"],
+                                          cu_seqlens=cu)
+    # outputs stored in bf16 are compared with the oracle rounded the same way (with a few
+    # hundred elements, as at T = 1 or 3, the rounding alone can approach the bound)
+    r16 = lambda x: seen(x, dt)
+    errs = dict(o=rel(host(o), r16(ro)), ht=rel(host(ht), rht), dq=rel(host(q.grad), r16(rq)),
+                dk=rel(host(k.grad), r16(rk)), dv=rel(host(v.grad), r16(rv)))
+    # dg is a difference of k * dk-sized terms (q dq - k dk + ...); with no initial state
+    # the first token's gate multiplies a zero state, so at T = 1 the exact dg is 0 and only
+    # the cancellation residue remains: measure it against the scale of those terms
+    den = max(float(np.linalg.norm(rg)), float(np.linalg.norm(sk * rk)))
+    errs["dg"] = float(np.linalg.norm(host(g.grad) - rg)) / den
+    if h0 is not None:
+        errs["dh0"] = rel(host(h0.grad), rh0)
+    print(" ".join(f"{n_}={e:.2e}" for n_, e in errs.items()))
+    lim = 1e-4 if dt == torch.float32 else 2e-3
+    for n_, e in errs.items():
+        assert e < lim, (n_, e)
+
+
+GAMMA = [
+    dict(B=2, T=32, H=4, K=32, V=64, shape="scalar"),
+    dict(B=2, T=32, H=4, K=32, V=64, shape="per_head"),
+    dict(B=2, T=32, H=4, K=32, V=64, shape="per_head_K"),
+    dict(B=1, T=64, H=2, K=16, V=32, shape="per_head_K", h0=True),
+    dict(B=4, T=48, H=2, K=32, V=64, shape="per_head"),
+    dict(B=2, T=32, H=4, K=32, V=64, shape="per_head", scale=0.1),
+    dict(B=1, T=256, H=2, K=32, V=64, shape="per_head"),
+]
+
+
+@pytest.mark.parametrize("c", GAMMA, ids=lambda c: "{shape}-B{B}-T{T}-H{H}-K{K}".format(**c))
+def test_reference_chunk_gla_g_gamma(c, cuda_device):
+    from tops.ops.gla import chunk_gla
+    B, T, H, K, V = (c[x] for x in "BTHKV")
+    scale = c.get("scale", K ** -0.5)
+    rng = np.random.default_rng(T + H)
+    gshape = {"scalar": (), "per_head": (1, 1, H, 1), "per_head_K": (1, 1, H, K)}[c["shape"]]
+    gam = (-np.abs(rng.standard_normal(gshape)) * 0.1).astype(np.float32)
+    d = gla_inputs(B, T, H, K, V, seed=T * 3 + K, h0=c.get("h0", False), grads=True)
+    f = lambda x: to_dev(x, torch.float32, cuda_device)
+    q, k, v = (f(d[x]).requires_grad_() for x in "qkv")
+    gg = torch.tensor(gam, device=cuda_device, requires_grad=True)
+    h0 = None if d["h0"] is None else f(d["h0"])
+    o, ht = chunk_gla(q, k, v, None, g_gamma=gg, scale=scale, initial_state=h0,
+                      output_final_state=True)
+    torch.autograd.backward((o, ht), (f(d["do"]), f(d["dht"])))
+    gfull = np.broadcast_to(gam, (B, T, H, K)).astype(np.float64)
+    ro, rht = O.chunk_gla(d["q"], d["k"], d["v"], gfull, scale, d["h0"], True)
+    rq, rk, rv, rg, _ = O.chunk_gla_bwd(d["q"], d["k"], d["v"], gfull, scale, d["h0"], d["do"],
+                                        d["dht"])
+    lead = 4 - len(gshape)               # g_gamma's gradient: sum over its broadcast axes
+    rgam = rg.sum(axis=tuple(i for i in range(4) if i < lead or gshape[i - lead] == 1))
+    errs = dict(o=rel(host(o), ro), ht=rel(host(ht), rht), dq=rel(host(q.grad), rq),
+                dk=rel(host(k.grad), rk), dv=rel(host(v.grad), rv),
+                dgamma=rel(host(gg.grad).reshape(-1), np.asarray(rgam).reshape(-1)))
+    print(" ".join(f"{n_}={e:.2e}" for n_, e in errs.items()))
+    for n_, e in errs.items():
+        assert e < 1e-4, (n_, e)
