@@ -137,3 +137,112 @@ def test_reference_chunk_gla_g_gamma(c, cuda_device):
     print(" ".join(f"{n_}={e:.2e}" for n_, e in errs.items()))
     for n_, e in errs.items():
         assert e < 1e-4, (n_, e)
+
+
+# tests/ops/simple_gla/test_chunk_simple_gla_tpu.py:43-74 (the T = 4096 / 8192 cases, beyond
+# what the float64 oracle checks in seconds, are left to the long-sequence tests)
+SIMPLE = [
+    dict(B=2, T=64, H=4, K=128, V=128), dict(B=2, T=128, H=4, K=128, V=128),
+    dict(B=1, T=256, H=2, K=128, V=128), dict(B=2, T=64, H=4, K=128, V=128, h0=True),
+    dict(B=2, T=128, H=4, K=128, V=128, h0=True), dict(B=1, T=256, H=2, K=128, V=128, h0=True),
+    dict(B=2, T=64, H=1, K=128, V=128), dict(B=1, T=64, H=2, K=128, V=256),
+    dict(B=2, T=64, H=4, K=256, V=128), dict(B=2, T=64, H=2, K=128, V=128),
+    dict(B=8, T=64, H=4, K=128, V=128), dict(B=1, T=128, H=16, K=128, V=128),
+    dict(B=2, T=64, H=4, K=128, V=128, scale=0.1),
+    dict(B=2, T=64, H=4, K=128, V=128, scale=0.1, h0=True),
+    dict(B=1, T=512, H=2, K=128, V=128), dict(B=1, T=512, H=2, K=128, V=128, h0=True),
+    dict(B=4, T=256, H=2, K=128, V=128), dict(B=2, T=256, H=4, K=128, V=128),
+    dict(B=1, T=256, H=2, K=128, V=128, chunk_size=128),
+    dict(B=2, T=256, H=4, K=128, V=128, chunk_size=128),
+]
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("c", SIMPLE, ids=_rid)
+def test_reference_simple_gla_shapes(c, dt, cuda_device):
+    from tops.ops.simple_gla import chunk_simple_gla
+    from oracle import simple_gla as S
+    from _inputs import simple_gla_inputs
+    B, T, H, K, V = (c[x] for x in "BTHKV")
+    scale = c.get("scale", K ** -0.5)
+    print(f"simple ref shape {_rid(c)} {dt}", flush=True)
+    d = simple_gla_inputs(B, T, H, K, V, seed=B * 100 + T + K + V, h0=c.get("h0", False),
+                          grads=True)
+    q, k, v = (to_dev(d[x], dt, cuda_device).requires_grad_() for x in "qkv")
+    gg = to_dev(d["g_gamma"], torch.float32, cuda_device)
+    h0 = to_dev(d["h0"], torch.float32, cuda_device)
+    if h0 is not None:
+        h0.requires_grad_()
+    o, ht = chunk_simple_gla(q, k, v, gg, initial_state=h0, scale=scale, output_final_state=True,
+                             chunk_size=c.get("chunk_size", 64))
+    torch.autograd.backward((o, ht), (to_dev(d["do"], dt, cuda_device),
+                                      to_dev(d["dht"], torch.float32, cuda_device)))
+    sq, sk, sv, sdo = (seen(d[x], dt) for x in ("q", "k", "v", "do"))
+    ro, rht = S.chunk_simple_gla(sq, sk, sv, g_gamma=d["g_gamma"], scale=scale,
+                                 initial_state=d["h0"], output_final_state=True)
+    rq, rk, rv, _, rh0 = S.chunk_simple_gla_bwd(sq, sk, sv, None, d["g_gamma"], d["h0"], sdo,
+                                                d["dht"], scale)
+    r16 = lambda x: seen(x, dt)
+    errs = dict(o=rel(host(o), r16(ro)), ht=rel(host(ht), rht), dq=rel(host(q.grad), r16(rq)),
+                dk=rel(host(k.grad), r16(rk)), dv=rel(host(v.grad), r16(rv)))
+    if h0 is not None:
+        errs["dh0"] = rel(host(h0.grad), rh0)
+    print(" ".join(f"{n_}={e:.2e}" for n_, e in errs.items()))
+    lim = 1e-4 if dt == torch.float32 else 2e-3
+    for n_, e in errs.items():
+        assert e < lim, (n_, e)
+
+
+# tests/ops/kda/test_chunk_kda_bwd_tpu.py:21-25
+KDA = [
+    dict(B=1, T=64, H=2, K=64, V=64), dict(B=2, T=128, H=4, K=64, V=64),
+    dict(B=1, T=256, H=2, K=128, V=128), dict(B=2, T=128, H=4, K=64, V=128, h0=True),
+    dict(B=1, T=128, H=2, K=64, V=64, h0=True),
+]
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("c", KDA, ids=_rid)
+def test_reference_kda_shapes(c, dt, cuda_device):
+    """chunk_kda forward + autograd and the functional chunk_kda_bwd on the reference's KDA
+    backward shapes, against the float64 oracle."""
+    from tops.ops.kda import chunk_kda
+    from tops.ops.kda.chunk_bwd import chunk_kda_bwd
+    from tops.ops.common.cumsum import chunk_local_cumsum_vector
+    from oracle import kda as KO
+    from _inputs import kda_inputs
+    B, T, H, K, V = (c[x] for x in "BTHKV")
+    print(f"kda ref shape {_rid(c)} {dt}", flush=True)
+    d = kda_inputs(B, T, H, K, V, seed=T + K + V + B, h0=c.get("h0", False), grads=True)
+    q, k, v = (to_dev(d[x], dt, cuda_device).requires_grad_() for x in "qkv")
+    f = lambda x: None if x is None else to_dev(x, torch.float32, cuda_device)
+    g, beta = f(d["g"]).requires_grad_(), f(d["beta"]).requires_grad_()
+    h0 = f(d["h0"])
+    if h0 is not None:
+        h0.requires_grad_()
+    o, ht = chunk_kda(q, k, v, g, beta, initial_state=h0, output_final_state=True)
+    do, dht = to_dev(d["do"], dt, cuda_device), f(d["dht"])
+    torch.autograd.backward((o, ht), (do, dht))
+    scale = K ** -0.5
+    sq, sk, sv, sdo = (seen(d[x], dt) for x in ("q", "k", "v", "do"))
+    ro, rht = KO.chunk_kda(sq, sk, sv, d["g"], d["beta"], scale, d["h0"], True)
+    rq, rk, rv, rb, rg, rh0 = KO.chunk_kda_bwd(sq, sk, sv, d["g"], d["beta"], scale, d["h0"], sdo,
+                                               d["dht"])
+    r16 = lambda x: seen(x, dt)
+    errs = dict(o=rel(host(o), r16(ro)), ht=rel(host(ht), rht), dq=rel(host(q.grad), r16(rq)),
+                dk=rel(host(k.grad), r16(rk)), dv=rel(host(v.grad), r16(rv)),
+                db=rel(host(beta.grad), rb), dg=rel(host(g.grad), rg))
+    if h0 is not None:
+        errs["dh0"] = rel(host(h0.grad), rh0)
+    # the functional backward on the log2 gate cumsum (dg in log2 units)
+    g2 = chunk_local_cumsum_vector(g.detach(), 64, scale=1 / np.log(2.0))
+    fq, fk, fv, fb, fg, fh0, _, _ = chunk_kda_bwd(q.detach(), k.detach(), v.detach(),
+                                                  beta.detach(), None, None, scale,
+                                                  None if h0 is None else h0.detach(), do, dht,
+                                                  g=g2)
+    errs["fn_dq"] = rel(host(fq), r16(rq))
+    errs["fn_dg"] = rel(host(fg) / np.log(2.0), rg)
+    print(" ".join(f"{n_}={e:.2e}" for n_, e in errs.items()))
+    lim = 1e-4 if dt == torch.float32 else 2e-3
+    for n_, e in errs.items():
+        assert e < lim, (n_, e)
