@@ -246,3 +246,83 @@ def test_reference_kda_shapes(c, dt, cuda_device):
     lim = 1e-4 if dt == torch.float32 else 2e-3
     for n_, e in errs.items():
         assert e < lim, (n_, e)
+
+
+# tests/ops/gla/test_pallas_fused_recurrent.py:26-119 (gates, reverse, varlen, scale, h0)
+FR = [
+    dict(B=2, T=32, H=4, K=32, V=64), dict(B=2, T=32, H=4, K=32, V=64, h0=True),
+    dict(B=1, T=128, H=2, K=64, V=128), dict(B=2, T=32, H=4, K=16, V=128),
+    dict(B=2, T=32, H=4, K=128, V=16), dict(B=1, T=1, H=2, K=32, V=64),
+    dict(B=1, T=3, H=2, K=32, V=64), dict(B=2, T=37, H=4, K=16, V=32),
+    dict(B=1, T=100, H=2, K=32, V=64, h0=True), dict(B=2, T=32, H=2, K=8, V=16, h0=True),
+    dict(B=2, T=32, H=4, K=32, V=64, gate="gv"), dict(B=2, T=32, H=4, K=32, V=64, gate="gk+gv"),
+    dict(B=2, T=32, H=4, K=32, V=64, gate="none"),
+    dict(B=2, T=32, H=4, K=32, V=64, reverse=True),
+    dict(B=2, T=32, H=4, K=32, V=64, reverse=True, h0=True),
+    dict(B=1, T=1, H=2, K=16, V=32, reverse=True), dict(B=2, T=32, H=4, K=32, V=64, scale=0.1),
+    dict(B=1, T=48, H=4, K=32, V=64, cu=[0, 10, 24, 48]),
+    dict(B=1, T=23, H=2, K=16, V=32, cu=[0, 7, 20, 23]),
+    dict(B=1, T=48, H=4, K=32, V=64, cu=[0, 10, 24, 48], h0=True),
+    dict(B=1, T=4, H=2, K=16, V=32, cu=[0, 1, 2, 3, 4]),
+    dict(B=1, T=67, H=2, K=32, V=64, cu=[0, 3, 67]),
+    dict(B=1, T=23, H=2, K=16, V=32, cu=[0, 7, 20, 23], reverse=True),
+    dict(B=1, T=32, H=4, K=32, V=64, gate="gk+gv", cu=[0, 16, 32]),
+    dict(B=2, T=32, H=4, K=32, V=64, gate="gv", h0=True),
+    dict(B=2, T=32, H=4, K=32, V=64, gate="gk+gv", reverse=True),
+    dict(B=1, T=32, H=4, K=32, V=64, scale=0.1, cu=[0, 16, 32]),
+    dict(B=1, T=512, H=2, K=32, V=64),
+]
+
+
+def _fid(c):
+    s = _rid(c) + "-" + c.get("gate", "gk")
+    return s + ("-rev" if c.get("reverse") else "")
+
+
+@pytest.mark.parametrize("c", FR, ids=_fid)
+def test_reference_fused_recurrent_shapes(c, cuda_device):
+    from tops.ops.gla import fused_recurrent_gla
+    B, T, H, K, V = (c[x] for x in "BTHKV")
+    cu = c.get("cu")
+    n = B if cu is None else len(cu) - 1
+    gate = c.get("gate", "gk")
+    rev = c.get("reverse", False)
+    scale = c.get("scale", K ** -0.5)
+    print(f"fused_recurrent ref shape {_fid(c)}", flush=True)
+    d = gla_inputs(B, T, H, K, V, seed=T * 7 + K + V, gate_div=4.0, h0=c.get("h0", False), N=n,
+                   grads=True)
+    rng = np.random.default_rng(T + K)
+    gvn = (np.log(1 / (1 + np.exp(-rng.standard_normal((B, T, H, V))))) / 4).astype(np.float32)
+    gkn = d["g"] if "gk" in gate else None
+    gvn = gvn if "gv" in gate else None
+    f = lambda x: None if x is None else to_dev(x, torch.float32, cuda_device)
+    q, k, v = (f(d[x]).requires_grad_() for x in "qkv")
+    gk = None if gkn is None else f(gkn).requires_grad_()
+    gv = None if gvn is None else f(gvn).requires_grad_()
+    h0 = f(d["h0"])
+    if h0 is not None:
+        h0.requires_grad_()
+    o, ht = fused_recurrent_gla(q, k, v, gk, gv, scale=scale, initial_state=h0,
+                                output_final_state=True, reverse=rev, cu_seqlens=cu)
+    torch.autograd.backward((o, ht), (f(d["do"]), f(d["dht"])))
+    ro, rht = O.fused_recurrent_gla(d["q"], d["k"], d["v"], gkn, gvn, scale, d["h0"], True,
+                                    reverse=rev, cu_seqlens=cu)
+    r = O.fused_recurrent_bwd(d["q"], d["k"], d["v"], gkn, gvn, ro, d["do"], d["dht"], scale,
+                              d["h0"], reverse=rev, cu_seqlens=cu)
+    errs = dict(o=rel(host(o), ro), ht=rel(host(ht), rht), dq=rel(host(q.grad), r[0]),
+                dk=rel(host(k.grad), r[1]), dv=rel(host(v.grad), r[2]))
+    # gate gradients are differences of k * dk (v * dv)-sized terms that cancel exactly for a
+    # sequence's first token without an initial state (T = 1, one-token sequences): measure
+    # them against the scale of those terms
+    def gerr(got, ref, x, dx):
+        den = max(float(np.linalg.norm(ref)), float(np.linalg.norm(np.asarray(x) * dx)))
+        return float(np.linalg.norm(host(got) - ref)) / den
+    if gk is not None:
+        errs["dgk"] = gerr(gk.grad, r[3], d["k"], r[1])
+    if gv is not None:
+        errs["dgv"] = gerr(gv.grad, r[4], d["v"], r[2])
+    if h0 is not None:
+        errs["dh0"] = rel(host(h0.grad), r[5])
+    print(" ".join(f"{n_}={e:.2e}" for n_, e in errs.items()))
+    for n_, e in errs.items():
+        assert e < 1e-4, (n_, e)
