@@ -34,7 +34,9 @@ extern "C" int tops_prepare_chunk_indices(const int32_t* cu_seqlens, int N, int 
   chunk_offsets[0] = 0;
   for (int n = 0; n < N; ++n) {
     const int len = cu_seqlens[n + 1] - cu_seqlens[n];
-    if (len <= 0) return tops_set_error(TOPS_ERR_SHAPE, "prepare_chunk_indices: empty or negative segment");
+    // an empty sequence has no chunk (tops/utils.py:71-90 gives it none); its state
+    // passes through unchanged
+    if (len < 0) return tops_set_error(TOPS_ERR_SHAPE, "prepare_chunk_indices: negative segment length");
     const int nc = (len + C - 1) / C;
     if (chunk_indices) {
       if (total + nc > capacity) return tops_set_error(TOPS_ERR_SHAPE, "prepare_chunk_indices: capacity");

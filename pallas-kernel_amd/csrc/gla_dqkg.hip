@@ -99,20 +99,19 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
   }
   const int t0 = c * C;
   const int nval = min(C, L - t0);
-  const long long rows_total = (long long)p.B * p.T;
   const size_t e0 = (size_t)(row0 + t0) * H + hh;
-  const long long remr = (rows_total - (row0 + t0)) * (long long)H;
+  const long long nrows = (long long)p.B * p.T * H;     // (token, head) rows of [B,T,H,.]
   const uint32_t rowK = (uint32_t)(H * K), rowV = (uint32_t)(H * V);
-  const rsrc_t Rq = make_rsrc((const TIn*)p.q + e0 * K, remr * K * ES);
-  const rsrc_t Rk = make_rsrc((const TIn*)p.k + e0 * K, remr * K * ES);
+  const rsrc_t Rq = make_rsrc_rows((const TIn*)p.q, e0, nrows, K);
+  const rsrc_t Rk = make_rsrc_rows((const TIn*)p.k, e0, nrows, K);
   const int gmode = p.gate_mode;
-  const rsrc_t Rg = make_rsrc(gmode == kGateK ? p.g + e0 * K : p.g + e0, remr * (gmode == kGateK ? K : 1) * 4);
+  const rsrc_t Rg = make_rsrc_rows(p.g, e0, nrows, gmode == kGateK ? K : 1);
   const float gam_h = gmode == kGateGamma ? p.g[hh] : 0.f;
 
   // ---------------- v / dO planes ([C][V], V contiguous)
   {
-    const rsrc_t Rv = make_rsrc((const TV*)p.v + e0 * V, remr * V * ESV);
-    const rsrc_t Rd = make_rsrc((const TIn*)p.dout + e0 * V, remr * V * ES);
+    const rsrc_t Rv = make_rsrc_rows((const TV*)p.v, e0, nrows, V);
+    const rsrc_t Rd = make_rsrc_rows((const TIn*)p.dout, e0, nrows, V);
     uint4 pv[NPTV], pd[NPT];
 #pragma unroll
     for (int i = 0; i < NPTV; ++i) {
@@ -228,12 +227,11 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
 
   const rsrc_t Rh = make_rsrc(p.hs + ((size_t)gc * H + hh) * K * V, (long long)K * V * 4);
   const rsrc_t Rdh = make_rsrc(p.dhs + ((size_t)gc * H + hh) * K * V, (long long)K * V * 4);
-  const rsrc_t Rdq = make_rsrc((TIn*)p.dq + e0 * K, remr * K * ES);
-  const rsrc_t Rdk = make_rsrc((TIn*)p.dk + e0 * K, remr * K * ES);
-  const rsrc_t Rdka = make_rsrc(p.dk_add ? p.dk_add + e0 * K : nullptr, p.dk_add ? remr * K * 4 : 0);
-  const rsrc_t Rdga = make_rsrc(p.dg_add ? p.dg_add + e0 * K : nullptr, p.dg_add ? remr * K * 4 : 0);
-  const rsrc_t Rdg = make_rsrc(p.dg ? (gmode == kGateS ? p.dg + e0 : p.dg + e0 * K) : nullptr,
-                               p.dg ? remr * (gmode == kGateS ? 1 : K) * 4 : 0);
+  const rsrc_t Rdq = make_rsrc_rows((const TIn*)p.dq, e0, nrows, K);
+  const rsrc_t Rdk = make_rsrc_rows((const TIn*)p.dk, e0, nrows, K);
+  const rsrc_t Rdka = make_rsrc_rows(p.dk_add, e0, nrows, K);
+  const rsrc_t Rdga = make_rsrc_rows(p.dg_add, e0, nrows, K);
+  const rsrc_t Rdg = make_rsrc_rows(p.dg, e0, nrows, gmode == kGateS ? 1 : K);
   if (kScalarGate && tid < 2 * C) sDgS[tid] = 0.f;
 
 #pragma unroll 1

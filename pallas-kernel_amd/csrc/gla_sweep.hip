@@ -145,8 +145,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     L = p.T;
     cbase = n * cdiv(p.T, C);
   }
-  const int NTs = cdiv(L, C);
-  const long long rows_total = (long long)p.B * p.T;   // rows of the [B*T, H, .] tensors
+  const int NTs = cdiv(L, C);                          // 0 for an empty sequence
+  const long long nrows = (long long)p.B * p.T * p.H;  // (token, head) rows of [B,T,H,.]
 
   // ---- staging coordinates and per-thread byte offsets within a chunk
   const int hw = tid >> 5;               // half-wave
@@ -201,21 +201,22 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     const int t0 = c * C;
     const int nval = min(C, L - t0);
     const size_t e0 = (size_t)(row0 + t0) * H + hh;     // first row of the chunk, this head
-    const long long rem = (rows_total - (row0 + t0)) * (long long)H;
-    const rsrc_t Rq = make_rsrc((const TIn*)p.q + e0 * K, rem * K * ES);
-    const rsrc_t Rk = make_rsrc((const TIn*)p.k + e0 * K, rem * K * ES);
-    const rsrc_t Rg = make_rsrc(gk_mode ? p.g + e0 * K : p.g + e0, rem * (gk_mode ? K : 1) * 4);
+    const rsrc_t Rq = make_rsrc_rows((const TIn*)p.q, e0, nrows, K);
+    const rsrc_t Rk = make_rsrc_rows((const TIn*)p.k, e0, nrows, K);
+    const rsrc_t Rg = make_rsrc_rows(p.g, e0, nrows, gk_mode ? K : 1);
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
       const bool ok = r0 + i < nval;
       rs.rq[i] = Wd::ld4(Rq, ok ? offQ : kOOB, i * rowK * ES);
       rs.rk[i] = Wd::ld4(Rk, ok ? offQ : kOOB, i * rowK * ES);
-      // one unconditional load whatever the gate mode (the mode's transform is applied
-      // when the chunk is consumed, so the prefetch never waits)
-      rs.rg[i] = bld128(Rg, ok ? offGm : kOOB, i * gstride);
+      // the gate mode's transform is applied when the chunk is consumed, so the prefetch
+      // never waits: four channels [.., K], or the one per-(token, head) word [.., 1]
+      // (gamma: offGm is out of range, nothing is read)
+      if (gk_mode) rs.rg[i] = bld128(Rg, ok ? offGm : kOOB, i * gstride);
+      else rs.rg[i] = make_uint4(bld32(Rg, ok ? offGm : kOOB, i * gstride), 0u, 0u, 0u);
     }
     if constexpr (!FWD_DELTA) {
-      const rsrc_t Ry = make_rsrc((const TIn*)p.y + e0 * V, rem * V * ES);
+      const rsrc_t Ry = make_rsrc_rows((const TIn*)p.y, e0, nrows, V);
 #pragma unroll
       for (int i = 0; i < YR; ++i) {
         const bool ok = yseg * YR + i < nval;
@@ -226,7 +227,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 
   auto cidx = [&](int it) { return REV ? NTs - 1 - it : it; };
   float dsum[4] = {0.f, 0.f, 0.f, 0.f};   // state-only pass: sum of Gamma of this lane's rows
-  load_chunk(cidx(0), rsA);
+  // (an empty sequence has no chunk: nothing is loaded, and the state passes through)
+  if (NTs > 0) load_chunk(cidx(0), rsA);
   if constexpr (PF == 2) {
     if (NTs > 1) load_chunk(cidx(1), rsB);
   }
@@ -244,9 +246,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     float ur[2][4];
     auto load_wu = [&]() {
       const size_t e0 = (size_t)(row0 + t0) * H + hh;
-      const long long rem = (rows_total - (row0 + t0)) * (long long)H;
-      const rsrc_t Rw = make_rsrc(p.w + e0 * K, rem * K * 4);
-      const rsrc_t Ru = make_rsrc(p.u + e0 * V, rem * V * 4);
+      const rsrc_t Rw = make_rsrc_rows(p.w, e0, nrows, K);
+      const rsrc_t Ru = make_rsrc_rows(p.u, e0, nrows, V);
       const int trow = 16 * R + l16;
 #pragma unroll
       for (int kc = 0; kc < KP / 32; ++kc) {
@@ -271,8 +272,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     float4 rw[RPT];
     if constexpr (REV_DELTA) {
       const size_t e0 = (size_t)(row0 + t0) * H + hh;
-      const long long rem = (rows_total - (row0 + t0)) * (long long)H;
-      const rsrc_t Rw = make_rsrc(p.w + e0 * K, rem * K * 4);
+      const rsrc_t Rw = make_rsrc_rows(p.w, e0, nrows, K);
 #pragma unroll
       for (int i = 0; i < RPT; ++i) {
         const uint4 x = bld128(Rw, r0 + i < nval ? offG : kOOB, i * rowK * 4);
@@ -628,10 +628,9 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       // v_new = u - w S for (token block R, column tiles 2nh, 2nh+1).  The A operand
       // w 2^-Gm is read straight from HBM in the MFMA row layout (against H^T = 2^Gm S).
       const size_t e0 = (size_t)(row0 + t0) * H + hh;
-      const long long rem = (rows_total - (row0 + t0)) * (long long)H;
-      const rsrc_t Rvn = make_rsrc(p.y32 ? p.y32 + e0 * V : nullptr, p.y32 ? rem * V * 4 : 0);
-      const rsrc_t Rw = make_rsrc(p.w + e0 * K, rem * K * 4);
-      const rsrc_t Ru = make_rsrc(p.u + e0 * V, rem * V * 4);
+      const rsrc_t Rvn = make_rsrc_rows(p.y32, e0, nrows, V);
+      const rsrc_t Rw = make_rsrc_rows(p.w, e0, nrows, K);
+      const rsrc_t Ru = make_rsrc_rows(p.u, e0, nrows, V);
       bf16x8 wh[KP / 32], wl[KP / 32];
 #pragma unroll
       for (int kc = 0; kc < KP / 32; ++kc) {
@@ -733,8 +732,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       // out^T tiles (nn, R); lane writes out[token 16R + l16][v = 16 nn + 4 lg + 0..3]
       const int tok = 16 * R + l16;
       const size_t eo = (size_t)(row0 + t0) * H + hh;
-      const rsrc_t Ro = make_rsrc((TIn*)p.out + eo * V,
-                                  (rows_total - (row0 + t0)) * (long long)H * V * ES);
+      const rsrc_t Ro = make_rsrc_rows((const TIn*)p.out, eo, nrows, V);
       const uint32_t oo = (tok < nval) ? ((uint32_t)tok * rowV + vt * BV + 4 * lg) * ES : kOOB;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {

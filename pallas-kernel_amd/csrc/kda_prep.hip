@@ -81,14 +81,13 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(KdaPrepParams p) {
   }
   const int t0 = c * C;
   const int nval = min(C, L - t0);
-  const long long rows_total = (long long)p.B * p.T;
   const size_t e0 = (size_t)(row0 + t0) * H + hh;
-  const long long remr = (rows_total - (row0 + t0)) * (long long)H;
+  const long long nrows = (long long)p.B * p.T * H;     // (token, head) rows of [B,T,H,.]
   const uint32_t rowK = (uint32_t)(H * K), rowV = (uint32_t)(H * V);
-  const rsrc_t Rk = make_rsrc((const TIn*)p.k + e0 * K, remr * K * ES);
-  const rsrc_t Rg = make_rsrc(p.g + e0 * K, remr * K * 4);
-  const rsrc_t Rv = make_rsrc((const TIn*)p.v + e0 * V, remr * V * ES);
-  const rsrc_t Rb = make_rsrc(p.beta + e0, remr * 4);
+  const rsrc_t Rk = make_rsrc_rows((const TIn*)p.k, e0, nrows, K);
+  const rsrc_t Rg = make_rsrc_rows(p.g, e0, nrows, K);
+  const rsrc_t Rv = make_rsrc_rows((const TIn*)p.v, e0, nrows, V);
+  const rsrc_t Rb = make_rsrc_rows(p.beta, e0, nrows, 1);
 
   // ---------------- loads: k / g rows r0.. (4 channels), v rows rv0.. (4 columns), beta
   // a 32-lane half-wave covers 8 channel quads x 4 row segments: the row-major K1 / K2 writes
@@ -297,8 +296,8 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(KdaPrepParams p) {
     }
     const int tok = 16 * R + l16;
     const bool tok_ok = tok < nval;
-    const rsrc_t Ru = make_rsrc(p.u + e0 * V, remr * V * 4);
-    const rsrc_t Rw = make_rsrc(p.w + e0 * K, remr * K * 4);
+    const rsrc_t Ru = make_rsrc_rows(p.u, e0, nrows, V);
+    const rsrc_t Rw = make_rsrc_rows(p.w, e0, nrows, K);
 #pragma unroll
     for (int up = 0; up < NUW; ++up) {
       if (up > 0) {

@@ -93,15 +93,14 @@ __global__ __launch_bounds__(256, 2) void kda_wy_kernel(KdaWyParams p) {
   }
   const int t0 = c * C;
   const int nval = min(C, L - t0);
-  const long long rows_total = (long long)p.B * p.T;
   const size_t e0 = (size_t)(row0 + t0) * H + hh;
-  const long long remr = (rows_total - (row0 + t0)) * (long long)H;
+  const long long nrows = (long long)p.B * p.T * H;     // (token, head) rows of [B,T,H,.]
   const uint32_t rowK = (uint32_t)(H * K), rowV = (uint32_t)(H * V);
-  const rsrc_t Rk = make_rsrc((const TIn*)p.k + e0 * K, remr * K * ES);
-  const rsrc_t Rg = make_rsrc(p.g + e0 * K, remr * K * 4);
-  const rsrc_t Rv = make_rsrc((const TIn*)p.v + e0 * V, remr * V * ES);
-  const rsrc_t Rvn = make_rsrc(p.vnew + e0 * V, remr * V * 4);
-  const rsrc_t Rb = make_rsrc(p.beta + e0, remr * 4);
+  const rsrc_t Rk = make_rsrc_rows((const TIn*)p.k, e0, nrows, K);
+  const rsrc_t Rg = make_rsrc_rows(p.g, e0, nrows, K);
+  const rsrc_t Rv = make_rsrc_rows((const TIn*)p.v, e0, nrows, V);
+  const rsrc_t Rvn = make_rsrc_rows(p.vnew, e0, nrows, V);
+  const rsrc_t Rb = make_rsrc_rows(p.beta, e0, nrows, 1);
   const rsrc_t Rtt = make_rsrc(p.tt + ((size_t)gc * H + hh) * C * C, (long long)C * C * 4);
   const rsrc_t Rdvt = make_rsrc(p.dvnt + ((size_t)gc * H + hh) * V * C, (long long)V * C * 4);
   const rsrc_t Rh = make_rsrc(p.hs + ((size_t)gc * H + hh) * K * V, (long long)K * V * 4);
@@ -114,7 +113,7 @@ __global__ __launch_bounds__(256, 2) void kda_wy_kernel(KdaWyParams p) {
   // the phase (dv_new^T and T^T fragments, v rows) is requested before the first product.
   {
     constexpr int NVW = (NVB + 3) / 4;          // V blocks per wave
-    const rsrc_t Rdv = make_rsrc((TIn*)p.dv + e0 * V, remr * V * ES);
+    const rsrc_t Rdv = make_rsrc_rows((const TIn*)p.dv, e0, nrows, V);
     uint4 draw[NVW][2][2], traw[4][2][2];
     typename Wd::W4 vraw[NVW][4];
 #pragma unroll
@@ -302,8 +301,8 @@ __global__ __launch_bounds__(256, 2) void kda_wy_kernel(KdaWyParams p) {
   }
 
   // ---------------- channel passes: wave (kb, tp) -> channels cb + 16kb.., tokens of blocks 2tp, 2tp+1
-  const rsrc_t Rdk = make_rsrc(p.dk_wy + e0 * K, remr * K * 4);
-  const rsrc_t Rdg = make_rsrc(p.dg_wy + e0 * K, remr * K * 4);
+  const rsrc_t Rdk = make_rsrc_rows(p.dk_wy, e0, nrows, K);
+  const rsrc_t Rdg = make_rsrc_rows(p.dg_wy, e0, nrows, K);
   const int ch = tid & 31, sg = tid >> 5;
   float dbk_acc[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};   // per (a, r): sum over channels
 #pragma unroll 1
@@ -480,7 +479,7 @@ __global__ __launch_bounds__(256, 2) void kda_wy_kernel(KdaWyParams p) {
   __syncthreads();
   if (tid < C) {
     const float x = sDbk[tid] + sDbk[C + tid] + sDbv[tid] + sDbv[C + tid] + sDbv[2 * C + tid] + sDbv[3 * C + tid];
-    const rsrc_t Rdb = make_rsrc(p.dbeta + e0, remr * 4);
+    const rsrc_t Rdb = make_rsrc_rows(p.dbeta, e0, nrows, 1);
     bst32(Rdb, __float_as_uint(x), tid < nval ? (uint32_t)tid * H * 4u : kOOB, 0);
   }
 }

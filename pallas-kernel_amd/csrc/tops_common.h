@@ -160,14 +160,26 @@ __device__ __forceinline__ int cdiv(int a, int b) { return (a + b - 1) / b; }
 // Raw (stride 0) buffer descriptors: 32-bit byte offsets from an SGPR base, and the
 // hardware range check returns 0 for a load (drops a store) whose offset is at or past
 // num_records.  Masked elements use kOOB, which is past any num_records set here
-// (num_records is capped at 2^31 - 1).
+// (num_records is capped at 2^31 - 1).  The software row / column masks are what keep
+// every access inside its tensor (the check covers the VGPR offset; the per-row SGPR
+// offsets the kernels add are guarded by their row masks); the resources of the chunk
+// kernels are built with make_rsrc_rows so that they also end at the tensor's end.
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 constexpr uint32_t kOOB = 0x80000000u;
 constexpr int kRsrcFlags = 0x00020000;  // gfx9 family: raw untyped dword access
 
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, long long bytes) {
-  const int n = bytes > 0x7fffffffLL ? 0x7fffffff : (int)bytes;
+  const int n = bytes <= 0 ? 0 : (bytes > 0x7fffffffLL ? 0x7fffffff : (int)bytes);
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, kRsrcFlags);
+}
+// Resource over the tail of a row tensor [nrows, width] of element type T (a [B, T, H, W]
+// tensor is nrows = B*T*H rows of W), starting at row e0 (= token_row * H + head): the range
+// ends exactly at the end of the tensor, whatever head e0 names, so the hardware check
+// drops any access past the last element.
+template <typename T>
+__device__ __forceinline__ rsrc_t make_rsrc_rows(const T* t, size_t e0, long long nrows, int width) {
+  if (t == nullptr) return make_rsrc(nullptr, 0);
+  return make_rsrc(t + e0 * (size_t)width, (nrows - (long long)e0) * width * (long long)sizeof(T));
 }
 __device__ __forceinline__ uint32_t bld32(rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);

@@ -56,7 +56,15 @@ def test_prepare_chunk_indices_matches_oracle():
         np.testing.assert_array_equal(prepare_chunk_indices(cu, C), ref(cu, C))
 
 
-def test_prepare_chunk_indices_rejects_empty_segment():
+def test_prepare_chunk_indices_empty_and_negative_segments():
+    """An empty sequence gets no chunk (tops/utils.py:71-90: repeat by cdiv(0, C) = 0); a
+    negative length is an error."""
     from tops.utils import prepare_chunk_indices
+    from oracle.common import prepare_chunk_indices as ref
+    for cu in ([0, 10, 10, 20], [0, 0, 64, 64], [0, 0, 0, 5]):
+        got = prepare_chunk_indices(cu, 16)
+        np.testing.assert_array_equal(got, ref(cu, 16))
+        assert 0 not in np.diff(cu) or got.shape[0] == sum(-(-int(x) // 16) for x in np.diff(cu))
+    np.testing.assert_array_equal(prepare_chunk_indices([0, 10, 10, 20], 16), [[0, 0], [2, 0]])
     with pytest.raises(ValueError):
-        prepare_chunk_indices([0, 10, 10, 20], 16)
+        prepare_chunk_indices([0, 10, 5, 20], 16)

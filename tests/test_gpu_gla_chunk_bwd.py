@@ -144,3 +144,35 @@ def test_many_sequences(cuda_device):
     want = [ro, rht] + list(ref)
     for name, a, b in zip(("o", "ht", "dq", "dk", "dv", "dg", "dh0"), got, want):
         assert rel(host(a), b) < 1e-4, name
+
+
+@pytest.mark.parametrize("cu", [[0, 0, 64, 64], [0, 50, 50, 130, 130], [0, 0, 0, 37]],
+                         ids=["empty-first-last", "empty-middle-last", "two-empty-first"])
+def test_empty_sequences(cu, cuda_device):
+    """Zero-length sequences (0 chunks, tops/utils.py:71-90): their final state is h0 and their
+    dh0 is dht; the other sequences match the oracle run on them alone."""
+    from tops.ops.gla import chunk_gla
+    lens = np.diff(cu)
+    n, T, H, K, V = len(lens), cu[-1], 2, 64, 64
+    d = gla_inputs(1, T, H, K, V, 77, gate_div=4.0, h0=True, N=n, grads=True)
+    q, k, v = (to_dev(d[x], torch.float32, cuda_device).requires_grad_() for x in "qkv")
+    g = to_dev(d["g"], torch.float32, cuda_device).requires_grad_()
+    h0 = to_dev(d["h0"], torch.float32, cuda_device).requires_grad_()
+    print(f"empty-sequence case cu={cu}", flush=True)
+    o, ht = chunk_gla(q, k, v, g, initial_state=h0, output_final_state=True, cu_seqlens=cu)
+    torch.autograd.backward((o, ht), (to_dev(d["do"], torch.float32, cuda_device),
+                                      to_dev(d["dht"], torch.float32, cuda_device)))
+    torch.cuda.synchronize()
+    keep = [i for i in range(n) if lens[i] > 0]
+    cu_ne = [0] + [int(x) for x in np.cumsum(lens[keep])]
+    ro, rht = O.chunk_gla(d["q"], d["k"], d["v"], d["g"], initial_state=d["h0"][keep],
+                          output_final_state=True, cu_seqlens=cu_ne)
+    rq, rk, rv, rg, rh0 = O.chunk_gla_bwd(d["q"], d["k"], d["v"], d["g"], K ** -0.5,
+                                          d["h0"][keep], d["do"], d["dht"][keep], cu_seqlens=cu_ne)
+    for name, a, b in (("o", o, ro), ("dq", q.grad, rq), ("dk", k.grad, rk), ("dv", v.grad, rv),
+                       ("dg", g.grad, rg)):
+        assert rel(host(a), b) < 1e-4, name
+    want_ht, want_dh0 = d["h0"].astype(np.float64).copy(), d["dht"].astype(np.float64).copy()
+    want_ht[keep], want_dh0[keep] = rht, rh0
+    assert rel(host(ht), want_ht) < 1e-4
+    assert rel(host(h0.grad), want_dh0) < 1e-4

@@ -14,13 +14,7 @@ from oracle import gla as O
 from _gpu import to_dev, seen, host, rel
 from _inputs import gla_inputs
 
-pytestmark = [
-    pytest.mark.gpu,
-    pytest.mark.skip(reason="the one full GPU-suite run that included this module ended in a GPU "
-                            "memory fault (reported at the start of the next module); each of its "
-                            "groups had passed when run alone, and the faulting kernel has not been "
-                            "identified yet, so the module stays off the GPU until it is"),
-]
+pytestmark = pytest.mark.gpu
 
 REF = [
     dict(B=2, T=32, H=4, K=32, V=64), dict(B=2, T=32, H=4, K=32, V=64, h0=True),
