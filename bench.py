@@ -7,8 +7,8 @@ One step = tops.ops.gla.chunk_gla forward (o, final state) plus its backward
 in HBM (q, k, v, dO ~ N(0,1) bf16; g = logsigmoid(N(0,1))/16 fp32; h0, dht ~
 N(0, 0.1^2) fp32).  Prints ONE JSON line with the throughput (tokens/s, tokens =
 B*T per step), the roofline of the dominant kernel timed live with HIP events on
-the stream the kernels run on, and a CPU baseline: the float64 NumPy oracle on a
-bounded sample of the same workload on this host.
+the stream the kernels run on, and a CPU baseline: a torch-CPU float32 restatement of
+the reference's algorithm timed on this host's cores on the same step.
 """
 from __future__ import annotations
 
@@ -69,31 +69,53 @@ def make_inputs(device, seed=1003):
     return q, k, v, g, h0, do, dht
 
 
-def cpu_baseline(repeats=3, heads=4):
-    """The float64 oracle (a restatement of the reference's tops/cpu, test infrastructure)
-    on a bounded sample: B=1, T=4096, `heads` heads, K=V=128, forward + backward, one
-    thread.  Returns tokens/s scaled to the full 16-head config."""
-    import numpy as np
-    from threadpoolctl import threadpool_limits
-    sys.path.insert(0, os.path.join(ROOT, "tests"))
-    from oracle import gla as O
-    from _inputs import gla_inputs
-    d = gla_inputs(1, T, heads, K, V, seed=1003, gate_div=16.0, h0=True, grads=True)
-    times = []
-    with threadpool_limits(1):
-        for _ in range(repeats):
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(repeats=3, warmup=1):
+    """The torch-CPU float32 restatement of the reference's chunked GLA (oracle/torch_cpu.py,
+    test infrastructure pinned against the float64 oracle), forward + backward on the full
+    config-3 step (B=8, T=4096, H=16, K=V=128; bf16-rounded inputs in fp32), on every CPU
+    thread this process is granted (OMP_NUM_THREADS, else os.cpu_count()).  One warm-up, the
+    median of `repeats` timed runs.  Returns tokens/s (tokens = B*T)."""
+    import torch
+    from oracle import torch_cpu as TC
+    threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or (os.cpu_count() or 1)
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        gen = torch.Generator().manual_seed(1003)
+        bf = torch.bfloat16
+
+        def n(*shape, std=1.0):
+            return torch.randn(*shape, generator=gen) * std
+        q, k = (n(B, T, H, K).to(bf).float() for _ in range(2))
+        v, do = (n(B, T, H, V).to(bf).float() for _ in range(2))
+        g = torch.nn.functional.logsigmoid(n(B, T, H, K)) / 16
+        h0, dht = n(B, H, K, V, std=0.1), n(B, H, K, V, std=0.1)
+        times = []
+        for i in range(warmup + repeats):
             t0 = time.perf_counter()
-            O.chunk_gla(d["q"], d["k"], d["v"], d["g"], initial_state=d["h0"],
-                        output_final_state=True, chunk_size=C)
-            O.chunk_gla_bwd(d["q"], d["k"], d["v"], d["g"], K ** -0.5, d["h0"], d["do"], d["dht"],
-                            chunk_size=C)
-            times.append(time.perf_counter() - t0)
+            TC.chunk_gla_fwd_bwd(q, k, v, g, h0, do, dht, K ** -0.5, C)
+            if i >= warmup:
+                times.append(time.perf_counter() - t0)
+    finally:
+        torch.set_num_threads(prev)
     med = statistics.median(times)
-    return {"value": round(T * heads / H / med, 1), "unit": "tokens/s", "cores": 1,
-            "kind": "port",
-            "sample": f"float64 NumPy oracle, chunk_gla fwd+bwd on B=1,T={T},H={heads},K=V={K} "
-                      f"(1/{B * H // heads} of one step), median of {repeats}, 1 thread; "
-                      f"tokens/s scaled to H={H}"}
+    return {"value": round(B * T / med, 1), "unit": "tokens/s", "cores": threads,
+            "kind": "port", "cpu_count": os.cpu_count(), "cpu_model": _cpu_model(),
+            "seconds_per_step": round(med, 3),
+            "sample": f"torch-CPU float32 restatement of tops/cpu chunk_gla fwd+bwd, the full "
+                      f"config-3 step (B={B},T={T},H={H},K=V={K}), {threads} threads, "
+                      f"1 warm-up + median of {repeats}"}
 
 
 def _time(fn, iters, warmup=2):

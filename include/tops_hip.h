@@ -108,6 +108,31 @@ int tops_gla_chunk_bwd_dqkg(const void* q, const void* k, const void* v, const f
                             int B, int T, int H, int K, int V, int N, int dtype, float scale,
                             void* stream);
 
+/* GLA with a constant gate: g_gamma [H,K] fp32, the log-decay of every (head, channel),
+ * applied at every token (a scalar or per-head g_gamma is passed expanded to [H,K]; no gate
+ * at all is g_gamma = 0).  Replaces the g is None branch of chunk_gla_fwd
+ * (tops/ops/gla/chunk.py:1134-1163: g = broadcast(g_gamma) or zeros, and the analytic
+ * cumsum g_gamma * (i + 1)) without a [B,T,H,K] gate in memory.  Arguments as
+ * tops_gla_chunk_fwd / _bwd_dh / _bwd_dqkg; dg (optional, [B,T,H,K] fp32) is the gradient
+ * w.r.t. the per-token gate the constant stands for: its sum over (B, T) is the gradient of
+ * g_gamma [H,K] (chunk.py:987-995). */
+int tops_gla_chunk_fwd_gamma(const void* q, const void* k, const void* v, const float* g_gamma,
+                             const float* h0, void* o, float* ht, float* h_ckpt,
+                             const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                             int B, int T, int H, int K, int V, int N, int dtype, float scale,
+                             void* stream);
+int tops_gla_chunk_bwd_dh_gamma(const void* q, const void* k, const float* g_gamma,
+                                const void* do_, const float* dht, float* dh_work, void* dv,
+                                float* dh0, const int32_t* cu_seqlens,
+                                const int32_t* chunk_offsets, int B, int T, int H, int K, int V,
+                                int N, int dtype, float scale, void* stream);
+int tops_gla_chunk_bwd_dqkg_gamma(const void* q, const void* k, const void* v,
+                                  const float* g_gamma, const void* do_, const float* h_ckpt,
+                                  const float* dh_work, void* dq, void* dk, float* dg,
+                                  const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                                  const int32_t* chunk_map, int total_chunks, int B, int T, int H,
+                                  int K, int V, int N, int dtype, float scale, void* stream);
+
 /* Simple GLA: one log-gate per (token, head) -- g [B,T,H] fp32 -- or a constant per-head
  * log-decay g_gamma [H] fp32; pass exactly one.  The state recurrence is GLA's with the
  * gate shared by all K channels.  Replaces tops.ops.simple_gla.chunk_simple_gla_fwd /
@@ -171,7 +196,8 @@ int tops_simple_gla_chunk_bwd_dqkg(const void* q, const void* k, const void* v, 
  * No counterpart in the reference, whose K7/K8 state kernels sweep every sequence serially
  * (tops/ops/common/chunk_h.py:160-238, 685-878); results equal those of tops_gla_chunk_fwd
  * and tops_gla_chunk_bwd_dh up to fp32 rounding.  gate_mode: 0 = per-channel g [B,T,H,K],
- * 1 = per-token g [B,T,H], 2 = g_gamma [H].  T = rows of the token-major tensors. */
+ * 1 = per-token g [B,T,H], 2 = g_gamma [H], 3 = g_gamma [H,K].  T = rows of the token-major
+ * tensors. */
 int tops_chunk_state_pass(const void* z, const void* y, const float* g, int gate_mode,
                           float* s_loc, float* dec, const int32_t* seg_start,
                           const int32_t* seg_end, int T, int H, int K, int V, int N, int dtype,

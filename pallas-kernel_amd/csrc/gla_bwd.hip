@@ -83,7 +83,7 @@ static int bwd_dqkg_impl(const void* q, const void* k, const void* v, const floa
                          int B, int T, int H, int K, int V, int N, int dtype, float scale,
                          int gate_mode, void* stream) {
   if (!q || !k || !v || !g || !do_ || !h_ckpt || !dh_work || !dq || !dk ||
-      (gate_mode != kGateGamma && !dg))
+      ((gate_mode == kGateK || gate_mode == kGateS) && !dg))
     return tops_set_error(TOPS_ERR_NULL, "gla_chunk_bwd_dqkg: null tensor");
   int rc = check_bwd("gla_chunk_bwd_dqkg", B, T, H, K, V, N, total_chunks, cu_seqlens,
                      chunk_offsets, chunk_map, true, dtype);
@@ -176,4 +176,27 @@ extern "C" int tops_simple_gla_chunk_bwd_dqkg(const void* q, const void* k, cons
   return bwd_dqkg_impl(q, k, v, g ? g : g_gamma, do_, h_ckpt, dh_work, dq, dk, g ? dg : nullptr,
                        cu_seqlens, chunk_offsets, chunk_map, total_chunks, B, T, H, K, V, N, dtype,
                        scale, g ? kGateS : kGateGamma, stream);
+}
+
+extern "C" int tops_gla_chunk_bwd_dh_gamma(const void* q, const void* k, const float* g_gamma,
+                                           const void* do_, const float* dht, float* dh_work,
+                                           void* dv, float* dh0, const int32_t* cu_seqlens,
+                                           const int32_t* chunk_offsets, int B, int T, int H,
+                                           int K, int V, int N, int dtype, float scale,
+                                           void* stream) {
+  return bwd_dh_impl(q, k, g_gamma, do_, dht, dh_work, dv, dh0, cu_seqlens, chunk_offsets, B, T, H,
+                     K, V, N, dtype, scale, kGateGammaK, stream);
+}
+
+extern "C" int tops_gla_chunk_bwd_dqkg_gamma(const void* q, const void* k, const void* v,
+                                             const float* g_gamma, const void* do_,
+                                             const float* h_ckpt, const float* dh_work, void* dq,
+                                             void* dk, float* dg, const int32_t* cu_seqlens,
+                                             const int32_t* chunk_offsets,
+                                             const int32_t* chunk_map, int total_chunks, int B,
+                                             int T, int H, int K, int V, int N, int dtype,
+                                             float scale, void* stream) {
+  return bwd_dqkg_impl(q, k, v, g_gamma, do_, h_ckpt, dh_work, dq, dk, dg, cu_seqlens,
+                       chunk_offsets, chunk_map, total_chunks, B, T, H, K, V, N, dtype, scale,
+                       kGateGammaK, stream);
 }

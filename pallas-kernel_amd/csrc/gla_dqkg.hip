@@ -153,7 +153,7 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
   // gate element (row r, channel kc): per-channel [.., K], per-token [.., 1], or none (gamma)
   const bool gk_mode = gmode == kGateK;
   const uint32_t gstr = gk_mode ? rowK * 4u : (uint32_t)H * 4u;
-  const bool gload = gmode != kGateGamma;
+  const bool gload = gmode == kGateK || gmode == kGateS;   // the constant gates load nothing
   auto load_pass = [&](int ps) {
     const int kc = ps * KH + ch;
     const bool ok = kc < K;
@@ -231,7 +231,7 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
   const rsrc_t Rdk = make_rsrc_rows((const TIn*)p.dk, e0, nrows, K);
   const rsrc_t Rdka = make_rsrc_rows(p.dk_add, e0, nrows, K);
   const rsrc_t Rdga = make_rsrc_rows(p.dg_add, e0, nrows, K);
-  const rsrc_t Rdg = make_rsrc_rows(p.dg, e0, nrows, gmode == kGateS ? 1 : K);
+  const rsrc_t Rdg = make_rsrc_rows(gmode == kGateGamma ? nullptr : p.dg, e0, nrows, gmode == kGateS ? 1 : K);
   if (kScalarGate && tid < 2 * C) sDgS[tid] = 0.f;
 
 #pragma unroll 1
@@ -266,7 +266,9 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
     float G[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float x = gmode == kGateGamma ? ((cb + ch < K && 8 * sg + i < nval) ? gam_h : 0.f) : rg[i];
+      float x = rg[i];
+      if (gmode == kGateGamma) x = (cb + ch < K && 8 * sg + i < nval) ? gam_h : 0.f;
+      else if (gmode == kGateGammaK) x = (cb + ch < K && 8 * sg + i < nval) ? p.g[(size_t)hh * K + cb + ch] : 0.f;
       G[i] = x * kLog2e + (i > 0 ? G[i - 1] : 0.f);
     }
     // (no barrier before this write: sTot is last read before the previous pass's planes
@@ -466,7 +468,7 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
       add[r] = fast_exp2(sGam[cl + r]) * sHdh[cl + r] + sZk[cl + r] + sZk[KH + cl + r];
       if (rh == 0) add[r] += sBlk[cl + r];
     }
-    if (gmode == kGateK) {
+    if (gmode == kGateK || (gmode == kGateGammaK && p.dg)) {
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
         const int tok = 16 * (2 * rh + a) + l16;

@@ -67,7 +67,7 @@ extern "C" int tops_chunk_state_pass(const void* z, const void* y, const float* 
     return tops_set_error(TOPS_ERR_SHAPE, "chunk_state_pass: need K, V <= 128 and multiples of 8");
   if ((long long)kChunk * H * (K > V ? K : V) * 4 >= (1LL << 31))
     return tops_set_error(TOPS_ERR_SHAPE, "chunk_state_pass: H * max(K, V) too large");
-  if (gate_mode != kGateK && gate_mode != kGateS && gate_mode != kGateGamma)
+  if (gate_mode != kGateK && gate_mode != kGateS && gate_mode != kGateGamma && gate_mode != kGateGammaK)
     return tops_set_error(TOPS_ERR_SHAPE, "chunk_state_pass: unknown gate mode");
   // z fills both the q and the k slot: the state-only sweep multiplies only one of them.
   SweepParams p{z, z, g, y, nullptr, nullptr, s_loc, nullptr, seg_start, nullptr,

@@ -8,7 +8,9 @@ namespace tops {
 //   kGateK     g is [B,T,H,K] per-channel log-gates (GLA)
 //   kGateS     g is [B,T,H] one log-gate per (token, head), shared by all K channels
 //   kGateGamma g is gamma[H], a constant log-decay per head (simple GLA g_gamma)
-enum { kGateK = 0, kGateS = 1, kGateGamma = 2 };
+//   kGateGammaK g is gamma[H,K], a constant log-decay per head and channel (GLA g_gamma;
+//              its gradient is written per token as for kGateK, [B,T,H,K])
+enum { kGateK = 0, kGateS = 1, kGateGamma = 2, kGateGammaK = 3 };
 
 struct SweepParams {
   const void* q;

@@ -170,6 +170,12 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   const uint32_t offGm = gk_mode ? offG : (gmode == kGateS ? (uint32_t)r0 * H * 4u : kOOB);
   const uint32_t gstride = gk_mode ? rowK * 4 : (uint32_t)H * 4;
   const float gam_h = gmode == kGateGamma ? p.g[hh] : 0.f;
+  // constant per-(head, channel) gate: the four channels c0..c0+3 of this thread
+  float gam4[4] = {gam_h, gam_h, gam_h, gam_h};
+  if (gmode == kGateGammaK) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) gam4[j] = colok ? p.g[(size_t)hh * K + c0 + j] : 0.f;
+  }
 
   // ---- state tiles: tile i of this wave -> (msb, nn)
   f32x4 S[NHT];
@@ -288,9 +294,11 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     for (int i = 0; i < RPT; ++i) {
       float x[4];
       unpack4(rs.rg[i], x);
-      if (!gk_mode) {
-        const float s1 = gmode == kGateS ? x[0] : (r0 + i < nval ? gam_h : 0.f);
-        x[0] = x[1] = x[2] = x[3] = s1;
+      if (gmode == kGateS) {
+        x[1] = x[2] = x[3] = x[0];
+      } else if (!gk_mode) {   // constant gates: zero on the rows past the sequence
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = r0 + i < nval ? gam4[j] : 0.f;
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) G[i][j] = x[j] * kLog2e + (i > 0 ? G[i - 1][j] : 0.f);
@@ -881,4 +889,14 @@ extern "C" int tops_simple_gla_chunk_fwd(const void* q, const void* k, const voi
     return tops_set_error(TOPS_ERR_NULL, "simple_gla_chunk_fwd: pass exactly one of g, g_gamma");
   return chunk_fwd_impl(q, k, v, g ? g : g_gamma, h0, o, ht, h_ckpt, cu_seqlens, chunk_offsets, B, T,
                         H, K, V, N, dtype, scale, g ? kGateS : kGateGamma, stream);
+}
+
+extern "C" int tops_gla_chunk_fwd_gamma(const void* q, const void* k, const void* v,
+                                        const float* g_gamma, const float* h0, void* o, float* ht,
+                                        float* h_ckpt, const int32_t* cu_seqlens,
+                                        const int32_t* chunk_offsets, int B, int T, int H, int K,
+                                        int V, int N, int dtype, float scale, void* stream) {
+  if (!g_gamma) return tops_set_error(TOPS_ERR_NULL, "gla_chunk_fwd_gamma: null g_gamma");
+  return chunk_fwd_impl(q, k, v, g_gamma, h0, o, ht, h_ckpt, cu_seqlens, chunk_offsets, B, T, H, K,
+                        V, N, dtype, scale, kGateGammaK, stream);
 }

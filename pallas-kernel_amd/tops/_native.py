@@ -32,6 +32,9 @@ SIGNATURES = {
     "tops_gla_chunk_bwd_dqkg": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                 _vp, _vp, _vp, _i32,
                                 _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp],
+    "tops_gla_chunk_fwd_gamma": [_vp] * 10 + [_i32] * 7 + [_f32, _vp],
+    "tops_gla_chunk_bwd_dh_gamma": [_vp] * 10 + [_i32] * 7 + [_f32, _vp],
+    "tops_gla_chunk_bwd_dqkg_gamma": [_vp] * 13 + [_i32] * 8 + [_f32, _vp],
     "tops_simple_gla_chunk_fwd": [_vp] * 11 + [_i32] * 7 + [_f32, _vp],
     "tops_simple_gla_chunk_bwd": [_vp] * 17 + [_i32] * 8 + [_f32, _vp],
     "tops_gla_fused_recurrent_fwd": [_vp] * 10 + [_i32] * 7 + [_f32, _i32, _vp],

@@ -7,7 +7,7 @@ import torch
 from .. import _native as N
 from ..utils import ChunkPlan
 
-GATE_K, GATE_S, GATE_GAMMA = "k", "s", "gamma"
+GATE_K, GATE_S, GATE_GAMMA, GATE_GAMMA_K = "k", "s", "gamma", "gamma_k"
 
 
 def tiling(K: int, V: int, tile_v: bool):
@@ -44,7 +44,7 @@ def check_qkv(q, k, v, initial_state, cu_seqlens, split_ok: bool = False):
     N.require_cuda(q, k, v, initial_state)
 
 
-_GATE_CODE = {GATE_K: 0, GATE_S: 1, GATE_GAMMA: 2}
+_GATE_CODE = {GATE_K: 0, GATE_S: 1, GATE_GAMMA: 2, GATE_GAMMA_K: 3}
 
 
 def _gate_ptrs(gate):
@@ -98,6 +98,8 @@ def _fwd_tile(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, kee
             Bx, Tx, H, K, V, Nx, N.dtype_code(q.dtype), float(scale), N.stream())
     if mode == GATE_K:
         N.call("tops_gla_chunk_fwd", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gt), *tail)
+    elif mode == GATE_GAMMA_K:
+        N.call("tops_gla_chunk_fwd_gamma", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gt), *tail)
     else:
         N.call("tops_simple_gla_chunk_fwd", N.ptr(q), N.ptr(k), N.ptr(v), *_gate_ptrs(gate),
                *tail)
@@ -107,10 +109,12 @@ def _fwd_tile(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, kee
     return o, ht, hs
 
 
-def _bwd_tile(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool):
+def _bwd_tile(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool,
+              want_dg: bool = True):
     """Run the backward (reverse sweep + chunk-parallel dq/dk/dg) on one tile (K, V <= 128).
-    Returns (dq, dk, dv, dg, dh0); dg is [B,T,H,K] for GATE_K, [B,T,H] for GATE_S and None
-    for GATE_GAMMA."""
+    Returns (dq, dk, dv, dg, dh0); dg is [B,T,H,K] for GATE_K (and for GATE_GAMMA_K when
+    want_dg: the gradient of the per-token gate the constant stands for), [B,T,H] for GATE_S
+    and None for GATE_GAMMA."""
     B, T, H, K = q.shape
     V = v.shape[-1]
     if V > 128:
@@ -120,7 +124,7 @@ def _bwd_tile(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
     dg = None
-    if mode == GATE_K:
+    if mode == GATE_K or (mode == GATE_GAMMA_K and want_dg):
         dg = torch.empty(B, T, H, K, device=q.device, dtype=torch.float32)
     elif mode == GATE_S:
         dg = torch.empty(B, T, H, device=q.device, dtype=torch.float32)
@@ -144,6 +148,10 @@ def _bwd_tile(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool
     if mode == GATE_K:
         N.call("tops_gla_chunk_bwd_dh", N.ptr(q), N.ptr(k), N.ptr(gt), *dh_args)
         N.call("tops_gla_chunk_bwd_dqkg", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gt), *dqkg_tail)
+    elif mode == GATE_GAMMA_K:
+        N.call("tops_gla_chunk_bwd_dh_gamma", N.ptr(q), N.ptr(k), N.ptr(gt), *dh_args)
+        N.call("tops_gla_chunk_bwd_dqkg_gamma", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gt),
+               *dqkg_tail)
     else:
         N.call("tops_simple_gla_chunk_bwd_dh", N.ptr(q), N.ptr(k), *_gate_ptrs(gate), *dh_args)
         N.call("tops_simple_gla_chunk_bwd_dqkg", N.ptr(q), N.ptr(k), N.ptr(v), *_gate_ptrs(gate),
@@ -163,7 +171,7 @@ def _direct(q, K, V, tile_v):
 
 def _k_gate(gate, ks):
     mode, gt = gate
-    return (mode, gt[..., ks].contiguous()) if mode == GATE_K else gate
+    return (mode, gt[..., ks].contiguous()) if mode in (GATE_K, GATE_GAMMA_K) else gate
 
 
 def chunk_fwd(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, keep_states: bool):
@@ -201,7 +209,8 @@ def chunk_fwd(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, kee
     return o.to(v.dtype), ht, hs
 
 
-def chunk_bwd(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool):
+def chunk_bwd(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool,
+              want_dg: bool = True):
     """Backward of GLA / simple GLA.  Returns (dq, dk, dv, dg, dh0); dg is [B,T,H,K] for
     GATE_K, [B,T,H] for GATE_S and None for GATE_GAMMA.  Sliced as chunk_fwd: dq, dk and a
     per-channel dg are the sums over the V slices, dv (and a scalar-gate dg) the sums over
@@ -209,7 +218,7 @@ def chunk_bwd(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool
     B, T, H, K = q.shape
     V = v.shape[-1]
     if _direct(q, K, V, True) and hs.dim() == 4:
-        return _bwd_tile(q, k, v, gate, do, dht, hs, scale, plan, want_dh0)
+        return _bwd_tile(q, k, v, gate, do, dht, hs, scale, plan, want_dh0, want_dg)
     nk, Kp, nv, Vp = tiling(K, V, True)
     f32 = torch.float32
     qf, kf, vf, dof = (x.to(f32) for x in (q, k, v, do))
@@ -217,7 +226,8 @@ def chunk_bwd(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool
     dq = torch.zeros(B, T, H, K, device=q.device, dtype=f32)
     dk = torch.zeros_like(dq)
     dv = torch.zeros(B, T, H, V, device=q.device, dtype=f32)
-    dg = torch.zeros_like(dq) if mode == GATE_K else \
+    k_dg = mode == GATE_K or (mode == GATE_GAMMA_K and want_dg)
+    dg = torch.zeros_like(dq) if k_dg else \
         torch.zeros(B, T, H, device=q.device, dtype=f32) if mode == GATE_S else None
     dh0 = torch.empty(plan.N, H, K, V, device=q.device, dtype=f32) if want_dh0 else None
     for a in range(nk):
@@ -228,11 +238,11 @@ def chunk_bwd(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool
             dhtab = None if dht is None else dht[:, :, ks, vs].contiguous()
             dqa, dka, dvb, dga, dh0ab = _bwd_tile(qa, ka, vf[..., vs].contiguous(), ga,
                                                    dof[..., vs].contiguous(), dhtab, hs[a * nv + b],
-                                                   scale, plan, want_dh0)
+                                                   scale, plan, want_dh0, want_dg)
             dq[..., ks] += dqa
             dk[..., ks] += dka
             dv[..., vs] += dvb
-            if mode == GATE_K:
+            if k_dg:
                 dg[..., ks] += dga
             elif mode == GATE_S:
                 dg += dga

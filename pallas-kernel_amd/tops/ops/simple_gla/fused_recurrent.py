@@ -1,17 +1,21 @@
 """fused_recurrent_simple_gla on MI355X (tops/ops/simple_gla/fused_recurrent.py:146-240).
 
 The per-token simple-GLA recurrence h_t = h_{t-1} exp(g_t + g_gamma) + k_t v_t^T,
-o_t = h_t^T (scale q_t) is GLA's with the gate shared by all K channels, so it runs on
-tops.ops.gla.fused_recurrent_gla with the gate expanded over K.  The expansion is a
-broadcast view inside the autograd graph: the gradients w.r.t. g [B,T,H] and g_gamma [H]
-come back summed over the broadcast axes, which is the gradient of the reference's
-lax.scan (g and g_gamma may be combined, as in tops/cpu/ops/simple_gla/naive.py:113-125).
+o_t = h_t^T (scale q_t) is GLA's with the gate shared by all K channels.  In forward time
+order it runs on the chunk kernels' per-token scalar-gate mode (tops.ops.simple_gla
+chunk_simple_gla with g [B,T,H]: the same sums grouped by 64-token chunks); g and g_gamma
+are combined into that one [B,T,H] gate, g + g_gamma (tops/cpu/ops/simple_gla/naive.py:
+113-125).  reverse=True runs the per-token kernels of tops.ops.gla.fused_recurrent_gla
+with the gate as a broadcast view over K.  Either way the combination is part of the
+autograd graph, so the gradients w.r.t. g [B,T,H] and g_gamma [H] come back summed over the
+broadcast axes: the gradient of the reference's lax.scan.
 """
 from __future__ import annotations
 
 import torch
 
 from ..gla.fused_recurrent import fused_recurrent_gla
+from .chunk import chunk_simple_gla
 
 
 def fused_recurrent_simple_gla(q, k, v, g=None, g_gamma=None, scale=None, initial_state=None,
@@ -20,6 +24,17 @@ def fused_recurrent_simple_gla(q, k, v, g=None, g_gamma=None, scale=None, initia
     B, T, H, K = q.shape
     assert g is None or tuple(g.shape) == (B, T, H), f"g shape {tuple(g.shape)} != {(B, T, H)}"
     assert g_gamma is None or tuple(g_gamma.shape) == (H,), f"g_gamma shape must be ({H},)"
+    V = v.shape[-1]
+    if not reverse and K % 8 == 0 and V % 8 == 0 and K <= 128 and V <= 128:
+        gs = None
+        if g is not None:
+            gs = g.to(torch.float32)
+        if g_gamma is not None:
+            gg = torch.as_tensor(g_gamma, device=q.device).to(torch.float32)
+            gs = gg.expand(B, T, H) if gs is None else gs + gg
+        return chunk_simple_gla(q, k, v, None, initial_state=initial_state, scale=scale,
+                                output_final_state=output_final_state, g=gs,
+                                cu_seqlens=cu_seqlens)
     gk = None
     if g is not None:
         gk = g.to(torch.float32)[..., None]

@@ -274,7 +274,7 @@ def dqkg(ck: Checker, p: dict, es: int, esv: int):
                         ck.acc(p[nm], e0 * K * 4, np.where(v_, off * 4, KOOB), 0, 4, "dqkg pass load")
                     else:
                         ck.acc(p[nm], e0 * K * 2, np.where(v_, (off & ~1) * 2, KOOB), 0, 4, "dqkg pass load")
-                if gm != 2:
+                if gm in (0, 1):      # the constant gates (2: [H], 3: [H, K]) load nothing
                     gstr, gcol, gwid = (rowK * 4, kc * 4, K) if gm == 0 else (H * 4, 0, 1)
                     ck.acc(p["g"], e0 * gwid * 4, np.where(v_, r * gstr + gcol, KOOB), 0, 4,
                            "dqkg load g")
@@ -299,7 +299,7 @@ def dqkg(ck: Checker, p: dict, es: int, esv: int):
                         ck.acc(p[nm], e0 * K * 4, np.where(ok, off * 4, KOOB), 0, 16, "dqkg epilogue load")
                 for nm in ("dq", "dk"):
                     ck.acc(p[nm], e0 * K * es, np.where(ok, off * es, KOOB), 0, 4 * es, f"dqkg store {nm}")
-                if gm == 0 and p.get("dg"):
+                if gm in (0, 3) and p.get("dg"):
                     ck.acc(p["dg"], e0 * K * 4, np.where(ok, off * 4, KOOB), 0, 16, "dqkg store dg")
         if gm == 1 and p.get("dg"):
             ck.acc(p["dg"], e0 * 4, np.where(tid < nval, tid * H * 4, KOOB), 0, 4, "dqkg store dg (scalar)")

@@ -35,8 +35,8 @@ def chunk_op(B, T, H, K, V, es, cu=None, gate_mode=0, h0=True, dht=True, gate_wi
     sizes = dict(q=B * T * H * K * es, k=B * T * H * K * es, v=B * T * H * V * es,
                  o=B * T * H * V * es, do=B * T * H * V * es, dv=B * T * H * V * es,
                  dq=B * T * H * K * es, dk=B * T * H * K * es,
-                 g={0: B * T * H * K * 4, 1: B * T * H * 4, 2: H * 4}[gate_mode],
-                 dg={0: B * T * H * K * 4, 1: B * T * H * 4, 2: 0}[gate_mode],
+                 g={0: B * T * H * K * 4, 1: B * T * H * 4, 2: H * 4, 3: H * K * 4}[gate_mode],
+                 dg={0: B * T * H * K * 4, 1: B * T * H * 4, 2: 0, 3: B * T * H * K * 4}[gate_mode],
                  hs=plan.total * H * K * V * 4, dhs=plan.total * H * K * V * 4,
                  h0=N * H * K * V * 4, ht=N * H * K * V * 4, dht=N * H * K * V * 4, dh0=N * H * K * V * 4)
     ck = M.Checker(sizes)
@@ -135,6 +135,13 @@ SIMPLE = [  # test_gpu_simple_gla.py CASES (+ the reference module's K / V = 256
 def test_simple_gla_in_bounds(c, es):
     K, V = _tile(c["K"], c["V"])
     chunk_op(c["B"], c["T"], c["H"], K, V, es, cu=c.get("cu"), gate_mode=c["gate"])
+
+
+@pytest.mark.parametrize("es", [4, 2], ids=["f32", "bf16"])
+def test_constant_gate_chunk_gla_in_bounds(es):
+    """chunk_gla with g = None or a g_gamma constant over (B, T): the [H, K] gate mode."""
+    chunk_op(2, 130, 3, 64, 64, es, gate_mode=3)
+    chunk_op(1, 300, 2, 128, 128, es, cu=[0, 13, 140, 141, 300], gate_mode=3)
 
 
 def test_planted_wide_scalar_gate_read_is_caught():

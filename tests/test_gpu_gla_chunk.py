@@ -101,3 +101,97 @@ def test_large_gates_finite(cuda_device):
     assert torch.isfinite(o).all() and torch.isfinite(ht).all()
     ro, rht = O.chunk_gla(d["q"], d["k"], d["v"], d["g"], output_final_state=True, chunk_size=64)
     assert rel(host(o), ro) < 1e-4
+
+
+def _padded_oracle(d, C, cu, scale):
+    """g_cumsum, A (full square) and h of the reference's padded layout, from the oracle's
+    stage functions: per sequence padded to a multiple of C (chunk.py:1140-1148)."""
+    from oracle.common import chunk_local_cumsum, chunk_fwd_h, pad_time
+    T = d["q"].shape[1]
+    bounds = [(0, T)] if cu is None else list(zip(cu[:-1], cu[1:]))
+    gcs, As, hs = [], [], []
+    for n, (a, b) in enumerate(bounds):
+        q, k, v, g = (pad_time(d[x][:, a:b].astype(np.float64), C) for x in ("q", "k", "v", "g"))
+        h0 = None if d["h0"] is None else (d["h0"] if cu is None else d["h0"][n:n + 1])
+        gc = chunk_local_cumsum(g, C)
+        gcs.append(gc)
+        As.append(O.chunk_gla_fwd_intra_gk(q, k, gc, scale, C))
+        hs.append(chunk_fwd_h(k, v, gk=gc, h0=h0, C=C)[0])
+    return np.concatenate(gcs, 1), np.concatenate(As, 1), np.concatenate(hs, 1)
+
+
+FWD_ORCH = [
+    dict(B=2, T=100, H=2, K=32, V=64, C=64, h0=True, seed=41),
+    dict(B=1, T=300, H=2, K=64, V=64, C=64, h0=True, seed=42, cu=[0, 13, 140, 141, 300]),
+    dict(B=2, T=96, H=2, K=32, V=32, C=16, h0=False, seed=43),
+    dict(B=1, T=200, H=2, K=64, V=64, C=32, h0=True, seed=44, cu=[0, 50, 200]),
+]
+
+
+@pytest.mark.parametrize("c", FWD_ORCH, ids=lambda c: "B{B}-T{T}-C{C}".format(**c) + ("-varlen" if "cu" in c else ""))
+def test_chunk_gla_fwd_intermediates(c, cuda_device):
+    """chunk_gla_fwd returns (g_cumsum, A, h, ht, o) as the reference (chunk.py:1103-1199);
+    g_cumsum fed back instead of g (g = None) reproduces o, ht and the gradients."""
+    from tops.ops.gla import chunk_gla_fwd, chunk_gla_bwd
+    B, T, H, K, V, C = (c[x] for x in "BTHKVC")
+    cu = c.get("cu")
+    n = len(cu) - 1 if cu else B
+    d = gla_inputs(B, T, H, K, V, c["seed"], gate_div=4.0, h0=c["h0"], N=n, grads=True)
+    t = {x: to_dev(d[x], torch.float32, cuda_device) for x in ("q", "k", "v", "g", "h0", "do", "dht")}
+    scale = K ** -0.5
+    gc, A, h, ht, o = chunk_gla_fwd(t["q"], t["k"], t["v"], t["g"], None, None, scale, t["h0"],
+                                    True, cu_seqlens=cu, chunk_size=C)
+    torch.cuda.synchronize()
+    rgc, rA, rh = _padded_oracle(d, C, cu, scale)
+    ro, rht = O.chunk_gla(d["q"], d["k"], d["v"], d["g"], initial_state=d["h0"],
+                          output_final_state=True, cu_seqlens=cu)
+    assert gc.shape == rgc.shape and A.shape == rA.shape, (gc.shape, A.shape)
+    assert h.shape == (1 if cu else B,) + rh.shape[1:], (h.shape, rh.shape)
+    for name, a, b in (("g_cumsum", gc, rgc), ("A", A, rA), ("h", h, rh), ("ht", ht, rht), ("o", o, ro)):
+        e = rel(host(a), b)
+        assert e < 1e-4, (name, e)
+    # the cumsum given back in place of g
+    _, _, _, ht2, o2 = chunk_gla_fwd(t["q"], t["k"], t["v"], None, None, gc, scale, t["h0"], True,
+                                     cu_seqlens=cu, chunk_size=C)
+    assert rel(host(o2), ro) < 1e-4 and rel(host(ht2), rht) < 1e-4
+    grads = chunk_gla_bwd(t["q"], t["k"], t["v"], None, None, gc, scale, t["h0"], h, A, t["do"],
+                          t["dht"], cu_seqlens=cu, chunk_size=C)
+    ref = O.chunk_gla_bwd(d["q"], d["k"], d["v"], d["g"], scale, d["h0"], d["do"], d["dht"],
+                          cu_seqlens=cu)
+    for name, a, b in zip(("dq", "dk", "dv", "dg", "dh0"), grads, ref):
+        if a is None or b is None:
+            continue
+        e = rel(host(a), b)
+        assert e < 1e-4, (name, e)
+
+
+@pytest.mark.parametrize("form", ["none", "scalar", "head", "head_channel"])
+def test_chunk_gla_constant_gates(form, cuda_device):
+    """g = None with no g_gamma or with the reference's three g_gamma forms runs the constant
+    [H, K] gate mode: forward, and the g_gamma gradient (the broadcast gate's gradient summed
+    to g_gamma's shape, chunk.py:987-995), against the oracle on the broadcast gate."""
+    from tops.ops.gla import chunk_gla
+    B, T, H, K, V = 2, 150, 3, 64, 32
+    d = gla_inputs(B, T, H, K, V, 45, h0=True, grads=True)
+    rng = np.random.default_rng(46)
+    shape = {"none": None, "scalar": (), "head": (1, 1, H, 1), "head_channel": (1, 1, H, K)}[form]
+    gam = None if shape is None else (-np.abs(rng.standard_normal(shape)) * 0.2).astype(np.float32)
+    q, k, v = (to_dev(d[x], torch.float32, cuda_device).requires_grad_() for x in "qkv")
+    h0 = to_dev(d["h0"], torch.float32, cuda_device).requires_grad_()
+    gg = None if gam is None else torch.tensor(gam, device=cuda_device, requires_grad=True)
+    o, ht = chunk_gla(q, k, v, g_gamma=gg, initial_state=h0, output_final_state=True)
+    torch.autograd.backward((o, ht), (to_dev(d["do"], torch.float32, cuda_device),
+                                      to_dev(d["dht"], torch.float32, cuda_device)))
+    gfull = np.zeros((B, T, H, K), np.float32) if gam is None else \
+        np.broadcast_to(gam, (B, T, H, K)).astype(np.float32)
+    ro, rht = O.chunk_gla(d["q"], d["k"], d["v"], gfull, initial_state=d["h0"], output_final_state=True)
+    rq, rk, rv, rg, rh0 = O.chunk_gla_bwd(d["q"], d["k"], d["v"], gfull, K ** -0.5, d["h0"],
+                                          d["do"], d["dht"])
+    for name, a, b in (("o", o, ro), ("ht", ht, rht), ("dq", q.grad, rq), ("dk", k.grad, rk),
+                       ("dv", v.grad, rv), ("dh0", h0.grad, rh0)):
+        assert rel(host(a), b) < 1e-4, name
+    if gg is not None:
+        want = rg.sum(axis=(0, 1), keepdims=True)
+        want = want.sum() if gam.ndim == 0 else want.sum(axis=tuple(i for i in range(4) if gam.shape[i] == 1 and want.shape[i] != 1), keepdims=True)
+        assert gg.grad.shape == gg.shape
+        assert rel(host(gg.grad).reshape(-1), np.asarray(want).reshape(-1)) < 1e-4
