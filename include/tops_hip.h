@@ -258,6 +258,20 @@ int tops_kda_chunk_fwd(const void* q, const void* k, const void* v, const float*
                        int B, int T, int H, int K, int V, int N, int dtype, float scale,
                        void* stream);
 
+/* Allocation-free KDA forward (inference).  No counterpart in the reference: for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  As tops_kda_chunk_fwd without the backward's saved
+ * tensors; the WY workspace u, w lives in the library's static device scratch of
+ * tops_kda_chunk_fwd_noalloc_max_bytes() bytes (64 MiB, one copy per GPU, held until the
+ * process ends), so B*T*H*(K+V)*4 must fit in it, else TOPS_ERR_SHAPE before any launch.
+ * The call allocates nothing; calls that overlap on one GPU share the scratch and race. */
+int64_t tops_kda_chunk_fwd_noalloc_max_bytes(void);
+int tops_kda_chunk_fwd_noalloc(const void* q, const void* k, const void* v, const float* g,
+                               const float* beta, const float* h0, void* o, float* ht,
+                               const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                               const int32_t* chunk_map, int total_chunks, int B, int T, int H,
+                               int K, int V, int N, int dtype, float scale, void* stream);
+
 /* Chunked KDA backward.  Replaces tops.ops.kda.chunk_bwd.chunk_kda_bwd
  * (tops/ops/kda/chunk_bwd.py:655-832: the dAv, dhu, WY/dqkg and intra stages)
  * from the tensors saved by tops_kda_chunk_fwd (w, tt, v_new, h_ckpt).

@@ -11,6 +11,8 @@
 // replacing chunk_kda_bwd (tops/ops/kda/chunk_bwd.py:655-832).
 #include <stdio.h>
 
+#include <mutex>
+
 #include "gla_sweep.h"
 #include "kda.h"
 #include "tops_common.h"
@@ -114,4 +116,70 @@ extern "C" int tops_kda_chunk_bwd(const void* q, const void* k, const void* v, c
   e = bf ? launch_gla_dqkg<uint16_t, float>(dp, s) : launch_gla_dqkg<float, float>(dp, s);
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   return TOPS_OK;
+}
+
+// ---------------------------------------------------------------------------------------
+// Allocation-free KDA forward (inference): the WY workspace u [B,T,H,V] and w [B,T,H,K]
+// lives in a static device array of kKdaScratchBytes, one copy per GPU, held until the
+// process ends.  Its address is taken with hipGetSymbolAddress once per device, with that
+// device current, on the first call there; host code never passes the array's name itself
+// to a kernel (on the host it is only a stand-in for the symbol).  Nothing in the array has
+// to start at zero: kda_prep writes every u / w element that the sweep later reads.  Calls
+// that overlap on one GPU share the array and race.
+namespace {
+constexpr size_t kKdaScratchBytes = size_t(64) << 20;  // 64 MiB: T*H*(K+V) <= 16M floats
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kKdaScratchBytes];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return tops_set_error(TOPS_ERR_SHAPE, "kda_chunk_fwd_noalloc: device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return tops_set_error(TOPS_ERR_LAUNCH, e != hipSuccess ? hipGetErrorString(e)
+                                                            : "kda_chunk_fwd_noalloc: null scratch");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return TOPS_OK;
+}
+}  // namespace
+
+extern "C" int64_t tops_kda_chunk_fwd_noalloc_max_bytes(void) { return (int64_t)kKdaScratchBytes; }
+
+extern "C" int tops_kda_chunk_fwd_noalloc(const void* q, const void* k, const void* v,
+                                          const float* g, const float* beta, const float* h0,
+                                          void* o, float* ht, const int32_t* cu_seqlens,
+                                          const int32_t* chunk_offsets, const int32_t* chunk_map,
+                                          int total_chunks, int B, int T, int H, int K, int V,
+                                          int N, int dtype, float scale, void* stream) {
+  if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0)
+    return tops_set_error(TOPS_ERR_SHAPE, "kda_chunk_fwd_noalloc: non-positive dimension");
+  const long long rows = (long long)B * T * H;
+  const long long u_bytes = (rows * V * 4 + 255) / 256 * 256;
+  const long long need = u_bytes + rows * K * 4;
+  if (need > (long long)kKdaScratchBytes) {
+    char msg[200];
+    snprintf(msg, sizeof(msg),
+             "kda_chunk_fwd_noalloc: B*T*H*(K+V)*4 = %lld bytes of workspace exceed the %lld-byte "
+             "static scratch (use tops_kda_chunk_fwd with a caller workspace)",
+             need, (long long)kKdaScratchBytes);
+    return tops_set_error(TOPS_ERR_SHAPE, msg);
+  }
+  void* base = nullptr;
+  int rc = scratch_address(&base);
+  if (rc != TOPS_OK) return rc;
+  float* u = (float*)base;
+  float* w = (float*)((unsigned char*)base + u_bytes);
+  return tops_kda_chunk_fwd(q, k, v, g, beta, h0, o, ht, u, w, nullptr, nullptr, nullptr,
+                            cu_seqlens, chunk_offsets, chunk_map, total_chunks, B, T, H, K, V, N,
+                            dtype, scale, stream);
 }

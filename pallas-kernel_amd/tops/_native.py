@@ -42,6 +42,7 @@ SIGNATURES = {
     "tops_prepare_chunk_indices": [_vp, _i32, _i32, _vp, _vp, _i32],
     "tops_kda_chunk_fwd": [_vp] * 16 + [_i32] * 8 + [_f32, _vp],
     "tops_kda_chunk_bwd": [_vp] * 24 + [_i32] * 8 + [_f32, _vp],
+    "tops_kda_chunk_fwd_noalloc": [_vp] * 11 + [_i32] * 8 + [_f32, _vp],
     "tops_simple_gla_chunk_bwd_dh": [_vp] * 11 + [_i32] * 7 + [_f32, _vp],
     "tops_simple_gla_chunk_bwd_dqkg": [_vp] * 14 + [_i32] * 8 + [_f32, _vp],
     "tops_chunk_state_pass": [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp] + [_i32] * 6 + [_f32, _i32, _vp],
@@ -89,6 +90,8 @@ def lib() -> ctypes.CDLL:
         L.tops_version.restype = ctypes.c_char_p
         L.tops_gla_state_bytes.restype = ctypes.c_int64
         L.tops_gla_state_bytes.argtypes = [_i32, _i32, _i32, _i32]
+        L.tops_kda_chunk_fwd_noalloc_max_bytes.restype = ctypes.c_int64
+        L.tops_kda_chunk_fwd_noalloc_max_bytes.argtypes = []
         L.tops_gla_fused_recurrent_bwd_workspace.restype = ctypes.c_int64
         L.tops_gla_fused_recurrent_bwd_workspace.argtypes = [_i32] * 7
         L.tops_kda_gate_bwd_workspace.restype = ctypes.c_int64

@@ -68,3 +68,15 @@ def test_prepare_chunk_indices_empty_and_negative_segments():
     np.testing.assert_array_equal(prepare_chunk_indices([0, 10, 10, 20], 16), [[0, 0], [2, 0]])
     with pytest.raises(ValueError):
         prepare_chunk_indices([0, 10, 5, 20], 16)
+
+
+def test_kda_noalloc_rejects_oversize_on_host():
+    """The allocation-free KDA forward checks its workspace against the static scratch before
+    any HIP call: an oversize call returns TOPS_ERR_SHAPE (no device needed)."""
+    from tops import _native as N
+    L = N.lib()
+    cap = L.tops_kda_chunk_fwd_noalloc_max_bytes()
+    T = cap // (8 * (128 + 128) * 4) + 64
+    rc = N._fn("tops_kda_chunk_fwd_noalloc")(*([None] * 11), 0, 1, T, 8, 128, 128, 1, 1,
+                                              ctypes.c_float(1.0), None)
+    assert rc == -2 and b"static scratch" in L.tops_last_error()
