@@ -30,7 +30,9 @@
 
 namespace tops {
 
-template <typename TIn, typename TV, int KP, int VP>
+// GK: the per-channel gate mode only (kGateK: GLA and KDA), compiled without gate-mode
+// branches; !GK serves the per-token and constant gates chosen at run time.
+template <typename TIn, typename TV, int KP, int VP, bool GK>
 __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
   constexpr int C = kChunk;
   constexpr int KH = 32;                       // channels per pass
@@ -104,7 +106,7 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
   const uint32_t rowK = (uint32_t)(H * K), rowV = (uint32_t)(H * V);
   const rsrc_t Rq = make_rsrc_rows((const TIn*)p.q, e0, nrows, K);
   const rsrc_t Rk = make_rsrc_rows((const TIn*)p.k, e0, nrows, K);
-  const int gmode = p.gate_mode;
+  const int gmode = GK ? kGateK : p.gate_mode;
   const rsrc_t Rg = make_rsrc_rows(p.g, e0, nrows, gmode == kGateK ? K : 1);
   const float gam_h = gmode == kGateGamma ? p.g[hh] : 0.f;
 
@@ -151,9 +153,9 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
   const int ch = tid & 31, sg = tid >> 5;
   float rq[8], rk[8], rg[8];
   // gate element (row r, channel kc): per-channel [.., K], per-token [.., 1], or none (gamma)
-  const bool gk_mode = gmode == kGateK;
+  const bool gk_mode = GK || gmode == kGateK;
   const uint32_t gstr = gk_mode ? rowK * 4u : (uint32_t)H * 4u;
-  const bool gload = gmode == kGateK || gmode == kGateS;   // the constant gates load nothing
+  const bool gload = GK || gmode == kGateK || gmode == kGateS;   // the constant gates load nothing
   auto load_pass = [&](int ps) {
     const int kc = ps * KH + ch;
     const bool ok = kc < K;
@@ -262,13 +264,19 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
         gadd[a] = bld128(Rdga, o, 0);
       }
     }
-    // ---- gate cumsum of the pass (thread: channel ch, rows 8sg..8sg+7)
+    // ---- gate cumsum of the pass (thread: channel ch, rows 8sg..8sg+7); the constant gates
+    // (g_gamma [H] or [H, K]) give every valid row the same value
+    float gconst = gam_h;
+    if constexpr (!GK) {
+      if (gmode == kGateGammaK) gconst = cb + ch < K ? p.g[(size_t)hh * K + cb + ch] : 0.f;
+    }
     float G[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       float x = rg[i];
-      if (gmode == kGateGamma) x = (cb + ch < K && 8 * sg + i < nval) ? gam_h : 0.f;
-      else if (gmode == kGateGammaK) x = (cb + ch < K && 8 * sg + i < nval) ? p.g[(size_t)hh * K + cb + ch] : 0.f;
+      if constexpr (!GK) {
+        if (!gload) x = (cb + ch < K && 8 * sg + i < nval) ? gconst : 0.f;
+      }
       G[i] = x * kLog2e + (i > 0 ? G[i - 1] : 0.f);
     }
     // (no barrier before this write: sTot is last read before the previous pass's planes
@@ -468,7 +476,7 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
       add[r] = fast_exp2(sGam[cl + r]) * sHdh[cl + r] + sZk[cl + r] + sZk[KH + cl + r];
       if (rh == 0) add[r] += sBlk[cl + r];
     }
-    if (gmode == kGateK || (gmode == kGateGammaK && p.dg)) {
+    if (GK || gmode == kGateK || (gmode == kGateGammaK && p.dg)) {
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
         const int tok = 16 * (2 * rh + a) + l16;
@@ -510,8 +518,16 @@ hipError_t launch_gla_dqkg(const DqkgParams& p, hipStream_t s) {
   const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
   const int vp = p.V <= 32 ? 32 : (p.V <= 64 ? 64 : 128);
   dim3 grid(p.total * p.H), block(256);
-#define TOPS_DQKG(KPV, VPV) \
-  if (kp == KPV && vp == VPV) { hipLaunchKernelGGL((gla_dqkg_kernel<TIn, TV, KPV, VPV>), grid, block, 0, s, p); return hipGetLastError(); }
+  // the fp32-v instantiation (the KDA backward) serves only the per-channel gate
+  constexpr bool kAllModes = std::is_same<TIn, TV>::value;
+  const bool gk = !kAllModes || p.gate_mode == kGateK;
+#define TOPS_DQKG(KPV, VPV)                                                                   \
+  if (kp == KPV && vp == VPV) {                                                               \
+    if (gk) hipLaunchKernelGGL((gla_dqkg_kernel<TIn, TV, KPV, VPV, true>), grid, block, 0, s, p); \
+    else if constexpr (kAllModes)                                                             \
+      hipLaunchKernelGGL((gla_dqkg_kernel<TIn, TV, KPV, VPV, false>), grid, block, 0, s, p);  \
+    return hipGetLastError();                                                                 \
+  }
   TOPS_DQKG(32, 32) TOPS_DQKG(32, 64) TOPS_DQKG(32, 128)
   TOPS_DQKG(64, 32) TOPS_DQKG(64, 64) TOPS_DQKG(64, 128)
   TOPS_DQKG(128, 32) TOPS_DQKG(128, 64) TOPS_DQKG(128, 128)

@@ -45,8 +45,10 @@
 
 namespace tops {
 
-
-template <typename TIn, int KP, bool REV, bool DELTA, bool ST>
+// GK: the per-channel gate mode only (kGateK, the GLA and KDA path), compiled on its own so
+// that the hot path carries no gate-mode branches; !GK serves the per-token and constant
+// gates (kGateS, kGateGamma, kGateGammaK) chosen at run time.
+template <typename TIn, int KP, bool REV, bool DELTA, bool ST, bool GK>
 __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   constexpr int NW = 8;                  // wave64s per workgroup
   constexpr int NTH = 64 * NW;
@@ -165,8 +167,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   const uint32_t offY = ycolok ? ((uint32_t)(yseg * YR) * rowV + yv) * ES : kOOB;
   // gate load: per-channel [.., K] float4, or the per-(token, head) scalar read as the first
   // word of a 16-byte load; the gamma mode loads nothing (out of range -> 0)
-  const int gmode = p.gate_mode;
-  const bool gk_mode = gmode == kGateK;
+  const int gmode = GK ? kGateK : p.gate_mode;
+  const bool gk_mode = GK || gmode == kGateK;
   const uint32_t offGm = gk_mode ? offG : (gmode == kGateS ? (uint32_t)r0 * H * 4u : kOOB);
   const uint32_t gstride = gk_mode ? rowK * 4 : (uint32_t)H * 4;
   const float gam_h = gmode == kGateGamma ? p.g[hh] : 0.f;
@@ -218,7 +220,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       // the gate mode's transform is applied when the chunk is consumed, so the prefetch
       // never waits: four channels [.., K], or the one per-(token, head) word [.., 1]
       // (gamma: offGm is out of range, nothing is read)
-      if (gk_mode) rs.rg[i] = bld128(Rg, ok ? offGm : kOOB, i * gstride);
+      if constexpr (GK) rs.rg[i] = bld128(Rg, ok ? offGm : kOOB, i * gstride);
+      else if (gk_mode) rs.rg[i] = bld128(Rg, ok ? offGm : kOOB, i * gstride);
       else rs.rg[i] = make_uint4(bld32(Rg, ok ? offGm : kOOB, i * gstride), 0u, 0u, 0u);
     }
     if constexpr (!FWD_DELTA) {
@@ -294,7 +297,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     for (int i = 0; i < RPT; ++i) {
       float x[4];
       unpack4(rs.rg[i], x);
-      if (gmode == kGateS) {
+      if constexpr (GK) {
+      } else if (gmode == kGateS) {
         x[1] = x[2] = x[3] = x[0];
       } else if (!gk_mode) {   // constant gates: zero on the rows past the sequence
 #pragma unroll
@@ -809,9 +813,23 @@ template <typename TIn, bool REV, bool DELTA>
 hipError_t launch_gla_sweep(const SweepParams& p, hipStream_t s) {
   const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
   dim3 grid(p.NV * p.H * p.N);
-  if (kp == 32) hipLaunchKernelGGL((gla_sweep_kernel<TIn, 32, REV, DELTA, false>), grid, dim3(512), 0, s, p);
-  else if (kp == 64) hipLaunchKernelGGL((gla_sweep_kernel<TIn, 64, REV, DELTA, false>), grid, dim3(512), 0, s, p);
-  else hipLaunchKernelGGL((gla_sweep_kernel<TIn, 128, REV, DELTA, false>), grid, dim3(512), 0, s, p);
+  const bool gk = DELTA || p.gate_mode == kGateK;
+#define TOPS_SWEEP(KPV, GKV) \
+  hipLaunchKernelGGL((gla_sweep_kernel<TIn, KPV, REV, DELTA, false, GKV>), grid, dim3(512), 0, s, p)
+  if constexpr (DELTA) {
+    if (kp == 32) TOPS_SWEEP(32, true);
+    else if (kp == 64) TOPS_SWEEP(64, true);
+    else TOPS_SWEEP(128, true);
+  } else if (gk) {
+    if (kp == 32) TOPS_SWEEP(32, true);
+    else if (kp == 64) TOPS_SWEEP(64, true);
+    else TOPS_SWEEP(128, true);
+  } else {
+    if (kp == 32) TOPS_SWEEP(32, false);
+    else if (kp == 64) TOPS_SWEEP(64, false);
+    else TOPS_SWEEP(128, false);
+  }
+#undef TOPS_SWEEP
   return hipGetLastError();
 }
 
@@ -819,9 +837,18 @@ template <typename TIn, bool REV>
 hipError_t launch_gla_state_pass(const SweepParams& p, hipStream_t s) {
   const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
   dim3 grid(p.NV * p.H * p.N);
-  if (kp == 32) hipLaunchKernelGGL((gla_sweep_kernel<TIn, 32, REV, false, true>), grid, dim3(512), 0, s, p);
-  else if (kp == 64) hipLaunchKernelGGL((gla_sweep_kernel<TIn, 64, REV, false, true>), grid, dim3(512), 0, s, p);
-  else hipLaunchKernelGGL((gla_sweep_kernel<TIn, 128, REV, false, true>), grid, dim3(512), 0, s, p);
+#define TOPS_STATE(KPV, GKV) \
+  hipLaunchKernelGGL((gla_sweep_kernel<TIn, KPV, REV, false, true, GKV>), grid, dim3(512), 0, s, p)
+  if (p.gate_mode == kGateK) {
+    if (kp == 32) TOPS_STATE(32, true);
+    else if (kp == 64) TOPS_STATE(64, true);
+    else TOPS_STATE(128, true);
+  } else {
+    if (kp == 32) TOPS_STATE(32, false);
+    else if (kp == 64) TOPS_STATE(64, false);
+    else TOPS_STATE(128, false);
+  }
+#undef TOPS_STATE
   return hipGetLastError();
 }
 

@@ -156,6 +156,36 @@ __device__ __forceinline__ bf16x8 cat44(const uint2& x, const uint2& y) {
 
 __device__ __forceinline__ int cdiv(int a, int b) { return (a + b - 1) / b; }
 
+// ---------------------------------------------------------------- LDS transpose reads
+// ds_read_b64_tr_b16 (gfx950), lane layout measured on MI355X: within each group of 16
+// lanes, lane i supplies the address of row i/4, columns 4(i%4)..4(i%4)+3 of a 4 x 16 block
+// of a row-major 16-bit matrix, and receives column i's four rows.  Two such reads give an
+// MFMA 16x16x32 operand whose contraction index runs down the rows of a row-major plane:
+// lane l gets P[r0 + 8(l/16) + 0..7][c0 + l%16].
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bf16x8 tr_read8(const uint16_t* plane, int ld, int r0, int c0, int lane) {
+  const int g = lane >> 4, i = lane & 15;
+  const uint16_t* p = plane + (r0 + 8 * g + (i >> 2)) * ld + c0 + 4 * (i & 3);
+  typedef __attribute__((address_space(3))) v4i16 lds_v4;
+  const v4i16 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4*)(p));
+  const v4i16 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4*)(p + 4 * ld));
+  const uint2 ua = __builtin_bit_cast(uint2, a), ub = __builtin_bit_cast(uint2, b);
+  return __builtin_bit_cast(bf16x8, make_uint4(ua.x, ua.y, ub.x, ub.y));
+}
+// The same for two separate 4-row blocks (rows ra + 4(l/16) + 0..3 and rb + 4(l/16) + 0..3):
+// the operand of a contraction permuted as the accumulator tiles of two 16-blocks hold it.
+__device__ __forceinline__ bf16x8 tr_read44(const uint16_t* plane, int ld, int ra, int rb, int c0,
+                                           int lane) {
+  const int g = lane >> 4, i = lane & 15;
+  typedef __attribute__((address_space(3))) v4i16 lds_v4;
+  const uint16_t* pa = plane + (ra + 4 * g + (i >> 2)) * ld + c0 + 4 * (i & 3);
+  const uint16_t* pb = plane + (rb + 4 * g + (i >> 2)) * ld + c0 + 4 * (i & 3);
+  const v4i16 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4*)(pa));
+  const v4i16 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4*)(pb));
+  const uint2 ua = __builtin_bit_cast(uint2, a), ub = __builtin_bit_cast(uint2, b);
+  return __builtin_bit_cast(bf16x8, make_uint4(ua.x, ua.y, ub.x, ub.y));
+}
+
 // ---------------------------------------------------------------- buffer resources
 // Raw (stride 0) buffer descriptors: 32-bit byte offsets from an SGPR base, and the
 // hardware range check returns 0 for a load (drops a store) whose offset is at or past
