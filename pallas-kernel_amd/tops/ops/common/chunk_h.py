@@ -114,4 +114,32 @@ def chunk_bwd_dh_kernel(q, k, v, g=None, g_gamma=None, gk=None, do=None, dht=Non
     return dh, dh0
 
 
-__all__ = ["chunk_fwd_h_ref", "chunk_fwd_h_kernel", "chunk_bwd_dh_ref", "chunk_bwd_dh_kernel"]
+def chunk_fwd_h_kernel_varlen(k, v, g=None, g_gamma=None, gk=None, gv=None, h0=None,
+                              output_final_state: bool = False, cu_seqlens_dev=None,
+                              chunk_size: int = 128, split_size: int | None = None,
+                              states_in_fp32: bool = False, interpret: bool = False):
+    """Packed-varlen form (tops/ops/common/chunk_h.py:970-1113): k [B,T,H,K], v [B,T,H,V]
+    with the B*T tokens one packed stream and cu_seqlens_dev [N+1] (multiples of
+    chunk_size) its sequence boundaries.  Returns h [B*T / chunk_size, H, K, V] (the state
+    before every chunk, k.dtype or float32 with ``states_in_fp32``) and ht [N, H, K, V]
+    float32 when ``output_final_state`` else None.  g and gv are rejected as there
+    (check_chunk_fwd, chunk_h.py:965-966)."""
+    del interpret
+    require(g is None, "x should be None.")
+    require(gv is None, "x should be None.")
+    C = int(chunk_size)
+    BS = C if split_size is None else int(split_size)
+    require(BS % C == 0, f"The `split_size` (got {BS}) must be a multiple of `chunk_size` {C}")
+    require(BS == C, "split_size with cu_seqlens is not supported")
+    B, T, H, K = k.shape
+    V = v.shape[-1]
+    require(T % C == 0, "T mod chunk_size must equal to 0.")
+    flat = (lambda x: None if x is None else x.reshape((1, B * T) + tuple(x.shape[2:])))
+    cu = cu_seqlens_dev if cu_seqlens_dev is not None else [0, B * T]
+    h, ht = _recurrence(flat(k), flat(v), None, g_gamma, flat(gk), h0, cu, C, False, 1.0, 1,
+                        torch.float32 if states_in_fp32 else k.dtype, output_final_state)
+    return h.reshape(-1, H, K, V), ht
+
+
+__all__ = ["chunk_fwd_h_ref", "chunk_fwd_h_kernel", "chunk_fwd_h_kernel_varlen", "chunk_bwd_dh_ref",
+           "chunk_bwd_dh_kernel"]

@@ -250,3 +250,19 @@ def chunk_gla_bwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, h, A, do,
             dg = dg.sum(dim=(0, 1))
         dg = dg.sum_to_size(*gg.shape) if gg.dim() > 0 else dg.sum()
     return dq, dk, dv, dg, dh0
+
+
+def chunk_gla_bwd_with_pl(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, h, A, do, dht,
+                          cu_seqlens=None, chunk_size: int = 64):
+    """The reference's kernel-backed backward orchestrator (tops/ops/gla/chunk.py:1000-1095):
+    the same contract as chunk_gla_bwd, including its asserts that T and the sequence
+    boundaries are multiples of chunk_size (chunk.py:1032-1035).  Here both orchestrators run
+    the same HIP backward."""
+    C = int(chunk_size)
+    assert q.shape[1] % C == 0, "T must be a multiple of chunk_size for chunk_gla_bwd_with_pl"
+    if cu_seqlens is not None:
+        cu = cu_seqlens.tolist() if isinstance(cu_seqlens, torch.Tensor) else list(cu_seqlens)
+        assert all(int(x) % C == 0 for x in cu), (
+            "cu_seqlens must be multiples of chunk_size for chunk_gla_bwd_with_pl")
+    return chunk_gla_bwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, h, A, do, dht,
+                         cu_seqlens=cu_seqlens, chunk_size=chunk_size)

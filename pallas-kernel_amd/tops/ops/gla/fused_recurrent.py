@@ -7,12 +7,15 @@
 
 `fused_recurrent_gla` is differentiable, covering gk, gv, reverse, initial_state and
 cu_seqlens.  Two HIP implementations of the same recurrence are used:
-  * without gv and in forward time order (the common case, and BASELINE config 2) the
-    recurrence is computed chunkwise on MFMA by the chunk kernels (gla_sweep.hip,
-    gla_dqkg.hip) -- the same sums, grouped by 64-token chunks;
-  * with gv or reverse=True, the per-token kernels of gla_recurrent.hip (state in
-    registers, one token at a time) run the forward, a replay + reverse backward and the
-    gate-gradient suffix sums.
+  * without gv (the common case, and BASELINE config 2) the recurrence is computed
+    chunkwise on MFMA by the chunk kernels (gla_sweep.hip, gla_dqkg.hip) -- the same
+    sums, grouped by 64-token chunks.  reverse=True runs the same recurrence from the last
+    token to the first (tops/cpu/ops/gla/fused_recurrent.py:116-160: one body, iterated
+    backwards), i.e. the forward recurrence on every sequence's time-reversed inputs: the
+    inputs are reversed per sequence, swept forward, and the output reversed back (the
+    reversal is part of the autograd graph);
+  * with gv, the per-token kernels of gla_recurrent.hip (state in registers, one token at
+    a time) run the forward, a replay + reverse backward and the gate-gradient suffix sums.
 """
 from __future__ import annotations
 
@@ -143,8 +146,28 @@ class _FusedRecurrentGLA(torch.autograd.Function):
 
 
 def _chunked(gv, reverse, K, V):
-    """Whether the chunk (MFMA) kernels compute this call."""
-    return gv is None and not reverse and K % 8 == 0 and V % 8 == 0 and V <= 128
+    """Whether the chunk (MFMA) kernels compute this call (reverse=True through a per-sequence
+    time reversal)."""
+    del reverse
+    return gv is None and K % 8 == 0 and V % 8 == 0 and V <= 128
+
+
+def time_reversal(T: int, cu_seqlens, device):
+    """Index that reverses every sequence in time: [T] for fixed length (applied per batch
+    row), the packed varlen layout otherwise.  Its own inverse."""
+    if cu_seqlens is None:
+        return torch.arange(T - 1, -1, -1, device=device)
+    cu = [int(x) for x in (cu_seqlens.tolist() if isinstance(cu_seqlens, torch.Tensor) else cu_seqlens)]
+    idx = [cu[n] + cu[n + 1] - 1 - t for n in range(len(cu) - 1) for t in range(cu[n], cu[n + 1])]
+    return torch.tensor(idx, device=device, dtype=torch.long)
+
+
+def _reversed_chunk(fn, q, k, v, g, cu_seqlens, **kw):
+    """fn (a chunk op) on the time-reversed sequences; returns (o in original order, ht)."""
+    rev = time_reversal(q.shape[1], cu_seqlens, q.device)
+    flip = (lambda x: None if x is None else x.index_select(1, rev))
+    o, ht = fn(flip(q), flip(k), flip(v), flip(g), cu_seqlens=cu_seqlens, **kw)
+    return flip(o), ht
 
 
 def fused_recurrent_gla(q, k, v, gk=None, gv=None, scale=None, initial_state=None,
@@ -160,6 +183,11 @@ def fused_recurrent_gla(q, k, v, gk=None, gv=None, scale=None, initial_state=Non
                        cu_seqlens)
     if _chunked(gv, reverse, K, V):
         from .chunk import chunk_gla
+        if reverse:
+            return _reversed_chunk(
+                lambda q_, k_, v_, g_, **kw: chunk_gla(q_, k_, v_, g_, **kw), q, k, v, gk,
+                cu_seqlens, scale=scale, initial_state=initial_state,
+                output_final_state=output_final_state)
         return chunk_gla(q, k, v, gk, scale=scale, initial_state=initial_state,
                          output_final_state=output_final_state, cu_seqlens=cu_seqlens)
     o, ht = _FusedRecurrentGLA.apply(q, k, v, gk, gv, initial_state, float(scale),
@@ -173,7 +201,7 @@ def fused_recurrent_gla_fwd(q, k, v, gk=None, gv=None, scale=None, initial_state
     B, T, H, K, V, n = _check(q, k, v, gk, gv, initial_state, cu_seqlens)
     if scale is None:
         scale = K ** -0.5
-    if _chunked(gv, reverse, K, V):
+    if _chunked(gv, reverse, K, V) and not reverse:
         from .chunk import chunk_gla
         return chunk_gla(q, k, v, gk, scale=scale, initial_state=initial_state,
                          output_final_state=output_final_state, cu_seqlens=cu_seqlens)
@@ -194,7 +222,7 @@ def fused_recurrent_gla_bwd(q, k, v, gk=None, gv=None, o=None, do=None, dht=None
     assert gv is None or o is not None, "o (forward output) is required when gv is used"
     if scale is None:
         scale = K ** -0.5
-    if _chunked(gv, reverse, K, V):
+    if _chunked(gv, reverse, K, V) and not reverse:
         from .chunk import chunk_gla_bwd
         dq, dk, dv, dg, dh0 = chunk_gla_bwd(q, k, v, gk, None, None, scale, initial_state, None,
                                             None, do, dht, cu_seqlens=cu_seqlens)

@@ -5,8 +5,10 @@ o_t = h_t^T (scale q_t) is GLA's with the gate shared by all K channels.  In for
 order it runs on the chunk kernels' per-token scalar-gate mode (tops.ops.simple_gla
 chunk_simple_gla with g [B,T,H]: the same sums grouped by 64-token chunks); g and g_gamma
 are combined into that one [B,T,H] gate, g + g_gamma (tops/cpu/ops/simple_gla/naive.py:
-113-125).  reverse=True runs the per-token kernels of tops.ops.gla.fused_recurrent_gla
-with the gate as a broadcast view over K.  Either way the combination is part of the
+113-125).  reverse=True runs the same on every sequence reversed in time (the recurrence
+iterated from the last token).  Shapes the chunk kernels do not take run the per-token
+kernels of tops.ops.gla.fused_recurrent_gla with the gate as a broadcast view over K.
+Either way the combination is part of the
 autograd graph, so the gradients w.r.t. g [B,T,H] and g_gamma [H] come back summed over the
 broadcast axes: the gradient of the reference's lax.scan.
 """
@@ -14,7 +16,7 @@ from __future__ import annotations
 
 import torch
 
-from ..gla.fused_recurrent import fused_recurrent_gla
+from ..gla.fused_recurrent import _reversed_chunk, fused_recurrent_gla
 from .chunk import chunk_simple_gla
 
 
@@ -25,16 +27,21 @@ def fused_recurrent_simple_gla(q, k, v, g=None, g_gamma=None, scale=None, initia
     assert g is None or tuple(g.shape) == (B, T, H), f"g shape {tuple(g.shape)} != {(B, T, H)}"
     assert g_gamma is None or tuple(g_gamma.shape) == (H,), f"g_gamma shape must be ({H},)"
     V = v.shape[-1]
-    if not reverse and K % 8 == 0 and V % 8 == 0 and K <= 128 and V <= 128:
+    if K % 8 == 0 and V % 8 == 0 and K <= 128 and V <= 128:
         gs = None
         if g is not None:
             gs = g.to(torch.float32)
         if g_gamma is not None:
             gg = torch.as_tensor(g_gamma, device=q.device).to(torch.float32)
             gs = gg.expand(B, T, H) if gs is None else gs + gg
-        return chunk_simple_gla(q, k, v, None, initial_state=initial_state, scale=scale,
-                                output_final_state=output_final_state, g=gs,
-                                cu_seqlens=cu_seqlens)
+
+        def run(q_, k_, v_, g_, cu_seqlens=None):
+            return chunk_simple_gla(q_, k_, v_, None, initial_state=initial_state, scale=scale,
+                                    output_final_state=output_final_state, g=g_,
+                                    cu_seqlens=cu_seqlens)
+        if reverse:
+            return _reversed_chunk(run, q, k, v, gs, cu_seqlens)
+        return run(q, k, v, gs, cu_seqlens)
     gk = None
     if g is not None:
         gk = g.to(torch.float32)[..., None]

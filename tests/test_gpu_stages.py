@@ -508,3 +508,71 @@ def test_chunk_kda_bwd_functional(case, cuda_device):
     print(" ".join(f"{n_}={e:.2e}" for n_, e in errs.items()))
     for n_, e in errs.items():
         assert e < 1e-4, (n_, e)
+
+
+VARLEN_H_CASES = [
+    dict(T=512, H=2, K=128, V=128, C=128, cu=[0, 128, 384, 512], gates=("gk",), h0=True),
+    dict(T=256, H=2, K=64, V=64, C=64, cu=[0, 64, 256], gates=("gk", "g_gamma"), h0=False),
+    dict(T=192, H=1, K=32, V=64, C=64, cu=[0, 192], gates=("g_gamma",), h0=True),
+]
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("c", VARLEN_H_CASES, ids=lambda c: "T{T}-H{H}-K{K}-V{V}-C{C}-".format(**c) + "+".join(c["gates"]))
+def test_chunk_fwd_h_kernel_varlen(c, dt, cuda_device):
+    """chunk_fwd_h_kernel_varlen (tops/ops/common/chunk_h.py:970-1113): the state before every
+    chunk of a packed varlen stream [NT, H, K, V] and the final states, against the oracle's
+    per-sequence recurrence; the scalar gate g and gv are rejected as in the reference."""
+    from tops.ops.common import chunk_fwd_h_kernel_varlen
+    T, H, K, V, C, cu = (c[x] for x in ("T", "H", "K", "V", "C", "cu"))
+    rng = np.random.default_rng(T + K + C)
+    k = rng.standard_normal((1, T, H, K)).astype(np.float32)
+    v = rng.standard_normal((1, T, H, V)).astype(np.float32)
+    n = len(cu) - 1
+    s0 = rng.standard_normal((n, H, K, V)) * 0.1 if c["h0"] else None
+    gates, total = _gates(rng, 1, T, H, K, C, c["gates"], cu)
+    f = lambda x: None if x is None else to_dev(x, torch.float32, cuda_device)
+    print(f"chunk_fwd_h_kernel_varlen {c} {dt}", flush=True)
+    h, ht = chunk_fwd_h_kernel_varlen(to_dev(k, dt, cuda_device), to_dev(v, dt, cuda_device),
+                                      g_gamma=f(gates.get("g_gamma")), gk=f(gates.get("gk")),
+                                      h0=f(s0), output_final_state=True,
+                                      cu_seqlens_dev=torch.tensor(cu, dtype=torch.int32, device=cuda_device),
+                                      chunk_size=C, states_in_fp32=True)
+    hs_ref, ht_ref = _oracle_states(seen(k, dt), seen(v, dt), total, s0, C, cu, False, 1.0)
+    assert h.shape == (T // C, H, K, V) and h.dtype == torch.float32
+    assert rel(host(h), hs_ref[0]) < _lim(dt) and rel(host(ht), ht_ref) < F32
+    with pytest.raises(AssertionError):
+        chunk_fwd_h_kernel_varlen(to_dev(k, dt, cuda_device), to_dev(v, dt, cuda_device),
+                                  g=torch.zeros(1, T, H, device=cuda_device), cu_seqlens_dev=cu,
+                                  chunk_size=C)
+
+
+@pytest.mark.parametrize("c", [dict(B=2, T=128, H=2, K=128, V=128, h0=False, dht=False),
+                               dict(B=1, T=128, H=2, K=128, V=128, h0=True, dht=False),
+                               dict(B=1, T=128, H=2, K=128, V=128, h0=False, dht=True),
+                               dict(B=1, T=128, H=2, K=128, V=128, h0=True, dht=True),
+                               dict(B=1, T=256, H=2, K=64, V=64, h0=True, dht=True, cu=[0, 64, 256])],
+                         ids=lambda c: "B{B}-T{T}-h0{h0}-dht{dht}".format(**c) + ("-varlen" if "cu" in c else ""))
+def test_chunk_gla_bwd_with_pl(c, cuda_device):
+    """chunk_gla_bwd_with_pl (tops/ops/gla/chunk.py:1000-1095) on the reference test's shapes
+    (tests/ops/gla/test_pallas_chunk_bwd_with_pl.py:17-22) against the oracle backward; T and
+    cu_seqlens off the chunk grid are rejected."""
+    from tops.ops.gla import chunk_gla_bwd_with_pl
+    from _inputs import gla_inputs
+    B, T, H, K, V = (c[x] for x in "BTHKV")
+    cu = c.get("cu")
+    n = B if cu is None else len(cu) - 1
+    d = gla_inputs(B, T, H, K, V, 42 + T + K, gate_div=4.0, h0=c["h0"], N=n, grads=True)
+    t = {x: to_dev(d[x], torch.float32, cuda_device) for x in ("q", "k", "v", "g", "h0", "do", "dht")}
+    dht = t["dht"] if c["dht"] else None
+    got = chunk_gla_bwd_with_pl(t["q"], t["k"], t["v"], t["g"], None, None, K ** -0.5, t["h0"], None,
+                                None, t["do"], dht, cu_seqlens=cu, chunk_size=64)
+    ref = O.chunk_gla_bwd(d["q"], d["k"], d["v"], d["g"], K ** -0.5, d["h0"], d["do"],
+                          d["dht"] if c["dht"] else None, cu_seqlens=cu)
+    for name, a, b in zip(("dq", "dk", "dv", "dg", "dh0"), got, ref):
+        if a is None or b is None:
+            continue
+        assert rel(host(a), b) < 1e-4, name
+    with pytest.raises(AssertionError):
+        chunk_gla_bwd_with_pl(t["q"][:, :100], t["k"][:, :100], t["v"][:, :100], t["g"][:, :100],
+                              None, None, K ** -0.5, None, None, None, t["do"][:, :100], None)

@@ -11,7 +11,7 @@ def test_gla_exports_match_reference_names():
     names = ["naive_recurrent_gla", "chunk_gla", "chunk_local_cumsum", "chunk_fwd_h",
              "chunk_gla_fwd_intra_gk", "chunk_gla_fwd_o_gk", "chunk_gla_fwd",
              "chunk_gla_bwd_dA_ref", "chunk_gla_bwd_dv_ref", "chunk_gla_bwd_dqk_intra_ref",
-             "chunk_gla_bwd_dqkg_ref", "chunk_gla_bwd", "fused_chunk_gla",
+             "chunk_gla_bwd_dqkg_ref", "chunk_gla_bwd", "chunk_gla_bwd_with_pl", "fused_chunk_gla",
              "fused_recurrent_gla", "fused_recurrent_gla_bwd"]
     for n in names:
         assert n in G.__all__ and callable(getattr(G, n)), n
@@ -41,7 +41,7 @@ def test_kda_exports_match_reference_names():
 
 def test_common_exports():
     from tops.ops.common import chunk_h, cumsum
-    for n in ("chunk_fwd_h_ref", "chunk_fwd_h_kernel", "chunk_bwd_dh_ref", "chunk_bwd_dh_kernel"):
+    for n in ("chunk_fwd_h_ref", "chunk_fwd_h_kernel", "chunk_fwd_h_kernel_varlen", "chunk_bwd_dh_ref", "chunk_bwd_dh_kernel"):
         assert callable(getattr(chunk_h, n))
     assert callable(cumsum.chunk_local_cumsum_vector)
 
