@@ -133,6 +133,39 @@ int tops_gla_chunk_bwd_dqkg_gamma(const void* q, const void* k, const void* v,
                                   const int32_t* chunk_map, int total_chunks, int B, int T, int H,
                                   int K, int V, int N, int dtype, float scale, void* stream);
 
+/* The training path of the GLA / simple GLA chunk ops with interleaved state checkpoints
+ * (bf16 inputs only; K, V <= 128): the same three stages as tops_gla_chunk_fwd /
+ * tops_gla_chunk_bwd_dh / tops_gla_chunk_bwd_dqkg (K7+K2+K3, K8 and K4 of
+ * tops/ops/gla/chunk.py:1103-1199, 832-1095 and tops/ops/common/chunk_h.py:685-878), with
+ * the residual states kept as one buffer ckpt [total_chunks,H,K,V] fp32:
+ *   tops_chunk_fwd_paired     writes the state before every even global chunk;
+ *   tops_chunk_bwd_dh_paired  writes dh (the gradient w.r.t. the state after the chunk)
+ *                             for every odd global chunk into the same buffer;
+ *   tops_chunk_bwd_dqkg_paired takes the chunks in pairs (2i, 2i+1) and rebuilds the
+ *                             missing state of each from its partner's (one sweep step);
+ *                             h0 / dht (the forward's initial state and the final-state
+ *                             gradient, [N,H,K,V] or NULL) stand in where the partner lies
+ *                             in another sequence.
+ * Half the checkpoint bytes of the unpaired path, written and read.  gate_mode and g as
+ * tops_chunk_state_pass (0: g [B,T,H,K]; 1: g [B,T,H]; 2: g_gamma [H]; 3: g_gamma [H,K]);
+ * dg as the unpaired entry of that gate (NULL for mode 2).  Other arguments as the
+ * unpaired entry points. */
+int tops_chunk_fwd_paired(const void* q, const void* k, const void* v, const float* g,
+                          int gate_mode, const float* h0, void* o, float* ht, float* ckpt,
+                          const int32_t* cu_seqlens, const int32_t* chunk_offsets, int B, int T,
+                          int H, int K, int V, int N, int dtype, float scale, void* stream);
+int tops_chunk_bwd_dh_paired(const void* q, const void* k, const float* g, int gate_mode,
+                             const void* do_, const float* dht, float* ckpt, void* dv,
+                             float* dh0, const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                             int B, int T, int H, int K, int V, int N, int dtype, float scale,
+                             void* stream);
+int tops_chunk_bwd_dqkg_paired(const void* q, const void* k, const void* v, const float* g,
+                               int gate_mode, const void* do_, const float* h0, const float* dht,
+                               const float* ckpt, void* dq, void* dk, float* dg,
+                               const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                               const int32_t* chunk_map, int total_chunks, int B, int T, int H,
+                               int K, int V, int N, int dtype, float scale, void* stream);
+
 /* Simple GLA: one log-gate per (token, head) -- g [B,T,H] fp32 -- or a constant per-head
  * log-decay g_gamma [H] fp32; pass exactly one.  The state recurrence is GLA's with the
  * gate shared by all K channels.  Replaces tops.ops.simple_gla.chunk_simple_gla_fwd /

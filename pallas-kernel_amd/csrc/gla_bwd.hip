@@ -61,7 +61,8 @@ using namespace tops;
 static int bwd_dh_impl(const void* q, const void* k, const float* g, const void* do_,
                        const float* dht, float* dh_work, void* dv, float* dh0,
                        const int32_t* cu_seqlens, const int32_t* chunk_offsets, int B, int T, int H,
-                       int K, int V, int N, int dtype, float scale, int gate_mode, void* stream) {
+                       int K, int V, int N, int dtype, float scale, int gate_mode, void* stream,
+                       int ckpt_par = 0) {
   if (!q || !k || !g || !do_ || !dh_work || !dv)
     return tops_set_error(TOPS_ERR_NULL, "gla_chunk_bwd_dh: null tensor");
   int rc = check_bwd("gla_chunk_bwd_dh", B, T, H, K, V, N, 0, cu_seqlens, chunk_offsets, nullptr,
@@ -69,6 +70,7 @@ static int bwd_dh_impl(const void* q, const void* k, const float* g, const void*
   if (rc != TOPS_OK) return rc;
   SweepParams p{q, k, g, do_, dht, dv, dh0, dh_work, cu_seqlens, chunk_offsets,
                 B, T, H, K, V, N, (V + 63) / 64, scale, gate_mode};
+  p.ckpt_par = ckpt_par;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e = dtype == TOPS_BF16 ? launch_gla_sweep<uint16_t, true>(p, s)
                                     : launch_gla_sweep<float, true>(p, s);
@@ -81,7 +83,8 @@ static int bwd_dqkg_impl(const void* q, const void* k, const void* v, const floa
                          void* dk, float* dg, const int32_t* cu_seqlens,
                          const int32_t* chunk_offsets, const int32_t* chunk_map, int total_chunks,
                          int B, int T, int H, int K, int V, int N, int dtype, float scale,
-                         int gate_mode, void* stream) {
+                         int gate_mode, void* stream, const float* h0 = nullptr,
+                         const float* dht = nullptr, int paired = 0) {
   if (!q || !k || !v || !g || !do_ || !h_ckpt || !dh_work || !dq || !dk ||
       ((gate_mode == kGateK || gate_mode == kGateS) && !dg))
     return tops_set_error(TOPS_ERR_NULL, "gla_chunk_bwd_dqkg: null tensor");
@@ -90,6 +93,9 @@ static int bwd_dqkg_impl(const void* q, const void* k, const void* v, const floa
   if (rc != TOPS_OK) return rc;
   DqkgParams p{q, k, v, g, do_, h_ckpt, dh_work, dq, dk, dg, cu_seqlens, chunk_offsets, chunk_map,
                total_chunks, B, T, H, K, V, N, scale, gate_mode};
+  p.paired = paired;
+  p.h0 = h0;
+  p.dht = dht;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e = dtype == TOPS_BF16 ? launch_gla_dqkg<uint16_t>(p, s) : launch_gla_dqkg<float>(p, s);
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
@@ -199,4 +205,48 @@ extern "C" int tops_gla_chunk_bwd_dqkg_gamma(const void* q, const void* k, const
   return bwd_dqkg_impl(q, k, v, g_gamma, do_, h_ckpt, dh_work, dq, dk, dg, cu_seqlens,
                        chunk_offsets, chunk_map, total_chunks, B, T, H, K, V, N, dtype, scale,
                        kGateGammaK, stream);
+}
+
+// Interleaved checkpoints: one [total_chunks, H, K, V] buffer, h before the even global
+// chunks (tops_chunk_fwd_paired), dh after the odd ones (stage 1 below); stage 2 rebuilds the
+// other state of every chunk from its pair partner.
+static int check_paired(const char* who, int gate_mode, int dtype) {
+  char msg[160];
+  if (gate_mode < kGateK || gate_mode > kGateGammaK) {
+    snprintf(msg, sizeof(msg), "%s: gate_mode must be 0..3", who);
+    return tops_set_error(TOPS_ERR_SHAPE, msg);
+  }
+  if (dtype != TOPS_BF16) {
+    snprintf(msg, sizeof(msg), "%s: the interleaved layout takes TOPS_BF16", who);
+    return tops_set_error(TOPS_ERR_DTYPE, msg);
+  }
+  return TOPS_OK;
+}
+
+extern "C" int tops_chunk_bwd_dh_paired(const void* q, const void* k, const float* g,
+                                        int gate_mode, const void* do_, const float* dht,
+                                        float* ckpt, void* dv, float* dh0,
+                                        const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                                        int B, int T, int H, int K, int V, int N, int dtype,
+                                        float scale, void* stream) {
+  int rc = check_paired("chunk_bwd_dh_paired", gate_mode, dtype);
+  if (rc != TOPS_OK) return rc;
+  return bwd_dh_impl(q, k, g, do_, dht, ckpt, dv, dh0, cu_seqlens, chunk_offsets, B, T, H, K, V, N,
+                     dtype, scale, gate_mode, stream, 2);
+}
+
+extern "C" int tops_chunk_bwd_dqkg_paired(const void* q, const void* k, const void* v,
+                                          const float* g, int gate_mode, const void* do_,
+                                          const float* h0, const float* dht, const float* ckpt,
+                                          void* dq, void* dk, float* dg,
+                                          const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                                          const int32_t* chunk_map, int total_chunks, int B,
+                                          int T, int H, int K, int V, int N, int dtype,
+                                          float scale, void* stream) {
+  int rc = check_paired("chunk_bwd_dqkg_paired", gate_mode, dtype);
+  if (rc != TOPS_OK) return rc;
+  if (gate_mode == kGateGamma) dg = nullptr;
+  return bwd_dqkg_impl(q, k, v, g, do_, ckpt, ckpt, dq, dk, dg, cu_seqlens, chunk_offsets,
+                       chunk_map, total_chunks, B, T, H, K, V, N, dtype, scale, gate_mode, stream,
+                       h0, dht, 1);
 }

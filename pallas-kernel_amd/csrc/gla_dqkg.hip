@@ -23,6 +23,17 @@
 // result layout: the reverse token cumsum of dg is a 16-lane shuffle scan plus a
 // cross-wave block total.  LDS holds the v / dO planes, the pass's gated q~^T / k~^T
 // planes and its fp32 gate cumsum: < 70 KB, so two workgroups share a CU.
+//
+// PAIR (bf16 inputs, interleaved checkpoints): one workgroup of 8 waves takes the chunk
+// pair (2i, 2i + 1), four waves per chunk, each half with its own LDS.  The buffer holds
+// h_(2i) and dh_(2i+1) only; the missing states come from the partner's planes on MFMA,
+//     dh_(2i)  = 2^Gamma' dh_(2i+1) + scale 2^Gm' (q~'^T dO')      (' = chunk 2i + 1)
+//     h_(2i+1) = 2^Gamma h_(2i) + 2^(Gamma-Gm) (k~^T v)             (chunk 2i)
+// the updates of the two sweeps, with dO' / v read transposed from the row-major planes
+// (ds_read_b64_tr_b16).  That halves the checkpoint bytes written and read.  The results
+// are [V-tile][channel] accumulator tiles, so every state row a lane holds is the runs
+// v = 32vc + 4lg + 0..3 and 32vc + 16 + 4lg + 0..3: the contraction over v of the
+// inter-chunk products takes dO / v in the same order.
 #include <type_traits>
 
 #include "gla_sweep.h"
@@ -32,9 +43,10 @@ namespace tops {
 
 // GK: the per-channel gate mode only (kGateK: GLA and KDA), compiled without gate-mode
 // branches; !GK serves the per-token and constant gates chosen at run time.
-template <typename TIn, typename TV, int KP, int VP, bool GK>
-__global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
+template <typename TIn, typename TV, int KP, int VP, bool GK, bool PAIR>
+__global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParams p) {
   constexpr int C = kChunk;
+  constexpr int NG = PAIR ? 2 : 1;             // chunks per workgroup
   constexpr int KH = 32;                       // channels per pass
   constexpr int NPS = KP / KH;                 // passes
   constexpr int VC = VP / 32;
@@ -54,53 +66,82 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
   static_assert(NPT >= 1 && C * NPC % 256 == 0, "VP must be 32, 64 or 128");
   static_assert(NPTV >= 1 && C * NPCV % 256 == 0, "VP must be 32, 64 or 128");
   static_assert(KP % KH == 0, "KP must be 32, 64 or 128");
+  static_assert(!PAIR || (!SIN && !SINV), "the paired layout takes bf16 inputs");
   typedef Words<TIn> Wd;
 
-  __shared__ __attribute__((aligned(16))) uint16_t sV[NPLV * C * LV];
-  __shared__ __attribute__((aligned(16))) uint16_t sD[NPL * C * LV];
-  __shared__ __attribute__((aligned(16))) uint16_t sQT[2 * KH * LT];
-  __shared__ __attribute__((aligned(16))) uint16_t sKT[2 * KH * LT];
-  __shared__ __attribute__((aligned(16))) float sG[C * LG];     // gate cumsum of the pass
-  __shared__ __attribute__((aligned(16))) float sTot[8 * KH];
-  __shared__ __attribute__((aligned(16))) float sGm[KH];
-  __shared__ __attribute__((aligned(16))) float sGam[KH];
-  __shared__ __attribute__((aligned(16))) float sZk[2 * KH];
-  __shared__ __attribute__((aligned(16))) float sHdh[KH];
-  __shared__ __attribute__((aligned(16))) float sBlk[KH];
+  constexpr int ZV = NPLV * C * LV, ZD = NPL * C * LV, ZT = 2 * KH * LT;
+  __shared__ __attribute__((aligned(16))) uint16_t sV[NG * ZV];
+  __shared__ __attribute__((aligned(16))) uint16_t sD[NG * ZD];
+  __shared__ __attribute__((aligned(16))) uint16_t sQT[NG * ZT];
+  __shared__ __attribute__((aligned(16))) uint16_t sKT[NG * ZT];
+  __shared__ __attribute__((aligned(16))) float sG[NG * C * LG];     // gate cumsum of the pass
+  __shared__ __attribute__((aligned(16))) float sTot[NG * 8 * KH];
+  __shared__ __attribute__((aligned(16))) float sGm[NG * KH];
+  __shared__ __attribute__((aligned(16))) float sGam[NG * KH];
+  __shared__ __attribute__((aligned(16))) float sZk[NG * 2 * KH];
+  __shared__ __attribute__((aligned(16))) float sHdh[NG * KH];
+  __shared__ __attribute__((aligned(16))) float sBlk[NG * KH];
   // kGateS: per channel-block token sums (the fp32-v instantiation serves only kGateK, and
   // dropping this keeps it under 80 KB of LDS: two workgroups per CU)
   constexpr bool kScalarGate = std::is_same<TIn, TV>::value;
-  __shared__ __attribute__((aligned(16))) float sDgS[kScalarGate ? 2 * C : 1];
-
-  const Plane Pv{sV, SINV ? sV + C * LV : sV, LV};
-  const Plane Pd{sD, SIN ? sD + C * LV : sD, LV};
-  const Plane Pqt{sQT, sQT + KH * LT, LT};
-  const Plane Pkt{sKT, sKT + KH * LT, LT};
+  __shared__ __attribute__((aligned(16))) float sDgS[kScalarGate ? NG * 2 * C : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int kb = wave & 1, rh = wave >> 1;     // channel block of the pass, token half
+  // The chunk of the pair is a compile-time index (GRP), so that every LDS address of the
+  // body folds to an immediate offset; the two halves run the same barriers in the same order.
+  auto run = [&](auto grp_tag) {
+  constexpr int grp = decltype(grp_tag)::value;
+  const int tq = PAIR ? tid & 255 : tid;       // thread index within the chunk's four waves
+  const int kb = wave & 1, rh = (wave >> 1) & 1;   // channel block of the pass, token half
   const int l16 = lane & 15, lg = lane >> 4;
   const int hh = blockIdx.x % p.H;
-  const int gc = blockIdx.x / p.H;
+  const int gc = PAIR ? 2 * (blockIdx.x / p.H) + grp : blockIdx.x / p.H;
   const int H = p.H, K = p.K, V = p.V;
   const float scale = p.scale;
 
-  int n, c, L, row0;
-  if (p.cu_seqlens) {
-    n = p.chunk_map[gc];
-    c = gc - p.chunk_offsets[n];
-    row0 = p.cu_seqlens[n];
-    L = p.cu_seqlens[n + 1] - row0;
-  } else {
-    const int nt = cdiv(p.T, C);
-    n = gc / nt;
-    c = gc % nt;
-    row0 = n * p.T;
-    L = p.T;
+  // this chunk's LDS (the partner's, for PAIR, at index pg)
+  constexpr int pg = PAIR ? 1 - grp : 0;
+  const Plane Pv{sV + grp * ZV, SINV ? sV + grp * ZV + C * LV : sV + grp * ZV, LV};
+  const Plane Pd{sD + grp * ZD, SIN ? sD + grp * ZD + C * LV : sD + grp * ZD, LV};
+  const Plane Pqt{sQT + grp * ZT, sQT + grp * ZT + KH * LT, LT};
+  const Plane Pkt{sKT + grp * ZT, sKT + grp * ZT + KH * LT, LT};
+  float* const gG = sG + grp * C * LG;
+  float* const gTot = sTot + grp * 8 * KH;
+  float* const gGm = sGm + grp * KH;
+  float* const gGam = sGam + grp * KH;
+  float* const gZk = sZk + grp * 2 * KH;
+  float* const gHdh = sHdh + grp * KH;
+  float* const gBlk = sBlk + grp * KH;
+  float* const gDgS = sDgS + (kScalarGate ? grp * 2 * C : 0);
+
+  auto seq_of = [&](int x) { return p.cu_seqlens ? p.chunk_map[x] : x / cdiv(p.T, C); };
+  // PAIR: the second chunk of the last pair may not exist (odd total): its waves take part
+  // in the barriers with every access masked (nval = 0, empty state ranges)
+  const bool present = !PAIR || gc < p.total;
+  int n = 0, c = 0, L = 0, row0 = 0;
+  if (present) {
+    if (p.cu_seqlens) {
+      n = p.chunk_map[gc];
+      c = gc - p.chunk_offsets[n];
+      row0 = p.cu_seqlens[n];
+      L = p.cu_seqlens[n + 1] - row0;
+    } else {
+      const int nt = cdiv(p.T, C);
+      n = gc / nt;
+      c = gc % nt;
+      row0 = n * p.T;
+      L = p.T;
+    }
+  }
+  // both chunks of the pair in one sequence: each recomputes its missing state from the other
+  bool linked = false;
+  if constexpr (PAIR) {
+    const int c0 = 2 * (blockIdx.x / p.H);
+    linked = c0 + 1 < p.total && seq_of(c0) == seq_of(c0 + 1);
   }
   const int t0 = c * C;
-  const int nval = min(C, L - t0);
+  const int nval = present ? min(C, L - t0) : 0;
   const size_t e0 = (size_t)(row0 + t0) * H + hh;
   const long long nrows = (long long)p.B * p.T * H;     // (token, head) rows of [B,T,H,.]
   const uint32_t rowK = (uint32_t)(H * K), rowV = (uint32_t)(H * V);
@@ -117,17 +158,17 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
     uint4 pv[NPTV], pd[NPT];
 #pragma unroll
     for (int i = 0; i < NPTV; ++i) {
-      const int pc = tid + 256 * i, row = pc / NPCV, col = (pc % NPCV) * EPV;
+      const int pc = tq + 256 * i, row = pc / NPCV, col = (pc % NPCV) * EPV;
       pv[i] = bld128(Rv, (row < nval && col < V) ? ((uint32_t)row * rowV + col) * ESV : kOOB, 0);
     }
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
-      const int pc = tid + 256 * i, row = pc / NPC, col = (pc % NPC) * EP;
+      const int pc = tq + 256 * i, row = pc / NPC, col = (pc % NPC) * EP;
       pd[i] = bld128(Rd, (row < nval && col < V) ? ((uint32_t)row * rowV + col) * ES : kOOB, 0);
     }
 #pragma unroll
     for (int i = 0; i < NPTV; ++i) {
-      const int pc = tid + 256 * i, row = pc / NPCV, col = (pc % NPCV) * EPV;
+      const int pc = tq + 256 * i, row = pc / NPCV, col = (pc % NPCV) * EPV;
       if constexpr (!SINV) {
         *(uint4*)(Pv.hi + row * LV + col) = pv[i];
       } else {
@@ -138,7 +179,7 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
     }
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
-      const int pc = tid + 256 * i, row = pc / NPC, col = (pc % NPC) * EP;
+      const int pc = tq + 256 * i, row = pc / NPC, col = (pc % NPC) * EP;
       if constexpr (!SIN) {
         *(uint4*)(Pd.hi + row * LV + col) = pd[i];
       } else {
@@ -150,7 +191,7 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
   }
 
   // ---------------- staging of a pass: thread = (channel ch, 8-row segment sg)
-  const int ch = tid & 31, sg = tid >> 5;
+  const int ch = tq & 31, sg = tq >> 5;
   float rq[8], rk[8], rg[8];
   // gate element (row r, channel kc): per-channel [.., K], per-token [.., 1], or none (gamma)
   const bool gk_mode = GK || gmode == kGateK;
@@ -227,29 +268,62 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
     }
   }
 
-  const rsrc_t Rh = make_rsrc(p.hs + ((size_t)gc * H + hh) * K * V, (long long)K * V * 4);
-  const rsrc_t Rdh = make_rsrc(p.dhs + ((size_t)gc * H + hh) * K * V, (long long)K * V * 4);
+  // the state rows: h_c and dh_c, or for PAIR this chunk's checkpoint and the partner's
+  // (linked) or the sequence's h0 / dht (not linked; NULL reads as zero)
+  const long long KVB = (long long)K * V * 4;
+  auto slot = [&](const float* b, int x) { return b + ((size_t)x * H + hh) * K * V; };
+  rsrc_t Rh, Rdh;
+  if constexpr (PAIR) {
+    const float* other = nullptr;
+    if (linked) other = slot(p.hs, grp == 0 ? gc + 1 : gc - 1);
+    else if (present) {
+      const float* b = grp == 0 ? p.dht : p.h0;
+      other = b ? b + ((size_t)n * H + hh) * K * V : nullptr;
+    }
+    const rsrc_t Ro = make_rsrc(present ? slot(p.hs, gc) : nullptr, present ? KVB : 0);
+    const rsrc_t Rx = make_rsrc(other, other ? KVB : 0);
+    Rh = grp == 0 ? Ro : Rx;
+    Rdh = grp == 0 ? Rx : Ro;
+  } else {
+    Rh = make_rsrc(slot(p.hs, gc), KVB);
+    Rdh = make_rsrc(slot(p.dhs, gc), KVB);
+  }
   const rsrc_t Rdq = make_rsrc_rows((const TIn*)p.dq, e0, nrows, K);
   const rsrc_t Rdk = make_rsrc_rows((const TIn*)p.dk, e0, nrows, K);
   const rsrc_t Rdka = make_rsrc_rows(p.dk_add, e0, nrows, K);
   const rsrc_t Rdga = make_rsrc_rows(p.dg_add, e0, nrows, K);
   const rsrc_t Rdg = make_rsrc_rows(gmode == kGateGamma ? nullptr : p.dg, e0, nrows, gmode == kGateS ? 1 : K);
-  if (kScalarGate && tid < 2 * C) sDgS[tid] = 0.f;
+  if (kScalarGate && tq < 2 * C) gDgS[tq] = 0.f;
+
+  // ---- the h / dh rows of a pass: a lane's 8 values of state row kk = 32 ps + 16 kb + l16,
+  // v = v0 .. v0 + 7, or (PAIR) the runs v0 .. v0 + 3 and v0 + 16 .. v0 + 19 of the
+  // accumulator-tile order.  h is requested at the start of the pass, so that its latency
+  // overlaps the staging, dh just before the planes barrier.
+  const int kl = 16 * kb + l16;            // channel of this lane's A-operand row (in pass)
+  uint4 hraw[VC][2], draw[VC][2];
+  auto load_state = [&](const rsrc_t& R, uint4 (&raw)[VC][2], int ps) {
+    const int kk = ps * KH + kl;
+    auto vrun = [&](int vc, int j) {
+      const int v0 = PAIR ? 32 * vc + 16 * j + 4 * lg : 32 * vc + 8 * lg;
+      return (kk < K && v0 < V) ? ((uint32_t)kk * V + v0) * 4u : kOOB;
+    };
+#pragma unroll
+    for (int vc = 0; vc < VC; ++vc) {
+      if constexpr (PAIR) {
+        raw[vc][0] = bld128(R, vrun(vc, 0), 0);
+        raw[vc][1] = bld128(R, vrun(vc, 1), 0);
+      } else {
+        const uint32_t o = vrun(vc, 0);
+        raw[vc][0] = bld128(R, o, 0);
+        raw[vc][1] = bld128(R, o, 16);
+      }
+    }
+  };
 
 #pragma unroll 1
   for (int ps = 0; ps < NPS; ++ps) {
     const int cb = ps * KH;
-    // ---- this pass's h rows, issued before the staging so their latency overlaps it
-    const int kl = 16 * kb + l16;          // channel of this lane's A-operand row (in pass)
-    const int kk = cb + kl;
-    uint4 hraw[VC][2], draw[VC][2];
-#pragma unroll
-    for (int vc = 0; vc < VC; ++vc) {
-      const int v0 = 32 * vc + 8 * lg;
-      const uint32_t o = (kk < K && v0 < V) ? ((uint32_t)kk * V + v0) * 4u : kOOB;
-      hraw[vc][0] = bld128(Rh, o, 0);
-      hraw[vc][1] = bld128(Rh, o, 16);
-    }
+    load_state(Rh, hraw, ps);
     // ---- the pass's WY parts of dk / dg (fp32-v instantiation only, the one the KDA
     // backward uses): requested now, added in the epilogue
     constexpr bool kEarlyAdd = !kScalarGate;
@@ -281,46 +355,85 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
     }
     // (no barrier before this write: sTot is last read before the previous pass's planes
     // barrier, and everything read after its final barrier is rewritten only after the next one)
-    sTot[sg * KH + ch] = G[7];
+    gTot[sg * KH + ch] = G[7];
     __syncthreads();
     float pre = 0.f, gam = 0.f;
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      const float t = sTot[s * KH + ch];
+      const float t = gTot[s * KH + ch];
       if (s < sg) pre += t;
       gam += t;
     }
     const float gmv = 0.5f * gam;
     if (sg == 0) {
-      sGm[ch] = gmv;
-      sGam[ch] = gam;
+      gGm[ch] = gmv;
+      gGam[ch] = gam;
     }
     {
       float qt[8], kt[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         G[i] += pre;
-        sG[(8 * sg + i) * LG + ch] = G[i];
+        gG[(8 * sg + i) * LG + ch] = G[i];
         qt[i] = rq[i] * fast_exp2(G[i] - gmv);
         kt[i] = rk[i] * fast_exp2(gmv - G[i]);
       }
       put_n<true, 8>(Pqt, ch, 8 * sg, qt);
       put_n<true, 8>(Pkt, ch, 8 * sg, kt);
     }
-    if (ps + 1 < NPS) load_pass(ps + 1);
+    // the next pass's q / k / g rows (PAIR: after the state rebuild, which needs the registers)
+    if (!PAIR && ps + 1 < NPS) load_pass(ps + 1);
     // this pass's dh rows, in flight across the barrier
-#pragma unroll
-    for (int vc = 0; vc < VC; ++vc) {
-      const int v0 = 32 * vc + 8 * lg;
-      const uint32_t o = (kk < K && v0 < V) ? ((uint32_t)kk * V + v0) * 4u : kOOB;
-      draw[vc][0] = bld128(Rdh, o, 0);
-      draw[vc][1] = bld128(Rdh, o, 16);
-    }
+    load_state(Rdh, draw, ps);
     __syncthreads();  // planes, sG, sGm, sGam visible
 
+    // ---- PAIR: the missing state from the partner chunk (see the header), accumulated onto
+    // the partner-side state it starts from (scaled by 2^Gamma' / f, then the sum by f)
+    if constexpr (PAIR) {
+      auto rebuild = [&](uint4 (&xr)[VC][2], const uint16_t* zplane, const uint16_t* yplane,
+                         float pre_s, float post_s) {
+        const Plane Pz{(uint16_t*)zplane, (uint16_t*)zplane + KH * LT, LT};
+        f32x4 acc[2 * VC];
+#pragma unroll
+        for (int vc = 0; vc < VC; ++vc)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) acc[2 * vc + j] = __builtin_bit_cast(f32x4, xr[vc][j]) * pre_s;
+        bf16x8 bh[2], bl[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          bh[ks] = Pz.hi8(kl, 32 * ks + 8 * lg);
+          bl[ks] = Pz.lo8(kl, 32 * ks + 8 * lg);
+        }
+#pragma unroll
+        for (int t = 0; t < 2 * VC; ++t) {
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            const bf16x8 a = tr_read8(yplane, LV, 32 * ks, 16 * t, lane);
+            acc[t] = mma<false, true>(acc[t], a, a, bh[ks], bl[ks]);
+          }
+        }
+#pragma unroll
+        for (int vc = 0; vc < VC; ++vc)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) xr[vc][j] = __builtin_bit_cast(uint4, acc[2 * vc + j] * post_s);
+      };
+      if (linked) {
+        const float pgam = sGam[pg * KH + kl], pgm = sGm[pg * KH + kl];
+        if (grp == 0) {
+          // dh_c = 2^Gamma' dh' + scale 2^Gm' (q~'^T dO')
+          rebuild(draw, sQT + pg * ZT, sD + pg * ZD, fast_exp2(pgam - pgm) / scale,
+                  scale * fast_exp2(pgm));
+        } else {
+          // h_c = 2^Gamma h'' + 2^(Gamma-Gm) (k~''^T v'')   (Gamma - Gm = Gm)
+          rebuild(hraw, sKT + pg * ZT, sV + pg * ZV, fast_exp2(pgm), fast_exp2(pgam - pgm));
+        }
+      }
+      if (ps + 1 < NPS) load_pass(ps + 1);
+    }
+
     // ---- inter-chunk: X^T += (alpha h) dO^T, W^T += (beta dh) v^T
-    const float al = scale * fast_exp2(sGm[kl]);
-    const float be = fast_exp2(sGam[kl] - sGm[kl]);
+    const float al = scale * fast_exp2(gGm[kl]);
+    const float be = fast_exp2(gGam[kl] - gGm[kl]);
     f32x4 X[2], Wt[2];
     X[0] = X[1] = Wt[0] = Wt[1] = f32x4{0.f, 0.f, 0.f, 0.f};
     float hd = 0.f;
@@ -349,8 +462,9 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
         const int B2 = 2 * rh + a;
-        const bf16x8 doh = Pd.hi8(16 * B2 + l16, v0);
-        const bf16x8 vh = Pv.hi8(16 * B2 + l16, v0);
+        const int tr = 16 * B2 + l16;
+        const bf16x8 doh = PAIR ? Pd.hi44(tr, 32 * vc + 4 * lg, 32 * vc + 16 + 4 * lg) : Pd.hi8(tr, v0);
+        const bf16x8 vh = PAIR ? Pv.hi44(tr, 32 * vc + 4 * lg, 32 * vc + 16 + 4 * lg) : Pv.hi8(tr, v0);
         bf16x8 dol = doh, vl = vh;
         if constexpr (SIN) dol = Pd.lo8(16 * B2 + l16, v0);
         if constexpr (SINV) vl = Pv.lo8(16 * B2 + l16, v0);
@@ -378,12 +492,12 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
       }
       if (l16 == 0) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sZk[rh * KH + 16 * kb + 4 * lg + r] = z[r];
+        for (int r = 0; r < 4; ++r) gZk[rh * KH + 16 * kb + 4 * lg + r] = z[r];
       }
       if (rh == 0) {
         hd += __shfl_xor(hd, 16, 64);
         hd += __shfl_xor(hd, 32, 64);
-        if (lg == 0) sHdh[kl] = hd;
+        if (lg == 0) gHdh[kl] = hd;
       }
     }
     // ---- intra-chunk: X^T += k~^T dA^T, W^T += q~^T dA
@@ -410,7 +524,7 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
     const int cl = 16 * kb + 4 * lg;       // first channel of the lane (in pass)
     const int kc = cb + cl;
     const bool chok = kc < K;
-    const float4 gm4 = *(const float4*)(sGm + cl);
+    const float4 gm4 = *(const float4*)(gGm + cl);
     const float gmr[4] = {gm4.x, gm4.y, gm4.z, gm4.w};
     float dgr[2][4];
 #pragma unroll
@@ -418,7 +532,7 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
       const int tok = 16 * (2 * rh + a) + l16;
       const bool ok = chok && tok < nval;
       const uint32_t off = (uint32_t)tok * rowK + kc;
-      const float4 g4 = *(const float4*)(sG + tok * LG + cl);
+      const float4 g4 = *(const float4*)(gG + tok * LG + cl);
       const float gr[4] = {g4.x, g4.y, g4.z, g4.w};
       // fp32 inputs re-read q, k (exact); bf16 inputs use q dq - k dk = q~ X - k~ W with
       // q~ / k~ read back from the pass planes (hi + lo: 2^-17 relative, far below bf16)
@@ -467,14 +581,14 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
     for (int r = 0; r < 4; ++r) dgr[0][r] += __shfl(dgr[1][r], lane & 48, 64);
     if (rh == 1 && l16 == 0) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sBlk[cl + r] = dgr[0][r];   // total of tokens 32..63
+      for (int r = 0; r < 4; ++r) gBlk[cl + r] = dgr[0][r];   // total of tokens 32..63
     }
     __syncthreads();  // sZk, sHdh, sBlk visible
     float add[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      add[r] = fast_exp2(sGam[cl + r]) * sHdh[cl + r] + sZk[cl + r] + sZk[KH + cl + r];
-      if (rh == 0) add[r] += sBlk[cl + r];
+      add[r] = fast_exp2(gGam[cl + r]) * gHdh[cl + r] + gZk[cl + r] + gZk[KH + cl + r];
+      if (rh == 0) add[r] += gBlk[cl + r];
     }
     if (GK || gmode == kGateK || (gmode == kGateGammaK && p.dg)) {
 #pragma unroll
@@ -500,16 +614,23 @@ __global__ __launch_bounds__(256, 2) void gla_dqkg_kernel(DqkgParams p) {
         }
         x += __shfl_xor(x, 16, 64);
         x += __shfl_xor(x, 32, 64);
-        if (lg == 0) sDgS[kb * C + 16 * (2 * rh + a) + l16] += x;
+        if (lg == 0) gDgS[kb * C + 16 * (2 * rh + a) + l16] += x;
       }
     }
   }
   if (kScalarGate && gmode == kGateS && p.dg) {
     __syncthreads();
-    if (tid < C) {
-      const float x = sDgS[tid] + sDgS[C + tid];
-      bst32(Rdg, __float_as_uint(x), tid < nval ? (uint32_t)tid * H * 4u : kOOB, 0);
+    if (tq < C) {
+      const float x = gDgS[tq] + gDgS[C + tq];
+      bst32(Rdg, __float_as_uint(x), tq < nval ? (uint32_t)tq * H * 4u : kOOB, 0);
     }
+  }
+  };
+  if constexpr (PAIR) {
+    if (wave >> 2) run(std::integral_constant<int, 1>{});
+    else run(std::integral_constant<int, 0>{});
+  } else {
+    run(std::integral_constant<int, 0>{});
   }
 }
 
@@ -520,12 +641,22 @@ hipError_t launch_gla_dqkg(const DqkgParams& p, hipStream_t s) {
   dim3 grid(p.total * p.H), block(256);
   // the fp32-v instantiation (the KDA backward) serves only the per-channel gate
   constexpr bool kAllModes = std::is_same<TIn, TV>::value;
+  constexpr bool kPairs = kAllModes && std::is_same<TIn, uint16_t>::value;
   const bool gk = !kAllModes || p.gate_mode == kGateK;
+  if (p.paired && !kPairs) return hipErrorInvalidValue;
+  const dim3 pgrid(((p.total + 1) / 2) * p.H), pblock(512);
 #define TOPS_DQKG(KPV, VPV)                                                                   \
   if (kp == KPV && vp == VPV) {                                                               \
-    if (gk) hipLaunchKernelGGL((gla_dqkg_kernel<TIn, TV, KPV, VPV, true>), grid, block, 0, s, p); \
+    if constexpr (kPairs) {                                                                   \
+      if (p.paired) {                                                                         \
+        if (gk) hipLaunchKernelGGL((gla_dqkg_kernel<TIn, TV, KPV, VPV, true, true>), pgrid, pblock, 0, s, p); \
+        else hipLaunchKernelGGL((gla_dqkg_kernel<TIn, TV, KPV, VPV, false, true>), pgrid, pblock, 0, s, p); \
+        return hipGetLastError();                                                             \
+      }                                                                                       \
+    }                                                                                         \
+    if (gk) hipLaunchKernelGGL((gla_dqkg_kernel<TIn, TV, KPV, VPV, true, false>), grid, block, 0, s, p); \
     else if constexpr (kAllModes)                                                             \
-      hipLaunchKernelGGL((gla_dqkg_kernel<TIn, TV, KPV, VPV, false>), grid, block, 0, s, p);  \
+      hipLaunchKernelGGL((gla_dqkg_kernel<TIn, TV, KPV, VPV, false, false>), grid, block, 0, s, p); \
     return hipGetLastError();                                                                 \
   }
   TOPS_DQKG(32, 32) TOPS_DQKG(32, 64) TOPS_DQKG(32, 128)

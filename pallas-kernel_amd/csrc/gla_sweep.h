@@ -35,6 +35,9 @@ struct SweepParams {
   float* dec_fin;        // [N,H,K] sum of the log2 gates over the sequence, or NULL
   const int* seg_end;    // [N] end row of sequence n (its start is cu_seqlens[n]), or NULL:
                          // sequence n then ends where n + 1 starts
+  // checkpoints written: 0 = every chunk, 1 = even global chunks only, 2 = odd only (the
+  // interleaved layout: h before the even chunks, dh after the odd ones, in one buffer)
+  int ckpt_par;
 };
 
 // TIn = uint16_t (bf16 bits) or float; REV = reverse (state-gradient) sweep;
@@ -67,6 +70,13 @@ struct DqkgParams {
   // optional fp32 terms added to dk and dg ([B,T,H,K]; the KDA WY part), or NULL
   const float* dk_add;
   const float* dg_add;
+  // interleaved checkpoints (bf16 inputs): hs = dhs = one [total, H, K, V] buffer holding h
+  // before every even global chunk and dh after every odd one; a workgroup takes a chunk
+  // pair and recomputes the missing state of each chunk from its partner's.  h0 / dht
+  // [N, H, K, V] (or NULL: zero) stand in where the partner is in another sequence.
+  int paired;
+  const float* h0;
+  const float* dht;
 };
 
 // TV = type of v (the KDA backward passes fp32 v_new with bf16 q / k / dO)

@@ -34,7 +34,8 @@
 // transposed per chunk for the WY backward.
 //
 // Every workgroup also writes S at the start of each chunk to `ckpt` when given (the
-// forward's state checkpoints, or the reverse sweep's dh per chunk).
+// forward's state checkpoints, or the reverse sweep's dh per chunk), or, in the
+// interleaved layout, at the start of every even (forward) or odd (reverse) global chunk.
 //
 // Pipelining: the raw q/k/g/Y of chunk c+1 are loaded into registers while chunk c is
 // computed; a full chunk takes a branch-free path (masked rows read out of range and are
@@ -193,6 +194,10 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       S[i][r] = x;
     }
   }
+  // Drain these loads here: a load still in flight when the chunk loop starts makes the
+  // compiler's wait before the first use of S inside the loop a full vmcnt(0) on every
+  // iteration, which also waits for the previous chunk's output and checkpoint stores.
+  __builtin_amdgcn_s_waitcnt(0);
 
   // ---- raw chunk registers (prefetch targets): PF sets, the chunk PF steps ahead is
   // loaded into the set just consumed.  One set is issued a whole chunk ahead (after B2),
@@ -353,13 +358,11 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       sbe[r] = REV ? scale * fast_exp2(g2) : fast_exp2(sgam[r] - g2);
     }
 
-    // ---------------- state -> H^T plane (alpha S); checkpoint of S
+    // ---------------- state -> H^T plane (alpha S)
     if constexpr (ST) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) dsum[r] += sgam[r];
     } else {
-      const rsrc_t Rck = make_rsrc(p.ckpt ? p.ckpt + ((size_t)(cbase + c) * H + hh) * K * V : nullptr,
-                                   p.ckpt ? (long long)K * V * 4 : 0);
 #pragma unroll
       for (int i = 0; i < NHT; ++i) {
         const int nn = (wave * NHT + i) % (BV / 16);
@@ -368,7 +371,20 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) x[r] = sal[r] * S[i][r];
         put_n<true, 4>(PHt, 16 * nn + l16, kr, x);
-        if (p.ckpt) {
+      }
+    }
+    // checkpoint of S (the state at the start of the chunk).  Issued here, ahead of the
+    // staging: stored after the next chunk's prefetch instead, the checkpoints measured
+    // slower (the memory counter retires in issue order, so the waits for the prefetched
+    // loads at the top of the next chunk then also cover the stores).
+    if constexpr (!ST) {
+      if (p.ckpt && (p.ckpt_par == 0 || ((cbase + c) & 1) == p.ckpt_par - 1)) {
+        const rsrc_t Rck = make_rsrc(p.ckpt + ((size_t)(cbase + c) * H + hh) * K * V,
+                                     (long long)K * V * 4);
+#pragma unroll
+        for (int i = 0; i < NHT; ++i) {
+          const int nn = (wave * NHT + i) % (BV / 16);
+          const int kr = 16 * msb + 4 * lg;
           const int vv = vt * BV + 16 * nn + l16;
           const uint32_t vo = (vv < V) ? ((uint32_t)kr * V + vv) * 4u : kOOB;
 #pragma unroll
@@ -377,7 +393,6 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
         }
       }
     }
-
     // ---------------- gated operands for the staging rows.  Z~ is split into bf16 hi / lo once;
     // the transposed plane reuses those halves, regrouped per channel with byte permutes.
     {
@@ -874,7 +889,7 @@ static int chunk_fwd_impl(const void* q, const void* k, const void* v, const flo
                           const float* h0, void* o, float* ht, float* h_ckpt,
                           const int32_t* cu_seqlens, const int32_t* chunk_offsets, int B, int T,
                           int H, int K, int V, int N, int dtype, float scale, int gate_mode,
-                          void* stream) {
+                          void* stream, int ckpt_par = 0) {
   if (!q || !k || !v || !g || !o) return tops_set_error(TOPS_ERR_NULL, "gla_chunk_fwd: null tensor");
   if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || N <= 0)
     return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd: non-positive dimension");
@@ -888,6 +903,7 @@ static int chunk_fwd_impl(const void* q, const void* k, const void* v, const flo
     return tops_set_error(TOPS_ERR_NULL, "gla_chunk_fwd: varlen checkpoints need chunk_offsets");
   SweepParams p{q, k, g, v, h0, o, ht, h_ckpt, cu_seqlens, chunk_offsets,
                 B, T, H, K, V, N, (V + 63) / 64, scale, gate_mode};
+  p.ckpt_par = ckpt_par;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
   if (dtype == TOPS_BF16) e = launch_gla_sweep<uint16_t, false>(p, s);
@@ -926,4 +942,18 @@ extern "C" int tops_gla_chunk_fwd_gamma(const void* q, const void* k, const void
   if (!g_gamma) return tops_set_error(TOPS_ERR_NULL, "gla_chunk_fwd_gamma: null g_gamma");
   return chunk_fwd_impl(q, k, v, g_gamma, h0, o, ht, h_ckpt, cu_seqlens, chunk_offsets, B, T, H, K,
                         V, N, dtype, scale, kGateGammaK, stream);
+}
+
+extern "C" int tops_chunk_fwd_paired(const void* q, const void* k, const void* v, const float* g,
+                                     int gate_mode, const float* h0, void* o, float* ht,
+                                     float* ckpt, const int32_t* cu_seqlens,
+                                     const int32_t* chunk_offsets, int B, int T, int H, int K,
+                                     int V, int N, int dtype, float scale, void* stream) {
+  if (gate_mode < kGateK || gate_mode > kGateGammaK)
+    return tops_set_error(TOPS_ERR_SHAPE, "chunk_fwd_paired: gate_mode must be 0..3");
+  if (dtype != TOPS_BF16)
+    return tops_set_error(TOPS_ERR_DTYPE, "chunk_fwd_paired: the interleaved layout takes TOPS_BF16");
+  if (!ckpt) return tops_set_error(TOPS_ERR_NULL, "chunk_fwd_paired: null ckpt");
+  return chunk_fwd_impl(q, k, v, g, h0, o, ht, ckpt, cu_seqlens, chunk_offsets, B, T, H, K, V, N,
+                        dtype, scale, gate_mode, stream, 1);
 }

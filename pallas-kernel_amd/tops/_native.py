@@ -45,6 +45,9 @@ SIGNATURES = {
     "tops_kda_chunk_fwd_noalloc": [_vp] * 11 + [_i32] * 8 + [_f32, _vp],
     "tops_simple_gla_chunk_bwd_dh": [_vp] * 11 + [_i32] * 7 + [_f32, _vp],
     "tops_simple_gla_chunk_bwd_dqkg": [_vp] * 14 + [_i32] * 8 + [_f32, _vp],
+    "tops_chunk_fwd_paired": [_vp] * 4 + [_i32] + [_vp] * 6 + [_i32] * 7 + [_f32, _vp],
+    "tops_chunk_bwd_dh_paired": [_vp] * 3 + [_i32] + [_vp] * 7 + [_i32] * 7 + [_f32, _vp],
+    "tops_chunk_bwd_dqkg_paired": [_vp] * 4 + [_i32] + [_vp] * 10 + [_i32] * 8 + [_f32, _vp],
     "tops_chunk_state_pass": [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp] + [_i32] * 6 + [_f32, _i32, _vp],
     "tops_chunk_state_combine": [_vp] * 7 + [_i32] * 5 + [_vp],
     "tops_kda_gate_fwd": [_vp, _i32, _vp, _vp, _vp] + [_i32] * 6 + [_f32, _vp],

@@ -5,7 +5,7 @@ from __future__ import annotations
 import torch
 
 from .. import _native as N
-from ..utils import ChunkPlan
+from ..utils import ChunkPlan, checkpoint_layout
 
 GATE_K, GATE_S, GATE_GAMMA, GATE_GAMMA_K = "k", "s", "gamma", "gamma_k"
 
@@ -75,9 +75,23 @@ def _segment_states(z, y, gate, s_in, scale, sp, reverse: bool):
     return init
 
 
-def _fwd_tile(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, keep_states: bool):
+def paired_states(q, K: int, V: int) -> bool:
+    """Whether chunk_fwd(keep_states=PAIRED) keeps the interleaved checkpoints: one
+    [chunks, H, K, V] buffer with the state before every even global chunk, into which the
+    backward's reverse sweep writes dh after every odd one; the dq / dk / dg kernel rebuilds
+    each chunk's other state from its pair partner.  Only with
+    tops.utils.set_checkpoint_layout("paired"), bf16 inputs and K, V <= 128."""
+    return (checkpoint_layout() == "paired" and q.dtype == torch.bfloat16
+            and _direct(q, K, V, True))
+
+
+PAIRED = "paired"
+
+
+def _fwd_tile(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, keep_states):
     """Run the forward chunk sweep on one tile (K <= 128).  gate = (mode, fp32 tensor).  Returns (o, ht, h_ckpt).
-    Long or few sequences sweep as concurrent segments (plan.segments)."""
+    Long or few sequences sweep as concurrent segments (plan.segments).  keep_states: False,
+    True (every chunk's state) or PAIRED (the interleaved layout, bf16 only)."""
     B, T, H, K = q.shape
     V = v.shape[-1]
     mode, gt = gate
@@ -96,7 +110,10 @@ def _fwd_tile(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, kee
         cu, offs, Bx, Tx, Nx = sp.cu_dev, sp.offsets_dev, 1, B * T, sp.Nv
     tail = (N.ptr(s0), N.ptr(o), N.ptr(fin), N.ptr(hs), N.ptr(cu), N.ptr(offs),
             Bx, Tx, H, K, V, Nx, N.dtype_code(q.dtype), float(scale), N.stream())
-    if mode == GATE_K:
+    if keep_states == PAIRED:
+        N.call("tops_chunk_fwd_paired", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gt),
+               _GATE_CODE[mode], *tail)
+    elif mode == GATE_K:
         N.call("tops_gla_chunk_fwd", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gt), *tail)
     elif mode == GATE_GAMMA_K:
         N.call("tops_gla_chunk_fwd_gamma", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gt), *tail)
@@ -110,11 +127,12 @@ def _fwd_tile(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, kee
 
 
 def _bwd_tile(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool,
-              want_dg: bool = True):
+              want_dg: bool = True, h0=None, paired: bool = False):
     """Run the backward (reverse sweep + chunk-parallel dq/dk/dg) on one tile (K, V <= 128).
     Returns (dq, dk, dv, dg, dh0); dg is [B,T,H,K] for GATE_K (and for GATE_GAMMA_K when
     want_dg: the gradient of the per-token gate the constant stands for), [B,T,H] for GATE_S
-    and None for GATE_GAMMA."""
+    and None for GATE_GAMMA.  paired: hs is the interleaved buffer of chunk_fwd(PAIRED) (the
+    reverse sweep fills in its odd chunks; h0 is then the forward's initial state)."""
     B, T, H, K = q.shape
     V = v.shape[-1]
     if V > 128:
@@ -128,7 +146,7 @@ def _bwd_tile(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool
         dg = torch.empty(B, T, H, K, device=q.device, dtype=torch.float32)
     elif mode == GATE_S:
         dg = torch.empty(B, T, H, device=q.device, dtype=torch.float32)
-    dh_work = torch.empty_like(hs)
+    dh_work = hs if paired else torch.empty_like(hs)
     dt, st = N.dtype_code(q.dtype), N.stream()
     sp = plan.segments(H, V)
     if sp is None:
@@ -145,7 +163,13 @@ def _bwd_tile(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool
     dqkg_tail = (N.ptr(do), N.ptr(hs), N.ptr(dh_work), N.ptr(dq), N.ptr(dk), N.ptr(dg),
                  N.ptr(plan.cu_dev), N.ptr(plan.offsets_dev), N.ptr(plan.chunk_map_dev),
                  plan.total, B, T, H, K, V, plan.N, dt, float(scale), st)
-    if mode == GATE_K:
+    if paired:
+        code = _GATE_CODE[mode]
+        N.call("tops_chunk_bwd_dh_paired", N.ptr(q), N.ptr(k), N.ptr(gt), code, *dh_args)
+        N.call("tops_chunk_bwd_dqkg_paired", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gt), code,
+               N.ptr(do), N.ptr(h0), N.ptr(dht), N.ptr(hs), N.ptr(dq), N.ptr(dk), N.ptr(dg),
+               *dqkg_tail[6:])
+    elif mode == GATE_K:
         N.call("tops_gla_chunk_bwd_dh", N.ptr(q), N.ptr(k), N.ptr(gt), *dh_args)
         N.call("tops_gla_chunk_bwd_dqkg", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gt), *dqkg_tail)
     elif mode == GATE_GAMMA_K:
@@ -174,8 +198,9 @@ def _k_gate(gate, ks):
     return (mode, gt[..., ks].contiguous()) if mode in (GATE_K, GATE_GAMMA_K) else gate
 
 
-def chunk_fwd(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, keep_states: bool):
-    """Forward of GLA / simple GLA.  Returns (o, ht, h_ckpt).
+def chunk_fwd(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, keep_states):
+    """Forward of GLA / simple GLA.  Returns (o, ht, h_ckpt).  keep_states: False, True or
+    PAIRED (the interleaved checkpoints where paired_states() holds, else every chunk's).
 
     K > 128 (and V > 128 when states are kept for the backward) runs as equal slices: the
     recurrence is separate per state entry, so the output is the sum of the K slices'
@@ -184,7 +209,9 @@ def chunk_fwd(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, kee
     as [slices, chunks, H, K/nK, V/nV]."""
     B, T, H, K = q.shape
     V = v.shape[-1]
-    if _direct(q, K, V, keep_states):
+    if keep_states == PAIRED and not paired_states(q, K, V):
+        keep_states = True
+    if _direct(q, K, V, bool(keep_states)):
         return _fwd_tile(q, k, v, gate, h0, scale, output_final_state, plan, keep_states)
     nk, Kp, nv, Vp = tiling(K, V, keep_states)
     f32 = torch.float32
@@ -210,7 +237,7 @@ def chunk_fwd(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, kee
 
 
 def chunk_bwd(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool,
-              want_dg: bool = True):
+              want_dg: bool = True, h0=None, paired: bool = False):
     """Backward of GLA / simple GLA.  Returns (dq, dk, dv, dg, dh0); dg is [B,T,H,K] for
     GATE_K, [B,T,H] for GATE_S and None for GATE_GAMMA.  Sliced as chunk_fwd: dq, dk and a
     per-channel dg are the sums over the V slices, dv (and a scalar-gate dg) the sums over
@@ -218,7 +245,7 @@ def chunk_bwd(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool
     B, T, H, K = q.shape
     V = v.shape[-1]
     if _direct(q, K, V, True) and hs.dim() == 4:
-        return _bwd_tile(q, k, v, gate, do, dht, hs, scale, plan, want_dh0, want_dg)
+        return _bwd_tile(q, k, v, gate, do, dht, hs, scale, plan, want_dh0, want_dg, h0, paired)
     nk, Kp, nv, Vp = tiling(K, V, True)
     f32 = torch.float32
     qf, kf, vf, dof = (x.to(f32) for x in (q, k, v, do))

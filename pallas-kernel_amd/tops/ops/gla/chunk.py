@@ -23,7 +23,7 @@ from __future__ import annotations
 import torch
 
 from ...utils import ChunkPlan, cdiv
-from .._chunk_core import (GATE_K, GATE_GAMMA_K, check_qkv, chunk_fwd as _core_fwd,
+from .._chunk_core import (GATE_K, GATE_GAMMA_K, PAIRED, check_qkv, paired_states, chunk_fwd as _core_fwd,
                            chunk_bwd as _core_bwd, states_for_bwd, states_full)
 
 
@@ -58,9 +58,10 @@ class _ChunkGLA(torch.autograd.Function):
         plan = ChunkPlan.get(q.shape[0], q.shape[1], cu_seqlens, q.device)
         train = any(ctx.needs_input_grad[:5])
         o, ht, hs = _core_fwd(q, k, v, (mode, g32), h032, scale, output_final_state, plan,
-                              keep_states=train)
+                              keep_states=PAIRED if train else False)
         if train:
-            ctx.save_for_backward(q, k, v, g32, hs)
+            ctx.save_for_backward(q, k, v, g32, hs, h032)
+            ctx.paired = paired_states(q, q.shape[-1], v.shape[-1])
             ctx.plan, ctx.scale, ctx.mode = plan, scale, mode
             ctx.g_dtype = gt.dtype
             ctx.h0_info = None if h0 is None else h0.dtype
@@ -68,13 +69,13 @@ class _ChunkGLA(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, do, dht):
-        q, k, v, g32, hs = ctx.saved_tensors
+        q, k, v, g32, hs, h032 = ctx.saved_tensors
         do = do.contiguous().to(q.dtype)
         dht = None if dht is None else dht.contiguous().to(torch.float32)
         want_dh0 = ctx.h0_info is not None
         want_dg = bool(ctx.needs_input_grad[3])
         dq, dk, dv, dg, dh0 = _core_bwd(q, k, v, (ctx.mode, g32), do, dht, hs, ctx.scale,
-                                        ctx.plan, want_dh0, want_dg)
+                                        ctx.plan, want_dh0, want_dg, h0=h032, paired=ctx.paired)
         if dh0 is not None:
             dh0 = dh0.to(ctx.h0_info)
         if dg is not None:

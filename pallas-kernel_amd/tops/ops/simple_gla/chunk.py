@@ -21,8 +21,8 @@ from __future__ import annotations
 import torch
 
 from ...utils import ChunkPlan
-from .._chunk_core import (GATE_S, GATE_GAMMA, check_qkv, chunk_fwd as _core_fwd,
-                           chunk_bwd as _core_bwd)
+from .._chunk_core import (GATE_S, GATE_GAMMA, PAIRED, check_qkv, chunk_fwd as _core_fwd,
+                           chunk_bwd as _core_bwd, paired_states)
 
 
 def _gate(q, g, g_gamma):
@@ -49,9 +49,10 @@ class _ChunkSimpleGLA(torch.autograd.Function):
         plan = ChunkPlan.get(q.shape[0], q.shape[1], cu_seqlens, q.device)
         train = any(ctx.needs_input_grad[:5])
         o, ht, hs = _core_fwd(q, k, v, (mode, g32), h032, scale, output_final_state, plan,
-                              keep_states=train)
+                              keep_states=PAIRED if train else False)
         if train:
-            ctx.save_for_backward(q, k, v, g32, hs)
+            ctx.save_for_backward(q, k, v, g32, hs, h032)
+            ctx.paired = paired_states(q, q.shape[-1], v.shape[-1])
             ctx.plan, ctx.scale, ctx.mode = plan, scale, mode
             ctx.g_info = (gt.dtype, gt.shape)
             ctx.h0_info = None if h0 is None else h0.dtype
@@ -59,11 +60,12 @@ class _ChunkSimpleGLA(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, do, dht):
-        q, k, v, g32, hs = ctx.saved_tensors
+        q, k, v, g32, hs, h032 = ctx.saved_tensors
         do = do.contiguous().to(q.dtype)
         dht = None if dht is None else dht.contiguous().to(torch.float32)
         dq, dk, dv, dg, dh0 = _core_bwd(q, k, v, (ctx.mode, g32), do, dht, hs, ctx.scale,
-                                        ctx.plan, ctx.h0_info is not None)
+                                        ctx.plan, ctx.h0_info is not None, h0=h032,
+                                        paired=ctx.paired)
         gdt, gshape = ctx.g_info
         if ctx.mode == GATE_GAMMA:
             dg = torch.zeros(gshape, device=q.device, dtype=gdt)

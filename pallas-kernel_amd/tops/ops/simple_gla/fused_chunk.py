@@ -12,7 +12,8 @@ from __future__ import annotations
 import torch
 
 from ...utils import ChunkPlan
-from .._chunk_core import GATE_GAMMA, check_qkv, chunk_fwd as _core_fwd, chunk_bwd as _core_bwd
+from .._chunk_core import (GATE_GAMMA, PAIRED, check_qkv, chunk_fwd as _core_fwd,
+                           chunk_bwd as _core_bwd, paired_states)
 from .chunk import chunk_simple_gla_fwd, chunk_simple_gla_bwd
 
 
@@ -26,20 +27,22 @@ class _FusedChunkSimpleGLA(torch.autograd.Function):
         plan = ChunkPlan.get(q.shape[0], q.shape[1], None, q.device)
         train = any(ctx.needs_input_grad[:5])
         o, ht, hs = _core_fwd(q, k, v, (GATE_GAMMA, gg), h032, scale, output_final_state, plan,
-                              keep_states=train)
+                              keep_states=PAIRED if train else False)
         if train:
-            ctx.save_for_backward(q, k, v, gg, hs)
+            ctx.save_for_backward(q, k, v, gg, hs, h032)
+            ctx.paired = paired_states(q, q.shape[-1], v.shape[-1])
             ctx.plan, ctx.scale, ctx.has_h0 = plan, scale, h0 is not None
             ctx.g_info = (g_gamma.dtype, g_gamma.shape)
         return o.to(dtype), (ht.to(dtype) if ht is not None else None)
 
     @staticmethod
     def backward(ctx, do, dht):
-        q, k, v, gg, hs = ctx.saved_tensors
+        q, k, v, gg, hs, h032 = ctx.saved_tensors
         qkv_dtype = do.dtype
         dht = None if dht is None else dht.contiguous().to(torch.float32)
         dq, dk, dv, _, dh0 = _core_bwd(q, k, v, (GATE_GAMMA, gg), do.contiguous().to(q.dtype), dht,
-                                       hs, ctx.scale, ctx.plan, ctx.has_h0)
+                                       hs, ctx.scale, ctx.plan, ctx.has_h0, h0=h032,
+                                       paired=ctx.paired)
         dg = torch.zeros(ctx.g_info[1], device=q.device, dtype=torch.float32)
         if dh0 is not None:
             dh0 = dh0.to(qkv_dtype)

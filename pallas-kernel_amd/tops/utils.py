@@ -134,6 +134,27 @@ def set_sequence_split(mode=None) -> None:
     _SPLIT["mode"] = mode
 
 
+# Residual states of the GLA / simple-GLA training path.  "full": the forward keeps the
+# state before every chunk and the backward's reverse sweep writes dh for every chunk
+# (2 x chunks x H x K x V fp32).  "paired" (bf16 inputs): one buffer of that size holding h
+# before the even chunks and dh after the odd ones; the dq / dk / dg kernel rebuilds the
+# rest from each chunk's pair partner.  Half the memory and checkpoint bytes, but the
+# rebuild needs both chunks of a pair on one CU: at B8 T4096 H16 K=V=128 on MI355X it is
+# about 0.1 ms per step slower, so "full" is the default.
+_CKPT = {"layout": "full"}
+
+
+def set_checkpoint_layout(layout: str = "full") -> None:
+    """"full" (default) or "paired": see the comment above."""
+    if layout not in ("full", "paired"):
+        raise ValueError("set_checkpoint_layout takes 'full' or 'paired'")
+    _CKPT["layout"] = layout
+
+
+def checkpoint_layout() -> str:
+    return _CKPT["layout"]
+
+
 def _device_cus(device) -> int:
     return int(torch.cuda.get_device_properties(device).multi_processor_count)
 

@@ -231,8 +231,12 @@ def _chunks(p):
     return out
 
 
-def dqkg(ck: Checker, p: dict, es: int, esv: int):
-    """gla_dqkg_kernel<TIn, TV, KP, VP> (csrc/gla_dqkg.hip)."""
+def dqkg(ck: Checker, p: dict, es: int, esv: int, pair: bool = False, planted_link: bool = False):
+    """gla_dqkg_kernel<TIn, TV, KP, VP> (csrc/gla_dqkg.hip).  pair: the PAIR instance
+    (interleaved checkpoints in p["hs"]: a workgroup takes global chunks 2i, 2i + 1, each
+    with the 256-thread mapping of the unpaired kernel; the state rows are read as two 4-float
+    runs, from the chunk's slot and the partner's, or from p["h0"] / p["dht"] of the
+    sequence when the partner lies in another one)."""
     H, K, V = p["H"], p["K"], p["V"]
     KP, VP = _kp(K), _kp(V)
     KH, NPS, VC = 32, KP // 32, VP // 32
@@ -248,7 +252,25 @@ def dqkg(ck: Checker, p: dict, es: int, esv: int):
     ch, sg = tid & 31, tid >> 5
     scalar_gate_inst = es == esv
     hh = np.arange(H, dtype=np.int64)[:, None]
-    for gc, n, c, row0, L in _chunks(p):
+    chunks = _chunks(p)
+    KVB = K * V * 4
+    for gc, n, c, row0, L in chunks:
+        # the state sources of this chunk: (tensor, base byte offset) for h and dh, or None
+        if pair:
+            c0 = gc - (gc & 1)
+            linked = c0 + 1 < p["total"] and chunks[c0][1] == chunks[c0 + 1][1]
+            linked = linked or planted_link     # (a planted mistake: partner always read)
+            own = ("hs", (gc * H + hh) * KVB)
+            if linked:
+                other = ("hs", ((gc + 1 if gc % 2 == 0 else gc - 1) * H + hh) * KVB)
+            else:
+                nm = p.get("dht") if gc % 2 == 0 else p.get("h0")
+                other = (nm, (n * H + hh) * KVB) if nm else None
+            states = [own, other]
+            runs = [(16 * j, 0) for j in range(2)]          # v0 = 32 vc + 16 j + 4 lg, 16 bytes
+        else:
+            states = [(p["hs"], (gc * H + hh) * KVB), (p["dhs"], (gc * H + hh) * KVB)]
+            runs = [(0, 0), (0, 16)]                        # v0 = 32 vc + 8 lg, 2 x 16 bytes
         t0 = c * C
         nval = min(C, L - t0)
         e0 = (row0 + t0) * H + hh
@@ -281,10 +303,12 @@ def dqkg(ck: Checker, p: dict, es: int, esv: int):
             cb = ps * KH
             kk = cb + 16 * kb + l16
             for vc in range(VC):
-                v0 = 32 * vc + 8 * lg
-                o = np.where((kk < K) & (v0 < V), (kk * V + v0) * 4, KOOB)
-                for nm in ("hs", "dhs"):
-                    ck.acc(p[nm], (gc * H + hh) * K * V * 4, o, 0, 32, f"dqkg load {nm}")
+                for dv0, soff in runs:
+                    v0 = 32 * vc + (4 if pair else 8) * lg + dv0
+                    o = np.where((kk < K) & (v0 < V), (kk * V + v0) * 4, KOOB)
+                    for st in states:
+                        if st is not None:
+                            ck.acc(st[0], st[1], o, soff, 16, f"dqkg load state {st[0]}")
             kc4 = cb + 16 * kb + 4 * lg
             for a in range(2):
                 tok = 16 * (2 * rh + a) + l16

@@ -27,9 +27,13 @@ def _np(t):
     return None if t is None else (t.numpy() if isinstance(t, torch.Tensor) else np.asarray(t))
 
 
-def chunk_op(B, T, H, K, V, es, cu=None, gate_mode=0, h0=True, dht=True, gate_width_bytes=4):
+def chunk_op(B, T, H, K, V, es, cu=None, gate_mode=0, h0=True, dht=True, gate_width_bytes=4,
+             paired=None):
     """Forward + backward launches of chunk_gla (gate_mode 0) / chunk_simple_gla (1: g [B,T,H],
-    2: g_gamma [H]) on one K, V <= 128 tile, as _fwd_tile / _bwd_tile make them."""
+    2: g_gamma [H]) on one K, V <= 128 tile, as _fwd_tile / _bwd_tile make them (bf16: the
+    interleaved checkpoints and the PAIR dq / dk / dg kernel, unless paired says otherwise)."""
+    if paired is None:
+        paired = es == 2
     plan = U.ChunkPlan(B, T, cu, "cpu")
     N = plan.N
     sizes = dict(q=B * T * H * K * es, k=B * T * H * K * es, v=B * T * H * V * es,
@@ -66,8 +70,11 @@ def chunk_op(B, T, H, K, V, es, cu=None, gate_mode=0, h0=True, dht=True, gate_wi
     p = dict(base, B=B, T=T, total=plan.total, cu=plan.cu_host if plan.varlen else None,
              offsets=_np(plan.offsets_dev), chunk_map=_np(plan.chunk_map_dev),
              q="q", k="k", v="v", do="do", hs="hs", dhs="dhs", dq="dq", dk="dk",
-             dg="dg" if gate_mode != 2 else None)
-    M.dqkg(ck, p, es, es)
+             dg="dg" if gate_mode != 2 else None,
+             h0="h0" if h0 else None, dht="dht" if dht else None)
+    M.dqkg(ck, p, es, es, pair=paired)
+    if paired:
+        M.dqkg(ck, p, es, es, pair=False)      # the unpaired instance serves the stage API
     return ck
 
 
@@ -191,6 +198,21 @@ def test_planted_unguarded_empty_prefetch_is_caught():
     M.sweep(ck, p, 2, rev=True, st=True)
     with pytest.raises(M.OOBError):
         M.sweep(ck, p, 2, rev=True, st=True, unguarded_prefetch=True)
+
+
+def test_planted_paired_partner_past_end_is_caught():
+    """With an odd number of chunks the last pair has no second chunk: reading the partner
+    slot of its first chunk without the same-sequence test runs past the checkpoints."""
+    B, T, H, K, V = 1, 192, 2, 32, 32          # 3 chunks
+    plan = U.ChunkPlan(B, T, None, "cpu")
+    sizes = dict(q=B * T * H * K * 2, k=B * T * H * K * 2, v=B * T * H * V * 2, do=B * T * H * V * 2,
+                 dq=B * T * H * K * 2, dk=B * T * H * K * 2, g=B * T * H * K * 4, dg=B * T * H * K * 4,
+                 hs=plan.total * H * K * V * 4, h0=H * K * V * 4, dht=H * K * V * 4)
+    p = dict(B=B, T=T, H=H, K=K, V=V, total=plan.total, cu=None, gate_mode=0, g="g", q="q", k="k",
+             v="v", do="do", hs="hs", dq="dq", dk="dk", dg="dg", h0="h0", dht="dht")
+    M.dqkg(M.Checker(sizes), p, 2, 2, pair=True)
+    with pytest.raises(M.OOBError, match="hs"):
+        M.dqkg(M.Checker(sizes), p, 2, 2, pair=True, planted_link=True)
 
 
 def test_segment_split_in_bounds():
