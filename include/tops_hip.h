@@ -505,6 +505,29 @@ int tops_gla_stage_dqkg(const void* q, const void* k, const void* v, const void*
                         const float* dk, float* dq_out, float* dk_out, float* dg, int B, int T,
                         int H, int K, int V, int chunk_size, float scale, void* stream);
 
+/* kda_intra_chunk_fwd (tops/ops/kda/chunk_intra.py:169-281, kernel :91-166), head-first
+ * layout: q, k [B,H,T,K] (dtype), g [B,H,T,K] fp32 (chunk-local gate cumsum, log2 units),
+ * beta [B,H,T] fp32, v [B,H,T,V] (dtype), segment_ids [B,T] int32 or NULL (tokens of
+ * different segments do not interact).  Writes, in dtype: u [B,H,T,V], w, qg, kg [B,H,T,K],
+ * Aqk and Akk_inv [B,H,T/C,C,C] (C = chunk_size: 16, 32, 64 or 128; T % C == 0). */
+int tops_kda_stage_intra_fwd(const void* q, const void* k, const float* g, const float* beta,
+                             const void* v, const int32_t* segment_ids, int dtype, void* u,
+                             void* w, void* qg, void* kg, void* Aqk, void* Akk_inv, int B, int H,
+                             int T, int K, int V, int chunk_size, float scale, void* stream);
+
+/* chunk_gated_delta_rule_fwd_h (tops/ops/common/chunk_delta_h.py:898-977; ref :44-166;
+ * oracle tops/cpu/ops/common/chunk_delta_h.py:22-118): the delta-rule state pass.
+ * k (already gated), w [B,T,H,K] and u [B,T,H,V] in dtype; g [B,T,H] and gk [B,T,H,K] fp32
+ * chunk-local gate cumsums in log2 units (either or both NULL); h0 [N,H,K,V] fp32 or NULL.
+ * Writes h [total_chunks,H,K,V] (dtype; the state before each chunk), v_new [B,T,H,V] fp32
+ * and ht [N,H,K,V] fp32 (each optional).  Varlen: cu_seqlens [N+1] with B == 1 and
+ * chunk_offsets [N] (first chunk of each sequence, its chunks counted on their own);
+ * otherwise T % chunk_size == 0 and N == B.  K <= 128, chunk_size <= 64. */
+int tops_delta_rule_fwd_h(const void* k, const void* w, const void* u, const float* g,
+                          const float* gk, int dtype, const float* h0, void* h, float* v_new,
+                          float* ht, const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                          int B, int T, int H, int K, int V, int N, int chunk_size, void* stream);
+
 /* KDA intra-chunk backward through Aqk and Akk, with E_ij = 2^{g_i - g_j} per channel (g the
  * chunk-local gate cumsum in log2 units) and dAqk, dAkk [B,T,H,C] used on i >= j:
  *   dq_i = sum_j dAqk_ij k_j E_ij;  row_i = sum_j dAkk_ij k_j E_ij;  db_i = row_i . k_i;

@@ -230,3 +230,104 @@ def chunk_kda_bwd_intra(q, k, g, beta, dAqk, dAkk, C=64):
     dg = qc * dq + kc * dkrow - kc * dkcol
     return (dq.reshape(B, T, H, K), (dkrow + dkcol).reshape(B, T, H, K), db.reshape(B, T, H),
             dg.reshape(B, T, H, K))
+
+
+def kda_intra_chunk_fwd(q, k, g, beta, v, segment_ids=None, scale=1.0, chunk_size=128):
+    """tops/ops/kda/chunk_intra.py:91-166 (kernel) and :169-281 (wrapper).  Head-first
+    [B, H, T, .] inputs, g the chunk-local gate cumsum in log2 units, segment_ids [B, T] (None:
+    one segment).  Per chunk (i, j rows; masks also require equal segment ids):
+        Aqk[i][j] = scale sum_d q_id k_jd 2^(g_id - g_jd)    (j <= i)
+        Akk[i][j] = beta_i sum_d k_id k_jd 2^(g_id - g_jd)   (j < i)
+        [u | w | Akk_inv] solves (I + Akk) X = [beta v | beta k 2^g | I] by forward
+        substitution (the reference's solve_unit_lower_triangular, :28-88)
+        qg = q 2^g,  kg = k 2^(g_last - g)
+    Returns (u [B,H,T,V], w, qg, kg [B,H,T,K], Aqk, Akk_inv [B,H,NC,C,C])."""
+    q, k, g, beta, v = map(f64, (q, k, g, beta, v))
+    B, H, T, K = k.shape
+    V = v.shape[-1]
+    C = chunk_size
+    NC = T // C
+    seg = np.zeros((B, T), np.int64) if segment_ids is None else np.asarray(segment_ids)
+    qc, kc, gc, vc = (x.reshape(B, H, NC, C, -1) for x in (q, k, g, v))
+    bc = beta.reshape(B, H, NC, C)
+    sc = seg.reshape(B, 1, NC, C)
+    same = sc[..., :, None] == sc[..., None, :]                     # [B,1,NC,C,C]
+    i = np.arange(C)
+    lower_qk = i[:, None] >= i[None, :]
+    lower = i[:, None] > i[None, :]
+    gd = np.where(lower_qk[..., None], gc[..., :, None, :] - gc[..., None, :, :], 0.0)
+    E = np.exp2(gd)                                                  # [B,H,NC,C,C,K]
+    Aqk = np.where(lower_qk & same, scale * np.einsum("...id,...jd,...ijd->...ij", qc, kc, E), 0.0)
+    Akk = np.where(lower & same, bc[..., :, None] * np.einsum("...id,...jd,...ijd->...ij", kc, kc, E),
+                   0.0)
+    rhs = np.concatenate([vc * bc[..., None], kc * np.exp2(gc) * bc[..., None],
+                          np.broadcast_to(np.eye(C), (B, H, NC, C, C))], axis=-1)
+    X = np.empty_like(rhs)
+    for r in range(C):
+        X[..., r, :] = rhs[..., r, :] - np.einsum("...j,...jc->...c", Akk[..., r, :r], X[..., :r, :])
+    u = X[..., :V].reshape(B, H, T, V)
+    w = X[..., V:V + K].reshape(B, H, T, K)
+    Akk_inv = X[..., V + K:]
+    qg = (qc * np.exp2(gc)).reshape(B, H, T, K)
+    kg = (kc * np.exp2(gc[..., -1:, :] - gc)).reshape(B, H, T, K)
+    return u, w, qg, kg, Aqk, Akk_inv
+
+
+def _delta_h_seq(k, w, u, g, gk, S, C):
+    """One sequence [L, H, .] of the delta-rule state pass; returns (h [NT, H, K, V], v_new, S)."""
+    L = k.shape[0]
+    NT = -(-L // C)
+    hs = np.empty((NT,) + S.shape, F64)
+    vn_all = np.empty_like(u)
+    for c in range(NT):
+        t0, t1 = c * C, min(L, (c + 1) * C)
+        hs[c] = S
+        vn = u[t0:t1] - np.einsum("thk,hkv->thv", w[t0:t1], S)
+        vn_all[t0:t1] = vn
+        if g is not None:
+            gl = g[t1 - 1]                                              # [H]
+            S = S * np.exp2(gl)[:, None, None]
+            vn = vn * np.exp2(gl[None] - g[t0:t1])[..., None]
+        if gk is not None:
+            S = S * np.exp2(gk[t1 - 1])[..., None]
+        S = S + np.einsum("thk,thv->hkv", k[t0:t1], vn)
+    return hs, vn_all, S
+
+
+def chunk_gated_delta_rule_fwd_h(k, w, u, g=None, gk=None, initial_state=None,
+                                 output_final_state=False, chunk_size=64, save_new_value=True,
+                                 use_exp2=True, cu_seqlens=None):
+    """tops/cpu/ops/common/chunk_delta_h.py:22-118 (per chunk: h = S; v_new = u - w S;
+    S *= 2^gk_last; S += k^T v_new, k already gated) with the scalar gate of
+    tops/ops/common/chunk_delta_h.py:44-166 (S *= 2^g_last; the update uses
+    v_new 2^(g_last - g), the returned v_new is ungated), and the varlen form of
+    :388-560 (chunks per sequence, a short last chunk gated at its last token).  Gates are
+    chunk-local cumsums, log2 units (natural with use_exp2=False).  Returns
+    (h [B, NT, H, K, V], v_new [B, T, H, V] or None, ht [N, H, K, V] or None)."""
+    k, w, u = f64(k), f64(w), f64(u)
+    f = 1.0 if use_exp2 else 1.0 / np.log(2.0)
+    g = None if g is None else f64(g) * f
+    gk = None if gk is None else f64(gk) * f
+    B, T, H, K = k.shape
+    V = u.shape[-1]
+    C = chunk_size
+    if cu_seqlens is None:
+        bounds = [(b, 0, T) for b in range(B)]
+    else:
+        cu = [int(x) for x in cu_seqlens]
+        bounds = [(0, cu[n], cu[n + 1]) for n in range(len(cu) - 1)]
+    N = len(bounds)
+    h0 = None if initial_state is None else f64(initial_state)
+    hs_all, vn = [], np.zeros((B, T, H, V), F64)
+    ht = np.empty((N, H, K, V), F64)
+    hb = [[] for _ in range(B)]
+    for n, (b, s0, s1) in enumerate(bounds):
+        S = np.zeros((H, K, V), F64) if h0 is None else h0[n].copy()
+        hs, vseq, S = _delta_h_seq(k[b, s0:s1], w[b, s0:s1], u[b, s0:s1],
+                                   None if g is None else g[b, s0:s1],
+                                   None if gk is None else gk[b, s0:s1], S, C)
+        hb[b].append(hs)
+        vn[b, s0:s1] = vseq
+        ht[n] = S
+    h = np.stack([np.concatenate(x, axis=0) for x in hb], axis=0)
+    return h, (vn if save_new_value else None), (ht if output_final_state else None)

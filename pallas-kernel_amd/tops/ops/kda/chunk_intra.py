@@ -1,10 +1,14 @@
-"""chunk_kda_bwd_intra on MI355X (mirrors tops/ops/kda/chunk_intra.py:477-574): the
-intra-chunk stage of the KDA backward, propagating dAqk and dAkk back to q, k, beta and
-the gate, added to the incoming gradients of the earlier stages.
+"""The intra-chunk stages of KDA on MI355X (mirror tops/ops/kda/chunk_intra.py):
 
-The fused KDA backward (tops_kda_chunk_bwd) computes this inside its WY kernel; this entry
-point serves callers that drive the stages themselves (tops_kda_stage_intra_bwd, one
-workgroup per (chunk, head), fp32 MFMA).
+  kda_intra_chunk_fwd (:169-281): per chunk, Aqk, the (I + Akk)^-1 solve giving u, w and
+      Akk_inv, and the gated qg, kg (tops_kda_stage_intra_fwd, csrc/kda_stages.hip: one
+      workgroup per (batch, head, chunk), fp32);
+  chunk_kda_bwd_intra (:477-574): dAqk and dAkk propagated back to q, k, beta and the gate,
+      added to the incoming gradients of the earlier stages (tops_kda_stage_intra_bwd, one
+      workgroup per (chunk, head), fp32 MFMA).
+
+The fused KDA path (tops_kda_chunk_fwd / _bwd) computes both inside its own kernels; these
+entry points serve callers that drive the stages themselves.
 """
 from __future__ import annotations
 
@@ -12,6 +16,38 @@ import torch
 
 from ... import _native as N
 from ..common._stage import act, f32, require
+
+
+def kda_intra_chunk_fwd(q, k, g, beta, v, segment_ids=None, scale: float = 1.0,
+                        chunk_size: int = 128):
+    """Head-first q, k, g [B,H,T,K] (g the chunk-local gate cumsum, log2 units), beta
+    [B,H,T], v [B,H,T,V]; segment_ids [B,T] (tokens of different segments do not interact;
+    None: one segment).  Returns (u [B,H,T,V], w, qg, kg [B,H,T,K], Aqk, Akk_inv
+    [B,H,NC,C,C]), all in k.dtype, as the reference."""
+    B, H, T, K = k.shape
+    V = v.shape[-1]
+    C = int(chunk_size)
+    require(T % C == 0, "Sequence length must be divisible by chunk_size")
+    for name, t, shp in (("q", q, (B, H, T, K)), ("g", g, (B, H, T, K)), ("beta", beta, (B, H, T)),
+                         ("v", v, (B, H, T, V))):
+        require(tuple(t.shape) == shp, f"{name} shape {tuple(t.shape)} != {shp}")
+    if C not in (16, 32, 64, 128):
+        raise NotImplementedError(f"tops-hip kda_intra_chunk_fwd takes chunk_size 16, 32, 64 or "
+                                  f"128, got {C}")
+    seg = None
+    if segment_ids is not None:
+        seg = torch.as_tensor(segment_ids, device=k.device).to(torch.int32).contiguous()
+        require(tuple(seg.shape) == (B, T), f"segment_ids shape {tuple(seg.shape)} != {(B, T)}")
+    (qq, kk, vv), code = act(q, k, v)
+    dev, dt = k.device, kk.dtype
+    u = torch.empty(B, H, T, V, device=dev, dtype=dt)
+    w, qg, kg = (torch.empty(B, H, T, K, device=dev, dtype=dt) for _ in range(3))
+    Aqk, Akk_inv = (torch.empty(B, H, T // C, C, C, device=dev, dtype=dt) for _ in range(2))
+    N.call("tops_kda_stage_intra_fwd", N.ptr(qq), N.ptr(kk), N.ptr(f32(g)), N.ptr(f32(beta)),
+           N.ptr(vv), N.ptr(seg), code, N.ptr(u), N.ptr(w), N.ptr(qg), N.ptr(kg), N.ptr(Aqk),
+           N.ptr(Akk_inv), B, H, T, K, V, C, float(scale), N.stream())
+    out = (u, w, qg, kg, Aqk, Akk_inv)
+    return tuple(x if x.dtype == k.dtype else x.to(k.dtype) for x in out)
 
 
 def chunk_kda_bwd_intra(q, k, g, beta, dAqk, dAkk, dq=None, dk=None, db=None, dg=None,
@@ -47,4 +83,4 @@ def chunk_kda_bwd_intra(q, k, g, beta, dAqk, dAkk, dq=None, dk=None, db=None, dg
             acc(dg, dgi, q.dtype))
 
 
-__all__ = ["chunk_kda_bwd_intra"]
+__all__ = ["kda_intra_chunk_fwd", "chunk_kda_bwd_intra"]

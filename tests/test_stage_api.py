@@ -44,6 +44,12 @@ def test_common_exports():
     for n in ("chunk_fwd_h_ref", "chunk_fwd_h_kernel", "chunk_fwd_h_kernel_varlen", "chunk_bwd_dh_ref", "chunk_bwd_dh_kernel"):
         assert callable(getattr(chunk_h, n))
     assert callable(cumsum.chunk_local_cumsum_vector)
+    # the KDA stages at the reference's module paths
+    from tops.ops.common import chunk_delta_h
+    from tops.ops.kda import chunk_intra
+    for n in ("chunk_gated_delta_rule_fwd_h", "chunk_gated_delta_rule_fwd_h_ref"):
+        assert callable(getattr(chunk_delta_h, n))
+    assert callable(chunk_intra.kda_intra_chunk_fwd)
 
 
 def test_argument_errors_before_device_work():
