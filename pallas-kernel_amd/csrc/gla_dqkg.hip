@@ -150,6 +150,20 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
   const int gmode = GK ? kGateK : p.gate_mode;
   const rsrc_t Rg = make_rsrc_rows(p.g, e0, nrows, gmode == kGateK ? K : 1);
   const float gam_h = gmode == kGateGamma ? p.g[hh] : 0.f;
+  // kGateGammaK: this thread's constant of every pass (channel ps * KH + ch), read up front
+  // through a range that is empty in the other modes.  The load is issued on every path: a
+  // vector load inside the pass loop taken only in some modes would make the compiler's
+  // waits for the prefetched rows conservative in all of them.
+  float gck[NPS];
+  if constexpr (!GK) {
+    const rsrc_t Rgc = make_rsrc(gmode == kGateGammaK ? p.g + (size_t)hh * K : nullptr,
+                                 gmode == kGateGammaK ? (long long)K * 4 : 0);
+#pragma unroll
+    for (int ps = 0; ps < NPS; ++ps) {
+      const int c = ps * KH + (tq & 31);
+      gck[ps] = __uint_as_float(bld32(Rgc, c < K ? (uint32_t)c * 4u : kOOB, 0));
+    }
+  }
 
   // ---------------- v / dO planes ([C][V], V contiguous)
   {
@@ -192,7 +206,17 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
 
   // ---------------- staging of a pass: thread = (channel ch, 8-row segment sg)
   const int ch = tq & 31, sg = tq >> 5;
-  float rq[8], rk[8], rg[8];
+  // raw words of the next pass's rows: fp32 elements, or (bf16) the aligned 32-bit word
+  // holding the element, whose half is the same for every row and pass (row strides H*K
+  // and pass offsets 32 are even: the half is ch's parity).  The element is taken out where
+  // it is used, so that the prefetch is not waited for at its issue.
+  uint32_t rq[8], rk[8];
+  float rg[8];
+  const uint32_t hsh = (ch & 1) ? 0u : 16u;
+  auto elem = [&](uint32_t w) {
+    if constexpr (SIN) return __uint_as_float(w);
+    else return __uint_as_float((w << hsh) & 0xffff0000u);
+  };
   // gate element (row r, channel kc): per-channel [.., K], per-token [.., 1], or none (gamma)
   const bool gk_mode = GK || gmode == kGateK;
   const uint32_t gstr = gk_mode ? rowK * 4u : (uint32_t)H * 4u;
@@ -207,14 +231,11 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
       const bool v_ = ok && r < nval;
       const uint32_t off = (uint32_t)r * rowK + kc;
       if constexpr (SIN) {
-        rq[i] = __uint_as_float(bld32(Rq, v_ ? off * 4u : kOOB, 0));
-        rk[i] = __uint_as_float(bld32(Rk, v_ ? off * 4u : kOOB, 0));
+        rq[i] = bld32(Rq, v_ ? off * 4u : kOOB, 0);
+        rk[i] = bld32(Rk, v_ ? off * 4u : kOOB, 0);
       } else {
-        // a 16-bit element through the aligned 32-bit word that holds it
-        const uint32_t wq = bld32(Rq, v_ ? (off & ~1u) * 2u : kOOB, 0);
-        const uint32_t wk = bld32(Rk, v_ ? (off & ~1u) * 2u : kOOB, 0);
-        rq[i] = (off & 1u) ? __uint_as_float(wq & 0xffff0000u) : __uint_as_float(wq << 16);
-        rk[i] = (off & 1u) ? __uint_as_float(wk & 0xffff0000u) : __uint_as_float(wk << 16);
+        rq[i] = bld32(Rq, v_ ? (off & ~1u) * 2u : kOOB, 0);
+        rk[i] = bld32(Rk, v_ ? (off & ~1u) * 2u : kOOB, 0);
       }
       // one unconditional load whatever the gate mode (gamma loads nothing: out of range)
       rg[i] = __uint_as_float(bld32(Rg, (v_ && gload) ? (uint32_t)r * gstr + gcol : kOOB, 0));
@@ -324,25 +345,13 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
   for (int ps = 0; ps < NPS; ++ps) {
     const int cb = ps * KH;
     load_state(Rh, hraw, ps);
-    // ---- the pass's WY parts of dk / dg (fp32-v instantiation only, the one the KDA
-    // backward uses): requested now, added in the epilogue
     constexpr bool kEarlyAdd = !kScalarGate;
     uint4 kadd[2], gadd[2];
-    if constexpr (kEarlyAdd) {
-#pragma unroll
-      for (int a = 0; a < 2; ++a) {
-        const int tok = 16 * (2 * rh + a) + l16;
-        const int kc = cb + 16 * kb + 4 * lg;
-        const uint32_t o = (kc < K && tok < nval) ? ((uint32_t)tok * rowK + kc) * 4u : kOOB;
-        kadd[a] = bld128(Rdka, o, 0);
-        gadd[a] = bld128(Rdga, o, 0);
-      }
-    }
     // ---- gate cumsum of the pass (thread: channel ch, rows 8sg..8sg+7); the constant gates
     // (g_gamma [H] or [H, K]) give every valid row the same value
     float gconst = gam_h;
     if constexpr (!GK) {
-      if (gmode == kGateGammaK) gconst = cb + ch < K ? p.g[(size_t)hh * K + cb + ch] : 0.f;
+      if (gmode == kGateGammaK) gconst = gck[ps];
     }
     float G[8];
 #pragma unroll
@@ -375,8 +384,8 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
       for (int i = 0; i < 8; ++i) {
         G[i] += pre;
         gG[(8 * sg + i) * LG + ch] = G[i];
-        qt[i] = rq[i] * fast_exp2(G[i] - gmv);
-        kt[i] = rk[i] * fast_exp2(gmv - G[i]);
+        qt[i] = elem(rq[i]) * fast_exp2(G[i] - gmv);
+        kt[i] = elem(rk[i]) * fast_exp2(gmv - G[i]);
       }
       put_n<true, 8>(Pqt, ch, 8 * sg, qt);
       put_n<true, 8>(Pkt, ch, 8 * sg, kt);
@@ -470,6 +479,19 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
         if constexpr (SINV) vl = Pv.lo8(16 * B2 + l16, v0);
         X[a] = mma<true, SIN>(X[a], Ah, Al, doh, dol);
         Wt[a] = mma<true, SINV>(Wt[a], Dh, Dl, vh, vl);
+      }
+    }
+    // ---- the pass's WY parts of dk / dg (fp32-v instantiation only, the one the KDA
+    // backward uses): requested once the inter-chunk products have freed their registers,
+    // added in the epilogue
+    if constexpr (kEarlyAdd) {
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const int tok = 16 * (2 * rh + a) + l16;
+        const int kc = cb + 16 * kb + 4 * lg;
+        const uint32_t o = (kc < K && tok < nval) ? ((uint32_t)tok * rowK + kc) * 4u : kOOB;
+        kadd[a] = bld128(Rdka, o, 0);
+        gadd[a] = bld128(Rdga, o, 0);
       }
     }
     // ---- sum_t k~ W_inter (this wave's tokens) and sum_v h dh (token-half-0 waves)
