@@ -232,8 +232,9 @@ def _config2(dev, gen, iters):
     with torch.no_grad():
         sec = _time(lambda: fused_recurrent_gla(q, k, v, gk, initial_state=h0,
                                                 output_final_state=True), iters)
-        # the same shape walked in reverse (time reversal onto the chunk kernels), and with a
-        # per-column gv gate instead of gk (the per-token kernel): same algorithmic bytes
+        # the same shape walked in reverse (the reverse chunk sweep with the gate read one
+        # token later), and with a per-column gv gate instead of gk (the per-token kernel):
+        # same algorithmic bytes
         sec_rev = _time(lambda: fused_recurrent_gla(q, k, v, gk, initial_state=h0,
                                                     output_final_state=True, reverse=True), iters)
         sec_gv = _time(lambda: fused_recurrent_gla(q, k, v, None, gv=gk, initial_state=h0,

@@ -166,6 +166,22 @@ int tops_chunk_bwd_dqkg_paired(const void* q, const void* k, const void* v, cons
                                const int32_t* chunk_map, int total_chunks, int B, int T, int H,
                                int K, int V, int N, int dtype, float scale, void* stream);
 
+/* Reverse-time recurrence, chunked: fused_recurrent_gla_fwd with reverse = True
+ * (tops/ops/gla/fused_recurrent.py:380-431; oracle tops/cpu/ops/gla/fused_recurrent.py:116-160,
+ * one body iterated from the last token to the first), without gv:
+ *     S_t = diag(exp(g_t)) S_(t+1) + k_t v_t^T   (S_T = h0),   o_t = scale S_t^T q_t,
+ * ht = S at the first token of each sequence.  Runs on the reverse chunk sweep (the state
+ * gradient recurrence has this form with q and k exchanged and the gate read one token
+ * later), so it takes no reversed copies of the inputs.  q, k [B,T,H,K], v [B,T,H,V] in dtype;
+ * g and gate_mode as tops_chunk_fwd_paired (natural-log gates); h0 [N,H,K,V] fp32 or NULL;
+ * o [B,T,H,V] in dtype; ht [N,H,K,V] fp32 or NULL.  Varlen: cu_seqlens [N+1] with B == 1
+ * (empty sequences pass h0 through).  K <= 128, K and V multiples of 8.  Inference only:
+ * nothing is kept for a backward. */
+int tops_chunk_reverse_fwd(const void* q, const void* k, const void* v, const float* g,
+                           int gate_mode, const float* h0, void* o, float* ht,
+                           const int32_t* cu_seqlens, int B, int T, int H, int K, int V, int N,
+                           int dtype, float scale, void* stream);
+
 /* Simple GLA: one log-gate per (token, head) -- g [B,T,H] fp32 -- or a constant per-head
  * log-decay g_gamma [H] fp32; pass exactly one.  The state recurrence is GLA's with the
  * gate shared by all K channels.  Replaces tops.ops.simple_gla.chunk_simple_gla_fwd /

@@ -38,6 +38,13 @@ struct SweepParams {
   // checkpoints written: 0 = every chunk, 1 = even global chunks only, 2 = odd only (the
   // interleaved layout: h before the even chunks, dh after the odd ones, in one buffer)
   int ckpt_par;
+  // reverse sweep only: gshift = 1 reads the gate of token t - 1 at token t (0 at the first
+  // token of a sequence) and starts from s0 decayed by the gate of the sequence's last
+  // token; every output element is multiplied by oscale.  With q and k exchanged, v as Y and
+  // scale 1 this is the reverse-time recurrence S_t = diag(2^g_t) S_(t+1) + k_t v_t^T,
+  // o_t = oscale S_t^T q_t (fused_recurrent with reverse = True).
+  int gshift = 0;
+  float oscale = 1.f;
 };
 
 // TIn = uint16_t (bf16 bits) or float; REV = reverse (state-gradient) sweep;

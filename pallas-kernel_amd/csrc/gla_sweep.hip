@@ -194,6 +194,28 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       S[i][r] = x;
     }
   }
+  // reverse-time recurrence (gshift): the state entering the last token is h0 decayed by
+  // that token's gate
+  constexpr bool RSH = REV && !ST && !DELTA;
+  const bool gsh = RSH && p.gshift;
+  if (gsh && L > 0) {
+    const size_t el = (size_t)(row0 + L - 1) * H + hh;
+    float fac[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int kr = 16 * msb + 4 * lg + r;
+      float gl = gam_h;
+      if (gk_mode) gl = kr < K ? p.g[el * K + kr] : 0.f;
+      else if (gmode == kGateS) gl = p.g[el];
+      else if (gmode == kGateGammaK) gl = kr < K ? p.g[(size_t)hh * K + kr] : 0.f;
+      fac[r] = fast_exp2(gl * kLog2e);
+    }
+#pragma unroll
+    for (int i = 0; i < NHT; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) S[i][r] *= fac[r];
+    }
+  }
   // Drain these loads here: a load still in flight when the chunk loop starts makes the
   // compiler's wait before the first use of S inside the loop a full vmcnt(0) on every
   // iteration, which also waits for the previous chunk's output and checkpoint stores.
@@ -216,7 +238,11 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     const size_t e0 = (size_t)(row0 + t0) * H + hh;     // first row of the chunk, this head
     const rsrc_t Rq = make_rsrc_rows((const TIn*)p.q, e0, nrows, K);
     const rsrc_t Rk = make_rsrc_rows((const TIn*)p.k, e0, nrows, K);
-    const rsrc_t Rg = make_rsrc_rows(p.g, e0, nrows, gk_mode ? K : 1);
+    // gshift: token t reads the gate row of token t - 1, so the rows start one token earlier,
+    // except in the sequence's first chunk, whose row 0 reads nothing (gate 0)
+    const int gadj = (gsh && t0 == 0) ? 1 : 0;
+    const size_t eg = gsh && t0 > 0 ? e0 - (size_t)H : e0;
+    const rsrc_t Rg = make_rsrc_rows(p.g, eg, nrows, gk_mode ? K : 1);
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
       const bool ok = r0 + i < nval;
@@ -225,9 +251,17 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       // the gate mode's transform is applied when the chunk is consumed, so the prefetch
       // never waits: four channels [.., K], or the one per-(token, head) word [.., 1]
       // (gamma: offGm is out of range, nothing is read)
-      if constexpr (GK) rs.rg[i] = bld128(Rg, ok ? offGm : kOOB, i * gstride);
-      else if (gk_mode) rs.rg[i] = bld128(Rg, ok ? offGm : kOOB, i * gstride);
-      else rs.rg[i] = make_uint4(bld32(Rg, ok ? offGm : kOOB, i * gstride), 0u, 0u, 0u);
+      uint32_t go = ok ? offGm : kOOB, gs = i * gstride;
+      if constexpr (RSH) {
+        // row r0 + i - gadj (>= 0 where read), as one vector offset; masked columns and the
+        // constant gates (offGm out of range) read nothing
+        const bool rd = ok && r0 + i >= gadj && offGm != kOOB;
+        go = rd ? offGm + (uint32_t)(i - gadj) * gstride : kOOB;
+        gs = 0;
+      }
+      if constexpr (GK) rs.rg[i] = bld128(Rg, go, gs);
+      else if (gk_mode) rs.rg[i] = bld128(Rg, go, gs);
+      else rs.rg[i] = make_uint4(bld32(Rg, go, gs), 0u, 0u, 0u);
     }
     if constexpr (!FWD_DELTA) {
       const rsrc_t Ry = make_rsrc_rows((const TIn*)p.y, e0, nrows, V);
@@ -305,9 +339,11 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       if constexpr (GK) {
       } else if (gmode == kGateS) {
         x[1] = x[2] = x[3] = x[0];
-      } else if (!gk_mode) {   // constant gates: zero on the rows past the sequence
+      } else if (!gk_mode) {   // constant gates: zero on the rows past the sequence (and, with
+                               // gshift, on the sequence's first token)
+        const bool on = r0 + i < nval && !(gsh && t0 == 0 && r0 + i == 0);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) x[j] = r0 + i < nval ? gam4[j] : 0.f;
+        for (int j = 0; j < 4; ++j) x[j] = on ? gam4[j] : 0.f;
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) G[i][j] = x[j] * kLog2e + (i > 0 ? G[i - 1][j] : 0.f);
@@ -781,6 +817,10 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
             acc = mma<SY, true>(acc, ah, al, cat44(dh[P0], dh[P1]), cat44(dl[P0], dl[P1]));
           }
         }
+        if constexpr (RSH) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[r] *= p.oscale;
+        }
         const int v0 = vt * BV + 16 * nn + 4 * lg;
         Wd::st4(Ro, acc, v0 < V ? oo : kOOB, (uint32_t)(16 * nn * ES));
       }
@@ -956,4 +996,35 @@ extern "C" int tops_chunk_fwd_paired(const void* q, const void* k, const void* v
   if (!ckpt) return tops_set_error(TOPS_ERR_NULL, "chunk_fwd_paired: null ckpt");
   return chunk_fwd_impl(q, k, v, g, h0, o, ht, ckpt, cu_seqlens, chunk_offsets, B, T, H, K, V, N,
                         dtype, scale, gate_mode, stream, 1);
+}
+
+extern "C" int tops_chunk_reverse_fwd(const void* q, const void* k, const void* v, const float* g,
+                                      int gate_mode, const float* h0, void* o, float* ht,
+                                      const int32_t* cu_seqlens, int B, int T, int H, int K, int V,
+                                      int N, int dtype, float scale, void* stream) {
+  if (!q || !k || !v || !g || !o) return tops_set_error(TOPS_ERR_NULL, "chunk_reverse_fwd: null tensor");
+  if (gate_mode < kGateK || gate_mode > kGateGammaK)
+    return tops_set_error(TOPS_ERR_SHAPE, "chunk_reverse_fwd: gate_mode must be 0..3");
+  if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || N <= 0)
+    return tops_set_error(TOPS_ERR_SHAPE, "chunk_reverse_fwd: non-positive dimension");
+  if (K > 128 || (K % 8) || (V % 8))
+    return tops_set_error(TOPS_ERR_SHAPE, "chunk_reverse_fwd: need K <= 128, K % 8 == 0, V % 8 == 0");
+  if (cu_seqlens && B != 1) return tops_set_error(TOPS_ERR_SHAPE, "chunk_reverse_fwd: varlen needs B == 1");
+  if (!cu_seqlens && N != B) return tops_set_error(TOPS_ERR_SHAPE, "chunk_reverse_fwd: N must equal B");
+  if ((long long)kChunk * H * (K > V ? K : V) * 4 >= (1LL << 31))
+    return tops_set_error(TOPS_ERR_SHAPE, "chunk_reverse_fwd: H * max(K, V) too large for 32-bit chunk offsets");
+  // The reverse sweep's state gradient recurrence D_t = diag(2^g'_(t+1)) D_(t+1) + q'_t dO'_t^T,
+  // out_t = D_t^T k'_t, with q' = k, k' = q, dO' = v, scale 1 and g'_t = g_(t-1) (gshift) is
+  // the reverse-time recurrence itself; o = scale * out.
+  SweepParams p{k, q, g, v, h0, o, ht, nullptr, cu_seqlens, nullptr,
+                B, T, H, K, V, N, (V + 63) / 64, 1.f, gate_mode};
+  p.gshift = 1;
+  p.oscale = scale;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e;
+  if (dtype == TOPS_BF16) e = launch_gla_sweep<uint16_t, true>(p, s);
+  else if (dtype == TOPS_F32) e = launch_gla_sweep<float, true>(p, s);
+  else return tops_set_error(TOPS_ERR_DTYPE, "chunk_reverse_fwd: dtype must be TOPS_F32 or TOPS_BF16");
+  if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
+  return TOPS_OK;
 }

@@ -11,9 +11,13 @@ cu_seqlens.  Two HIP implementations of the same recurrence are used:
     chunkwise on MFMA by the chunk kernels (gla_sweep.hip, gla_dqkg.hip) -- the same
     sums, grouped by 64-token chunks.  reverse=True runs the same recurrence from the last
     token to the first (tops/cpu/ops/gla/fused_recurrent.py:116-160: one body, iterated
-    backwards), i.e. the forward recurrence on every sequence's time-reversed inputs: the
-    inputs are reversed per sequence, swept forward, and the output reversed back (the
-    reversal is part of the autograd graph);
+    backwards).  Without gradients that is the reverse chunk sweep itself
+    (tops_chunk_reverse_fwd: the backward's state-gradient recurrence has the same form
+    with q and k exchanged and the gate read one token later), reading the inputs in place;
+    with gradients, or where the sweep would be split into sequence-parallel segments, it is
+    the forward recurrence on every sequence's time-reversed inputs: the inputs are reversed
+    per sequence, swept forward, and the output reversed back (the reversal is part of the
+    autograd graph);
   * with gv, the per-token kernels of gla_recurrent.hip (state in registers, one token at
     a time) run the forward, a replay + reverse backward and the gate-gradient suffix sums.
 """
@@ -23,6 +27,7 @@ import numpy as np
 import torch
 
 from ... import _native as N
+from ...utils import ChunkPlan
 
 
 def _cu_dev(cu_seqlens, device):
@@ -162,6 +167,37 @@ def time_reversal(T: int, cu_seqlens, device):
     return torch.tensor(idx, device=device, dtype=torch.long)
 
 
+_REV_GATE_CODE = {"k": 0, "s": 1, "gamma": 2}
+
+
+def reverse_chunk_native(q, k, v, mode, g, initial_state, scale, output_final_state, cu_seqlens):
+    """The reverse-time recurrence on the reverse chunk sweep (tops_chunk_reverse_fwd), for
+    calls that need no gradient.  mode: "k" (g [B,T,H,K]), "s" (g [B,T,H]) or "gamma"
+    (g [H], a constant log-gate per head).  Returns (o, ht or None), or None where it does
+    not apply: gradients wanted, dtypes or shapes the kernel does not take, or a call whose
+    sequences the chunk kernels would split into sequence-parallel segments (the time-reversal
+    route keeps that split)."""
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad
+                                       for t in (q, k, v, g, initial_state)):
+        return None
+    if q.dtype not in (torch.float32, torch.bfloat16) or K > 128 or K % 8 or V % 8:
+        return None
+    plan = ChunkPlan(B, T, cu_seqlens, q.device)
+    if plan.segments(H, V) is not None:
+        return None
+    q, k, v = (x.contiguous() for x in (q, k, v))
+    gt = g.contiguous().to(torch.float32)
+    o = torch.empty_like(v)
+    ht = torch.empty(plan.N, H, K, V, device=q.device, dtype=torch.float32) \
+        if output_final_state else None
+    N.call("tops_chunk_reverse_fwd", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gt), _REV_GATE_CODE[mode],
+           N.ptr(_f32(initial_state)), N.ptr(o), N.ptr(ht), N.ptr(plan.cu_dev), B, T, H, K, V,
+           plan.N, N.dtype_code(q.dtype), float(scale), N.stream())
+    return o, ht
+
+
 def _reversed_chunk(fn, q, k, v, g, cu_seqlens, **kw):
     """fn (a chunk op) on the time-reversed sequences; returns (o in original order, ht)."""
     rev = time_reversal(q.shape[1], cu_seqlens, q.device)
@@ -178,6 +214,12 @@ def fused_recurrent_gla(q, k, v, gk=None, gv=None, scale=None, initial_state=Non
     wide = K > 128 or q.dtype not in (torch.float32, torch.bfloat16)
     if scale is None:
         scale = K ** -0.5
+    if reverse and gv is None:
+        r = reverse_chunk_native(q, k, v, "k" if gk is not None else "gamma",
+                                 gk if gk is not None else torch.zeros(H, device=q.device),
+                                 initial_state, scale, output_final_state, cu_seqlens)
+        if r is not None:
+            return r
     if wide and not _chunked(gv, reverse, K, V):
         return _sliced(q, k, v, gk, gv, scale, initial_state, output_final_state, reverse,
                        cu_seqlens)
@@ -205,6 +247,12 @@ def fused_recurrent_gla_fwd(q, k, v, gk=None, gv=None, scale=None, initial_state
         from .chunk import chunk_gla
         return chunk_gla(q, k, v, gk, scale=scale, initial_state=initial_state,
                          output_final_state=output_final_state, cu_seqlens=cu_seqlens)
+    if reverse and gv is None:
+        r = reverse_chunk_native(q, k, v, "k" if gk is not None else "gamma",
+                                 gk if gk is not None else torch.zeros(H, device=q.device),
+                                 initial_state, scale, output_final_state, cu_seqlens)
+        if r is not None:
+            return r
     o, _, ht = _fwd(q.contiguous(), k.contiguous(), v.contiguous(), _f32(gk), _f32(gv),
                     _f32(initial_state), scale, output_final_state, reverse,
                     _cu_dev(cu_seqlens, q.device), n, want_o32=False)

@@ -5,8 +5,9 @@ o_t = h_t^T (scale q_t) is GLA's with the gate shared by all K channels.  In for
 order it runs on the chunk kernels' per-token scalar-gate mode (tops.ops.simple_gla
 chunk_simple_gla with g [B,T,H]: the same sums grouped by 64-token chunks); g and g_gamma
 are combined into that one [B,T,H] gate, g + g_gamma (tops/cpu/ops/simple_gla/naive.py:
-113-125).  reverse=True runs the same on every sequence reversed in time (the recurrence
-iterated from the last token).  Shapes the chunk kernels do not take run the per-token
+113-125).  reverse=True (the recurrence iterated from the last token) runs on the reverse
+chunk sweep when no gradient is wanted, else on every sequence reversed in time
+(tops.ops.gla.fused_recurrent.reverse_chunk_native / _reversed_chunk).  Shapes the chunk kernels do not take run the per-token
 kernels of tops.ops.gla.fused_recurrent_gla with the gate as a broadcast view over K.
 Either way the combination is part of the
 autograd graph, so the gradients w.r.t. g [B,T,H] and g_gamma [H] come back summed over the
@@ -16,7 +17,7 @@ from __future__ import annotations
 
 import torch
 
-from ..gla.fused_recurrent import _reversed_chunk, fused_recurrent_gla
+from ..gla.fused_recurrent import _reversed_chunk, fused_recurrent_gla, reverse_chunk_native
 from .chunk import chunk_simple_gla
 
 
@@ -40,6 +41,16 @@ def fused_recurrent_simple_gla(q, k, v, g=None, g_gamma=None, scale=None, initia
                                     output_final_state=output_final_state, g=g_,
                                     cu_seqlens=cu_seqlens)
         if reverse:
+            sc = K ** -0.5 if scale is None else scale
+            if g is None and g_gamma is not None:
+                r = reverse_chunk_native(q, k, v, "gamma", gg, initial_state, sc,
+                                         output_final_state, cu_seqlens)
+            else:
+                r = reverse_chunk_native(q, k, v, "s" if gs is not None else "gamma",
+                                         gs if gs is not None else torch.zeros(H, device=q.device),
+                                         initial_state, sc, output_final_state, cu_seqlens)
+            if r is not None:
+                return r
             return _reversed_chunk(run, q, k, v, gs, cu_seqlens)
         return run(q, k, v, gs, cu_seqlens)
     gk = None

@@ -68,10 +68,14 @@ def _kp(K):
 
 # --------------------------------------------------------------------------- gla_sweep_kernel
 def sweep(ck: Checker, p: dict, es: int, rev: bool, delta: bool = False, st: bool = False,
-          gate_width_bytes: int = 4, unguarded_prefetch: bool = False):
+          gate_width_bytes: int = 4, unguarded_prefetch: bool = False, gshift: bool = False,
+          planted_shift: bool = False):
     """gla_sweep_kernel<TIn, KP, REV, DELTA, ST> (csrc/gla_sweep.hip).  p holds the SweepParams
     fields: B, T, H, K, V, N, cu (host array or None), seg_end, offsets, gate_mode and which of
-    s0 / s_fin / ckpt / y32 / dec_fin / u / w are bound (tensor names in ck.sizes)."""
+    s0 / s_fin / ckpt / y32 / dec_fin / u / w are bound (tensor names in ck.sizes).  gshift:
+    the reverse sweep reads the gate one token later (tops_chunk_reverse_fwd); planted_shift
+    moves the gate rows one token earlier in the sequence's first chunk too (the mistake the
+    first-chunk case exists for)."""
     B, T, H, K, V, N = (p[x] for x in ("B", "T", "H", "K", "V", "N"))
     KP = _kp(K)
     NTH, BV = 512, 64
@@ -126,6 +130,20 @@ def sweep(ck: Checker, p: dict, es: int, rev: bool, delta: bool = False, st: boo
         else:
             row0, L, cbase = n * T, T, n * (-(-T // C))
         NTs = -(-L // C)
+        gsh = gshift and rev and not delta and not st
+        if gsh and L > 0:
+            # the decay of h0 by the last token's gate (plain loads, kr < K checked)
+            el = (row0 + L - 1) * H + hh
+            for r in range(4):
+                kr = 16 * msb + 4 * lg + r
+                if gm == 0:
+                    ck.acc(p["g"], 0, np.where(kr < K, (el * K + kr) * 4, KOOB), 0, 4, "sweep g last")
+                elif gm == 1:
+                    ck.acc(p["g"], 0, el * 4 + 0 * kr, 0, 4, "sweep g last")
+                elif gm == 2:
+                    ck.acc(p["g"], 0, hh * 4 + 0 * kr, 0, 4, "sweep g_gamma")
+                else:
+                    ck.acc(p["g"], 0, np.where(kr < K, (hh * K + kr) * 4, KOOB), 0, 4, "sweep g_gamma")
         # the first chunk is prefetched only when there is one (unguarded_prefetch plants the
         # unconditional prefetch, which for an empty sequence walked in reverse is chunk -1)
         walk = [NTs - 1 - it if rev else it for it in range(NTs)]
@@ -160,7 +178,16 @@ def sweep(ck: Checker, p: dict, es: int, rev: bool, delta: bool = False, st: boo
                 for nm in ("q", "k"):
                     ck.acc(p[nm], e0 * K * es, np.where(ok, offQ, KOOB), i * rowK * es, 4 * es,
                            f"sweep load {nm} chunk {c}")
-                if gw:
+                if gsh:
+                    gadj = 1 if (t0 == 0 and not planted_shift) else 0
+                    eg = e0 - H if (t0 > 0 or planted_shift) else e0
+                    if gm in (0, 1):
+                        ck.rows_rsrc(p["g"], eg, nrows, gname_w, 4)
+                    rd = ok & (r0 + i >= gadj) & (offGm < KOOB)
+                    ck.acc(p["g"], eg * gname_w * 4,
+                           np.where(rd, offGm + (i - gadj) * gstride, KOOB), 0, gw,
+                           f"sweep load shifted g (mode {gm}) chunk {c}")
+                elif gw:
                     ck.acc(p["g"], e0 * gname_w * 4, np.where(ok, offGm, KOOB), i * gstride, gw,
                            f"sweep load g (mode {gm}) chunk {c}")
             if not fwd_delta:

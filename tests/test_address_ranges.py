@@ -221,3 +221,48 @@ def test_segment_split_in_bounds():
     ck = chunk_op(1, 2048, 2, 128, 128, 2, gate_mode=0)
     assert ck.count > 0
     chunk_op(1, 3000, 2, 64, 64, 4, cu=[0, 100, 3000], gate_mode=1)
+
+
+def reverse_op(B, T, H, K, V, es, cu=None, gate_mode=0, h0=True, planted_shift=False):
+    """The launch of tops_chunk_reverse_fwd (fused_recurrent reverse=True without gradients):
+    the reverse sweep with q and k exchanged, v as Y, the gate read one token later, no
+    checkpoints."""
+    plan = U.ChunkPlan(B, T, cu, "cpu")
+    N = plan.N
+    sizes = dict(q=B * T * H * K * es, k=B * T * H * K * es, v=B * T * H * V * es,
+                 o=B * T * H * V * es,
+                 g={0: B * T * H * K * 4, 1: B * T * H * 4, 2: H * 4, 3: H * K * 4}[gate_mode],
+                 h0=N * H * K * V * 4, ht=N * H * K * V * 4)
+    ck = M.Checker(sizes)
+    p = dict(B=B, T=T, H=H, K=K, V=V, N=N, cu=plan.cu_host if plan.varlen else None, offsets=None,
+             gate_mode=gate_mode, g="g", q="k", k="q", y="v", out="o",
+             s0="h0" if h0 else None, s_fin="ht")
+    M.sweep(ck, p, es, rev=True, gshift=True, planted_shift=planted_shift)
+    return ck
+
+
+# test_gpu_reverse_native.py's launches
+REVERSE = [dict(B=2, T=64, H=2, K=32, V=32), dict(B=2, T=50, H=2, K=64, V=64),
+           dict(B=1, T=1, H=2, K=32, V=64), dict(B=2, T=200, H=3, K=16, V=40),
+           dict(B=1, T=150, H=2, K=32, V=32, cu=[0, 13, 13, 64, 65, 150]),
+           dict(B=1, T=4, H=2, K=8, V=16, cu=[0, 1, 2, 3, 4]),
+           dict(B=2, T=256, H=2, K=128, V=128), dict(B=1, T=70, H=1, K=128, V=200),
+           dict(B=1, T=150, H=2, K=32, V=48, cu=[0, 40, 40, 99, 150])]
+
+
+@pytest.mark.parametrize("es", [4, 2], ids=["f32", "bf16"])
+@pytest.mark.parametrize("c", REVERSE, ids=lambda c: "B{B}-T{T}-H{H}-K{K}-V{V}".format(**c))
+def test_reverse_native_in_bounds(c, es):
+    for gm in (0, 1, 2, 3):
+        ck = reverse_op(c["B"], c["T"], c["H"], c["K"], c["V"], es, cu=c.get("cu"), gate_mode=gm)
+        assert ck.count > 0
+
+
+def test_planted_reverse_first_chunk_shift_is_caught():
+    """Reading the first chunk's gate rows one token early runs before the tensor for the
+    first sequence."""
+    reverse_op(1, 100, 2, 32, 32, 4, gate_mode=0)
+    with pytest.raises(M.OOBError, match="g"):
+        reverse_op(1, 100, 2, 32, 32, 4, gate_mode=0, planted_shift=True)
+    with pytest.raises(M.OOBError, match="g"):
+        reverse_op(1, 100, 2, 32, 32, 4, gate_mode=1, planted_shift=True)
