@@ -182,6 +182,18 @@ int tops_chunk_reverse_fwd(const void* q, const void* k, const void* v, const fl
                            const int32_t* cu_seqlens, int B, int T, int H, int K, int V, int N,
                            int dtype, float scale, void* stream);
 
+/* Value-side gate, chunked: fused_recurrent_gla_fwd with gv and without gk
+ * (tops/ops/gla/fused_recurrent.py:380-431; oracle tops/cpu/ops/gla/fused_recurrent.py:51-167):
+ *     S_t = S_(t-1) diag(exp(gv_t)) + k_t v_t^T   (S_0 = h0),   o_t = scale S_t^T q_t,
+ * computed in 64-token chunks on MFMA (the forward sweep with the gate applied per V column:
+ * v~ = v 2^(Gm - G) in, 2^(G - Gm) out, per-column state decay).  q, k [B,T,H,K], v [B,T,H,V]
+ * bf16; gv [B,T,H,V] fp32 natural-log gates; h0 [N,H,K,V] fp32 or NULL; o [B,T,H,V] bf16;
+ * ht [N,H,K,V] fp32 or NULL.  Varlen: cu_seqlens [N+1] with B == 1.  K <= 128, K and V
+ * multiples of 8; dtype TOPS_BF16 only.  Inference only: nothing is kept for a backward. */
+int tops_gla_chunk_fwd_gv(const void* q, const void* k, const void* v, const float* gv,
+                          const float* h0, void* o, float* ht, const int32_t* cu_seqlens, int B,
+                          int T, int H, int K, int V, int N, int dtype, float scale, void* stream);
+
 /* Simple GLA: one log-gate per (token, head) -- g [B,T,H] fp32 -- or a constant per-head
  * log-decay g_gamma [H] fp32; pass exactly one.  The state recurrence is GLA's with the
  * gate shared by all K channels.  Replaces tops.ops.simple_gla.chunk_simple_gla_fwd /

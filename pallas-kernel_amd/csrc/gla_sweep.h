@@ -52,6 +52,10 @@ struct SweepParams {
 template <typename TIn, bool REV, bool DELTA = false>
 hipError_t launch_gla_sweep(const SweepParams& p, hipStream_t s);
 
+// Forward sweep with the gate on the value side (g = gv [B,T,H,V], bf16 inputs): see
+// gla_sweep.hip.
+hipError_t launch_gla_sweep_gv(const SweepParams& p, hipStream_t s);
+
 // State-only sweep: the end state s_fin of every sequence (from s0, usually zero) and the
 // decay sums dec_fin; no output, no checkpoints.
 template <typename TIn, bool REV>

@@ -33,6 +33,13 @@
 // H^T = 2^Gm S); reverse, the state update gains - w^T dv_new, and dv_new is written
 // transposed per chunk for the WY backward.
 //
+// GV (forward, bf16): the gate sits on the value side, one log-gate per (token, V column)
+// (fused_recurrent_gla's gv), S[:, v] <- 2^gv S[:, v] + k v^T.  q and k enter ungated (exact
+// bf16: the X / Z planes carry no lo half), v~ = v 2^(Gm - G) per column is split into hi /
+// lo, every output element is multiplied by 2^(G - Gm) of its (token, column) from an fp32
+// LDS plane, and S decays per column: o^T = (2^Gm S)^T q^T + v~^T M, S = 2^Gamma S +
+// 2^(Gamma-Gm) (k^T v~), M[i][j] = scale q_i.k_j (j <= i).
+//
 // Every workgroup also writes S at the start of each chunk to `ckpt` when given (the
 // forward's state checkpoints, or the reverse sweep's dh per chunk), or, in the
 // interleaved layout, at the start of every even (forward) or odd (reverse) global chunk.
@@ -49,7 +56,7 @@ namespace tops {
 // GK: the per-channel gate mode only (kGateK, the GLA and KDA path), compiled on its own so
 // that the hot path carries no gate-mode branches; !GK serves the per-token and constant
 // gates (kGateS, kGateGamma, kGateGammaK) chosen at run time.
-template <typename TIn, int KP, bool REV, bool DELTA, bool ST, bool GK>
+template <typename TIn, int KP, bool REV, bool DELTA, bool ST, bool GK, bool GV = false>
 __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   constexpr int NW = 8;                  // wave64s per workgroup
   constexpr int NTH = 64 * NW;
@@ -66,7 +73,9 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   constexpr bool SIN = !In<TIn>::kExactBf16;
   constexpr bool FWD_DELTA = DELTA && !REV;
   constexpr bool REV_DELTA = DELTA && REV;
-  constexpr bool SY = SIN || FWD_DELTA;  // the Y plane carries a lo half (fp32 Y, or v_new)
+  constexpr bool SY = SIN || FWD_DELTA || GV;  // the Y plane carries a lo half (fp32 Y, v_new, v~)
+  constexpr bool XL = !GV;               // the X / Z planes carry a lo half (gated q / k)
+  static_assert(!GV || (!REV && !DELTA && !ST && !GK && !SIN), "GV: the bf16 forward sweep only");
   constexpr int LQ = KP + 8, LT = C + 8, LH = KP + 8;
   constexpr int NHT = (KP / 16) * (BV / 16) / NW;  // state tiles per wave (4, 2, 1), one K block
   constexpr int ES = sizeof(TIn);
@@ -75,28 +84,33 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   static_assert(YR == 4, "Y staging assumes 4 rows x 2 columns per thread");
   typedef Words<TIn> Wd;
 
-  __shared__ __attribute__((aligned(16))) uint16_t sX[2 * C * LQ];
-  __shared__ __attribute__((aligned(16))) uint16_t sZ[2 * C * LQ];
-  __shared__ __attribute__((aligned(16))) uint16_t sZT[2 * KP * LT];
+  __shared__ __attribute__((aligned(16))) uint16_t sX[(XL ? 2 : 1) * C * LQ];
+  __shared__ __attribute__((aligned(16))) uint16_t sZ[(XL ? 2 : 1) * C * LQ];
+  __shared__ __attribute__((aligned(16))) uint16_t sZT[(XL ? 2 : 1) * KP * LT];
   __shared__ __attribute__((aligned(16))) uint16_t sYT[(SY ? 2 : 1) * BV * LT];
   // (the reverse delta rule reuses sHT for the [BV][LT] dv_new^T plane: size for both)
   constexpr int NHTS = 2 * BV * (REV_DELTA && LT > LH ? LT : LH);
   __shared__ __attribute__((aligned(16))) uint16_t sHT[NHTS];
   __shared__ __attribute__((aligned(16))) float sTot[NSGH * KP]; // gate totals per segment group
+  // GV: the output factors 2^(G - Gm) [C][BV + 4] and the gate totals of the 16-row groups
+  constexpr int LE = BV + 4;
+  __shared__ __attribute__((aligned(16))) float sE[GV ? C * LE : 1];
+  __shared__ __attribute__((aligned(16))) float sGvTot[GV ? 4 * BV : 1];
   // Causal D tiles of the chunk shared through LDS (bf16 hi/lo per lane, 10 tiles x 1 KB):
   // each tile is computed once instead of once per column-tile wave, and the work is spread
   // evenly over the waves.  Only where the 160 KB budget allows (not the delta sweeps).
-  constexpr int LDS_BASE = 2 * (2 * C * LQ) * 2 + 2 * KP * LT * 2 + (SY ? 2 : 1) * BV * LT * 2 +
-                           NHTS * 2 + NSGH * KP * 4;
+  constexpr int LDS_BASE = 2 * ((XL ? 2 : 1) * C * LQ) * 2 + (XL ? 2 : 1) * KP * LT * 2 +
+                           (SY ? 2 : 1) * BV * LT * 2 + NHTS * 2 + NSGH * KP * 4 +
+                           (GV ? (C * LE + 4 * BV) * 4 : 0);
   constexpr bool SHARED_D = !DELTA && !ST && LDS_BASE + 10 * 64 * 16 <= 160 * 1024;
   __shared__ __attribute__((aligned(16))) uint4 sDt[SHARED_D ? 10 * 64 : 1];
   // Gamma / 2 of channel c sits in the padding columns of the X hi plane (row c / 4, word c % 4):
   // no MFMA fragment or staging write touches columns >= KP
   auto gm_at = [&](int c4) { return (float*)(sX + (c4 >> 2) * LQ + KP); };
 
-  const Plane PX{sX, sX + C * LQ, LQ};
-  const Plane PZ{sZ, sZ + C * LQ, LQ};
-  const Plane PZt{sZT, sZT + KP * LT, LT};
+  const Plane PX{sX, XL ? sX + C * LQ : sX, LQ};
+  const Plane PZ{sZ, XL ? sZ + C * LQ : sZ, LQ};
+  const Plane PZt{sZT, XL ? sZT + KP * LT : sZT, LT};
   const Plane PYt{sYT, SY ? sYT + BV * LT : sYT, LT};
   const Plane PHt{sHT, sHT + BV * LH, LH};
   // reverse delta rule: once the output pass is done, w^T [K][C] reuses sZT and
@@ -166,13 +180,14 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   const uint32_t offQ = colok ? ((uint32_t)r0 * rowK + c0) * ES : kOOB;        // q, k
   const uint32_t offG = colok ? ((uint32_t)r0 * rowK + c0) * 4u : kOOB;        // g, w
   const uint32_t offY = ycolok ? ((uint32_t)(yseg * YR) * rowV + yv) * ES : kOOB;
+  const uint32_t offYg = ycolok ? ((uint32_t)(yseg * YR) * rowV + yv) * 4u : kOOB;   // GV gates
   // gate load: per-channel [.., K] float4, or the per-(token, head) scalar read as the first
   // word of a 16-byte load; the gamma mode loads nothing (out of range -> 0)
-  const int gmode = GK ? kGateK : p.gate_mode;
+  const int gmode = GK ? kGateK : (GV ? kGateGamma : p.gate_mode);   // GV: no K-side gate
   const bool gk_mode = GK || gmode == kGateK;
   const uint32_t offGm = gk_mode ? offG : (gmode == kGateS ? (uint32_t)r0 * H * 4u : kOOB);
   const uint32_t gstride = gk_mode ? rowK * 4 : (uint32_t)H * 4;
-  const float gam_h = gmode == kGateGamma ? p.g[hh] : 0.f;
+  const float gam_h = gmode == kGateGamma && !GV ? p.g[hh] : 0.f;
   // constant per-(head, channel) gate: the four channels c0..c0+3 of this thread
   float gam4[4] = {gam_h, gam_h, gam_h, gam_h};
   if (gmode == kGateGammaK) {
@@ -230,6 +245,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     typename Wd::W4 rq[RPT], rk[RPT];
     uint4 rg[RPT];
     typename Wd::W2 ry[YR];
+    uint2 rgv[GV ? YR : 1];              // GV: the gates of the two Y columns
   };
   Raw rsA, rsB;
   auto load_chunk = [&](int c, Raw& rs) {
@@ -251,7 +267,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       // the gate mode's transform is applied when the chunk is consumed, so the prefetch
       // never waits: four channels [.., K], or the one per-(token, head) word [.., 1]
       // (gamma: offGm is out of range, nothing is read)
-      uint32_t go = ok ? offGm : kOOB, gs = i * gstride;
+      uint32_t go = (ok && !GV) ? offGm : kOOB, gs = i * gstride;
       if constexpr (RSH) {
         // row r0 + i - gadj (>= 0 where read), as one vector offset; masked columns and the
         // constant gates (offGm out of range) read nothing
@@ -259,7 +275,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
         go = rd ? offGm + (uint32_t)(i - gadj) * gstride : kOOB;
         gs = 0;
       }
-      if constexpr (GK) rs.rg[i] = bld128(Rg, go, gs);
+      if constexpr (GV) rs.rg[i] = make_uint4(0u, 0u, 0u, 0u);
+      else if constexpr (GK) rs.rg[i] = bld128(Rg, go, gs);
       else if (gk_mode) rs.rg[i] = bld128(Rg, go, gs);
       else rs.rg[i] = make_uint4(bld32(Rg, go, gs), 0u, 0u, 0u);
     }
@@ -269,6 +286,14 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       for (int i = 0; i < YR; ++i) {
         const bool ok = yseg * YR + i < nval;
         rs.ry[i] = Wd::ld2(Ry, ok ? offY : kOOB, i * rowV * ES);
+      }
+      if constexpr (GV) {
+        const rsrc_t Rgv = make_rsrc_rows(p.g, e0, nrows, V);
+#pragma unroll
+        for (int i = 0; i < YR; ++i) {
+          const bool ok = yseg * YR + i < nval;
+          rs.rgv[i] = bld64(Rgv, ok ? offYg : kOOB, i * rowV * 4);
+        }
       }
     }
   };
@@ -332,6 +357,35 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     // ---------------- gate cumsum: thread rows, a shuffle scan over the half-wave's row
     // segments, then segment-group totals through LDS
     float G[RPT][4];
+    float pre[4], gam[4];
+    // GV: the value-side gate cumsum of this thread's two Y columns (rows yseg*YR..+3), the
+    // prefix of the earlier row groups of its half-wave, and (after B1) of the earlier groups
+    float gvc[YR][2], prev[2] = {0.f, 0.f};
+    if constexpr (GV) {
+#pragma unroll
+      for (int i = 0; i < RPT; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) G[i][j] = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pre[j] = gam[j] = 0.f;
+#pragma unroll
+      for (int i = 0; i < YR; ++i) {
+        gvc[i][0] = __uint_as_float(rs.rgv[i].x) * kLog2e + (i > 0 ? gvc[i - 1][0] : 0.f);
+        gvc[i][1] = __uint_as_float(rs.rgv[i].y) * kLog2e + (i > 0 ? gvc[i - 1][1] : 0.f);
+      }
+#pragma unroll
+      for (int c2 = 0; c2 < 2; ++c2) {
+        const float t = gvc[YR - 1][c2];
+        float x = t;
+#pragma unroll
+        for (int d = 8; d < 32; d <<= 1) {
+          const float y = __shfl_up(x, d, 64);
+          if ((lane & 31) >= d) x += y;
+        }
+        prev[c2] = x - t;
+        if (((lane >> 3) & 3) == 3) sGvTot[(hw >> 2) * BV + 2 * yc + c2] = x;
+      }
+    } else {
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
       float x[4];
@@ -348,7 +402,6 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) G[i][j] = x[j] * kLog2e + (i > 0 ? G[i - 1][j] : 0.f);
     }
-    float pre[4], gam[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float t = G[RPT - 1][j];
@@ -362,8 +415,10 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       gam[j] = x;                        // inclusive; the last segment holds the group total
     }
     if (sgl == SGL - 1) *(float4*)(sTot + sgh * KP + c0) = make_float4(gam[0], gam[1], gam[2], gam[3]);
+    }  // !GV
     __syncthreads();  // B1: totals visible; every wave is done with the previous chunk's planes
 
+    if constexpr (!GV) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) gam[j] = 0.f;
 #pragma unroll
@@ -371,6 +426,32 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       const float4 t = *(const float4*)(sTot + s2 * KP + c0);
       if (s2 < sgh) { pre[0] += t.x; pre[1] += t.y; pre[2] += t.z; pre[3] += t.w; }
       gam[0] += t.x; gam[1] += t.y; gam[2] += t.z; gam[3] += t.w;
+    }
+    }
+    // GV: Gm of the thread's Y columns (and the prefix of its rows), and per state tile the
+    // column factors 2^Gamma, 2^(Gamma - Gm), scale 2^Gm of the lane's column 16 nn + l16
+    float gmv[2] = {0.f, 0.f};
+    float cga[NHT], cbe[NHT], cal[NHT];
+    if constexpr (GV) {
+#pragma unroll
+      for (int c2 = 0; c2 < 2; ++c2) {
+        float tot = 0.f;
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) {
+          const float t = sGvTot[s2 * BV + 2 * yc + c2];
+          if (s2 < (hw >> 2)) prev[c2] += t;
+          tot += t;
+        }
+        gmv[c2] = 0.5f * tot;
+      }
+#pragma unroll
+      for (int i = 0; i < NHT; ++i) {
+        const int col = 16 * ((wave * NHT + i) % (BV / 16)) + l16;
+        const float tot = sGvTot[col] + sGvTot[BV + col] + sGvTot[2 * BV + col] + sGvTot[3 * BV + col];
+        cga[i] = fast_exp2(tot);
+        cbe[i] = fast_exp2(0.5f * tot);
+        cal[i] = scale * cbe[i];
+      }
     }
     float gm[4];
 #pragma unroll
@@ -381,7 +462,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     // Gamma of this lane's state rows kr = 16 msb + 4 lg + r
     float sgam[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s2 = 0; s2 < NSGH; ++s2) {
+    for (int s2 = 0; s2 < (GV ? 0 : NSGH); ++s2) {
       const float4 t = *(const float4*)(sTot + s2 * KP + 16 * msb + 4 * lg);
       sgam[0] += t.x; sgam[1] += t.y; sgam[2] += t.z; sgam[3] += t.w;
     }
@@ -405,7 +486,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
         const int kr = 16 * msb + 4 * lg;
         float x[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) x[r] = sal[r] * S[i][r];
+        for (int r = 0; r < 4; ++r) x[r] = (GV ? cal[i] : sal[r]) * S[i][r];
         put_n<true, 4>(PHt, 16 * nn + l16, kr, x);
       }
     }
@@ -441,18 +522,23 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
         unpack4(rs.rk[i], kv);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float Gv = G[i][j] + pre[j];
-          xq[j] = (FWD_DELTA ? scale : 1.f) * qv[j] * fast_exp2(Gv - gm[j]);
-          xk[j] = kv[j] * fast_exp2(gm[j] - Gv);
+          if constexpr (GV) {
+            xq[j] = qv[j];
+            xk[j] = kv[j];
+          } else {
+            const float Gv = G[i][j] + pre[j];
+            xq[j] = (FWD_DELTA ? scale : 1.f) * qv[j] * fast_exp2(Gv - gm[j]);
+            xk[j] = kv[j] * fast_exp2(gm[j] - Gv);
+          }
         }
         const float* xx = REV ? xk : xq;
         const float* zz = REV ? xq : xk;
-        if constexpr (!ST) put_n<true, 4>(PX, r0 + i, c0, xx);
+        if constexpr (!ST) put_n<XL, 4>(PX, r0 + i, c0, xx);
         split_bf16x2(zz[0], zz[1], zh[i][0], zl[i][0]);
         split_bf16x2(zz[2], zz[3], zh[i][1], zl[i][1]);
         if constexpr (!ST) {
           *(uint2*)(PZ.hi + (r0 + i) * PZ.ld + c0) = make_uint2(zh[i][0], zh[i][1]);
-          *(uint2*)(PZ.lo + (r0 + i) * PZ.ld + c0) = make_uint2(zl[i][0], zl[i][1]);
+          if constexpr (XL) *(uint2*)(PZ.lo + (r0 + i) * PZ.ld + c0) = make_uint2(zl[i][0], zl[i][1]);
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) zt[j][i] = zz[j];
@@ -472,20 +558,30 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
           uint16_t* pl = PZt.lo + (c0 + j) * PZt.ld + r0;
           if constexpr (RPT == 4) {
             *(uint2*)ph = make_uint2(th[0], th[1]);
-            *(uint2*)pl = make_uint2(tl[0], tl[1]);
+            if constexpr (XL) *(uint2*)pl = make_uint2(tl[0], tl[1]);
           } else {
             *(uint32_t*)ph = th[0];
-            *(uint32_t*)pl = tl[0];
+            if constexpr (XL) *(uint32_t*)pl = tl[0];
           }
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) put_n<true, RPT>(PZt, c0 + j, r0, zt[j]);
+        for (int j = 0; j < 4; ++j) put_n<XL, RPT>(PZt, c0 + j, r0, zt[j]);
       }
       if constexpr (!FWD_DELTA) {
         float ya[YR], yb[YR];
 #pragma unroll
         for (int i = 0; i < YR; ++i) unpack2(rs.ry[i], ya[i], yb[i]);
+        if constexpr (GV) {
+          // v~ = v 2^(Gm - G) into the Y plane; the output factor 2^(G - Gm) into sE
+#pragma unroll
+          for (int i = 0; i < YR; ++i) {
+            const float ga = gvc[i][0] + prev[0] - gmv[0], gb = gvc[i][1] + prev[1] - gmv[1];
+            ya[i] *= fast_exp2(-ga);
+            yb[i] *= fast_exp2(-gb);
+            *(float2*)(sE + (yseg * YR + i) * LE + 2 * yc) = make_float2(fast_exp2(ga), fast_exp2(gb));
+          }
+        }
         put_n<SY, YR>(PYt, 2 * yc, yseg * YR, ya);
         put_n<SY, YR>(PYt, 2 * yc + 1, yseg * YR, yb);
       }
@@ -523,7 +619,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 #pragma unroll
         for (int kc = 0; kc < C / 32; ++kc) {
           zh[kc] = PZt.hi8(16 * msb + l16, 32 * kc + 8 * lg);
-          zl[kc] = PZt.lo8(16 * msb + l16, 32 * kc + 8 * lg);
+          if constexpr (XL) zl[kc] = PZt.lo8(16 * msb + l16, 32 * kc + 8 * lg);
 #pragma unroll
           for (int i = 0; i < NHT; ++i) {
             const int nn = (wave * NHT + i) % (BV / 16);
@@ -535,8 +631,10 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
         for (int i = 0; i < NHT; ++i) dsu[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kc = 0; kc < C / 32; ++kc) {
+          if constexpr (XL) {
 #pragma unroll
-          for (int i = 0; i < NHT; ++i) dsu[i] = mfma(zl[kc], yh[i][kc], dsu[i]);
+            for (int i = 0; i < NHT; ++i) dsu[i] = mfma(zl[kc], yh[i][kc], dsu[i]);
+          }
           if constexpr (SY) {
 #pragma unroll
             for (int i = 0; i < NHT; ++i) dsu[i] = mfma(zh[kc], yl[i][kc], dsu[i]);
@@ -560,8 +658,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
             const bf16x8 bh = PYt.hi8(16 * nn + l16, 32 * kc + 8 * lg);
             bf16x8 bl = bh;
             if constexpr (SY) bl = PYt.lo8(16 * nn + l16, 32 * kc + 8 * lg);
-            d = mma<true, SY>(d, PZt.hi8(16 * msb + l16, 32 * kc + 8 * lg),
-                              PZt.lo8(16 * msb + l16, 32 * kc + 8 * lg), bh, bl);
+            d = mma<XL, SY>(d, PZt.hi8(16 * msb + l16, 32 * kc + 8 * lg),
+                            PZt.lo8(16 * msb + l16, 32 * kc + 8 * lg), bh, bl);
           }
         } else {
           d = dsu[i];
@@ -569,6 +667,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           if constexpr (REV_DELTA) S[i][r] = sga[r] * S[i][r] + sbe[r] * d1[i][r] - d[r];
+          else if constexpr (GV) S[i][r] = cga[i] * S[i][r] + cbe[i] * d[r];
           else S[i][r] = sga[r] * S[i][r] + sbe[r] * d[r];
         }
       }
@@ -583,7 +682,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 #pragma unroll
       for (int kc = 0; kc < KP / 32; ++kc) {
         xh[kc] = PX.hi8(16 * R + l16, 32 * kc + 8 * lg);
-        xl[kc] = PX.lo8(16 * R + l16, 32 * kc + 8 * lg);
+        xl[kc] = xh[kc];
+        if constexpr (XL) xl[kc] = PX.lo8(16 * R + l16, 32 * kc + 8 * lg);
       }
     };
     if constexpr (!SHARED_D) load_x();
@@ -601,17 +701,21 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       bf16x8 fz[2][2], fx[2][2];
       auto ld = [&](int kc, int b) {
         fz[b][0] = PZ.hi8(16 * Pt + l16, 32 * kc + 8 * lg);
-        fz[b][1] = PZ.lo8(16 * Pt + l16, 32 * kc + 8 * lg);
         fx[b][0] = PX.hi8(16 * Rt + l16, 32 * kc + 8 * lg);
-        fx[b][1] = PX.lo8(16 * Rt + l16, 32 * kc + 8 * lg);
+        if constexpr (XL) {
+          fz[b][1] = PZ.lo8(16 * Pt + l16, 32 * kc + 8 * lg);
+          fx[b][1] = PX.lo8(16 * Rt + l16, 32 * kc + 8 * lg);
+        }
       };
       ld(0, 0);
 #pragma unroll
       for (int kc = 0; kc < KP / 32; ++kc) {
         const int b = kc & 1;
         if (kc + 1 < KP / 32) ld(kc + 1, b ^ 1);
-        a0 = mfma(fz[b][1], fx[b][0], a0);
-        a1 = mfma(fz[b][0], fx[b][1], a1);
+        if constexpr (XL) {
+          a0 = mfma(fz[b][1], fx[b][0], a0);
+          a1 = mfma(fz[b][0], fx[b][1], a1);
+        }
         a2 = mfma(fz[b][0], fx[b][0], a2);
       }
       f32x4 acc;
@@ -673,8 +777,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
         f32x4 t = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kc = 0; kc < KP / 32; ++kc)
-          t = mma<true, true>(t, PZ.hi8(16 * P + l16, 32 * kc + 8 * lg),
-                              PZ.lo8(16 * P + l16, 32 * kc + 8 * lg), xh[kc], xl[kc]);
+          t = mma<XL, XL>(t, PZ.hi8(16 * P + l16, 32 * kc + 8 * lg),
+                          PZ.lo8(16 * P + l16, 32 * kc + 8 * lg), xh[kc], xl[kc]);
         const int rr = 16 * R + l16;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -803,8 +907,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kc = 0; kc < KP / 32; ++kc)
-          acc = mma<true, true>(acc, PHt.hi8(16 * nn + l16, 32 * kc + 8 * lg),
-                                PHt.lo8(16 * nn + l16, 32 * kc + 8 * lg), xh[kc], xl[kc]);
+          acc = mma<true, XL>(acc, PHt.hi8(16 * nn + l16, 32 * kc + 8 * lg),
+                              PHt.lo8(16 * nn + l16, 32 * kc + 8 * lg), xh[kc], xl[kc]);
         // out^T += Y^T D  (contraction over p, two 16-blocks per MFMA)
 #pragma unroll
         for (int Pp = 0; Pp < 2; ++Pp) {
@@ -820,6 +924,10 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
         if constexpr (RSH) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[r] *= p.oscale;
+        }
+        if constexpr (GV) {
+          const float4 e4 = *(const float4*)(sE + tok * LE + 16 * nn + 4 * lg);
+          acc[0] *= e4.x; acc[1] *= e4.y; acc[2] *= e4.z; acc[3] *= e4.w;
         }
         const int v0 = vt * BV + 16 * nn + 4 * lg;
         Wd::st4(Ro, acc, v0 < V ? oo : kOOB, (uint32_t)(16 * nn * ES));
@@ -885,6 +993,18 @@ hipError_t launch_gla_sweep(const SweepParams& p, hipStream_t s) {
     else TOPS_SWEEP(128, false);
   }
 #undef TOPS_SWEEP
+  return hipGetLastError();
+}
+
+hipError_t launch_gla_sweep_gv(const SweepParams& p, hipStream_t s) {
+  const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
+  dim3 grid(p.NV * p.H * p.N);
+#define TOPS_SWEEP_GV(KPV) \
+  hipLaunchKernelGGL((gla_sweep_kernel<uint16_t, KPV, false, false, false, false, true>), grid, dim3(512), 0, s, p)
+  if (kp == 32) TOPS_SWEEP_GV(32);
+  else if (kp == 64) TOPS_SWEEP_GV(64);
+  else TOPS_SWEEP_GV(128);
+#undef TOPS_SWEEP_GV
   return hipGetLastError();
 }
 
@@ -1025,6 +1145,28 @@ extern "C" int tops_chunk_reverse_fwd(const void* q, const void* k, const void* 
   if (dtype == TOPS_BF16) e = launch_gla_sweep<uint16_t, true>(p, s);
   else if (dtype == TOPS_F32) e = launch_gla_sweep<float, true>(p, s);
   else return tops_set_error(TOPS_ERR_DTYPE, "chunk_reverse_fwd: dtype must be TOPS_F32 or TOPS_BF16");
+  if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
+  return TOPS_OK;
+}
+
+extern "C" int tops_gla_chunk_fwd_gv(const void* q, const void* k, const void* v, const float* gv,
+                                     const float* h0, void* o, float* ht,
+                                     const int32_t* cu_seqlens, int B, int T, int H, int K, int V,
+                                     int N, int dtype, float scale, void* stream) {
+  if (!q || !k || !v || !gv || !o) return tops_set_error(TOPS_ERR_NULL, "gla_chunk_fwd_gv: null tensor");
+  if (dtype != TOPS_BF16)
+    return tops_set_error(TOPS_ERR_DTYPE, "gla_chunk_fwd_gv: the value-gate sweep takes TOPS_BF16");
+  if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || N <= 0)
+    return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd_gv: non-positive dimension");
+  if (K > 128 || (K % 8) || (V % 8))
+    return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd_gv: need K <= 128, K % 8 == 0, V % 8 == 0");
+  if (cu_seqlens && B != 1) return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd_gv: varlen needs B == 1");
+  if (!cu_seqlens && N != B) return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd_gv: N must equal B");
+  if ((long long)kChunk * H * (K > V ? K : V) * 4 >= (1LL << 31))
+    return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd_gv: H * max(K, V) too large for 32-bit chunk offsets");
+  SweepParams p{q, k, gv, v, h0, o, ht, nullptr, cu_seqlens, nullptr,
+                B, T, H, K, V, N, (V + 63) / 64, scale, kGateGamma};
+  hipError_t e = launch_gla_sweep_gv(p, (hipStream_t)stream);
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   return TOPS_OK;
 }

@@ -18,8 +18,11 @@ cu_seqlens.  Two HIP implementations of the same recurrence are used:
     the forward recurrence on every sequence's time-reversed inputs: the inputs are reversed
     per sequence, swept forward, and the output reversed back (the reversal is part of the
     autograd graph);
-  * with gv, the per-token kernels of gla_recurrent.hip (state in registers, one token at
-    a time) run the forward, a replay + reverse backward and the gate-gradient suffix sums.
+  * with gv and without gk, a forward that needs no gradient (bf16, K <= 128) runs chunkwise
+    on the forward sweep with the gate applied per V column (tops_gla_chunk_fwd_gv);
+  * otherwise with gv, the per-token kernels of gla_recurrent.hip (state in registers, one
+    token at a time) run the forward, a replay + reverse backward and the gate-gradient
+    suffix sums.
 """
 from __future__ import annotations
 
@@ -198,6 +201,31 @@ def reverse_chunk_native(q, k, v, mode, g, initial_state, scale, output_final_st
     return o, ht
 
 
+def gv_chunk_native(q, k, v, gv, initial_state, scale, output_final_state, cu_seqlens):
+    """The value-gated forward (gv, no gk) on the chunk sweep (tops_gla_chunk_fwd_gv), for
+    calls that need no gradient.  Returns (o, ht or None), or None where it does not apply:
+    gradients wanted, inputs other than bf16, K > 128 or K, V not multiples of 8, or a call
+    whose sequences the chunk kernels would split into sequence-parallel segments."""
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad
+                                       for t in (q, k, v, gv, initial_state)):
+        return None
+    if q.dtype != torch.bfloat16 or K > 128 or K % 8 or V % 8:
+        return None
+    plan = ChunkPlan(B, T, cu_seqlens, q.device)
+    if plan.segments(H, V) is not None:
+        return None
+    q, k, v = (x.contiguous() for x in (q, k, v))
+    o = torch.empty_like(v)
+    ht = torch.empty(plan.N, H, K, V, device=q.device, dtype=torch.float32) \
+        if output_final_state else None
+    N.call("tops_gla_chunk_fwd_gv", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(_f32(gv)),
+           N.ptr(_f32(initial_state)), N.ptr(o), N.ptr(ht), N.ptr(plan.cu_dev), B, T, H, K, V,
+           plan.N, N.dtype_code(q.dtype), float(scale), N.stream())
+    return o, ht
+
+
 def _reversed_chunk(fn, q, k, v, g, cu_seqlens, **kw):
     """fn (a chunk op) on the time-reversed sequences; returns (o in original order, ht)."""
     rev = time_reversal(q.shape[1], cu_seqlens, q.device)
@@ -218,6 +246,10 @@ def fused_recurrent_gla(q, k, v, gk=None, gv=None, scale=None, initial_state=Non
         r = reverse_chunk_native(q, k, v, "k" if gk is not None else "gamma",
                                  gk if gk is not None else torch.zeros(H, device=q.device),
                                  initial_state, scale, output_final_state, cu_seqlens)
+        if r is not None:
+            return r
+    if gv is not None and gk is None and not reverse:
+        r = gv_chunk_native(q, k, v, gv, initial_state, scale, output_final_state, cu_seqlens)
         if r is not None:
             return r
     if wide and not _chunked(gv, reverse, K, V):
@@ -251,6 +283,10 @@ def fused_recurrent_gla_fwd(q, k, v, gk=None, gv=None, scale=None, initial_state
         r = reverse_chunk_native(q, k, v, "k" if gk is not None else "gamma",
                                  gk if gk is not None else torch.zeros(H, device=q.device),
                                  initial_state, scale, output_final_state, cu_seqlens)
+        if r is not None:
+            return r
+    if gv is not None and gk is None and not reverse:
+        r = gv_chunk_native(q, k, v, gv, initial_state, scale, output_final_state, cu_seqlens)
         if r is not None:
             return r
     o, _, ht = _fwd(q.contiguous(), k.contiguous(), v.contiguous(), _f32(gk), _f32(gv),

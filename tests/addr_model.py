@@ -69,13 +69,14 @@ def _kp(K):
 # --------------------------------------------------------------------------- gla_sweep_kernel
 def sweep(ck: Checker, p: dict, es: int, rev: bool, delta: bool = False, st: bool = False,
           gate_width_bytes: int = 4, unguarded_prefetch: bool = False, gshift: bool = False,
-          planted_shift: bool = False):
+          planted_shift: bool = False, gv: bool = False):
     """gla_sweep_kernel<TIn, KP, REV, DELTA, ST> (csrc/gla_sweep.hip).  p holds the SweepParams
     fields: B, T, H, K, V, N, cu (host array or None), seg_end, offsets, gate_mode and which of
     s0 / s_fin / ckpt / y32 / dec_fin / u / w are bound (tensor names in ck.sizes).  gshift:
     the reverse sweep reads the gate one token later (tops_chunk_reverse_fwd); planted_shift
     moves the gate rows one token earlier in the sequence's first chunk too (the mistake the
-    first-chunk case exists for)."""
+    first-chunk case exists for).  gv: the value-gate forward (tops_gla_chunk_fwd_gv): g is
+    [B,T,H,V], read as two columns per Y row, and the K-side gate reads nothing."""
     B, T, H, K, V, N = (p[x] for x in ("B", "T", "H", "K", "V", "N"))
     KP = _kp(K)
     NTH, BV = 512, 64
@@ -112,6 +113,7 @@ def sweep(ck: Checker, p: dict, es: int, rev: bool, delta: bool = False, st: boo
     offQ = np.where(colok, (r0 * rowK + c0) * es, KOOB)
     offG = np.where(colok, (r0 * rowK + c0) * 4, KOOB)
     offY = np.where(yv < V, ((yseg * YR) * rowV + yv) * es, KOOB)
+    offYg = np.where(yv < V, ((yseg * YR) * rowV + yv) * 4, KOOB)
     if gm == 0:
         offGm, gstride, gw, gname_w = offG, rowK * 4, 16, K
     elif gm == 1:
@@ -187,7 +189,7 @@ def sweep(ck: Checker, p: dict, es: int, rev: bool, delta: bool = False, st: boo
                     ck.acc(p["g"], eg * gname_w * 4,
                            np.where(rd, offGm + (i - gadj) * gstride, KOOB), 0, gw,
                            f"sweep load shifted g (mode {gm}) chunk {c}")
-                elif gw:
+                elif gw and not gv:
                     ck.acc(p["g"], e0 * gname_w * 4, np.where(ok, offGm, KOOB), i * gstride, gw,
                            f"sweep load g (mode {gm}) chunk {c}")
             if not fwd_delta:
@@ -195,6 +197,12 @@ def sweep(ck: Checker, p: dict, es: int, rev: bool, delta: bool = False, st: boo
                     ok = yseg * YR + i < nval
                     ck.acc(p["y"], e0 * V * es, np.where(ok, offY, KOOB), i * rowV * es, 2 * es,
                            f"sweep load y chunk {c}")
+            if gv:
+                ck.rows_rsrc(p["g"], e0, nrows, V, 4)
+                for i in range(YR):
+                    ok = yseg * YR + i < nval
+                    ck.acc(p["g"], e0 * V * 4, np.where(ok, offYg, KOOB), i * rowV * 4, 8,
+                           f"sweep load gv chunk {c}")
             if fwd_delta:
                 trow = 16 * R + l16
                 for kc in range(KP // 32):

@@ -266,3 +266,32 @@ def test_planted_reverse_first_chunk_shift_is_caught():
         reverse_op(1, 100, 2, 32, 32, 4, gate_mode=0, planted_shift=True)
     with pytest.raises(M.OOBError, match="g"):
         reverse_op(1, 100, 2, 32, 32, 4, gate_mode=1, planted_shift=True)
+
+
+def gv_op(B, T, H, K, V, cu=None, h0=True):
+    """The launch of tops_gla_chunk_fwd_gv (fused_recurrent_gla with gv, no gk, no gradients):
+    the bf16 forward sweep with g = gv [B,T,H,V], no checkpoints."""
+    plan = U.ChunkPlan(B, T, cu, "cpu")
+    N, es = plan.N, 2
+    sizes = dict(q=B * T * H * K * es, k=B * T * H * K * es, v=B * T * H * V * es,
+                 o=B * T * H * V * es, g=B * T * H * V * 4, h0=N * H * K * V * 4,
+                 ht=N * H * K * V * 4)
+    ck = M.Checker(sizes)
+    p = dict(B=B, T=T, H=H, K=K, V=V, N=N, cu=plan.cu_host if plan.varlen else None, offsets=None,
+             gate_mode=2, g="g", q="q", k="k", y="v", out="o", s0="h0" if h0 else None,
+             s_fin="ht")
+    M.sweep(ck, p, es, rev=False, gv=True)
+    return ck
+
+
+# test_gpu_gv_native.py's launches
+GV = [dict(B=2, T=64, H=2, K=32, V=32), dict(B=2, T=50, H=2, K=64, V=64),
+      dict(B=1, T=1, H=2, K=32, V=64), dict(B=2, T=200, H=3, K=16, V=40),
+      dict(B=1, T=150, H=2, K=32, V=32, cu=[0, 13, 13, 64, 65, 150]),
+      dict(B=2, T=256, H=2, K=128, V=128), dict(B=1, T=70, H=1, K=128, V=200),
+      dict(B=1, T=100, H=2, K=24, V=72)]
+
+
+@pytest.mark.parametrize("c", GV, ids=lambda c: "B{B}-T{T}-H{H}-K{K}-V{V}".format(**c))
+def test_gv_native_in_bounds(c):
+    assert gv_op(c["B"], c["T"], c["H"], c["K"], c["V"], cu=c.get("cu")).count > 0
