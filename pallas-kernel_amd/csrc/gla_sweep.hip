@@ -33,12 +33,16 @@
 // H^T = 2^Gm S); reverse, the state update gains - w^T dv_new, and dv_new is written
 // transposed per chunk for the WY backward.
 //
-// GV (forward, bf16): the gate sits on the value side, one log-gate per (token, V column)
-// (fused_recurrent_gla's gv), S[:, v] <- 2^gv S[:, v] + k v^T.  q and k enter ungated (exact
-// bf16: the X / Z planes carry no lo half), v~ = v 2^(Gm - G) per column is split into hi /
-// lo, every output element is multiplied by 2^(G - Gm) of its (token, column) from an fp32
-// LDS plane, and S decays per column: o^T = (2^Gm S)^T q^T + v~^T M, S = 2^Gamma S +
-// 2^(Gamma-Gm) (k^T v~), M[i][j] = scale q_i.k_j (j <= i).
+// YG (bf16): the gate is applied on the value side.  YG = 1 (forward): one log-gate per
+// (token, V column) (fused_recurrent_gla's gv), S[:, v] <- 2^gv S[:, v] + k v^T.  YG = 2
+// (forward and reverse): one log-gate per token (simple GLA's g [B,T,H], or g_gamma [H]),
+// which factors out of every q.k product: D[i][j] = 2^(G_i - G_j) (q_i.k_j).  Either way q and
+// k enter ungated (exact bf16: the X / Z planes carry no lo half), Y~ = Y 2^(s(Gm - G)) is
+// split into hi / lo (s = 1 forward, -1 reverse), every output element is multiplied by
+// 2^(s(G - Gm)) of its (token, column) from an fp32 LDS plane, and S decays per column:
+//   forward:  o^T = (scale 2^Gm S)^T q^T + v~^T M,  S = 2^Gamma S + 2^(Gamma-Gm) (k^T v~)
+//   reverse:  dv^T = (2^(Gamma-Gm) S)^T k^T + dO~^T M,  S = 2^Gamma S + scale 2^Gm (q^T dO~)
+// with M[i][j] = scale q_i.k_j on the causal side.
 //
 // Every workgroup also writes S at the start of each chunk to `ckpt` when given (the
 // forward's state checkpoints, or the reverse sweep's dh per chunk), or, in the
@@ -47,6 +51,8 @@
 // Pipelining: the raw q/k/g/Y of chunk c+1 are loaded into registers while chunk c is
 // computed; a full chunk takes a branch-free path (masked rows read out of range and are
 // zeroed by the buffer range check).  Two barriers per chunk (three or four with DELTA).
+#include <type_traits>
+
 #include "gla_sweep.h"
 #include "tops_common.h"
 #include "tops_hip.h"
@@ -56,7 +62,7 @@ namespace tops {
 // GK: the per-channel gate mode only (kGateK, the GLA and KDA path), compiled on its own so
 // that the hot path carries no gate-mode branches; !GK serves the per-token and constant
 // gates (kGateS, kGateGamma, kGateGammaK) chosen at run time.
-template <typename TIn, int KP, bool REV, bool DELTA, bool ST, bool GK, bool GV = false>
+template <typename TIn, int KP, bool REV, bool DELTA, bool ST, bool GK, int YG = 0>
 __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   constexpr int NW = 8;                  // wave64s per workgroup
   constexpr int NTH = 64 * NW;
@@ -73,9 +79,11 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   constexpr bool SIN = !In<TIn>::kExactBf16;
   constexpr bool FWD_DELTA = DELTA && !REV;
   constexpr bool REV_DELTA = DELTA && REV;
-  constexpr bool SY = SIN || FWD_DELTA || GV;  // the Y plane carries a lo half (fp32 Y, v_new, v~)
+  constexpr bool GV = YG != 0;           // value-side gate (either form)
+  constexpr bool SY = SIN || FWD_DELTA || GV;  // the Y plane carries a lo half (fp32 Y, v_new, Y~)
   constexpr bool XL = !GV;               // the X / Z planes carry a lo half (gated q / k)
-  static_assert(!GV || (!REV && !DELTA && !ST && !GK && !SIN), "GV: the bf16 forward sweep only");
+  static_assert(!GV || (!DELTA && !ST && !GK && !SIN), "YG: the bf16 full sweeps only");
+  static_assert(YG != 1 || !REV, "YG = 1: forward only");
   constexpr int LQ = KP + 8, LT = C + 8, LH = KP + 8;
   constexpr int NHT = (KP / 16) * (BV / 16) / NW;  // state tiles per wave (4, 2, 1), one K block
   constexpr int ES = sizeof(TIn);
@@ -183,7 +191,10 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   const uint32_t offYg = ycolok ? ((uint32_t)(yseg * YR) * rowV + yv) * 4u : kOOB;   // GV gates
   // gate load: per-channel [.., K] float4, or the per-(token, head) scalar read as the first
   // word of a 16-byte load; the gamma mode loads nothing (out of range -> 0)
-  const int gmode = GK ? kGateK : (GV ? kGateGamma : p.gate_mode);   // GV: no K-side gate
+  const int gmode = GK ? kGateK : (GV ? kGateGamma : p.gate_mode);   // YG: no K-side gate
+  // YG = 2: the value-side gate is per token, g [B,T,H] (kGateS) or the constant g_gamma [H]
+  const bool yg_s = YG == 2 && p.gate_mode == kGateS;
+  const float yg_gam = (YG == 2 && p.gate_mode == kGateGamma) ? p.g[hh] : 0.f;
   const bool gk_mode = GK || gmode == kGateK;
   const uint32_t offGm = gk_mode ? offG : (gmode == kGateS ? (uint32_t)r0 * H * 4u : kOOB);
   const uint32_t gstride = gk_mode ? rowK * 4 : (uint32_t)H * 4;
@@ -245,7 +256,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     typename Wd::W4 rq[RPT], rk[RPT];
     uint4 rg[RPT];
     typename Wd::W2 ry[YR];
-    uint2 rgv[GV ? YR : 1];              // GV: the gates of the two Y columns
+    uint2 rgv[GV ? YR : 1];              // YG: the gates of the two Y columns
   };
   Raw rsA, rsB;
   auto load_chunk = [&](int c, Raw& rs) {
@@ -287,12 +298,21 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
         const bool ok = yseg * YR + i < nval;
         rs.ry[i] = Wd::ld2(Ry, ok ? offY : kOOB, i * rowV * ES);
       }
-      if constexpr (GV) {
+      if constexpr (YG == 1) {
         const rsrc_t Rgv = make_rsrc_rows(p.g, e0, nrows, V);
 #pragma unroll
         for (int i = 0; i < YR; ++i) {
           const bool ok = yseg * YR + i < nval;
           rs.rgv[i] = bld64(Rgv, ok ? offYg : kOOB, i * rowV * 4);
+        }
+      } else if constexpr (YG == 2) {
+        // one word per row (the constant gate reads nothing: out of range)
+        const rsrc_t Rgs = make_rsrc_rows(p.g, e0, nrows, 1);
+#pragma unroll
+        for (int i = 0; i < YR; ++i) {
+          const bool ok = yseg * YR + i < nval && yg_s;
+          const uint32_t w = bld32(Rgs, ok ? (uint32_t)(yseg * YR) * H * 4u : kOOB, i * H * 4);
+          rs.rgv[i] = make_uint2(w, w);
         }
       }
     }
@@ -370,8 +390,10 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       for (int j = 0; j < 4; ++j) pre[j] = gam[j] = 0.f;
 #pragma unroll
       for (int i = 0; i < YR; ++i) {
-        gvc[i][0] = __uint_as_float(rs.rgv[i].x) * kLog2e + (i > 0 ? gvc[i - 1][0] : 0.f);
-        gvc[i][1] = __uint_as_float(rs.rgv[i].y) * kLog2e + (i > 0 ? gvc[i - 1][1] : 0.f);
+        float a = __uint_as_float(rs.rgv[i].x), b = __uint_as_float(rs.rgv[i].y);
+        if (YG == 2 && !yg_s) a = b = yseg * YR + i < nval ? yg_gam : 0.f;
+        gvc[i][0] = a * kLog2e + (i > 0 ? gvc[i - 1][0] : 0.f);
+        gvc[i][1] = b * kLog2e + (i > 0 ? gvc[i - 1][1] : 0.f);
       }
 #pragma unroll
       for (int c2 = 0; c2 < 2; ++c2) {
@@ -428,8 +450,9 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       gam[0] += t.x; gam[1] += t.y; gam[2] += t.z; gam[3] += t.w;
     }
     }
-    // GV: Gm of the thread's Y columns (and the prefix of its rows), and per state tile the
-    // column factors 2^Gamma, 2^(Gamma - Gm), scale 2^Gm of the lane's column 16 nn + l16
+    // YG: Gm of the thread's Y columns (and the prefix of its rows), and per state tile the
+    // factors of the lane's column 16 nn + l16: 2^Gamma (decay), the update scaling and alpha
+    // (forward 2^(Gamma - Gm) and scale 2^Gm, reverse scale 2^Gm and 2^(Gamma - Gm))
     float gmv[2] = {0.f, 0.f};
     float cga[NHT], cbe[NHT], cal[NHT];
     if constexpr (GV) {
@@ -449,8 +472,9 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
         const int col = 16 * ((wave * NHT + i) % (BV / 16)) + l16;
         const float tot = sGvTot[col] + sGvTot[BV + col] + sGvTot[2 * BV + col] + sGvTot[3 * BV + col];
         cga[i] = fast_exp2(tot);
-        cbe[i] = fast_exp2(0.5f * tot);
-        cal[i] = scale * cbe[i];
+        const float hf = fast_exp2(0.5f * tot);
+        cbe[i] = REV ? scale * hf : hf;
+        cal[i] = REV ? hf : scale * hf;
       }
     }
     float gm[4];
@@ -573,10 +597,11 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 #pragma unroll
         for (int i = 0; i < YR; ++i) unpack2(rs.ry[i], ya[i], yb[i]);
         if constexpr (GV) {
-          // v~ = v 2^(Gm - G) into the Y plane; the output factor 2^(G - Gm) into sE
+          // Y~ = Y 2^(s(Gm - G)) into the Y plane; the output factor 2^(s(G - Gm)) into sE
 #pragma unroll
           for (int i = 0; i < YR; ++i) {
-            const float ga = gvc[i][0] + prev[0] - gmv[0], gb = gvc[i][1] + prev[1] - gmv[1];
+            float ga = gvc[i][0] + prev[0] - gmv[0], gb = gvc[i][1] + prev[1] - gmv[1];
+            if constexpr (REV) { ga = -ga; gb = -gb; }
             ya[i] *= fast_exp2(-ga);
             yb[i] *= fast_exp2(-gb);
             *(float2*)(sE + (yseg * YR + i) * LE + 2 * yc) = make_float2(fast_exp2(ga), fast_exp2(gb));
@@ -987,6 +1012,17 @@ hipError_t launch_gla_sweep(const SweepParams& p, hipStream_t s) {
     if (kp == 32) TOPS_SWEEP(32, true);
     else if (kp == 64) TOPS_SWEEP(64, true);
     else TOPS_SWEEP(128, true);
+  } else if (std::is_same<TIn, uint16_t>::value && !p.gshift &&
+             (p.gate_mode == kGateS || p.gate_mode == kGateGamma)) {
+    // one gate per token (bf16): on the value side, q and k stay exact
+#define TOPS_SWEEP_YG(KPV) \
+  hipLaunchKernelGGL((gla_sweep_kernel<uint16_t, KPV, REV, false, false, false, 2>), grid, dim3(512), 0, s, p)
+    if constexpr (std::is_same<TIn, uint16_t>::value && !DELTA) {
+      if (kp == 32) TOPS_SWEEP_YG(32);
+      else if (kp == 64) TOPS_SWEEP_YG(64);
+      else TOPS_SWEEP_YG(128);
+    }
+#undef TOPS_SWEEP_YG
   } else {
     if (kp == 32) TOPS_SWEEP(32, false);
     else if (kp == 64) TOPS_SWEEP(64, false);
@@ -1000,7 +1036,7 @@ hipError_t launch_gla_sweep_gv(const SweepParams& p, hipStream_t s) {
   const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
   dim3 grid(p.NV * p.H * p.N);
 #define TOPS_SWEEP_GV(KPV) \
-  hipLaunchKernelGGL((gla_sweep_kernel<uint16_t, KPV, false, false, false, false, true>), grid, dim3(512), 0, s, p)
+  hipLaunchKernelGGL((gla_sweep_kernel<uint16_t, KPV, false, false, false, false, 1>), grid, dim3(512), 0, s, p)
   if (kp == 32) TOPS_SWEEP_GV(32);
   else if (kp == 64) TOPS_SWEEP_GV(64);
   else TOPS_SWEEP_GV(128);
