@@ -24,6 +24,12 @@
 // cross-wave block total.  LDS holds the v / dO planes, the pass's gated q~^T / k~^T
 // planes and its fp32 gate cumsum: < 70 KB, so two workgroups share a CU.
 //
+// RG (bf16, one gate per token: simple GLA's g [B,T,H] or g_gamma [H]): the gate cumsum G_t
+// is the same for every channel, computed once per chunk, and 2^(G - Gm) factors out of q~
+// and k~ per token: the intra products take exact q / k planes (no lo half) against dA
+// tiles that carry the token factors (dA 2^(Gm - G_j) for dq, 2^(G_i - Gm) dA for dk), and
+// dq, dk take their token's factor in the epilogue.
+//
 // PAIR (bf16 inputs, interleaved checkpoints): one workgroup of 8 waves takes the chunk
 // pair (2i, 2i + 1), four waves per chunk, each half with its own LDS.  The buffer holds
 // h_(2i) and dh_(2i+1) only; the missing states come from the partner's planes on MFMA,
@@ -43,7 +49,7 @@ namespace tops {
 
 // GK: the per-channel gate mode only (kGateK: GLA and KDA), compiled without gate-mode
 // branches; !GK serves the per-token and constant gates chosen at run time.
-template <typename TIn, typename TV, int KP, int VP, bool GK, bool PAIR>
+template <typename TIn, typename TV, int KP, int VP, bool GK, bool PAIR, bool RG = false>
 __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParams p) {
   constexpr int C = kChunk;
   constexpr int NG = PAIR ? 2 : 1;             // chunks per workgroup
@@ -67,14 +73,16 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
   static_assert(NPTV >= 1 && C * NPCV % 256 == 0, "VP must be 32, 64 or 128");
   static_assert(KP % KH == 0, "KP must be 32, 64 or 128");
   static_assert(!PAIR || (!SIN && !SINV), "the paired layout takes bf16 inputs");
+  static_assert(!RG || (!GK && !PAIR && !SIN && !SINV), "RG: bf16, per-token gates, unpaired");
   typedef Words<TIn> Wd;
 
-  constexpr int ZV = NPLV * C * LV, ZD = NPL * C * LV, ZT = 2 * KH * LT;
+  constexpr int ZV = NPLV * C * LV, ZD = NPL * C * LV, ZT = (RG ? 1 : 2) * KH * LT;
   __shared__ __attribute__((aligned(16))) uint16_t sV[NG * ZV];
   __shared__ __attribute__((aligned(16))) uint16_t sD[NG * ZD];
   __shared__ __attribute__((aligned(16))) uint16_t sQT[NG * ZT];
   __shared__ __attribute__((aligned(16))) uint16_t sKT[NG * ZT];
-  __shared__ __attribute__((aligned(16))) float sG[NG * C * LG];     // gate cumsum of the pass
+  __shared__ __attribute__((aligned(16))) float sG[RG ? 1 : NG * C * LG];  // gate cumsum of the pass
+  __shared__ __attribute__((aligned(16))) float sRG[RG ? C : 1];          // RG: token gate cumsum
   __shared__ __attribute__((aligned(16))) float sTot[NG * 8 * KH];
   __shared__ __attribute__((aligned(16))) float sGm[NG * KH];
   __shared__ __attribute__((aligned(16))) float sGam[NG * KH];
@@ -104,9 +112,9 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
   constexpr int pg = PAIR ? 1 - grp : 0;
   const Plane Pv{sV + grp * ZV, SINV ? sV + grp * ZV + C * LV : sV + grp * ZV, LV};
   const Plane Pd{sD + grp * ZD, SIN ? sD + grp * ZD + C * LV : sD + grp * ZD, LV};
-  const Plane Pqt{sQT + grp * ZT, sQT + grp * ZT + KH * LT, LT};
-  const Plane Pkt{sKT + grp * ZT, sKT + grp * ZT + KH * LT, LT};
-  float* const gG = sG + grp * C * LG;
+  const Plane Pqt{sQT + grp * ZT, sQT + grp * ZT + (RG ? 0 : KH * LT), LT};
+  const Plane Pkt{sKT + grp * ZT, sKT + grp * ZT + (RG ? 0 : KH * LT), LT};
+  float* const gG = sG + (RG ? 0 : grp * C * LG);
   float* const gTot = sTot + grp * 8 * KH;
   float* const gGm = sGm + grp * KH;
   float* const gGam = sGam + grp * KH;
@@ -204,6 +212,22 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
     }
   }
 
+  // ---------------- RG: the token gate cumsum (log2 units) of the chunk, by the first wave
+  if constexpr (RG) {
+    if (tq < C) {
+      float x = 0.f;
+      if (gmode == kGateS) x = __uint_as_float(bld32(Rg, tq < nval ? (uint32_t)tq * H * 4u : kOOB, 0));
+      else x = tq < nval ? gam_h : 0.f;
+      x *= kLog2e;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const float y = __shfl_up(x, d, 64);
+        if (lane >= d) x += y;
+      }
+      sRG[tq] = x;
+    }
+  }
+
   // ---------------- staging of a pass: thread = (channel ch, 8-row segment sg)
   const int ch = tq & 31, sg = tq >> 5;
   // raw words of the next pass's rows: fp32 elements, or (bf16) the aligned 32-bit word
@@ -220,7 +244,8 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
   // gate element (row r, channel kc): per-channel [.., K], per-token [.., 1], or none (gamma)
   const bool gk_mode = GK || gmode == kGateK;
   const uint32_t gstr = gk_mode ? rowK * 4u : (uint32_t)H * 4u;
-  const bool gload = GK || gmode == kGateK || gmode == kGateS;   // the constant gates load nothing
+  const bool gload = !RG && (GK || gmode == kGateK || gmode == kGateS);   // the constant gates
+                                                                         // (and RG) load nothing
   auto load_pass = [&](int ps) {
     const int kc = ps * KH + ch;
     const bool ok = kc < K;
@@ -238,7 +263,8 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
         rk[i] = bld32(Rk, v_ ? (off & ~1u) * 2u : kOOB, 0);
       }
       // one unconditional load whatever the gate mode (gamma loads nothing: out of range)
-      rg[i] = __uint_as_float(bld32(Rg, (v_ && gload) ? (uint32_t)r * gstr + gcol : kOOB, 0));
+      if constexpr (RG) rg[i] = 0.f;
+      else rg[i] = __uint_as_float(bld32(Rg, (v_ && gload) ? (uint32_t)r * gstr + gcol : kOOB, 0));
     }
   };
   load_pass(0);
@@ -246,7 +272,9 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
   // ---------------- dA tiles (registers, all passes)
   // dth[a][J] (row block B = 2rh + a, J <= B): lane holds dA[16B + l16][16J + 4lg + r]
   // dah[a][I] (col block B = 2rh + a, I >= B): lane holds dA[16I + 4lg + r][16B + l16]
-  __syncthreads();  // v / dO planes visible
+  __syncthreads();  // v / dO planes (and the RG token cumsum) visible
+  // RG: Gamma and Gm of the chunk (rows past the sequence add nothing)
+  const float rgam = RG ? sRG[C - 1] : 0.f, rgm = 0.5f * rgam;
   uint2 dthh[2][4], dthl[2][4], dahh[2][4], dahl[2][4];
 #pragma unroll
   for (int a = 0; a < 2; ++a) {
@@ -268,6 +296,10 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
         const int i = 16 * B2 + l16;
 #pragma unroll
         for (int r = 0; r < 4; ++r) t[r] = (16 * J + 4 * lg + r <= i) ? t[r] * scale : 0.f;
+        if constexpr (RG) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) t[r] *= fast_exp2(rgm - sRG[16 * J + 4 * lg + r]);
+        }
         acc_to_bf16x4(t, dthh[a][J], dthl[a][J]);
       }
       if (J >= B2) {
@@ -284,6 +316,10 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
         const int j = 16 * B2 + l16;
 #pragma unroll
         for (int r = 0; r < 4; ++r) t[r] = (j <= 16 * J + 4 * lg + r) ? t[r] * scale : 0.f;
+        if constexpr (RG) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) t[r] *= fast_exp2(sRG[16 * J + 4 * lg + r] - rgm);
+        }
         acc_to_bf16x4(t, dahh[a][J], dahl[a][J]);
       }
     }
@@ -349,6 +385,17 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
     uint4 kadd[2], gadd[2];
     // ---- gate cumsum of the pass (thread: channel ch, rows 8sg..8sg+7); the constant gates
     // (g_gamma [H] or [H, K]) give every valid row the same value
+    if constexpr (RG) {
+      // exact q / k planes (hi only); the token factors live in the dA tiles and the epilogue
+      float qt[8], kt[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        qt[i] = elem(rq[i]);
+        kt[i] = elem(rk[i]);
+      }
+      put_n<false, 8>(Pqt, ch, 8 * sg, qt);
+      put_n<false, 8>(Pkt, ch, 8 * sg, kt);
+    } else {
     float gconst = gam_h;
     if constexpr (!GK) {
       if (gmode == kGateGammaK) gconst = gck[ps];
@@ -390,6 +437,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
       put_n<true, 8>(Pqt, ch, 8 * sg, qt);
       put_n<true, 8>(Pkt, ch, 8 * sg, kt);
     }
+    }  // !RG
     // the next pass's q / k / g rows (PAIR: after the state rebuild, which needs the registers)
     if (!PAIR && ps + 1 < NPS) load_pass(ps + 1);
     // this pass's dh rows, in flight across the barrier
@@ -441,8 +489,8 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
     }
 
     // ---- inter-chunk: X^T += (alpha h) dO^T, W^T += (beta dh) v^T
-    const float al = scale * fast_exp2(gGm[kl]);
-    const float be = fast_exp2(gGam[kl] - gGm[kl]);
+    const float al = scale * fast_exp2(RG ? rgm : gGm[kl]);
+    const float be = fast_exp2(RG ? rgam - rgm : gGam[kl] - gGm[kl]);
     f32x4 X[2], Wt[2];
     X[0] = X[1] = Wt[0] = Wt[1] = f32x4{0.f, 0.f, 0.f, 0.f};
     float hd = 0.f;
@@ -500,10 +548,12 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
         const int j = 16 * (2 * rh + a) + l16;
+        const float fk = RG ? fast_exp2(rgm - sRG[j]) : 1.f;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int cr = 16 * kb + 4 * lg + r;
-          const float kv = bf16_to_f32(Pkt.hi[cr * LT + j]) + bf16_to_f32(Pkt.lo[cr * LT + j]);
+          const float kv = RG ? bf16_to_f32(Pkt.hi[cr * LT + j]) * fk
+                              : bf16_to_f32(Pkt.hi[cr * LT + j]) + bf16_to_f32(Pkt.lo[cr * LT + j]);
           z[r] += kv * Wt[a][r];
         }
       }
@@ -530,12 +580,12 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
       for (int Pp = 0; Pp < 2; ++Pp) {
         const int P0 = 2 * Pp, P1 = 2 * Pp + 1;
         if (P0 <= B2) {
-          X[a] = mma<true, true>(X[a], Pkt.hi44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
+          X[a] = mma<!RG, true>(X[a], Pkt.hi44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
                                  Pkt.lo44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
                                  cat44(dthh[a][P0], dthh[a][P1]), cat44(dthl[a][P0], dthl[a][P1]));
         }
         if (P1 >= B2) {
-          Wt[a] = mma<true, true>(Wt[a], Pqt.hi44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
+          Wt[a] = mma<!RG, true>(Wt[a], Pqt.hi44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
                                   Pqt.lo44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
                                   cat44(dahh[a][P0], dahh[a][P1]), cat44(dahl[a][P0], dahl[a][P1]));
         }
@@ -546,16 +596,24 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
     const int cl = 16 * kb + 4 * lg;       // first channel of the lane (in pass)
     const int kc = cb + cl;
     const bool chok = kc < K;
-    const float4 gm4 = *(const float4*)(gGm + cl);
-    const float gmr[4] = {gm4.x, gm4.y, gm4.z, gm4.w};
+    float gmr[4] = {rgm, rgm, rgm, rgm};
+    if constexpr (!RG) {
+      const float4 gm4 = *(const float4*)(gGm + cl);
+      gmr[0] = gm4.x; gmr[1] = gm4.y; gmr[2] = gm4.z; gmr[3] = gm4.w;
+    }
     float dgr[2][4];
 #pragma unroll
     for (int a = 0; a < 2; ++a) {
       const int tok = 16 * (2 * rh + a) + l16;
       const bool ok = chok && tok < nval;
       const uint32_t off = (uint32_t)tok * rowK + kc;
-      const float4 g4 = *(const float4*)(gG + tok * LG + cl);
-      const float gr[4] = {g4.x, g4.y, g4.z, g4.w};
+      float gr[4];
+      if constexpr (RG) {
+        gr[0] = gr[1] = gr[2] = gr[3] = sRG[tok];
+      } else {
+        const float4 g4 = *(const float4*)(gG + tok * LG + cl);
+        gr[0] = g4.x; gr[1] = g4.y; gr[2] = g4.z; gr[3] = g4.w;
+      }
       // fp32 inputs re-read q, k (exact); bf16 inputs use q dq - k dk = q~ X - k~ W with
       // q~ / k~ read back from the pass planes (hi + lo: 2^-17 relative, far below bf16)
       float qv[4], kv[4];
@@ -572,9 +630,14 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
           dgr[a][r] = qv[r] * dqv[r] - kv[r] * dkv[r];
         } else {
           const int pi = (cl + r) * LT + tok;
-          const float qt = bf16_to_f32(Pqt.hi[pi]) + bf16_to_f32(Pqt.lo[pi]);
-          const float kt = bf16_to_f32(Pkt.hi[pi]) + bf16_to_f32(Pkt.lo[pi]);
-          dgr[a][r] = qt * X[a][r] - kt * Wt[a][r];
+          if constexpr (RG) {
+            // q dq - k dk with exact q, k
+            dgr[a][r] = bf16_to_f32(Pqt.hi[pi]) * dqv[r] - bf16_to_f32(Pkt.hi[pi]) * dkv[r];
+          } else {
+            const float qt = bf16_to_f32(Pqt.hi[pi]) + bf16_to_f32(Pqt.lo[pi]);
+            const float kt = bf16_to_f32(Pkt.hi[pi]) + bf16_to_f32(Pkt.lo[pi]);
+            dgr[a][r] = qt * X[a][r] - kt * Wt[a][r];
+          }
         }
       }
       if (kEarlyAdd || p.dk_add) {
@@ -609,7 +672,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
     float add[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      add[r] = fast_exp2(gGam[cl + r]) * gHdh[cl + r] + gZk[cl + r] + gZk[KH + cl + r];
+      add[r] = fast_exp2(RG ? rgam : gGam[cl + r]) * gHdh[cl + r] + gZk[cl + r] + gZk[KH + cl + r];
       if (rh == 0) add[r] += gBlk[cl + r];
     }
     if (GK || gmode == kGateK || (gmode == kGateGammaK && p.dg)) {
@@ -673,6 +736,12 @@ hipError_t launch_gla_dqkg(const DqkgParams& p, hipStream_t s) {
       if (p.paired) {                                                                         \
         if (gk) hipLaunchKernelGGL((gla_dqkg_kernel<TIn, TV, KPV, VPV, true, true>), pgrid, pblock, 0, s, p); \
         else hipLaunchKernelGGL((gla_dqkg_kernel<TIn, TV, KPV, VPV, false, true>), pgrid, pblock, 0, s, p); \
+        return hipGetLastError();                                                             \
+      }                                                                                       \
+    }                                                                                         \
+    if constexpr (kPairs) {                                                                   \
+      if (!gk && (p.gate_mode == kGateS || p.gate_mode == kGateGamma)) {                      \
+        hipLaunchKernelGGL((gla_dqkg_kernel<TIn, TV, KPV, VPV, false, false, true>), grid, block, 0, s, p); \
         return hipGetLastError();                                                             \
       }                                                                                       \
     }                                                                                         \

@@ -96,7 +96,10 @@ def test_paired_matches_unpaired(cfg, gate, cuda_device):
     for a, b in ((dq1, dq2), (dk1, dk2)):
         assert rel(host(b), host(a)) < 2e-3
     if dg1 is not None:
-        assert rel(host(dg2), host(dg1)) < 1e-5
+        # per-channel gates: the same arithmetic but for the rebuilt states (1e-5); one gate
+        # per token: the unpaired kernel factors the gate out of q / k (exact planes, factors
+        # in the dA tiles) while the paired one gates the planes, two fp32 formulations (1e-4)
+        assert rel(host(dg2), host(dg1)) < (1e-5 if gate in ("k", "gamma_k") else 1e-4)
 
 
 @pytest.mark.parametrize("cfg", CASES, ids=[_id(c) for c in CASES])
