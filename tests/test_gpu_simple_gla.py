@@ -39,7 +39,7 @@ def _run(cfg, dtype, device):
     cu = cfg.get("cu")
     n = len(cu) - 1 if cu else B
     d = simple_gla_inputs(B, T, H, K, V, seed=T + 7 * K + H, h0=cfg.get("h0", False), N=n,
-                          grads=True)
+                          grads=True, gate_div=cfg.get("gate_div", 1.0))
     q, k, v = (to_dev(d[x], dtype, device).requires_grad_() for x in "qkv")
     g = to_dev(d["g"], torch.float32, device).requires_grad_() if cfg["gate"] == "g" else None
     gg = to_dev(d["g_gamma"], torch.float32, device) if cfg["gate"] == "gamma" else None
@@ -63,6 +63,25 @@ def _run(cfg, dtype, device):
                dg=None if g is None else g.grad, dh0=None if h0 is None else h0.grad)
     ref = dict(o=ro, ht=rht, dq=rq, dk=rk, dv=rv, dg=rg, dh0=None if h0 is None else rh0)
     return got, ref
+
+
+STRONG = [dict(B=1, T=300, H=2, K=64, V=64, gate="g", h0=True, gate_div=0.5, cu=[0, 13, 140, 141, 300]),
+          dict(B=2, T=192, H=2, K=128, V=128, gate="g", h0=True, gate_div=0.5)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("cfg", STRONG, ids=[_id(c) for c in STRONG])
+def test_strong_gates(cfg, dtype, cuda_device):
+    """Per-token gates twice config 4's (mean about -1.6 per token, a chunk's cumsum about
+    -100): the value-side gate factors reach 2^±73 (bf16) and stay finite; every output and
+    gradient within the tolerance."""
+    got, ref = _run(cfg, dtype, cuda_device)
+    for n, r in ref.items():
+        if r is None:
+            continue
+        assert torch.isfinite(got[n]).all(), n
+        e = rel(host(got[n]), r)
+        assert e < tol(dtype), (n, e)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
