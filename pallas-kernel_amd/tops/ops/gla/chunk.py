@@ -23,7 +23,7 @@ from __future__ import annotations
 import torch
 
 from ...utils import ChunkPlan, cdiv
-from .._chunk_core import (GATE_K, GATE_GAMMA_K, PAIRED, check_qkv, paired_states, chunk_fwd as _core_fwd,
+from .._chunk_core import (GATE_K, GATE_GAMMA, GATE_GAMMA_K, PAIRED, check_qkv, paired_states, chunk_fwd as _core_fwd,
                            chunk_bwd as _core_bwd, states_for_bwd, states_full)
 
 
@@ -108,6 +108,12 @@ def chunk_gla(
     assert chunk_size > 0, "chunk_size must be positive"
     K = q.shape[-1]
     mode, gt = _gate(q, g, g_gamma)
+    if mode == GATE_GAMMA_K and not gt.requires_grad and (g_gamma is None or
+                                                          torch.as_tensor(g_gamma).dim() == 0 or
+                                                          torch.as_tensor(g_gamma).shape[-1] == 1):
+        # no gate, or a constant shared by the K channels, and no gradient for it: the
+        # one-decay-per-head mode (whose bf16 kernels keep q and k exact)
+        mode, gt = GATE_GAMMA, gt[:, 0].contiguous()
     _check(q, k, v, initial_state, cu_seqlens)
     if scale is None:
         scale = K ** -0.5

@@ -195,3 +195,40 @@ def test_chunk_gla_constant_gates(form, cuda_device):
         want = want.sum() if gam.ndim == 0 else want.sum(axis=tuple(i for i in range(4) if gam.shape[i] == 1 and want.shape[i] != 1), keepdims=True)
         assert gg.grad.shape == gg.shape
         assert rel(host(gg.grad).reshape(-1), np.asarray(want).reshape(-1)) < 1e-4
+
+
+@pytest.mark.parametrize("form", ["none", "scalar", "head"])
+def test_chunk_gla_constant_gate_per_head_bf16(form, cuda_device, monkeypatch):
+    """bf16 chunk_gla with no gate, or a g_gamma shared by the K channels that needs no
+    gradient, runs the one-decay-per-head mode (the value-side gate kernels: q and k stay
+    exact): o, ht and dq, dk, dv, dh0 against the oracle on the broadcast gate."""
+    from tops import _native as N
+    from tops.ops.gla import chunk_gla
+    names = []
+    real = N.call
+    monkeypatch.setattr(N, "call", lambda name, *a: (names.append(name), real(name, *a))[1])
+    B, T, H, K, V = 1, 300, 2, 64, 64
+    cu = [0, 13, 140, 141, 300]
+    d = gla_inputs(B, T, H, K, V, 47, h0=True, N=len(cu) - 1, grads=True)
+    rng = np.random.default_rng(48)
+    shape = {"none": None, "scalar": (), "head": (1, 1, H, 1)}[form]
+    gam = None if shape is None else (-np.abs(rng.standard_normal(shape)) * 0.3).astype(np.float32)
+    bf = torch.bfloat16
+    q, k, v = (to_dev(d[x], bf, cuda_device).requires_grad_() for x in "qkv")
+    h0 = to_dev(d["h0"], torch.float32, cuda_device).requires_grad_()
+    gg = None if gam is None else torch.tensor(gam, device=cuda_device)
+    o, ht = chunk_gla(q, k, v, g_gamma=gg, initial_state=h0, output_final_state=True, cu_seqlens=cu)
+    torch.autograd.backward((o, ht), (to_dev(d["do"], bf, cuda_device),
+                                      to_dev(d["dht"], torch.float32, cuda_device)))
+    torch.cuda.synchronize()
+    assert "tops_simple_gla_chunk_fwd" in names and "tops_gla_chunk_fwd_gamma" not in names
+    gfull = np.zeros((B, T, H, K), np.float32) if gam is None else \
+        np.broadcast_to(gam, (B, T, H, K)).astype(np.float32)
+    sq, sk, sv, sdo = (seen(d[x], bf) for x in ("q", "k", "v", "do"))
+    ro, rht = O.chunk_gla(sq, sk, sv, gfull, initial_state=d["h0"], output_final_state=True,
+                          cu_seqlens=cu)
+    rq, rk, rv, _, rh0 = O.chunk_gla_bwd(sq, sk, sv, gfull, K ** -0.5, d["h0"], sdo, d["dht"],
+                                         cu_seqlens=cu)
+    for name, a, b in (("o", o, ro), ("ht", ht, rht), ("dq", q.grad, rq), ("dk", k.grad, rk),
+                       ("dv", v.grad, rv), ("dh0", h0.grad, rh0)):
+        assert rel(host(a), b) < 2e-3, name
