@@ -338,7 +338,9 @@ int tops_kda_chunk_fwd_noalloc(const void* q, const void* k, const void* v, cons
  * from the tensors saved by tops_kda_chunk_fwd (w, tt, v_new, h_ckpt).
  *   do [B,T,H,V] (dtype); dht [N,H,K,V] or NULL.
  *   Workspace (fp32, written): dh_work [total,H,K,V] (dS per chunk),
- *   dvn_work [total,H,V,64] (dv_new transposed per chunk), dk_work, dg_work [B,T,H,K].
+ *   dvn_work [total,H,V,64] (dv_new transposed per chunk), dk_work, dg_work [B,T,H,K]
+ *   (fp32 inputs only; bf16 runs the WY and dq / dk / dg stages as one kernel that keeps
+ *   those parts on chip, and dk_work / dg_work may be NULL).
  *   Outputs: dq, dk [B,T,H,K] and dv [B,T,H,V] (dtype); dbeta [B,T,H], dg [B,T,H,K]
  *   (w.r.t. the natural-log gates) fp32; dh0 [N,H,K,V] fp32 or NULL. */
 int tops_kda_chunk_bwd(const void* q, const void* k, const void* v, const float* g,

@@ -46,4 +46,32 @@ struct KdaWyParams {
 template <typename TIn>
 hipError_t launch_kda_wy(const KdaWyParams& p, hipStream_t s);
 
+// The bf16 backward's WY stage and dq / dk / dg in one kernel (kda_bwd_fused.hip): one
+// 8-wave workgroup per (chunk, head).
+struct KdaBwdParams {
+  const void* q;
+  const void* k;
+  const void* v;           // the layer's v (bf16), for dbeta
+  const float* g;          // [B,T,H,K] natural-log gates
+  const float* beta;       // [B,T,H]
+  const float* tt;         // [total,H,C,C]  T transposed
+  const float* dvnt;       // [total,H,V,C]  dv_new transposed per chunk
+  const float* vnew;       // [B,T,H,V]
+  const float* hs;         // [total,H,K,V]  state before each chunk
+  const float* dhs;        // [total,H,K,V]  gradient w.r.t. the state after each chunk
+  const void* dout;        // dO [B,T,H,V]
+  void* dq;
+  void* dk;
+  void* dv;
+  float* dbeta;            // [B,T,H]
+  float* dg;               // [B,T,H,K]
+  const int* cu_seqlens;
+  const int* chunk_offsets;
+  const int* chunk_map;
+  int total, B, T, H, K, V, N;
+  float scale;
+};
+
+hipError_t launch_kda_bwd_fused(const KdaBwdParams& p, hipStream_t s);
+
 }  // namespace tops

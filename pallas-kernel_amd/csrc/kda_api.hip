@@ -6,9 +6,10 @@
 // (tops/ops/kda/chunk.py:25-190).
 //
 // Backward (tops_kda_chunk_bwd): the reverse delta-rule sweep (dv_new, dS per chunk,
-// dh0), the WY backward (kda_wy.hip: dv, dbeta and the WY parts of dk, dg), then the
-// GLA-shaped dq / dk / dg kernel (gla_dqkg.hip with v := v_new) which adds the WY parts,
-// replacing chunk_kda_bwd (tops/ops/kda/chunk_bwd.py:655-832).
+// dh0), then for bf16 inputs one kernel for the WY backward and the GLA-shaped dq / dk /
+// dg (kda_bwd_fused.hip); for fp32 inputs the WY backward (kda_wy.hip: dv, dbeta and the WY
+// parts of dk, dg) followed by the dq / dk / dg kernel (gla_dqkg.hip with v := v_new) which
+// adds them, replacing chunk_kda_bwd (tops/ops/kda/chunk_bwd.py:655-832).
 #include <stdio.h>
 
 #include <mutex>
@@ -93,8 +94,11 @@ extern "C" int tops_kda_chunk_bwd(const void* q, const void* k, const void* v, c
                                   int total_chunks, int B, int T, int H, int K, int V, int N,
                                   int dtype, float scale, void* stream) {
   if (!q || !k || !v || !g || !beta || !w || !tt || !v_new || !h_ckpt || !do_ || !dh_work ||
-      !dvn_work || !dk_work || !dg_work || !dq || !dk || !dv || !dbeta || !dg)
+      !dvn_work || !dq || !dk || !dv || !dbeta || !dg)
     return tops_set_error(TOPS_ERR_NULL, "kda_chunk_bwd: null tensor");
+  // bf16: the WY stage and dq / dk / dg run as one kernel and need no dk / dg workspace
+  if (dtype != TOPS_BF16 && (!dk_work || !dg_work))
+    return tops_set_error(TOPS_ERR_NULL, "kda_chunk_bwd: fp32 inputs need dk_work and dg_work");
   int rc = kda_check("kda_chunk_bwd", B, T, H, K, V, N, total_chunks, cu_seqlens, chunk_offsets,
                      chunk_map, dtype);
   if (rc != TOPS_OK) return rc;
@@ -105,6 +109,14 @@ extern "C" int tops_kda_chunk_bwd(const void* q, const void* k, const void* v, c
                  B, T, H, K, V, N, (V + 63) / 64, scale, kGateK, nullptr, w, dvn_work};
   hipError_t e = bf ? launch_gla_sweep<uint16_t, true, true>(sp, s) : launch_gla_sweep<float, true, true>(sp, s);
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
+  if (bf) {
+    // 2+3. the WY backward and dq, dk, dg in one kernel (the WY parts through LDS)
+    KdaBwdParams fp{q, k, v, g, beta, tt, dvn_work, v_new, h_ckpt, dh_work, do_, dq, dk, dv, dbeta, dg,
+                    cu_seqlens, chunk_offsets, chunk_map, total_chunks, B, T, H, K, V, N, scale};
+    e = launch_kda_bwd_fused(fp, s);
+    if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
+    return TOPS_OK;
+  }
   // 2. WY backward: dv, dbeta, dk_wy, dg_wy
   KdaWyParams wp{k, v, g, beta, tt, dvn_work, v_new, h_ckpt, dv, dbeta, dk_work, dg_work,
                  cu_seqlens, chunk_offsets, chunk_map, total_chunks, B, T, H, K, V, N};

@@ -69,8 +69,10 @@ def _bwd(q, k, v, g32, b32, do, dht, saved, scale, plan: ChunkPlan, want_dh0: bo
     dh0 = torch.empty(plan.N, H, K, V, device=dev, dtype=f32) if want_dh0 else None
     dh_work = torch.empty_like(hs)
     dvn_work = torch.empty(plan.total, H, V, CHUNK, device=dev, dtype=f32)
-    dk_work = torch.empty(B, T, H, K, device=dev, dtype=f32)
-    dg_work = torch.empty(B, T, H, K, device=dev, dtype=f32)
+    # bf16 keeps the WY parts of dk / dg on chip (one kernel); fp32 passes them through HBM
+    split = q.dtype == torch.float32
+    dk_work = torch.empty(B, T, H, K, device=dev, dtype=f32) if split else None
+    dg_work = torch.empty(B, T, H, K, device=dev, dtype=f32) if split else None
     N.call("tops_kda_chunk_bwd", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(g32), N.ptr(b32), N.ptr(w),
            N.ptr(tt), N.ptr(vn), N.ptr(hs), N.ptr(do), N.ptr(dht), N.ptr(dh_work), N.ptr(dvn_work),
            N.ptr(dk_work), N.ptr(dg_work), N.ptr(dq), N.ptr(dk), N.ptr(dv), N.ptr(dbeta), N.ptr(dg),

@@ -420,8 +420,12 @@ def kda_prep(ck: Checker, p: dict, es: int):
                 ck.acc(p["tt"], (gc * H + hh) * C * C * 4, (i * C + j0) * 4, 0, 16, "prep store T^T")
 
 
-def kda_wy(ck: Checker, p: dict, es: int):
-    """kda_wy_kernel<TIn, KP, VP> (csrc/kda_wy.hip)."""
+def kda_wy(ck: Checker, p: dict, es: int, fused: bool = False):
+    """kda_wy_kernel<TIn, KP, VP> (csrc/kda_wy.hip).  fused: the WY group of
+    kda_bwd_fused_kernel (csrc/kda_bwd_fused.hip, bf16): v_new comes from the dq/dk/dg group's
+    plane, the epilogue reads k as 4 channels of one token, and the WY parts of dk / dg stay
+    in LDS (its other accesses are those of gla_dqkg_kernel<bf16, fp32 v> without dk_add /
+    dg_add)."""
     H, K, V = p["H"], p["K"], p["V"]
     KP, VP = _kp(K), _kp(V)
     NPS, VC, NVB = KP // 32, VP // 32, VP // 16
@@ -454,7 +458,7 @@ def kda_wy(ck: Checker, p: dict, es: int):
                 if kc == 1 or I < 2:
                     ck.acc(p["tt"], blk * C * C * 4, ((16 * I + l16) * C + 32 * kc + 8 * lg) * 4, 0, 32,
                            "wy load T^T")
-        for a in range(2):
+        for a in range(2 if not fused else 0):
             j = 16 * (2 * tp + a) + l16
             for vc in range(VC):
                 v0 = 32 * vc + 8 * lg
@@ -477,6 +481,14 @@ def kda_wy(ck: Checker, p: dict, es: int):
                 else:
                     ck.acc(p["k"], e0 * K * 2, np.where(ok, (off & ~1) * 2, KOOB), 0, 4, "wy load k")
                 ck.acc(p["g"], e0 * K * 4, np.where(ok, off * 4, KOOB), 0, 4, "wy load g")
+            if fused:
+                for a in range(2):
+                    tok = 16 * (2 * tp + a) + l16
+                    kq = cb + 16 * kb + 4 * lg
+                    ok = (kq < K) & (tok < nval)
+                    ck.acc(p["k"], e0 * K * 2, np.where(ok, (tok * rowK + kq) * 2, KOOB), 0, 8,
+                           "fused wy load k (epilogue)")
+                continue
             for a in range(2):
                 t = 2 * tp + a
                 for r in range(4):

@@ -97,12 +97,14 @@ def kda_op(B, T, H, K, V, es, cu=None, h0=True):
     M.sweep(ck, dict(sw, u="u", y32="vnew", out="o", ckpt="hs", s0="h0" if h0 else None, s_fin="ht"),
             es, rev=False, delta=True)
     M.sweep(ck, dict(sw, y="do", y32="dvnt", ckpt="dhs", s0="dht", s_fin="dh0"), es, rev=True, delta=True)
+    # bf16: the WY backward and dq / dk / dg run as one kernel (kda_bwd_fused.hip)
+    fused = es == 2
     M.kda_wy(ck, dict(vl, H=H, K=K, V=V, B=B, T=T, total=tot, k="k", g="g", v="v", beta="beta",
                       tt="tt", dvnt="dvnt", vnew="vnew", hs="hs", dv="dv", dbeta="dbeta",
-                      dk_wy="dk_wy", dg_wy="dg_wy"), es)
+                      dk_wy="dk_wy", dg_wy="dg_wy"), es, fused=fused)
     M.dqkg(ck, dict(vl, B=B, T=T, H=H, K=K, V=V, total=tot, gate_mode=0, q="q", k="k", v="vnew",
                     g="g", do="do", hs="hs", dhs="dhs", dq="dq", dk="dk", dg="dg",
-                    dk_add="dk_wy", dg_add="dg_wy"), es, 4)
+                    dk_add=None if fused else "dk_wy", dg_add=None if fused else "dg_wy"), es, 4)
     return ck
 
 
