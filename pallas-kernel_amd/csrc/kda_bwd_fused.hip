@@ -282,11 +282,49 @@ __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
       load_state(Rdh, draw, ps);
       __syncthreads();  // S2: planes, gate cumsum, Gm, Gamma visible
       float dkv[2][4], dgr[2][4];
-      // ---- A: inter-chunk X^T += (alpha h) dO^T, W^T += (beta dh) v_new^T
+      // ---- A: inter-chunk X^T += (alpha h) dO^T (the h rows were requested first)
       const float al = scale * fast_exp2(sGm[kl]);
       const float be = fast_exp2(sGam[kl] - sGm[kl]);
-      f32x4 X[2], Wt[2];
-      X[0] = X[1] = Wt[0] = Wt[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      f32x4 X[2], Wt[2], Wq[2];
+      X[0] = X[1] = Wt[0] = Wt[1] = Wq[0] = Wq[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int vc = 0; vc < VC; ++vc) {
+        const int v0 = 32 * vc + 8 * lg;
+        float hv[8];
+        unpack4(hraw[vc][0], hv);
+        unpack4(hraw[vc][1], hv + 4);
+        uint32_t ah_[4], al_[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) split_bf16x2(al * hv[2 * e], al * hv[2 * e + 1], ah_[e], al_[e]);
+        const bf16x8 Ah = __builtin_bit_cast(bf16x8, make_uint4(ah_[0], ah_[1], ah_[2], ah_[3]));
+        const bf16x8 Al = __builtin_bit_cast(bf16x8, make_uint4(al_[0], al_[1], al_[2], al_[3]));
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+          const bf16x8 doh = Pd.hi8(16 * (2 * rh + a) + l16, v0);
+          X[a] = mma<true, false>(X[a], Ah, Al, doh, doh);
+        }
+      }
+      // ---- intra-chunk: X^T += k~^T dA^T, Wq^T = q~^T dA (LDS operands only: they cover the
+      // wait for the dh rows)
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const int B2 = 2 * rh + a;
+#pragma unroll
+        for (int Pp = 0; Pp < 2; ++Pp) {
+          const int P0 = 2 * Pp, P1 = 2 * Pp + 1;
+          if (P0 <= B2) {
+            X[a] = mma<true, true>(X[a], Pkt.hi44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
+                                   Pkt.lo44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
+                                   cat44(dthh[a][P0], dthh[a][P1]), cat44(dthl[a][P0], dthl[a][P1]));
+          }
+          if (P1 >= B2) {
+            Wq[a] = mma<true, true>(Wq[a], Pqt.hi44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
+                                    Pqt.lo44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
+                                    cat44(dahh[a][P0], dahh[a][P1]), cat44(dahl[a][P0], dahl[a][P1]));
+          }
+        }
+      }
+      // ---- inter-chunk W^T = (beta dh) v_new^T, and sum_v h dh (token-half-0 waves)
       float hd = 0.f;
 #pragma unroll
       for (int vc = 0; vc < VC; ++vc) {
@@ -300,21 +338,14 @@ __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) hd += hv[e] * dv[e];
         }
-        uint32_t ah_[4], al_[4], bh_[4], bl_[4];
+        uint32_t bh_[4], bl_[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          split_bf16x2(al * hv[2 * e], al * hv[2 * e + 1], ah_[e], al_[e]);
-          split_bf16x2(be * dv[2 * e], be * dv[2 * e + 1], bh_[e], bl_[e]);
-        }
-        const bf16x8 Ah = __builtin_bit_cast(bf16x8, make_uint4(ah_[0], ah_[1], ah_[2], ah_[3]));
-        const bf16x8 Al = __builtin_bit_cast(bf16x8, make_uint4(al_[0], al_[1], al_[2], al_[3]));
+        for (int e = 0; e < 4; ++e) split_bf16x2(be * dv[2 * e], be * dv[2 * e + 1], bh_[e], bl_[e]);
         const bf16x8 Dh = __builtin_bit_cast(bf16x8, make_uint4(bh_[0], bh_[1], bh_[2], bh_[3]));
         const bf16x8 Dl = __builtin_bit_cast(bf16x8, make_uint4(bl_[0], bl_[1], bl_[2], bl_[3]));
 #pragma unroll
         for (int a = 0; a < 2; ++a) {
           const int tr = 16 * (2 * rh + a) + l16;
-          const bf16x8 doh = Pd.hi8(tr, v0);
-          X[a] = mma<true, false>(X[a], Ah, Al, doh, doh);
           Wt[a] = mma<true, true>(Wt[a], Dh, Dl, Pv.hi8(tr, v0), Pv.lo8(tr, v0));
         }
       }
@@ -334,10 +365,7 @@ __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
           }
         }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-#pragma unroll
-          for (int o = 1; o < 16; o <<= 1) z[r] += __shfl_xor(z[r], o, 64);
-        }
+        for (int r = 0; r < 4; ++r) z[r] = row16_sum(z[r]);
         if (l16 == 0) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) sZk[rh * KH + 16 * kb + 4 * lg + r] = z[r];
@@ -348,24 +376,10 @@ __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
           if (lg == 0) sHdh[kl] = hd;
         }
       }
-      // ---- intra-chunk: X^T += k~^T dA^T, W^T += q~^T dA
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
-        const int B2 = 2 * rh + a;
 #pragma unroll
-        for (int Pp = 0; Pp < 2; ++Pp) {
-          const int P0 = 2 * Pp, P1 = 2 * Pp + 1;
-          if (P0 <= B2) {
-            X[a] = mma<true, true>(X[a], Pkt.hi44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
-                                   Pkt.lo44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
-                                   cat44(dthh[a][P0], dthh[a][P1]), cat44(dthl[a][P0], dthl[a][P1]));
-          }
-          if (P1 >= B2) {
-            Wt[a] = mma<true, true>(Wt[a], Pqt.hi44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
-                                    Pqt.lo44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
-                                    cat44(dahh[a][P0], dahh[a][P1]), cat44(dahl[a][P0], dahl[a][P1]));
-          }
-        }
+        for (int r = 0; r < 4; ++r) Wt[a][r] += Wq[a][r];
       }
       // ---- epilogue, part 1: lane holds (token 16(2rh+a) + l16, channels cb + cl + r)
       const float4 gm4 = *(const float4*)(sGm + cl);
@@ -402,20 +416,14 @@ __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
         dgr[a][0] += xg.x; dgr[a][1] += xg.y; dgr[a][2] += xg.z; dgr[a][3] += xg.w;
         Wd::st4(Rdk, dk4, ok ? off * 2u : kOOB, 0);
       }
-      // reverse cumsum over tokens: 16-lane suffix scan, block a=1 into a=0, half 1 into 0
+      // reverse cumsum over tokens: 16-lane suffix sums, block a=1's total into a=0, half 1
+      // into half 0 (through sBlk)
 #pragma unroll
-      for (int a = 0; a < 2; ++a) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-#pragma unroll
-          for (int o = 1; o < 16; o <<= 1) {
-            const float y = __shfl_down(dgr[a][r], o, 16);
-            if (l16 + o < 16) dgr[a][r] += y;
-          }
-        }
+      for (int r = 0; r < 4; ++r) {
+        const float t1 = row16_sum(dgr[1][r]);
+        dgr[0][r] = row16_suffix_sum(dgr[0][r]) + t1;
+        dgr[1][r] = row16_suffix_sum(dgr[1][r]);
       }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) dgr[0][r] += __shfl(dgr[1][r], lane & 48, 64);
       if (rh == 1 && l16 == 0) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) sBlk[cl + r] = dgr[0][r];   // total of tokens 32..63
@@ -570,7 +578,14 @@ __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
 #pragma unroll 1
   for (int ps = 0; ps < NPS; ++ps) {
     const int cb = ps * KH;
-    load_state(Rh, hraw, ps);              // A: h rows of the inter products; B: S rows of dbk
+    load_state(Rh, hraw, ps);              // S rows of dbk
+    // k of the epilogue's (token, 4 channels), requested with the state rows
+    Wd::W4 kvraw[2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      const int tok = 16 * (2 * rh + a) + l16, kq = cb + 16 * kb + 4 * lg;
+      kvraw[a] = Wd::ld4(Rk, (kq < K && tok < nval) ? ((uint32_t)tok * rowK + kq) * 2u : kOOB, 0);
+    }
     // ---- gate cumsum of the pass (thread: channel ch, rows 8sg..8sg+7); A publishes the
     // segment totals, both groups read them
     float G[8];
@@ -635,9 +650,8 @@ __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
                                  cat44(dach[a][P0], dach[a][P1]), cat44(dacl[a][P0], dacl[a][P1]));
         }
         const int tok = 16 * t + l16;
-        const bool ok = chok && tok < nval;
         float kv[4];
-        unpack4(Wd::ld4(Rk, ok ? ((uint32_t)tok * rowK + kc) * 2u : kOOB, 0), kv);
+        unpack4(kvraw[a], kv);
         const float4 g4 = *(const float4*)(sG + tok * LG + cl);
         const float gt[4] = {g4.x, g4.y, g4.z, g4.w};
         const float b = sBeta[tok];

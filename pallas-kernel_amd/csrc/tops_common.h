@@ -51,6 +51,29 @@ __device__ __forceinline__ void split_bf16x2(float a, float b, uint32_t& hi, uin
 }
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Cross-lane sums inside one 16-lane DPP row, on the VALU (no LDS round trip).  A lane whose
+// DPP source lies outside its row reads 0.
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+// every lane of a row gets the sum over the row's 16 lanes
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_row<0xB1>(x);   // quad_perm [1,0,3,2]: pairs
+  x += dpp_row<0x4E>(x);   // quad_perm [2,3,0,1]: quads
+  x += dpp_row<0x141>(x);  // row_half_mirror: lane i <- 7 - i, the other quad of the half
+  x += dpp_row<0x140>(x);  // row_mirror: lane i <- 15 - i, the other half of the row
+  return x;
+}
+// lane l of a row gets the sum over lanes l .. 15 of its row (inclusive suffix sum)
+__device__ __forceinline__ float row16_suffix_sum(float x) {
+  x += dpp_row<0x101>(x);  // row_shl:1, lane l <- l + 1
+  x += dpp_row<0x102>(x);
+  x += dpp_row<0x104>(x);
+  x += dpp_row<0x108>(x);
+  return x;
+}
+
 // Input element loads (bf16 stored as uint16_t, or fp32)
 template <typename T> struct In;
 template <> struct In<uint16_t> {
