@@ -18,6 +18,8 @@
 // Group B computes its products with the operands exchanged, so its results sit in group
 // A's result layout: lane holds (token 16 t + l16, channels 4 lg + r of a 16-channel block).
 // Both groups run the same barrier sequence.
+#include <type_traits>
+
 #include "kda.h"
 #include "tops_common.h"
 
@@ -177,7 +179,8 @@ __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
     }
   };
   // ---------------- group A: dq / dk / dg
-  auto runA = [&]() {
+  auto runA = [&](auto RHc) {
+  constexpr int rh = decltype(RHc)::value;   // token-block pair, a constant per instance
   uint2 dthh[2][4], dthl[2][4], dahh[2][4], dahl[2][4];
     // A: v_new (fp32, split into hi / lo) and dO planes ([C][V], V contiguous)
     const rsrc_t Rvn = make_rsrc_rows(p.vnew, e0, nrows, V);
@@ -450,7 +453,8 @@ __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
   };
 
   // ---------------- group B: the WY backward
-  auto runB = [&]() {
+  auto runB = [&](auto RHc) {
+  constexpr int rh = decltype(RHc)::value;
   uint2 darh[2][4], darl[2][4], dach[2][4], dacl[2][4];
     // B: the P phase's global operands (dv_new^T and T^T fragments, v rows), requested first
     uint4 pdraw[NVW][2][2], ptraw[4][2][2];
@@ -691,8 +695,16 @@ __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
   }
   };
 
-  if (grpB) runB();
-  else runA();
+  // one instance per token-block pair: the dA / dAkk tiles a wave never uses take no registers
+  typedef std::integral_constant<int, 0> RH0;
+  typedef std::integral_constant<int, 1> RH1;
+  if (grpB) {
+    if (rh == 0) runB(RH0{});
+    else runB(RH1{});
+  } else {
+    if (rh == 0) runA(RH0{});
+    else runA(RH1{});
+  }
 }
 
 hipError_t launch_kda_bwd_fused(const KdaBwdParams& p, hipStream_t s) {
