@@ -558,10 +558,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
         }
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) z[r] += __shfl_xor(z[r], o, 64);
-      }
+      for (int r = 0; r < 4; ++r) z[r] = row16_sum(z[r]);
       if (l16 == 0) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) gZk[rh * KH + 16 * kb + 4 * lg + r] = z[r];
@@ -650,20 +647,14 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
       Wd::st4(Rdq, dqv, ok ? off * ES : kOOB, 0);
       Wd::st4(Rdk, dkv, ok ? off * ES : kOOB, 0);
     }
-    // reverse cumsum over tokens: 16-lane suffix scan, block a=1 into a=0, half 1 into 0
+    // reverse cumsum over tokens: 16-lane suffix sums, block a=1's total into a=0, half 1
+    // into half 0 (through gBlk)
 #pragma unroll
-    for (int a = 0; a < 2; ++a) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) {
-          const float y = __shfl_down(dgr[a][r], o, 16);
-          if (l16 + o < 16) dgr[a][r] += y;
-        }
-      }
+    for (int r = 0; r < 4; ++r) {
+      const float t1 = row16_sum(dgr[1][r]);
+      dgr[0][r] = row16_suffix_sum(dgr[0][r]) + t1;
+      dgr[1][r] = row16_suffix_sum(dgr[1][r]);
     }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) dgr[0][r] += __shfl(dgr[1][r], lane & 48, 64);
     if (rh == 1 && l16 == 0) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) gBlk[cl + r] = dgr[0][r];   // total of tokens 32..63
