@@ -98,10 +98,12 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // The chunk of the pair is a compile-time index (GRP), so that every LDS address of the
   // body folds to an immediate offset; the two halves run the same barriers in the same order.
-  auto run = [&](auto grp_tag) {
+  // The token half (rh) is one too: the dA tiles a wave never uses then take no registers.
+  auto run = [&](auto grp_tag, auto rh_tag) {
   constexpr int grp = decltype(grp_tag)::value;
+  constexpr int rh = decltype(rh_tag)::value;  // token half
   const int tq = PAIR ? tid & 255 : tid;       // thread index within the chunk's four waves
-  const int kb = wave & 1, rh = (wave >> 1) & 1;   // channel block of the pass, token half
+  const int kb = wave & 1;                     // channel block of the pass
   const int l16 = lane & 15, lg = lane >> 4;
   const int hh = blockIdx.x % p.H;
   const int gc = PAIR ? 2 * (blockIdx.x / p.H) + grp : blockIdx.x / p.H;
@@ -488,11 +490,54 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
       if (ps + 1 < NPS) load_pass(ps + 1);
     }
 
-    // ---- inter-chunk: X^T += (alpha h) dO^T, W^T += (beta dh) v^T
+    // ---- inter-chunk X^T += (alpha h) dO^T first: the h rows were requested a phase before
+    // the dh rows
     const float al = scale * fast_exp2(RG ? rgm : gGm[kl]);
     const float be = fast_exp2(RG ? rgam - rgm : gGam[kl] - gGm[kl]);
-    f32x4 X[2], Wt[2];
-    X[0] = X[1] = Wt[0] = Wt[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 X[2], Wt[2], Wq[2];
+    X[0] = X[1] = Wt[0] = Wt[1] = Wq[0] = Wq[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int vc = 0; vc < VC; ++vc) {
+      const int v0 = 32 * vc + 8 * lg;
+      float hv[8];
+      unpack4(hraw[vc][0], hv);
+      unpack4(hraw[vc][1], hv + 4);
+      uint32_t ah_[4], al_[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) split_bf16x2(al * hv[2 * e], al * hv[2 * e + 1], ah_[e], al_[e]);
+      const bf16x8 Ah = __builtin_bit_cast(bf16x8, make_uint4(ah_[0], ah_[1], ah_[2], ah_[3]));
+      const bf16x8 Al = __builtin_bit_cast(bf16x8, make_uint4(al_[0], al_[1], al_[2], al_[3]));
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const int B2 = 2 * rh + a;
+        const int tr = 16 * B2 + l16;
+        const bf16x8 doh = PAIR ? Pd.hi44(tr, 32 * vc + 4 * lg, 32 * vc + 16 + 4 * lg) : Pd.hi8(tr, v0);
+        bf16x8 dol = doh;
+        if constexpr (SIN) dol = Pd.lo8(16 * B2 + l16, v0);
+        X[a] = mma<true, SIN>(X[a], Ah, Al, doh, dol);
+      }
+    }
+    // ---- intra-chunk: X^T += k~^T dA^T, Wq^T = q~^T dA (LDS operands only: they cover the
+    // wait for the dh rows)
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      const int B2 = 2 * rh + a;
+#pragma unroll
+      for (int Pp = 0; Pp < 2; ++Pp) {
+        const int P0 = 2 * Pp, P1 = 2 * Pp + 1;
+        if (P0 <= B2) {
+          X[a] = mma<!RG, true>(X[a], Pkt.hi44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
+                                 Pkt.lo44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
+                                 cat44(dthh[a][P0], dthh[a][P1]), cat44(dthl[a][P0], dthl[a][P1]));
+        }
+        if (P1 >= B2) {
+          Wq[a] = mma<!RG, true>(Wq[a], Pqt.hi44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
+                                  Pqt.lo44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
+                                  cat44(dahh[a][P0], dahh[a][P1]), cat44(dahl[a][P0], dahl[a][P1]));
+        }
+      }
+    }
+    // ---- inter-chunk W^T = (beta dh) v^T, and sum_v h dh (token-half-0 waves)
     float hd = 0.f;
 #pragma unroll
     for (int vc = 0; vc < VC; ++vc) {
@@ -506,26 +551,18 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
 #pragma unroll
         for (int e = 0; e < 8; ++e) hd += hv[e] * dv[e];
       }
-      uint32_t ah_[4], al_[4], bh_[4], bl_[4];
+      uint32_t bh_[4], bl_[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        split_bf16x2(al * hv[2 * e], al * hv[2 * e + 1], ah_[e], al_[e]);
-        split_bf16x2(be * dv[2 * e], be * dv[2 * e + 1], bh_[e], bl_[e]);
-      }
-      const bf16x8 Ah = __builtin_bit_cast(bf16x8, make_uint4(ah_[0], ah_[1], ah_[2], ah_[3]));
-      const bf16x8 Al = __builtin_bit_cast(bf16x8, make_uint4(al_[0], al_[1], al_[2], al_[3]));
+      for (int e = 0; e < 4; ++e) split_bf16x2(be * dv[2 * e], be * dv[2 * e + 1], bh_[e], bl_[e]);
       const bf16x8 Dh = __builtin_bit_cast(bf16x8, make_uint4(bh_[0], bh_[1], bh_[2], bh_[3]));
       const bf16x8 Dl = __builtin_bit_cast(bf16x8, make_uint4(bl_[0], bl_[1], bl_[2], bl_[3]));
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
         const int B2 = 2 * rh + a;
         const int tr = 16 * B2 + l16;
-        const bf16x8 doh = PAIR ? Pd.hi44(tr, 32 * vc + 4 * lg, 32 * vc + 16 + 4 * lg) : Pd.hi8(tr, v0);
         const bf16x8 vh = PAIR ? Pv.hi44(tr, 32 * vc + 4 * lg, 32 * vc + 16 + 4 * lg) : Pv.hi8(tr, v0);
-        bf16x8 dol = doh, vl = vh;
-        if constexpr (SIN) dol = Pd.lo8(16 * B2 + l16, v0);
+        bf16x8 vl = vh;
         if constexpr (SINV) vl = Pv.lo8(16 * B2 + l16, v0);
-        X[a] = mma<true, SIN>(X[a], Ah, Al, doh, dol);
         Wt[a] = mma<true, SINV>(Wt[a], Dh, Dl, vh, vl);
       }
     }
@@ -569,24 +606,10 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
         if (lg == 0) gHdh[kl] = hd;
       }
     }
-    // ---- intra-chunk: X^T += k~^T dA^T, W^T += q~^T dA
 #pragma unroll
     for (int a = 0; a < 2; ++a) {
-      const int B2 = 2 * rh + a;
 #pragma unroll
-      for (int Pp = 0; Pp < 2; ++Pp) {
-        const int P0 = 2 * Pp, P1 = 2 * Pp + 1;
-        if (P0 <= B2) {
-          X[a] = mma<!RG, true>(X[a], Pkt.hi44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
-                                 Pkt.lo44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
-                                 cat44(dthh[a][P0], dthh[a][P1]), cat44(dthl[a][P0], dthl[a][P1]));
-        }
-        if (P1 >= B2) {
-          Wt[a] = mma<!RG, true>(Wt[a], Pqt.hi44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
-                                  Pqt.lo44(kl, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg),
-                                  cat44(dahh[a][P0], dahh[a][P1]), cat44(dahl[a][P0], dahl[a][P1]));
-        }
-      }
+      for (int r = 0; r < 4; ++r) Wt[a][r] += Wq[a][r];
     }
     // ---- epilogue in the result layout: lane holds (token 16(2rh+a) + l16,
     //      channels cb + 16kb + 4lg + r), r = 0..3
@@ -702,11 +725,15 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
     }
   }
   };
-  if constexpr (PAIR) {
-    if (wave >> 2) run(std::integral_constant<int, 1>{});
-    else run(std::integral_constant<int, 0>{});
+  typedef std::integral_constant<int, 0> I0;
+  typedef std::integral_constant<int, 1> I1;
+  const bool r1 = (wave >> 1) & 1;
+  if (PAIR && (wave >> 2)) {
+    if (r1) run(I1{}, I1{});
+    else run(I1{}, I0{});
   } else {
-    run(std::integral_constant<int, 0>{});
+    if (r1) run(I0{}, I1{});
+    else run(I0{}, I0{});
   }
 }
 
