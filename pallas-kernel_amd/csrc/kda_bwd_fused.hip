@@ -8,8 +8,8 @@
 // tops/cpu/ops/kda/chunk_bwd.py:525-668).  Here:
 //   * 8 waves: waves 0-3 (group A) run the dq / dk / dg passes of 32 channels, waves 4-7
 //     (group B) the WY passes over the same channels, on shared LDS planes: v_new (bf16
-//     hi / lo), dO, the pass's q~ / k~ (k~ = k 2^(Gm - G) is the WY's k-plane too) and its
-//     gate cumsum;
+//     hi / lo), dO, the pass's q~ / k~ / k^ (k~ = k 2^(Gm - G), k^ = k 2^(G - Gm)) and its
+//     gate cumsum, all staged by group A (B reads no q / k / g rows of its own);
 //   * the WY parts of dk and of the gate gradient go from group B to group A through an
 //     LDS exchange per pass, not through two [B,T,H,K] fp32 tensors in HBM, and are added
 //     before A's reverse token cumsum (the cumsum is linear);
@@ -107,7 +107,7 @@ __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
   const long long KVB = (long long)K * V * 4;
   const rsrc_t Rh = make_rsrc(p.hs + ((size_t)gc * H + hh) * K * V, KVB);
 
-  // ---------------- staging registers of a pass: thread = (channel ch, rows 8 sg .. 8 sg + 7)
+  // ---------------- group A's staging registers: thread = (channel ch, rows 8 sg .. 8 sg + 7)
   const int ch = tq & 31, sg = tq >> 5;
   const uint32_t hsh = (ch & 1) ? 0u : 16u;
   auto elem = [&](uint32_t w) { return __uint_as_float((w << hsh) & 0xffff0000u); };
@@ -121,7 +121,7 @@ __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
       const int r = 8 * sg + i;
       const bool v_ = ok && r < nval;
       const uint32_t off = (uint32_t)r * rowK + kc;
-      rq[i] = grpB ? 0u : bld32(Rq, v_ ? (off & ~1u) * 2u : kOOB, 0);
+      rq[i] = bld32(Rq, v_ ? (off & ~1u) * 2u : kOOB, 0);
       rk[i] = bld32(Rk, v_ ? (off & ~1u) * 2u : kOOB, 0);
       rg[i] = __uint_as_float(bld32(Rg, v_ ? off * 4u : kOOB, 0));
     }
@@ -272,16 +272,19 @@ __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
         sGm[ch] = gmv;
         sGam[ch] = gam;
       }
-      float qt[8], kt[8];
+      float qt[8], kt[8], k1[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         G[i] += pre;
         sG[(8 * sg + i) * LG + ch] = G[i];
-        qt[i] = elem(rq[i]) * fast_exp2(G[i] - gmv);
+        const float e = fast_exp2(G[i] - gmv);
+        qt[i] = elem(rq[i]) * e;
+        k1[i] = elem(rk[i]) * e;
         kt[i] = elem(rk[i]) * fast_exp2(gmv - G[i]);
       }
       put_n<true, 8>(Pqt, ch, 8 * sg, qt);
       put_n<true, 8>(Pkt, ch, 8 * sg, kt);
+      put_n<true, 8>(Pk1, ch, 8 * sg, k1);
       load_state(Rdh, draw, ps);
       __syncthreads();  // S2: planes, gate cumsum, Gm, Gamma visible
       float dkv[2][4], dgr[2][4];
@@ -492,7 +495,6 @@ __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
         }
       }
     }
-    load_pass(0);
     if (tq < C) sBeta[tq] = __uint_as_float(braw);
     __syncthreads();  // P1: v_new / dO planes and beta visible
     {
@@ -590,30 +592,10 @@ __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
       const int tok = 16 * (2 * rh + a) + l16, kq = cb + 16 * kb + 4 * lg;
       kvraw[a] = Wd::ld4(Rk, (kq < K && tok < nval) ? ((uint32_t)tok * rowK + kq) * 2u : kOOB, 0);
     }
-    // ---- gate cumsum of the pass (thread: channel ch, rows 8sg..8sg+7); A publishes the
-    // segment totals, both groups read them
-    float G[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) G[i] = rg[i] * kLog2e + (i > 0 ? G[i - 1] : 0.f);
-    __syncthreads();  // S1: segment totals visible
-    float pre = 0.f, gam = 0.f;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const float t = sTot[s * KH + ch];
-      if (s < sg) pre += t;
-      gam += t;
-    }
-    const float gmv = 0.5f * gam;
+    __syncthreads();  // S1
     const int cl = 16 * kb + 4 * lg;       // first channel of the lane's result (in pass)
-    const int kc = cb + cl;
-    const bool chok = kc < K;
     {
-      float k1[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) k1[i] = elem(rk[i]) * fast_exp2(G[i] + pre - gmv);
-      put_n<true, 8>(Pk1, ch, 8 * sg, k1);
-      if (ps + 1 < NPS) load_pass(ps + 1);
-      __syncthreads();  // S2
+      __syncthreads();  // S2: group A's planes (k~, k^), gate cumsum and Gm visible
       // ---- B: dbk' = S P^T, Y1' = k~^T dAkk^T, Y2' = k^^T (beta dAkk), all transposed:
       // lane holds (channel cb + cl + r, token 16t + l16)
       bf16x8 sh[VC], sl[VC];

@@ -472,7 +472,7 @@ def kda_wy(ck: Checker, p: dict, es: int, fused: bool = False):
                 ck.acc(p["hs"], blk * K * V * 4, np.where((kk < K) & (v0 < V), (kk * V + v0) * 4, KOOB),
                        0, 32, "wy load state")
             kc = cb + ch
-            for i in range(8):
+            for i in range(8 if not fused else 0):   # fused: the gated k plane comes from LDS
                 r = 8 * sg + i
                 ok = (kc < K) & (r < nval)
                 off = r * rowK + kc
