@@ -112,9 +112,9 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
                            (GV ? (C * LE + 4 * BV) * 4 : 0);
   constexpr bool SHARED_D = !DELTA && !ST && LDS_BASE + 10 * 64 * 16 <= 160 * 1024;
   __shared__ __attribute__((aligned(16))) uint4 sDt[SHARED_D ? 10 * 64 : 1];
-  // Gamma / 2 of channel c sits in the padding columns of the X hi plane (row c / 4, word c % 4):
-  // no MFMA fragment or staging write touches columns >= KP
-  auto gm_at = [&](int c4) { return (float*)(sX + (c4 >> 2) * LQ + KP); };
+  // (forward delta rule) 2^-Gm of channel c, Gm = Gamma / 2, sits in the padding columns of the
+  // X hi plane (row c / 4, word c % 4): no MFMA fragment or staging write touches columns >= KP
+  auto egm_at = [&](int c4) { return (float*)(sX + (c4 >> 2) * LQ + KP); };
 
   const Plane PX{sX, XL ? sX + C * LQ : sX, LQ};
   const Plane PZ{sZ, XL ? sZ + C * LQ : sZ, LQ};
@@ -481,7 +481,9 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) gm[j] = 0.5f * gam[j];
     if constexpr (FWD_DELTA) {
-      if (seg == 0) *(float4*)gm_at(c0) = make_float4(gm[0], gm[1], gm[2], gm[3]);
+      if (seg == 0)
+        *(float4*)egm_at(c0) =
+            make_float4(fast_exp2(-gm[0]), fast_exp2(-gm[1]), fast_exp2(-gm[2]), fast_exp2(-gm[3]));
     }
     // Gamma of this lane's state rows kr = 16 msb + 4 lg + r
     float sgam[4] = {0.f, 0.f, 0.f, 0.f};
@@ -837,12 +839,11 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
           unpack4(bld128(Rw, o, 0), a);
           unpack4(bld128(Rw, o == kOOB ? kOOB : o + 16u, 0), a + 4);
         }
-        const float4 g0 = *(const float4*)gm_at(k0), g1 = *(const float4*)gm_at(k0 + 4);
-        const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+        const float4 g0 = *(const float4*)egm_at(k0), g1 = *(const float4*)egm_at(k0 + 4);
+        const float eg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
         uint32_t h4[4], l4[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          split_bf16x2(a[2 * e] * fast_exp2(-gg[2 * e]), a[2 * e + 1] * fast_exp2(-gg[2 * e + 1]), h4[e], l4[e]);
+        for (int e = 0; e < 4; ++e) split_bf16x2(a[2 * e] * eg[2 * e], a[2 * e + 1] * eg[2 * e + 1], h4[e], l4[e]);
         wh[kc] = __builtin_bit_cast(bf16x8, make_uint4(h4[0], h4[1], h4[2], h4[3]));
         wl[kc] = __builtin_bit_cast(bf16x8, make_uint4(l4[0], l4[1], l4[2], l4[3]));
       }
