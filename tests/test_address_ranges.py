@@ -169,7 +169,9 @@ def test_planted_rows_range_past_end_is_caught():
 KDA = [dict(B=2, T=64, H=2, K=32, V=32), dict(B=1, T=100, H=3, K=64, V=128),
        dict(B=2, T=130, H=2, K=128, V=64), dict(B=1, T=1, H=2, K=16, V=32),
        dict(B=1, T=300, H=2, K=64, V=64, cu=[0, 13, 140, 141, 300]),
-       dict(B=1, T=256, H=4, K=128, V=128, cu=[0, 64, 128, 192, 256])]
+       dict(B=1, T=256, H=4, K=128, V=128, cu=[0, 64, 128, 192, 256]),
+       dict(B=1, T=150, H=2, K=40, V=120), dict(B=2, T=70, H=1, K=64, V=24),
+       dict(B=1, T=129, H=2, K=120, V=56), dict(B=1, T=96, H=2, K=24, V=128)]
 
 
 @pytest.mark.parametrize("es", [4, 2], ids=["f32", "bf16"])

@@ -29,6 +29,13 @@ CASES = [
     dict(B=1, T=300, H=2, K=128, V=128, h0=True, cu=[0, 13, 140, 141, 300]),
     dict(B=1, T=1000, H=2, K=128, V=128, cu=varlen_cu(1000, 6, 77)),
     dict(B=1, T=1024, H=4, K=128, V=128),     # config 5 shape at reduced T
+    # the remaining channel-pass / column-tile instances (K, V padded to 32, 64, 128), with
+    # channels and columns past K / V in the last pass or tile
+    dict(B=1, T=100, H=2, K=32, V=32),
+    dict(B=1, T=150, H=2, K=40, V=120, h0=True),
+    dict(B=2, T=70, H=1, K=64, V=24),
+    dict(B=1, T=129, H=2, K=120, V=56, h0=True),
+    dict(B=1, T=96, H=2, K=24, V=128, h0=True),
 ]
 
 
