@@ -281,6 +281,21 @@ int tops_gla_fused_recurrent_fwd(const void* q, const void* k, const void* v, co
                                  const int32_t* cu_seqlens, int B, int T, int H, int K, int V,
                                  int N, int dtype, float scale, int reverse, void* stream);
 
+/* The same forward for sequences of a few tokens (decode steps against a state cache): one
+ * wave per (sequence, head, 8 V columns) keeps its state slice in registers, so the launch
+ * reads h0 and writes ht once and is bound by those bytes.  Same arguments, semantics and
+ * limits as tops_gla_fused_recurrent_fwd, which takes this kernel by itself for fixed-length
+ * calls with T <= 4; varlen callers that know every sequence is short call it directly.  Any
+ * length is computed correctly; long sequences run one token at a time.  Replaces
+ * tops.ops.gla.fused_recurrent_gla_fwd (tops/ops/gla/fused_recurrent.py:380-431) on the
+ * decode route of the reference's layer (tops/layers/gla.py:288-297, q_len <= 64). */
+int tops_gla_fused_recurrent_fwd_decode(const void* q, const void* k, const void* v,
+                                        const float* gk, const float* gv, const float* h0,
+                                        void* o, float* o32, float* ht,
+                                        const int32_t* cu_seqlens, int B, int T, int H, int K,
+                                        int V, int N, int dtype, float scale, int reverse,
+                                        void* stream);
+
 /* Bytes of the workspace tops_gla_fused_recurrent_bwd needs (with_gv: a gv gate is used). */
 int64_t tops_gla_fused_recurrent_bwd_workspace(int B, int T, int H, int K, int V, int N,
                                                int with_gv);

@@ -398,6 +398,160 @@ __global__ __launch_bounds__(256) void fr_finish_kernel(FrFinishParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Short sequences (decode steps): one wave per (sequence, head, 32-column tile) with the state
+// slice in registers.  Lane (kr, cq) = (lane % 8, lane / 8) holds rows RL kr .. RL kr + RL - 1
+// (RL = KP / 8) and columns 4 cq .. 4 cq + 3 of the tile, so each state load or store of a wave
+// covers whole 128-byte rows of the tile and no two waves share a line (one wave's tile never
+// straddles the L2s of two XCDs).  Tokens are staged DT at a time into LDS with coalesced
+// loads (q scaled, the gates as decay factors exp(g), one exponential per element), so their
+// latency is paid once per block; o_t[v] is reduced over the 8 row groups with three DPP steps
+// inside a 16-lane row.  With a few tokens the launch is bound by the state read and write
+// (h0 in, ht out).
+constexpr int kFrDecodeT = 4;    // longest sequence the fixed-length entry sends here
+
+// sum over the 8 lanes l .. l | 7 (bits 0-2 of the lane index), in every one of them
+__device__ __forceinline__ float oct_sum(float x) {
+  x += dpp_row<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp_row<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp_row<0x141>(x);  // row_half_mirror: lane i <- 7 - i within each 8 lanes
+  return x;
+}
+
+template <typename TIn, int KP>
+__global__ __launch_bounds__(64) void fr_decode_kernel(FrParams p) {
+  constexpr int RL = KP / 8;            // rows per lane
+  constexpr int DT = 8;                 // tokens per staged block
+  __shared__ __attribute__((aligned(16))) float sQ[DT][KP];
+  __shared__ __attribute__((aligned(16))) float sK[DT][KP];
+  __shared__ __attribute__((aligned(16))) float sD[DT][KP];    // exp(gk)
+  __shared__ __attribute__((aligned(16))) float sV[DT][32];
+  __shared__ __attribute__((aligned(16))) float sDV[DT][32];   // exp(gv)
+  const int lane = threadIdx.x;
+  const int kr = lane & 7, cq = lane >> 3;
+  const int H = p.H, K = p.K, V = p.V;
+  const int NT = (V + 31) / 32;
+  const int tile = blockIdx.x % NT;
+  const int hh = (blockIdx.x / NT) % H;
+  const int n = blockIdx.x / (NT * H);
+  int bos, L;
+  if (p.cu_seqlens) {
+    bos = p.cu_seqlens[n];
+    L = p.cu_seqlens[n + 1] - bos;
+  } else {
+    bos = n * p.T;
+    L = p.T;
+  }
+  const int r0 = RL * kr, c0 = 32 * tile + 4 * cq;
+  // K % 4 == 0: each quad of rows is wholly in or out
+  bool qok[RL / 4];
+#pragma unroll
+  for (int m = 0; m < RL / 4; ++m) qok[m] = r0 + 4 * m < K;
+  bool cok[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) cok[c] = c0 + c < V;
+  const bool vec = (V % 4) == 0 && cok[3];
+  const size_t sbase = ((size_t)n * H + hh) * K * V;
+  const TIn* q = (const TIn*)p.q;
+  const TIn* kk = (const TIn*)p.k;
+  const TIn* v = (const TIn*)p.v;
+  auto tok = [&](int j) { return p.reverse ? bos + L - 1 - j : bos + j; };
+
+  float S[RL][4];
+#pragma unroll
+  for (int i = 0; i < RL; ++i) {
+    const bool rok = qok[i / 4];
+    const size_t o = sbase + (size_t)(r0 + i) * V + c0;
+    if (p.s0 && rok && vec) {
+      const float4 x = *(const float4*)(p.s0 + o);
+      S[i][0] = x.x; S[i][1] = x.y; S[i][2] = x.z; S[i][3] = x.w;
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) S[i][c] = (p.s0 && rok && cok[c]) ? p.s0[o + c] : 0.f;
+    }
+  }
+  for (int b0 = 0; b0 < L; b0 += DT) {
+    const int nb = min(DT, L - b0);
+    // ---- stage tokens b0 .. b0 + nb - 1: element e = lane + 64 u of the [DT][KP] / [DT][32] blocks
+#pragma unroll
+    for (int u = 0; u < DT * KP / 64; ++u) {
+      const int e = lane + 64 * u, j = e / KP, r = e % KP;
+      const bool ok = j < nb && r < K;
+      const size_t o = ok ? ((size_t)tok(b0 + j) * H + hh) * K + r : 0;
+      sQ[j][r] = ok ? ld_elem(q, o) * p.scale : 0.f;
+      sK[j][r] = ok ? ld_elem(kk, o) : 0.f;
+      sD[j][r] = (ok && p.gk) ? fast_exp2(p.gk[o] * kLog2e) : 1.f;
+    }
+#pragma unroll
+    for (int u = 0; u < DT * 32 / 64; ++u) {
+      const int e = lane + 64 * u, j = e / 32, c = e % 32, col = 32 * tile + c;
+      const bool ok = j < nb && col < V;
+      const size_t o = ok ? ((size_t)tok(b0 + j) * H + hh) * V + col : 0;
+      sV[j][c] = ok ? ld_elem(v, o) : 0.f;
+      sDV[j][c] = (ok && p.gv) ? fast_exp2(p.gv[o] * kLog2e) : 1.f;
+    }
+    __syncthreads();
+    for (int j = 0; j < nb; ++j) {
+      const float4 v4 = *(const float4*)&sV[j][4 * cq], d4 = *(const float4*)&sDV[j][4 * cq];
+      const float vv[4] = {v4.x, v4.y, v4.z, v4.w}, dv[4] = {d4.x, d4.y, d4.z, d4.w};
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i4 = 0; i4 < RL; i4 += 4) {
+        const float4 q4 = *(const float4*)&sQ[j][r0 + i4];
+        const float4 k4 = *(const float4*)&sK[j][r0 + i4];
+        const float4 g4 = *(const float4*)&sD[j][r0 + i4];
+        const float qs[4] = {q4.x, q4.y, q4.z, q4.w}, ks[4] = {k4.x, k4.y, k4.z, k4.w};
+        const float ds[4] = {g4.x, g4.y, g4.z, g4.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            S[i4 + u][c] = S[i4 + u][c] * (ds[u] * dv[c]) + ks[u] * vv[c];
+            acc[c] += S[i4 + u][c] * qs[u];
+          }
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[c] = oct_sum(acc[c]);
+      if (kr == 0) {
+        const size_t ov = ((size_t)tok(b0 + j) * H + hh) * V + c0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          if (cok[c]) {
+            st_elem((TIn*)p.o, ov + c, acc[c]);
+            if (p.o32) p.o32[ov + c] = acc[c];
+          }
+        }
+      }
+    }
+    __syncthreads();   // the block's tokens are consumed before the next block is staged
+  }
+  if (p.s_fin) {
+#pragma unroll
+    for (int i = 0; i < RL; ++i) {
+      if (!qok[i / 4]) continue;
+      const size_t o = sbase + (size_t)(r0 + i) * V + c0;
+      if (vec) {
+        *(float4*)(p.s_fin + o) = make_float4(S[i][0], S[i][1], S[i][2], S[i][3]);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (cok[c]) p.s_fin[o + c] = S[i][c];
+      }
+    }
+  }
+}
+
+template <typename TIn>
+static hipError_t launch_fr_decode(const FrParams& p, hipStream_t s) {
+  const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
+  dim3 grid(((p.V + 31) / 32) * p.H * p.N);
+  if (kp == 32) hipLaunchKernelGGL((fr_decode_kernel<TIn, 32>), grid, dim3(64), 0, s, p);
+  else if (kp == 64) hipLaunchKernelGGL((fr_decode_kernel<TIn, 64>), grid, dim3(64), 0, s, p);
+  else hipLaunchKernelGGL((fr_decode_kernel<TIn, 128>), grid, dim3(64), 0, s, p);
+  return hipGetLastError();
+}
+
 template <typename TIn, bool BWD>
 static hipError_t launch_fr(const FrParams& p, hipStream_t s) {
   const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
@@ -457,7 +611,28 @@ extern "C" int tops_gla_fused_recurrent_fwd(const void* q, const void* k, const 
   FrParams p{q, k, v, gk, gv, h0, nullptr, nullptr, o, o32, ht, nullptr, nullptr, nullptr, nullptr,
              nullptr, cu_seqlens, B, T, H, K, V, N, (V + kFrBV - 1) / kFrBV, scale, reverse ? 1 : 0};
   hipStream_t s = (hipStream_t)stream;
-  hipError_t e = dtype == TOPS_BF16 ? launch_fr<uint16_t, false>(p, s) : launch_fr<float, false>(p, s);
+  hipError_t e;
+  if (!cu_seqlens && T <= kFrDecodeT)
+    e = dtype == TOPS_BF16 ? launch_fr_decode<uint16_t>(p, s) : launch_fr_decode<float>(p, s);
+  else
+    e = dtype == TOPS_BF16 ? launch_fr<uint16_t, false>(p, s) : launch_fr<float, false>(p, s);
+  if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
+  return TOPS_OK;
+}
+
+extern "C" int tops_gla_fused_recurrent_fwd_decode(const void* q, const void* k, const void* v,
+                                                   const float* gk, const float* gv, const float* h0,
+                                                   void* o, float* o32, float* ht,
+                                                   const int32_t* cu_seqlens, int B, int T, int H,
+                                                   int K, int V, int N, int dtype, float scale,
+                                                   int reverse, void* stream) {
+  if (!q || !k || !v || !o) return tops_set_error(TOPS_ERR_NULL, "gla_fused_recurrent_fwd_decode: null tensor");
+  int rc = fr_check("gla_fused_recurrent_fwd_decode", B, T, H, K, V, N, cu_seqlens, dtype);
+  if (rc != TOPS_OK) return rc;
+  FrParams p{q, k, v, gk, gv, h0, nullptr, nullptr, o, o32, ht, nullptr, nullptr, nullptr, nullptr,
+             nullptr, cu_seqlens, B, T, H, K, V, N, (V + kFrBV - 1) / kFrBV, scale, reverse ? 1 : 0};
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = dtype == TOPS_BF16 ? launch_fr_decode<uint16_t>(p, s) : launch_fr_decode<float>(p, s);
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   return TOPS_OK;
 }

@@ -226,6 +226,40 @@ def gv_chunk_native(q, k, v, gv, initial_state, scale, output_final_state, cu_se
     return o, ht
 
 
+DECODE_MAX_TOKENS = 4    # beyond this the chunk kernels are faster (measured at K = V = 128)
+
+
+def decode_native(q, k, v, gk, gv, initial_state, scale, output_final_state, reverse, cu_seqlens):
+    """Sequences of at most DECODE_MAX_TOKENS tokens (decode steps against a state cache) on
+    the register-state kernel (tops_gla_fused_recurrent_fwd_decode), for calls that need no
+    gradient: it reads h0 and writes ht once, with no per-chunk staging.  Returns (o, ht or
+    None), or None where it does not apply (gradients wanted, dtypes other than fp32 / bf16,
+    K > 128 or K % 4, a longer sequence)."""
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad
+                                       for t in (q, k, v, gk, gv, initial_state)):
+        return None
+    if q.dtype not in (torch.float32, torch.bfloat16) or K > 128 or K % 4:
+        return None
+    if cu_seqlens is None:
+        n, longest = B, T
+    else:
+        cu = cu_seqlens.tolist() if isinstance(cu_seqlens, torch.Tensor) else list(cu_seqlens)
+        n = len(cu) - 1
+        longest = max((cu[i + 1] - cu[i] for i in range(n)), default=0)
+    if longest > DECODE_MAX_TOKENS:
+        return None
+    q, k, v = (x.contiguous() for x in (q, k, v))
+    o = torch.empty_like(v)
+    ht = torch.empty(n, H, K, V, device=q.device, dtype=torch.float32) if output_final_state else None
+    N.call("tops_gla_fused_recurrent_fwd_decode", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(_f32(gk)),
+           N.ptr(_f32(gv)), N.ptr(_f32(initial_state)), N.ptr(o), None, N.ptr(ht),
+           N.ptr(_cu_dev(cu_seqlens, q.device)), B, T, H, K, V, n, N.dtype_code(q.dtype),
+           float(scale), int(bool(reverse)), N.stream())
+    return o, ht
+
+
 def _reversed_chunk(fn, q, k, v, g, cu_seqlens, **kw):
     """fn (a chunk op) on the time-reversed sequences; returns (o in original order, ht)."""
     rev = time_reversal(q.shape[1], cu_seqlens, q.device)
@@ -242,6 +276,9 @@ def fused_recurrent_gla(q, k, v, gk=None, gv=None, scale=None, initial_state=Non
     wide = K > 128 or q.dtype not in (torch.float32, torch.bfloat16)
     if scale is None:
         scale = K ** -0.5
+    r = decode_native(q, k, v, gk, gv, initial_state, scale, output_final_state, reverse, cu_seqlens)
+    if r is not None:
+        return r
     if reverse and gv is None:
         r = reverse_chunk_native(q, k, v, "k" if gk is not None else "gamma",
                                  gk if gk is not None else torch.zeros(H, device=q.device),
@@ -275,6 +312,9 @@ def fused_recurrent_gla_fwd(q, k, v, gk=None, gv=None, scale=None, initial_state
     B, T, H, K, V, n = _check(q, k, v, gk, gv, initial_state, cu_seqlens)
     if scale is None:
         scale = K ** -0.5
+    r = decode_native(q, k, v, gk, gv, initial_state, scale, output_final_state, reverse, cu_seqlens)
+    if r is not None:
+        return r
     if _chunked(gv, reverse, K, V) and not reverse:
         from .chunk import chunk_gla
         return chunk_gla(q, k, v, gk, scale=scale, initial_state=initial_state,

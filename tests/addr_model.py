@@ -1,8 +1,8 @@
 """CPU replay of the address arithmetic of the buffer-resource kernels (test infrastructure).
 
 Every global access of gla_sweep_kernel (all instances: GLA / simple-GLA gate modes, the KDA
-delta rule, the state-only pass), gla_dqkg_kernel (bf16 / fp32, fp32 v), kda_prep_kernel and
-kda_wy_kernel is re-evaluated here per workgroup, chunk and thread, with the kernels' own
+delta rule, the state-only pass), gla_dqkg_kernel (bf16 / fp32, fp32 v), kda_prep_kernel,
+kda_wy_kernel / kda_bwd_fused_kernel and fr_decode_kernel is re-evaluated here per workgroup, chunk and thread, with the kernels' own
 thread mappings, masks and (voffset, soffset, width) decomposition.  An access whose voffset
 is kOOB is dropped by the hardware and skipped; every other access must lie entirely inside
 its tensor.  The launches are derived from the host code's own plans (ChunkPlan / SegPlan of
@@ -502,3 +502,69 @@ def kda_wy(ck: Checker, p: dict, es: int, fused: bool = False):
                     for nm in ("dk_wy", "dg_wy"):
                         ck.acc(p[nm], e0 * K * 4, np.where(ok, off * 4, KOOB), 0, 4, f"wy store {nm}")
         ck.acc(p["dbeta"], e0 * 4, np.where(tid < nval, tid * H * 4, KOOB), 0, 4, "wy store dbeta")
+
+
+# --------------------------------------------------------------------------- fr_decode_kernel
+def fr_decode(ck: Checker, p: dict, es: int):
+    """fr_decode_kernel<TIn, KP> (csrc/gla_recurrent.hip): one 64-lane wave per (sequence, head,
+    32-column tile); lane (kr, cq) = (lane % 8, lane / 8) owns rows RL kr .. RL kr + RL - 1
+    (RL = KP / 8) and columns 32 tile + 4 cq .. + 3 of the state.  Tokens are staged 8 at a
+    time: element e = lane + 64 u of the [8][KP] q / k / gk block and of the [8][32] v / gv block.
+    p: B, T, H, K, V, cu (host list or None), reverse, and which of gk / gv / s0 / s_fin / o32
+    are bound.  Plain pointer accesses (no buffer resource)."""
+    B, T, H, K, V = (p[x] for x in ("B", "T", "H", "K", "V"))
+    cu = p.get("cu")
+    N = len(cu) - 1 if cu is not None else B
+    KP = _kp(K)
+    RL, DT = KP // 8, 8
+    lane = np.arange(64, dtype=np.int64)
+    kr, cq = lane & 7, lane >> 3
+    r0 = RL * kr
+    NT = (V + 31) // 32
+    for n in range(N):
+        bos, L = (cu[n], cu[n + 1] - cu[n]) if cu is not None else (n * T, T)
+        tok = (lambda j: bos + L - 1 - j) if p.get("reverse") else (lambda j: bos + j)
+        for hh in range(H):
+            sbase = (n * H + hh) * K * V
+            for tile in range(NT):
+                c0 = 32 * tile + 4 * cq
+                vec = (V % 4 == 0) & (c0 + 3 < V)
+                for i in range(RL):
+                    rok = r0 + 4 * (i // 4) < K
+                    for nm in ("s0", "s_fin"):
+                        if not p.get(nm):
+                            continue
+                        o = sbase + (r0 + i) * V + c0
+                        ck.acc(p[nm], 0, np.where(rok & vec, o * 4, KOOB), 0, 16, f"decode {nm} (vector)")
+                        for c in range(4):
+                            ok = rok & ~vec & (c0 + c < V)
+                            ck.acc(p[nm], 0, np.where(ok, (o + c) * 4, KOOB), 0, 4, f"decode {nm}")
+                for b0 in range(0, L, DT):
+                    nb = min(DT, L - b0)
+                    for u in range(DT * KP // 64):
+                        e = lane + 64 * u
+                        j, r = e // KP, e % KP
+                        ok = (j < nb) & (r < K)
+                        t = np.array([tok(b0 + x) for x in np.minimum(j, nb - 1)])
+                        o = (t * H + hh) * K + r
+                        ck.acc("q", 0, np.where(ok, o * es, KOOB), 0, es, "decode stage q")
+                        ck.acc("k", 0, np.where(ok, o * es, KOOB), 0, es, "decode stage k")
+                        if p.get("gk"):
+                            ck.acc("gk", 0, np.where(ok, o * 4, KOOB), 0, 4, "decode stage gk")
+                    for u in range(DT * 32 // 64):
+                        e = lane + 64 * u
+                        j, c = e // 32, e % 32
+                        col = 32 * tile + c
+                        ok = (j < nb) & (col < V)
+                        t = np.array([tok(b0 + x) for x in np.minimum(j, nb - 1)])
+                        o = (t * H + hh) * V + col
+                        ck.acc("v", 0, np.where(ok, o * es, KOOB), 0, es, "decode stage v")
+                        if p.get("gv"):
+                            ck.acc("gv", 0, np.where(ok, o * 4, KOOB), 0, 4, "decode stage gv")
+                    for j in range(nb):
+                        ov = (tok(b0 + j) * H + hh) * V + c0
+                        for c in range(4):
+                            st = (c0 + c < V) & (kr == 0)
+                            ck.acc("o", 0, np.where(st, (ov + c) * es, KOOB), 0, es, "decode store o")
+                            if p.get("o32"):
+                                ck.acc("o32", 0, np.where(st, (ov + c) * 4, KOOB), 0, 4, "decode store o32")

@@ -299,3 +299,26 @@ GV = [dict(B=2, T=64, H=2, K=32, V=32), dict(B=2, T=50, H=2, K=64, V=64),
 @pytest.mark.parametrize("c", GV, ids=lambda c: "B{B}-T{T}-H{H}-K{K}-V{V}".format(**c))
 def test_gv_native_in_bounds(c):
     assert gv_op(c["B"], c["T"], c["H"], c["K"], c["V"], cu=c.get("cu")).count > 0
+
+
+DECODE = [dict(B=3, T=1, H=2, K=128, V=128), dict(B=2, T=5, H=1, K=64, V=20),
+          dict(B=1, T=9, H=2, K=36, V=100, cu=[0, 1, 1, 4, 9]), dict(B=2, T=16, H=1, K=128, V=64),
+          dict(B=1, T=3, H=3, K=4, V=7)]
+
+
+@pytest.mark.parametrize("es", [4, 2], ids=["f32", "bf16"])
+@pytest.mark.parametrize("c", DECODE, ids=lambda c: "B{B}-T{T}-H{H}-K{K}-V{V}".format(**c))
+def test_fr_decode_in_bounds(c, es):
+    """The decode kernel's state, input and output accesses, both directions, all optional
+    tensors bound."""
+    B, T, H, K, V = (c[x] for x in "BTHKV")
+    cu = c.get("cu")
+    N = len(cu) - 1 if cu else B
+    rK, rV = B * T * H * K, B * T * H * V
+    sizes = dict(q=rK * es, k=rK * es, gk=rK * 4, v=rV * es, gv=rV * 4, o=rV * es, o32=rV * 4,
+                 h0=N * H * K * V * 4, ht=N * H * K * V * 4)
+    for rev in (False, True):
+        ck = M.Checker(sizes)
+        M.fr_decode(ck, dict(B=B, T=T, H=H, K=K, V=V, cu=cu, gk="gk", gv="gv", s0="h0",
+                             s_fin="ht", o32="o32", reverse=rev), es)
+        assert ck.count > 0

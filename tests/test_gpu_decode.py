@@ -1,0 +1,178 @@
+"""fused_recurrent_gla on sequences of a few tokens (decode steps) vs the float64 oracle.
+
+Without gradients, calls whose longest sequence has at most 4 tokens run on the register-state
+kernel (tops_gla_fused_recurrent_fwd_decode): the per-token recurrence
+h <- h*exp(gk_t)[:,None]*exp(gv_t)[None,:] + k_t v_t^T, o_t = scale h^T q_t
+(tops/cpu/ops/gla/fused_recurrent.py:51-167).  Checked against the oracle's per-token recurrence
+(oracle.gla.fused_recurrent_fwd) for gk, gv, both and no gate, reverse, h0 present or absent,
+K and V off the 8-column tile (K = 4, 36; V = 7, 20, 100), fixed length and varlen (empty and
+one-token sequences, many one-token sequences packed), fp32 and bf16; every case checks that the
+decode entry point ran (and that a 5-token call does not).  The fixed-length per-token entry takes
+the same kernel for T <= 4, and a call with gradients keeps the autograd path (checked against the
+oracle's backward).
+Tolerance: fp32 1e-4, bf16 2e-3 (relative L2).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gla as O
+from _inputs import gla_inputs
+from _gpu import to_dev, seen, host, rel, tol
+
+pytestmark = pytest.mark.gpu
+
+DECODE = "tops_gla_fused_recurrent_fwd_decode"
+
+
+@pytest.fixture
+def calls(monkeypatch):
+    """Names of the C entry points called during the test."""
+    from tops import _native as N
+    seen_calls = []
+    real = N.call
+
+    def spy(name, *args):
+        seen_calls.append(name)
+        return real(name, *args)
+    monkeypatch.setattr(N, "call", spy)
+    return seen_calls
+
+
+CASES = [
+    dict(B=4, T=1, H=4, K=128, V=128, gate="gk", h0=True),          # one decode step
+    dict(B=2, T=3, H=2, K=64, V=64, gate="gv", h0=True),
+    dict(B=2, T=4, H=2, K=128, V=128, gate="both", h0=True),
+    dict(B=1, T=4, H=2, K=36, V=20, gate="gk", h0=True, reverse=True),
+    dict(B=1, T=8, H=3, K=32, V=100, gate="none", cu=[0, 1, 1, 4, 8]),
+    dict(B=1, T=64, H=2, K=128, V=64, gate="gk", h0=True, cu=list(range(65))),   # 64 x 1 token
+    dict(B=3, T=2, H=1, K=4, V=7, gate="gk", h0=True),
+    dict(B=2, T=3, H=2, K=128, V=128, gate="both", h0=True, reverse=True, scale=0.3),
+]
+
+
+def _id(c):
+    return "-".join(f"{k}{v}" for k, v in c.items() if k != "cu") + ("-varlen" if "cu" in c else "")
+
+
+def _gates(cfg, d, B, T, H, V, seed):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    gv = (np.log(1 / (1 + np.exp(-rng.standard_normal((B, T, H, V))))) / 8).astype(np.float32)
+    gk = d["g"] if cfg["gate"] in ("gk", "both") else None
+    return gk, (gv if cfg["gate"] in ("gv", "both") else None)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("cfg", CASES, ids=[_id(c) for c in CASES])
+def test_decode_matches_oracle(cfg, dtype, cuda_device, calls):
+    from tops.ops.gla import fused_recurrent_gla
+    B, T, H, K, V = (cfg[x] for x in "BTHKV")
+    cu = cfg.get("cu")
+    n = len(cu) - 1 if cu else B
+    print(f"decode case {_id(cfg)} {dtype}", flush=True)
+    d = gla_inputs(B, T, H, K, V, seed=T * 5 + K + V, gate_div=4.0, h0=cfg.get("h0", False), N=n)
+    gk, gv = _gates(cfg, d, B, T, H, V, T + K)
+    sc, rev = cfg.get("scale"), cfg.get("reverse", False)
+    dv = lambda x: to_dev(x, torch.float32, cuda_device)
+    q, k, v = (to_dev(d[x], dtype, cuda_device) for x in "qkv")
+    with torch.no_grad():
+        o, ht = fused_recurrent_gla(q, k, v, dv(gk), dv(gv), scale=sc, initial_state=dv(d["h0"]),
+                                    output_final_state=True, reverse=rev, cu_seqlens=cu)
+    torch.cuda.synchronize()
+    assert DECODE in calls
+    ro, rht = O.fused_recurrent_fwd(seen(d["q"], dtype), seen(d["k"], dtype), seen(d["v"], dtype),
+                                    gk, gv, scale=sc, initial_state=d["h0"], output_final_state=True,
+                                    reverse=rev, cu_seqlens=cu)
+    assert o.dtype == dtype and ht.dtype == torch.float32 and tuple(ht.shape) == rht.shape
+    eo, eh = rel(host(o), ro), rel(host(ht), rht)
+    print(f"o {eo:.2e} ht {eh:.2e}")
+    assert eo < tol(dtype) and eh < tol(dtype)
+
+
+def test_decode_fwd_api_without_final_state(cuda_device, calls):
+    """fused_recurrent_gla_fwd takes the decode kernel too; without output_final_state no state
+    comes back, and o is the same as with it."""
+    from tops.ops.gla import fused_recurrent_gla_fwd
+    B, T, H, K, V = 8, 1, 4, 128, 128
+    d = gla_inputs(B, T, H, K, V, seed=11, h0=True)
+    bf = torch.bfloat16
+    q, k, v = (to_dev(d[x], bf, cuda_device) for x in "qkv")
+    g, h0 = to_dev(d["g"], torch.float32, cuda_device), to_dev(d["h0"], torch.float32, cuda_device)
+    o1, ht1 = fused_recurrent_gla_fwd(q, k, v, g, initial_state=h0, output_final_state=True)
+    o2, ht2 = fused_recurrent_gla_fwd(q, k, v, g, initial_state=h0)
+    torch.cuda.synchronize()
+    assert calls.count(DECODE) == 2 and ht2 is None
+    assert torch.equal(o1, o2)
+    ro, rht = O.fused_recurrent_fwd(seen(d["q"], bf), seen(d["k"], bf), seen(d["v"], bf), d["g"],
+                                    initial_state=d["h0"], output_final_state=True)
+    assert rel(host(o1), ro) < 2e-3 and rel(host(ht1), rht) < 2e-3
+
+
+def test_decode_steps_chain(cuda_device, calls):
+    """Eight one-token steps, each starting from the previous step's state, give the outputs
+    and final state of one 8-token call (the state cache of a decode loop; the 8-token call
+    itself runs on the chunk kernels)."""
+    from tops.ops.gla import fused_recurrent_gla
+    B, T, H, K, V = 2, 8, 2, 64, 128
+    d = gla_inputs(B, T, H, K, V, seed=21, h0=True)
+    q, k, v = (to_dev(d[x], torch.float32, cuda_device) for x in "qkv")
+    g, h = to_dev(d["g"], torch.float32, cuda_device), to_dev(d["h0"], torch.float32, cuda_device)
+    outs = []
+    with torch.no_grad():
+        for t in range(T):
+            s = slice(t, t + 1)
+            o_t, h = fused_recurrent_gla(q[:, s], k[:, s], v[:, s], g[:, s], initial_state=h,
+                                         output_final_state=True)
+            outs.append(o_t)
+        o_all, h_all = fused_recurrent_gla(q, k, v, g, initial_state=to_dev(d["h0"], torch.float32,
+                                                                              cuda_device),
+                                           output_final_state=True)
+    torch.cuda.synchronize()
+    assert calls.count(DECODE) == T
+    assert rel(host(torch.cat(outs, 1)), host(o_all)) < 1e-5 and rel(host(h), host(h_all)) < 1e-5
+
+
+def test_longer_call_skips_decode(cuda_device, calls):
+    """A 5-token call goes to the chunk kernels."""
+    from tops.ops.gla import fused_recurrent_gla
+    B, T, H, K, V = 2, 5, 2, 64, 64
+    d = gla_inputs(B, T, H, K, V, seed=41, h0=True)
+    q, k, v = (to_dev(d[x], torch.bfloat16, cuda_device) for x in "qkv")
+    with torch.no_grad():
+        o, ht = fused_recurrent_gla(q, k, v, to_dev(d["g"], torch.float32, cuda_device),
+                                    initial_state=to_dev(d["h0"], torch.float32, cuda_device),
+                                    output_final_state=True)
+    torch.cuda.synchronize()
+    assert DECODE not in calls and "tops_gla_chunk_fwd" in calls
+    ro, rht = O.fused_recurrent_fwd(seen(d["q"], torch.bfloat16), seen(d["k"], torch.bfloat16),
+                                    seen(d["v"], torch.bfloat16), d["g"], initial_state=d["h0"],
+                                    output_final_state=True)
+    assert rel(host(o), ro) < 2e-3 and rel(host(ht), rht) < 2e-3
+
+
+def test_short_call_with_grad_keeps_autograd(cuda_device, calls):
+    """With gradients wanted the autograd path runs.  With gk and gv that is the per-token
+    entry, whose forward takes the decode kernel itself for T <= 4 (o also in fp32 for the gv
+    gradient); its gradients match the oracle's backward."""
+    from tops.ops.gla import fused_recurrent_gla
+    B, T, H, K, V = 2, 4, 2, 32, 48
+    d = gla_inputs(B, T, H, K, V, seed=31, h0=True, grads=True)
+    gk, gv = _gates(dict(gate="both"), d, B, T, H, V, 32)
+    q, k, v = (to_dev(d[x], torch.float32, cuda_device).requires_grad_() for x in "qkv")
+    g = to_dev(gk, torch.float32, cuda_device).requires_grad_()
+    gvt = to_dev(gv, torch.float32, cuda_device).requires_grad_()
+    h0 = to_dev(d["h0"], torch.float32, cuda_device).requires_grad_()
+    o, ht = fused_recurrent_gla(q, k, v, g, gvt, initial_state=h0, output_final_state=True)
+    torch.autograd.backward((o, ht), (to_dev(d["do"], torch.float32, cuda_device),
+                                      to_dev(d["dht"], torch.float32, cuda_device)))
+    torch.cuda.synchronize()
+    assert DECODE not in calls and "tops_gla_fused_recurrent_fwd" in calls
+    ro, rht = O.fused_recurrent_fwd(d["q"], d["k"], d["v"], gk, gv, initial_state=d["h0"],
+                                    output_final_state=True)
+    rdq, rdk, rdv, rdg, rdgv, rdh0 = O.fused_recurrent_bwd(d["q"], d["k"], d["v"], gk, gv, ro,
+                                                           d["do"], d["dht"], initial_state=d["h0"])
+    errs = dict(o=rel(host(o), ro), ht=rel(host(ht), rht), dq=rel(host(q.grad), rdq),
+                dk=rel(host(k.grad), rdk), dv=rel(host(v.grad), rdv), dgk=rel(host(g.grad), rdg),
+                dgv=rel(host(gvt.grad), rdgv), dh0=rel(host(h0.grad), rdh0))
+    print({x: f"{e:.2e}" for x, e in errs.items()})
+    assert all(e < 1e-4 for e in errs.values()), errs

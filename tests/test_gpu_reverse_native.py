@@ -72,7 +72,9 @@ def test_reverse_gla_native(cfg, dtype, cuda_device, calls):
                                     scale=sc, initial_state=to_dev(d["h0"], torch.float32, cuda_device),
                                     output_final_state=True, reverse=True, cu_seqlens=cu)
     torch.cuda.synchronize()
-    assert "tops_chunk_reverse_fwd" in calls
+    # sequences of at most 4 tokens take the decode kernel, longer ones the reverse sweep
+    longest = T if cu is None else max(b - a for a, b in zip(cu[:-1], cu[1:]))
+    assert ("tops_gla_fused_recurrent_fwd_decode" if longest <= 4 else "tops_chunk_reverse_fwd") in calls
     ro, rht = O.fused_recurrent_fwd(seen(d["q"], dtype), seen(d["k"], dtype), seen(d["v"], dtype),
                                     g, None, scale=sc, initial_state=d["h0"],
                                     output_final_state=True, reverse=True, cu_seqlens=cu)
