@@ -473,7 +473,7 @@ __global__ __launch_bounds__(64) void fr_decode_kernel(FrParams p) {
   for (int b0 = 0; b0 < L; b0 += DT) {
     const int nb = min(DT, L - b0);
     // ---- stage tokens b0 .. b0 + nb - 1: element e = lane + 64 u of the [DT][KP] / [DT][32] blocks
-#pragma unroll
+#pragma unroll 2
     for (int u = 0; u < DT * KP / 64; ++u) {
       const int e = lane + 64 * u, j = e / KP, r = e % KP;
       const bool ok = j < nb && r < K;
