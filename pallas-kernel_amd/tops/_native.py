@@ -157,8 +157,22 @@ def call(name: str, *args) -> None:
         raise TopsError(f"{name} failed ({rc}): {msg}")
 
 
+class _Ptr(int):
+    """A device address that keeps its tensor alive.  `call(name, ptr(f(x)), ...)` evaluates
+    every argument before the launch; a bare address of a temporary such as `f(x)` would let
+    the tensor go back to the caching allocator at once, and a later argument's own
+    allocation (a copy, an upload) could then take that block and write it before the kernel
+    that reads it is queued.  Holding the tensor until `call` returns closes that window;
+    freeing it afterwards is stream-ordered behind the launch."""
+
+    def __new__(cls, t):
+        p = super().__new__(cls, t.data_ptr())
+        p.tensor = t
+        return p
+
+
 def ptr(t) -> int | None:
-    return None if t is None else t.data_ptr()
+    return None if t is None else _Ptr(t)
 
 
 def stream() -> int:

@@ -15,6 +15,7 @@ import numpy as np
 import torch
 
 from ... import _native as N
+from ...utils import to_device
 from ._stage import act, cu_host, f32, require
 
 
@@ -59,7 +60,7 @@ def chunk_gated_delta_rule_fwd_h(k, w, u, g=None, gk=None, initial_state=None,
     h = torch.empty(total, H, K, V, device=dev, dtype=kk.dtype)
     v_new = torch.empty(B, T, H, V, device=dev, dtype=torch.float32) if save_new_value else None
     ht = torch.empty(Nseq, H, K, V, device=dev, dtype=torch.float32) if output_final_state else None
-    cu_dev = None if cu is None else torch.tensor(cu, dtype=torch.int32, device=dev)
+    cu_dev = None if cu is None else to_device(cu, dev, torch.int32)
     N.call("tops_delta_rule_fwd_h", N.ptr(kk), N.ptr(ww), N.ptr(uu), N.ptr(g32), N.ptr(gk32), code,
            N.ptr(h0), N.ptr(h), N.ptr(v_new), N.ptr(ht), N.ptr(cu_dev), N.ptr(offs),
            B, T, H, K, V, Nseq, C, N.stream())

@@ -15,6 +15,7 @@ from __future__ import annotations
 import torch
 
 from ... import _native as N
+from ...utils import to_device
 from ._stage import act, chunk_size_ok, cu_host, f32, require
 
 
@@ -44,7 +45,7 @@ def _recurrence(x, y, g, g_gamma, gk, s0, cu, C, reverse, scale, every, states_d
     final = torch.empty((Nseq, H, K, V), device=x.device, dtype=torch.float32) if want_final else None
     cu_dev = None
     if cuh is not None:
-        cu_dev = torch.tensor(cuh, dtype=torch.int32, device=x.device)
+        cu_dev = to_device(cuh, x.device, torch.int32)
     with torch.no_grad():
         N.call("tops_chunk_state_recurrence", N.ptr(xk), N.ptr(yk), code, N.ptr(f32(gk)),
                N.ptr(f32(g)), N.ptr(f32(g_gamma)), N.ptr(f32(s0)), N.ptr(states),

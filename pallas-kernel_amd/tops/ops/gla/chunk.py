@@ -22,7 +22,7 @@ from __future__ import annotations
 
 import torch
 
-from ...utils import ChunkPlan, cdiv
+from ...utils import ChunkPlan, cdiv, to_device
 from .._chunk_core import (GATE_K, GATE_GAMMA, GATE_GAMMA_K, PAIRED, check_qkv, paired_states, chunk_fwd as _core_fwd,
                            chunk_bwd as _core_bwd, states_for_bwd, states_full)
 
@@ -146,7 +146,7 @@ class _Padded:
             self.T = pcu[-1]
             self.cu = pcu
             idx = [pcu[n] + i for n in range(len(cu) - 1) for i in range(cu[n + 1] - cu[n])]
-            self.dest = torch.tensor(idx, device=device, dtype=torch.long)
+            self.dest = to_device(idx, device, torch.int64)
 
     def pad(self, x):
         out = x.new_zeros((x.shape[0], self.T) + tuple(x.shape[2:]))

@@ -30,15 +30,13 @@ import numpy as np
 import torch
 
 from ... import _native as N
-from ...utils import ChunkPlan
+from ...utils import ChunkPlan, to_device
 
 
 def _cu_dev(cu_seqlens, device):
     if cu_seqlens is None:
         return None
-    if isinstance(cu_seqlens, torch.Tensor):
-        return cu_seqlens.to(device=device, dtype=torch.int32).contiguous()
-    return torch.from_numpy(np.ascontiguousarray(np.asarray(cu_seqlens, np.int32))).to(device)
+    return to_device(cu_seqlens, device, torch.int32).contiguous()
 
 
 def _check(q, k, v, gk, gv, initial_state, cu_seqlens, wide_ok: bool = False):
@@ -167,7 +165,7 @@ def time_reversal(T: int, cu_seqlens, device):
         return torch.arange(T - 1, -1, -1, device=device)
     cu = [int(x) for x in (cu_seqlens.tolist() if isinstance(cu_seqlens, torch.Tensor) else cu_seqlens)]
     idx = [cu[n] + cu[n + 1] - 1 - t for n in range(len(cu) - 1) for t in range(cu[n], cu[n + 1])]
-    return torch.tensor(idx, device=device, dtype=torch.long)
+    return to_device(np.asarray(idx, np.int64), device, torch.int64)
 
 
 _REV_GATE_CODE = {"k": 0, "s": 1, "gamma": 2}
@@ -229,6 +227,14 @@ def gv_chunk_native(q, k, v, gv, initial_state, scale, output_final_state, cu_se
 DECODE_MAX_TOKENS = 4    # beyond this the chunk kernels are faster (measured at K = V = 128)
 
 
+def longest_sequence(T, cu_seqlens):
+    """Tokens in the longest sequence of a call (T for fixed length)."""
+    if cu_seqlens is None:
+        return T
+    cu = cu_seqlens.tolist() if isinstance(cu_seqlens, torch.Tensor) else list(cu_seqlens)
+    return max((cu[i + 1] - cu[i] for i in range(len(cu) - 1)), default=0)
+
+
 def decode_native(q, k, v, gk, gv, initial_state, scale, output_final_state, reverse, cu_seqlens):
     """Sequences of at most DECODE_MAX_TOKENS tokens (decode steps against a state cache) on
     the register-state kernel (tops_gla_fused_recurrent_fwd_decode), for calls that need no
@@ -242,13 +248,8 @@ def decode_native(q, k, v, gk, gv, initial_state, scale, output_final_state, rev
         return None
     if q.dtype not in (torch.float32, torch.bfloat16) or K > 128 or K % 4:
         return None
-    if cu_seqlens is None:
-        n, longest = B, T
-    else:
-        cu = cu_seqlens.tolist() if isinstance(cu_seqlens, torch.Tensor) else list(cu_seqlens)
-        n = len(cu) - 1
-        longest = max((cu[i + 1] - cu[i] for i in range(n)), default=0)
-    if longest > DECODE_MAX_TOKENS:
+    n = B if cu_seqlens is None else len(cu_seqlens) - 1
+    if longest_sequence(T, cu_seqlens) > DECODE_MAX_TOKENS:
         return None
     q, k, v = (x.contiguous() for x in (q, k, v))
     o = torch.empty_like(v)

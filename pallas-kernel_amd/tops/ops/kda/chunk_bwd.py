@@ -16,7 +16,7 @@ import math
 import numpy as np
 import torch
 
-from ...utils import ChunkPlan
+from ...utils import ChunkPlan, to_device
 from ..common._stage import cu_host, require
 from .chunk import _bwd, _check, _fwd
 
@@ -32,7 +32,7 @@ def _chunk_starts(B: int, T: int, cu, C: int, device) -> torch.Tensor:
         m = np.zeros(T, bool)
         for a, b in zip(cu[:-1], cu[1:]):
             m[a:b] = (t[a:b] - a) % C == 0
-    return torch.from_numpy(m).to(device)
+    return to_device(m, device, torch.bool)
 
 
 def chunk_kda_bwd(q, k, v, beta, Aqk, Akk, scale, initial_state, do, dht, *, g=None, g_org=None,

@@ -8,8 +8,10 @@ are combined into that one [B,T,H] gate, g + g_gamma (tops/cpu/ops/simple_gla/na
 113-125).  reverse=True (the recurrence iterated from the last token) runs on the reverse
 chunk sweep when no gradient is wanted, else on every sequence reversed in time
 (tops.ops.gla.fused_recurrent.reverse_chunk_native / _reversed_chunk).  Shapes the chunk kernels do not take run the per-token
-kernels of tops.ops.gla.fused_recurrent_gla with the gate as a broadcast view over K.
-Either way the combination is part of the
+kernels of tops.ops.gla.fused_recurrent_gla with the gate as a broadcast view over K.  Calls
+of at most a few tokens per sequence that need no gradient (decode steps) run on the decode
+kernel (tops.ops.gla.fused_recurrent.decode_native) with the gate broadcast over K, which at
+that length costs a few KB.  Either way the combination is part of the
 autograd graph, so the gradients w.r.t. g [B,T,H] and g_gamma [H] come back summed over the
 broadcast axes: the gradient of the reference's lax.scan.
 """
@@ -17,7 +19,8 @@ from __future__ import annotations
 
 import torch
 
-from ..gla.fused_recurrent import _reversed_chunk, fused_recurrent_gla, reverse_chunk_native
+from ..gla.fused_recurrent import (DECODE_MAX_TOKENS, _reversed_chunk, decode_native,
+                                   fused_recurrent_gla, longest_sequence, reverse_chunk_native)
 from .chunk import chunk_simple_gla
 
 
@@ -28,6 +31,20 @@ def fused_recurrent_simple_gla(q, k, v, g=None, g_gamma=None, scale=None, initia
     assert g is None or tuple(g.shape) == (B, T, H), f"g shape {tuple(g.shape)} != {(B, T, H)}"
     assert g_gamma is None or tuple(g_gamma.shape) == (H,), f"g_gamma shape must be ({H},)"
     V = v.shape[-1]
+    if longest_sequence(T, cu_seqlens) <= DECODE_MAX_TOKENS:
+        gk = None
+        if g is not None or g_gamma is not None:
+            gk = torch.zeros(B, T, H, 1, device=q.device, dtype=torch.float32)
+            if g is not None:
+                gk = gk + g.to(torch.float32)[..., None]
+            if g_gamma is not None:
+                gk = gk + torch.as_tensor(g_gamma, device=q.device).to(torch.float32)[None, None, :, None]
+            gk = gk.expand(B, T, H, K)
+        sc = K ** -0.5 if scale is None else scale
+        r = decode_native(q, k, v, gk, None, initial_state, sc, output_final_state, reverse,
+                          cu_seqlens)
+        if r is not None:
+            return r
     if K % 8 == 0 and V % 8 == 0 and K <= 128 and V <= 128:
         gs = None
         if g is not None:

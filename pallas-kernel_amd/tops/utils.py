@@ -46,7 +46,24 @@ def prepare_chunk_indices(cu_seqlens, chunk_size: int) -> np.ndarray:
 def _upload(a: np.ndarray, device) -> torch.Tensor:
     """One int32 host array to the device; staged through pinned memory so the copy is
     queued on the current stream instead of draining it."""
-    t = torch.from_numpy(np.ascontiguousarray(a, np.int32))
+    return to_device(a, device, torch.int32)
+
+
+_NP = {torch.int32: np.int32, torch.int64: np.int64, torch.bool: np.bool_, torch.float32: np.float32}
+
+
+def to_device(a, device, dtype=torch.int32) -> torch.Tensor:
+    """A small host array (list, numpy array or CPU tensor) on `device`, staged through pinned
+    memory and queued on the current stream behind the work already there.  A copy from
+    pageable memory instead was seen to land in a block the caching allocator had just
+    recycled before a queued kernel had finished reading it (a temporary freed on the host
+    while its reader was still queued); device tensors are only converted."""
+    if isinstance(a, torch.Tensor):
+        if a.device.type != "cpu":
+            return a.to(device=device, dtype=dtype)
+        t = a.to(dtype).contiguous()
+    else:
+        t = torch.from_numpy(np.ascontiguousarray(np.asarray(a), _NP[dtype]))
     if torch.device(device).type == "cuda":
         return t.pin_memory().to(device, non_blocking=True)
     return t.to(device)

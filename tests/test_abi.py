@@ -80,3 +80,24 @@ def test_kda_noalloc_rejects_oversize_on_host():
     rc = N._fn("tops_kda_chunk_fwd_noalloc")(*([None] * 11), 0, 1, T, 8, 128, 128, 1, 1,
                                               ctypes.c_float(1.0), None)
     assert rc == -2 and b"static scratch" in L.tops_last_error()
+
+
+def test_ptr_keeps_its_tensor_alive():
+    """A pointer taken from a temporary (ptr(f(x)) inside a call's argument list) holds the
+    tensor until the pointer itself is dropped, so a later argument's allocation cannot take
+    the block before the kernel that reads it is queued."""
+    import gc
+    import weakref
+    import torch
+    from tops import _native as N
+    t = torch.arange(6, dtype=torch.float32) * 2
+    w = weakref.ref(t)
+    p = N.ptr(t)
+    del t
+    gc.collect()
+    assert w() is not None and int(p) == w().data_ptr()
+    assert ctypes.c_void_p.from_param(p) is not None     # still a plain address for ctypes
+    del p
+    gc.collect()
+    assert w() is None
+    assert N.ptr(None) is None

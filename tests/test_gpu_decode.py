@@ -176,3 +176,33 @@ def test_short_call_with_grad_keeps_autograd(cuda_device, calls):
                 dgv=rel(host(gvt.grad), rdgv), dh0=rel(host(h0.grad), rdh0))
     print({x: f"{e:.2e}" for x, e in errs.items()})
     assert all(e < 1e-4 for e in errs.values()), errs
+
+
+@pytest.mark.parametrize("gates", ["g", "gamma", "both", "none"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_simple_gla_decode(gates, dtype, cuda_device, calls):
+    """fused_recurrent_simple_gla without gradients on sequences of at most 4 tokens: per-token
+    g [B,T,H], g_gamma [H], both or none, on the decode kernel (the gate broadcast over K), vs
+    the naive simple-GLA oracle; varlen with an empty and a one-token sequence."""
+    from tops.ops.simple_gla import fused_recurrent_simple_gla
+    from oracle import simple_gla as S
+    from _inputs import simple_gla_inputs
+    B, T, H, K, V = 1, 8, 3, 64, 96
+    cu = [0, 3, 3, 4, 8]
+    d = simple_gla_inputs(B, T, H, K, V, seed=51, h0=True, N=len(cu) - 1)
+    g = d["g"] if gates in ("g", "both") else None
+    gg = d["g_gamma"] if gates in ("gamma", "both") else None
+    q, k, v = (to_dev(d[x], dtype, cuda_device) for x in "qkv")
+    with torch.no_grad():
+        o, ht = fused_recurrent_simple_gla(q, k, v, g=to_dev(g, torch.float32, cuda_device),
+                                           g_gamma=to_dev(gg, torch.float32, cuda_device),
+                                           initial_state=to_dev(d["h0"], torch.float32, cuda_device),
+                                           output_final_state=True, cu_seqlens=cu)
+    torch.cuda.synchronize()
+    assert DECODE in calls
+    ro, rht = S.naive_simple_gla(seen(d["q"], dtype), seen(d["k"], dtype), seen(d["v"], dtype),
+                                 g=g, g_gamma=gg, initial_state=d["h0"], output_final_state=True,
+                                 cu_seqlens=cu)
+    eo, eh = rel(host(o), ro), rel(host(ht), rht)
+    print(f"simple gla decode {gates} {dtype}: o {eo:.2e} ht {eh:.2e}")
+    assert eo < tol(dtype) and eh < tol(dtype)
