@@ -576,3 +576,31 @@ def test_chunk_gla_bwd_with_pl(c, cuda_device):
     with pytest.raises(AssertionError):
         chunk_gla_bwd_with_pl(t["q"][:, :100], t["k"][:, :100], t["v"][:, :100], t["g"][:, :100],
                               None, None, K ** -0.5, None, None, None, t["do"][:, :100], None)
+
+
+def test_stage_inputs_converted_in_one_call_match_fp32(cuda_device):
+    """chunk_gla_bwd_dqkg_ref converts five fp32 operands (g_cumsum, h, dh, dq, dk) inside one
+    call's argument list.  Given them in bf16, each conversion is a temporary; the result must
+    equal, bit for bit, the call given the same (bf16-rounded) values already in fp32 (each
+    temporary stays alive until its kernel is queued)."""
+    from tops.ops.gla import chunk_gla_bwd_dqkg_ref
+    B, T, H, K, V, C = 2, 128, 2, 64, 64, 64
+    NT = T // C
+    rng = np.random.default_rng(7)
+    q, k = (rng.standard_normal((B, T, H, K)).astype(np.float32) for _ in range(2))
+    v, do = (rng.standard_normal((B, T, H, V)).astype(np.float32) for _ in range(2))
+    gc = OC.chunk_local_cumsum(np.log(1 / (1 + np.exp(-rng.standard_normal((B, T, H, K))))) / 4, C)
+    hs = rng.standard_normal((B, NT, H, K, V)) * 0.3
+    dh = rng.standard_normal((B, NT, H, K, V)) * 0.3
+    dq_in, dk_in = rng.standard_normal((2, B, T, H, K))
+    bf = lambda x: to_dev(x, torch.bfloat16, cuda_device)
+    fb = lambda x: to_dev(x, torch.bfloat16, cuda_device).to(torch.float32)
+    f = lambda x: to_dev(x, torch.float32, cuda_device)
+    for _ in range(3):       # repeated, so freed blocks of earlier calls are in the cache too
+        a = chunk_gla_bwd_dqkg_ref(f(q), f(k), f(v), bf(hs), bf(gc), f(do), bf(dh), bf(dq_in),
+                                   bf(dk_in), K ** -0.5, chunk_size=C)
+        b = chunk_gla_bwd_dqkg_ref(f(q), f(k), f(v), fb(hs), fb(gc), f(do), fb(dh), fb(dq_in),
+                                   fb(dk_in), K ** -0.5, chunk_size=C)
+        torch.cuda.synchronize()
+        for x, y in zip(a, b):
+            assert x.dtype == y.dtype == torch.float32 and torch.equal(x, y)
