@@ -296,6 +296,19 @@ int tops_gla_fused_recurrent_fwd_decode(const void* q, const void* k, const void
                                         int V, int N, int dtype, float scale, int reverse,
                                         void* stream);
 
+/* KDA decode steps: the per-token delta rule
+ *   S <- diag(exp g_t) S;  S <- S + beta_t k_t (v_t - S^T k_t)^T;  o_t = S^T (scale q_t)
+ * on the same register-state kernel, for sequences of a few tokens.  q, k [B,T,H,K] and
+ * v [B,T,H,V] (dtype); g [B,T,H,K] natural-log gates fp32; beta [B,T,H] fp32; h0 [N,H,K,V] fp32
+ * or NULL; o [B,T,H,V] (dtype); ht [N,H,K,V] fp32 or NULL.  K <= 128, K % 4 == 0; varlen with
+ * B == 1.  Replaces the decode use of tops.ops.kda.fused_recurrent_kda
+ * (tops/cpu/ops/kda/fused_recurrent.py:71-209; the recurrence of tops/cpu/ops/kda/naive.py:10-118). */
+int tops_kda_fused_recurrent_fwd_decode(const void* q, const void* k, const void* v,
+                                        const float* g, const float* beta, const float* h0,
+                                        void* o, float* ht, const int32_t* cu_seqlens, int B,
+                                        int T, int H, int K, int V, int N, int dtype, float scale,
+                                        void* stream);
+
 /* Bytes of the workspace tops_gla_fused_recurrent_bwd needs (with_gv: a gv gate is used). */
 int64_t tops_gla_fused_recurrent_bwd_workspace(int B, int T, int H, int K, int V, int N,
                                                int with_gv);

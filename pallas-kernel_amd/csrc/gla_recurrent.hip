@@ -44,6 +44,7 @@ struct FrParams {
   int B, T, H, K, V, N, NV;
   float scale;
   int reverse;
+  const float* beta = nullptr;   // KDA decode: the delta-rule rate [B,T,H]
 };
 
 constexpr int kFrBV = 32;   // V tile
@@ -418,10 +419,14 @@ __device__ __forceinline__ float oct_sum(float x) {
   return x;
 }
 
-template <typename TIn, int KP>
+// DELTA: the KDA delta rule instead of the GLA update (tops/cpu/ops/kda/naive.py:10-118):
+// S <- diag(exp g_t) S;  S <- S + beta_t k_t (v_t - S^T k_t)^T;  o_t = S^T (scale q_t), with a
+// second 8-lane reduction for S^T k_t before the update.
+template <typename TIn, int KP, bool DELTA>
 __global__ __launch_bounds__(64) void fr_decode_kernel(FrParams p) {
   constexpr int RL = KP / 8;            // rows per lane
   constexpr int DT = 8;                 // tokens per staged block
+  __shared__ float sB[DT];              // beta (DELTA)
   __shared__ __attribute__((aligned(16))) float sQ[DT][KP];
   __shared__ __attribute__((aligned(16))) float sK[DT][KP];
   __shared__ __attribute__((aligned(16))) float sD[DT][KP];    // exp(gk)
@@ -490,11 +495,50 @@ __global__ __launch_bounds__(64) void fr_decode_kernel(FrParams p) {
       sV[j][c] = ok ? ld_elem(v, o) : 0.f;
       sDV[j][c] = (ok && p.gv) ? fast_exp2(p.gv[o] * kLog2e) : 1.f;
     }
+    if constexpr (DELTA) {
+      if (lane < DT) sB[lane] = lane < nb ? p.beta[(size_t)tok(b0 + lane) * H + hh] : 0.f;
+    }
     __syncthreads();
     for (int j = 0; j < nb; ++j) {
       const float4 v4 = *(const float4*)&sV[j][4 * cq], d4 = *(const float4*)&sDV[j][4 * cq];
       const float vv[4] = {v4.x, v4.y, v4.z, v4.w}, dv[4] = {d4.x, d4.y, d4.z, d4.w};
       float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (DELTA) {
+        // decay, then S^T k over the lane's rows, reduced over the 8 row groups
+        float pr[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i4 = 0; i4 < RL; i4 += 4) {
+          const float4 k4 = *(const float4*)&sK[j][r0 + i4];
+          const float4 g4 = *(const float4*)&sD[j][r0 + i4];
+          const float ks[4] = {k4.x, k4.y, k4.z, k4.w}, ds[4] = {g4.x, g4.y, g4.z, g4.w};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              S[i4 + u][c] *= ds[u];
+              pr[c] += ks[u] * S[i4 + u][c];
+            }
+          }
+        }
+        const float b = sB[j];
+        float du[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) du[c] = b * (vv[c] - oct_sum(pr[c]));
+#pragma unroll
+        for (int i4 = 0; i4 < RL; i4 += 4) {
+          const float4 q4 = *(const float4*)&sQ[j][r0 + i4];
+          const float4 k4 = *(const float4*)&sK[j][r0 + i4];
+          const float qs[4] = {q4.x, q4.y, q4.z, q4.w}, ks[4] = {k4.x, k4.y, k4.z, k4.w};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              S[i4 + u][c] += ks[u] * du[c];
+              acc[c] += S[i4 + u][c] * qs[u];
+            }
+          }
+        }
+      } else {
 #pragma unroll
       for (int i4 = 0; i4 < RL; i4 += 4) {
         const float4 q4 = *(const float4*)&sQ[j][r0 + i4];
@@ -511,6 +555,7 @@ __global__ __launch_bounds__(64) void fr_decode_kernel(FrParams p) {
           }
         }
       }
+      }  // DELTA
 #pragma unroll
       for (int c = 0; c < 4; ++c) acc[c] = oct_sum(acc[c]);
       if (kr == 0) {
@@ -542,13 +587,13 @@ __global__ __launch_bounds__(64) void fr_decode_kernel(FrParams p) {
   }
 }
 
-template <typename TIn>
+template <typename TIn, bool DELTA = false>
 static hipError_t launch_fr_decode(const FrParams& p, hipStream_t s) {
   const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
   dim3 grid(((p.V + 31) / 32) * p.H * p.N);
-  if (kp == 32) hipLaunchKernelGGL((fr_decode_kernel<TIn, 32>), grid, dim3(64), 0, s, p);
-  else if (kp == 64) hipLaunchKernelGGL((fr_decode_kernel<TIn, 64>), grid, dim3(64), 0, s, p);
-  else hipLaunchKernelGGL((fr_decode_kernel<TIn, 128>), grid, dim3(64), 0, s, p);
+  if (kp == 32) hipLaunchKernelGGL((fr_decode_kernel<TIn, 32, DELTA>), grid, dim3(64), 0, s, p);
+  else if (kp == 64) hipLaunchKernelGGL((fr_decode_kernel<TIn, 64, DELTA>), grid, dim3(64), 0, s, p);
+  else hipLaunchKernelGGL((fr_decode_kernel<TIn, 128, DELTA>), grid, dim3(64), 0, s, p);
   return hipGetLastError();
 }
 
@@ -633,6 +678,25 @@ extern "C" int tops_gla_fused_recurrent_fwd_decode(const void* q, const void* k,
              nullptr, cu_seqlens, B, T, H, K, V, N, (V + kFrBV - 1) / kFrBV, scale, reverse ? 1 : 0};
   hipStream_t s = (hipStream_t)stream;
   hipError_t e = dtype == TOPS_BF16 ? launch_fr_decode<uint16_t>(p, s) : launch_fr_decode<float>(p, s);
+  if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
+  return TOPS_OK;
+}
+
+extern "C" int tops_kda_fused_recurrent_fwd_decode(const void* q, const void* k, const void* v,
+                                                   const float* g, const float* beta,
+                                                   const float* h0, void* o, float* ht,
+                                                   const int32_t* cu_seqlens, int B, int T, int H,
+                                                   int K, int V, int N, int dtype, float scale,
+                                                   void* stream) {
+  if (!q || !k || !v || !g || !beta || !o)
+    return tops_set_error(TOPS_ERR_NULL, "kda_fused_recurrent_fwd_decode: null tensor");
+  int rc = fr_check("kda_fused_recurrent_fwd_decode", B, T, H, K, V, N, cu_seqlens, dtype);
+  if (rc != TOPS_OK) return rc;
+  FrParams p{q, k, v, g, nullptr, h0, nullptr, nullptr, o, nullptr, ht, nullptr, nullptr, nullptr,
+             nullptr, nullptr, cu_seqlens, B, T, H, K, V, N, (V + kFrBV - 1) / kFrBV, scale, 0, beta};
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = dtype == TOPS_BF16 ? launch_fr_decode<uint16_t, true>(p, s)
+                                    : launch_fr_decode<float, true>(p, s);
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   return TOPS_OK;
 }

@@ -5,7 +5,9 @@ The reference runs the per-token delta rule as a scan:
     S' = S * exp(g_t);  S = S' + beta_t k_t (v_t - k_t^T S')^T;  o_t = S^T (scale q_t).
 Here the same recurrence runs through the chunked KDA kernels (the chunk form is an exact
 rewrite of the per-token recurrence, equal up to fp32 rounding), which keeps the state on
-chip across a chunk instead of re-reading it per token.
+chip across a chunk instead of re-reading it per token; calls of at most a few tokens per
+sequence that need no gradient (decode steps) run the per-token recurrence itself on the
+register-state decode kernel, which reads and writes each state once.
 
 FLA options (keyword-only here, so the accelerator tier's positional order
 q, k, v, g, beta, scale, initial_state, output_final_state is kept):
@@ -24,8 +26,35 @@ from __future__ import annotations
 
 import torch
 
+from ... import _native as N
+from ...utils import to_device
+from ..gla.fused_recurrent import DECODE_MAX_TOKENS, longest_sequence
 from .chunk import _prologue, chunk_kda
 from .l2norm import l2norm
+
+
+def _decode(q, k, v, g, beta, scale, h0, output_final_state, cu_seqlens, n):
+    """Sequences of at most DECODE_MAX_TOKENS tokens that need no gradient (decode steps) on the
+    register-state kernel (tops_kda_fused_recurrent_fwd_decode).  Returns (o, ht or None) or
+    None where it does not apply."""
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad
+                                       for t in (q, k, v, g, beta, h0)):
+        return None
+    if q.dtype not in (torch.float32, torch.bfloat16) or K > 128 or K % 4:
+        return None
+    if longest_sequence(T, cu_seqlens) > DECODE_MAX_TOKENS:
+        return None
+    q, k, v = (x.contiguous() for x in (q, k, v))
+    f32 = lambda x: None if x is None else x.contiguous().to(torch.float32)  # noqa: E731
+    o = torch.empty_like(v)
+    ht = torch.empty(n, H, K, V, device=q.device, dtype=torch.float32) if output_final_state else None
+    cu = None if cu_seqlens is None else to_device(cu_seqlens, q.device, torch.int32)
+    N.call("tops_kda_fused_recurrent_fwd_decode", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(f32(g)),
+           N.ptr(f32(beta)), N.ptr(f32(h0)), N.ptr(o), N.ptr(ht), N.ptr(cu), B, T, H, K, V, n,
+           N.dtype_code(q.dtype), float(K ** -0.5 if scale is None else scale), N.stream())
+    return o, ht
 
 
 def _require(cond, msg):
@@ -73,8 +102,10 @@ def _run(q, k, v, g, beta, A_log, dt_bias, scale, initial_state, output_final_st
     q, k, v, g = _prologue(q, k, v, g, A_log, dt_bias, use_gate_in_kernel, lower_bound, False)
     if q.dtype != v.dtype:        # e.g. bf16 q, k with fp32 v: run in float32
         q, k, v = (x.to(torch.float32) for x in (q, k, v))
-    o, ht = chunk_kda(q, k, v, g, beta, scale=scale, initial_state=h0,
-                      output_final_state=output_final_state, cu_seqlens=cu_seqlens)
+    r = _decode(q, k, v, g, beta, scale, h0, output_final_state, cu_seqlens, n)
+    o, ht = r if r is not None else chunk_kda(q, k, v, g, beta, scale=scale, initial_state=h0,
+                                              output_final_state=output_final_state,
+                                              cu_seqlens=cu_seqlens)
     if ht is not None and transpose_state_layout:
         ht = ht.transpose(-1, -2)
     return o.to(out_dtype), ht

@@ -561,6 +561,10 @@ def fr_decode(ck: Checker, p: dict, es: int):
                         ck.acc("v", 0, np.where(ok, o * es, KOOB), 0, es, "decode stage v")
                         if p.get("gv"):
                             ck.acc("gv", 0, np.where(ok, o * 4, KOOB), 0, 4, "decode stage gv")
+                    if p.get("beta"):         # the KDA instance: lanes < nb read beta [B,T,H]
+                        bt = np.array([tok(b0 + min(x, nb - 1)) for x in range(64)])
+                        ck.acc("beta", 0, np.where(lane < nb, (bt * H + hh) * 4, KOOB), 0, 4,
+                               "decode stage beta")
                     for j in range(nb):
                         ov = (tok(b0 + j) * H + hh) * V + c0
                         for c in range(4):

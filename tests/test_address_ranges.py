@@ -316,9 +316,12 @@ def test_fr_decode_in_bounds(c, es):
     N = len(cu) - 1 if cu else B
     rK, rV = B * T * H * K, B * T * H * V
     sizes = dict(q=rK * es, k=rK * es, gk=rK * 4, v=rV * es, gv=rV * 4, o=rV * es, o32=rV * 4,
-                 h0=N * H * K * V * 4, ht=N * H * K * V * 4)
+                 h0=N * H * K * V * 4, ht=N * H * K * V * 4, beta=B * T * H * 4)
     for rev in (False, True):
         ck = M.Checker(sizes)
         M.fr_decode(ck, dict(B=B, T=T, H=H, K=K, V=V, cu=cu, gk="gk", gv="gv", s0="h0",
                              s_fin="ht", o32="o32", reverse=rev), es)
         assert ck.count > 0
+    ck = M.Checker(sizes)        # the KDA instance (tops_kda_fused_recurrent_fwd_decode)
+    M.fr_decode(ck, dict(B=B, T=T, H=H, K=K, V=V, cu=cu, gk="gk", beta="beta", s0="h0",
+                         s_fin="ht"), es)

@@ -391,3 +391,52 @@ def test_chunk_kda_gate_in_kernel(cuda_device):
         assert e < 2e-3, (x, e)
     # dg lands in g's dtype (bf16)
     assert g.grad.dtype == torch.bfloat16 and rel(host(g.grad), r["dg"]) < 4e-3
+
+
+DECODE_CASES = [
+    dict(B=4, T=1, H=2, HV=2, K=128, V=128, gate="base", l2=True, h0=True),
+    dict(B=2, T=3, H=1, HV=2, K=64, V=96, gate="full", lb=-0.5, l2=True, h0=True),
+    dict(B=2, T=4, H=2, HV=2, K=40, V=24, gate=None, l2=False, h0=True),
+    dict(B=1, T=6, H=2, HV=4, K=64, V=64, gate="base", l2=True, h0=True, cu=[0, 1, 4, 6],
+         transpose=True),
+    dict(B=1, T=2, H=2, HV=2, K=32, V=32, gate=None, l2=False, h0=False, cu=[0, 1, 2]),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("cfg", DECODE_CASES, ids=_fid)
+def test_fused_recurrent_kda_decode(cfg, dtype, cuda_device, monkeypatch):
+    """fused_recurrent_kda without gradients on sequences of at most 4 tokens runs on the KDA
+    decode kernel (tops_kda_fused_recurrent_fwd_decode), with the FLA options (gate in kernel,
+    lower bound, q / k L2 norm, grouped heads, varlen, transposed state layout); o and the final
+    state against the oracle."""
+    from tops import _native as N
+    from tops.ops.kda import fused_recurrent_kda
+    names, real = [], N.call
+    monkeypatch.setattr(N, "call", lambda name, *a: (names.append(name), real(name, *a))[1])
+    d = _fr_inputs(cfg, seed=cfg["T"] + cfg["K"] + 1)
+    tr = cfg.get("transpose", False)
+    dev = cuda_device
+    q, k, v = (to_dev(d[x], dtype, dev) for x in "qkv")
+    g, beta = to_dev(d["g"], torch.float32, dev), to_dev(d["beta"], torch.float32, dev)
+    h0 = to_dev(d["h0"], torch.float32, dev)
+    if h0 is not None and tr:
+        h0 = h0.transpose(-1, -2).contiguous()
+    kw = {}
+    if cfg["gate"]:
+        kw = dict(A_log=to_dev(d["A_log"], torch.float32, dev),
+                  dt_bias=to_dev(d["dt_bias"], torch.float32, dev), use_gate_in_kernel=True,
+                  lower_bound=cfg.get("lb"))
+    scale = cfg["K"] ** -0.5
+    with torch.no_grad():
+        o, ht = fused_recurrent_kda(q, k, v, g, beta, scale, h0, True,
+                                    use_qk_l2norm_in_kernel=cfg["l2"], cu_seqlens=cfg.get("cu"),
+                                    transpose_state_layout=tr, **kw)
+    torch.cuda.synchronize()
+    assert "tops_kda_fused_recurrent_fwd_decode" in names and "tops_kda_chunk_fwd" not in names
+    r = _fr_oracle(cfg, d, dtype, scale)
+    hto = host(ht)
+    eo, eh = rel(host(o), r["o"]), rel(np.swapaxes(hto, -1, -2) if tr else hto, r["ht"])
+    print(f"kda decode {_fid(cfg)} {dtype}: o {eo:.2e} ht {eh:.2e}")
+    t = 1e-4 if (dtype == torch.float32 or cfg["l2"]) else 2e-3
+    assert eo < (2e-3 if dtype == torch.bfloat16 else t) and eh < t
