@@ -146,7 +146,63 @@ def secondary(dev, iters=10, configs=(2, 4, 5)):
         out.append(_config5(dev, gen, iters))
     if 6 in configs:
         out.append(_neighbours(dev, gen, iters))
+    if 7 in configs:
+        out.append(_decode(dev, gen, iters))
     return out
+
+
+def _decode(dev, gen, iters):
+    """Decode steps (one token per sequence against a state cache), the route the reference's
+    layer takes for q_len <= 64: fused_recurrent_gla (B256 H16 K=V=128, gk) and
+    fused_recurrent_kda (B64 H32 K=V=128), bf16 inputs, fp32 states.  Each decode kernel is
+    timed per launch with HIP events on its stream; its bytes are the state read and written
+    (2 K V 4 per sequence and head) plus the token's inputs and output."""
+    import torch
+    from tops import _native as NT
+    from tops.ops.gla import fused_recurrent_gla
+    from tops.ops.kda import fused_recurrent_kda
+    bf = torch.bfloat16
+    D = 128
+    cases = []
+    Bg, Hg = 256, 16
+    q1, k1, v1 = (torch.randn(Bg, 1, Hg, D, device=dev, generator=gen).to(bf) for _ in range(3))
+    g1 = torch.nn.functional.logsigmoid(torch.randn(Bg, 1, Hg, D, device=dev, generator=gen)) / 16
+    s1 = torch.randn(Bg, Hg, D, D, device=dev, generator=gen) * 0.1
+    cases.append(("tops_gla_fused_recurrent_fwd_decode", "fused_recurrent_gla B256 T1 H16 K=V=128 gk",
+                  Bg * Hg * (2 * D * D * 4 + 3 * D * 2 + D * 4 + D * 2),
+                  lambda: fused_recurrent_gla(q1, k1, v1, g1, initial_state=s1, output_final_state=True)))
+    Bk, Hk = 64, 32
+    q2, k2 = (torch.nn.functional.normalize(torch.randn(Bk, 1, Hk, D, device=dev, generator=gen), dim=-1).to(bf)
+              for _ in range(2))
+    v2 = torch.randn(Bk, 1, Hk, D, device=dev, generator=gen).to(bf)
+    g2 = torch.nn.functional.logsigmoid(torch.randn(Bk, 1, Hk, D, device=dev, generator=gen)) / 16
+    b2 = torch.sigmoid(torch.randn(Bk, 1, Hk, device=dev, generator=gen))
+    s2 = torch.randn(Bk, Hk, D, D, device=dev, generator=gen) * 0.1
+    cases.append(("tops_kda_fused_recurrent_fwd_decode", "fused_recurrent_kda B64 T1 H32 K=V=128",
+                  Bk * Hk * (2 * D * D * 4 + 3 * D * 2 + D * 4 + 4 + D * 2),
+                  lambda: fused_recurrent_kda(q2, k2, v2, g2, b2, None, s2, True)))
+    rows = []
+    with torch.no_grad():
+        for _, _, _, f in cases:
+            f()
+        torch.cuda.synchronize()
+        NT.enable_timing(True)
+        for _ in range(iters):
+            for _, _, _, f in cases:
+                f()
+        torch.cuda.synchronize()
+        ev = NT.timing_events()
+        NT.enable_timing(False)
+    for name, shape, nbytes, _ in cases:
+        ms = [e0.elapsed_time(e1) for e0, e1 in ev.get(name, [])]
+        if not ms:
+            continue
+        avg = sum(ms) / len(ms)
+        gbs = nbytes / (avg * 1e-3) / 1e9
+        rows.append({"entry": name, "shape": shape, "avg_ms": round(avg, 4), "launches": len(ms),
+                     "algo_bytes": nbytes, "hbm_gbs": round(gbs, 1),
+                     "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
+    return {"config": "decode steps (state-cache bound)", "kernels": rows}
 
 
 def _neighbours(dev, gen, iters):
@@ -322,8 +378,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the config 2 / 4 / 5 lines")
-    ap.add_argument("--configs", default="2,4,5,6",
-                    help="secondary configs to measure (6: the gate / norm / conv kernels)")
+    ap.add_argument("--configs", default="2,4,5,6,7",
+                    help="secondary configs to measure (6: the gate / norm / conv kernels, "
+                         "7: decode steps)")
     ap.add_argument("--only-secondary", action="store_true",
                     help="measure only the secondary configs (for profiling them alone)")
     ap.add_argument("--copy-calibration", action="store_true",
