@@ -423,22 +423,26 @@ __device__ __forceinline__ float oct_sum(float x) {
 // S <- diag(exp g_t) S;  S <- S + beta_t k_t (v_t - S^T k_t)^T;  o_t = S^T (scale q_t), with a
 // second 8-lane reduction for S^T k_t before the update.
 template <typename TIn, int KP, bool DELTA>
-__global__ __launch_bounds__(64) void fr_decode_kernel(FrParams p) {
+__global__ __launch_bounds__(256) void fr_decode_kernel(FrParams p) {
   constexpr int RL = KP / 8;            // rows per lane
   constexpr int DT = 8;                 // tokens per staged block
+  constexpr int WV = 4;                 // waves (32-column tiles) per workgroup
   __shared__ float sB[DT];              // beta (DELTA)
   __shared__ __attribute__((aligned(16))) float sQ[DT][KP];
   __shared__ __attribute__((aligned(16))) float sK[DT][KP];
   __shared__ __attribute__((aligned(16))) float sD[DT][KP];    // exp(gk)
-  __shared__ __attribute__((aligned(16))) float sV[DT][32];
-  __shared__ __attribute__((aligned(16))) float sDV[DT][32];   // exp(gv)
-  const int lane = threadIdx.x;
+  __shared__ __attribute__((aligned(16))) float sV[DT][32 * WV];
+  __shared__ __attribute__((aligned(16))) float sDV[DT][32 * WV];   // exp(gv)
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kr = lane & 7, cq = lane >> 3;
   const int H = p.H, K = p.K, V = p.V;
-  const int NT = (V + 31) / 32;
-  const int tile = blockIdx.x % NT;
-  const int hh = (blockIdx.x / NT) % H;
-  const int n = blockIdx.x / (NT * H);
+  const int NT = (V + 31) / 32, NG = (NT + WV - 1) / WV;
+  const int tg = blockIdx.x % NG;       // the workgroup's group of WV tiles (the same tokens)
+  const int tile = WV * tg + wave;      // this wave's tile; waves past the last one only stage
+  const bool live = tile < NT;
+  const int hh = (blockIdx.x / NG) % H;
+  const int n = blockIdx.x / (NG * H);
   int bos, L;
   if (p.cu_seqlens) {
     bos = p.cu_seqlens[n];
@@ -456,6 +460,10 @@ __global__ __launch_bounds__(64) void fr_decode_kernel(FrParams p) {
 #pragma unroll
   for (int c = 0; c < 4; ++c) cok[c] = c0 + c < V;
   const bool vec = (V % 4) == 0 && cok[3];
+  if (!live) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) cok[c] = false;
+  }
   const size_t sbase = ((size_t)n * H + hh) * K * V;
   const TIn* q = (const TIn*)p.q;
   const TIn* kk = (const TIn*)p.k;
@@ -467,7 +475,7 @@ __global__ __launch_bounds__(64) void fr_decode_kernel(FrParams p) {
   for (int i = 0; i < RL; ++i) {
     const bool rok = qok[i / 4];
     const size_t o = sbase + (size_t)(r0 + i) * V + c0;
-    if (p.s0 && rok && vec) {
+    if (p.s0 && rok && vec && live) {
       const float4 x = *(const float4*)(p.s0 + o);
       S[i][0] = x.x; S[i][1] = x.y; S[i][2] = x.z; S[i][3] = x.w;
     } else {
@@ -477,10 +485,11 @@ __global__ __launch_bounds__(64) void fr_decode_kernel(FrParams p) {
   }
   for (int b0 = 0; b0 < L; b0 += DT) {
     const int nb = min(DT, L - b0);
-    // ---- stage tokens b0 .. b0 + nb - 1: element e = lane + 64 u of the [DT][KP] / [DT][32] blocks
+    // ---- stage tokens b0 .. b0 + nb - 1 for the workgroup's tiles: element e = tid + 256 u of
+    // the [DT][KP] / [DT][32 WV] blocks
 #pragma unroll 2
-    for (int u = 0; u < DT * KP / 64; ++u) {
-      const int e = lane + 64 * u, j = e / KP, r = e % KP;
+    for (int u = 0; u < DT * KP / 256; ++u) {
+      const int e = tid + 256 * u, j = e / KP, r = e % KP;
       const bool ok = j < nb && r < K;
       const size_t o = ok ? ((size_t)tok(b0 + j) * H + hh) * K + r : 0;
       sQ[j][r] = ok ? ld_elem(q, o) * p.scale : 0.f;
@@ -488,19 +497,20 @@ __global__ __launch_bounds__(64) void fr_decode_kernel(FrParams p) {
       sD[j][r] = (ok && p.gk) ? fast_exp2(p.gk[o] * kLog2e) : 1.f;
     }
 #pragma unroll
-    for (int u = 0; u < DT * 32 / 64; ++u) {
-      const int e = lane + 64 * u, j = e / 32, c = e % 32, col = 32 * tile + c;
+    for (int u = 0; u < DT * 32 * WV / 256; ++u) {
+      const int e = tid + 256 * u, j = e / (32 * WV), c = e % (32 * WV), col = 32 * WV * tg + c;
       const bool ok = j < nb && col < V;
       const size_t o = ok ? ((size_t)tok(b0 + j) * H + hh) * V + col : 0;
       sV[j][c] = ok ? ld_elem(v, o) : 0.f;
       sDV[j][c] = (ok && p.gv) ? fast_exp2(p.gv[o] * kLog2e) : 1.f;
     }
     if constexpr (DELTA) {
-      if (lane < DT) sB[lane] = lane < nb ? p.beta[(size_t)tok(b0 + lane) * H + hh] : 0.f;
+      if (tid < DT) sB[tid] = tid < nb ? p.beta[(size_t)tok(b0 + tid) * H + hh] : 0.f;
     }
     __syncthreads();
     for (int j = 0; j < nb; ++j) {
-      const float4 v4 = *(const float4*)&sV[j][4 * cq], d4 = *(const float4*)&sDV[j][4 * cq];
+      const float4 v4 = *(const float4*)&sV[j][32 * wave + 4 * cq];
+      const float4 d4 = *(const float4*)&sDV[j][32 * wave + 4 * cq];
       const float vv[4] = {v4.x, v4.y, v4.z, v4.w}, dv[4] = {d4.x, d4.y, d4.z, d4.w};
       float acc[4] = {0.f, 0.f, 0.f, 0.f};
       if constexpr (DELTA) {
@@ -571,7 +581,7 @@ __global__ __launch_bounds__(64) void fr_decode_kernel(FrParams p) {
     }
     __syncthreads();   // the block's tokens are consumed before the next block is staged
   }
-  if (p.s_fin) {
+  if (p.s_fin && live) {
 #pragma unroll
     for (int i = 0; i < RL; ++i) {
       if (!qok[i / 4]) continue;
@@ -590,10 +600,10 @@ __global__ __launch_bounds__(64) void fr_decode_kernel(FrParams p) {
 template <typename TIn, bool DELTA = false>
 static hipError_t launch_fr_decode(const FrParams& p, hipStream_t s) {
   const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
-  dim3 grid(((p.V + 31) / 32) * p.H * p.N);
-  if (kp == 32) hipLaunchKernelGGL((fr_decode_kernel<TIn, 32, DELTA>), grid, dim3(64), 0, s, p);
-  else if (kp == 64) hipLaunchKernelGGL((fr_decode_kernel<TIn, 64, DELTA>), grid, dim3(64), 0, s, p);
-  else hipLaunchKernelGGL((fr_decode_kernel<TIn, 128, DELTA>), grid, dim3(64), 0, s, p);
+  dim3 grid((((p.V + 31) / 32 + 3) / 4) * p.H * p.N);
+  if (kp == 32) hipLaunchKernelGGL((fr_decode_kernel<TIn, 32, DELTA>), grid, dim3(256), 0, s, p);
+  else if (kp == 64) hipLaunchKernelGGL((fr_decode_kernel<TIn, 64, DELTA>), grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((fr_decode_kernel<TIn, 128, DELTA>), grid, dim3(256), 0, s, p);
   return hipGetLastError();
 }
 

@@ -506,43 +506,54 @@ def kda_wy(ck: Checker, p: dict, es: int, fused: bool = False):
 
 # --------------------------------------------------------------------------- fr_decode_kernel
 def fr_decode(ck: Checker, p: dict, es: int):
-    """fr_decode_kernel<TIn, KP> (csrc/gla_recurrent.hip): one 64-lane wave per (sequence, head,
-    32-column tile); lane (kr, cq) = (lane % 8, lane / 8) owns rows RL kr .. RL kr + RL - 1
+    """fr_decode_kernel<TIn, KP> (csrc/gla_recurrent.hip): a 256-thread workgroup per (sequence,
+    head, group tg of four 32-column tiles); wave w holds tile 4 tg + w (a wave past the last
+    tile only stages), and its lane (kr, cq) = (lane % 8, lane / 8) owns rows RL kr .. + RL - 1
     (RL = KP / 8) and columns 32 tile + 4 cq .. + 3 of the state.  Tokens are staged 8 at a
-    time: element e = lane + 64 u of the [8][KP] q / k / gk block and of the [8][32] v / gv block.
+    time for the whole workgroup: element e = tid + 256 u of the [8][KP] q / k / gk block and of
+    the [8][128] v / gv block (columns 128 tg + c).
     p: B, T, H, K, V, cu (host list or None), reverse, and which of gk / gv / s0 / s_fin / o32
     are bound.  Plain pointer accesses (no buffer resource)."""
     B, T, H, K, V = (p[x] for x in ("B", "T", "H", "K", "V"))
     cu = p.get("cu")
     N = len(cu) - 1 if cu is not None else B
     KP = _kp(K)
-    RL, DT = KP // 8, 8
-    lane = np.arange(64, dtype=np.int64)
+    RL, DT, WV = KP // 8, 8, 4
+    tid, lane, wave = _tid(256)
     kr, cq = lane & 7, lane >> 3
     r0 = RL * kr
     NT = (V + 31) // 32
+    NG = (NT + WV - 1) // WV
     for n in range(N):
         bos, L = (cu[n], cu[n + 1] - cu[n]) if cu is not None else (n * T, T)
         tok = (lambda j: bos + L - 1 - j) if p.get("reverse") else (lambda j: bos + j)
         for hh in range(H):
             sbase = (n * H + hh) * K * V
-            for tile in range(NT):
+            for tg in range(NG):
+                tile = WV * tg + wave
+                live = tile < NT
                 c0 = 32 * tile + 4 * cq
                 vec = (V % 4 == 0) & (c0 + 3 < V)
                 for i in range(RL):
                     rok = r0 + 4 * (i // 4) < K
-                    for nm in ("s0", "s_fin"):
-                        if not p.get(nm):
-                            continue
-                        o = sbase + (r0 + i) * V + c0
-                        ck.acc(p[nm], 0, np.where(rok & vec, o * 4, KOOB), 0, 16, f"decode {nm} (vector)")
+                    o = sbase + (r0 + i) * V + c0
+                    if p.get("s0"):
+                        ck.acc(p["s0"], 0, np.where(rok & vec & live, o * 4, KOOB), 0, 16,
+                               "decode s0 (vector)")
                         for c in range(4):
-                            ok = rok & ~vec & (c0 + c < V)
-                            ck.acc(p[nm], 0, np.where(ok, (o + c) * 4, KOOB), 0, 4, f"decode {nm}")
+                            ok = rok & ~(vec & live) & live & (c0 + c < V)
+                            ck.acc(p["s0"], 0, np.where(ok, (o + c) * 4, KOOB), 0, 4, "decode s0")
+                    if p.get("s_fin"):
+                        ck.acc(p["s_fin"], 0, np.where(rok & vec & live, o * 4, KOOB), 0, 16,
+                               "decode s_fin (vector)")
+                        for c in range(4):
+                            ok = rok & ~vec & live & (c0 + c < V)
+                            ck.acc(p["s_fin"], 0, np.where(ok, (o + c) * 4, KOOB), 0, 4,
+                                   "decode s_fin")
                 for b0 in range(0, L, DT):
                     nb = min(DT, L - b0)
-                    for u in range(DT * KP // 64):
-                        e = lane + 64 * u
+                    for u in range(DT * KP // 256):
+                        e = tid + 256 * u
                         j, r = e // KP, e % KP
                         ok = (j < nb) & (r < K)
                         t = np.array([tok(b0 + x) for x in np.minimum(j, nb - 1)])
@@ -551,24 +562,24 @@ def fr_decode(ck: Checker, p: dict, es: int):
                         ck.acc("k", 0, np.where(ok, o * es, KOOB), 0, es, "decode stage k")
                         if p.get("gk"):
                             ck.acc("gk", 0, np.where(ok, o * 4, KOOB), 0, 4, "decode stage gk")
-                    for u in range(DT * 32 // 64):
-                        e = lane + 64 * u
-                        j, c = e // 32, e % 32
-                        col = 32 * tile + c
+                    for u in range(DT * 32 * WV // 256):
+                        e = tid + 256 * u
+                        j, c = e // (32 * WV), e % (32 * WV)
+                        col = 32 * WV * tg + c
                         ok = (j < nb) & (col < V)
                         t = np.array([tok(b0 + x) for x in np.minimum(j, nb - 1)])
                         o = (t * H + hh) * V + col
                         ck.acc("v", 0, np.where(ok, o * es, KOOB), 0, es, "decode stage v")
                         if p.get("gv"):
                             ck.acc("gv", 0, np.where(ok, o * 4, KOOB), 0, 4, "decode stage gv")
-                    if p.get("beta"):         # the KDA instance: lanes < nb read beta [B,T,H]
-                        bt = np.array([tok(b0 + min(x, nb - 1)) for x in range(64)])
-                        ck.acc("beta", 0, np.where(lane < nb, (bt * H + hh) * 4, KOOB), 0, 4,
+                    if p.get("beta"):         # the KDA instance: threads < nb read beta [B,T,H]
+                        bt = np.array([tok(b0 + min(x, nb - 1)) for x in range(256)])
+                        ck.acc("beta", 0, np.where(tid < nb, (bt * H + hh) * 4, KOOB), 0, 4,
                                "decode stage beta")
                     for j in range(nb):
                         ov = (tok(b0 + j) * H + hh) * V + c0
                         for c in range(4):
-                            st = (c0 + c < V) & (kr == 0)
+                            st = live & (c0 + c < V) & (kr == 0)
                             ck.acc("o", 0, np.where(st, (ov + c) * es, KOOB), 0, es, "decode store o")
                             if p.get("o32"):
                                 ck.acc("o32", 0, np.where(st, (ov + c) * 4, KOOB), 0, 4, "decode store o32")

@@ -303,7 +303,7 @@ def test_gv_native_in_bounds(c):
 
 DECODE = [dict(B=3, T=1, H=2, K=128, V=128), dict(B=2, T=5, H=1, K=64, V=20),
           dict(B=1, T=9, H=2, K=36, V=100, cu=[0, 1, 1, 4, 9]), dict(B=2, T=16, H=1, K=128, V=64),
-          dict(B=1, T=3, H=3, K=4, V=7)]
+          dict(B=1, T=3, H=3, K=4, V=7), dict(B=2, T=3, H=2, K=64, V=160)]
 
 
 @pytest.mark.parametrize("es", [4, 2], ids=["f32", "bf16"])

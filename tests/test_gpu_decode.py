@@ -48,6 +48,7 @@ CASES = [
     dict(B=1, T=64, H=2, K=128, V=64, gate="gk", h0=True, cu=list(range(65))),   # 64 x 1 token
     dict(B=3, T=2, H=1, K=4, V=7, gate="gk", h0=True),
     dict(B=2, T=3, H=2, K=128, V=128, gate="both", h0=True, reverse=True, scale=0.3),
+    dict(B=2, T=3, H=2, K=64, V=160, gate="both", h0=True),        # two tile groups, 3 idle waves
 ]
 
 
