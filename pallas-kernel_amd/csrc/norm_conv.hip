@@ -28,9 +28,12 @@
 
 namespace tops {
 
-// sigmoid from e = exp(-|x|) and the hardware reciprocal (1 ulp); no overflow for any x
+// sigmoid from e = exp(-|x|) and the hardware reciprocal (1 ulp); no overflow for any x.
+// e is the hardware 2^x of -|x| log2(e): its relative error, about |x| 2^-24 from rounding
+// the product, moves the sigmoid by at most ~1e-7 for |x| < 16 (and e itself is below 2^-23
+// beyond that), two VALU operations instead of the library expf's range reduction.
 __device__ __forceinline__ float sigm(float x) {
-  const float e = expf(-fabsf(x));
+  const float e = fast_exp2(-fabsf(x) * kLog2e);
   const float r = __builtin_amdgcn_rcpf(1.f + e);
   return x >= 0.f ? r : e * r;
 }
@@ -586,16 +589,15 @@ __global__ void __launch_bounds__(256) short_conv_bwd_kernel(
       // the next group's loads are issued before this group is processed
       float gy2[4][VC], xn2[4][VC];
       load_group(t - 4, gy2, xn2);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int cur = t - s;
-        float g[VC];
+      // one token of the walk: dx at cur from the pre-activation gradients in the window,
+      // the weight / bias partials, then both windows shift one token toward the past
+      auto step = [&](const float (&gy)[VC], float (&g)[VC]) {
 #pragma unroll
         for (int c = 0; c < VC; ++c) {
           float pre = bias[c];
 #pragma unroll
           for (int j = 0; j < MAXW; ++j) pre += xw[c][j] * wt[c][j];
-          const float dpt = dpre_of(pre, gyv[s][c]);
+          const float dpt = dpre_of(pre, gy[c]);
           // dx[cur] = sum_i dpre[cur + i] w[W - 1 - i]
           float a = dpt * wt[c][MAXW - 1];
 #pragma unroll
@@ -604,13 +606,30 @@ __global__ void __launch_bounds__(256) short_conv_bwd_kernel(
 #pragma unroll
           for (int j = 0; j < MAXW; ++j) pw[c][j] += xw[c][j] * dpt;
           pb[c] += dpt;
-          // shift toward the past (undone below when the sequence changes)
 #pragma unroll
           for (int i = MAXW - 2; i > 0; --i) dp[c][i] = dp[c][i - 1];
           dp[c][0] = dpt;
 #pragma unroll
           for (int j = MAXW - 1; j > 0; --j) xw[c][j] = xw[c][j - 1];
         }
+      };
+      if (t - 4 >= r0 && t - 3 - MAXW >= sc.bos) {
+        // the whole group and the next token lie inside the run and inside one sequence with
+        // full windows: no branch, so the window shifts compile to register renaming
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          float g[VC];
+          step(gyv[s], g);
+          VecC<TX, VC>::st(dx + (long long)(t - s) * D + d0, g);
+#pragma unroll
+          for (int c = 0; c < VC; ++c) xw[c][0] = xn[s][c];
+        }
+      } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int cur = t - s;
+        float g[VC];
+        step(gyv[s], g);
         VecC<TX, VC>::st(dx + (long long)cur * D + d0, g);
         const int nxt = cur - 1;
         if (nxt < r0) {
@@ -640,6 +659,7 @@ __global__ void __launch_bounds__(256) short_conv_bwd_kernel(
 #pragma unroll
           for (int c = 0; c < VC; ++c) xw[c][0] = in ? xn[s][c] : 0.f;
         }
+      }
       }
       t -= 4;
 #pragma unroll
@@ -890,11 +910,29 @@ static int conv_check(const char* who, int x_dtype, int y_dtype, const int32_t* 
 
 static int conv_vc(int D) { return D % 4 == 0 ? 4 : 1; }
 
-// row blocks: about 2048 workgroups over (column tiles x row blocks), runs of >= 16 tokens,
-// at most 4096 blocks (the partials' column sum handles up to that many)
-static void conv_split(int total, int D, int& nrb, int& per) {
+// Workgroups of a kernel instance that are resident on the whole device at once (CUs x
+// workgroups per CU at the instance's register and LDS use).  The walks below are all of one
+// length, so a grid of exactly one such round finishes together; a round and a fraction
+// leaves most of the device idle during the fraction (short_conv_bwd at [8, 4096, 2048]:
+// 0.19 ms with one round of 128-token runs, 0.24 ms with one and a half rounds, 0.21 ms with
+// two rounds of 64-token runs).
+template <typename Kern>
+static int resident_wgs(Kern kernel) {
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    return 2048;
+  }
+  return cus * per_cu > 0 ? cus * per_cu : 2048;
+}
+
+// row blocks: `target` workgroups over (column tiles x row blocks), runs of >= 16 tokens,
+// at most 4096 blocks
+static void conv_split(int total, int D, int target, int& nrb, int& per) {
   const int tiles = (D / conv_vc(D) + 255) / 256;
-  nrb = (2048 + tiles - 1) / tiles;
+  nrb = (target + tiles - 1) / tiles;
   int maxb = (total + 15) / 16;
   if (nrb > maxb) nrb = maxb;
   if (nrb > 4096) nrb = 4096;
@@ -905,11 +943,13 @@ static void conv_split(int total, int D, int& nrb, int& per) {
   if (nrb < 1) nrb = 1;
 }
 
-// backward: runs of tokens per column group (one wave each, about 8192 waves), 4 runs per
-// workgroup, one weight-gradient partial row per workgroup
-static void conv_bwd_split(int total, int D, int& nrb4, int& per) {
+// backward: runs of tokens per column group (one wave each, `waves` of them, at most 8192),
+// 4 runs per workgroup, one weight-gradient partial row per workgroup.  The workspace is
+// sized for 8192 waves, which bounds the partial rows of every smaller target.
+static void conv_bwd_split(int total, int D, int waves, int& nrb4, int& per) {
   const int tiles = (D / conv_vc(D) + 63) / 64;
-  int runs = (8192 + tiles - 1) / tiles;
+  if (waves > 8192 || waves < 1) waves = 8192;
+  int runs = (waves + tiles - 1) / tiles;
   const int maxr = (total + 15) / 16;
   if (runs > maxr) runs = maxr;
   if (runs > 4 * 4096) runs = 4 * 4096;
@@ -925,13 +965,16 @@ template <typename TX, typename TY>
 static hipError_t conv_fwd_t(const void* x, const float* w, const float* b, void* y,
                              const int32_t* cu, int N, int T, int total, int D, int W, int act,
                              hipStream_t s) {
-  int nrb, per;
-  conv_split(total, D, nrb, per);
   const int vc = conv_vc(D);
-  dim3 grid((D / vc + 255) / 256, nrb);
 #define TOPS_CONV_F(MW, VC)                                                                   \
-  short_conv_fwd_kernel<TX, TY, MW, VC><<<grid, 256, 0, s>>>((const TX*)x, w, b, (TY*)y, cu, \
-                                                             N, T, total, D, W, per, act)
+  do {                                                                                        \
+    static const int target = resident_wgs(short_conv_fwd_kernel<TX, TY, MW, VC>);           \
+    int nrb, per;                                                                             \
+    conv_split(total, D, target, nrb, per);                                                   \
+    dim3 grid((D / vc + 255) / 256, nrb);                                                     \
+    short_conv_fwd_kernel<TX, TY, MW, VC><<<grid, 256, 0, s>>>((const TX*)x, w, b, (TY*)y,   \
+                                                               cu, N, T, total, D, W, per, act); \
+  } while (0)
   if (vc == 4) {
     if (W <= 4) TOPS_CONV_F(4, 4); else TOPS_CONV_F(8, 4);
   } else {
@@ -978,7 +1021,7 @@ extern "C" int tops_short_conv_fwd(const void* x, int x_dtype, const float* weig
 extern "C" int64_t tops_short_conv_bwd_workspace(int B, int T, int D, int W) {
   if (B <= 0 || T < 0 || D <= 0 || W < 1) return TOPS_ERR_SHAPE;
   int nrb, per;
-  conv_bwd_split(B * T, D, nrb, per);
+  conv_bwd_split(B * T, D, 8192, nrb, per);
   const int ncols = (W + 1) * D;
   return (int64_t)nrb * ncols + colsum_scratch(nrb, ncols);
 }
@@ -986,14 +1029,17 @@ extern "C" int64_t tops_short_conv_bwd_workspace(int B, int T, int D, int W) {
 template <typename TX, typename TY>
 static hipError_t conv_bwd_t(const void* x, const float* w, const float* b, const void* dy,
                              void* dx, float* part, const int32_t* cu, int N, int T, int total,
-                             int D, int W, int act, hipStream_t s) {
-  int nrb, per;
-  conv_bwd_split(total, D, nrb, per);
+                             int D, int W, int act, hipStream_t s, int& nrb) {
   const int vc = conv_vc(D);
-  dim3 grid((D / vc + 63) / 64, nrb);
 #define TOPS_CONV_B(MW, VC)                                                                  \
-  short_conv_bwd_kernel<TX, TY, MW, VC><<<grid, 256, 0, s>>>(                                \
-      (const TX*)x, w, b, (const TY*)dy, (TX*)dx, part, cu, N, T, total, D, W, per, act)
+  do {                                                                                       \
+    static const int waves = 4 * resident_wgs(short_conv_bwd_kernel<TX, TY, MW, VC>);        \
+    int per;                                                                                 \
+    conv_bwd_split(total, D, waves, nrb, per);                                               \
+    dim3 grid((D / vc + 63) / 64, nrb);                                                      \
+    short_conv_bwd_kernel<TX, TY, MW, VC><<<grid, 256, 0, s>>>(                              \
+        (const TX*)x, w, b, (const TY*)dy, (TX*)dx, part, cu, N, T, total, D, W, per, act);  \
+  } while (0)
   if (vc == 4) {
     if (W <= 4) TOPS_CONV_B(4, 4); else TOPS_CONV_B(8, 4);
   } else {
@@ -1014,7 +1060,7 @@ extern "C" int tops_short_conv_bwd(const void* x, int x_dtype, const float* weig
   if (rc != TOPS_OK) return rc;
   const int total = B * T;
   int nrb, per;
-  conv_bwd_split(total, D, nrb, per);
+  conv_bwd_split(total, D, 8192, nrb, per);   // the bound the workspace is sized for
   const int ncols = (W + 1) * D;
   if (workspace_floats < (int64_t)nrb * ncols + colsum_scratch(nrb, ncols))
     return tops_set_error(TOPS_ERR_SHAPE, "short_conv_bwd: workspace smaller than tops_short_conv_bwd_workspace()");
@@ -1023,10 +1069,10 @@ extern "C" int tops_short_conv_bwd(const void* x, int x_dtype, const float* weig
   hipError_t e = hipSuccess;
   if (total > 0) {
     const bool xb = x_dtype == TOPS_BF16, yb = dy_dtype == TOPS_BF16;
-    e = xb ? (yb ? conv_bwd_t<uint16_t, uint16_t>(x, weight, bias, dy, dx, workspace, cu_seqlens, N, T, total, D, W, act, s)
-                 : conv_bwd_t<uint16_t, float>(x, weight, bias, dy, dx, workspace, cu_seqlens, N, T, total, D, W, act, s))
-           : (yb ? conv_bwd_t<float, uint16_t>(x, weight, bias, dy, dx, workspace, cu_seqlens, N, T, total, D, W, act, s)
-                 : conv_bwd_t<float, float>(x, weight, bias, dy, dx, workspace, cu_seqlens, N, T, total, D, W, act, s));
+    e = xb ? (yb ? conv_bwd_t<uint16_t, uint16_t>(x, weight, bias, dy, dx, workspace, cu_seqlens, N, T, total, D, W, act, s, nrb)
+                 : conv_bwd_t<uint16_t, float>(x, weight, bias, dy, dx, workspace, cu_seqlens, N, T, total, D, W, act, s, nrb))
+           : (yb ? conv_bwd_t<float, uint16_t>(x, weight, bias, dy, dx, workspace, cu_seqlens, N, T, total, D, W, act, s, nrb)
+                 : conv_bwd_t<float, float>(x, weight, bias, dy, dx, workspace, cu_seqlens, N, T, total, D, W, act, s, nrb));
     if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   }
   e = launch_colsum(workspace, total > 0 ? nrb : 0, ncols, W * D, dweight, dbias, s);
