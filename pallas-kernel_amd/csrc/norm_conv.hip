@@ -499,12 +499,13 @@ __global__ void __launch_bounds__(256) short_conv_bwd_kernel(
   // the 4 waves of a workgroup share 64 * VC columns and take 4 consecutive runs; their
   // weight / bias partials are added in LDS, one partial row per workgroup
   __shared__ float red[4][(MAXW + 1) * 64 * VC];
-  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int d0 = (blockIdx.x * 64 + lane) * VC;
   const bool col_ok = d0 < D;
+  const int da = col_ok ? d0 : 0;
   const int rb = blockIdx.y * 4 + wv;
   const int r0 = rb * per;
-  const int r1 = col_ok ? min(r0 + per, total) : r0;
+  const int r1 = min(r0 + per, total);
   float wt[VC][MAXW];
   load_taps<MAXW, VC>(w, col_ok ? d0 : 0, W, wt);
   float bias[VC];
@@ -523,7 +524,7 @@ __global__ void __launch_bounds__(256) short_conv_bwd_kernel(
     return g * (s * (1.f + pre * (1.f - s)));
   };
   auto ldx = [&](int p, float* v) {
-    VecC<TX, VC>::ld(x + (long long)p * D + d0, v);
+    VecC<TX, VC>::ld(x + (long long)p * D + da, v);
   };
 
   if (r0 < r1) {
@@ -553,7 +554,7 @@ __global__ void __launch_bounds__(256) short_conv_bwd_kernel(
         const int p = t + 1 + i;
         float gy[VC];
         const bool in = p < sc.eos;
-        if (in) VecC<TY, VC>::ld(dy + (long long)p * D + d0, gy);
+        if (in) VecC<TY, VC>::ld(dy + (long long)p * D + da, gy);
 #pragma unroll
         for (int c = 0; c < VC; ++c) {
           float v = 0.f;
@@ -573,7 +574,7 @@ __global__ void __launch_bounds__(256) short_conv_bwd_kernel(
       for (int s = 0; s < 4; ++s) {
         const int cur = t0 - s;
         if (cur >= r0) {
-          VecC<TY, VC>::ld(dy + (long long)cur * D + d0, gyv[s]);
+          VecC<TY, VC>::ld(dy + (long long)cur * D + da, gyv[s]);
           const int p = cur - MAXW;
           if (p >= 0) ldx(p, xn[s]);
           else
@@ -620,7 +621,7 @@ __global__ void __launch_bounds__(256) short_conv_bwd_kernel(
         for (int s = 0; s < 4; ++s) {
           float g[VC];
           step(gyv[s], g);
-          VecC<TX, VC>::st(dx + (long long)(t - s) * D + d0, g);
+          if (col_ok) VecC<TX, VC>::st(dx + (long long)(t - s) * D + da, g);
 #pragma unroll
           for (int c = 0; c < VC; ++c) xw[c][0] = xn[s][c];
         }
@@ -630,7 +631,7 @@ __global__ void __launch_bounds__(256) short_conv_bwd_kernel(
         const int cur = t - s;
         float g[VC];
         step(gyv[s], g);
-        VecC<TX, VC>::st(dx + (long long)cur * D + d0, g);
+        if (col_ok) VecC<TX, VC>::st(dx + (long long)cur * D + da, g);
         const int nxt = cur - 1;
         if (nxt < r0) {
           done = true;
