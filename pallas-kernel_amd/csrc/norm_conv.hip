@@ -491,11 +491,11 @@ __global__ void __launch_bounds__(256) short_conv_state_kernel(const TX* __restr
 // backward, walking the run from its end.  xw[c][j] = x[t - MAXW + 1 + j] (zero before bos),
 // dp[c][i] = dpre[t + 1 + i] (zero at or after eos), i < MAXW - 1.  Partials: [nrb][W*D + D]
 // with the weight gradient at d * W + j and the bias gradient at W * D + d.
-template <typename TX, typename TY, int MAXW, int VC>
+template <typename TX, typename TY, int MAXW, int VC, bool ACT>
 __global__ void __launch_bounds__(256) short_conv_bwd_kernel(
     const TX* __restrict__ x, const float* __restrict__ w, const float* __restrict__ b,
     const TY* __restrict__ dy, TX* __restrict__ dx, float* __restrict__ part,
-    const int32_t* __restrict__ cu, int N, int T, int total, int D, int W, int per, int act) {
+    const int32_t* __restrict__ cu, int N, int T, int total, int D, int W, int per) {
   // the 4 waves of a workgroup share 64 * VC columns and take 4 consecutive runs; their
   // weight / bias partials are added in LDS, one partial row per workgroup
   __shared__ float red[4][(MAXW + 1) * 64 * VC];
@@ -519,7 +519,9 @@ __global__ void __launch_bounds__(256) short_conv_bwd_kernel(
     for (int j = 0; j < MAXW; ++j) pw[c][j] = 0.f;
   }
   auto dpre_of = [&](float pre, float g) -> float {
-    if (!act) return g;
+    // a compile-time switch: a run-time flag here splits every token of the walk into
+    // separate blocks
+    if constexpr (!ACT) return g;
     const float s = sigm(pre);
     return g * (s * (1.f + pre * (1.f - s)));
   };
@@ -1034,12 +1036,16 @@ static hipError_t conv_bwd_t(const void* x, const float* w, const float* b, cons
   const int vc = conv_vc(D);
 #define TOPS_CONV_B(MW, VC)                                                                  \
   do {                                                                                       \
-    static const int waves = 4 * resident_wgs(short_conv_bwd_kernel<TX, TY, MW, VC>);        \
+    static const int waves = 4 * resident_wgs(short_conv_bwd_kernel<TX, TY, MW, VC, true>);  \
     int per;                                                                                 \
     conv_bwd_split(total, D, waves, nrb, per);                                               \
     dim3 grid((D / vc + 63) / 64, nrb);                                                      \
-    short_conv_bwd_kernel<TX, TY, MW, VC><<<grid, 256, 0, s>>>(                              \
-        (const TX*)x, w, b, (const TY*)dy, (TX*)dx, part, cu, N, T, total, D, W, per, act);  \
+    if (act)                                                                                 \
+      short_conv_bwd_kernel<TX, TY, MW, VC, true><<<grid, 256, 0, s>>>(                      \
+          (const TX*)x, w, b, (const TY*)dy, (TX*)dx, part, cu, N, T, total, D, W, per);     \
+    else                                                                                     \
+      short_conv_bwd_kernel<TX, TY, MW, VC, false><<<grid, 256, 0, s>>>(                     \
+          (const TX*)x, w, b, (const TY*)dy, (TX*)dx, part, cu, N, T, total, D, W, per);     \
   } while (0)
   if (vc == 4) {
     if (W <= 4) TOPS_CONV_B(4, 4); else TOPS_CONV_B(8, 4);
