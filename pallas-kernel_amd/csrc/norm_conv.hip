@@ -382,6 +382,16 @@ template <typename T> struct VecC<T, 1> {
   __device__ __forceinline__ static void ld(const T* p, float* v) { v[0] = In<T>::ld(p); }
   __device__ __forceinline__ static void st(T* p, const float* v) { In<T>::st(p, v[0]); }
 };
+template <> struct VecC<uint16_t, 2> {
+  __device__ __forceinline__ static void ld(const uint16_t* p, float* v) { In<uint16_t>::ld2(p, v[0], v[1]); }
+  __device__ __forceinline__ static void st(uint16_t* p, const float* v) {
+    *(uint32_t*)p = pack_bf16x2(v[0], v[1]);
+  }
+};
+template <> struct VecC<float, 2> {
+  __device__ __forceinline__ static void ld(const float* p, float* v) { In<float>::ld2(p, v[0], v[1]); }
+  __device__ __forceinline__ static void st(float* p, const float* v) { *(float2*)p = make_float2(v[0], v[1]); }
+};
 template <typename T> struct VecC<T, 4> {
   __device__ __forceinline__ static void ld(const T* p, float* v) { V4<T>::ld(p, v); }
   __device__ __forceinline__ static void st(T* p, const float* v) { V4<T>::st(p, v); }
@@ -949,8 +959,9 @@ static void conv_split(int total, int D, int target, int& nrb, int& per) {
 // backward: runs of tokens per column group (one wave each, `waves` of them, at most 8192),
 // 4 runs per workgroup, one weight-gradient partial row per workgroup.  The workspace is
 // sized for 8192 waves, which bounds the partial rows of every smaller target.
+static int conv_bwd_vc(int D) { return D % 2 == 0 ? 2 : 1; }
 static void conv_bwd_split(int total, int D, int waves, int& nrb4, int& per) {
-  const int tiles = (D / conv_vc(D) + 63) / 64;
+  const int tiles = (D / conv_bwd_vc(D) + 63) / 64;
   if (waves > 8192 || waves < 1) waves = 8192;
   int runs = (waves + tiles - 1) / tiles;
   const int maxr = (total + 15) / 16;
@@ -1033,7 +1044,7 @@ template <typename TX, typename TY>
 static hipError_t conv_bwd_t(const void* x, const float* w, const float* b, const void* dy,
                              void* dx, float* part, const int32_t* cu, int N, int T, int total,
                              int D, int W, int act, hipStream_t s, int& nrb) {
-  const int vc = conv_vc(D);
+  const int vc = conv_bwd_vc(D);
 #define TOPS_CONV_B(MW, VC)                                                                  \
   do {                                                                                       \
     static const int waves = 4 * resident_wgs(short_conv_bwd_kernel<TX, TY, MW, VC, true>);  \
@@ -1047,8 +1058,8 @@ static hipError_t conv_bwd_t(const void* x, const float* w, const float* b, cons
       short_conv_bwd_kernel<TX, TY, MW, VC, false><<<grid, 256, 0, s>>>(                     \
           (const TX*)x, w, b, (const TY*)dy, (TX*)dx, part, cu, N, T, total, D, W, per);     \
   } while (0)
-  if (vc == 4) {
-    if (W <= 4) TOPS_CONV_B(4, 4); else TOPS_CONV_B(8, 4);
+  if (vc == 2) {
+    if (W <= 4) TOPS_CONV_B(4, 2); else TOPS_CONV_B(8, 2);
   } else {
     if (W <= 4) TOPS_CONV_B(4, 1); else TOPS_CONV_B(8, 1);
   }
