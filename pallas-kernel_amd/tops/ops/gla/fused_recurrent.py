@@ -228,11 +228,25 @@ DECODE_MAX_TOKENS = 4    # beyond this the chunk kernels are faster (measured at
 
 
 def longest_sequence(T, cu_seqlens):
-    """Tokens in the longest sequence of a call (T for fixed length)."""
+    """Tokens in the longest sequence of a call (T for fixed length).  Reads cu_seqlens on
+    the host (a device tensor is copied back, which synchronises its stream)."""
     if cu_seqlens is None:
         return T
     cu = cu_seqlens.tolist() if isinstance(cu_seqlens, torch.Tensor) else list(cu_seqlens)
     return max((cu[i + 1] - cu[i] for i in range(len(cu) - 1)), default=0)
+
+
+def decode_sized(T, cu_seqlens) -> bool:
+    """Whether a call is a batch of decode steps: sequences of at most DECODE_MAX_TOKENS
+    tokens.  Boundaries in host memory (a list, an array, a CPU tensor) are read exactly.
+    A device tensor is not read back, since that would synchronise the stream ahead of the
+    launch on every step; its mean length T / N stands in for the longest.  The decode
+    kernel is exact at any length (it walks a sequence token by token), so that estimate
+    only decides which kernel is faster."""
+    if isinstance(cu_seqlens, torch.Tensor) and cu_seqlens.device.type != "cpu":
+        n = cu_seqlens.numel() - 1
+        return n > 0 and T <= DECODE_MAX_TOKENS * n
+    return longest_sequence(T, cu_seqlens) <= DECODE_MAX_TOKENS
 
 
 def decode_native(q, k, v, gk, gv, initial_state, scale, output_final_state, reverse, cu_seqlens):
@@ -249,7 +263,7 @@ def decode_native(q, k, v, gk, gv, initial_state, scale, output_final_state, rev
     if q.dtype not in (torch.float32, torch.bfloat16) or K > 128 or K % 4:
         return None
     n = B if cu_seqlens is None else len(cu_seqlens) - 1
-    if longest_sequence(T, cu_seqlens) > DECODE_MAX_TOKENS:
+    if not decode_sized(T, cu_seqlens):
         return None
     q, k, v = (x.contiguous() for x in (q, k, v))
     o = torch.empty_like(v)

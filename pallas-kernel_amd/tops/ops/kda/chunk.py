@@ -21,6 +21,7 @@ the same result up to fp32 rounding.
 """
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from ... import _native as N
@@ -152,11 +153,55 @@ def chunk_kda(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor
     return o.to(out_dtype), ht
 
 
-def _g_cumsum_log2(g: torch.Tensor, cu_seqlens) -> torch.Tensor:
-    """Chunk-local cumsum of g / ln 2 (the reference's kda_gate_chunk_cumsum output,
-    tops/ops/kda/gate.py:19-51), on tops_kda_gate_chunk_cumsum."""
-    from .gate import kda_gate_chunk_cumsum
-    return kda_gate_chunk_cumsum(g, CHUNK, cu_seqlens)
+def _padded_rows(cu: "np.ndarray", C: int):
+    """Row map of the per-sequence chunk layout: each sequence of the packed axis padded to
+    a multiple of C.  Returns (index of each padded row's token or -1 for padding, padded
+    length, position of each token in the padded layout)."""
+    lens = np.diff(cu)
+    plens = -(-lens // C) * C
+    pstart = np.concatenate([[0], np.cumsum(plens)]).astype(np.int64)
+    src = np.full(int(pstart[-1]), -1, np.int64)
+    dst = np.empty(int(cu[-1]), np.int64)
+    for s in range(len(lens)):
+        n = int(lens[s])
+        src[pstart[s]:pstart[s] + n] = np.arange(cu[s], cu[s] + n)
+        dst[cu[s]:cu[s] + n] = np.arange(pstart[s], pstart[s] + n)
+    return src, int(pstart[-1]), dst
+
+
+def _intra_matrices(q, k, v, g_cumsum, beta, scale, C, cu_seqlens):
+    """Aqk and Akk_inv [B,T,H,C] in k.dtype, the flattened per-chunk matrices of the
+    reference's chunk_kda_fwd (tops/ops/kda/chunk.py:173-190), from the intra-chunk stage
+    kernel at chunk size C.  A ragged last chunk is zero-padded (padded rows and columns
+    never reach a valid row: both matrices are lower triangular); with cu_seqlens each
+    sequence is chunked on its own, as FLA's varlen layout does."""
+    from .chunk_intra import kda_intra_chunk_fwd
+    B, T, H, _ = q.shape
+    xs = (q, k, v, g_cumsum, beta)
+    if cu_seqlens is not None:
+        from ...utils import _host_cu
+        src, Tp, dst = _padded_rows(_host_cu(cu_seqlens), C)
+        idx = torch.as_tensor(np.maximum(src, 0), device=q.device)
+        keep = torch.as_tensor(src >= 0, device=q.device)
+        padded = []
+        for x in xs:
+            y = x[:, idx]
+            m = keep.view(1, -1, *([1] * (x.dim() - 2)))
+            padded.append(torch.where(m, y, torch.zeros((), dtype=y.dtype, device=y.device)))
+        rows = torch.as_tensor(dst, device=q.device)
+    else:
+        Tp = -(-T // C) * C
+        padded = [torch.nn.functional.pad(x, (0, 0) * (x.dim() - 2) + (0, Tp - T)) for x in xs]
+        rows = None
+    qp, kp, vp, gp, bp = padded
+    hf = lambda x: x.transpose(1, 2)          # noqa: E731  [B,T,H,D] -> [B,H,T,D]
+    *_, aqk, akk = kda_intra_chunk_fwd(hf(qp), hf(kp), hf(gp), bp.transpose(1, 2), hf(vp),
+                                       scale=scale, chunk_size=C)
+    out = []
+    for a in (aqk, akk):
+        a = a.reshape(B, H, Tp, C).transpose(1, 2)
+        out.append((a[:, rows] if rows is not None else a[:, :T]).contiguous())
+    return out
 
 
 def chunk_kda_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
@@ -164,11 +209,18 @@ def chunk_kda_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
                   initial_state: torch.Tensor | None = None, output_final_state: bool = False,
                   cu_seqlens=None, chunk_size: int = 64):
     """Forward only (tops/ops/kda/chunk.py:25-190).  Returns (o, final_state, g_cumsum,
-    Aqk, Akk_inv) like the reference: g_cumsum [B,T,H,K] is the chunk-local log2 cumsum and
-    Akk_inv [B,T,H,64] the per-chunk (I + Akk)^-1 (fixed-length input; None for varlen,
-    whose chunks do not tile the packed axis).  Aqk is not materialised by these kernels
-    (the state sweep recomputes it in registers) and is returned as None."""
+    Aqk, Akk_inv) as the reference: g_cumsum [B,T,H,K] is the chunk-local cumsum of g / ln 2
+    at `chunk_size`; Aqk [B,T,H,C] (row t holds scale * sum_d q_td k_jd 2^(G_td - G_jd) for
+    the tokens j of its chunk, j <= t) and Akk_inv [B,T,H,C] (the rows of (I + Akk)^-1,
+    Akk_ij = beta_i sum_d k_id k_jd 2^(G_id - G_jd), j < i) are in k.dtype, per chunk of
+    `chunk_size` (16, 32, 64 or 128).  o and final_state come from the fused kernels (64-row
+    tiles; the same result up to fp32 rounding).  Unlike the reference, T need not be a
+    multiple of chunk_size and cu_seqlens is honoured (each sequence chunked on its own)."""
     _check(q, k, v, g, beta, initial_state, cu_seqlens)
+    C = int(chunk_size)
+    if C not in (16, 32, 64, 128):
+        raise NotImplementedError(f"tops-hip chunk_kda_fwd takes chunk_size 16, 32, 64 or 128, "
+                                  f"got {C}")
     if scale is None:
         scale = q.shape[-1] ** -0.5
     q, k, v = (x.contiguous() for x in (q, k, v))
@@ -176,14 +228,9 @@ def chunk_kda_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
     b32 = beta.contiguous().to(torch.float32)
     h0 = None if initial_state is None else initial_state.contiguous().to(torch.float32)
     plan = ChunkPlan.get(q.shape[0], q.shape[1], cu_seqlens, q.device)
+    from .gate import kda_gate_chunk_cumsum
     with torch.no_grad():
-        o, ht, (w, tt, vn, hs) = _fwd(q, k, v, g32, b32, h0, scale, output_final_state, plan,
-                                      keep=True)
-        g_cumsum = _g_cumsum_log2(g32, cu_seqlens)
-        akk = None
-        if cu_seqlens is None:
-            B, T, H, _ = q.shape
-            nt = plan.total // B
-            akk = tt.view(B, nt, H, CHUNK, CHUNK).permute(0, 1, 4, 2, 3).reshape(
-                B, nt * CHUNK, H, CHUNK)[:, :T]
-    return o, ht, g_cumsum, None, akk
+        o, ht, _ = _fwd(q, k, v, g32, b32, h0, scale, output_final_state, plan, keep=False)
+        g_cumsum = kda_gate_chunk_cumsum(g32, C, cu_seqlens)
+        aqk, akk = _intra_matrices(q, k, v, g_cumsum, b32, float(scale), C, cu_seqlens)
+    return o, ht, g_cumsum, aqk, akk

@@ -28,7 +28,7 @@ import torch
 
 from ... import _native as N
 from ...utils import to_device
-from ..gla.fused_recurrent import DECODE_MAX_TOKENS, longest_sequence
+from ..gla.fused_recurrent import decode_sized
 from .chunk import _prologue, chunk_kda
 from .l2norm import l2norm
 
@@ -44,7 +44,7 @@ def _decode(q, k, v, g, beta, scale, h0, output_final_state, cu_seqlens, n):
         return None
     if q.dtype not in (torch.float32, torch.bfloat16) or K > 128 or K % 4:
         return None
-    if longest_sequence(T, cu_seqlens) > DECODE_MAX_TOKENS:
+    if not decode_sized(T, cu_seqlens):
         return None
     q, k, v = (x.contiguous() for x in (q, k, v))
     f32 = lambda x: None if x is None else x.contiguous().to(torch.float32)  # noqa: E731

@@ -19,8 +19,8 @@ from __future__ import annotations
 
 import torch
 
-from ..gla.fused_recurrent import (DECODE_MAX_TOKENS, _reversed_chunk, decode_native,
-                                   fused_recurrent_gla, longest_sequence, reverse_chunk_native)
+from ..gla.fused_recurrent import (_reversed_chunk, decode_native, decode_sized,
+                                   fused_recurrent_gla, reverse_chunk_native)
 from .chunk import chunk_simple_gla
 
 
@@ -31,7 +31,7 @@ def fused_recurrent_simple_gla(q, k, v, g=None, g_gamma=None, scale=None, initia
     assert g is None or tuple(g.shape) == (B, T, H), f"g shape {tuple(g.shape)} != {(B, T, H)}"
     assert g_gamma is None or tuple(g_gamma.shape) == (H,), f"g_gamma shape must be ({H},)"
     V = v.shape[-1]
-    if longest_sequence(T, cu_seqlens) <= DECODE_MAX_TOKENS:
+    if decode_sized(T, cu_seqlens):
         gk = None
         if g is not None or g_gamma is not None:
             gk = torch.zeros(B, T, H, 1, device=q.device, dtype=torch.float32)

@@ -101,3 +101,16 @@ def test_ptr_keeps_its_tensor_alive():
     gc.collect()
     assert w() is None
     assert N.ptr(None) is None
+
+
+def test_decode_routing_reads_no_device_boundaries():
+    """The decode route decides on host boundaries exactly and on device boundaries by the mean
+    length, without reading them back (a meta tensor has no data: reading it would raise)."""
+    import torch
+    from tops.ops.gla.fused_recurrent import decode_sized
+    assert decode_sized(4, None) and not decode_sized(5, None)
+    assert decode_sized(8, [0, 4, 8]) and not decode_sized(8, [0, 1, 8])
+    assert decode_sized(8, torch.tensor([0, 4, 8])) and not decode_sized(8, np.array([0, 1, 8]))
+    assert decode_sized(8, torch.empty(3, dtype=torch.int32, device="meta"))       # mean 4
+    assert not decode_sized(9, torch.empty(3, dtype=torch.int32, device="meta"))   # mean 4.5
+    assert not decode_sized(0, torch.empty(1, dtype=torch.int32, device="meta"))   # no sequence

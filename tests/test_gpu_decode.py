@@ -207,3 +207,71 @@ def test_simple_gla_decode(gates, dtype, cuda_device, calls):
     eo, eh = rel(host(o), ro), rel(host(ht), rht)
     print(f"simple gla decode {gates} {dtype}: o {eo:.2e} ht {eh:.2e}")
     assert eo < tol(dtype) and eh < tol(dtype)
+
+
+LONG_CASES = [
+    dict(B=2, T=9, H=2, K=128, V=128, gate="gk", h0=True),
+    dict(B=1, T=20, H=2, K=64, V=96, gate="both", h0=True, reverse=True),
+    dict(B=1, T=40, H=2, K=128, V=64, gate="gv", h0=True, cu=[0, 9, 9, 25, 26, 40]),
+    dict(B=1, T=33, H=3, K=32, V=128, gate="none", cu=[0, 16, 17, 33]),
+    dict(B=3, T=17, H=1, K=36, V=20, gate="gk", h0=True, reverse=True),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("cfg", LONG_CASES, ids=[_id(c) for c in LONG_CASES])
+def test_decode_entry_longer_sequences(cfg, dtype, cuda_device):
+    """tops_gla_fused_recurrent_fwd_decode called directly through the C ABI on sequences of
+    9-20 tokens (the route sends it at most 4): the kernel stages 8 tokens at a time in LDS,
+    so these walk two or three token blocks, restaging between them; varlen with empty and
+    one-token sequences, reverse, every gate form."""
+    from tops import _native as N
+    B, T, H, K, V = (cfg[x] for x in "BTHKV")
+    cu = cfg.get("cu")
+    n = len(cu) - 1 if cu else B
+    print(f"decode entry {_id(cfg)} {dtype}", flush=True)
+    d = gla_inputs(B, T, H, K, V, seed=T * 3 + K, gate_div=4.0, h0=cfg.get("h0", False), N=n)
+    gk, gv = _gates(cfg, d, B, T, H, V, T + V)
+    rev = cfg.get("reverse", False)
+    f = lambda x: to_dev(x, torch.float32, cuda_device)  # noqa: E731
+    q, k, v = (to_dev(d[x], dtype, cuda_device) for x in "qkv")
+    gkt, gvt, h0 = f(gk), f(gv), f(d["h0"])
+    o = torch.empty_like(v)
+    ht = torch.empty(n, H, K, V, device=cuda_device, dtype=torch.float32)
+    cut = None if cu is None else torch.tensor(cu, dtype=torch.int32, device=cuda_device)
+    scale = K ** -0.5
+    N.call("tops_gla_fused_recurrent_fwd_decode", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gkt),
+           N.ptr(gvt), N.ptr(h0), N.ptr(o), None, N.ptr(ht), N.ptr(cut), B, T, H, K, V, n,
+           N.dtype_code(dtype), float(scale), int(rev), N.stream())
+    torch.cuda.synchronize()
+    ro, rht = O.fused_recurrent_fwd(seen(d["q"], dtype), seen(d["k"], dtype), seen(d["v"], dtype),
+                                    gk, gv, scale=scale, initial_state=d["h0"],
+                                    output_final_state=True, reverse=rev, cu_seqlens=cu)
+    eo, eh = rel(host(o), ro), rel(host(ht), rht)
+    print(f"o {eo:.2e} ht {eh:.2e}")
+    assert eo < tol(dtype) and eh < tol(dtype)
+
+
+def test_device_cu_seqlens_routes_without_readback(cuda_device, calls):
+    """Boundaries given as a device tensor are not read back on the decode route: a batch of
+    one-token sequences (mean length 1) takes the decode kernel, a batch whose mean length is
+    above 4 takes the chunk kernels; both against the oracle."""
+    from tops.ops.gla import fused_recurrent_gla
+    H, K, V = 2, 64, 64
+    for cu, want in (([0, 1, 2, 3, 4, 5, 6], True), ([0, 3, 20], False)):
+        T = cu[-1]
+        d = gla_inputs(1, T, H, K, V, seed=T, h0=True, N=len(cu) - 1)
+        q, k, v = (to_dev(d[x], torch.bfloat16, cuda_device) for x in "qkv")
+        cut = torch.tensor(cu, dtype=torch.int32, device=cuda_device)
+        calls.clear()
+        with torch.no_grad():
+            o, ht = fused_recurrent_gla(q, k, v, to_dev(d["g"], torch.float32, cuda_device),
+                                        initial_state=to_dev(d["h0"], torch.float32, cuda_device),
+                                        output_final_state=True, cu_seqlens=cut)
+        torch.cuda.synchronize()
+        assert (DECODE in calls) == want
+        bf = torch.bfloat16
+        ro, rht = O.fused_recurrent_fwd(seen(d["q"], bf), seen(d["k"], bf), seen(d["v"], bf),
+                                        d["g"], initial_state=d["h0"], output_final_state=True,
+                                        cu_seqlens=cu)
+        assert rel(host(o), ro) < 2e-3 and rel(host(ht), rht) < 2e-3

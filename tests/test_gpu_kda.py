@@ -130,21 +130,75 @@ def test_kda_forward_stages(dtype, cuda_device):
     assert not bad, f"rel err over {t}: {bad}"
 
 
-def test_chunk_kda_fwd_extras(cuda_device):
-    """chunk_kda_fwd's g_cumsum (log2, chunk-local) and Akk_inv against the oracle."""
+def _intra_ref(d, C, scale, cu=None):
+    """Oracle g_cumsum (log2, chunk-local at C), Aqk and Akk_inv [B,T,H,C]: the reference's
+    chunk_kda_fwd outputs (tops/ops/kda/chunk.py:120-190), each sequence of a varlen batch
+    padded to a multiple of C and chunked on its own."""
+    from oracle import kda_gate as KG
+    q, k, v, g, beta = (d[x] for x in ("q", "k", "v", "g", "beta"))
+    B, T, H, K = q.shape
+    gc = KG.kda_gate_chunk_cumsum(g, C, cu)
+    spans = [(0, T)] if cu is None else list(zip(cu[:-1], cu[1:]))
+    aqk = np.zeros((B, T, H, C))
+    akk = np.zeros((B, T, H, C))
+    for s, e in spans:
+        n = e - s
+        if n == 0:
+            continue
+        Tp = -(-n // C) * C
+        def hf(x):
+            y = np.zeros((B, Tp) + x.shape[2:])
+            y[:, :n] = x[:, s:e]
+            return np.swapaxes(y, 1, 2)
+        *_, A, Ai = KO.kda_intra_chunk_fwd(hf(q), hf(k), hf(gc), hf(beta), hf(v), scale=scale,
+                                           chunk_size=C)
+        flat = lambda M: np.swapaxes(M.reshape(B, H, Tp, C), 1, 2)[:, :n]  # noqa: E731
+        aqk[:, s:e], akk[:, s:e] = flat(A), flat(Ai)
+    return gc, aqk, akk
+
+
+FWD_EXTRA_CASES = [dict(T=128, C=32), dict(T=192, C=64), dict(T=256, C=128), dict(T=150, C=64),
+                   dict(T=70, C=32), dict(T=300, C=64, cu=[0, 13, 140, 141, 300]),
+                   dict(T=260, C=128, cu=[0, 200, 260])]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("case", FWD_EXTRA_CASES,
+                         ids=[f"T{c['T']}C{c['C']}{'v' if 'cu' in c else ''}" for c in FWD_EXTRA_CASES])
+def test_chunk_kda_fwd_extras(case, dtype, cuda_device):
+    """chunk_kda_fwd's (o, ht, g_cumsum, Aqk, Akk_inv) against the oracle at the caller's
+    chunk size: g_cumsum the chunk-local log2 cumsum, Aqk and Akk_inv [B,T,H,C] in k.dtype
+    (tops/ops/kda/chunk.py:180-190), ragged T and varlen included."""
     from tops.ops.kda import chunk_kda_fwd
-    B, T, H, K, V = 1, 128, 2, 64, 64
-    d = kda_inputs(B, T, H, K, V, seed=8)
-    q, k, v = (to_dev(d[x], torch.float32, cuda_device) for x in "qkv")
-    g, beta = (to_dev(d[x], torch.float32, cuda_device) for x in ("g", "beta"))
-    o, ht, gc, aqk, akk = chunk_kda_fwd(q, k, v, g, beta, output_final_state=True)
-    P = KO.chunk_kda_fwd_parts(d["q"], d["k"], d["v"], d["g"], d["beta"], K ** -0.5, None)
-    gc_ref = (P["Gn"] / np.log(2.0)).reshape(B, T, H, K)
-    akk_ref = np.transpose(P["T"], (0, 1, 2, 4, 3)).reshape(B, T, H, 64)
-    assert aqk is None
-    assert rel(host(gc), gc_ref) < 1e-6
-    assert rel(host(akk), akk_ref) < 1e-4
-    assert rel(host(o), P["o"]) < 1e-4
+    T, C, cu = case["T"], case["C"], case.get("cu")
+    B, H, K, V = (1 if cu else 2), 2, 64, 64
+    n = B if cu is None else len(cu) - 1
+    d = kda_inputs(B, T, H, K, V, seed=8 + C, h0=True, N=n)
+    q, k, v = (to_dev(d[x], dtype, cuda_device) for x in "qkv")
+    g, beta, h0 = (to_dev(d[x], torch.float32, cuda_device) for x in ("g", "beta", "h0"))
+    cut = None if cu is None else torch.tensor(cu, dtype=torch.int32, device=cuda_device)
+    o, ht, gc, aqk, akk = chunk_kda_fwd(q, k, v, g, beta, initial_state=h0,
+                                        output_final_state=True, cu_seqlens=cut, chunk_size=C)
+    scale = K ** -0.5
+    dd = dict(d, q=seen(d["q"], dtype), k=seen(d["k"], dtype), v=seen(d["v"], dtype))
+    gc_ref, aqk_ref, akk_ref = _intra_ref(dd, C, scale, cu)
+    assert aqk.dtype == k.dtype and akk.dtype == k.dtype
+    assert tuple(aqk.shape) == (B, T, H, C) and tuple(akk.shape) == (B, T, H, C)
+    if cu is None:
+        ro, rht = KO.chunk_kda(dd["q"], dd["k"], dd["v"], d["g"], d["beta"], scale, d["h0"], True)
+    else:
+        parts = [KO.chunk_kda(dd["q"][:, s:e], dd["k"][:, s:e], dd["v"][:, s:e], d["g"][:, s:e],
+                              d["beta"][:, s:e], scale, d["h0"][i:i + 1], True)
+                 for i, (s, e) in enumerate(zip(cu[:-1], cu[1:]))]
+        ro = np.concatenate([p[0] for p in parts], axis=1)
+        rht = np.concatenate([p[1] for p in parts], axis=0)
+    t = tol(dtype)
+    errs = {"g_cumsum": rel(host(gc), gc_ref), "Aqk": rel(host(aqk), aqk_ref),
+            "Akk_inv": rel(host(akk), akk_ref), "o": rel(host(o), ro), "ht": rel(host(ht), rht)}
+    print({k_: f"{e:.2e}" for k_, e in errs.items()})
+    assert errs["g_cumsum"] < 1e-6
+    bad = {k_: e for k_, e in errs.items() if not e <= t}
+    assert not bad, f"rel err over {t}: {bad}"
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])

@@ -440,3 +440,52 @@ def test_fused_recurrent_kda_decode(cfg, dtype, cuda_device, monkeypatch):
     print(f"kda decode {_fid(cfg)} {dtype}: o {eo:.2e} ht {eh:.2e}")
     t = 1e-4 if (dtype == torch.float32 or cfg["l2"]) else 2e-3
     assert eo < (2e-3 if dtype == torch.bfloat16 else t) and eh < t
+
+
+KDA_LONG = [dict(B=2, T=9, H=2, K=128, V=128, h0=True), dict(B=1, T=20, H=2, K=64, V=96, h0=True),
+            dict(B=1, T=40, H=2, K=128, V=64, h0=True, cu=[0, 9, 9, 25, 26, 40]),
+            dict(B=1, T=33, H=1, K=32, V=128, h0=False, cu=[0, 16, 17, 33])]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("cfg", KDA_LONG,
+                         ids=[f"T{c['T']}K{c['K']}V{c['V']}{'-varlen' if 'cu' in c else ''}"
+                              for c in KDA_LONG])
+def test_kda_decode_entry_longer_sequences(cfg, dtype, cuda_device):
+    """tops_kda_fused_recurrent_fwd_decode called directly through the C ABI on sequences of
+    9-20 tokens (the route sends it at most 4): two or three 8-token LDS blocks per sequence,
+    varlen with empty and one-token sequences; o and the final state against the per-token
+    recurrence (tops/cpu/ops/kda/naive.py:10-118)."""
+    from tops import _native as N
+    from _inputs import kda_inputs
+    B, T, H, K, V = (cfg[x] for x in "BTHKV")
+    cu = cfg.get("cu")
+    n = len(cu) - 1 if cu else B
+    print(f"kda decode entry T{T} K{K} V{V} {dtype}", flush=True)
+    d = kda_inputs(B, T, H, K, V, seed=T + 2 * K, gate_div=4.0, h0=cfg["h0"], N=n)
+    q, k, v = (to_dev(d[x], dtype, cuda_device) for x in "qkv")
+    g, beta = (to_dev(d[x], torch.float32, cuda_device) for x in ("g", "beta"))
+    h0 = to_dev(d["h0"], torch.float32, cuda_device)
+    o = torch.empty_like(v)
+    ht = torch.empty(n, H, K, V, device=cuda_device, dtype=torch.float32)
+    cut = None if cu is None else torch.tensor(cu, dtype=torch.int32, device=cuda_device)
+    scale = K ** -0.5
+    N.call("tops_kda_fused_recurrent_fwd_decode", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(g),
+           N.ptr(beta), N.ptr(h0), N.ptr(o), N.ptr(ht), N.ptr(cut), B, T, H, K, V, n,
+           N.dtype_code(dtype), float(scale), N.stream())
+    torch.cuda.synchronize()
+    sq, sk, sv = (seen(d[x], dtype) for x in "qkv")
+    spans = [(b, 0, T) for b in range(B)] if cu is None else \
+        [(0, cu[i], cu[i + 1]) for i in range(n)]
+    ro = np.zeros((B, T, H, V))
+    rht = np.zeros((n, H, K, V))
+    for i, (b, s, e) in enumerate(spans):
+        h0i = None if d["h0"] is None else d["h0"][i:i + 1]
+        oo, hh = KO.naive_recurrent_kda(sq[b:b + 1, s:e], sk[b:b + 1, s:e], sv[b:b + 1, s:e],
+                                        d["g"][b:b + 1, s:e], d["beta"][b:b + 1, s:e], scale, h0i,
+                                        True)
+        ro[b, s:e] = oo[0]
+        rht[i] = hh[0]
+    eo, eh = rel(host(o), ro), rel(host(ht), rht)
+    print(f"o {eo:.2e} ht {eh:.2e}")
+    assert eo < tol(dtype) and eh < tol(dtype)

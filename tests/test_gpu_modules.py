@@ -93,6 +93,14 @@ CONV_CASES = [
     dict(B=1, T=600, D=96, W=8, bias=True, act="silu", cu=[0, 1, 2, 300, 301, 600]),
     dict(B=1, T=200, D=256, W=5, bias=False, act="swish", cu=[0, 7, 200]),
     dict(B=2, T=5000, D=128, W=4, bias=True, act="silu"),
+    # odd D (one column per lane, forward and backward) and D = 2 mod 4 (two-column lanes,
+    # a half-empty last lane pair), W = 3 and 8, varlen with short sequences, and runs long
+    # enough for both the interior and the edge walks of the backward
+    dict(B=2, T=1000, D=301, W=3, bias=True, act="silu"),
+    dict(B=1, T=700, D=301, W=8, bias=False, act=None, cu=[0, 1, 5, 350, 700]),
+    dict(B=2, T=777, D=302, W=4, bias=True, act="silu"),
+    dict(B=1, T=520, D=302, W=8, bias=True, act="silu", cu=[0, 3, 4, 260, 520]),
+    dict(B=1, T=2049, D=302, W=3, bias=False, act="silu", cu=[0, 2, 2049]),
 ]
 
 

@@ -4,14 +4,16 @@ and autograd backward) on MI355X against the float64 oracle: tiny and ragged T, 
 K / V from 8 to 128, custom scale, h0, chunk-aligned and chunk-crossing varlen, and the
 three g_gamma forms (scalar, per head (1,1,H,1), per head and channel (1,1,H,K)) whose
 gradient is the broadcast gate's gradient summed to g_gamma's shape.
-Tolerances (relative L2): fp32 1e-4, bf16 2e-3.
+Tolerances (relative L2 against the unrounded float64 oracle): fp32 1e-4, bf16 2e-3; a bf16
+output of a few dozen elements, whose correctly rounded value alone can miss 2e-3, gets that
+rounding floor plus 2.5e-4 (_gpu.out_bound).
 """
 import numpy as np
 import pytest
 import torch
 
 from oracle import gla as O
-from _gpu import to_dev, seen, host, rel
+from _gpu import to_dev, seen, host, rel, out_bound
 from _inputs import gla_inputs
 
 pytestmark = pytest.mark.gpu
@@ -80,11 +82,12 @@ def test_reference_chunk_gla_shapes(c, dt, cuda_device):
     ro, rht = O.chunk_gla(sq, sk, sv, d["g"], scale, d["h0"], True, cu_seqlens=cu)
     rq, rk, rv, rg, rh0 = O.chunk_gla_bwd(sq, sk, sv, d["g"], scale, d["h0"], sdo, d["dht"],
                                           cu_seqlens=cu)
-    # outputs stored in bf16 are compared with the oracle rounded the same way (with a few
-    # hundred elements, as at T = 1 or 3, the rounding alone can approach the bound)
-    r16 = lambda x: seen(x, dt)
-    errs = dict(o=rel(host(o), r16(ro)), ht=rel(host(ht), rht), dq=rel(host(q.grad), r16(rq)),
-                dk=rel(host(k.grad), r16(rk)), dv=rel(host(v.grad), r16(rv)))
+    # every output against the unrounded oracle (out_bound: 2e-3 for bf16, or the rounding
+    # floor of a tensor too small for 2e-3 plus 2.5e-4)
+    errs = dict(o=rel(host(o), ro), ht=rel(host(ht), rht), dq=rel(host(q.grad), rq),
+                dk=rel(host(k.grad), rk), dv=rel(host(v.grad), rv))
+    lims = dict(o=out_bound(ro, dt, dt), dq=out_bound(rq, dt, dt), dk=out_bound(rk, dt, dt),
+                dv=out_bound(rv, dt, dt))
     # dg is a difference of k * dk-sized terms (q dq - k dk + ...); with no initial state
     # the first token's gate multiplies a zero state, so at T = 1 the exact dg is 0 and only
     # the cancellation residue remains: measure it against the scale of those terms
@@ -95,7 +98,7 @@ def test_reference_chunk_gla_shapes(c, dt, cuda_device):
     print(" ".join(f"{n_}={e:.2e}" for n_, e in errs.items()))
     lim = 1e-4 if dt == torch.float32 else 2e-3
     for n_, e in errs.items():
-        assert e < lim, (n_, e)
+        assert e < lims.get(n_, lim), (n_, e, lims.get(n_, lim))
 
 
 GAMMA = [
@@ -182,15 +185,16 @@ def test_reference_simple_gla_shapes(c, dt, cuda_device):
                                  initial_state=d["h0"], output_final_state=True)
     rq, rk, rv, _, rh0 = S.chunk_simple_gla_bwd(sq, sk, sv, None, d["g_gamma"], d["h0"], sdo,
                                                 d["dht"], scale)
-    r16 = lambda x: seen(x, dt)
-    errs = dict(o=rel(host(o), r16(ro)), ht=rel(host(ht), rht), dq=rel(host(q.grad), r16(rq)),
-                dk=rel(host(k.grad), r16(rk)), dv=rel(host(v.grad), r16(rv)))
+    errs = dict(o=rel(host(o), ro), ht=rel(host(ht), rht), dq=rel(host(q.grad), rq),
+                dk=rel(host(k.grad), rk), dv=rel(host(v.grad), rv))
+    lims = dict(o=out_bound(ro, dt, dt), dq=out_bound(rq, dt, dt), dk=out_bound(rk, dt, dt),
+                dv=out_bound(rv, dt, dt))
     if h0 is not None:
         errs["dh0"] = rel(host(h0.grad), rh0)
     print(" ".join(f"{n_}={e:.2e}" for n_, e in errs.items()))
     lim = 1e-4 if dt == torch.float32 else 2e-3
     for n_, e in errs.items():
-        assert e < lim, (n_, e)
+        assert e < lims.get(n_, lim), (n_, e, lims.get(n_, lim))
 
 
 # tests/ops/kda/test_chunk_kda_bwd_tpu.py:21-25
@@ -228,10 +232,11 @@ def test_reference_kda_shapes(c, dt, cuda_device):
     ro, rht = KO.chunk_kda(sq, sk, sv, d["g"], d["beta"], scale, d["h0"], True)
     rq, rk, rv, rb, rg, rh0 = KO.chunk_kda_bwd(sq, sk, sv, d["g"], d["beta"], scale, d["h0"], sdo,
                                                d["dht"])
-    r16 = lambda x: seen(x, dt)
-    errs = dict(o=rel(host(o), r16(ro)), ht=rel(host(ht), rht), dq=rel(host(q.grad), r16(rq)),
-                dk=rel(host(k.grad), r16(rk)), dv=rel(host(v.grad), r16(rv)),
+    errs = dict(o=rel(host(o), ro), ht=rel(host(ht), rht), dq=rel(host(q.grad), rq),
+                dk=rel(host(k.grad), rk), dv=rel(host(v.grad), rv),
                 db=rel(host(beta.grad), rb), dg=rel(host(g.grad), rg))
+    lims = dict(o=out_bound(ro, dt, dt), dq=out_bound(rq, dt, dt), dk=out_bound(rk, dt, dt),
+                dv=out_bound(rv, dt, dt), fn_dq=out_bound(rq, dt, dt))
     if h0 is not None:
         errs["dh0"] = rel(host(h0.grad), rh0)
     # the functional backward on the log2 gate cumsum (dg in log2 units)
@@ -240,12 +245,12 @@ def test_reference_kda_shapes(c, dt, cuda_device):
                                                   beta.detach(), None, None, scale,
                                                   None if h0 is None else h0.detach(), do, dht,
                                                   g=g2)
-    errs["fn_dq"] = rel(host(fq), r16(rq))
+    errs["fn_dq"] = rel(host(fq), rq)
     errs["fn_dg"] = rel(host(fg) / np.log(2.0), rg)
     print(" ".join(f"{n_}={e:.2e}" for n_, e in errs.items()))
     lim = 1e-4 if dt == torch.float32 else 2e-3
     for n_, e in errs.items():
-        assert e < lim, (n_, e)
+        assert e < lims.get(n_, lim), (n_, e, lims.get(n_, lim))
 
 
 # tests/ops/gla/test_pallas_fused_recurrent.py:26-119 (gates, reverse, varlen, scale, h0)

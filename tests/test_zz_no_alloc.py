@@ -68,3 +68,104 @@ def test_kda_fwd_noalloc_rejects_oversize(cuda_device):
     fn = N._fn("tops_kda_chunk_fwd_noalloc")
     rc = fn(*([None] * 11), 0, 1, T, 8, 128, 128, 1, 1, ctypes.c_float(1.0), None)
     assert rc == -2 and b"static scratch" in L.tops_last_error()
+
+
+def test_kda_fwd_noalloc_allocates_nothing_and_replays_in_a_graph(cuda_device):
+    """After a first call (which resolves the scratch address on this device), a call changes
+    neither the device's free memory nor torch's reserved pool, although the workspace it
+    uses (u and w, 8 MiB here) is far larger than any allocation granule; the call also
+    captures into a HIP graph whose replays, with eager work and synchronisations between
+    them, reproduce the eager outputs bit for bit."""
+    from tops.utils import ChunkPlan
+    B, T, H, K, V = 2, 1024, 4, 128, 128
+    dev = cuda_device
+    d = kda_inputs(B, T, H, K, V, 91, h0=True)
+    q, k, v = (to_dev(d[x], torch.bfloat16, dev) for x in "qkv")
+    g, beta, h0 = (to_dev(d[x], torch.float32, dev) for x in ("g", "beta", "h0"))
+    plan = ChunkPlan.get(B, T, None, dev)
+    o = torch.empty(B, T, H, V, device=dev, dtype=torch.bfloat16)
+    ht = torch.empty(B, H, K, V, device=dev, dtype=torch.float32)
+    scale = K ** -0.5
+    run = lambda: _call("tops_kda_chunk_fwd_noalloc", q, k, v, g, beta, h0, o, ht, plan,  # noqa: E731
+                        B, T, H, K, V, scale)
+    print("no-alloc: warm-up call", flush=True)
+    run()
+    torch.cuda.synchronize()
+    free0, res0 = torch.cuda.mem_get_info(dev)[0], torch.cuda.memory_reserved(dev)
+    run()
+    torch.cuda.synchronize()
+    free1, res1 = torch.cuda.mem_get_info(dev)[0], torch.cuda.memory_reserved(dev)
+    assert res1 == res0 and abs(free1 - free0) < (1 << 20), (free0, free1, res0, res1)
+    ref_o, ref_ht = o.clone(), ht.clone()
+    print("no-alloc: graph capture", flush=True)
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            run()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for i in range(3):
+        o.zero_()
+        ht.fill_(float(i + 1))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"no-alloc: replay {i}", flush=True)
+        assert torch.equal(o, ref_o) and torch.equal(ht, ref_ht), f"replay {i}"
+
+
+_CHILD = r"""
+import sys
+sys.path[:0] = [ROOT + "/pallas-kernel_amd", ROOT + "/tests"]
+import torch
+from tops import _native as N
+from tops.ops.gla import chunk_gla
+from tops.ops.kda import chunk_kda
+from tops.utils import ChunkPlan
+torch.zeros(1, device="cuda")
+torch.cuda.synchronize()
+B, T, H, K, V = 1, 128, 2, 64, 64
+q = torch.randn(B, T, H, K, device="cuda")
+g = torch.nn.functional.logsigmoid(torch.randn(B, T, H, K, device="cuda")) / 16
+beta = torch.sigmoid(torch.randn(B, T, H, device="cuda"))
+qb = q.to(torch.bfloat16)
+ob = torch.empty_like(qb)
+plan = ChunkPlan.get(B, T, None, q.device)
+torch.cuda.synchronize()
+free0 = torch.cuda.mem_get_info()[0]
+with torch.no_grad():
+    chunk_gla(q, q, q, g)
+    chunk_kda(q, q, q, g, beta)
+torch.cuda.synchronize()
+free1 = torch.cuda.mem_get_info()[0]
+N.call("tops_kda_chunk_fwd_noalloc", N.ptr(qb), N.ptr(qb), N.ptr(qb), N.ptr(g), N.ptr(beta), None,
+       N.ptr(ob), None, None, None, None, plan.total, B, T, H, K, V, plan.N,
+       N.dtype_code(qb.dtype), 0.125, N.stream())
+torch.cuda.synchronize()
+free2 = torch.cuda.mem_get_info()[0]
+print("FREE", free0, free1, free2, flush=True)
+"""
+
+
+def test_scratch_reserved_only_by_noalloc_callers(cuda_device):
+    """The static scratch lives in the code object of the entry point's own source file, which
+    the HIP runtime loads on a device the first time it is used there.  So a process that runs
+    the other kernels (chunk_gla, chunk_kda) does not hold the 64 MiB; the first no-alloc call
+    does.  Measured in a fresh child process (device free memory before and after)."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("no-alloc: child process for the scratch residency check", flush=True)
+    r = subprocess.run([sys.executable, "-c", f"ROOT = {root!r}\n" + _CHILD], capture_output=True,
+                       text=True, timeout=180)
+    assert r.returncode == 0, r.stderr[-2000:]
+    line = [x for x in r.stdout.splitlines() if x.startswith("FREE")][-1]
+    free0, free1, free2 = (int(x) for x in line.split()[1:])
+    MiB = 1 << 20
+    print(f"other kernels: -{(free0 - free1) / MiB:.1f} MiB; no-alloc call: "
+          f"-{(free1 - free2) / MiB:.1f} MiB")
+    assert free0 - free1 < 32 * MiB
+    assert free1 - free2 >= 64 * MiB
