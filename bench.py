@@ -7,8 +7,11 @@ One step = tops.ops.gla.chunk_gla forward (o, final state) plus its backward
 in HBM (q, k, v, dO ~ N(0,1) bf16; g = logsigmoid(N(0,1))/16 fp32; h0, dht ~
 N(0, 0.1^2) fp32).  Prints ONE JSON line with the throughput (tokens/s, tokens =
 B*T per step), the roofline of the dominant kernel timed live with HIP events on
-the stream the kernels run on, and a CPU baseline: a torch-CPU float32 restatement of
-the reference's algorithm timed on this host's cores on the same step.
+the stream the kernels run on, and a CPU baseline: torch-CPU float32 restatements of the
+reference's algorithms (oracle/torch_cpu.py, pinned against the float64 oracle) timed on this
+host's cores, forward and forward + backward, on each measured config's own inputs copied
+from the GPU.  The same CPU runs are the parity reference at the full BASELINE shapes: the
+line carries the relative L2 error of every output and gradient of the GPU step against them.
 """
 from __future__ import annotations
 
@@ -80,42 +83,84 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(repeats=3, warmup=1):
-    """The torch-CPU float32 restatement of the reference's chunked GLA (oracle/torch_cpu.py,
-    test infrastructure pinned against the float64 oracle), forward + backward on the full
-    config-3 step (B=8, T=4096, H=16, K=V=128; bf16-rounded inputs in fp32), on every CPU
-    thread this process is granted (OMP_NUM_THREADS, else os.cpu_count()).  One warm-up, the
-    median of `repeats` timed runs.  Returns tokens/s (tokens = B*T)."""
-    import torch
-    from oracle import torch_cpu as TC
-    threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or (os.cpu_count() or 1)
-    prev = torch.get_num_threads()
-    torch.set_num_threads(threads)
-    try:
-        gen = torch.Generator().manual_seed(1003)
-        bf = torch.bfloat16
+def _host(t):
+    return None if t is None else t.detach().float().cpu()
 
-        def n(*shape, std=1.0):
-            return torch.randn(*shape, generator=gen) * std
-        q, k = (n(B, T, H, K).to(bf).float() for _ in range(2))
-        v, do = (n(B, T, H, V).to(bf).float() for _ in range(2))
-        g = torch.nn.functional.logsigmoid(n(B, T, H, K)) / 16
-        h0, dht = n(B, H, K, V, std=0.1), n(B, H, K, V, std=0.1)
-        times = []
-        for i in range(warmup + repeats):
+
+def _rel(a, b):
+    """Relative L2 error ||a - b|| / ||b|| in float64."""
+    import torch
+    a, b = a.double(), b.double()
+    return float(torch.linalg.norm(a - b) / torch.linalg.norm(b))
+
+
+class CpuLeg:
+    """The CPU baseline and full-shape parity leg.  Each measured config registers its inputs
+    (copied from the GPU after its timing), its GPU outputs and the torch-CPU restatement of
+    its reference function; run() then times the restatement, forward alone and forward +
+    backward, on every CPU thread this process is granted (OMP_NUM_THREADS, else
+    os.cpu_count()), one warm-up and the median of `repeats`, and compares the GPU outputs
+    with the forward + backward result.  Reported only; the tolerance is north_star's
+    (bf16 paths 2e-3, fp32 1e-4, relative L2)."""
+
+    def __init__(self, repeats=3, warmup=1):
+        self.repeats, self.warmup, self.cases = repeats, warmup, []
+
+    def add(self, name, tokens, gpu_ms, fwd, fwd_bwd, gpu_out, tol):
+        self.cases.append(dict(name=name, tokens=tokens, gpu_ms=gpu_ms, fwd=fwd,
+                               fwd_bwd=fwd_bwd, gpu_out=gpu_out, tol=tol))
+
+    def _median(self, fn):
+        times, out = [], None
+        for i in range(self.warmup + self.repeats):
             t0 = time.perf_counter()
-            TC.chunk_gla_fwd_bwd(q, k, v, g, h0, do, dht, K ** -0.5, C)
-            if i >= warmup:
+            out = fn()
+            if i >= self.warmup:
                 times.append(time.perf_counter() - t0)
-    finally:
-        torch.set_num_threads(prev)
-    med = statistics.median(times)
-    return {"value": round(B * T / med, 1), "unit": "tokens/s", "cores": threads,
+        return statistics.median(times), out
+
+    def run(self):
+        import torch
+        threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or (os.cpu_count() or 1)
+        prev = torch.get_num_threads()
+        torch.set_num_threads(threads)
+        res = {}
+        try:
+            for c in self.cases:
+                row = {}
+                t_f, ref = self._median(c["fwd"])
+                row["fwd_s"] = round(t_f, 4)
+                row["fwd_tokens_s"] = round(c["tokens"] / t_f, 1)
+                if c["fwd_bwd"] is not None:
+                    t_fb, ref = self._median(c["fwd_bwd"])
+                    row["fwd_bwd_s"] = round(t_fb, 4)
+                    row["fwd_bwd_tokens_s"] = round(c["tokens"] / t_fb, 1)
+                gms = c["gpu_ms"]
+                for key, ms in gms.items():
+                    cpu_s = row.get(key + "_s")
+                    if cpu_s:
+                        row[f"gpu_speedup_{key}"] = round(cpu_s / (ms * 1e-3), 1)
+                errs = {n: _rel(g, ref[n]) for n, g in c["gpu_out"].items()
+                        if g is not None and ref.get(n) is not None}
+                row["parity"] = {"rel_err": {n: float(f"{e:.3e}") for n, e in errs.items()},
+                                 "tolerance": c["tol"],
+                                 "pass": all(e <= c["tol"] for e in errs.values())}
+                res[c["name"]] = row
+        finally:
+            torch.set_num_threads(prev)
+        return res, threads
+
+
+def cpu_summary(res, threads):
+    head = res.get("3", {})
+    return {"value": head.get("fwd_bwd_tokens_s"), "unit": "tokens/s", "cores": threads,
             "kind": "port", "cpu_count": os.cpu_count(), "cpu_model": _cpu_model(),
-            "seconds_per_step": round(med, 3),
-            "sample": f"torch-CPU float32 restatement of tops/cpu chunk_gla fwd+bwd, the full "
-                      f"config-3 step (B={B},T={T},H={H},K=V={K}), {threads} threads, "
-                      f"1 warm-up + median of {repeats}"}
+            "seconds_per_step": head.get("fwd_bwd_s"),
+            "sample": f"torch-CPU float32 restatements of tops/cpu (oracle/torch_cpu.py, pinned "
+                      f"to the float64 oracle) on each config's own GPU inputs: the full step of "
+                      f"each config, forward and forward + backward, {threads} threads, 1 warm-up "
+                      f"+ median of 3; value = config 3 fwd+bwd",
+            "configs": {k: {x: y for x, y in v.items() if x != "parity"} for k, v in res.items()}}
 
 
 def _time(fn, iters, warmup=2):
@@ -130,20 +175,23 @@ def _time(fn, iters, warmup=2):
     return (time.perf_counter() - t0) / iters
 
 
-def secondary(dev, iters=10, configs=(2, 4, 5)):
+def secondary(dev, iters=10, configs=(2, 4, 5), leg=None):
     """The other BASELINE configs that fit one GPU, measured the same way (inputs resident,
-    synchronise around the timed iterations): config 2 (fused_recurrent_gla forward),
-    config 4 (simple GLA, varlen, forward + backward) and config 5 (KDA, forward +
-    backward)."""
+    synchronise around the timed iterations): config 1 (chunk_gla forward, fp32), config 2
+    (fused_recurrent_gla forward), config 4 (simple GLA, varlen, forward + backward) and
+    config 5 (KDA, forward + backward); each registers its inputs and outputs with the CPU
+    leg when one is given."""
     import torch
     out = []
     gen = torch.Generator(device=dev).manual_seed(1002)
+    if 1 in configs:
+        out.append(_config1(dev, iters, leg))
     if 2 in configs:
-        out.append(_config2(dev, gen, iters))
+        out.append(_config2(dev, gen, iters, leg))
     if 4 in configs:
-        out.append(_config4(dev, gen, iters))
+        out.append(_config4(dev, gen, iters, leg))
     if 5 in configs:
-        out.append(_config5(dev, gen, iters))
+        out.append(_config5(dev, gen, iters, leg))
     if 6 in configs:
         out.append(_neighbours(dev, gen, iters))
     if 7 in configs:
@@ -294,9 +342,36 @@ def _neighbours(dev, gen, iters):
     return {"config": "layer-side and KDA gate kernels (HBM-bound streams)", "kernels": rows}
 
 
-def _config2(dev, gen, iters):
+def _config1(dev, iters, leg):
+    """config 1: chunk_gla forward, fp32, B2 T512 H4 K=V=64; q, k, v ~ N(0,1), then q scaled
+    by K^-1/2 (and the default scale K^-1/2 applied on top); g = logsigmoid(N(0,1))/16; no
+    initial state; o + final state."""
+    import torch
+    from oracle import torch_cpu as TC
+    from tops.ops.gla import chunk_gla
+    B1, T1, H1, D1 = 2, 512, 4, 64
+    gen = torch.Generator(device=dev).manual_seed(1001)
+    q, k, v = (torch.randn(B1, T1, H1, D1, device=dev, generator=gen) for _ in range(3))
+    q = q * D1 ** -0.5
+    g = torch.nn.functional.logsigmoid(torch.randn(B1, T1, H1, D1, device=dev, generator=gen)) / 16
+    with torch.no_grad():
+        sec = _time(lambda: chunk_gla(q, k, v, g, output_final_state=True), iters)
+        o, ht = chunk_gla(q, k, v, g, output_final_state=True)
+    torch.cuda.synchronize()
+    if leg is not None:
+        hq, hk, hv, hg = (_host(x) for x in (q, k, v, g))
+        leg.add("1", B1 * T1, {"fwd": sec * 1e3},
+                lambda: dict(zip(("o", "ht"), TC.chunk_gla_fwd_bwd(hq, hk, hv, hg, None, None, None,
+                                                                   D1 ** -0.5, backward=False))),
+                None, {"o": _host(o), "ht": _host(ht)}, 1e-4)
+    return {"config": "BASELINE config 1: chunk_gla fwd B2 T512 H4 K=V=64 fp32",
+            "tokens_per_s": round(B1 * T1 / sec, 1), "ms": round(sec * 1e3, 4)}
+
+
+def _config2(dev, gen, iters, leg):
     """config 2: B16 T2048 H8 K=V=128, bf16 q/k/v, fp32 gk and h0; o + final state."""
     import torch
+    from oracle import torch_cpu as TC
     from tops.ops.gla import fused_recurrent_gla
     bf = torch.bfloat16
     B2, T2, H2, D2 = 16, 2048, 8, 128
@@ -313,6 +388,14 @@ def _config2(dev, gen, iters):
                                                     output_final_state=True, reverse=True), iters)
         sec_gv = _time(lambda: fused_recurrent_gla(q, k, v, None, gv=gk, initial_state=h0,
                                                    output_final_state=True), iters)
+        o, ht = fused_recurrent_gla(q, k, v, gk, initial_state=h0, output_final_state=True)
+    torch.cuda.synchronize()
+    if leg is not None:
+        hq, hk, hv, hg, hh0 = (_host(x) for x in (q, k, v, gk, h0))
+        leg.add("2", B2 * T2, {"fwd": sec * 1e3},
+                lambda: dict(zip(("o", "ht"), TC.chunk_gla_fwd_bwd(hq, hk, hv, hg, hh0, None, None,
+                                                                   D2 ** -0.5, backward=False))),
+                None, {"o": _host(o), "ht": _host(ht)}, 2e-3)
     algo = 419_430_400
 
     def frac(s):
@@ -324,10 +407,11 @@ def _config2(dev, gen, iters):
             "gv": {"ms": round(sec_gv * 1e3, 4), "hbm_frac": frac(sec_gv)}}
 
 
-def _config4(dev, gen, iters):
+def _config4(dev, gen, iters, leg):
     """config 4: simple GLA, T_total 16384 in 8 seeded varlen sequences, H32 K=V=128, bf16."""
     import numpy as np
     import torch
+    from oracle import torch_cpu as TC
     from tops.ops.simple_gla import chunk_simple_gla
     bf = torch.bfloat16
     T4, H4, D2 = 16384, 32, 128
@@ -340,17 +424,33 @@ def _config4(dev, gen, iters):
 
     def step4():
         o, _ = chunk_simple_gla(q, k, v, None, g=g, cu_seqlens=cu)
-        return torch.autograd.grad(o, (q, k, v, g), do)
+        return (o,) + torch.autograd.grad(o, (q, k, v, g), do)
     sec = _time(step4, iters)
+    with torch.no_grad():
+        sec_f = _time(lambda: chunk_simple_gla(q, k, v, None, g=g, cu_seqlens=cu), iters)
+    res = step4()
+    torch.cuda.synchronize()
+    if leg is not None:
+        hq, hk, hv, hg, hdo = (_host(x) for x in (q, k, v, g, do))
+        names = ("o", "ht", "dq", "dk", "dv", "dg", "dh0")
+        sc = D2 ** -0.5
+        leg.add("4", T4, {"fwd": sec_f * 1e3, "fwd_bwd": sec * 1e3},
+                lambda: dict(zip(names[:2], TC.chunk_simple_gla_fwd_bwd(
+                    hq, hk, hv, hg, sc, cu_seqlens=cu, backward=False))),
+                lambda: dict(zip(names, TC.chunk_simple_gla_fwd_bwd(hq, hk, hv, hg, sc, do=hdo,
+                                                                    cu_seqlens=cu))),
+                dict(zip(("o", "dq", "dk", "dv", "dg"), (_host(x) for x in res))), 2e-3)
     return {"config": "BASELINE config 4: chunk_simple_gla fwd+bwd, varlen T16384 (8 seqs) "
                       "H32 K=V=128 bf16, per-token g",
             "tokens_per_s": round(T4 / sec, 1), "ms": round(sec * 1e3, 4),
+            "fwd_ms": round(sec_f * 1e3, 4),
             "hbm_floor_ms": round(1.483e9 / (HBM_PEAK_GBS * 1e9) * 1e3, 4)}
 
 
-def _config5(dev, gen, iters):
+def _config5(dev, gen, iters, leg):
     """config 5: KDA B4 T8192 H32 K=V=128; q, k L2-normalised, bf16 q/k/v, fp32 g, beta."""
     import torch
+    from oracle import torch_cpu as TC
     from tops.ops.kda import chunk_kda
     bf = torch.bfloat16
     B5, T5, H5, D2 = 4, 8192, 32, 128
@@ -366,15 +466,30 @@ def _config5(dev, gen, iters):
     do = torch.randn(B5, T5, H5, D2, device=dev, generator=gen).to(bf)
 
     def step5():
-        o, _ = chunk_kda(q, k, v, g, beta)
-        return torch.autograd.grad(o, (q, k, v, g, beta), do)
+        o, ht = chunk_kda(q, k, v, g, beta, output_final_state=True)
+        return (o, ht) + torch.autograd.grad(o, (q, k, v, g, beta), do)
     sec = _time(step5, iters)
+    with torch.no_grad():
+        sec_f = _time(lambda: chunk_kda(q, k, v, g, beta, output_final_state=True), iters)
+    res = step5()
+    torch.cuda.synchronize()
+    if leg is not None:
+        hq, hk, hv, hg, hb, hdo = (_host(x) for x in (q, k, v, g, beta, do))
+        names = ("o", "ht", "dq", "dk", "dv", "dbeta", "dg", "dh0")
+        sc = D2 ** -0.5
+        leg.add("5", B5 * T5, {"fwd": sec_f * 1e3, "fwd_bwd": sec * 1e3},
+                lambda: dict(zip(names[:2], TC.chunk_kda_fwd_bwd(hq, hk, hv, hg, hb, sc,
+                                                                 backward=False))),
+                lambda: dict(zip(names, TC.chunk_kda_fwd_bwd(hq, hk, hv, hg, hb, sc, do=hdo))),
+                dict(zip(("o", "ht", "dq", "dk", "dv", "dg", "dbeta"), (_host(x) for x in res))),
+                2e-3)
     # input/output floor: fwd reads q, k, v (bf16), g (fp32), writes o; bwd reads q, k, v, g, dO,
     # writes dq, dk, dv (bf16), dg (fp32); beta / dbeta
     n5 = B5 * T5 * H5 * D2
     io5 = n5 * (2 * 3 + 4 + 2) + n5 * (2 * 4 + 4 + 2 * 3 + 4) + B5 * T5 * H5 * 4 * 3
     return {"config": "BASELINE config 5: chunk_kda fwd+bwd B4 T8192 H32 K=V=128 bf16",
             "tokens_per_s": round(B5 * T5 / sec, 1), "ms": round(sec * 1e3, 4),
+            "fwd_ms": round(sec_f * 1e3, 4),
             "io_bytes": io5, "hbm_floor_ms": round(io5 / (HBM_PEAK_GBS * 1e9) * 1e3, 4)}
 
 
@@ -395,10 +510,10 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-secondary", action="store_true", help="skip the config 2 / 4 / 5 lines")
-    ap.add_argument("--configs", default="2,4,5,6,7",
-                    help="secondary configs to measure (6: the gate / norm / conv kernels, "
-                         "7: decode steps)")
+    ap.add_argument("--no-secondary", action="store_true", help="skip the config 1 / 2 / 4 / 5 lines")
+    ap.add_argument("--configs", default="1,2,4,5,6,7",
+                    help="secondary configs to measure (1, 2, 4, 5: BASELINE configs; 6: the "
+                         "gate / norm / conv kernels, 7: decode steps)")
     ap.add_argument("--only-secondary", action="store_true",
                     help="measure only the secondary configs (for profiling them alone)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -470,15 +585,42 @@ def main():
             "hbm_floor_ms": round(t_floor * 1e3, 4),
             "frac_of_roofline": round(t_floor / (ms_step * 1e-3), 4),
             "mfma_frac": round(PATH_FLOPS / (ms_step * 1e-3) / (MFMA_BF16_PEAK_TFS * 1e12), 4)}
+    leg = None if a.no_cpu else CpuLeg()
+    # the forward alone, and one more step whose outputs go to the parity check (untimed)
+    with torch.no_grad():
+        sec_f = _time(lambda: chunk_gla(q, k, v, g, initial_state=h0, output_final_state=True), 10)
+        o3, ht3 = chunk_gla(q, k, v, g, initial_state=h0, output_final_state=True)
+    grads3 = step()
+    torch.cuda.synchronize()
+    if leg is not None:
+        from oracle import torch_cpu as TC
+        hq, hk, hv, hg, hh0, hdo, hdht = (_host(x) for x in (q, k, v, g, h0, do, dht))
+        names = ("o", "ht", "dq", "dk", "dv", "dg", "dh0")
+        leg.add("3", B * T, {"fwd": sec_f * 1e3, "fwd_bwd": ms_step},
+                lambda: dict(zip(names[:2], TC.chunk_gla_fwd_bwd(hq, hk, hv, hg, hh0, None, None,
+                                                                 K ** -0.5, C, backward=False))),
+                lambda: dict(zip(names, TC.chunk_gla_fwd_bwd(hq, hk, hv, hg, hh0, hdo, hdht,
+                                                             K ** -0.5, C))),
+                dict(zip(names, (_host(x) for x in (o3, ht3) + tuple(grads3)))), 2e-3)
+    del o3, ht3, grads3
+    sec_rows = None if a.no_secondary else secondary(dev, configs=configs, leg=leg)
+    cpu, parity = None, None
+    if leg is not None:
+        res, threads = leg.run()
+        cpu = cpu_summary(res, threads)
+        parity = {"reference": "torch-CPU float32 restatement of tops/cpu on the GPU run's own "
+                               "inputs (oracle/torch_cpu.py, pinned to the float64 oracle at 1e-5)",
+                  "metric": "relative L2 error per output, ||gpu - ref|| / ||ref||",
+                  "configs": {name: row["parity"] for name, row in res.items()}}
     out = {"metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1,
            "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_step, 4),
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
            "data": "synthetic",
            "config": {"workload": "chunk_gla fwd+bwd (BASELINE config 3)", "B": B, "T": T,
                       "H": H, "K": K, "V": V, "chunk": C, "h0": True, "dht": True},
+           "fwd_ms": round(sec_f * 1e3, 4),
            "roofline": roofline, "path_roofline": path, "kernels": kern,
-           "secondary": None if a.no_secondary else secondary(dev, configs=configs),
-           "cpu_baseline": None if a.no_cpu else cpu_baseline()}
+           "parity": parity, "secondary": sec_rows, "cpu_baseline": cpu}
     print(json.dumps(out), flush=True)
 
 
