@@ -207,7 +207,8 @@ def _decode(dev, gen, iters):
     (2 K V 4 per sequence and head) plus the token's inputs and output."""
     import torch
     from tops import _native as NT
-    from tops.ops.gla import fused_recurrent_gla
+    from tops.modules import rms_norm_gated
+    from tops.ops.gla import fused_recurrent_gla, fused_recurrent_gla_norm_gate
     from tops.ops.kda import fused_recurrent_kda
     bf = torch.bfloat16
     D = 128
@@ -219,6 +220,15 @@ def _decode(dev, gen, iters):
     cases.append(("tops_gla_fused_recurrent_fwd_decode", "fused_recurrent_gla B256 T1 H16 K=V=128 gk",
                   Bg * Hg * (2 * D * D * 4 + 3 * D * 2 + D * 4 + D * 2),
                   lambda: fused_recurrent_gla(q1, k1, v1, g1, initial_state=s1, output_final_state=True)))
+    # the layer's decode route with its output norm fused into the same kernel:
+    # y = RMSNorm(o) * w * silu(g) over V; bytes as above plus the gate read (o is never stored)
+    og1 = torch.randn(Bg, 1, Hg, D, device=dev, generator=gen).to(bf)
+    nw1 = torch.ones(D, device=dev)
+    cases.append(("tops_gla_fused_recurrent_fwd_decode_norm_gate",
+                  "fused_recurrent_gla + FusedRMSNormGated B256 T1 H16 K=V=128 gk",
+                  Bg * Hg * (2 * D * D * 4 + 3 * D * 2 + D * 4 + D * 2 + D * 2),
+                  lambda: fused_recurrent_gla_norm_gate(q1, k1, v1, g1, None, og1, nw1,
+                                                        initial_state=s1, output_final_state=True)))
     Bk, Hk = 64, 32
     q2, k2 = (torch.nn.functional.normalize(torch.randn(Bk, 1, Hk, D, device=dev, generator=gen), dim=-1).to(bf)
               for _ in range(2))
@@ -268,7 +278,18 @@ def _decode(dev, gen, iters):
                      "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
     for r in rows:
         r["frac_of_copy"] = round(r["hbm_gbs"] / copy_ref["hbm_gbs"], 4)
-    return {"config": "decode steps (state-cache bound)", "kernels": rows, "copy_ref": copy_ref}
+    # the same norm unfused: the decode kernel writes o, the standalone norm kernel reads it
+    with torch.no_grad():
+        unf = _time(lambda: rms_norm_gated(fused_recurrent_gla(q1, k1, v1, g1, initial_state=s1,
+                                                               output_final_state=True)[0],
+                                           og1, nw1), iters)
+        fus = _time(lambda: fused_recurrent_gla_norm_gate(q1, k1, v1, g1, None, og1, nw1,
+                                                          initial_state=s1,
+                                                          output_final_state=True), iters)
+    norm_route = {"what": "decode step + output norm, B256 H16 K=V=128, wall time per call",
+                  "fused_ms": round(fus * 1e3, 4), "unfused_ms": round(unf * 1e3, 4)}
+    return {"config": "decode steps (state-cache bound)", "kernels": rows, "copy_ref": copy_ref,
+            "norm_route": norm_route}
 
 
 def _neighbours(dev, gen, iters):

@@ -282,8 +282,8 @@ int tops_gla_fused_recurrent_fwd(const void* q, const void* k, const void* v, co
                                  int N, int dtype, float scale, int reverse, void* stream);
 
 /* The same forward for sequences of a few tokens (decode steps against a state cache): one
- * wave per (sequence, head, 8 V columns) keeps its state slice in registers, so the launch
- * reads h0 and writes ht once and is bound by those bytes.  Same arguments, semantics and
+ * workgroup per (sequence, head, 128 V columns), a wave per 32-column tile, keeps the state in
+ * registers, so the launch reads h0 and writes ht once and is bound by those bytes.  Same arguments, semantics and
  * limits as tops_gla_fused_recurrent_fwd, which takes this kernel by itself for fixed-length
  * calls with T <= 4; varlen callers that know every sequence is short call it directly.  Any
  * length is computed correctly; long sequences run one token at a time.  Replaces
@@ -295,6 +295,23 @@ int tops_gla_fused_recurrent_fwd_decode(const void* q, const void* k, const void
                                         const int32_t* cu_seqlens, int B, int T, int H, int K,
                                         int V, int N, int dtype, float scale, int reverse,
                                         void* stream);
+
+/* Decode steps with the GLA layer's output norm fused as the epilogue:
+ *   y_t = o_t / sqrt(mean_v(o_t^2) + eps) * weight * silu(g_t)     (per token and head, over V)
+ * with o_t the output of tops_gla_fused_recurrent_fwd_decode (same recurrence and arguments).
+ * Replaces the decode route of the reference's GLA layer: fused_recurrent_gla followed by
+ * FusedRMSNormGated(o, g) (tops/layers/gla.py:288-297, 330-336; tops/modules/fused_norm_gate.py:
+ * 6-37); with g NULL, RMSNorm(o) * weight (the layer's g_norm, tops/modules/layernorm.py:6-35).
+ *   g [B,T,H,V] (dtype) or NULL; weight [V] fp32 or NULL; eps >= 0
+ *   y [B,T,H,V] (dtype); ht [N,H,K,V] fp32 or NULL (o itself is not written)
+ * Limits: as tops_gla_fused_recurrent_fwd_decode, and V <= 128 (one workgroup holds a row). */
+int tops_gla_fused_recurrent_fwd_decode_norm_gate(const void* q, const void* k, const void* v,
+                                                  const float* gk, const float* gv,
+                                                  const float* h0, const void* g,
+                                                  const float* weight, float eps, void* y,
+                                                  float* ht, const int32_t* cu_seqlens, int B,
+                                                  int T, int H, int K, int V, int N, int dtype,
+                                                  float scale, int reverse, void* stream);
 
 /* KDA decode steps: the per-token delta rule
  *   S <- diag(exp g_t) S;  S <- S + beta_t k_t (v_t - S^T k_t)^T;  o_t = S^T (scale q_t)

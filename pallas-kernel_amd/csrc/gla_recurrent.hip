@@ -45,6 +45,11 @@ struct FrParams {
   float scale;
   int reverse;
   const float* beta = nullptr;   // KDA decode: the delta-rule rate [B,T,H]
+  // decode with the output norm (NORM instance): y = RMSNorm(o) * nw * silu(ng) over V
+  const void* ng = nullptr;      // output gate [B,T,H,V] in the input dtype, or NULL
+  const float* nw = nullptr;     // norm weight [V], or NULL
+  float neps = 0.f;
+  float ninv = 0.f;              // 1 / V
 };
 
 constexpr int kFrBV = 32;   // V tile
@@ -54,6 +59,18 @@ __device__ __forceinline__ float ld_elem(const uint16_t* p, size_t i) { return b
 __device__ __forceinline__ float ld_elem(const float* p, size_t i) { return p[i]; }
 __device__ __forceinline__ void st_elem(uint16_t* p, size_t i, float x) { p[i] = f32_to_bf16(x); }
 __device__ __forceinline__ void st_elem(float* p, size_t i, float x) { p[i] = x; }
+// 4 consecutive elements at p + i (i a multiple of 4: 8- / 16-byte aligned)
+__device__ __forceinline__ float4 ld4(const uint16_t* p, size_t i) {
+  const uint2 w = *(const uint2*)(p + i);
+  return make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                     __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u));
+}
+__device__ __forceinline__ float4 ld4(const float* p, size_t i) { return *(const float4*)(p + i); }
+__device__ __forceinline__ void st4(uint16_t* p, size_t i, float4 x) {
+  *(uint2*)(p + i) = make_uint2((uint32_t)f32_to_bf16(x.x) | ((uint32_t)f32_to_bf16(x.y) << 16),
+                                (uint32_t)f32_to_bf16(x.z) | ((uint32_t)f32_to_bf16(x.w) << 16));
+}
+__device__ __forceinline__ void st4(float* p, size_t i, float4 x) { *(float4*)(p + i) = x; }
 
 // Sum of v[0..NR-1] over the 32 lanes of a half-wave, reduce-scattered (v is clobbered):
 // returns the total of row `row` (lanes 2j and 2j+1 of the half-wave get row j for
@@ -422,8 +439,17 @@ __device__ __forceinline__ float oct_sum(float x) {
 // DELTA: the KDA delta rule instead of the GLA update (tops/cpu/ops/kda/naive.py:10-118):
 // S <- diag(exp g_t) S;  S <- S + beta_t k_t (v_t - S^T k_t)^T;  o_t = S^T (scale q_t), with a
 // second 8-lane reduction for S^T k_t before the update.
-template <typename TIn, int KP, bool DELTA>
-__global__ __launch_bounds__(256) void fr_decode_kernel(FrParams p) {
+// NORM: the output norm of the GLA layer fused as the epilogue (V <= 128, so the workgroup
+// holds the whole head_v_dim row of every token): y_t = o_t / sqrt(mean_v o_t^2 + eps) * w *
+// silu(g_t) (tops/modules/fused_norm_gate.py:6-37; without g: RMSNorm, layernorm.py:6-35).
+// Each wave leaves its 32 columns of o_t in LDS, in the v block it has just read (a wave
+// reads its own columns of v_t before it writes the same columns of o_t, and no other wave
+// touches them), so the kernel keeps the plain instance's LDS size and with it the compiler's
+// occupancy target; after the block's closing barrier a thread takes 4 columns of one token,
+// the 32 lanes of a half-wave sum a token's squares, and the stores of y are coalesced.  o_t
+// stays in fp32 on the way (the unfused route rounds it to the input dtype first).
+template <typename TIn, int KP, bool DELTA, bool NORM>
+__device__ __forceinline__ void fr_decode_body(const FrParams& p) {
   constexpr int RL = KP / 8;            // rows per lane
   constexpr int DT = 8;                 // tokens per staged block
   constexpr int WV = 4;                 // waves (32-column tiles) per workgroup
@@ -433,6 +459,7 @@ __global__ __launch_bounds__(256) void fr_decode_kernel(FrParams p) {
   __shared__ __attribute__((aligned(16))) float sD[DT][KP];    // exp(gk)
   __shared__ __attribute__((aligned(16))) float sV[DT][32 * WV];
   __shared__ __attribute__((aligned(16))) float sDV[DT][32 * WV];   // exp(gv)
+  float (*sO)[32 * WV] = sV;            // NORM: o_t of the block, over the consumed v
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kr = lane & 7, cq = lane >> 3;
@@ -483,6 +510,24 @@ __global__ __launch_bounds__(256) void fr_decode_kernel(FrParams p) {
       for (int c = 0; c < 4; ++c) S[i][c] = (p.s0 && rok && cok[c]) ? p.s0[o + c] : 0.f;
     }
   }
+  auto store_state = [&]() {
+    if (!p.s_fin || !live) return;
+    // opaque copies: the addresses are formed here, not hoisted into the block loop
+    int rr = r0, cc = c0;
+    asm volatile("" : "+v"(rr), "+v"(cc));
+#pragma unroll
+    for (int i = 0; i < RL; ++i) {
+      if (!qok[i / 4]) continue;
+      const size_t o = sbase + (size_t)(rr + i) * V + cc;
+      if (vec) {
+        *(float4*)(p.s_fin + o) = make_float4(S[i][0], S[i][1], S[i][2], S[i][3]);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (cok[c]) p.s_fin[o + c] = S[i][c];
+      }
+    }
+  };
   for (int b0 = 0; b0 < L; b0 += DT) {
     const int nb = min(DT, L - b0);
     // ---- stage tokens b0 .. b0 + nb - 1 for the workgroup's tiles: element e = tid + 256 u of
@@ -568,7 +613,10 @@ __global__ __launch_bounds__(256) void fr_decode_kernel(FrParams p) {
       }  // DELTA
 #pragma unroll
       for (int c = 0; c < 4; ++c) acc[c] = oct_sum(acc[c]);
-      if (kr == 0) {
+      if constexpr (NORM) {
+        if (kr == 0 && live)
+          *(float4*)&sO[j][32 * wave + 4 * cq] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      } else if (kr == 0) {
         const size_t ov = ((size_t)tok(b0 + j) * H + hh) * V + c0;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -580,30 +628,92 @@ __global__ __launch_bounds__(256) void fr_decode_kernel(FrParams p) {
       }
     }
     __syncthreads();   // the block's tokens are consumed before the next block is staged
-  }
-  if (p.s_fin && live) {
+    if constexpr (NORM) {
+      if (b0 + DT >= L) store_state();   // the state is final: its stores go out first
+      // Thread tid < 128: token j = tid / 16 of the block, columns 8 (tid % 16) .. + 7; the 16
+      // threads of a token are one DPP row, which sums the token's squares on the VALU.
+      // Columns past V (never written, or zero) are left out of the sum.
+      // the lane index is made opaque here, so that the epilogue's addresses are computed
+      // here rather than hoisted out of the block loop and carried through the token loop
+      int et = tid;
+      asm volatile("" : "+v"(et));
+      if (et < 16 * DT) {
+        const int j = et >> 4, c8 = 8 * (et & 15);
+        const float4 oa = *(const float4*)&sO[j][c8], ob4 = *(const float4*)&sO[j][c8 + 4];
+        const float ov[8] = {oa.x, oa.y, oa.z, oa.w, ob4.x, ob4.y, ob4.z, ob4.w};
+        float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < RL; ++i) {
-      if (!qok[i / 4]) continue;
-      const size_t o = sbase + (size_t)(r0 + i) * V + c0;
-      if (vec) {
-        *(float4*)(p.s_fin + o) = make_float4(S[i][0], S[i][1], S[i][2], S[i][3]);
-      } else {
+        for (int c = 0; c < 8; ++c) ss += c8 + c < V ? ov[c] * ov[c] : 0.f;
+        ss = row16_sum(ss);
+        if (j < nb) {
+          const float r = 1.f / sqrtf(ss * p.ninv + p.neps);
+          const size_t ob = ((size_t)tok(b0 + j) * H + hh) * V;
+          const TIn* gate = (const TIn*)p.ng;
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-          if (cok[c]) p.s_fin[o + c] = S[i][c];
+          for (int h4 = 0; h4 < 8; h4 += 4) {
+            const int c4 = c8 + h4;
+            if (c4 >= V) continue;
+            if ((V & 3) == 0) {   // whole quads: one load of gate and weight, one store
+              float y[4] = {ov[h4] * r, ov[h4 + 1] * r, ov[h4 + 2] * r, ov[h4 + 3] * r};
+              if (p.nw) {
+                const float4 w4 = *(const float4*)(p.nw + c4);
+                y[0] *= w4.x; y[1] *= w4.y; y[2] *= w4.z; y[3] *= w4.w;
+              }
+              if (gate) {
+                const float4 g4 = ld4(gate, ob + c4);
+                const float gt[4] = {g4.x, g4.y, g4.z, g4.w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) y[c] *= gt[c] * sigm(gt[c]);
+              }
+              st4((TIn*)p.o, ob + c4, make_float4(y[0], y[1], y[2], y[3]));
+            } else {
+#pragma unroll
+              for (int c = 0; c < 4; ++c) {
+                if (c4 + c >= V) continue;
+                float y = ov[h4 + c] * r;
+                if (p.nw) y *= p.nw[c4 + c];
+                if (gate) {
+                  const float gt = ld_elem(gate, ob + c4 + c);
+                  y *= gt * sigm(gt);
+                }
+                st_elem((TIn*)p.o, ob + c4 + c, y);
+              }
+            }
+          }
+        }
       }
+      if (b0 + DT < L) __syncthreads();   // sO is the next block's v: read before restaged
     }
   }
+  // NORM stores the final state before its last epilogue (below, inside the block loop);
+  // a sequence with no tokens passes h0 through here
+  if (!(NORM && L > 0)) store_state();
 }
 
-template <typename TIn, bool DELTA = false>
+// The GLA instances hold 138 VGPRs (3 waves per SIMD; a 4-wave bound spills); the delta rule
+// fits 128 without spills, so its wrapper asks for 4 waves per SIMD.
+template <typename TIn, int KP, bool DELTA, bool NORM = false>
+__global__ __launch_bounds__(256) void fr_decode_kernel(FrParams p) {
+  fr_decode_body<TIn, KP, DELTA, NORM>(p);
+}
+template <typename TIn, int KP>
+__global__ __launch_bounds__(256, 4) void fr_decode_delta_kernel(FrParams p) {
+  fr_decode_body<TIn, KP, true, false>(p);
+}
+
+template <typename TIn, bool DELTA = false, bool NORM = false>
 static hipError_t launch_fr_decode(const FrParams& p, hipStream_t s) {
   const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
   dim3 grid((((p.V + 31) / 32 + 3) / 4) * p.H * p.N);
-  if (kp == 32) hipLaunchKernelGGL((fr_decode_kernel<TIn, 32, DELTA>), grid, dim3(256), 0, s, p);
-  else if (kp == 64) hipLaunchKernelGGL((fr_decode_kernel<TIn, 64, DELTA>), grid, dim3(256), 0, s, p);
-  else hipLaunchKernelGGL((fr_decode_kernel<TIn, 128, DELTA>), grid, dim3(256), 0, s, p);
+  if constexpr (DELTA) {
+    if (kp == 32) hipLaunchKernelGGL((fr_decode_delta_kernel<TIn, 32>), grid, dim3(256), 0, s, p);
+    else if (kp == 64) hipLaunchKernelGGL((fr_decode_delta_kernel<TIn, 64>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((fr_decode_delta_kernel<TIn, 128>), grid, dim3(256), 0, s, p);
+  } else {
+    if (kp == 32) hipLaunchKernelGGL((fr_decode_kernel<TIn, 32, false, NORM>), grid, dim3(256), 0, s, p);
+    else if (kp == 64) hipLaunchKernelGGL((fr_decode_kernel<TIn, 64, false, NORM>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((fr_decode_kernel<TIn, 128, false, NORM>), grid, dim3(256), 0, s, p);
+  }
   return hipGetLastError();
 }
 
@@ -688,6 +798,32 @@ extern "C" int tops_gla_fused_recurrent_fwd_decode(const void* q, const void* k,
              nullptr, cu_seqlens, B, T, H, K, V, N, (V + kFrBV - 1) / kFrBV, scale, reverse ? 1 : 0};
   hipStream_t s = (hipStream_t)stream;
   hipError_t e = dtype == TOPS_BF16 ? launch_fr_decode<uint16_t>(p, s) : launch_fr_decode<float>(p, s);
+  if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
+  return TOPS_OK;
+}
+
+extern "C" int tops_gla_fused_recurrent_fwd_decode_norm_gate(
+    const void* q, const void* k, const void* v, const float* gk, const float* gv, const float* h0,
+    const void* g, const float* weight, float eps, void* y, float* ht, const int32_t* cu_seqlens,
+    int B, int T, int H, int K, int V, int N, int dtype, float scale, int reverse, void* stream) {
+  if (!q || !k || !v || !y)
+    return tops_set_error(TOPS_ERR_NULL, "gla_fused_recurrent_fwd_decode_norm_gate: null tensor");
+  int rc = fr_check("gla_fused_recurrent_fwd_decode_norm_gate", B, T, H, K, V, N, cu_seqlens, dtype);
+  if (rc != TOPS_OK) return rc;
+  if (V > 128)
+    return tops_set_error(TOPS_ERR_SHAPE,
+                          "gla_fused_recurrent_fwd_decode_norm_gate: the fused norm needs V <= 128");
+  if (!(eps >= 0.f))
+    return tops_set_error(TOPS_ERR_SHAPE, "gla_fused_recurrent_fwd_decode_norm_gate: eps must be >= 0");
+  FrParams p{q, k, v, gk, gv, h0, nullptr, nullptr, y, nullptr, ht, nullptr, nullptr, nullptr, nullptr,
+             nullptr, cu_seqlens, B, T, H, K, V, N, (V + kFrBV - 1) / kFrBV, scale, reverse ? 1 : 0};
+  p.ng = g;
+  p.nw = weight;
+  p.neps = eps;
+  p.ninv = 1.f / (float)V;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = dtype == TOPS_BF16 ? launch_fr_decode<uint16_t, false, true>(p, s)
+                                    : launch_fr_decode<float, false, true>(p, s);
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   return TOPS_OK;
 }

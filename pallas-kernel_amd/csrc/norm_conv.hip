@@ -28,16 +28,6 @@
 
 namespace tops {
 
-// sigmoid from e = exp(-|x|) and the hardware reciprocal (1 ulp); no overflow for any x.
-// e is the hardware 2^x of -|x| log2(e): its relative error, about |x| 2^-24 from rounding
-// the product, moves the sigmoid by at most ~1e-7 for |x| < 16 (and e itself is below 2^-23
-// beyond that), two VALU operations instead of the library expf's range reduction.
-__device__ __forceinline__ float sigm(float x) {
-  const float e = fast_exp2(-fabsf(x) * kLog2e);
-  const float r = __builtin_amdgcn_rcpf(1.f + e);
-  return x >= 0.f ? r : e * r;
-}
-
 template <typename T> __device__ __forceinline__ float ldf(const T* p, long long i) {
   return In<T>::ld(p + i);
 }

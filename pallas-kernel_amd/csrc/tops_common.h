@@ -51,6 +51,16 @@ __device__ __forceinline__ void split_bf16x2(float a, float b, uint32_t& hi, uin
 }
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// sigmoid from e = exp(-|x|) and the hardware reciprocal (1 ulp); no overflow for any x.
+// e is the hardware 2^x of -|x| log2(e): its relative error, about |x| 2^-24 from rounding
+// the product, moves the sigmoid by at most ~1e-7 for |x| < 16 (and e itself is below 2^-23
+// beyond that), two VALU operations instead of the library expf's range reduction.
+__device__ __forceinline__ float sigm(float x) {
+  const float e = fast_exp2(-fabsf(x) * kLog2e);
+  const float r = __builtin_amdgcn_rcpf(1.f + e);
+  return x >= 0.f ? r : e * r;
+}
+
 // Cross-lane sums inside one 16-lane DPP row, on the VALU (no LDS round trip).  A lane whose
 // DPP source lies outside its row reads 0.
 template <int CTRL>

@@ -39,6 +39,8 @@ SIGNATURES = {
     "tops_simple_gla_chunk_bwd": [_vp] * 17 + [_i32] * 8 + [_f32, _vp],
     "tops_gla_fused_recurrent_fwd": [_vp] * 10 + [_i32] * 7 + [_f32, _i32, _vp],
     "tops_gla_fused_recurrent_fwd_decode": [_vp] * 10 + [_i32] * 7 + [_f32, _i32, _vp],
+    "tops_gla_fused_recurrent_fwd_decode_norm_gate": [_vp] * 8 + [_f32, _vp, _vp, _vp]
+                                                     + [_i32] * 7 + [_f32, _i32, _vp],
     "tops_kda_fused_recurrent_fwd_decode": [_vp] * 9 + [_i32] * 7 + [_f32, _vp],
     "tops_gla_fused_recurrent_bwd": [_vp] * 17 + [_i32] * 7 + [_f32, _i32, _vp],
     "tops_prepare_chunk_indices": [_vp, _i32, _i32, _vp, _vp, _i32],

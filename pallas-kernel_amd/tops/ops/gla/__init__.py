@@ -5,7 +5,8 @@ from .stages import (chunk_local_cumsum, chunk_fwd_h, chunk_gla_fwd_intra_gk, ch
                      chunk_gla_bwd_dA_ref, chunk_gla_bwd_dv_ref, chunk_gla_bwd_dqk_intra_ref,
                      chunk_gla_bwd_dqkg_ref)
 from .fused_chunk import fused_chunk_gla
-from .fused_recurrent import fused_recurrent_gla, fused_recurrent_gla_fwd, fused_recurrent_gla_bwd
+from .fused_recurrent import (fused_recurrent_gla, fused_recurrent_gla_fwd, fused_recurrent_gla_bwd,
+                              fused_recurrent_gla_norm_gate)
 
 __all__ = [
     "naive_recurrent_gla",
@@ -25,4 +26,5 @@ __all__ = [
     "fused_recurrent_gla",
     "fused_recurrent_gla_fwd",
     "fused_recurrent_gla_bwd",
+    "fused_recurrent_gla_norm_gate",
 ]

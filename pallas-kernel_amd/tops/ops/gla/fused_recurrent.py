@@ -321,6 +321,53 @@ def fused_recurrent_gla(q, k, v, gk=None, gv=None, scale=None, initial_state=Non
     return o, (ht if output_final_state else None)
 
 
+def fused_recurrent_gla_norm_gate(q, k, v, gk=None, gv=None, g=None, weight=None,
+                                  eps: float = 1e-5, scale=None, initial_state=None,
+                                  output_final_state=False, reverse=False, cu_seqlens=None):
+    """The decode route of the reference's GLA layer as one op: fused_recurrent_gla followed by
+    the layer's output norm over head_v_dim,
+        y = o / sqrt(mean_v(o^2) + eps) * weight * silu(g)
+    (FusedRMSNormGated, tops/modules/fused_norm_gate.py:6-37, applied at
+    tops/layers/gla.py:330-336 after fused_recurrent_gla at :288-297; with g None, the layer's
+    RMSNorm branch, tops/modules/layernorm.py:6-35).
+
+    q, k, v, gk, gv, scale, initial_state, output_final_state, reverse, cu_seqlens: as
+    fused_recurrent_gla.  g [B,T,H,V] (the output gate, per head) or None; weight [V] or None.
+    Returns (y [B,T,H,V] in q.dtype, final state [N,H,K,V] fp32 or None).
+
+    Decode steps (every sequence at most 4 tokens) that need no gradient, with V <= 128 and g
+    in q's dtype, run as one kernel (tops_gla_fused_recurrent_fwd_decode_norm_gate): the norm
+    is the epilogue of the recurrence, on o in fp32, and o itself never reaches HBM.  Other
+    calls compose fused_recurrent_gla and the standalone norm kernel (differentiable)."""
+    B, T, H, K, V, n = _check(q, k, v, gk, gv, initial_state, cu_seqlens, wide_ok=True)
+    assert g is None or tuple(g.shape) == (B, T, H, V), \
+        f"g shape {tuple(g.shape)} != expected {(B, T, H, V)}"
+    assert weight is None or tuple(weight.shape) == (V,), \
+        f"weight shape {tuple(weight.shape)} != expected {(V,)}"
+    if scale is None:
+        scale = K ** -0.5
+    grads = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (q, k, v, gk, gv, g, weight, initial_state))
+    fused = (not grads and V <= 128 and K <= 128 and K % 4 == 0
+             and q.dtype in (torch.float32, torch.bfloat16)
+             and (g is None or g.dtype == q.dtype) and decode_sized(T, cu_seqlens))
+    if not fused:
+        from ...modules.layernorm import rms_norm_gated
+        o, ht = fused_recurrent_gla(q, k, v, gk, gv, scale=scale, initial_state=initial_state,
+                                    output_final_state=output_final_state, reverse=reverse,
+                                    cu_seqlens=cu_seqlens)
+        return rms_norm_gated(o, g, weight, eps), ht
+    q, k, v = (x.contiguous() for x in (q, k, v))
+    y = torch.empty_like(v)
+    ht = torch.empty(n, H, K, V, device=q.device, dtype=torch.float32) if output_final_state else None
+    N.call("tops_gla_fused_recurrent_fwd_decode_norm_gate", N.ptr(q), N.ptr(k), N.ptr(v),
+           N.ptr(_f32(gk)), N.ptr(_f32(gv)), N.ptr(_f32(initial_state)),
+           N.ptr(None if g is None else g.contiguous()), N.ptr(_f32(weight)), float(eps),
+           N.ptr(y), N.ptr(ht), N.ptr(_cu_dev(cu_seqlens, q.device)), B, T, H, K, V, n,
+           N.dtype_code(q.dtype), float(scale), int(bool(reverse)), N.stream())
+    return y, ht
+
+
 def fused_recurrent_gla_fwd(q, k, v, gk=None, gv=None, scale=None, initial_state=None,
                             output_final_state=False, reverse=False, cu_seqlens=None):
     """tops/ops/gla/fused_recurrent.py:380-431.  Returns (o, ht), o in q.dtype."""

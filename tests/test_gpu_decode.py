@@ -18,7 +18,7 @@ import torch
 
 from oracle import gla as O
 from _inputs import gla_inputs
-from _gpu import to_dev, seen, host, rel, tol
+from _gpu import to_dev, seen, host, rel, tol, out_bound
 
 pytestmark = pytest.mark.gpu
 
@@ -275,3 +275,98 @@ def test_device_cu_seqlens_routes_without_readback(cuda_device, calls):
                                         d["g"], initial_state=d["h0"], output_final_state=True,
                                         cu_seqlens=cu)
         assert rel(host(o), ro) < 2e-3 and rel(host(ht), rht) < 2e-3
+
+
+NORM_CASES = [
+    dict(B=8, T=1, H=4, K=128, V=128, gate="gk", h0=True, og=True, w=True),
+    dict(B=2, T=3, H=2, K=64, V=100, gate="both", h0=True, og=True, w=False),
+    dict(B=1, T=8, H=3, K=32, V=64, gate="gv", og=False, w=True, cu=[0, 1, 1, 4, 8]),
+    dict(B=2, T=4, H=2, K=36, V=20, gate="none", h0=True, og=True, w=True, reverse=True),
+    dict(B=1, T=12, H=2, K=128, V=128, gate="gk", h0=True, og=True, w=True, direct=True),
+    dict(B=1, T=40, H=2, K=64, V=96, gate="both", h0=True, og=True, w=True, direct=True,
+         cu=[0, 9, 9, 25, 26, 40]),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("cfg", NORM_CASES, ids=[_id(c) for c in NORM_CASES])
+def test_decode_norm_gate(cfg, dtype, cuda_device, calls):
+    """The GLA layer's decode route with its output norm fused into the decode kernel:
+    y = RMSNorm(o) * weight * silu(g) over V (tops/layers/gla.py:288-297, 330-336), against
+    the oracle's recurrence composed with the norm oracle (oracle.modules.rmsnorm_gated), for
+    gk / gv / both / no gate, output gate and weight on and off, reverse, varlen with empty
+    sequences, V off the 32-column tile; the `direct` cases call the C entry with sequences of
+    up to 20 tokens (several 8-token blocks, the epilogue between their barriers)."""
+    from oracle import modules as M
+    from tops import _native as N
+    from tops.ops.gla import fused_recurrent_gla_norm_gate
+    B, T, H, K, V = (cfg[x] for x in "BTHKV")
+    cu = cfg.get("cu")
+    n = len(cu) - 1 if cu else B
+    print(f"decode norm case {_id(cfg)} {dtype}", flush=True)
+    d = gla_inputs(B, T, H, K, V, seed=T * 7 + V, gate_div=4.0, h0=cfg.get("h0", False), N=n)
+    gk, gv = _gates(cfg, d, B, T, H, V, T + K + 1)
+    rng = np.random.Generator(np.random.PCG64(V + T))
+    og = rng.standard_normal((B, T, H, V)).astype(np.float32) * 2 if cfg["og"] else None
+    w = (1 + 0.3 * rng.standard_normal(V)).astype(np.float32) if cfg["w"] else None
+    rev, eps = cfg.get("reverse", False), 1e-5
+    f = lambda x: to_dev(x, torch.float32, cuda_device)  # noqa: E731
+    q, k, v = (to_dev(d[x], dtype, cuda_device) for x in "qkv")
+    ogt = to_dev(og, dtype, cuda_device)
+    if cfg.get("direct"):
+        y = torch.empty_like(v)
+        ht = torch.empty(n, H, K, V, device=cuda_device, dtype=torch.float32)
+        cut = None if cu is None else torch.tensor(cu, dtype=torch.int32, device=cuda_device)
+        N.call("tops_gla_fused_recurrent_fwd_decode_norm_gate", N.ptr(q), N.ptr(k), N.ptr(v),
+               N.ptr(f(gk)), N.ptr(f(gv)), N.ptr(f(d["h0"])), N.ptr(ogt), N.ptr(f(w)), eps,
+               N.ptr(y), N.ptr(ht), N.ptr(cut), B, T, H, K, V, n, N.dtype_code(dtype),
+               float(K ** -0.5), int(rev), N.stream())
+    else:
+        with torch.no_grad():
+            y, ht = fused_recurrent_gla_norm_gate(q, k, v, f(gk), f(gv), ogt, f(w), eps,
+                                                  initial_state=f(d["h0"]), output_final_state=True,
+                                                  reverse=rev, cu_seqlens=cu)
+        assert "tops_gla_fused_recurrent_fwd_decode_norm_gate" in calls
+        assert "tops_rmsnorm_gated_fwd" not in calls
+    torch.cuda.synchronize()
+    ro, rht = O.fused_recurrent_fwd(seen(d["q"], dtype), seen(d["k"], dtype), seen(d["v"], dtype),
+                                    gk, gv, scale=K ** -0.5, initial_state=d["h0"],
+                                    output_final_state=True, reverse=rev, cu_seqlens=cu)
+    ry = M.rmsnorm_gated(ro, seen(og, dtype), w, eps)
+    assert y.dtype == dtype
+    ey, eh = rel(host(y), ry), rel(host(ht), rht)
+    print(f"y {ey:.2e} ht {eh:.2e}")
+    assert ey < out_bound(ry, dtype, dtype) and eh < tol(dtype)
+
+
+def test_decode_norm_gate_unfused_routes(cuda_device, calls):
+    """Calls the fused kernel does not take compose fused_recurrent_gla with the standalone norm
+    kernel: a 6-token sequence (chunk kernels), and a decode step with gradients (autograd
+    through both ops), each against the oracle; the gradient of y w.r.t. the output gate too."""
+    from oracle import modules as M
+    from tops.ops.gla import fused_recurrent_gla_norm_gate
+    B, H, K, V = 2, 2, 64, 64
+    rng = np.random.Generator(np.random.PCG64(3))
+    for T, grad in ((6, False), (1, True)):
+        calls.clear()
+        d = gla_inputs(B, T, H, K, V, seed=60 + T, h0=True)
+        og = rng.standard_normal((B, T, H, V)).astype(np.float32)
+        w = (1 + 0.3 * rng.standard_normal(V)).astype(np.float32)
+        q, k, v = (to_dev(d[x], torch.float32, cuda_device) for x in "qkv")
+        g, h0 = to_dev(d["g"], torch.float32, cuda_device), to_dev(d["h0"], torch.float32, cuda_device)
+        ogt = to_dev(og, torch.float32, cuda_device).requires_grad_(grad)
+        y, ht = fused_recurrent_gla_norm_gate(q, k, v, g, None, ogt, to_dev(w, torch.float32, cuda_device),
+                                              initial_state=h0, output_final_state=True)
+        if grad:
+            dy = rng.standard_normal((B, T, H, V)).astype(np.float32)
+            y.backward(to_dev(dy, torch.float32, cuda_device))
+        torch.cuda.synchronize()
+        assert "tops_gla_fused_recurrent_fwd_decode_norm_gate" not in calls
+        assert "tops_rmsnorm_gated_fwd" in calls
+        ro, rht = O.fused_recurrent_fwd(d["q"], d["k"], d["v"], d["g"], initial_state=d["h0"],
+                                        output_final_state=True)
+        assert rel(host(y), M.rmsnorm_gated(ro, og, w, 1e-5)) < 1e-4
+        assert rel(host(ht), rht) < 1e-4
+        if grad:
+            rdg = M.rmsnorm_gated_bwd(ro, og, w, dy, 1e-5)[1]
+            assert rel(host(ogt.grad), rdg) < 1e-4
