@@ -27,9 +27,10 @@ pytestmark = pytest.mark.gpu
 @pytest.fixture(autouse=True)
 def _paired_layout():
     from tops import utils as U
+    prev = U.checkpoint_layout()
     U.set_checkpoint_layout("paired")
     yield
-    U.set_checkpoint_layout("full")
+    U.set_checkpoint_layout(prev)
 
 CASES = [
     dict(B=2, T=130, H=3, K=64, V=64, seed=31),                       # 3 chunks per sequence
