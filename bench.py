@@ -288,6 +288,43 @@ def _decode(dev, gen, iters):
                                                           output_final_state=True), iters)
     norm_route = {"what": "decode step + output norm, B256 H16 K=V=128, wall time per call",
                   "fused_ms": round(fus * 1e3, 4), "unfused_ms": round(unf * 1e3, 4)}
+    # the layer's whole decode route from the projections: three ShortConvolution steps (W 4,
+    # SiLU, fp32 caches), the recurrence and the norm, unfused and as one kernel
+    from tops.modules import short_conv_step
+    from tops.ops.gla import fused_recurrent_gla_conv_norm_gate
+    Dk = Hg * D
+    xq, xk, xv = (torch.randn(Bg, 1, Dk, device=dev, generator=gen).to(bf) for _ in range(3))
+    cws = [torch.randn(Dk, 4, device=dev, generator=gen) / 2 for _ in range(3)]
+    ccs = [torch.randn(Bg, Dk, 4, device=dev, generator=gen) for _ in range(3)]
+
+    def unfused_layer():
+        qkv = [short_conv_step(x, w, None, "silu", c, True)[0].reshape(Bg, 1, Hg, D)
+               for x, w, c in zip((xq, xk, xv), cws, ccs)]
+        o, _ = fused_recurrent_gla(*qkv, g1, initial_state=s1, output_final_state=True)
+        return rms_norm_gated(o, og1.float(), nw1)
+
+    with torch.no_grad():
+        unf_l = _time(unfused_layer, iters)
+        fus_l = _time(lambda: fused_recurrent_gla_conv_norm_gate(
+            *(x.reshape(Bg, 1, Hg, D) for x in (xq, xk, xv)), cws, None, ccs, "silu", g1, og1,
+            nw1, initial_state=s1, output_final_state=True), iters)
+    norm_route["layer_route"] = {
+        "what": "ShortConvolution q/k/v steps + decode step + output norm, B256 H16 K=V=128 W4",
+        "fused_ms": round(fus_l * 1e3, 4), "unfused_ms": round(unf_l * 1e3, 4)}
+    # the same route at a small serving batch (B 8), where the launches dominate
+    b8 = slice(0, 8)
+    with torch.no_grad():
+        unf8 = _time(lambda: rms_norm_gated(fused_recurrent_gla(
+            *[short_conv_step(x[b8], w, None, "silu", c[b8], True)[0].reshape(8, 1, Hg, D)
+              for x, w, c in zip((xq, xk, xv), cws, ccs)], g1[b8], initial_state=s1[b8],
+            output_final_state=True)[0], og1[b8].float(), nw1), iters)
+        fus8 = _time(lambda: fused_recurrent_gla_conv_norm_gate(
+            *(x[b8].reshape(8, 1, Hg, D) for x in (xq, xk, xv)), cws, None,
+            [c[b8] for c in ccs], "silu", g1[b8], og1[b8], nw1, initial_state=s1[b8],
+            output_final_state=True), iters)
+    norm_route["layer_route_b8"] = {"what": "the same at B8 (launch-bound)",
+                                    "fused_ms": round(fus8 * 1e3, 4),
+                                    "unfused_ms": round(unf8 * 1e3, 4)}
     return {"config": "decode steps (state-cache bound)", "kernels": rows, "copy_ref": copy_ref,
             "norm_route": norm_route}
 

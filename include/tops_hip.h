@@ -313,6 +313,32 @@ int tops_gla_fused_recurrent_fwd_decode_norm_gate(const void* q, const void* k, 
                                                   int T, int H, int K, int V, int N, int dtype,
                                                   float scale, int reverse, void* stream);
 
+/* The GLA layer's decode route from its projections to the normalised output, one kernel:
+ *   q, k, v = act(ShortConvolution(xq, xk, xv)) with the conv caches rolled, then the recurrence
+ *   of tops_gla_fused_recurrent_fwd_decode (gk, h0 -> ht), then y = RMSNorm(o) * weight * silu(g).
+ * Replaces, on the reference layer's decode route (tops/layers/gla.py:236-262, 288-297,
+ * 330-336), the three ShortConvolution calls (tops/modules/convolution.py:44-173),
+ * fused_recurrent_gla and FusedRMSNormGated (tops/modules/fused_norm_gate.py:6-37).
+ *   xq, xk [B,T,H,K], xv [B,T,H,V] (dtype): the projections before the convolutions
+ *   conv_w_* [D,W] fp32 (D = H*K, H*K, H*V), 1 <= W <= 8; conv_b_* [D] fp32 or NULL
+ *   cache_* [N,D,W] fp32 or NULL (zeros; pass NULL for a prefill, which reads no cache);
+ *   cache_*_out [N,D,W] fp32 or NULL: the last W inputs of each sequence (positions before it
+ *   from cache_*); may alias cache_*.  activation 1: SiLU after the convolution
+ *   gk [B,T,H,K] fp32 log gates or NULL; h0 [N,H,K,V] fp32 or NULL; g [B,T,H,V] (dtype) or NULL;
+ *   weight [V] fp32 or NULL; y [B,T,H,V] (fp32 when y_fp32, else dtype); ht [N,H,K,V] fp32 or NULL
+ * Limits: K <= 128, K % 4 == 0, V <= 128; forward time only. */
+int tops_gla_decode_conv_norm_gate(const void* xq, const void* xk, const void* xv,
+                                   const float* conv_w_q, const float* conv_w_k,
+                                   const float* conv_w_v, const float* conv_b_q,
+                                   const float* conv_b_k, const float* conv_b_v,
+                                   const float* cache_q, const float* cache_k,
+                                   const float* cache_v, float* cache_q_out, float* cache_k_out,
+                                   float* cache_v_out, int W, int activation, const float* gk,
+                                   const float* h0, const void* g, const float* weight, float eps,
+                                   void* y, int y_fp32, float* ht, const int32_t* cu_seqlens,
+                                   int B, int T, int H, int K, int V, int N, int dtype,
+                                   float scale, void* stream);
+
 /* KDA decode steps: the per-token delta rule
  *   S <- diag(exp g_t) S;  S <- S + beta_t k_t (v_t - S^T k_t)^T;  o_t = S^T (scale q_t)
  * on the same register-state kernel, for sequences of a few tokens.  q, k [B,T,H,K] and

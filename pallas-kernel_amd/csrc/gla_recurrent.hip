@@ -50,6 +50,17 @@ struct FrParams {
   const float* nw = nullptr;     // norm weight [V], or NULL
   float neps = 0.f;
   float ninv = 0.f;              // 1 / V
+  // decode with the layer's ShortConvolutions fused into the token staging (CONV instance):
+  // q, k, v are then the projections before the convolutions; per input (0 q, 1 k, 2 v) the
+  // weights [D,W] fp32, bias [D] or NULL, cache [N,D,W] fp32 in (NULL: zeros) and out (NULL:
+  // not kept; may alias the input cache), D = H*K or H*V
+  const float* cw[3] = {nullptr, nullptr, nullptr};
+  const float* cb[3] = {nullptr, nullptr, nullptr};
+  const float* cci[3] = {nullptr, nullptr, nullptr};
+  float* cco[3] = {nullptr, nullptr, nullptr};
+  int cW = 0;                    // taps
+  int cact = 0;                  // 1: SiLU after the convolution
+  int y32 = 0;                   // 1: the output is fp32 (whatever the input dtype)
 };
 
 constexpr int kFrBV = 32;   // V tile
@@ -448,7 +459,7 @@ __device__ __forceinline__ float oct_sum(float x) {
 // occupancy target; after the block's closing barrier a thread takes 4 columns of one token,
 // the 32 lanes of a half-wave sum a token's squares, and the stores of y are coalesced.  o_t
 // stays in fp32 on the way (the unfused route rounds it to the input dtype first).
-template <typename TIn, int KP, bool DELTA, bool NORM>
+template <typename TIn, int KP, bool DELTA, bool NORM, bool CONV = false>
 __device__ __forceinline__ void fr_decode_body(const FrParams& p) {
   constexpr int RL = KP / 8;            // rows per lane
   constexpr int DT = 8;                 // tokens per staged block
@@ -496,6 +507,31 @@ __device__ __forceinline__ void fr_decode_body(const FrParams& p) {
   const TIn* kk = (const TIn*)p.k;
   const TIn* v = (const TIn*)p.v;
   auto tok = [&](int j) { return p.reverse ? bos + L - 1 - j : bos + j; };
+  // CONV: the convolution of input x (weights wt, bias, cache cin) for channel d (column c of
+  // head hh, row width DW) at position jj of the sequence: the causal W-tap window over the
+  // projections, positions before the sequence read from the conv cache (position -1 = its
+  // newest entry, W - 1)
+  // (the taps are unrolled to the largest W, 8, so that every load of a window issues before
+  // the first is used)
+  auto conv_in = [&](const TIn* x, const float* wt, const float* bias, const float* cin, int D,
+                     int d, int DW, int c, int jj) __attribute__((always_inline)) {
+    const int W = p.cW;
+    const float* w = wt + (size_t)d * W;
+    const float* cache = cin ? cin + ((size_t)n * D + d) * W : nullptr;
+    float wv[8], xv[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int pos = jj - (W - 1) + t;
+      wv[t] = t < W ? w[t] : 0.f;
+      xv[t] = t >= W ? 0.f
+                     : (pos >= 0 ? ld_elem(x, ((size_t)(bos + pos) * H + hh) * DW + c)
+                                 : (cache ? cache[W + pos] : 0.f));
+    }
+    float acc = bias ? bias[d] : 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc += wv[t] * xv[t];
+    return p.cact ? acc * sigm(acc) : acc;
+  };
 
   float S[RL][4];
 #pragma unroll
@@ -510,6 +546,25 @@ __device__ __forceinline__ void fr_decode_body(const FrParams& p) {
       for (int c = 0; c < 4; ++c) S[i][c] = (p.s0 && rok && cok[c]) ? p.s0[o + c] : 0.f;
     }
   }
+  // CONV: the rolled conv caches, one thread per channel: entry t of channel d is the input at
+  // position L - W + t (before the sequence: the old cache entry W + pos); written after the
+  // last block (below).  One call per input with its own pointers: selecting among the
+  // parameter block's pointers by a run-time index would put the whole block in private memory.
+  auto roll = [&](const TIn* x, const float* cache, float* out, int DW) __attribute__((always_inline)) {
+    if (!out) return;
+    const int W = p.cW, D = H * DW;
+    for (int c = tid; c < DW; c += 256) {
+      const int d = hh * DW + c;
+      const size_t cbase = ((size_t)n * D + d) * W;
+      for (int t = 0; t < W; ++t) {
+        const int pos = L - W + t;
+        float val;
+        if (pos >= 0) val = ld_elem(x, ((size_t)(bos + pos) * H + hh) * DW + c);
+        else val = cache ? cache[cbase + W + pos] : 0.f;
+        out[cbase + t] = val;
+      }
+    }
+  };
   auto store_state = [&]() {
     if (!p.s_fin || !live) return;
     // opaque copies: the addresses are formed here, not hoisted into the block loop
@@ -532,21 +587,36 @@ __device__ __forceinline__ void fr_decode_body(const FrParams& p) {
     const int nb = min(DT, L - b0);
     // ---- stage tokens b0 .. b0 + nb - 1 for the workgroup's tiles: element e = tid + 256 u of
     // the [DT][KP] / [DT][32 WV] blocks
+    // CONV: an opaque copy of the lane index, so that the window's addresses are formed here
+    // rather than hoisted out of the block loop and carried through the token loop
+    int stid = tid;
+    if constexpr (CONV) asm volatile("" : "+v"(stid));
 #pragma unroll 2
     for (int u = 0; u < DT * KP / 256; ++u) {
-      const int e = tid + 256 * u, j = e / KP, r = e % KP;
+      const int e = stid + 256 * u, j = e / KP, r = e % KP;
       const bool ok = j < nb && r < K;
       const size_t o = ok ? ((size_t)tok(b0 + j) * H + hh) * K + r : 0;
-      sQ[j][r] = ok ? ld_elem(q, o) * p.scale : 0.f;
-      sK[j][r] = ok ? ld_elem(kk, o) : 0.f;
+      if constexpr (CONV) {
+        sQ[j][r] = ok ? conv_in(q, p.cw[0], p.cb[0], p.cci[0], H * K, hh * K + r, K, r, b0 + j) *
+                            p.scale
+                      : 0.f;
+        sK[j][r] = ok ? conv_in(kk, p.cw[1], p.cb[1], p.cci[1], H * K, hh * K + r, K, r, b0 + j)
+                      : 0.f;
+      } else {
+        sQ[j][r] = ok ? ld_elem(q, o) * p.scale : 0.f;
+        sK[j][r] = ok ? ld_elem(kk, o) : 0.f;
+      }
       sD[j][r] = (ok && p.gk) ? fast_exp2(p.gk[o] * kLog2e) : 1.f;
     }
 #pragma unroll
     for (int u = 0; u < DT * 32 * WV / 256; ++u) {
-      const int e = tid + 256 * u, j = e / (32 * WV), c = e % (32 * WV), col = 32 * WV * tg + c;
+      const int e = stid + 256 * u, j = e / (32 * WV), c = e % (32 * WV), col = 32 * WV * tg + c;
       const bool ok = j < nb && col < V;
       const size_t o = ok ? ((size_t)tok(b0 + j) * H + hh) * V + col : 0;
-      sV[j][c] = ok ? ld_elem(v, o) : 0.f;
+      if constexpr (CONV)
+        sV[j][c] = ok ? conv_in(v, p.cw[2], p.cb[2], p.cci[2], H * V, hh * V + col, V, col, b0 + j)
+                      : 0.f;
+      else sV[j][c] = ok ? ld_elem(v, o) : 0.f;
       sDV[j][c] = (ok && p.gv) ? fast_exp2(p.gv[o] * kLog2e) : 1.f;
     }
     if constexpr (DELTA) {
@@ -665,7 +735,8 @@ __device__ __forceinline__ void fr_decode_body(const FrParams& p) {
 #pragma unroll
                 for (int c = 0; c < 4; ++c) y[c] *= gt[c] * sigm(gt[c]);
               }
-              st4((TIn*)p.o, ob + c4, make_float4(y[0], y[1], y[2], y[3]));
+              if (CONV && p.y32) st4((float*)p.o, ob + c4, make_float4(y[0], y[1], y[2], y[3]));
+              else st4((TIn*)p.o, ob + c4, make_float4(y[0], y[1], y[2], y[3]));
             } else {
 #pragma unroll
               for (int c = 0; c < 4; ++c) {
@@ -676,7 +747,8 @@ __device__ __forceinline__ void fr_decode_body(const FrParams& p) {
                   const float gt = ld_elem(gate, ob + c4 + c);
                   y *= gt * sigm(gt);
                 }
-                st_elem((TIn*)p.o, ob + c4 + c, y);
+                if (CONV && p.y32) st_elem((float*)p.o, ob + c4 + c, y);
+                else st_elem((TIn*)p.o, ob + c4 + c, y);
               }
             }
           }
@@ -688,6 +760,13 @@ __device__ __forceinline__ void fr_decode_body(const FrParams& p) {
   // NORM stores the final state before its last epilogue (below, inside the block loop);
   // a sequence with no tokens passes h0 through here
   if (!(NORM && L > 0)) store_state();
+  // CONV: the rolled caches, now that every block's staging has read the old entries (so an
+  // output may alias its input cache)
+  if constexpr (CONV) {
+    roll(q, p.cci[0], p.cco[0], K);
+    roll(kk, p.cci[1], p.cco[1], K);
+    roll(v, p.cci[2], p.cco[2], V);
+  }
 }
 
 // The GLA instances hold 138 VGPRs (3 waves per SIMD; a 4-wave bound spills); the delta rule
@@ -699,6 +778,20 @@ __global__ __launch_bounds__(256) void fr_decode_kernel(FrParams p) {
 template <typename TIn, int KP>
 __global__ __launch_bounds__(256, 4) void fr_decode_delta_kernel(FrParams p) {
   fr_decode_body<TIn, KP, true, false>(p);
+}
+template <typename TIn, int KP>
+__global__ __launch_bounds__(256) void fr_decode_conv_kernel(FrParams p) {
+  fr_decode_body<TIn, KP, false, true, true>(p);
+}
+
+template <typename TIn>
+static hipError_t launch_fr_decode_conv(const FrParams& p, hipStream_t s) {
+  const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
+  dim3 grid(p.H * p.N);
+  if (kp == 32) hipLaunchKernelGGL((fr_decode_conv_kernel<TIn, 32>), grid, dim3(256), 0, s, p);
+  else if (kp == 64) hipLaunchKernelGGL((fr_decode_conv_kernel<TIn, 64>), grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((fr_decode_conv_kernel<TIn, 128>), grid, dim3(256), 0, s, p);
+  return hipGetLastError();
 }
 
 template <typename TIn, bool DELTA = false, bool NORM = false>
@@ -824,6 +917,51 @@ extern "C" int tops_gla_fused_recurrent_fwd_decode_norm_gate(
   hipStream_t s = (hipStream_t)stream;
   hipError_t e = dtype == TOPS_BF16 ? launch_fr_decode<uint16_t, false, true>(p, s)
                                     : launch_fr_decode<float, false, true>(p, s);
+  if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
+  return TOPS_OK;
+}
+
+extern "C" int tops_gla_decode_conv_norm_gate(
+    const void* xq, const void* xk, const void* xv, const float* conv_w_q, const float* conv_w_k,
+    const float* conv_w_v, const float* conv_b_q, const float* conv_b_k, const float* conv_b_v,
+    const float* cache_q, const float* cache_k, const float* cache_v, float* cache_q_out,
+    float* cache_k_out, float* cache_v_out, int W, int activation, const float* gk,
+    const float* h0, const void* g, const float* weight, float eps, void* y, int y_fp32,
+    float* ht, const int32_t* cu_seqlens, int B, int T, int H, int K, int V, int N, int dtype,
+    float scale, void* stream) {
+  if (!xq || !xk || !xv || !conv_w_q || !conv_w_k || !conv_w_v || !y)
+    return tops_set_error(TOPS_ERR_NULL, "gla_decode_conv_norm_gate: null tensor");
+  int rc = fr_check("gla_decode_conv_norm_gate", B, T, H, K, V, N, cu_seqlens, dtype);
+  if (rc != TOPS_OK) return rc;
+  if (V > 128)
+    return tops_set_error(TOPS_ERR_SHAPE, "gla_decode_conv_norm_gate: the fused norm needs V <= 128");
+  if (W < 1 || W > 8)
+    return tops_set_error(TOPS_ERR_SHAPE, "gla_decode_conv_norm_gate: need 1 <= W <= 8");
+  if (!(eps >= 0.f))
+    return tops_set_error(TOPS_ERR_SHAPE, "gla_decode_conv_norm_gate: eps must be >= 0");
+  FrParams p{xq, xk, xv, gk, nullptr, h0, nullptr, nullptr, y, nullptr, ht, nullptr, nullptr,
+             nullptr, nullptr, nullptr, cu_seqlens, B, T, H, K, V, N, (V + kFrBV - 1) / kFrBV,
+             scale, 0};
+  p.ng = g;
+  p.nw = weight;
+  p.neps = eps;
+  p.ninv = 1.f / (float)V;
+  const float* cw[3] = {conv_w_q, conv_w_k, conv_w_v};
+  const float* cb[3] = {conv_b_q, conv_b_k, conv_b_v};
+  const float* ci[3] = {cache_q, cache_k, cache_v};
+  float* co[3] = {cache_q_out, cache_k_out, cache_v_out};
+  for (int i = 0; i < 3; ++i) {
+    p.cw[i] = cw[i];
+    p.cb[i] = cb[i];
+    p.cci[i] = ci[i];
+    p.cco[i] = co[i];
+  }
+  p.cW = W;
+  p.cact = activation ? 1 : 0;
+  p.y32 = y_fp32 ? 1 : 0;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = dtype == TOPS_BF16 ? launch_fr_decode_conv<uint16_t>(p, s)
+                                    : launch_fr_decode_conv<float>(p, s);
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   return TOPS_OK;
 }

@@ -41,6 +41,9 @@ SIGNATURES = {
     "tops_gla_fused_recurrent_fwd_decode": [_vp] * 10 + [_i32] * 7 + [_f32, _i32, _vp],
     "tops_gla_fused_recurrent_fwd_decode_norm_gate": [_vp] * 8 + [_f32, _vp, _vp, _vp]
                                                      + [_i32] * 7 + [_f32, _i32, _vp],
+    "tops_gla_decode_conv_norm_gate": [_vp] * 15 + [_i32, _i32] + [_vp] * 4 + [_f32, _vp, _i32,
+                                                                               _vp, _vp]
+                                      + [_i32] * 7 + [_f32, _vp],
     "tops_kda_fused_recurrent_fwd_decode": [_vp] * 9 + [_i32] * 7 + [_f32, _vp],
     "tops_gla_fused_recurrent_bwd": [_vp] * 17 + [_i32] * 7 + [_f32, _i32, _vp],
     "tops_prepare_chunk_indices": [_vp, _i32, _i32, _vp, _vp, _i32],

@@ -113,6 +113,35 @@ def short_conv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None 
     return _ShortConv.apply(x, weight, bias, _act(activation), cu, n, bool(output_final_state))
 
 
+@torch.no_grad()
+def short_conv_step(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
+                    activation: str | None = "silu", cache: torch.Tensor | None = None,
+                    output_final_state: bool = False, cu_seqlens=None):
+    """One decode step of ShortConvolution (tops/modules/convolution.py:82-126): x [B,1,D] (or
+    [1,N,D] with cu_seqlens), weight [D,1,W] or [D,W], cache [N,D,W].  The cache rolls by one
+    token and takes x; y = act(sum_j cache[.., j] w[.., j] + bias), or act(x w[.., W-1] + bias)
+    without a cache.  Returns (y shaped like x, the rolled cache or None).  Inference only."""
+    D = x.shape[-1]
+    W = weight.numel() // D
+    n = x.shape[0] if cu_seqlens is None else len(cu_seqlens) - 1
+    N.require_cuda(x, cache)
+    if output_final_state and cache is None:
+        cache = torch.zeros(n, D, W, device=x.device, dtype=torch.float32)
+    xs = _kin(x[0] if cu_seqlens is not None else x[:, 0])
+    if cache is not None and tuple(cache.shape) != (n, D, W):
+        raise AssertionError(f"cache shape {tuple(cache.shape)} != {(n, D, W)}")
+    cin = None if cache is None else cache.to(torch.float32).contiguous()
+    cout = None if cache is None else torch.empty_like(cin)
+    w32 = weight.reshape(D, W).to(torch.float32).contiguous()
+    b32 = None if bias is None else bias.to(torch.float32).contiguous()
+    ydt = _out_dtype(x, weight)
+    y = torch.empty(n, D, device=x.device, dtype=ydt)
+    N.call("tops_short_conv_step", N.ptr(xs), N.dtype_code(xs.dtype), N.ptr(cin), N.ptr(cout),
+           N.ptr(w32), N.ptr(b32), N.ptr(y), N.dtype_code(ydt), n, D, W, _act(activation),
+           N.stream())
+    return y.reshape(x.shape), None if cout is None else cout.to(cache.dtype)
+
+
 class ShortConvolution(nn.Module):
     """Causal depthwise 1D convolution (groups = hidden_size, W - 1 left padding), optional
     SiLU activation."""
@@ -148,21 +177,6 @@ class ShortConvolution(nn.Module):
              output_final_state: bool = False, cu_seqlens=None):
         """One decode step: x [B,1,D] (or [1,N,D] with cu_seqlens), cache [N,D,W].  Returns
         (y shaped like x, the rolled cache or None).  Inference only (no autograd)."""
-        W, D = self.kernel_size, self.hidden_size
-        n = x.shape[0] if cu_seqlens is None else len(cu_seqlens) - 1
-        N.require_cuda(x, cache)
-        if output_final_state and cache is None:
-            cache = torch.zeros(n, D, W, device=x.device, dtype=torch.float32)
-        xs = _kin(x[0] if cu_seqlens is not None else x[:, 0])
-        if cache is not None and tuple(cache.shape) != (n, D, W):
-            raise AssertionError(f"cache shape {tuple(cache.shape)} != {(n, D, W)}")
-        cin = None if cache is None else cache.to(torch.float32).contiguous()
-        cout = None if cache is None else torch.empty_like(cin)
-        w32 = self.weight.detach().reshape(D, W).to(torch.float32).contiguous()
-        b32 = None if self.bias is None else self.bias.detach().to(torch.float32).contiguous()
-        ydt = _out_dtype(x, self.weight)
-        y = torch.empty(n, D, device=x.device, dtype=ydt)
-        N.call("tops_short_conv_step", N.ptr(xs), N.dtype_code(xs.dtype), N.ptr(cin), N.ptr(cout),
-               N.ptr(w32), N.ptr(b32), N.ptr(y), N.dtype_code(ydt), n, D, W,
-               _act(self.activation), N.stream())
-        return y.reshape(x.shape), None if cout is None else cout.to(cache.dtype)
+        return short_conv_step(x, self.weight.detach(),
+                               None if self.bias is None else self.bias.detach(),
+                               self.activation, cache, output_final_state, cu_seqlens)

@@ -6,7 +6,7 @@ from .stages import (chunk_local_cumsum, chunk_fwd_h, chunk_gla_fwd_intra_gk, ch
                      chunk_gla_bwd_dqkg_ref)
 from .fused_chunk import fused_chunk_gla
 from .fused_recurrent import (fused_recurrent_gla, fused_recurrent_gla_fwd, fused_recurrent_gla_bwd,
-                              fused_recurrent_gla_norm_gate)
+                              fused_recurrent_gla_norm_gate, fused_recurrent_gla_conv_norm_gate)
 
 __all__ = [
     "naive_recurrent_gla",
@@ -27,4 +27,5 @@ __all__ = [
     "fused_recurrent_gla_fwd",
     "fused_recurrent_gla_bwd",
     "fused_recurrent_gla_norm_gate",
+    "fused_recurrent_gla_conv_norm_gate",
 ]

@@ -368,6 +368,99 @@ def fused_recurrent_gla_norm_gate(q, k, v, gk=None, gv=None, g=None, weight=None
     return y, ht
 
 
+def fused_recurrent_gla_conv_norm_gate(x_q, x_k, x_v, conv_weights, conv_biases=None,
+                                       conv_caches=None, conv_activation="silu", gk=None, g=None,
+                                       weight=None, eps: float = 1e-5, scale=None,
+                                       initial_state=None, output_final_state=False,
+                                       cu_seqlens=None):
+    """The reference GLA layer's decode route from its projections to the normalised output
+    (tops/layers/gla.py:236-262, 288-297, 330-336), as one op:
+        q, k, v = ShortConvolution(x_q), (x_k), (x_v)    (tops/modules/convolution.py:44-173)
+        o, ht = fused_recurrent_gla(q, k, v, gk, initial_state, output_final_state)
+        y = RMSNorm(o) * weight * silu(g)                 (tops/modules/fused_norm_gate.py:6-37)
+
+    x_q, x_k [B,T,H,K] and x_v [B,T,H,V]: the q / k / v projections before their
+    convolutions; conv_weights (w_q, w_k, w_v), each [D,1,W] or [D,W] (D = H*K, H*K, H*V);
+    conv_biases (b_q, b_k, b_v) or None; conv_caches (c_q, c_k, c_v), each [N,D,W], or None;
+    conv_activation "silu" / "swish" / None; gk [B,T,H,K] log gates; g [B,T,H,V] or None;
+    weight [V] or None.  As in the layer, a call with one token per sequence (B*T == N) is a
+    conv decode step (the caches roll by one token), any other call a prefill (the caches are
+    not read, the new ones are the last W inputs).  Returns (y [B,T,H,V], final state
+    [N,H,K,V] fp32 or None, (c_q, c_k, c_v) or None): y in the dtype the layer's route gives
+    (the promotion of x and the conv weights).
+
+    Without gradients, with every sequence at most 4 tokens, K <= 128, V <= 128 and no
+    num_kv_groups repeat, it runs as one kernel (tops_gla_decode_conv_norm_gate): the
+    convolutions are the decode kernel's token staging, the norm its epilogue; q, k, v and o
+    never reach HBM.  Other calls compose short_conv / short_conv_step,
+    fused_recurrent_gla and the norm kernel (differentiable)."""
+    from ...modules.convolution import _act, short_conv, short_conv_step
+    B, T, H, K = x_q.shape
+    V = x_v.shape[-1]
+    assert tuple(x_k.shape) == (B, T, H, K) and x_v.ndim == 4 and tuple(x_v.shape[:3]) == (B, T, H), \
+        "x_q, x_k [B,T,H,K] and x_v [B,T,H,V] expected"
+    n = B if cu_seqlens is None else len(cu_seqlens) - 1
+    ws = [w.reshape(w.shape[0], -1) for w in conv_weights]
+    W = ws[0].shape[1]
+    dims = (H * K, H * K, H * V)
+    for w, D in zip(ws, dims):
+        assert tuple(w.shape) == (D, W), f"conv weight shape {tuple(w.shape)} != {(D, W)}"
+    bs = tuple(conv_biases) if conv_biases is not None else (None, None, None)
+    cs = tuple(conv_caches) if conv_caches is not None else (None, None, None)
+    step = B * T == n
+    ydt = torch.promote_types(x_q.dtype, ws[0].dtype)
+    if ydt not in (torch.float32, torch.bfloat16):
+        ydt = torch.float32
+    grads = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad
+        for t in (x_q, x_k, x_v, gk, g, weight, initial_state, *conv_weights, *bs))
+    fused = (not grads and V <= 128 and K <= 128 and K % 4 == 0 and 1 <= W <= 8
+             and x_q.dtype in (torch.float32, torch.bfloat16)
+             and x_q.dtype == x_k.dtype == x_v.dtype
+             and (g is None or g.dtype == x_q.dtype) and decode_sized(T, cu_seqlens))
+    if scale is None:
+        scale = K ** -0.5
+    if not fused:
+        outs, new = [], []
+        for x, w, b, c, D in zip((x_q, x_k, x_v), conv_weights, bs, cs, dims):
+            x3 = x.reshape(B, T, D)
+            if step:
+                y3, c2 = short_conv_step(x3, w, b, conv_activation, c, output_final_state,
+                                         cu_seqlens)
+            else:
+                y3, c2 = short_conv(x3, w, b, conv_activation, cu_seqlens, output_final_state)
+            outs.append(y3.reshape(x.shape))
+            new.append(c2)
+        y, ht = fused_recurrent_gla_norm_gate(*outs, gk, None, g, weight, eps, scale=scale,
+                                              initial_state=initial_state,
+                                              output_final_state=output_final_state,
+                                              cu_seqlens=cu_seqlens)
+        return y, ht, (tuple(new) if any(c is not None for c in new) else None)
+    xs = [x.contiguous() for x in (x_q, x_k, x_v)]
+    dev = x_q.device
+    w32 = [w.to(torch.float32).contiguous() for w in ws]
+    b32 = [None if b is None else b.to(torch.float32).contiguous() for b in bs]
+    # a decode step reads and rolls the caches; a prefill reads none and keeps the last W inputs
+    keep = output_final_state or (step and cs[0] is not None)
+    cin = [None if (c is None or not step) else c.to(torch.float32).contiguous() for c in cs]
+    cout = [torch.empty(n, D, W, device=dev, dtype=torch.float32) if keep else None for D in dims]
+    y = torch.empty(B, T, H, V, device=dev, dtype=ydt)
+    ht = torch.empty(n, H, K, V, device=dev, dtype=torch.float32) if output_final_state else None
+    N.call("tops_gla_decode_conv_norm_gate", *(N.ptr(x) for x in xs), *(N.ptr(w) for w in w32),
+           *(N.ptr(b) for b in b32), *(N.ptr(c) for c in cin), *(N.ptr(c) for c in cout), W,
+           _act(conv_activation), N.ptr(_f32(gk)), N.ptr(_f32(initial_state)),
+           N.ptr(None if g is None else g.contiguous()), N.ptr(_f32(weight)), float(eps), N.ptr(y),
+           int(ydt == torch.float32 and x_q.dtype != torch.float32), N.ptr(ht),
+           N.ptr(_cu_dev(cu_seqlens, dev)), B, T, H, K, V, n, N.dtype_code(x_q.dtype),
+           float(scale), N.stream())
+    new = None
+    if keep:
+        # cache dtypes as the module gives them: a step keeps the cache's, a prefill x's
+        new = tuple(co.to(c.dtype if (step and c is not None) else (torch.float32 if step else x.dtype))
+                    for co, c, x in zip(cout, cs, (x_q, x_k, x_v)))
+    return y, ht, new
+
+
 def fused_recurrent_gla_fwd(q, k, v, gk=None, gv=None, scale=None, initial_state=None,
                             output_final_state=False, reverse=False, cu_seqlens=None):
     """tops/ops/gla/fused_recurrent.py:380-431.  Returns (o, ht), o in q.dtype."""

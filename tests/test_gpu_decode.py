@@ -17,7 +17,7 @@ import pytest
 import torch
 
 from oracle import gla as O
-from _inputs import gla_inputs
+from _inputs import gla_inputs, bf16_round
 from _gpu import to_dev, seen, host, rel, tol, out_bound
 
 pytestmark = pytest.mark.gpu
@@ -370,3 +370,85 @@ def test_decode_norm_gate_unfused_routes(cuda_device, calls):
         if grad:
             rdg = M.rmsnorm_gated_bwd(ro, og, w, dy, 1e-5)[1]
             assert rel(host(ogt.grad), rdg) < 1e-4
+
+
+CONV_CASES = [
+    dict(B=8, T=1, H=4, K=128, V=128, W=4, bias=True, act="silu", cache=True, og=True, w=True),
+    dict(B=1, T=5, H=2, K=64, V=96, W=3, bias=False, act=None, cache=True, og=True, w=False,
+         cu=[0, 1, 2, 3, 4, 5]),
+    dict(B=2, T=3, H=2, K=32, V=64, W=4, bias=True, act="silu", cache=True, og=False, w=True),
+    dict(B=1, T=5, H=2, K=64, V=64, W=4, bias=True, act="silu", cache=False, og=True, w=True,
+         cu=[0, 2, 2, 5]),
+    dict(B=4, T=1, H=2, K=36, V=20, W=2, bias=True, act="swish", cache=False, og=True, w=True),
+    dict(B=2, T=1, H=3, K=128, V=128, W=8, bias=False, act="silu", cache=True, og=True, w=True,
+         wdt="bf16"),
+]
+
+
+def _cid(c):
+    return "-".join(f"{k}{v}" for k, v in c.items() if k != "cu") + ("-varlen" if "cu" in c else "")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("cfg", CONV_CASES, ids=[_cid(c) for c in CONV_CASES])
+def test_decode_conv_norm_gate(cfg, dtype, cuda_device, calls):
+    """The GLA layer's decode route from the projections to the normalised output as one kernel
+    (ShortConvolution q / k / v -> fused_recurrent_gla -> FusedRMSNormGated), against the
+    oracle's conv step (one token per sequence: the caches roll) or prefill (the caches are not
+    read; the new ones are the last W inputs, zero-padded), per-token recurrence and norm:
+    y, the final state and the three new conv caches; W 2-8, SiLU or none, bias on / off,
+    varlen with an empty sequence, no cache, and bf16 conv weights (then y in bf16)."""
+    from oracle import modules as M
+    from tops.ops.gla import fused_recurrent_gla_conv_norm_gate
+    B, T, H, K, V, W = (cfg[x] for x in "BTHKVW")
+    cu = cfg.get("cu")
+    n = len(cu) - 1 if cu else B
+    step = B * T == n
+    print(f"decode conv case {_cid(cfg)} {dtype}", flush=True)
+    rng = np.random.Generator(np.random.PCG64(B * T + K + V + W))
+    d = gla_inputs(B, T, H, K, V, seed=T + K + W, gate_div=4.0, h0=True, N=n)
+    xs = [rng.standard_normal((B, T, H, D)).astype(np.float32) for D in (K, K, V)]
+    dims = (H * K, H * K, H * V)
+    ws = [(rng.standard_normal((D, W)) / np.sqrt(W)).astype(np.float32) for D in dims]
+    wdt = torch.bfloat16 if cfg.get("wdt") == "bf16" else torch.float32
+    if wdt == torch.bfloat16:
+        ws = [bf16_round(w) for w in ws]
+    bs = [rng.standard_normal(D).astype(np.float32) * 0.1 for D in dims] if cfg["bias"] else [None] * 3
+    cs = [rng.standard_normal((n, D, W)).astype(np.float32) for D in dims] if cfg["cache"] else [None] * 3
+    og = (rng.standard_normal((B, T, H, V)) * 2).astype(np.float32) if cfg["og"] else None
+    nw = (1 + 0.3 * rng.standard_normal(V)).astype(np.float32) if cfg["w"] else None
+    f = lambda x: to_dev(x, torch.float32, cuda_device)  # noqa: E731
+    with torch.no_grad():
+        y, ht, new = fused_recurrent_gla_conv_norm_gate(
+            *(to_dev(x, dtype, cuda_device) for x in xs),
+            tuple(to_dev(w, wdt, cuda_device) for w in ws),
+            None if not cfg["bias"] else tuple(f(b) for b in bs),
+            None if not cfg["cache"] else tuple(f(c) for c in cs),
+            cfg["act"], f(d["g"]), to_dev(og, dtype, cuda_device), f(nw), 1e-5,
+            initial_state=f(d["h0"]), output_final_state=True, cu_seqlens=cu)
+    torch.cuda.synchronize()
+    assert "tops_gla_decode_conv_norm_gate" in calls
+    ydt = torch.promote_types(dtype, wdt)
+    assert y.dtype == ydt
+    # oracle: the three convolutions, the recurrence, the norm
+    sx = [seen(x, dtype) for x in xs]
+    conv_out, conv_new = [], []
+    for x, w, b, c, D in zip(sx, ws, bs, cs, dims):
+        x3 = x.reshape(B, T, D)
+        if step:
+            xin = x3[0] if cu else x3[:, 0]
+            yv, cn = M.short_conv_step(xin, c if c is not None else np.zeros((n, D, W)), w, b, cfg["act"])
+            yv = yv.reshape(B, T, D)
+        else:
+            yv = M.short_conv(x3, w, b, cfg["act"], cu)
+            cn = M.short_conv_final_state(x3, W, cu)
+        conv_out.append(yv.reshape(x.shape))
+        conv_new.append(cn)
+    ro, rht = O.fused_recurrent_fwd(*conv_out, d["g"], None, scale=K ** -0.5,
+                                    initial_state=d["h0"], output_final_state=True, cu_seqlens=cu)
+    ry = M.rmsnorm_gated(ro, seen(og, dtype), nw, 1e-5)
+    ey, eh = rel(host(y), ry), rel(host(ht), rht)
+    ec = [rel(host(a), b) for a, b in zip(new, conv_new)]
+    print(f"y {ey:.2e} ht {eh:.2e} caches {[f'{e:.1e}' for e in ec]}")
+    lim = out_bound(ry, ydt, ydt)
+    assert ey < lim and eh < 1e-4 and max(ec) < 1e-6
