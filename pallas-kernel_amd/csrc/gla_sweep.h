@@ -52,6 +52,13 @@ struct SweepParams {
 template <typename TIn, bool REV, bool DELTA = false>
 hipError_t launch_gla_sweep(const SweepParams& p, hipStream_t s);
 
+// The software-pipelined sweep (gla_sweep_pipe.hip) for bf16 calls with per-channel gates:
+// same results as gla_sweep_kernel, the staging of chunk c + 1 overlapped with chunk c's
+// matrix products.  launch_gla_sweep routes eligible calls to it.
+bool gla_pipe_eligible(const SweepParams& p);
+template <bool REV>
+hipError_t launch_gla_pipe(const SweepParams& p, hipStream_t s);
+
 // Forward sweep with the gate on the value side (g = gv [B,T,H,V], bf16 inputs): see
 // gla_sweep.hip.
 hipError_t launch_gla_sweep_gv(const SweepParams& p, hipStream_t s);

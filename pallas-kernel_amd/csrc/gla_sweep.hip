@@ -1000,6 +1000,9 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 
 template <typename TIn, bool REV, bool DELTA>
 hipError_t launch_gla_sweep(const SweepParams& p, hipStream_t s) {
+  if constexpr (std::is_same<TIn, uint16_t>::value && !DELTA) {
+    if (gla_pipe_eligible(p)) return launch_gla_pipe<REV>(p, s);
+  }
   const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
   dim3 grid(p.NV * p.H * p.N);
   const bool gk = DELTA || p.gate_mode == kGateK;

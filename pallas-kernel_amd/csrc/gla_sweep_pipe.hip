@@ -1,0 +1,525 @@
+// Software-pipelined GLA chunk sweep for bf16 inputs with per-channel gates (the chunk_gla
+// hot path: the forward of tops/ops/gla/chunk.py:1103-1199 and the state-gradient sweep of its
+// backward, chunk.py:1447-1509 with tops/ops/common/chunk_h.py:685-878).
+//
+// Same products, operand planes, thread mappings and summation order as gla_sweep_kernel
+// (gla_sweep.hip, instance TIn = bf16, DELTA = ST = false, GK = true, YG = 0); only the
+// schedule differs (the compiler may contract the fp32 state update differently, a last-bit
+// difference).  The serial kernel runs each chunk as
+//   gate cumsum | B1 | VALU staging (exponentials, bf16 hi / lo splits) + plane writes | B2 |
+//   D tiles + state update (MFMA) | B3 | output products (MFMA)
+// and the VALU staging (~600 VALU instructions per wave, 4 cycles each on a 16-lane SIMD)
+// cannot overlap the LDS-bound MFMA phases behind the barriers.  Here the staging of chunk
+// c + 1 is computed into registers while chunk c's MFMA phase runs, so each chunk is
+//   B1 | plane writes from registers, partial gate cumsum of c + 1 | B2 |
+//   D tiles + state update of c, staging of c + 1 (VALU) | B3 | output products of c
+// The gate totals of chunk c + 1 are exchanged across the B2 barrier of chunk c (sTot is read
+// only between B2 and B3 and written only between B1 and B2, so one buffer serves).
+#include <stdlib.h>
+
+#include "gla_sweep.h"
+#include "tops_common.h"
+#include "tops_hip.h"
+
+namespace tops {
+
+// make_rsrc_rows for a pointer known to be non-null (no branch in the chunk loop)
+template <typename T>
+__device__ __forceinline__ rsrc_t rows_rsrc(const T* t, size_t e0, long long nrows, int width) {
+  return make_rsrc(t + e0 * (size_t)width, (nrows - (long long)e0) * width * (long long)sizeof(T));
+}
+
+// Keeps the computation of x at this point of the program: the compiler may otherwise sink
+// the staging arithmetic past the barriers to its first use (the plane writes of the next
+// chunk), where nothing overlaps it.
+__device__ __forceinline__ void pin(uint32_t& x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
+
+template <int KP, bool REV>
+__global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
+  constexpr int NW = 8;
+  constexpr int NTH = 64 * NW;
+  constexpr int C = kChunk, BV = 64;
+  constexpr int NQ = KP / 4;             // column quads of a [C][KP] tile
+  constexpr int NSEG = NTH / NQ;         // row segments
+  constexpr int RPT = C / NSEG;          // rows per thread (4, 2, 1)
+  constexpr int CQL = 8, SGL = 32 / CQL; // a half-wave: 8 column quads x 4 row segments
+  constexpr int NCQH = NQ / CQL;
+  constexpr int NSGH = NSEG / SGL;       // segment groups
+  static_assert(NQ % CQL == 0, "KP must be a multiple of 32");
+  static_assert(RPT == 1 || RPT == 2 || RPT == 4, "KP must be 32, 64 or 128");
+  constexpr int LQ = KP + 8, LT = C + 8, LH = KP + 8;
+  constexpr int NHT = (KP / 16) * (BV / 16) / NW;  // state tiles per wave
+  constexpr int YR = C * BV / (2 * NTH);
+  static_assert(YR == 4, "Y staging assumes 4 rows x 2 columns per thread");
+  constexpr int ES = 2;
+
+  __shared__ __attribute__((aligned(16))) uint16_t sX[2 * C * LQ];
+  __shared__ __attribute__((aligned(16))) uint16_t sZ[2 * C * LQ];
+  __shared__ __attribute__((aligned(16))) uint16_t sZT[2 * KP * LT];
+  __shared__ __attribute__((aligned(16))) uint16_t sYT[BV * LT];
+  __shared__ __attribute__((aligned(16))) uint16_t sHT[2 * BV * LH];
+  __shared__ __attribute__((aligned(16))) float sTot[NSGH * KP];
+  __shared__ __attribute__((aligned(16))) uint4 sDt[10 * 64];
+
+  const Plane PX{sX, sX + C * LQ, LQ};
+  const Plane PZ{sZ, sZ + C * LQ, LQ};
+  const Plane PZt{sZT, sZT + KP * LT, LT};
+  const Plane PYt{sYT, sYT, LT};
+  const Plane PHt{sHT, sHT + BV * LH, LH};
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int R = wave >> 1;
+  const int nh = wave & 1;
+  const int msb = (wave * NHT) / (BV / 16);
+  const int wg = xcd_remap(blockIdx.x, gridDim.x, p.NV);
+  const int vt = wg % p.NV;
+  const int hh = (wg / p.NV) % p.H;
+  int n = wg / (p.NV * p.H);
+  auto seq_end = [&](int j) { return p.seg_end ? p.seg_end[j] : p.cu_seqlens[j + 1]; };
+  if (p.cu_seqlens && p.N > 1 && p.N <= 256) {
+    // varlen: longest sequence first (LPT) over the slots, ties by index
+    const int slot = n;
+    if (tid < p.N) {
+      const int li = seq_end(tid) - p.cu_seqlens[tid];
+      int rank = 0;
+      for (int j = 0; j < p.N; ++j) {
+        const int lj = seq_end(j) - p.cu_seqlens[j];
+        rank += (lj > li) || (lj == li && j < tid);
+      }
+      if (rank == slot) *(int*)sTot = tid;
+    }
+    __syncthreads();
+    n = *(const int*)sTot;
+    __syncthreads();
+  }
+  n = __builtin_amdgcn_readfirstlane(n);
+  const int H = p.H, K = p.K, V = p.V;
+  const float scale = p.scale;
+
+  int L, row0, cbase;
+  if (p.cu_seqlens) {
+    row0 = p.cu_seqlens[n];
+    L = seq_end(n) - row0;
+    cbase = p.chunk_offsets ? p.chunk_offsets[n] : 0;
+  } else {
+    row0 = n * p.T;
+    L = p.T;
+    cbase = n * cdiv(p.T, C);
+  }
+  const int NTs = cdiv(L, C);
+  const long long nrows = (long long)p.B * p.T * p.H;
+
+  // ---- staging coordinates (as gla_sweep_kernel)
+  const int hw = tid >> 5;
+  const int sgl = (lane & 31) / CQL;
+  const int sgh = hw / NCQH;
+  const int cq = (lane & 31) % CQL + CQL * (hw % NCQH), seg = sgl + SGL * sgh;
+  const int c0 = 4 * cq, r0 = seg * RPT;
+  const bool colok = c0 < K;
+  const int yc = (lane & 7) + 8 * (hw & 3), yseg = ((lane >> 3) & 3) + 4 * (hw >> 2);
+  const int yv = vt * BV + 2 * yc;
+  const bool ycolok = yv < V;
+  const uint32_t rowK = (uint32_t)(H * K), rowV = (uint32_t)(H * V);
+  const uint32_t offQ = colok ? ((uint32_t)r0 * rowK + c0) * ES : kOOB;
+  const uint32_t offG = colok ? ((uint32_t)r0 * rowK + c0) * 4u : kOOB;
+  const uint32_t offY = ycolok ? ((uint32_t)(yseg * YR) * rowV + yv) * ES : kOOB;
+
+  // ---- state tiles: tile i of this wave -> (msb, nn)
+  f32x4 S[NHT];
+#pragma unroll
+  for (int i = 0; i < NHT; ++i) {
+    const int nn = (wave * NHT + i) % (BV / 16);
+    const int vv = vt * BV + 16 * nn + l16;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int kr = 16 * msb + 4 * lg + r;
+      float x = 0.f;
+      if (p.s0 && kr < K && vv < V) x = p.s0[((size_t)(n * H + hh) * K + kr) * V + vv];
+      S[i][r] = x;
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+
+  // ---- raw chunk registers: loaded one chunk ahead of their staging
+  struct Raw {
+    uint2 rq[RPT], rk[RPT];
+    uint4 rg[RPT];
+    uint32_t ry[YR];
+  };
+  Raw rs;
+  // (a chunk index outside the sequence loads zeros: every row is masked)
+  auto load_chunk = [&](int c) {
+    const bool in = c >= 0 && c < NTs;
+    if (!in) c = 0;
+    const int t0 = c * C;
+    const int nval = in ? min(C, L - t0) : 0;
+    const size_t e0 = (size_t)(row0 + t0) * H + hh;
+    const rsrc_t Rq = rows_rsrc((const uint16_t*)p.q, e0, nrows, K);
+    const rsrc_t Rk = rows_rsrc((const uint16_t*)p.k, e0, nrows, K);
+    const rsrc_t Rg = rows_rsrc(p.g, e0, nrows, K);
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const bool ok = r0 + i < nval;
+      rs.rq[i] = bld64(Rq, ok ? offQ : kOOB, i * rowK * ES);
+      rs.rk[i] = bld64(Rk, ok ? offQ : kOOB, i * rowK * ES);
+      rs.rg[i] = bld128(Rg, ok ? offG : kOOB, i * rowK * 4);
+    }
+    const rsrc_t Ry = rows_rsrc((const uint16_t*)p.y, e0, nrows, V);
+#pragma unroll
+    for (int i = 0; i < YR; ++i) {
+      const bool ok = yseg * YR + i < nval;
+      rs.ry[i] = bld32(Ry, ok ? offY : kOOB, i * rowV * ES);
+    }
+  };
+  auto cidx = [&](int it) { return REV ? NTs - 1 - it : it; };
+
+  // ---- the staged chunk: plane words and state factors, computed one chunk ahead
+  uint32_t xh[RPT][2], xl[RPT][2], zh[RPT][2], zl[RPT][2], yw[YR];
+  float sga[4], sal[4], sbe[4];
+  // partial gate cumsum of the raw chunk (thread rows, then the half-wave scan); the group
+  // totals go to sTot
+  float G[RPT][4], pre[4];
+  auto cumsum = [&]() {
+    float gam[4];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      float x[4];
+      unpack4(rs.rg[i], x);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) G[i][j] = x[j] * kLog2e + (i > 0 ? G[i - 1][j] : 0.f);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float t = G[RPT - 1][j];
+      float x = t;
+#pragma unroll
+      for (int d = CQL; d < 32; d <<= 1) {
+        const float y = __shfl_up(x, d, 64);
+        if ((lane & 31) >= d) x += y;
+      }
+      pre[j] = x - t;
+      gam[j] = x;
+    }
+    if (sgl == SGL - 1) *(float4*)(sTot + sgh * KP + c0) = make_float4(gam[0], gam[1], gam[2], gam[3]);
+  };
+  // staging of the raw chunk after its totals are visible, in two parts so that each can be
+  // scheduled beside one group of matrix products: stage_sums() completes the gate prefix
+  // and the state factors, stage_rows(i0, i1) the X / Z plane words (bf16 hi / lo) of rows
+  // i0 .. i1 - 1 of the thread
+  float gm[4];
+  auto stage_sums = [&]() {
+    float gam[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) gam[j] = 0.f;
+#pragma unroll
+    for (int s2 = 0; s2 < NSGH; ++s2) {
+      const float4 t = *(const float4*)(sTot + s2 * KP + c0);
+      if (s2 < sgh) { pre[0] += t.x; pre[1] += t.y; pre[2] += t.z; pre[3] += t.w; }
+      gam[0] += t.x; gam[1] += t.y; gam[2] += t.z; gam[3] += t.w;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) gm[j] = 0.5f * gam[j];
+    float sgam[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s2 = 0; s2 < NSGH; ++s2) {
+      const float4 t = *(const float4*)(sTot + s2 * KP + 16 * msb + 4 * lg);
+      sgam[0] += t.x; sgam[1] += t.y; sgam[2] += t.z; sgam[3] += t.w;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float g2 = 0.5f * sgam[r];
+      sga[r] = fast_exp2(sgam[r]);
+      sal[r] = REV ? fast_exp2(sgam[r] - g2) : scale * fast_exp2(g2);
+      sbe[r] = REV ? scale * fast_exp2(g2) : fast_exp2(sgam[r] - g2);
+      pin(sga[r]); pin(sal[r]); pin(sbe[r]);
+    }
+  };
+  auto stage_rows = [&](int i0, int i1) {
+#pragma unroll
+    for (int i = i0; i < i1; ++i) {
+      float qv[4], kv[4], xq[4], xk[4];
+      unpack4(rs.rq[i], qv);
+      unpack4(rs.rk[i], kv);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float Gv = G[i][j] + pre[j];
+        xq[j] = 1.f * qv[j] * fast_exp2(Gv - gm[j]);
+        xk[j] = kv[j] * fast_exp2(gm[j] - Gv);
+      }
+      const float* xx = REV ? xk : xq;
+      const float* zz = REV ? xq : xk;
+      split_bf16x2(xx[0], xx[1], xh[i][0], xl[i][0]);
+      split_bf16x2(xx[2], xx[3], xh[i][1], xl[i][1]);
+      split_bf16x2(zz[0], zz[1], zh[i][0], zl[i][0]);
+      split_bf16x2(zz[2], zz[3], zh[i][1], zl[i][1]);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        pin(xh[i][e]); pin(xl[i][e]); pin(zh[i][e]); pin(zl[i][e]);
+      }
+    }
+  };
+  auto stage = [&]() {
+    stage_sums();
+    stage_rows(0, RPT);
+#pragma unroll
+    for (int i = 0; i < YR; ++i) yw[i] = rs.ry[i];
+  };
+  // plane writes of the staged chunk (after B1: no wave reads the previous chunk's planes)
+  auto write_planes = [&]() {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      *(uint2*)(PX.hi + (r0 + i) * PX.ld + c0) = make_uint2(xh[i][0], xh[i][1]);
+      *(uint2*)(PX.lo + (r0 + i) * PX.ld + c0) = make_uint2(xl[i][0], xl[i][1]);
+      *(uint2*)(PZ.hi + (r0 + i) * PZ.ld + c0) = make_uint2(zh[i][0], zh[i][1]);
+      *(uint2*)(PZ.lo + (r0 + i) * PZ.ld + c0) = make_uint2(zl[i][0], zl[i][1]);
+    }
+    if constexpr (RPT >= 2) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+        uint32_t th[RPT / 2], tl[RPT / 2];
+#pragma unroll
+        for (int m = 0; m < RPT / 2; ++m) {
+          th[m] = __builtin_amdgcn_perm(zh[2 * m + 1][j >> 1], zh[2 * m][j >> 1], sel);
+          tl[m] = __builtin_amdgcn_perm(zl[2 * m + 1][j >> 1], zl[2 * m][j >> 1], sel);
+        }
+        uint16_t* ph = PZt.hi + (c0 + j) * PZt.ld + r0;
+        uint16_t* pl = PZt.lo + (c0 + j) * PZt.ld + r0;
+        if constexpr (RPT == 4) {
+          *(uint2*)ph = make_uint2(th[0], th[1]);
+          *(uint2*)pl = make_uint2(tl[0], tl[1]);
+        } else {
+          *(uint32_t*)ph = th[0];
+          *(uint32_t*)pl = tl[0];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t w = zh[0][j >> 1], wl = zl[0][j >> 1];
+        PZt.hi[(c0 + j) * PZt.ld + r0] = (uint16_t)((j & 1) ? (w >> 16) : (w & 0xffffu));
+        PZt.lo[(c0 + j) * PZt.ld + r0] = (uint16_t)((j & 1) ? (wl >> 16) : (wl & 0xffffu));
+      }
+    }
+    // Y^T: column 2 yc (low halves) and 2 yc + 1 (high halves) of rows yseg * 4 + 0..3
+    *(uint2*)(PYt.hi + (2 * yc) * PYt.ld + yseg * YR) =
+        make_uint2(__builtin_amdgcn_perm(yw[1], yw[0], 0x05040100u),
+                   __builtin_amdgcn_perm(yw[3], yw[2], 0x05040100u));
+    *(uint2*)(PYt.hi + (2 * yc + 1) * PYt.ld + yseg * YR) =
+        make_uint2(__builtin_amdgcn_perm(yw[1], yw[0], 0x07060302u),
+                   __builtin_amdgcn_perm(yw[3], yw[2], 0x07060302u));
+  };
+
+  // checkpoint: S as the state entering chunk c (stored at the start of the chunk's matrix
+  // phase, which measured fastest of the placements tried: there, at the end of that phase,
+  // and after the output products)
+  auto store_ckpt = [&](int c) {
+    if (p.ckpt && (p.ckpt_par == 0 || ((cbase + c) & 1) == p.ckpt_par - 1)) {
+      const rsrc_t Rck = make_rsrc(p.ckpt + ((size_t)(cbase + c) * H + hh) * K * V,
+                                   (long long)K * V * 4);
+#pragma unroll
+      for (int i = 0; i < NHT; ++i) {
+        const int nn = (wave * NHT + i) % (BV / 16);
+        const int kr = 16 * msb + 4 * lg;
+        const int vv = vt * BV + 16 * nn + l16;
+        const uint32_t vo = (vv < V) ? ((uint32_t)kr * V + vv) * 4u : kOOB;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          bst32(Rck, __float_as_uint(S[i][r]), (kr + r < K) ? vo : kOOB, (uint32_t)(r * V * 4));
+      }
+    }
+  };
+
+  // ---- prologue: chunk 0 staged, chunk 1 loaded
+  if (NTs > 0) {
+    load_chunk(cidx(0));
+    cumsum();
+    __syncthreads();
+    stage();
+    if (NTs > 1) load_chunk(cidx(1));
+  }
+
+  for (int it = 0; it < NTs; ++it) {
+    const int c = cidx(it);
+    const int t0 = c * C;
+    const int nval = min(C, L - t0);
+
+    __syncthreads();  // B1: the previous chunk's planes and the totals are no longer read
+    write_planes();
+    // the state factors of this chunk, kept for its update (stage() overwrites them)
+    float cga[4], cbe[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) { cga[r] = sga[r]; cbe[r] = sbe[r]; }
+    cumsum();         // (past the last chunk: zeros, never staged into planes)
+    __syncthreads();  // B2: planes and the next chunk's totals visible
+
+    // H^T plane = alpha S (the state entering this chunk; read after B3 only)
+#pragma unroll
+    for (int i = 0; i < NHT; ++i) {
+      const int nn = (wave * NHT + i) % (BV / 16);
+      const int kr = 16 * msb + 4 * lg;
+      float x[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[r] = sal[r] * S[i][r];
+      put_n<true, 4>(PHt, 16 * nn + l16, kr, x);
+    }
+    store_ckpt(c);
+
+    // ---------------- D tiles of this chunk (shared through LDS), staging of the next
+    auto dtile = [&](int t) -> uint4 {
+      const int Rc = t >= 6 ? 3 : (t >= 3 ? 2 : (t >= 1 ? 1 : 0));
+      const int Pc = t - Rc * (Rc + 1) / 2;
+      const int Rt = REV ? 3 - Rc : Rc, Pt = REV ? 3 - Pc : Pc;
+      f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0, a2 = a0;
+#pragma unroll
+      for (int kc = 0; kc < KP / 32; ++kc) {
+        const bf16x8 zh8 = PZ.hi8(16 * Pt + l16, 32 * kc + 8 * lg);
+        const bf16x8 xh8 = PX.hi8(16 * Rt + l16, 32 * kc + 8 * lg);
+        const bf16x8 zl8 = PZ.lo8(16 * Pt + l16, 32 * kc + 8 * lg);
+        const bf16x8 xl8 = PX.lo8(16 * Rt + l16, 32 * kc + 8 * lg);
+        a0 = mfma(zl8, xh8, a0);
+        a1 = mfma(zh8, xl8, a1);
+        a2 = mfma(zh8, xh8, a2);
+      }
+      f32x4 acc;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = (a0[r] + a1[r]) + a2[r];
+      const int rr = 16 * Rt + l16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int pp = 16 * Pt + 4 * lg + r;
+        const bool keep = REV ? (pp >= rr) : (pp <= rr);
+        acc[r] = keep ? acc[r] * scale : 0.f;
+      }
+      uint2 th, tl;
+      acc_to_bf16x4(acc, th, tl);
+      return make_uint4(th.x, th.y, tl.x, tl.y);
+    };
+    // (the staging of the next chunk is issued between the matrix products; past the last
+    // chunk it stages zeros that are never written)
+    stage_sums();
+    sDt[wave * 64 + lane] = dtile(wave);
+    stage_rows(0, RPT / 2 > 0 ? RPT / 2 : RPT);
+    if (wave < 2) sDt[(wave + 8) * 64 + lane] = dtile(wave + 8);
+
+    // state update: S = 2^Gamma S + beta (Z~^T Y)
+    {
+      f32x4 dsu[NHT];
+#pragma unroll
+      for (int i = 0; i < NHT; ++i) dsu[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kc = 0; kc < C / 32; ++kc) {
+        const bf16x8 fzh = PZt.hi8(16 * msb + l16, 32 * kc + 8 * lg);
+        const bf16x8 fzl = PZt.lo8(16 * msb + l16, 32 * kc + 8 * lg);
+        bf16x8 fyh[NHT];
+#pragma unroll
+        for (int i = 0; i < NHT; ++i) {
+          const int nn = (wave * NHT + i) % (BV / 16);
+          fyh[i] = PYt.hi8(16 * nn + l16, 32 * kc + 8 * lg);
+        }
+#pragma unroll
+        for (int i = 0; i < NHT; ++i) dsu[i] = mfma(fzl, fyh[i], dsu[i]);
+#pragma unroll
+        for (int i = 0; i < NHT; ++i) dsu[i] = mfma(fzh, fyh[i], dsu[i]);
+      }
+      if constexpr (RPT > 1) stage_rows(RPT / 2, RPT);
+#pragma unroll
+      for (int i = 0; i < YR; ++i) yw[i] = rs.ry[i];
+      load_chunk(cidx(it + 2));
+#pragma unroll
+      for (int i = 0; i < NHT; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float x = cga[r] * S[i][r] + cbe[r] * dsu[i][r];
+          pin(x);
+          S[i][r] = x;
+        }
+    }
+    __syncthreads();  // B3: D tiles visible
+
+    // ---------------- output block: token block R, column tiles 2 nh, 2 nh + 1
+    bf16x8 fxh[KP / 32], fxl[KP / 32];
+#pragma unroll
+    for (int kc = 0; kc < KP / 32; ++kc) {
+      fxh[kc] = PX.hi8(16 * R + l16, 32 * kc + 8 * lg);
+      fxl[kc] = PX.lo8(16 * R + l16, 32 * kc + 8 * lg);
+    }
+    uint2 dh[4], dl[4];
+#pragma unroll
+    for (int P = 0; P < 4; ++P) {
+      dh[P] = make_uint2(0u, 0u);
+      dl[P] = make_uint2(0u, 0u);
+      const bool live = REV ? (P >= R) : (P <= R);
+      if (live) {
+        const int Rc = REV ? 3 - R : R, Pc = REV ? 3 - P : P;
+        const uint4 x = sDt[(Rc * (Rc + 1) / 2 + Pc) * 64 + lane];
+        dh[P] = make_uint2(x.x, x.y);
+        dl[P] = make_uint2(x.z, x.w);
+      }
+    }
+    const int tok = 16 * R + l16;
+    const size_t eo = (size_t)(row0 + t0) * H + hh;
+    const rsrc_t Ro = rows_rsrc((const uint16_t*)p.out, eo, nrows, V);
+    const uint32_t oo = (tok < nval) ? ((uint32_t)tok * rowV + vt * BV + 4 * lg) * ES : kOOB;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int nn = 2 * nh + j;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kc = 0; kc < KP / 32; ++kc)
+        acc = mma<true, true>(acc, PHt.hi8(16 * nn + l16, 32 * kc + 8 * lg),
+                              PHt.lo8(16 * nn + l16, 32 * kc + 8 * lg), fxh[kc], fxl[kc]);
+#pragma unroll
+      for (int Pp = 0; Pp < 2; ++Pp) {
+        const int P0 = 2 * Pp, P1 = 2 * Pp + 1;
+        const bool live = REV ? (P1 >= R) : (P0 <= R);
+        if (live) {
+          const bf16x8 ah = PYt.hi44(16 * nn + l16, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg);
+          acc = mma<false, true>(acc, ah, ah, cat44(dh[P0], dh[P1]), cat44(dl[P0], dl[P1]));
+        }
+      }
+      const int v0 = vt * BV + 16 * nn + 4 * lg;
+      Words<uint16_t>::st4(Ro, acc, v0 < V ? oo : kOOB, (uint32_t)(16 * nn * ES));
+    }
+  }
+
+  if (p.s_fin) {
+#pragma unroll
+    for (int i = 0; i < NHT; ++i) {
+      const int nn = (wave * NHT + i) % (BV / 16);
+      const int vv = vt * BV + 16 * nn + l16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kr = 16 * msb + 4 * lg + r;
+        if (kr < K && vv < V) p.s_fin[((size_t)(n * H + hh) * K + kr) * V + vv] = S[i][r];
+      }
+    }
+  }
+}
+
+// Whether launch_gla_sweep routes a call to the pipelined kernel: bf16, per-channel gates,
+// not the delta rule, no gate shift.  TOPS_SWEEP_SERIAL=1 in the environment keeps every call
+// on gla_sweep_kernel (the reference schedule, for A/B timing and bitwise comparisons).
+bool gla_pipe_eligible(const SweepParams& p) {
+  if (p.gate_mode != kGateK || p.gshift) return false;
+  const char* e = getenv("TOPS_SWEEP_SERIAL");
+  return !(e && e[0] == '1');
+}
+
+template <bool REV>
+hipError_t launch_gla_pipe(const SweepParams& p, hipStream_t s) {
+  const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
+  dim3 grid(p.NV * p.H * p.N);
+  if (kp == 32) hipLaunchKernelGGL((gla_pipe_kernel<32, REV>), grid, dim3(512), 0, s, p);
+  else if (kp == 64) hipLaunchKernelGGL((gla_pipe_kernel<64, REV>), grid, dim3(512), 0, s, p);
+  else hipLaunchKernelGGL((gla_pipe_kernel<128, REV>), grid, dim3(512), 0, s, p);
+  return hipGetLastError();
+}
+
+template hipError_t launch_gla_pipe<false>(const SweepParams&, hipStream_t);
+template hipError_t launch_gla_pipe<true>(const SweepParams&, hipStream_t);
+
+}  // namespace tops
