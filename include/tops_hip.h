@@ -166,6 +166,45 @@ int tops_chunk_bwd_dqkg_paired(const void* q, const void* k, const void* v, cons
                                const int32_t* chunk_map, int total_chunks, int B, int T, int H,
                                int K, int V, int N, int dtype, float scale, void* stream);
 
+/* Heads wider than one kernel tile (K or V above 128): the reference pads K and V to
+ * multiples of 128 and tiles them inside one kernel (tops/ops/gla/chunk.py:1146-1152, the
+ * K / V block grid of K7 / K3 / K4).  Here the caller loops over channel slices (K) and, in
+ * the dq / dk / dg stage, value slices (V), each at most 128 wide and a multiple of 8, and
+ * calls these entry points once per slice on the same stream, with pointers at the slice's
+ * first column of the full tensors (no copies):
+ *   q, k, g (per-channel gate [B,T,H,ldk], or a constant [H,ldk]), dq, dk, dg (per-channel)
+ *     rows of ldk elements; v, dO rows of ldv (the forward and the dh stage take all of V:
+ *     their sweeps tile V themselves);
+ *   h0 / ht / dht / dh0 / h_ckpt / dh_work [.., ldk, ldv] with the slice's rows (and, for
+ *     the dq / dk / dg stage, columns) starting at the pointer.
+ * Results that sum over slices are accumulated in fp32: the forward's o and the dh stage's
+ * dv over channel slices (o_sum / dv_sum [B,T,H,V]), and dq, dk over value slices (dq_sum,
+ * dk_sum [B,T,H,ldk]): acc_mode 0 writes the output directly (one slice), 1 writes the sum
+ * buffer, 2 adds into it, 3 writes the output = sum + this slice (the last slice).  The
+ * output pointer may be NULL for modes 1 and 2.  dg_accum != 0 adds this call's dg into dg
+ * (a per-channel dg over value slices; a per-token dg [B,T,H] over every slice).  Slices
+ * add up exactly: the recurrence is separate per state entry, so o and dv are sums over
+ * channel slices, and dq, dk, dg sums over value slices.  gate_mode as
+ * tops_chunk_fwd_paired.  dtype TOPS_F32 or TOPS_BF16. */
+int tops_chunk_fwd_slice(const void* q, const void* k, const void* v, const float* g,
+                         int gate_mode, const float* h0, void* o, float* o_sum, int acc_mode,
+                         float* ht, float* h_ckpt, const int32_t* cu_seqlens,
+                         const int32_t* chunk_offsets, int B, int T, int H, int K, int V, int N,
+                         int ldk, int dtype, float scale, void* stream);
+int tops_chunk_bwd_dh_slice(const void* q, const void* k, const float* g, int gate_mode,
+                            const void* do_, const float* dht, float* dh_work, void* dv,
+                            float* dv_sum, int acc_mode, float* dh0, const int32_t* cu_seqlens,
+                            const int32_t* chunk_offsets, int B, int T, int H, int K, int V,
+                            int N, int ldk, int dtype, float scale, void* stream);
+int tops_chunk_bwd_dqkg_slice(const void* q, const void* k, const void* v, const float* g,
+                              int gate_mode, const void* do_, const float* h_ckpt,
+                              const float* dh_work, void* dq, void* dk, float* dg,
+                              float* dq_sum, float* dk_sum, int acc_mode, int dg_accum,
+                              const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                              const int32_t* chunk_map, int total_chunks, int B, int T, int H,
+                              int K, int V, int N, int ldk, int ldv, int dtype, float scale,
+                              void* stream);
+
 /* Reverse-time recurrence, chunked: fused_recurrent_gla_fwd with reverse = True
  * (tops/ops/gla/fused_recurrent.py:380-431; oracle tops/cpu/ops/gla/fused_recurrent.py:116-160,
  * one body iterated from the last token to the first), without gv:

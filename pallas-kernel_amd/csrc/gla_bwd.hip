@@ -17,17 +17,23 @@ namespace tops {
 // Shape checks shared by the backward entry points; returns TOPS_OK or an error code.
 static int check_bwd(const char* who, int B, int T, int H, int K, int V, int N, int total_chunks,
                      const int32_t* cu_seqlens, const int32_t* chunk_offsets,
-                     const int32_t* chunk_map, bool need_map, int dtype) {
+                     const int32_t* chunk_map, bool need_map, int dtype, int ldk = 0,
+                     int ldv = 0, bool wide_v = false) {
   char msg[160];
   if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || N <= 0) {
     snprintf(msg, sizeof(msg), "%s: non-positive dimension", who);
     return tops_set_error(TOPS_ERR_SHAPE, msg);
   }
-  if (K > 128 || V > 128 || (K % 8) || (V % 8)) {
+  if (K > 128 || (V > 128 && !wide_v) || (K % 8) || (V % 8)) {
     snprintf(msg, sizeof(msg), "%s: need K, V <= 128 and multiples of 8", who);
     return tops_set_error(TOPS_ERR_SHAPE, msg);
   }
-  if ((long long)kChunk * H * (K > V ? K : V) * 4 >= (1LL << 31)) {
+  const int kw = ldk > 0 ? ldk : K, vw = ldv > 0 ? ldv : V;
+  if ((ldk && (ldk < K || (ldk % 8))) || (ldv && (ldv < V || (ldv % 8)))) {
+    snprintf(msg, sizeof(msg), "%s: ldk / ldv must be multiples of 8, at least K / V", who);
+    return tops_set_error(TOPS_ERR_SHAPE, msg);
+  }
+  if ((long long)kChunk * H * (kw > vw ? kw : vw) * 4 >= (1LL << 31)) {
     snprintf(msg, sizeof(msg), "%s: H * max(K, V) too large for 32-bit chunk offsets", who);
     return tops_set_error(TOPS_ERR_SHAPE, msg);
   }
@@ -62,15 +68,21 @@ static int bwd_dh_impl(const void* q, const void* k, const float* g, const void*
                        const float* dht, float* dh_work, void* dv, float* dh0,
                        const int32_t* cu_seqlens, const int32_t* chunk_offsets, int B, int T, int H,
                        int K, int V, int N, int dtype, float scale, int gate_mode, void* stream,
-                       int ckpt_par = 0) {
+                       int ckpt_par = 0, int ldk = 0, float* dv_sum = nullptr, int acc_mode = 0) {
   if (!q || !k || !g || !do_ || !dh_work || !dv)
     return tops_set_error(TOPS_ERR_NULL, "gla_chunk_bwd_dh: null tensor");
+  // (the sweep tiles V by 64, so a channel slice takes the whole V)
   int rc = check_bwd("gla_chunk_bwd_dh", B, T, H, K, V, N, 0, cu_seqlens, chunk_offsets, nullptr,
-                     false, dtype);
+                     false, dtype, ldk, 0, ldk > 0);
   if (rc != TOPS_OK) return rc;
+  if (acc_mode < 0 || acc_mode > 3 || (acc_mode && !dv_sum))
+    return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_bwd_dh: acc_mode 1..3 needs the fp32 sum buffer");
   SweepParams p{q, k, g, do_, dht, dv, dh0, dh_work, cu_seqlens, chunk_offsets,
                 B, T, H, K, V, N, (V + 63) / 64, scale, gate_mode};
   p.ckpt_par = ckpt_par;
+  p.ldk = ldk;
+  p.acc32 = dv_sum;
+  p.acc_mode = acc_mode;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e = dtype == TOPS_BF16 ? launch_gla_sweep<uint16_t, true>(p, s)
                                     : launch_gla_sweep<float, true>(p, s);
@@ -84,18 +96,28 @@ static int bwd_dqkg_impl(const void* q, const void* k, const void* v, const floa
                          const int32_t* chunk_offsets, const int32_t* chunk_map, int total_chunks,
                          int B, int T, int H, int K, int V, int N, int dtype, float scale,
                          int gate_mode, void* stream, const float* h0 = nullptr,
-                         const float* dht = nullptr, int paired = 0) {
+                         const float* dht = nullptr, int paired = 0, int ldk = 0, int ldv = 0,
+                         float* dq_sum = nullptr, float* dk_sum = nullptr, int acc_mode = 0,
+                         int dg_accum = 0) {
   if (!q || !k || !v || !g || !do_ || !h_ckpt || !dh_work || !dq || !dk ||
       ((gate_mode == kGateK || gate_mode == kGateS) && !dg))
     return tops_set_error(TOPS_ERR_NULL, "gla_chunk_bwd_dqkg: null tensor");
   int rc = check_bwd("gla_chunk_bwd_dqkg", B, T, H, K, V, N, total_chunks, cu_seqlens,
-                     chunk_offsets, chunk_map, true, dtype);
+                     chunk_offsets, chunk_map, true, dtype, ldk, ldv);
   if (rc != TOPS_OK) return rc;
+  if (acc_mode < 0 || acc_mode > 3 || (acc_mode && (!dq_sum || !dk_sum)))
+    return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_bwd_dqkg: acc_mode 1..3 needs the fp32 sum buffers");
   DqkgParams p{q, k, v, g, do_, h_ckpt, dh_work, dq, dk, dg, cu_seqlens, chunk_offsets, chunk_map,
                total_chunks, B, T, H, K, V, N, scale, gate_mode};
   p.paired = paired;
   p.h0 = h0;
   p.dht = dht;
+  p.ldk = ldk;
+  p.ldv = ldv;
+  p.dq32 = dq_sum;
+  p.dk32 = dk_sum;
+  p.acc_mode = acc_mode;
+  p.dg_accum = dg_accum;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e = dtype == TOPS_BF16 ? launch_gla_dqkg<uint16_t>(p, s) : launch_gla_dqkg<float>(p, s);
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
@@ -205,6 +227,55 @@ extern "C" int tops_gla_chunk_bwd_dqkg_gamma(const void* q, const void* k, const
   return bwd_dqkg_impl(q, k, v, g_gamma, do_, h_ckpt, dh_work, dq, dk, dg, cu_seqlens,
                        chunk_offsets, chunk_map, total_chunks, B, T, H, K, V, N, dtype, scale,
                        kGateGammaK, stream);
+}
+
+// Channel / value slices of heads wider than one kernel tile (the caller loops over them).
+static int check_slice_gate(const char* who, int gate_mode) {
+  if (gate_mode < kGateK || gate_mode > kGateGammaK) {
+    char msg[160];
+    snprintf(msg, sizeof(msg), "%s: gate_mode must be 0..3", who);
+    return tops_set_error(TOPS_ERR_SHAPE, msg);
+  }
+  return TOPS_OK;
+}
+
+extern "C" int tops_chunk_bwd_dh_slice(const void* q, const void* k, const float* g,
+                                       int gate_mode, const void* do_, const float* dht,
+                                       float* dh_work, void* dv, float* dv_sum, int acc_mode,
+                                       float* dh0, const int32_t* cu_seqlens,
+                                       const int32_t* chunk_offsets, int B, int T, int H, int K,
+                                       int V, int N, int ldk, int dtype, float scale,
+                                       void* stream) {
+  int rc = check_slice_gate("chunk_bwd_dh_slice", gate_mode);
+  if (rc != TOPS_OK) return rc;
+  if (acc_mode != 1 && acc_mode != 2 && !dv)
+    return tops_set_error(TOPS_ERR_NULL, "chunk_bwd_dh_slice: null dv");
+  return bwd_dh_impl(q, k, g, do_, dht, dh_work, dv ? dv : (void*)dv_sum, dh0, cu_seqlens,
+                     chunk_offsets, B, T, H, K, V, N, dtype, scale, gate_mode, stream, 0,
+                     ldk > 0 ? ldk : K, dv_sum, acc_mode);
+}
+
+extern "C" int tops_chunk_bwd_dqkg_slice(const void* q, const void* k, const void* v,
+                                         const float* g, int gate_mode, const void* do_,
+                                         const float* h_ckpt, const float* dh_work, void* dq,
+                                         void* dk, float* dg, float* dq_sum, float* dk_sum,
+                                         int acc_mode, int dg_accum, const int32_t* cu_seqlens,
+                                         const int32_t* chunk_offsets, const int32_t* chunk_map,
+                                         int total_chunks, int B, int T, int H, int K, int V,
+                                         int N, int ldk, int ldv, int dtype, float scale,
+                                         void* stream) {
+  int rc = check_slice_gate("chunk_bwd_dqkg_slice", gate_mode);
+  if (rc != TOPS_OK) return rc;
+  if (gate_mode == kGateGamma) dg = nullptr;
+  // dq / dk are written only by acc_mode 0 and 3
+  if (acc_mode == 1 || acc_mode == 2) {
+    if (!dq) dq = dq_sum;
+    if (!dk) dk = dk_sum;
+  }
+  return bwd_dqkg_impl(q, k, v, g, do_, h_ckpt, dh_work, dq, dk, dg, cu_seqlens, chunk_offsets,
+                       chunk_map, total_chunks, B, T, H, K, V, N, dtype, scale, gate_mode, stream,
+                       nullptr, nullptr, 0, ldk > 0 ? ldk : K, ldv > 0 ? ldv : V, dq_sum, dk_sum,
+                       acc_mode, dg_accum);
 }
 
 // Interleaved checkpoints: one [total_chunks, H, K, V] buffer, h before the even global

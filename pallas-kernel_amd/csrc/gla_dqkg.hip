@@ -108,6 +108,8 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
   const int hh = blockIdx.x % p.H;
   const int gc = PAIR ? 2 * (blockIdx.x / p.H) + grp : blockIdx.x / p.H;
   const int H = p.H, K = p.K, V = p.V;
+  // row lengths of the channel- and value-indexed tensors (slices of wider heads)
+  const int LDK = p.ldk > 0 ? p.ldk : K, LDV = p.ldv > 0 ? p.ldv : V;
   const float scale = p.scale;
 
   // this chunk's LDS (the partner's, for PAIR, at index pg)
@@ -154,11 +156,11 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
   const int nval = present ? min(C, L - t0) : 0;
   const size_t e0 = (size_t)(row0 + t0) * H + hh;
   const long long nrows = (long long)p.B * p.T * H;     // (token, head) rows of [B,T,H,.]
-  const uint32_t rowK = (uint32_t)(H * K), rowV = (uint32_t)(H * V);
-  const rsrc_t Rq = make_rsrc_rows((const TIn*)p.q, e0, nrows, K);
-  const rsrc_t Rk = make_rsrc_rows((const TIn*)p.k, e0, nrows, K);
+  const uint32_t rowK = (uint32_t)(H * LDK), rowV = (uint32_t)(H * LDV);
+  const rsrc_t Rq = make_rsrc_rows((const TIn*)p.q, e0, nrows, LDK);
+  const rsrc_t Rk = make_rsrc_rows((const TIn*)p.k, e0, nrows, LDK);
   const int gmode = GK ? kGateK : p.gate_mode;
-  const rsrc_t Rg = make_rsrc_rows(p.g, e0, nrows, gmode == kGateK ? K : 1);
+  const rsrc_t Rg = make_rsrc_rows(p.g, e0, nrows, gmode == kGateK ? LDK : 1);
   const float gam_h = gmode == kGateGamma ? p.g[hh] : 0.f;
   // kGateGammaK: this thread's constant of every pass (channel ps * KH + ch), read up front
   // through a range that is empty in the other modes.  The load is issued on every path: a
@@ -166,7 +168,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
   // waits for the prefetched rows conservative in all of them.
   float gck[NPS];
   if constexpr (!GK) {
-    const rsrc_t Rgc = make_rsrc(gmode == kGateGammaK ? p.g + (size_t)hh * K : nullptr,
+    const rsrc_t Rgc = make_rsrc(gmode == kGateGammaK ? p.g + (size_t)hh * LDK : nullptr,
                                  gmode == kGateGammaK ? (long long)K * 4 : 0);
 #pragma unroll
     for (int ps = 0; ps < NPS; ++ps) {
@@ -177,8 +179,8 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
 
   // ---------------- v / dO planes ([C][V], V contiguous)
   {
-    const rsrc_t Rv = make_rsrc_rows((const TV*)p.v, e0, nrows, V);
-    const rsrc_t Rd = make_rsrc_rows((const TIn*)p.dout, e0, nrows, V);
+    const rsrc_t Rv = make_rsrc_rows((const TV*)p.v, e0, nrows, LDV);
+    const rsrc_t Rd = make_rsrc_rows((const TIn*)p.dout, e0, nrows, LDV);
     uint4 pv[NPTV], pd[NPT];
 #pragma unroll
     for (int i = 0; i < NPTV; ++i) {
@@ -329,15 +331,15 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
 
   // the state rows: h_c and dh_c, or for PAIR this chunk's checkpoint and the partner's
   // (linked) or the sequence's h0 / dht (not linked; NULL reads as zero)
-  const long long KVB = (long long)K * V * 4;
-  auto slot = [&](const float* b, int x) { return b + ((size_t)x * H + hh) * K * V; };
+  const long long KVB = (long long)K * LDV * 4;
+  auto slot = [&](const float* b, int x) { return b + ((size_t)x * H + hh) * LDK * LDV; };
   rsrc_t Rh, Rdh;
   if constexpr (PAIR) {
     const float* other = nullptr;
     if (linked) other = slot(p.hs, grp == 0 ? gc + 1 : gc - 1);
     else if (present) {
       const float* b = grp == 0 ? p.dht : p.h0;
-      other = b ? b + ((size_t)n * H + hh) * K * V : nullptr;
+      other = b ? b + ((size_t)n * H + hh) * LDK * LDV : nullptr;
     }
     const rsrc_t Ro = make_rsrc(present ? slot(p.hs, gc) : nullptr, present ? KVB : 0);
     const rsrc_t Rx = make_rsrc(other, other ? KVB : 0);
@@ -347,11 +349,14 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
     Rh = make_rsrc(slot(p.hs, gc), KVB);
     Rdh = make_rsrc(slot(p.dhs, gc), KVB);
   }
-  const rsrc_t Rdq = make_rsrc_rows((const TIn*)p.dq, e0, nrows, K);
-  const rsrc_t Rdk = make_rsrc_rows((const TIn*)p.dk, e0, nrows, K);
-  const rsrc_t Rdka = make_rsrc_rows(p.dk_add, e0, nrows, K);
-  const rsrc_t Rdga = make_rsrc_rows(p.dg_add, e0, nrows, K);
-  const rsrc_t Rdg = make_rsrc_rows(gmode == kGateGamma ? nullptr : p.dg, e0, nrows, gmode == kGateS ? 1 : K);
+  const rsrc_t Rdq = make_rsrc_rows((const TIn*)p.dq, e0, nrows, LDK);
+  const rsrc_t Rdk = make_rsrc_rows((const TIn*)p.dk, e0, nrows, LDK);
+  const rsrc_t Rdka = make_rsrc_rows(p.dk_add, e0, nrows, LDK);
+  const rsrc_t Rdga = make_rsrc_rows(p.dg_add, e0, nrows, LDK);
+  const rsrc_t Rdg = make_rsrc_rows(gmode == kGateGamma ? nullptr : p.dg, e0, nrows, gmode == kGateS ? 1 : LDK);
+  // value slices: fp32 sums of dq / dk over the slices (acc_mode 1..3)
+  const rsrc_t Rdq32 = make_rsrc_rows(p.dq32, e0, nrows, LDK);
+  const rsrc_t Rdk32 = make_rsrc_rows(p.dk32, e0, nrows, LDK);
   if (kScalarGate && tq < 2 * C) gDgS[tq] = 0.f;
 
   // ---- the h / dh rows of a pass: a lane's 8 values of state row kk = 32 ps + 16 kb + l16,
@@ -364,7 +369,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
     const int kk = ps * KH + kl;
     auto vrun = [&](int vc, int j) {
       const int v0 = PAIR ? 32 * vc + 16 * j + 4 * lg : 32 * vc + 8 * lg;
-      return (kk < K && v0 < V) ? ((uint32_t)kk * V + v0) * 4u : kOOB;
+      return (kk < K && v0 < V) ? ((uint32_t)kk * LDV + v0) * 4u : kOOB;
     };
 #pragma unroll
     for (int vc = 0; vc < VC; ++vc) {
@@ -667,8 +672,13 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
 #pragma unroll
         for (int r = 0; r < 4; ++r) dkv[r] += ka[r];
       }
-      Wd::st4(Rdq, dqv, ok ? off * ES : kOOB, 0);
-      Wd::st4(Rdk, dkv, ok ? off * ES : kOOB, 0);
+      if (p.acc_mode == 0) {
+        Wd::st4(Rdq, dqv, ok ? off * ES : kOOB, 0);
+        Wd::st4(Rdk, dkv, ok ? off * ES : kOOB, 0);
+      } else {
+        acc_slice_t<TIn>(Rdq, Rdq32, dqv, ok ? off * 4u : kOOB, ok ? off * ES : kOOB, 0, p.acc_mode);
+        acc_slice_t<TIn>(Rdk, Rdk32, dkv, ok ? off * 4u : kOOB, ok ? off * ES : kOOB, 0, p.acc_mode);
+      }
     }
     // reverse cumsum over tokens: 16-lane suffix sums, block a=1's total into a=0, half 1
     // into half 0 (through gBlk)
@@ -698,6 +708,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
         float ga[4] = {0.f, 0.f, 0.f, 0.f};
         if constexpr (kEarlyAdd) unpack4(gadd[a], ga);
         else if (p.dg_add) unpack4(bld128(Rdga, ok ? off * 4u : kOOB, 0), ga);
+        else if (p.dg_accum) unpack4(bld128(Rdg, ok ? off * 4u : kOOB, 0), ga);   // earlier slices
         bst128(Rdg, make_uint4(__float_as_uint(dgr[a][0] + add[0] + ga[0]), __float_as_uint(dgr[a][1] + add[1] + ga[1]),
                                __float_as_uint(dgr[a][2] + add[2] + ga[2]), __float_as_uint(dgr[a][3] + add[3] + ga[3])),
                ok ? off * 4u : kOOB, 0);
@@ -720,8 +731,10 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
   if (kScalarGate && gmode == kGateS && p.dg) {
     __syncthreads();
     if (tq < C) {
-      const float x = gDgS[tq] + gDgS[C + tq];
-      bst32(Rdg, __float_as_uint(x), tq < nval ? (uint32_t)tq * H * 4u : kOOB, 0);
+      float x = gDgS[tq] + gDgS[C + tq];
+      const uint32_t o = tq < nval ? (uint32_t)tq * H * 4u : kOOB;
+      if (p.dg_accum) x += __uint_as_float(bld32(Rdg, o, 0));   // earlier slices
+      bst32(Rdg, __float_as_uint(x), o, 0);
     }
   }
   };

@@ -45,6 +45,15 @@ struct SweepParams {
   // o_t = oscale S_t^T q_t (fused_recurrent with reverse = True).
   int gshift = 0;
   float oscale = 1.f;
+  // Channel slices (K beyond one 128-channel tile runs as slices; the caller loops over them):
+  // q, k, a per-channel g and the state rows are read with row length ldk (0: K), the pointers
+  // at the slice's first channel; s0 / s_fin / ckpt are [.., ldk, V] with this slice's rows
+  // starting at their pointers (a constant per-channel gate [H, ldk] likewise).
+  int ldk = 0;
+  // Output accumulation over the slices, in fp32 acc32 [B,T,H,V]: acc_mode 0 writes out as
+  // usual; 1 writes acc32 = result; 2 adds acc32 += result; 3 writes out = acc32 + result.
+  float* acc32 = nullptr;
+  int acc_mode = 0;
 };
 
 // TIn = uint16_t (bf16 bits) or float; REV = reverse (state-gradient) sweep;
@@ -95,6 +104,17 @@ struct DqkgParams {
   int paired;
   const float* h0;
   const float* dht;
+  // Channel / value slices: q, k, g (per-channel), dq, dk, dg (per-channel) have row length
+  // ldk (0: K) and v, dO row length ldv (0: V), their pointers at the slice's first column;
+  // hs / dhs are [total, H, ldk, ldv] with the slice's (row, column) origin at their pointers.
+  int ldk = 0, ldv = 0;
+  // Accumulation of dq / dk over value slices, in fp32 dq32 / dk32 [B,T,H,ldk]: acc_mode 0
+  // writes dq / dk; 1 writes dq32 / dk32 = result; 2 adds into them; 3 writes dq / dk =
+  // dq32 / dk32 + result.  dg_accum != 0 adds this call's dg into dg instead of writing it.
+  float* dq32 = nullptr;
+  float* dk32 = nullptr;
+  int acc_mode = 0;
+  int dg_accum = 0;
 };
 
 // TV = type of v (the KDA backward passes fp32 v_new with bf16 q / k / dO)

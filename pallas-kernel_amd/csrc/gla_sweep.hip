@@ -158,6 +158,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   }
   n = __builtin_amdgcn_readfirstlane(n);
   const int H = p.H, K = p.K, V = p.V;
+  const int LDK = p.ldk > 0 ? p.ldk : K;   // row length of q / k / g and of the state rows
   const float scale = p.scale;
 
   int L, row0, cbase;
@@ -184,7 +185,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   const int yc = (lane & 7) + 8 * (hw & 3), yseg = ((lane >> 3) & 3) + 4 * (hw >> 2);
   const int yv = vt * BV + 2 * yc;
   const bool ycolok = yv < V;
-  const uint32_t rowK = (uint32_t)(H * K), rowV = (uint32_t)(H * V);
+  const uint32_t rowK = (uint32_t)(H * LDK), rowV = (uint32_t)(H * V);
   const uint32_t offQ = colok ? ((uint32_t)r0 * rowK + c0) * ES : kOOB;        // q, k
   const uint32_t offG = colok ? ((uint32_t)r0 * rowK + c0) * 4u : kOOB;        // g, w
   const uint32_t offY = ycolok ? ((uint32_t)(yseg * YR) * rowV + yv) * ES : kOOB;
@@ -203,7 +204,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   float gam4[4] = {gam_h, gam_h, gam_h, gam_h};
   if (gmode == kGateGammaK) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) gam4[j] = colok ? p.g[(size_t)hh * K + c0 + j] : 0.f;
+    for (int j = 0; j < 4; ++j) gam4[j] = colok ? p.g[(size_t)hh * LDK + c0 + j] : 0.f;
   }
 
   // ---- state tiles: tile i of this wave -> (msb, nn)
@@ -216,7 +217,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     for (int r = 0; r < 4; ++r) {
       const int kr = 16 * msb + 4 * lg + r;
       float x = 0.f;
-      if (p.s0 && kr < K && vv < V) x = p.s0[((size_t)(n * H + hh) * K + kr) * V + vv];
+      if (p.s0 && kr < K && vv < V) x = p.s0[((size_t)(n * H + hh) * LDK + kr) * V + vv];
       S[i][r] = x;
     }
   }
@@ -231,9 +232,9 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     for (int r = 0; r < 4; ++r) {
       const int kr = 16 * msb + 4 * lg + r;
       float gl = gam_h;
-      if (gk_mode) gl = kr < K ? p.g[el * K + kr] : 0.f;
+      if (gk_mode) gl = kr < K ? p.g[el * LDK + kr] : 0.f;
       else if (gmode == kGateS) gl = p.g[el];
-      else if (gmode == kGateGammaK) gl = kr < K ? p.g[(size_t)hh * K + kr] : 0.f;
+      else if (gmode == kGateGammaK) gl = kr < K ? p.g[(size_t)hh * LDK + kr] : 0.f;
       fac[r] = fast_exp2(gl * kLog2e);
     }
 #pragma unroll
@@ -263,13 +264,13 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     const int t0 = c * C;
     const int nval = min(C, L - t0);
     const size_t e0 = (size_t)(row0 + t0) * H + hh;     // first row of the chunk, this head
-    const rsrc_t Rq = make_rsrc_rows((const TIn*)p.q, e0, nrows, K);
-    const rsrc_t Rk = make_rsrc_rows((const TIn*)p.k, e0, nrows, K);
+    const rsrc_t Rq = make_rsrc_rows((const TIn*)p.q, e0, nrows, LDK);
+    const rsrc_t Rk = make_rsrc_rows((const TIn*)p.k, e0, nrows, LDK);
     // gshift: token t reads the gate row of token t - 1, so the rows start one token earlier,
     // except in the sequence's first chunk, whose row 0 reads nothing (gate 0)
     const int gadj = (gsh && t0 == 0) ? 1 : 0;
     const size_t eg = gsh && t0 > 0 ? e0 - (size_t)H : e0;
-    const rsrc_t Rg = make_rsrc_rows(p.g, eg, nrows, gk_mode ? K : 1);
+    const rsrc_t Rg = make_rsrc_rows(p.g, eg, nrows, gk_mode ? LDK : 1);
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
       const bool ok = r0 + i < nval;
@@ -339,7 +340,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     float ur[2][4];
     auto load_wu = [&]() {
       const size_t e0 = (size_t)(row0 + t0) * H + hh;
-      const rsrc_t Rw = make_rsrc_rows(p.w, e0, nrows, K);
+      const rsrc_t Rw = make_rsrc_rows(p.w, e0, nrows, LDK);
       const rsrc_t Ru = make_rsrc_rows(p.u, e0, nrows, V);
       const int trow = 16 * R + l16;
 #pragma unroll
@@ -365,7 +366,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     float4 rw[RPT];
     if constexpr (REV_DELTA) {
       const size_t e0 = (size_t)(row0 + t0) * H + hh;
-      const rsrc_t Rw = make_rsrc_rows(p.w, e0, nrows, K);
+      const rsrc_t Rw = make_rsrc_rows(p.w, e0, nrows, LDK);
 #pragma unroll
       for (int i = 0; i < RPT; ++i) {
         const uint4 x = bld128(Rw, r0 + i < nval ? offG : kOOB, i * rowK * 4);
@@ -522,7 +523,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     // loads at the top of the next chunk then also cover the stores).
     if constexpr (!ST) {
       if (p.ckpt && (p.ckpt_par == 0 || ((cbase + c) & 1) == p.ckpt_par - 1)) {
-        const rsrc_t Rck = make_rsrc(p.ckpt + ((size_t)(cbase + c) * H + hh) * K * V,
+        const rsrc_t Rck = make_rsrc(p.ckpt + ((size_t)(cbase + c) * H + hh) * LDK * V,
                                      (long long)K * V * 4);
 #pragma unroll
         for (int i = 0; i < NHT; ++i) {
@@ -823,7 +824,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       // w 2^-Gm is read straight from HBM in the MFMA row layout (against H^T = 2^Gm S).
       const size_t e0 = (size_t)(row0 + t0) * H + hh;
       const rsrc_t Rvn = make_rsrc_rows(p.y32, e0, nrows, V);
-      const rsrc_t Rw = make_rsrc_rows(p.w, e0, nrows, K);
+      const rsrc_t Rw = make_rsrc_rows(p.w, e0, nrows, LDK);
       const rsrc_t Ru = make_rsrc_rows(p.u, e0, nrows, V);
       bf16x8 wh[KP / 32], wl[KP / 32];
 #pragma unroll
@@ -956,7 +957,14 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
           acc[0] *= e4.x; acc[1] *= e4.y; acc[2] *= e4.z; acc[3] *= e4.w;
         }
         const int v0 = vt * BV + 16 * nn + 4 * lg;
-        Wd::st4(Ro, acc, v0 < V ? oo : kOOB, (uint32_t)(16 * nn * ES));
+        if (p.acc_mode == 0) {
+          Wd::st4(Ro, acc, v0 < V ? oo : kOOB, (uint32_t)(16 * nn * ES));
+        } else {
+          // channel slices: the fp32 sum of the slices' outputs (element offset as oo's)
+          const rsrc_t Ra = make_rsrc_rows(p.acc32, eo, nrows, V);
+          const uint32_t fo = (v0 < V && tok < nval) ? ((uint32_t)tok * rowV + v0) * 4u : kOOB;
+          acc_slice_t<TIn>(Ro, Ra, acc, fo, v0 < V ? oo : kOOB, (uint32_t)(16 * nn * ES), p.acc_mode);
+        }
       }
     }
 
@@ -980,7 +988,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int kr = 16 * msb + 4 * lg + r;
-        if (kr < K) p.dec_fin[(size_t)(n * H + hh) * K + kr] = dsum[r];
+        if (kr < K) p.dec_fin[(size_t)(n * H + hh) * LDK + kr] = dsum[r];
       }
     }
   }
@@ -992,7 +1000,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int kr = 16 * msb + 4 * lg + r;
-        if (kr < K && vv < V) p.s_fin[((size_t)(n * H + hh) * K + kr) * V + vv] = S[i][r];
+        if (kr < K && vv < V) p.s_fin[((size_t)(n * H + hh) * LDK + kr) * V + vv] = S[i][r];
       }
     }
   }
@@ -1089,21 +1097,30 @@ static int chunk_fwd_impl(const void* q, const void* k, const void* v, const flo
                           const float* h0, void* o, float* ht, float* h_ckpt,
                           const int32_t* cu_seqlens, const int32_t* chunk_offsets, int B, int T,
                           int H, int K, int V, int N, int dtype, float scale, int gate_mode,
-                          void* stream, int ckpt_par = 0) {
+                          void* stream, int ckpt_par = 0, int ldk = 0, float* o_sum = nullptr,
+                          int acc_mode = 0) {
   if (!q || !k || !v || !g || !o) return tops_set_error(TOPS_ERR_NULL, "gla_chunk_fwd: null tensor");
   if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || N <= 0)
     return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd: non-positive dimension");
   if (K > 128 || (K % 8) || (V % 8))
     return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd: need K <= 128, K % 8 == 0, V % 8 == 0");
   if (cu_seqlens && B != 1) return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd: varlen needs B == 1");
-  if ((long long)kChunk * H * (K > V ? K : V) * 4 >= (1LL << 31))
+  const int kw = ldk > 0 ? ldk : K;
+  if (ldk && (ldk < K || (ldk % 8)))
+    return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd: ldk must be a multiple of 8, at least K");
+  if ((long long)kChunk * H * (kw > V ? kw : V) * 4 >= (1LL << 31))
     return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd: H * max(K, V) too large for 32-bit chunk offsets");
+  if (acc_mode < 0 || acc_mode > 3 || (acc_mode && !o_sum))
+    return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd: acc_mode 1..3 needs the fp32 sum buffer");
   if (!cu_seqlens && N != B) return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd: N must equal B");
   if (h_ckpt && cu_seqlens && !chunk_offsets)
     return tops_set_error(TOPS_ERR_NULL, "gla_chunk_fwd: varlen checkpoints need chunk_offsets");
   SweepParams p{q, k, g, v, h0, o, ht, h_ckpt, cu_seqlens, chunk_offsets,
                 B, T, H, K, V, N, (V + 63) / 64, scale, gate_mode};
   p.ckpt_par = ckpt_par;
+  p.ldk = ldk;
+  p.acc32 = o_sum;
+  p.acc_mode = acc_mode;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
   if (dtype == TOPS_BF16) e = launch_gla_sweep<uint16_t, false>(p, s);
@@ -1156,6 +1173,22 @@ extern "C" int tops_chunk_fwd_paired(const void* q, const void* k, const void* v
   if (!ckpt) return tops_set_error(TOPS_ERR_NULL, "chunk_fwd_paired: null ckpt");
   return chunk_fwd_impl(q, k, v, g, h0, o, ht, ckpt, cu_seqlens, chunk_offsets, B, T, H, K, V, N,
                         dtype, scale, gate_mode, stream, 1);
+}
+
+extern "C" int tops_chunk_fwd_slice(const void* q, const void* k, const void* v, const float* g,
+                                    int gate_mode, const float* h0, void* o, float* o_sum,
+                                    int acc_mode, float* ht, float* h_ckpt,
+                                    const int32_t* cu_seqlens, const int32_t* chunk_offsets, int B,
+                                    int T, int H, int K, int V, int N, int ldk, int dtype,
+                                    float scale, void* stream) {
+  if (gate_mode < kGateK || gate_mode > kGateGammaK)
+    return tops_set_error(TOPS_ERR_SHAPE, "chunk_fwd_slice: gate_mode must be 0..3");
+  if (acc_mode != 1 && acc_mode != 2 && !o)
+    return tops_set_error(TOPS_ERR_NULL, "chunk_fwd_slice: null o");
+  // o is written only by acc_mode 0 and 3; the generic null check needs a pointer
+  return chunk_fwd_impl(q, k, v, g, h0, o ? o : (void*)o_sum, ht, h_ckpt, cu_seqlens,
+                        chunk_offsets, B, T, H, K, V, N, dtype, scale, gate_mode, stream, 0, ldk,
+                        o_sum, acc_mode);
 }
 
 extern "C" int tops_chunk_reverse_fwd(const void* q, const void* k, const void* v, const float* g,

@@ -97,6 +97,7 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
   }
   n = __builtin_amdgcn_readfirstlane(n);
   const int H = p.H, K = p.K, V = p.V;
+  const int LDK = p.ldk > 0 ? p.ldk : K;   // row length of q / k / g and of the state rows
   const float scale = p.scale;
 
   int L, row0, cbase;
@@ -122,7 +123,7 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
   const int yc = (lane & 7) + 8 * (hw & 3), yseg = ((lane >> 3) & 3) + 4 * (hw >> 2);
   const int yv = vt * BV + 2 * yc;
   const bool ycolok = yv < V;
-  const uint32_t rowK = (uint32_t)(H * K), rowV = (uint32_t)(H * V);
+  const uint32_t rowK = (uint32_t)(H * LDK), rowV = (uint32_t)(H * V);
   const uint32_t offQ = colok ? ((uint32_t)r0 * rowK + c0) * ES : kOOB;
   const uint32_t offG = colok ? ((uint32_t)r0 * rowK + c0) * 4u : kOOB;
   const uint32_t offY = ycolok ? ((uint32_t)(yseg * YR) * rowV + yv) * ES : kOOB;
@@ -137,7 +138,7 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
     for (int r = 0; r < 4; ++r) {
       const int kr = 16 * msb + 4 * lg + r;
       float x = 0.f;
-      if (p.s0 && kr < K && vv < V) x = p.s0[((size_t)(n * H + hh) * K + kr) * V + vv];
+      if (p.s0 && kr < K && vv < V) x = p.s0[((size_t)(n * H + hh) * LDK + kr) * V + vv];
       S[i][r] = x;
     }
   }
@@ -157,9 +158,9 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
     const int t0 = c * C;
     const int nval = in ? min(C, L - t0) : 0;
     const size_t e0 = (size_t)(row0 + t0) * H + hh;
-    const rsrc_t Rq = rows_rsrc((const uint16_t*)p.q, e0, nrows, K);
-    const rsrc_t Rk = rows_rsrc((const uint16_t*)p.k, e0, nrows, K);
-    const rsrc_t Rg = rows_rsrc(p.g, e0, nrows, K);
+    const rsrc_t Rq = rows_rsrc((const uint16_t*)p.q, e0, nrows, LDK);
+    const rsrc_t Rk = rows_rsrc((const uint16_t*)p.k, e0, nrows, LDK);
+    const rsrc_t Rg = rows_rsrc(p.g, e0, nrows, LDK);
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
       const bool ok = r0 + i < nval;
@@ -318,7 +319,7 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
   // and after the output products)
   auto store_ckpt = [&](int c) {
     if (p.ckpt && (p.ckpt_par == 0 || ((cbase + c) & 1) == p.ckpt_par - 1)) {
-      const rsrc_t Rck = make_rsrc(p.ckpt + ((size_t)(cbase + c) * H + hh) * K * V,
+      const rsrc_t Rck = make_rsrc(p.ckpt + ((size_t)(cbase + c) * H + hh) * LDK * V,
                                    (long long)K * V * 4);
 #pragma unroll
       for (int i = 0; i < NHT; ++i) {
@@ -482,7 +483,15 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
         }
       }
       const int v0 = vt * BV + 16 * nn + 4 * lg;
-      Words<uint16_t>::st4(Ro, acc, v0 < V ? oo : kOOB, (uint32_t)(16 * nn * ES));
+      if (p.acc_mode == 0) {
+        Words<uint16_t>::st4(Ro, acc, v0 < V ? oo : kOOB, (uint32_t)(16 * nn * ES));
+      } else {
+        // channel slices: the fp32 sum of the slices' outputs
+        const rsrc_t Ra = make_rsrc_rows(p.acc32, eo, nrows, V);
+        const uint32_t fo = (v0 < V && tok < nval) ? ((uint32_t)tok * rowV + v0) * 4u : kOOB;
+        acc_slice_t<uint16_t>(Ro, Ra, acc, fo, v0 < V ? oo : kOOB, (uint32_t)(16 * nn * ES),
+                              p.acc_mode);
+      }
     }
   }
 
@@ -494,7 +503,7 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int kr = 16 * msb + 4 * lg + r;
-        if (kr < K && vv < V) p.s_fin[((size_t)(n * H + hh) * K + kr) * V + vv] = S[i][r];
+        if (kr < K && vv < V) p.s_fin[((size_t)(n * H + hh) * LDK + kr) * V + vv] = S[i][r];
       }
     }
   }

@@ -193,106 +193,145 @@ def _direct(q, K, V, tile_v):
     return q.dtype in _KERNEL_DTYPES and K <= 128 and (V <= 128 or not tile_v)
 
 
-def _k_gate(gate, ks):
+def _k_gate(gate, k0: int, kw: int):
+    """The gate of channel slice [k0, k0 + kw): a strided view for the per-channel forms."""
     mode, gt = gate
-    return (mode, gt[..., ks].contiguous()) if mode in (GATE_K, GATE_GAMMA_K) else gate
+    if mode == GATE_K:
+        return gt[..., k0:k0 + kw]
+    if mode == GATE_GAMMA_K:
+        return gt[:, k0:k0 + kw]
+    return gt
+
+
+def _acc(i: int, n: int) -> int:
+    """acc_mode of slice i of n (include/tops_hip.h, the sliced entry points)."""
+    return 0 if n == 1 else (1 if i == 0 else (3 if i == n - 1 else 2))
+
+
+def _kv_view(x, k0, kw, v0=None, vw=None):
+    """Rows [k0, k0 + kw) (and columns [v0, v0 + vw)) of a [.., K, V] state tensor, as a view."""
+    if x is None:
+        return None
+    x = x[..., k0:k0 + kw, :]
+    return x if v0 is None else x[..., v0:v0 + vw]
+
+
+def _fwd_sliced(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, keep_states):
+    """Forward of heads with K > 128 (bf16 / fp32): one sweep per channel slice of at most 128,
+    reading strided views of q, k, g and the states (no copies); o is the fp32 sum of the
+    slices' outputs, written in v's dtype by the last slice.  Checkpoints keep the whole
+    [chunks, H, K, V] layout."""
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    nk, Kp, _, _ = tiling(K, V, False)
+    mode, gt = gate
+    dev = q.device
+    o = torch.empty_like(v)
+    o_sum = torch.empty(B, T, H, V, device=dev, dtype=torch.float32) if nk > 1 else None
+    ht = torch.empty(plan.N, H, K, V, device=dev, dtype=torch.float32) if output_final_state else None
+    hs = torch.empty(plan.total, H, K, V, device=dev, dtype=torch.float32) if keep_states else None
+    code, dt, st = _GATE_CODE[mode], N.dtype_code(q.dtype), N.stream()
+    for a in range(nk):
+        k0 = a * Kp
+        acc = _acc(a, nk)
+        N.call("tops_chunk_fwd_slice", N.ptr(q[..., k0:k0 + Kp]), N.ptr(k[..., k0:k0 + Kp]),
+               N.ptr(v), N.ptr(_k_gate(gate, k0, Kp)), code, N.ptr(_kv_view(h0, k0, Kp)),
+               N.ptr(o) if acc in (0, 3) else None, N.ptr(o_sum), acc,
+               N.ptr(_kv_view(ht, k0, Kp)), N.ptr(_kv_view(hs, k0, Kp)), N.ptr(plan.cu_dev),
+               N.ptr(plan.offsets_dev), B, T, H, Kp, V, plan.N, K, dt, float(scale), st)
+    return o, ht, hs
+
+
+def _bwd_sliced(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool,
+                want_dg: bool):
+    """Backward of heads beyond one tile (bf16 / fp32): the dh sweep per channel slice (dv
+    summed over them in fp32), then dq / dk / dg per (channel slice, value slice) with dq,
+    dk summed over the value slices in fp32 and dg accumulated in place."""
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    nk, Kp, nv, Vp = tiling(K, V, True)
+    mode, gt = gate
+    dev = q.device
+    f32 = torch.float32
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    k_dg = mode == GATE_K or (mode == GATE_GAMMA_K and want_dg)
+    dg = torch.empty(B, T, H, K, device=dev, dtype=f32) if k_dg else \
+        torch.empty(B, T, H, device=dev, dtype=f32) if mode == GATE_S else None
+    dh_work = torch.empty_like(hs)
+    dh0 = torch.empty(plan.N, H, K, V, device=dev, dtype=f32) if want_dh0 else None
+    dv_sum = torch.empty(B, T, H, V, device=dev, dtype=f32) if nk > 1 else None
+    dq_sum = torch.empty(B, T, H, K, device=dev, dtype=f32) if nv > 1 else None
+    dk_sum = torch.empty_like(dq_sum) if nv > 1 else None
+    code, dt, st = _GATE_CODE[mode], N.dtype_code(q.dtype), N.stream()
+    cu, offs = N.ptr(plan.cu_dev), N.ptr(plan.offsets_dev)
+    for a in range(nk):
+        k0 = a * Kp
+        acc = _acc(a, nk)
+        N.call("tops_chunk_bwd_dh_slice", N.ptr(q[..., k0:k0 + Kp]), N.ptr(k[..., k0:k0 + Kp]),
+               N.ptr(_k_gate(gate, k0, Kp)), code, N.ptr(do), N.ptr(_kv_view(dht, k0, Kp)),
+               N.ptr(_kv_view(dh_work, k0, Kp)), N.ptr(dv) if acc in (0, 3) else None,
+               N.ptr(dv_sum), acc, N.ptr(_kv_view(dh0, k0, Kp)), cu, offs, B, T, H, Kp, V,
+               plan.N, K, dt, float(scale), st)
+    first = True
+    for a in range(nk):
+        k0 = a * Kp
+        ks = slice(k0, k0 + Kp)
+        for b in range(nv):
+            v0 = b * Vp
+            acc = _acc(b, nv)
+            dga = None if dg is None else (dg[..., ks] if k_dg else dg)
+            dg_accum = int(b > 0) if k_dg else int(not first)
+            N.call("tops_chunk_bwd_dqkg_slice", N.ptr(q[..., ks]), N.ptr(k[..., ks]),
+                   N.ptr(v[..., v0:v0 + Vp]), N.ptr(_k_gate(gate, k0, Kp)), code,
+                   N.ptr(do[..., v0:v0 + Vp]), N.ptr(_kv_view(hs, k0, Kp, v0, Vp)),
+                   N.ptr(_kv_view(dh_work, k0, Kp, v0, Vp)),
+                   N.ptr(dq[..., ks]) if acc in (0, 3) else None,
+                   N.ptr(dk[..., ks]) if acc in (0, 3) else None, N.ptr(dga),
+                   N.ptr(None if dq_sum is None else dq_sum[..., ks]),
+                   N.ptr(None if dk_sum is None else dk_sum[..., ks]), acc, dg_accum, cu, offs,
+                   N.ptr(plan.chunk_map_dev), plan.total, B, T, H, Kp, Vp, plan.N, K, V, dt,
+                   float(scale), st)
+            first = False
+    return dq, dk, dv, dg, dh0
 
 
 def chunk_fwd(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, keep_states):
     """Forward of GLA / simple GLA.  Returns (o, ht, h_ckpt).  keep_states: False, True or
     PAIRED (the interleaved checkpoints where paired_states() holds, else every chunk's).
 
-    K > 128 (and V > 128 when states are kept for the backward) runs as equal slices: the
-    recurrence is separate per state entry, so the output is the sum of the K slices'
-    outputs and the V slices are independent.  Such calls, and dtypes the kernels do not
-    take (fp16), compute in fp32 and cast o back; h_ckpt then holds the slices' checkpoints
-    as [slices, chunks, H, K/nK, V/nV]."""
+    K > 128 runs as channel slices on the strided entry points (the recurrence is separate
+    per state entry, so o is the sum of the slices' outputs); V of any width is tiled by the
+    sweep itself.  fp16 inputs are computed in fp32 and o cast back.  h_ckpt is always
+    [chunks, H, K, V] (or the interleaved buffer)."""
     B, T, H, K = q.shape
     V = v.shape[-1]
+    if q.dtype == torch.float16:
+        f32 = torch.float32
+        o, ht, hs = chunk_fwd(q.to(f32), k.to(f32), v.to(f32), gate, h0, scale,
+                              output_final_state, plan, keep_states)
+        return o.to(v.dtype), ht, hs
     if keep_states == PAIRED and not paired_states(q, K, V):
         keep_states = True
-    if _direct(q, K, V, bool(keep_states)):
+    if _direct(q, K, V, False):
         return _fwd_tile(q, k, v, gate, h0, scale, output_final_state, plan, keep_states)
-    nk, Kp, nv, Vp = tiling(K, V, keep_states)
-    f32 = torch.float32
-    qf, kf, vf = (x.to(f32) for x in (q, k, v))
-    o = torch.zeros(B, T, H, V, device=q.device, dtype=f32)
-    ht = torch.empty(plan.N, H, K, V, device=q.device, dtype=f32) if output_final_state else None
-    hs = torch.empty(nk * nv, plan.total, H, Kp, Vp, device=q.device, dtype=f32) \
-        if keep_states else None
-    for a in range(nk):
-        ks = slice(a * Kp, (a + 1) * Kp)
-        qa, ka, ga = qf[..., ks].contiguous(), kf[..., ks].contiguous(), _k_gate(gate, ks)
-        for b in range(nv):
-            vs = slice(b * Vp, (b + 1) * Vp)
-            h0ab = None if h0 is None else h0[:, :, ks, vs].contiguous()
-            oab, htab, hsab = _fwd_tile(qa, ka, vf[..., vs].contiguous(), ga, h0ab, scale,
-                                        output_final_state, plan, keep_states)
-            o[..., vs] += oab
-            if ht is not None:
-                ht[:, :, ks, vs] = htab
-            if hs is not None:
-                hs[a * nv + b] = hsab
-    return o.to(v.dtype), ht, hs
+    if q.dtype not in _KERNEL_DTYPES:
+        raise TypeError(f"tops-hip chunk kernels take float32, bfloat16 or float16, got {q.dtype}")
+    return _fwd_sliced(q, k, v, gate, h0, scale, output_final_state, plan, keep_states)
 
 
 def chunk_bwd(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool,
               want_dg: bool = True, h0=None, paired: bool = False):
     """Backward of GLA / simple GLA.  Returns (dq, dk, dv, dg, dh0); dg is [B,T,H,K] for
-    GATE_K, [B,T,H] for GATE_S and None for GATE_GAMMA.  Sliced as chunk_fwd: dq, dk and a
-    per-channel dg are the sums over the V slices, dv (and a scalar-gate dg) the sums over
-    the K slices."""
+    GATE_K, [B,T,H] for GATE_S and None for GATE_GAMMA.  K or V > 128 run as slices
+    (chunk_fwd); fp16 computes in fp32 and casts dq, dk, dv back."""
     B, T, H, K = q.shape
     V = v.shape[-1]
-    if _direct(q, K, V, True) and hs.dim() == 4:
-        return _bwd_tile(q, k, v, gate, do, dht, hs, scale, plan, want_dh0, want_dg, h0, paired)
-    nk, Kp, nv, Vp = tiling(K, V, True)
-    f32 = torch.float32
-    qf, kf, vf, dof = (x.to(f32) for x in (q, k, v, do))
-    mode = gate[0]
-    dq = torch.zeros(B, T, H, K, device=q.device, dtype=f32)
-    dk = torch.zeros_like(dq)
-    dv = torch.zeros(B, T, H, V, device=q.device, dtype=f32)
-    k_dg = mode == GATE_K or (mode == GATE_GAMMA_K and want_dg)
-    dg = torch.zeros_like(dq) if k_dg else \
-        torch.zeros(B, T, H, device=q.device, dtype=f32) if mode == GATE_S else None
-    dh0 = torch.empty(plan.N, H, K, V, device=q.device, dtype=f32) if want_dh0 else None
-    for a in range(nk):
-        ks = slice(a * Kp, (a + 1) * Kp)
-        qa, ka, ga = qf[..., ks].contiguous(), kf[..., ks].contiguous(), _k_gate(gate, ks)
-        for b in range(nv):
-            vs = slice(b * Vp, (b + 1) * Vp)
-            dhtab = None if dht is None else dht[:, :, ks, vs].contiguous()
-            dqa, dka, dvb, dga, dh0ab = _bwd_tile(qa, ka, vf[..., vs].contiguous(), ga,
-                                                   dof[..., vs].contiguous(), dhtab, hs[a * nv + b],
-                                                   scale, plan, want_dh0, want_dg)
-            dq[..., ks] += dqa
-            dk[..., ks] += dka
-            dv[..., vs] += dvb
-            if k_dg:
-                dg[..., ks] += dga
-            elif mode == GATE_S:
-                dg += dga
-            if dh0 is not None:
-                dh0[:, :, ks, vs] = dh0ab
-    return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg, dh0
-
-
-def states_full(hs, K: int, V: int):
-    """Checkpoints [chunks, H, K, V] from chunk_fwd's h_ckpt (whole or sliced)."""
-    if hs.dim() == 4:
-        return hs
-    nk, Kp, nv, Vp = tiling(K, V, True)
-    n, H = hs.shape[1], hs.shape[2]
-    return hs.reshape(nk, nv, n, H, Kp, Vp).permute(2, 3, 0, 4, 1, 5).reshape(n, H, K, V)
-
-
-def states_for_bwd(hs, q, V: int):
-    """chunk_bwd's h_ckpt layout for whole checkpoints [chunks, H, K, V]."""
-    K = q.shape[-1]
+    if q.dtype == torch.float16:
+        f32 = torch.float32
+        dq, dk, dv, dg, dh0 = chunk_bwd(q.to(f32), k.to(f32), v.to(f32), gate, do.to(f32), dht,
+                                        hs, scale, plan, want_dh0, want_dg, h0, paired)
+        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg, dh0
     if _direct(q, K, V, True):
-        return hs
-    nk, Kp, nv, Vp = tiling(K, V, True)
-    n, H = hs.shape[0], hs.shape[1]
-    return hs.reshape(n, H, nk, Kp, nv, Vp).permute(2, 4, 0, 1, 3, 5).reshape(nk * nv, n, H, Kp, Vp) \
-        .contiguous()
+        return _bwd_tile(q, k, v, gate, do, dht, hs, scale, plan, want_dh0, want_dg, h0, paired)
+    return _bwd_sliced(q, k, v, gate, do, dht, hs, scale, plan, want_dh0, want_dg)
+

@@ -24,7 +24,7 @@ import torch
 
 from ...utils import ChunkPlan, cdiv, to_device
 from .._chunk_core import (GATE_K, GATE_GAMMA, GATE_GAMMA_K, PAIRED, check_qkv, paired_states, chunk_fwd as _core_fwd,
-                           chunk_bwd as _core_bwd, states_for_bwd, states_full)
+                           chunk_bwd as _core_bwd)
 
 
 def _check(q, k, v, initial_state, cu_seqlens):
@@ -216,7 +216,7 @@ def chunk_gla_fwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, output_fi
     g_cumsum = g_cumsum.to(torch.float32).contiguous()
     A = chunk_gla_fwd_intra_gk(qp, kp, g_cumsum, scale, chunk_size=C)
     if C == 64:
-        h = states_full(hs, K, V).reshape(B if cu_seqlens is None else 1, -1, H, K, V)
+        h = hs.reshape(B if cu_seqlens is None else 1, -1, H, K, V)
     else:
         h, _ = _recurrence(kp, pad.pad(v), None, None, g_cumsum, h0, pad.cu, C, False, 1.0, 1,
                            torch.float32, False)
@@ -246,7 +246,7 @@ def chunk_gla_bwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, h, A, do,
     if h is None or int(chunk_size) != 64:
         _, _, hs = _core_fwd(q, k, v, (mode, g32), h0, scale, False, plan, keep_states=True)
     else:
-        hs = states_for_bwd(h.reshape(plan.total, H, K, V).contiguous().to(torch.float32), q, V)
+        hs = h.reshape(plan.total, H, K, V).contiguous().to(torch.float32)
     want_dh0 = initial_state is not None or dht is not None
     dq, dk, dv, dg, dh0 = _core_bwd(q, k, v, (mode, g32), do.contiguous().to(q.dtype),
                                     None if dht is None else dht.contiguous().to(torch.float32),

@@ -1,6 +1,7 @@
 """GLA and simple GLA beyond one kernel tile, and fp16 inputs, on MI355X against the float64
-oracle.  K > 128 (and V > 128 in training) runs as equal slices whose outputs add up (the
-recurrence is separate per state entry); fp16 inputs compute in fp32 and cast back.
+oracle.  K > 128 (and V > 128 in the dq / dk / dg stage) runs as equal slices of at most 128
+on the strided entry points (tops_chunk_*_slice: pointers into the full tensors, no copies),
+whose outputs add up in fp32 (the recurrence is separate per state entry).
 Shapes include the reference's simple-GLA K = 256 cases
 (tests/ops/simple_gla/test_chunk_simple_gla_tpu.py:54, test_fused_chunk_simple_gla_tpu.py:53)
 and its V = 256 state tests.  Tolerances (relative L2): fp32 1e-4; bf16 / fp16 2e-3.

@@ -64,20 +64,24 @@ def test_argument_errors_before_device_work():
         simple_gla_bwd(g, g, g, g, g_gamma=torch.zeros(1), mode="bogus")
 
 
-def test_tiling_and_checkpoint_layouts():
-    """The K / V slicing of the chunk core and its checkpoint layouts (host only)."""
-    from tops.ops._chunk_core import states_for_bwd, states_full, tiling
+def test_tiling_and_slice_views():
+    """The K / V slicing of the chunk core (host only): slice widths, the accumulation mode of
+    each slice, and state views that address a slice of [.., K, V] without a copy."""
+    from tops.ops._chunk_core import _acc, _kv_view, tiling
     assert tiling(256, 128, True) == (2, 128, 1, 128)
     assert tiling(192, 256, True) == (2, 96, 2, 128)
     assert tiling(64, 512, False) == (1, 64, 1, 512)
     with pytest.raises(NotImplementedError):
         tiling(200, 64, True)                   # 2 slices of 100: not a multiple of 8
+    assert [_acc(i, 1) for i in range(1)] == [0]
+    assert [_acc(i, 2) for i in range(2)] == [1, 3]
+    assert [_acc(i, 4) for i in range(4)] == [1, 2, 2, 3]
     hs = torch.randn(3, 2, 256, 192)
-    q = torch.zeros(1, 1, 2, 256)
-    tiles = states_for_bwd(hs, q, 192)
-    assert tiles.shape == (4, 3, 2, 128, 96)
-    assert torch.equal(tiles[1], hs[:, :, :128, 96:])
-    assert torch.equal(states_full(tiles, 256, 192), hs)
+    t = _kv_view(hs, 128, 128, 96, 96)
+    assert t.data_ptr() == hs.data_ptr() + (128 * 192 + 96) * 4
+    assert t.stride() == hs.stride()
+    assert torch.equal(t, hs[:, :, 128:, 96:])
+    assert _kv_view(None, 0, 8) is None
 
 
 def test_reference_utils_helpers():
