@@ -11,7 +11,7 @@
  * per-channel log-gates g [B,T,H,K] (fp32); states [N,H,K,V] (fp32).
  * Varlen packing (cu_seqlens != NULL) requires B == 1; N = number of
  * sequences, otherwise N == B.  dtype selects the element type of
- * q/k/v/o/do and their gradients: TOPS_F32 or TOPS_BF16.
+ * q/k/v/o/do and their gradients: TOPS_F32 or TOPS_BF16 (and TOPS_F16 where stated).
  *
  * Each declaration names the reference interface it replaces
  * (paths relative to the reference repository root).
@@ -27,6 +27,13 @@ extern "C" {
 
 #define TOPS_F32 0
 #define TOPS_BF16 1
+/* fp16 inputs: taken by the GLA / simple GLA chunk entry points (tops_gla_chunk_fwd,
+ * tops_simple_gla_chunk_fwd, tops_gla_chunk_fwd_gamma, the _bwd, _bwd_dh and _bwd_dqkg
+ * stages of all three, tops_chunk_*_slice, tops_chunk_state_pass and
+ * tops_chunk_reverse_fwd); every other entry point rejects it (TOPS_ERR_DTYPE).  The
+ * kernels read fp16 elements directly and split them into exact bf16 hi / lo halves, as
+ * they do fp32 inputs; outputs in the input dtype are written as fp16. */
+#define TOPS_F16 2
 
 #define TOPS_OK 0
 #define TOPS_ERR_NULL -1

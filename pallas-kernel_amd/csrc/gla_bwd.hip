@@ -53,8 +53,8 @@ static int check_bwd(const char* who, int B, int T, int H, int K, int V, int N, 
     snprintf(msg, sizeof(msg), "%s: total_chunks must be positive", who);
     return tops_set_error(TOPS_ERR_SHAPE, msg);
   }
-  if (dtype != TOPS_BF16 && dtype != TOPS_F32) {
-    snprintf(msg, sizeof(msg), "%s: dtype must be TOPS_F32 or TOPS_BF16", who);
+  if (dtype != TOPS_BF16 && dtype != TOPS_F32 && dtype != TOPS_F16) {
+    snprintf(msg, sizeof(msg), "%s: dtype must be TOPS_F32, TOPS_BF16 or TOPS_F16", who);
     return tops_set_error(TOPS_ERR_DTYPE, msg);
   }
   return TOPS_OK;
@@ -85,7 +85,8 @@ static int bwd_dh_impl(const void* q, const void* k, const float* g, const void*
   p.acc_mode = acc_mode;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e = dtype == TOPS_BF16 ? launch_gla_sweep<uint16_t, true>(p, s)
-                                    : launch_gla_sweep<float, true>(p, s);
+                 : dtype == TOPS_F16  ? launch_gla_sweep<_Float16, true>(p, s)
+                                      : launch_gla_sweep<float, true>(p, s);
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   return TOPS_OK;
 }
@@ -119,7 +120,9 @@ static int bwd_dqkg_impl(const void* q, const void* k, const void* v, const floa
   p.acc_mode = acc_mode;
   p.dg_accum = dg_accum;
   hipStream_t s = (hipStream_t)stream;
-  hipError_t e = dtype == TOPS_BF16 ? launch_gla_dqkg<uint16_t>(p, s) : launch_gla_dqkg<float>(p, s);
+  hipError_t e = dtype == TOPS_BF16 ? launch_gla_dqkg<uint16_t>(p, s)
+                 : dtype == TOPS_F16  ? launch_gla_dqkg<_Float16>(p, s)
+                                      : launch_gla_dqkg<float>(p, s);
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   return TOPS_OK;
 }

@@ -58,6 +58,9 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
   constexpr int VC = VP / 32;
   constexpr bool SIN = !In<TIn>::kExactBf16;
   constexpr bool SINV = !In<TV>::kExactBf16;
+  // fp16 inputs: split like fp32 ones, loaded as 2-byte elements like bf16 ones
+  constexpr bool F16 = std::is_same<TIn, _Float16>::value;
+  constexpr bool F16V = std::is_same<TV, _Float16>::value;
   constexpr int NPL = SIN ? 2 : 1;
   constexpr int NPLV = SINV ? 2 : 1;
   constexpr int ES = sizeof(TIn);
@@ -197,6 +200,10 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
       const int pc = tq + 256 * i, row = pc / NPCV, col = (pc % NPCV) * EPV;
       if constexpr (!SINV) {
         *(uint4*)(Pv.hi + row * LV + col) = pv[i];
+      } else if constexpr (F16V) {
+        float a[8];
+        unpack8_f16(pv[i], a);
+        put_n<true, 8>(Pv, row, col, a);
       } else {
         float a[4];
         unpack4(pv[i], a);
@@ -208,6 +215,10 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
       const int pc = tq + 256 * i, row = pc / NPC, col = (pc % NPC) * EP;
       if constexpr (!SIN) {
         *(uint4*)(Pd.hi + row * LV + col) = pd[i];
+      } else if constexpr (F16) {
+        float b[8];
+        unpack8_f16(pd[i], b);
+        put_n<true, 8>(Pd, row, col, b);
       } else {
         float b[4];
         unpack4(pd[i], b);
@@ -242,7 +253,8 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
   float rg[8];
   const uint32_t hsh = (ch & 1) ? 0u : 16u;
   auto elem = [&](uint32_t w) {
-    if constexpr (SIN) return __uint_as_float(w);
+    if constexpr (F16) return f16_to_f32(hsh ? w : (w >> 16));
+    else if constexpr (SIN) return __uint_as_float(w);
     else return __uint_as_float((w << hsh) & 0xffff0000u);
   };
   // gate element (row r, channel kc): per-channel [.., K], per-token [.., 1], or none (gamma)
@@ -259,7 +271,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
       const int r = 8 * sg + i;
       const bool v_ = ok && r < nval;
       const uint32_t off = (uint32_t)r * rowK + kc;
-      if constexpr (SIN) {
+      if constexpr (SIN && !F16) {
         rq[i] = bld32(Rq, v_ ? off * 4u : kOOB, 0);
         rk[i] = bld32(Rk, v_ ? off * 4u : kOOB, 0);
       } else {
@@ -789,6 +801,7 @@ hipError_t launch_gla_dqkg(const DqkgParams& p, hipStream_t s) {
 }
 
 template hipError_t launch_gla_dqkg<uint16_t, uint16_t>(const DqkgParams&, hipStream_t);
+template hipError_t launch_gla_dqkg<_Float16, _Float16>(const DqkgParams&, hipStream_t);
 template hipError_t launch_gla_dqkg<float, float>(const DqkgParams&, hipStream_t);
 template hipError_t launch_gla_dqkg<uint16_t, float>(const DqkgParams&, hipStream_t);
 

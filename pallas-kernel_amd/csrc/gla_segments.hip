@@ -80,8 +80,10 @@ extern "C" int tops_chunk_state_pass(const void* z, const void* y, const float* 
     e = reverse ? launch_gla_state_pass<uint16_t, true>(p, s) : launch_gla_state_pass<uint16_t, false>(p, s);
   else if (dtype == TOPS_F32)
     e = reverse ? launch_gla_state_pass<float, true>(p, s) : launch_gla_state_pass<float, false>(p, s);
+  else if (dtype == TOPS_F16)
+    e = reverse ? launch_gla_state_pass<_Float16, true>(p, s) : launch_gla_state_pass<_Float16, false>(p, s);
   else
-    return tops_set_error(TOPS_ERR_DTYPE, "chunk_state_pass: dtype must be TOPS_F32 or TOPS_BF16");
+    return tops_set_error(TOPS_ERR_DTYPE, "chunk_state_pass: dtype must be TOPS_F32, TOPS_BF16 or TOPS_F16");
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   return TOPS_OK;
 }

@@ -1079,11 +1079,15 @@ template hipError_t launch_gla_state_pass<uint16_t, false>(const SweepParams&, h
 template hipError_t launch_gla_state_pass<uint16_t, true>(const SweepParams&, hipStream_t);
 template hipError_t launch_gla_state_pass<float, false>(const SweepParams&, hipStream_t);
 template hipError_t launch_gla_state_pass<float, true>(const SweepParams&, hipStream_t);
+template hipError_t launch_gla_state_pass<_Float16, false>(const SweepParams&, hipStream_t);
+template hipError_t launch_gla_state_pass<_Float16, true>(const SweepParams&, hipStream_t);
 
 template hipError_t launch_gla_sweep<uint16_t, false, false>(const SweepParams&, hipStream_t);
 template hipError_t launch_gla_sweep<uint16_t, true, false>(const SweepParams&, hipStream_t);
 template hipError_t launch_gla_sweep<float, false, false>(const SweepParams&, hipStream_t);
 template hipError_t launch_gla_sweep<float, true, false>(const SweepParams&, hipStream_t);
+template hipError_t launch_gla_sweep<_Float16, false, false>(const SweepParams&, hipStream_t);
+template hipError_t launch_gla_sweep<_Float16, true, false>(const SweepParams&, hipStream_t);
 template hipError_t launch_gla_sweep<uint16_t, false, true>(const SweepParams&, hipStream_t);
 template hipError_t launch_gla_sweep<uint16_t, true, true>(const SweepParams&, hipStream_t);
 template hipError_t launch_gla_sweep<float, false, true>(const SweepParams&, hipStream_t);
@@ -1125,7 +1129,8 @@ static int chunk_fwd_impl(const void* q, const void* k, const void* v, const flo
   hipError_t e;
   if (dtype == TOPS_BF16) e = launch_gla_sweep<uint16_t, false>(p, s);
   else if (dtype == TOPS_F32) e = launch_gla_sweep<float, false>(p, s);
-  else return tops_set_error(TOPS_ERR_DTYPE, "gla_chunk_fwd: dtype must be TOPS_F32 or TOPS_BF16");
+  else if (dtype == TOPS_F16) e = launch_gla_sweep<_Float16, false>(p, s);
+  else return tops_set_error(TOPS_ERR_DTYPE, "gla_chunk_fwd: dtype must be TOPS_F32, TOPS_BF16 or TOPS_F16");
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   return TOPS_OK;
 }
@@ -1217,7 +1222,8 @@ extern "C" int tops_chunk_reverse_fwd(const void* q, const void* k, const void* 
   hipError_t e;
   if (dtype == TOPS_BF16) e = launch_gla_sweep<uint16_t, true>(p, s);
   else if (dtype == TOPS_F32) e = launch_gla_sweep<float, true>(p, s);
-  else return tops_set_error(TOPS_ERR_DTYPE, "chunk_reverse_fwd: dtype must be TOPS_F32 or TOPS_BF16");
+  else if (dtype == TOPS_F16) e = launch_gla_sweep<_Float16, true>(p, s);
+  else return tops_set_error(TOPS_ERR_DTYPE, "chunk_reverse_fwd: dtype must be TOPS_F32, TOPS_BF16 or TOPS_F16");
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   return TOPS_OK;
 }

@@ -107,6 +107,32 @@ template <> struct In<float> {
   __device__ __forceinline__ static void st(float* p, float x) { *p = x; }
 };
 
+// fp16 elements (_Float16): 11 mantissa bits and an exponent range inside bf16's, so a bf16
+// hi / lo pair holds every fp16 value exactly and fp16 inputs take the split path of fp32
+// ones.  The word types are distinct from the bf16 ones (uint2 / uint32_t) so that the
+// unpack overloads pick the fp16 conversion.
+struct H4 { uint2 u; };        // 4 consecutive fp16 elements
+struct H2 { uint32_t u; };     // 2 consecutive fp16 elements
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xffffu));
+}
+// round-to-nearest-even pack of two floats to fp16 (v_cvt_f16_f32)
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+  const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)a);
+  const uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)b);
+  return lo | (hi << 16);
+}
+template <> struct In<_Float16> {
+  static constexpr bool kExactBf16 = false;
+  __device__ __forceinline__ static float ld(const _Float16* p) { return (float)*p; }
+  __device__ __forceinline__ static void ld2(const _Float16* p, float& a, float& b) {
+    const uint32_t u = *(const uint32_t*)p;
+    a = f16_to_f32(u);
+    b = f16_to_f32(u >> 16);
+  }
+  __device__ __forceinline__ static void st(_Float16* p, float x) { *p = (_Float16)x; }
+};
+
 // ---------------------------------------------------------------- MFMA
 __device__ __forceinline__ f32x4 mfma(const bf16x8& a, const bf16x8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -303,6 +329,19 @@ __device__ __forceinline__ void unpack2(const uint2& u, float& a, float& b) {
   a = __uint_as_float(u.x);
   b = __uint_as_float(u.y);
 }
+__device__ __forceinline__ void unpack4(const H4& w, float* x) {
+  x[0] = f16_to_f32(w.u.x); x[1] = f16_to_f32(w.u.x >> 16);
+  x[2] = f16_to_f32(w.u.y); x[3] = f16_to_f32(w.u.y >> 16);
+}
+__device__ __forceinline__ void unpack2(const H2& w, float& a, float& b) {
+  a = f16_to_f32(w.u);
+  b = f16_to_f32(w.u >> 16);
+}
+// 8 fp16 elements of a 16-byte piece
+__device__ __forceinline__ void unpack8_f16(const uint4& u, float* x) {
+  unpack4(H4{make_uint2(u.x, u.y)}, x);
+  unpack4(H4{make_uint2(u.z, u.w)}, x + 4);
+}
 // Word types: 4 and 2 consecutive elements of TIn
 template <typename TIn> struct Words;
 template <> struct Words<uint16_t> {
@@ -312,6 +351,15 @@ template <> struct Words<uint16_t> {
   __device__ __forceinline__ static W2 ld2(rsrc_t r, uint32_t v, uint32_t s) { return bld32(r, v, s); }
   __device__ __forceinline__ static void st4(rsrc_t r, const f32x4& x, uint32_t v, uint32_t s) {
     bst64(r, make_uint2(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])), v, s);
+  }
+};
+template <> struct Words<_Float16> {
+  typedef H4 W4;
+  typedef H2 W2;
+  __device__ __forceinline__ static W4 ld4(rsrc_t r, uint32_t v, uint32_t s) { return H4{bld64(r, v, s)}; }
+  __device__ __forceinline__ static W2 ld2(rsrc_t r, uint32_t v, uint32_t s) { return H2{bld32(r, v, s)}; }
+  __device__ __forceinline__ static void st4(rsrc_t r, const f32x4& x, uint32_t v, uint32_t s) {
+    bst64(r, make_uint2(pack_f16x2(x[0], x[1]), pack_f16x2(x[2], x[3])), v, s);
   }
 };
 template <> struct Words<float> {

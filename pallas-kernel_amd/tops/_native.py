@@ -14,6 +14,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "lib
 
 TOPS_F32 = 0
 TOPS_BF16 = 1
+TOPS_F16 = 2
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int
@@ -197,6 +198,11 @@ def dtype_code(dt: torch.dtype) -> int:
     if dt == torch.float32:
         return TOPS_F32
     raise TypeError(f"tops-hip kernels take float32 or bfloat16 tensors, got {dt}")
+
+
+def chunk_dtype_code(dt: torch.dtype) -> int:
+    """dtype code of the GLA / simple GLA chunk entry points, which also take fp16."""
+    return TOPS_F16 if dt == torch.float16 else dtype_code(dt)
 
 
 def require_cuda(*ts) -> None:

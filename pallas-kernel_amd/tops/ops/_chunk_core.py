@@ -67,7 +67,7 @@ def _segment_states(z, y, gate, s_in, scale, sp, reverse: bool):
         dec = torch.empty(pc.n, H, K, device=dev, dtype=torch.float32)
         N.call("tops_chunk_state_pass", N.ptr(z), N.ptr(y), N.ptr(gt), _GATE_CODE[mode],
                N.ptr(s_loc), N.ptr(dec), N.ptr(pc.start_dev), N.ptr(pc.end_dev), B * T, H, K, V,
-               pc.n, N.dtype_code(z.dtype), float(scale), int(reverse), N.stream())
+               pc.n, N.chunk_dtype_code(z.dtype), float(scale), int(reverse), N.stream())
     init = torch.empty(sp.Nv, H, K, V, device=dev, dtype=torch.float32)
     N.call("tops_chunk_state_combine", N.ptr(s_loc), N.ptr(dec), N.ptr(s_in), N.ptr(init),
            N.ptr(sp.seg_first_dev), N.ptr(pc.first_dev), N.ptr(pc.dst_dev),
@@ -109,7 +109,7 @@ def _fwd_tile(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, kee
             if output_final_state else None
         cu, offs, Bx, Tx, Nx = sp.cu_dev, sp.offsets_dev, 1, B * T, sp.Nv
     tail = (N.ptr(s0), N.ptr(o), N.ptr(fin), N.ptr(hs), N.ptr(cu), N.ptr(offs),
-            Bx, Tx, H, K, V, Nx, N.dtype_code(q.dtype), float(scale), N.stream())
+            Bx, Tx, H, K, V, Nx, N.chunk_dtype_code(q.dtype), float(scale), N.stream())
     if keep_states == PAIRED:
         N.call("tops_chunk_fwd_paired", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gt),
                _GATE_CODE[mode], *tail)
@@ -147,7 +147,7 @@ def _bwd_tile(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool
     elif mode == GATE_S:
         dg = torch.empty(B, T, H, device=q.device, dtype=torch.float32)
     dh_work = hs if paired else torch.empty_like(hs)
-    dt, st = N.dtype_code(q.dtype), N.stream()
+    dt, st = N.chunk_dtype_code(q.dtype), N.stream()
     sp = plan.segments(H, V)
     if sp is None:
         dh0 = torch.empty(plan.N, H, K, V, device=q.device, dtype=torch.float32) \
@@ -186,7 +186,7 @@ def _bwd_tile(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool
     return dq, dk, dv, dg, dh0
 
 
-_KERNEL_DTYPES = (torch.float32, torch.bfloat16)
+_KERNEL_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
 
 def _direct(q, K, V, tile_v):
@@ -230,7 +230,7 @@ def _fwd_sliced(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, k
     o_sum = torch.empty(B, T, H, V, device=dev, dtype=torch.float32) if nk > 1 else None
     ht = torch.empty(plan.N, H, K, V, device=dev, dtype=torch.float32) if output_final_state else None
     hs = torch.empty(plan.total, H, K, V, device=dev, dtype=torch.float32) if keep_states else None
-    code, dt, st = _GATE_CODE[mode], N.dtype_code(q.dtype), N.stream()
+    code, dt, st = _GATE_CODE[mode], N.chunk_dtype_code(q.dtype), N.stream()
     for a in range(nk):
         k0 = a * Kp
         acc = _acc(a, nk)
@@ -262,7 +262,7 @@ def _bwd_sliced(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bo
     dv_sum = torch.empty(B, T, H, V, device=dev, dtype=f32) if nk > 1 else None
     dq_sum = torch.empty(B, T, H, K, device=dev, dtype=f32) if nv > 1 else None
     dk_sum = torch.empty_like(dq_sum) if nv > 1 else None
-    code, dt, st = _GATE_CODE[mode], N.dtype_code(q.dtype), N.stream()
+    code, dt, st = _GATE_CODE[mode], N.chunk_dtype_code(q.dtype), N.stream()
     cu, offs = N.ptr(plan.cu_dev), N.ptr(plan.offsets_dev)
     for a in range(nk):
         k0 = a * Kp
@@ -301,15 +301,11 @@ def chunk_fwd(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, kee
 
     K > 128 runs as channel slices on the strided entry points (the recurrence is separate
     per state entry, so o is the sum of the slices' outputs); V of any width is tiled by the
-    sweep itself.  fp16 inputs are computed in fp32 and o cast back.  h_ckpt is always
-    [chunks, H, K, V] (or the interleaved buffer)."""
+    sweep itself.  fp32, bf16 and fp16 inputs are read as they are (fp16 and fp32 split
+    into bf16 hi / lo halves inside the kernels).  h_ckpt is always [chunks, H, K, V] (or the
+    interleaved buffer)."""
     B, T, H, K = q.shape
     V = v.shape[-1]
-    if q.dtype == torch.float16:
-        f32 = torch.float32
-        o, ht, hs = chunk_fwd(q.to(f32), k.to(f32), v.to(f32), gate, h0, scale,
-                              output_final_state, plan, keep_states)
-        return o.to(v.dtype), ht, hs
     if keep_states == PAIRED and not paired_states(q, K, V):
         keep_states = True
     if _direct(q, K, V, False):
@@ -323,14 +319,9 @@ def chunk_bwd(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool
               want_dg: bool = True, h0=None, paired: bool = False):
     """Backward of GLA / simple GLA.  Returns (dq, dk, dv, dg, dh0); dg is [B,T,H,K] for
     GATE_K, [B,T,H] for GATE_S and None for GATE_GAMMA.  K or V > 128 run as slices
-    (chunk_fwd); fp16 computes in fp32 and casts dq, dk, dv back."""
+    (chunk_fwd); dq, dk, dv come back in the input dtype."""
     B, T, H, K = q.shape
     V = v.shape[-1]
-    if q.dtype == torch.float16:
-        f32 = torch.float32
-        dq, dk, dv, dg, dh0 = chunk_bwd(q.to(f32), k.to(f32), v.to(f32), gate, do.to(f32), dht,
-                                        hs, scale, plan, want_dh0, want_dg, h0, paired)
-        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg, dh0
     if _direct(q, K, V, True):
         return _bwd_tile(q, k, v, gate, do, dht, hs, scale, plan, want_dh0, want_dg, h0, paired)
     return _bwd_sliced(q, k, v, gate, do, dht, hs, scale, plan, want_dh0, want_dg)

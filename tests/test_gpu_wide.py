@@ -1,7 +1,8 @@
 """GLA and simple GLA beyond one kernel tile, and fp16 inputs, on MI355X against the float64
 oracle.  K > 128 (and V > 128 in the dq / dk / dg stage) runs as equal slices of at most 128
 on the strided entry points (tops_chunk_*_slice: pointers into the full tensors, no copies),
-whose outputs add up in fp32 (the recurrence is separate per state entry).
+whose outputs add up in fp32 (the recurrence is separate per state entry).  fp16 inputs are
+read by the kernels as fp16 (TOPS_F16) and split into exact bf16 hi / lo halves.
 Shapes include the reference's simple-GLA K = 256 cases
 (tests/ops/simple_gla/test_chunk_simple_gla_tpu.py:54, test_fused_chunk_simple_gla_tpu.py:53)
 and its V = 256 state tests.  Tolerances (relative L2): fp32 1e-4; bf16 / fp16 2e-3.
@@ -196,3 +197,35 @@ def test_simple_gla_naive_mode_returns_float32(cuda_device):
     ro, rht = S.naive_simple_gla(sq, sk, sv, g=d["g"], initial_state=d["h0"],
                                  output_final_state=True)
     assert rel(host(o), ro) < 1e-4 and rel(host(ht), rht) < 1e-4
+
+
+@pytest.mark.parametrize("K,V", [(128, 128), (64, 96), (256, 128)])
+def test_fp16_entry_points_read_fp16(K, V, cuda_device):
+    """The chunk entry points take fp16 tensors themselves (TOPS_F16): forward and both
+    backward stages through the C ABI on fp16 inputs match the fp32 entry points run on the
+    same (fp16-representable) values, up to the fp16 rounding of the stored outputs.  K = 256
+    goes through the channel-slice entry points."""
+    import tops._native as N
+    from tops.ops._chunk_core import chunk_bwd, chunk_fwd
+    from tops.utils import ChunkPlan
+    B, T, H = 2, 150, 2
+    d = gla_inputs(B, T, H, K, V, seed=K + V, h0=True, grads=True)
+    f16 = lambda x: to_dev(x, torch.float16, cuda_device)
+    q, k, v, do = (f16(d[x]) for x in ("q", "k", "v", "do"))
+    q32, k32, v32, do32 = (x.float() for x in (q, k, v, do))
+    g = to_dev(d["g"], torch.float32, cuda_device)
+    h0 = to_dev(d["h0"], torch.float32, cuda_device)
+    dht = to_dev(d["dht"], torch.float32, cuda_device)
+    plan = ChunkPlan.get(B, T, None, cuda_device)
+    gate = ("k", g)
+    o, ht, hs = chunk_fwd(q, k, v, gate, h0, K ** -0.5, True, plan, True)
+    o32, ht32, hs32 = chunk_fwd(q32, k32, v32, gate, h0, K ** -0.5, True, plan, True)
+    assert o.dtype == torch.float16 and N.chunk_dtype_code(q.dtype) == N.TOPS_F16
+    assert rel(host(o), host(o32)) < 1e-3
+    assert rel(host(ht), host(ht32)) < 1e-5 and rel(host(hs), host(hs32)) < 1e-5
+    a = chunk_bwd(q, k, v, gate, do, dht, hs, K ** -0.5, plan, True)
+    b = chunk_bwd(q32, k32, v32, gate, do32, dht, hs32, K ** -0.5, plan, True)
+    for name, x, y in zip(("dq", "dk", "dv", "dg", "dh0"), a, b):
+        lim = 1e-3 if x.dtype == torch.float16 else 1e-5
+        assert rel(host(x), host(y)) < lim, name
+    assert a[0].dtype == a[1].dtype == a[2].dtype == torch.float16
