@@ -38,10 +38,10 @@ _TH = B * T * H
 _S = B * H * K * V * 4
 KERNELS = {
     # q, k, v, g read; o written; h0 read; ht written
-    "tops_gla_chunk_fwd": dict(kernel="gla_sweep_kernel<fwd>",
+    "tops_gla_chunk_fwd": dict(kernel="gla_pipe_kernel<fwd>",
                                bytes=_TH * (2 * K + 2 * K + 2 * V + 4 * K + 2 * V) + 2 * _S),
     # q, k, g, dO read; dv written; dht read; dh0 written
-    "tops_gla_chunk_bwd_dh": dict(kernel="gla_sweep_kernel<rev>",
+    "tops_gla_chunk_bwd_dh": dict(kernel="gla_pipe_kernel<rev>",
                                   bytes=_TH * (2 * K + 2 * K + 4 * K + 2 * V + 2 * V) + 2 * _S),
     # q, k, v, g, dO read; dq, dk, dg written
     "tops_gla_chunk_bwd_dqkg": dict(kernel="gla_dqkg_kernel",

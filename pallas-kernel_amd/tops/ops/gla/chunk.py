@@ -22,7 +22,7 @@ from __future__ import annotations
 
 import torch
 
-from ...utils import ChunkPlan, cdiv, to_device
+from ...utils import ChunkPlan, cdiv, inference_inputs, to_device
 from .._chunk_core import (GATE_K, GATE_GAMMA, GATE_GAMMA_K, PAIRED, check_qkv, paired_states, chunk_fwd as _core_fwd,
                            chunk_bwd as _core_bwd)
 
@@ -117,6 +117,7 @@ def chunk_gla(
     _check(q, k, v, initial_state, cu_seqlens)
     if scale is None:
         scale = K ** -0.5
+    q, k, v, gt, initial_state = inference_inputs(q, k, v, gt, initial_state)
     o, ht = _ChunkGLA.apply(q, k, v, gt, initial_state, mode, float(scale),
                             bool(output_final_state), cu_seqlens)
     return o, (ht if output_final_state else None)

@@ -30,7 +30,7 @@ import numpy as np
 import torch
 
 from ... import _native as N
-from ...utils import ChunkPlan, to_device
+from ...utils import ChunkPlan, inference_inputs, to_device
 
 
 def _cu_dev(cu_seqlens, device):
@@ -75,6 +75,7 @@ def _sliced(q, k, v, gk, gv, scale, initial_state, output_final_state, reverse, 
         raise NotImplementedError(f"tops-hip fused recurrent kernels need K <= 128 or K in equal "
                                   f"slices of at most 128, multiples of 4 (got K={K})")
     f32 = torch.float32
+    q, k, v, gk, gv, initial_state = inference_inputs(q, k, v, gk, gv, initial_state)
     qf, kf, vf = (x.to(f32) for x in (q, k, v))
     o, hts = None, []
     for sl in ks:
@@ -316,6 +317,7 @@ def fused_recurrent_gla(q, k, v, gk=None, gv=None, scale=None, initial_state=Non
                 output_final_state=output_final_state)
         return chunk_gla(q, k, v, gk, scale=scale, initial_state=initial_state,
                          output_final_state=output_final_state, cu_seqlens=cu_seqlens)
+    q, k, v, gk, gv, initial_state = inference_inputs(q, k, v, gk, gv, initial_state)
     o, ht = _FusedRecurrentGLA.apply(q, k, v, gk, gv, initial_state, float(scale),
                                      bool(output_final_state), bool(reverse), cu_seqlens)
     return o, (ht if output_final_state else None)

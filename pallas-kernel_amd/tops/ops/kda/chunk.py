@@ -25,7 +25,7 @@ import numpy as np
 import torch
 
 from ... import _native as N
-from ...utils import CHUNK, ChunkPlan
+from ...utils import CHUNK, ChunkPlan, inference_inputs
 from .._chunk_core import check_qkv
 
 
@@ -148,6 +148,7 @@ def chunk_kda(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor
     _check(q, k, v, g, beta, initial_state, cu_seqlens)
     if scale is None:
         scale = q.shape[-1] ** -0.5
+    q, k, v, g, beta, initial_state = inference_inputs(q, k, v, g, beta, initial_state)
     o, ht = _ChunkKDA.apply(q, k, v, g, beta, float(scale), initial_state,
                             bool(output_final_state), cu_seqlens)
     return o.to(out_dtype), ht

@@ -20,7 +20,7 @@ from __future__ import annotations
 
 import torch
 
-from ...utils import ChunkPlan
+from ...utils import ChunkPlan, inference_inputs
 from .._chunk_core import (GATE_S, GATE_GAMMA, PAIRED, check_qkv, chunk_fwd as _core_fwd,
                            chunk_bwd as _core_bwd, paired_states)
 
@@ -98,6 +98,7 @@ def chunk_simple_gla(
     check_qkv(q, k, v, initial_state, cu_seqlens, split_ok=True)
     if scale is None:
         scale = q.shape[-1] ** -0.5
+    q, k, v, gt, initial_state = inference_inputs(q, k, v, gt, initial_state)
     o, ht = _ChunkSimpleGLA.apply(q, k, v, gt, initial_state, mode, float(scale),
                                   bool(output_final_state), cu_seqlens)
     return o, (ht if output_final_state else None)

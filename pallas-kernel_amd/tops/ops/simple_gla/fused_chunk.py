@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import torch
 
-from ...utils import ChunkPlan
+from ...utils import ChunkPlan, inference_inputs
 from .._chunk_core import (GATE_GAMMA, PAIRED, check_qkv, chunk_fwd as _core_fwd,
                            chunk_bwd as _core_bwd, paired_states)
 from .chunk import chunk_simple_gla_fwd, chunk_simple_gla_bwd
@@ -63,6 +63,7 @@ def fused_chunk_simple_gla(q, k, v, g_gamma, initial_state=None, scale=None,
     check_qkv(q, k, v, initial_state, None, split_ok=True)
     if scale is None:
         scale = K ** -0.5
+    q, k, v, gg, initial_state = inference_inputs(q, k, v, gg, initial_state)
     o, ht = _FusedChunkSimpleGLA.apply(q, k, v, gg, initial_state, float(scale),
                                        bool(output_final_state))
     return o, (ht if output_final_state else None)

@@ -16,6 +16,16 @@ def cdiv(x: int, y: int) -> int:
     return (x + y - 1) // y
 
 
+def inference_inputs(*ts):
+    """The op's tensor arguments as its autograd Function should see them: detached when grad
+    mode is off (torch.no_grad / inference_mode), since a Function's forward sees
+    needs_input_grad = True for inputs that require grad even then, and would keep the
+    backward's state checkpoints for a backward that cannot run."""
+    if torch.is_grad_enabled():
+        return ts
+    return tuple(t.detach() if isinstance(t, torch.Tensor) else t for t in ts)
+
+
 def _host_cu(cu_seqlens) -> np.ndarray:
     if isinstance(cu_seqlens, torch.Tensor):
         cu_seqlens = cu_seqlens.detach().cpu().numpy()

@@ -37,3 +37,16 @@ def test_cpu_tensors_fail_loudly():
     q = _t(1, 8, 2, 16)
     with pytest.raises(TopsError):
         chunk_simple_gla(q, q, q, _t(2))
+
+
+def test_inference_inputs_detach_only_without_grad_mode():
+    """Under no_grad an autograd Function still sees needs_input_grad = True for inputs that
+    require grad; the ops detach their inputs there so that no backward state is kept."""
+    import torch
+    from tops.utils import inference_inputs
+    x = torch.ones(3, requires_grad=True)
+    a, b = inference_inputs(x, None)
+    assert a is x and b is None
+    with torch.no_grad():
+        a, b, c = inference_inputs(x, None, 2.0)
+    assert not a.requires_grad and a.data_ptr() == x.data_ptr() and b is None and c == 2.0
