@@ -173,6 +173,35 @@ int tops_chunk_bwd_dqkg_paired(const void* q, const void* k, const void* v, cons
                                const int32_t* chunk_map, int total_chunks, int B, int T, int H,
                                int K, int V, int N, int dtype, float scale, void* stream);
 
+/* fp16 state checkpoints for the GLA training path (bf16 inputs, per-channel gates,
+ * K, V <= 128): tops_gla_chunk_fwd / _bwd_dh / _bwd_dqkg (tops/ops/gla/chunk.py:1103-1199,
+ * 832-1095; tops/ops/common/chunk_h.py:685-878) with the forward's h and the reverse sweep's
+ * dh kept as fp16 [total_chunks,H,K,V] (h_ckpt16 / dh16) plus one factor per (chunk, head,
+ * 64-column tile of V), h_scale / dh_scale [total_chunks,H,ceil(V/64)] fp32: the stored
+ * value times its tile's factor is the state (the factor is a power of two chosen from the
+ * tile's largest magnitude, so the fp16 values stay below 2^15 and the scaling is exact;
+ * the fp16 rounding is 2^-12 of the tile's largest entry).  Half the checkpoint bytes of the
+ * fp32 entry points, written by the sweeps and read by dq / dk / dg.  No reference
+ * counterpart for the format (the reference keeps h in fp32).  Other arguments as the fp32
+ * entry points; dtype TOPS_BF16. */
+int tops_gla_chunk_fwd_c16(const void* q, const void* k, const void* v, const float* g,
+                           const float* h0, void* o, float* ht, uint16_t* h_ckpt16,
+                           float* h_scale, const int32_t* cu_seqlens,
+                           const int32_t* chunk_offsets, int B, int T, int H, int K, int V,
+                           int N, int dtype, float scale, void* stream);
+int tops_gla_chunk_bwd_dh_c16(const void* q, const void* k, const float* g, const void* do_,
+                              const float* dht, uint16_t* dh16, float* dh_scale, void* dv,
+                              float* dh0, const int32_t* cu_seqlens,
+                              const int32_t* chunk_offsets, int B, int T, int H, int K, int V,
+                              int N, int dtype, float scale, void* stream);
+int tops_gla_chunk_bwd_dqkg_c16(const void* q, const void* k, const void* v, const float* g,
+                                const void* do_, const uint16_t* h16, const float* h_scale,
+                                const uint16_t* dh16, const float* dh_scale, void* dq, void* dk,
+                                float* dg, const int32_t* cu_seqlens,
+                                const int32_t* chunk_offsets, const int32_t* chunk_map,
+                                int total_chunks, int B, int T, int H, int K, int V, int N,
+                                int dtype, float scale, void* stream);
+
 /* Heads wider than one kernel tile (K or V above 128): the reference pads K and V to
  * multiples of 128 and tiles them inside one kernel (tops/ops/gla/chunk.py:1146-1152, the
  * K / V block grid of K7 / K3 / K4).  Here the caller loops over channel slices (K) and, in

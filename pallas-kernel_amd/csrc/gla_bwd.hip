@@ -68,7 +68,8 @@ static int bwd_dh_impl(const void* q, const void* k, const float* g, const void*
                        const float* dht, float* dh_work, void* dv, float* dh0,
                        const int32_t* cu_seqlens, const int32_t* chunk_offsets, int B, int T, int H,
                        int K, int V, int N, int dtype, float scale, int gate_mode, void* stream,
-                       int ckpt_par = 0, int ldk = 0, float* dv_sum = nullptr, int acc_mode = 0) {
+                       int ckpt_par = 0, int ldk = 0, float* dv_sum = nullptr, int acc_mode = 0,
+                       float* dh_scale = nullptr) {
   if (!q || !k || !g || !do_ || !dh_work || !dv)
     return tops_set_error(TOPS_ERR_NULL, "gla_chunk_bwd_dh: null tensor");
   // (the sweep tiles V by 64, so a channel slice takes the whole V)
@@ -83,6 +84,12 @@ static int bwd_dh_impl(const void* q, const void* k, const float* g, const void*
   p.ldk = ldk;
   p.acc32 = dv_sum;
   p.acc_mode = acc_mode;
+  if (dh_scale) {
+    if (dtype != TOPS_BF16 || gate_mode != kGateK || V > 128 || ldk || ckpt_par)
+      return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_bwd_dh_c16: bf16, per-channel gates, V <= 128, no slices");
+    p.ckpt16 = 1;
+    p.ckpt_scale = dh_scale;
+  }
   hipStream_t s = (hipStream_t)stream;
   hipError_t e = dtype == TOPS_BF16 ? launch_gla_sweep<uint16_t, true>(p, s)
                  : dtype == TOPS_F16  ? launch_gla_sweep<_Float16, true>(p, s)
@@ -99,7 +106,8 @@ static int bwd_dqkg_impl(const void* q, const void* k, const void* v, const floa
                          int gate_mode, void* stream, const float* h0 = nullptr,
                          const float* dht = nullptr, int paired = 0, int ldk = 0, int ldv = 0,
                          float* dq_sum = nullptr, float* dk_sum = nullptr, int acc_mode = 0,
-                         int dg_accum = 0) {
+                         int dg_accum = 0, const float* h_scale = nullptr,
+                         const float* dh_scale = nullptr) {
   if (!q || !k || !v || !g || !do_ || !h_ckpt || !dh_work || !dq || !dk ||
       ((gate_mode == kGateK || gate_mode == kGateS) && !dg))
     return tops_set_error(TOPS_ERR_NULL, "gla_chunk_bwd_dqkg: null tensor");
@@ -119,6 +127,13 @@ static int bwd_dqkg_impl(const void* q, const void* k, const void* v, const floa
   p.dk32 = dk_sum;
   p.acc_mode = acc_mode;
   p.dg_accum = dg_accum;
+  if (h_scale || dh_scale) {
+    if (!h_scale || !dh_scale || dtype != TOPS_BF16 || gate_mode != kGateK || paired || ldk || ldv)
+      return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_bwd_dqkg_c16: bf16, per-channel gates, both scales, unpaired, no slices");
+    p.ckpt16 = 1;
+    p.hs_scale = h_scale;
+    p.dhs_scale = dh_scale;
+  }
   hipStream_t s = (hipStream_t)stream;
   hipError_t e = dtype == TOPS_BF16 ? launch_gla_dqkg<uint16_t>(p, s)
                  : dtype == TOPS_F16  ? launch_gla_dqkg<_Float16>(p, s)
@@ -230,6 +245,35 @@ extern "C" int tops_gla_chunk_bwd_dqkg_gamma(const void* q, const void* k, const
   return bwd_dqkg_impl(q, k, v, g_gamma, do_, h_ckpt, dh_work, dq, dk, dg, cu_seqlens,
                        chunk_offsets, chunk_map, total_chunks, B, T, H, K, V, N, dtype, scale,
                        kGateGammaK, stream);
+}
+
+// fp16 checkpoints (bf16 inputs, per-channel gates): the same three stages with h and dh
+// stored as fp16 [total,H,K,V] plus one power-of-two factor per (chunk, head, 64-column tile).
+extern "C" int tops_gla_chunk_bwd_dh_c16(const void* q, const void* k, const float* g,
+                                         const void* do_, const float* dht, uint16_t* dh16,
+                                         float* dh_scale, void* dv, float* dh0,
+                                         const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                                         int B, int T, int H, int K, int V, int N, int dtype,
+                                         float scale, void* stream) {
+  if (!dh16 || !dh_scale) return tops_set_error(TOPS_ERR_NULL, "gla_chunk_bwd_dh_c16: null checkpoint");
+  return bwd_dh_impl(q, k, g, do_, dht, (float*)dh16, dv, dh0, cu_seqlens, chunk_offsets, B, T, H,
+                     K, V, N, dtype, scale, kGateK, stream, 0, 0, nullptr, 0, dh_scale);
+}
+
+extern "C" int tops_gla_chunk_bwd_dqkg_c16(const void* q, const void* k, const void* v,
+                                           const float* g, const void* do_, const uint16_t* h16,
+                                           const float* h_scale, const uint16_t* dh16,
+                                           const float* dh_scale, void* dq, void* dk, float* dg,
+                                           const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                                           const int32_t* chunk_map, int total_chunks, int B,
+                                           int T, int H, int K, int V, int N, int dtype,
+                                           float scale, void* stream) {
+  if (!h16 || !dh16 || !h_scale || !dh_scale)
+    return tops_set_error(TOPS_ERR_NULL, "gla_chunk_bwd_dqkg_c16: null checkpoint");
+  return bwd_dqkg_impl(q, k, v, g, do_, (const float*)h16, (const float*)dh16, dq, dk, dg,
+                       cu_seqlens, chunk_offsets, chunk_map, total_chunks, B, T, H, K, V, N, dtype,
+                       scale, kGateK, stream, nullptr, nullptr, 0, 0, 0, nullptr, nullptr, 0, 0,
+                       h_scale, dh_scale);
 }
 
 // Channel / value slices of heads wider than one kernel tile (the caller loops over them).

@@ -49,7 +49,10 @@ namespace tops {
 
 // GK: the per-channel gate mode only (kGateK: GLA and KDA), compiled without gate-mode
 // branches; !GK serves the per-token and constant gates chosen at run time.
-template <typename TIn, typename TV, int KP, int VP, bool GK, bool PAIR, bool RG = false>
+// C16: the checkpoints are fp16 with one power-of-two factor per 64-column tile
+// (SweepParams::ckpt16), read as 8 values per 16-byte load and scaled on the way.
+template <typename TIn, typename TV, int KP, int VP, bool GK, bool PAIR, bool RG = false,
+          bool C16 = false>
 __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParams p) {
   constexpr int C = kChunk;
   constexpr int NG = PAIR ? 2 : 1;             // chunks per workgroup
@@ -77,6 +80,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
   static_assert(KP % KH == 0, "KP must be 32, 64 or 128");
   static_assert(!PAIR || (!SIN && !SINV), "the paired layout takes bf16 inputs");
   static_assert(!RG || (!GK && !PAIR && !SIN && !SINV), "RG: bf16, per-token gates, unpaired");
+  static_assert(!C16 || (!PAIR && !RG), "fp16 checkpoints: the unpaired layout");
   typedef Words<TIn> Wd;
 
   constexpr int ZV = NPLV * C * LV, ZD = NPL * C * LV, ZT = (RG ? 1 : 2) * KH * LT;
@@ -358,9 +362,40 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
     Rh = grp == 0 ? Ro : Rx;
     Rdh = grp == 0 ? Rx : Ro;
   } else {
-    Rh = make_rsrc(slot(p.hs, gc), KVB);
-    Rdh = make_rsrc(slot(p.dhs, gc), KVB);
+    if constexpr (C16) {
+      const size_t o = ((size_t)gc * H + hh) * LDK * LDV;
+      Rh = make_rsrc((const uint16_t*)p.hs + o, (long long)K * LDV * 2);
+      Rdh = make_rsrc((const uint16_t*)p.dhs + o, (long long)K * LDV * 2);
+    } else {
+      Rh = make_rsrc(slot(p.hs, gc), KVB);
+      Rdh = make_rsrc(slot(p.dhs, gc), KVB);
+    }
   }
+  // C16: the factors of this chunk's two 64-column tiles (h and dh)
+  float hsc[2] = {1.f, 1.f}, dhsc[2] = {1.f, 1.f};
+  if constexpr (C16) {
+    const int nv = cdiv(V, 64);
+    const size_t so = ((size_t)gc * H + hh) * nv;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if (t < nv) {
+        hsc[t] = p.hs_scale[so + t];
+        dhsc[t] = p.dhs_scale[so + t];
+      }
+    }
+  }
+  // the lane's 8 state values of value block vc (scaled back for fp16 checkpoints)
+  auto state8 = [&](const uint4 (&raw)[VC][2], int vc, const float* sc, float* x) {
+    if constexpr (C16) {
+      unpack8_f16(raw[vc][0], x);
+      const float f = sc[(32 * vc + 8 * lg) >> 6];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] *= f;
+    } else {
+      unpack4(raw[vc][0], x);
+      unpack4(raw[vc][1], x + 4);
+    }
+  };
   const rsrc_t Rdq = make_rsrc_rows((const TIn*)p.dq, e0, nrows, LDK);
   const rsrc_t Rdk = make_rsrc_rows((const TIn*)p.dk, e0, nrows, LDK);
   const rsrc_t Rdka = make_rsrc_rows(p.dk_add, e0, nrows, LDK);
@@ -381,13 +416,15 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
     const int kk = ps * KH + kl;
     auto vrun = [&](int vc, int j) {
       const int v0 = PAIR ? 32 * vc + 16 * j + 4 * lg : 32 * vc + 8 * lg;
-      return (kk < K && v0 < V) ? ((uint32_t)kk * LDV + v0) * 4u : kOOB;
+      return (kk < K && v0 < V) ? ((uint32_t)kk * LDV + v0) * (C16 ? 2u : 4u) : kOOB;
     };
 #pragma unroll
     for (int vc = 0; vc < VC; ++vc) {
       if constexpr (PAIR) {
         raw[vc][0] = bld128(R, vrun(vc, 0), 0);
         raw[vc][1] = bld128(R, vrun(vc, 1), 0);
+      } else if constexpr (C16) {
+        raw[vc][0] = bld128(R, vrun(vc, 0), 0);
       } else {
         const uint32_t o = vrun(vc, 0);
         raw[vc][0] = bld128(R, o, 0);
@@ -517,8 +554,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
     for (int vc = 0; vc < VC; ++vc) {
       const int v0 = 32 * vc + 8 * lg;
       float hv[8];
-      unpack4(hraw[vc][0], hv);
-      unpack4(hraw[vc][1], hv + 4);
+      state8(hraw, vc, hsc, hv);
       uint32_t ah_[4], al_[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) split_bf16x2(al * hv[2 * e], al * hv[2 * e + 1], ah_[e], al_[e]);
@@ -560,10 +596,8 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
     for (int vc = 0; vc < VC; ++vc) {
       const int v0 = 32 * vc + 8 * lg;
       float hv[8], dv[8];
-      unpack4(hraw[vc][0], hv);
-      unpack4(hraw[vc][1], hv + 4);
-      unpack4(draw[vc][0], dv);
-      unpack4(draw[vc][1], dv + 4);
+      state8(hraw, vc, hsc, hv);
+      state8(draw, vc, dhsc, dv);
       if (rh == 0) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) hd += hv[e] * dv[e];
@@ -773,9 +807,14 @@ hipError_t launch_gla_dqkg(const DqkgParams& p, hipStream_t s) {
   const bool gk = !kAllModes || p.gate_mode == kGateK;
   if (p.paired && !kPairs) return hipErrorInvalidValue;
   const dim3 pgrid(((p.total + 1) / 2) * p.H), pblock(512);
+  if (p.ckpt16 && (!kPairs || !gk || p.paired)) return hipErrorInvalidValue;
 #define TOPS_DQKG(KPV, VPV)                                                                   \
   if (kp == KPV && vp == VPV) {                                                               \
     if constexpr (kPairs) {                                                                   \
+      if (p.ckpt16) {                                                                         \
+        hipLaunchKernelGGL((gla_dqkg_kernel<TIn, TV, KPV, VPV, true, false, false, true>), grid, block, 0, s, p); \
+        return hipGetLastError();                                                             \
+      }                                                                                       \
       if (p.paired) {                                                                         \
         if (gk) hipLaunchKernelGGL((gla_dqkg_kernel<TIn, TV, KPV, VPV, true, true>), pgrid, pblock, 0, s, p); \
         else hipLaunchKernelGGL((gla_dqkg_kernel<TIn, TV, KPV, VPV, false, true>), pgrid, pblock, 0, s, p); \

@@ -54,6 +54,12 @@ struct SweepParams {
   // usual; 1 writes acc32 = result; 2 adds acc32 += result; 3 writes out = acc32 + result.
   float* acc32 = nullptr;
   int acc_mode = 0;
+  // fp16 checkpoints (the pipelined bf16 sweep only): ckpt then points at fp16
+  // [total, H, K, V] holding the state divided by 2^e, one power of two per (chunk, head,
+  // 64-column V tile) chosen from the tile's largest magnitude (at most 2^15 after scaling),
+  // and ckpt_scale [total, H, NV] receives the factors 2^e.
+  int ckpt16 = 0;
+  float* ckpt_scale = nullptr;
 };
 
 // TIn = uint16_t (bf16 bits) or float; REV = reverse (state-gradient) sweep;
@@ -115,6 +121,11 @@ struct DqkgParams {
   float* dk32 = nullptr;
   int acc_mode = 0;
   int dg_accum = 0;
+  // fp16 checkpoints (SweepParams::ckpt16): hs / dhs point at fp16 [total, H, K, V] and
+  // hs_scale / dhs_scale [total, H, NV] hold each 64-column tile's factor
+  int ckpt16 = 0;
+  const float* hs_scale = nullptr;
+  const float* dhs_scale = nullptr;
 };
 
 // TV = type of v (the KDA backward passes fp32 v_new with bf16 q / k / dO)

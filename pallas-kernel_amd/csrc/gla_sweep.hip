@@ -1011,6 +1011,7 @@ hipError_t launch_gla_sweep(const SweepParams& p, hipStream_t s) {
   if constexpr (std::is_same<TIn, uint16_t>::value && !DELTA) {
     if (gla_pipe_eligible(p)) return launch_gla_pipe<REV>(p, s);
   }
+  if (p.ckpt16) return hipErrorInvalidValue;   // fp16 checkpoints: the pipelined kernel only
   const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
   dim3 grid(p.NV * p.H * p.N);
   const bool gk = DELTA || p.gate_mode == kGateK;
@@ -1102,7 +1103,7 @@ static int chunk_fwd_impl(const void* q, const void* k, const void* v, const flo
                           const int32_t* cu_seqlens, const int32_t* chunk_offsets, int B, int T,
                           int H, int K, int V, int N, int dtype, float scale, int gate_mode,
                           void* stream, int ckpt_par = 0, int ldk = 0, float* o_sum = nullptr,
-                          int acc_mode = 0) {
+                          int acc_mode = 0, float* ckpt_scale = nullptr) {
   if (!q || !k || !v || !g || !o) return tops_set_error(TOPS_ERR_NULL, "gla_chunk_fwd: null tensor");
   if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || N <= 0)
     return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd: non-positive dimension");
@@ -1125,6 +1126,12 @@ static int chunk_fwd_impl(const void* q, const void* k, const void* v, const flo
   p.ldk = ldk;
   p.acc32 = o_sum;
   p.acc_mode = acc_mode;
+  if (ckpt_scale) {
+    if (dtype != TOPS_BF16 || gate_mode != kGateK || V > 128 || ldk || ckpt_par || !h_ckpt)
+      return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd_c16: bf16, per-channel gates, V <= 128, no slices");
+    p.ckpt16 = 1;
+    p.ckpt_scale = ckpt_scale;
+  }
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
   if (dtype == TOPS_BF16) e = launch_gla_sweep<uint16_t, false>(p, s);
@@ -1142,6 +1149,16 @@ extern "C" int tops_gla_chunk_fwd(const void* q, const void* k, const void* v, c
                                   float scale, void* stream) {
   return chunk_fwd_impl(q, k, v, g, h0, o, ht, h_ckpt, cu_seqlens, chunk_offsets, B, T, H, K, V, N,
                         dtype, scale, kGateK, stream);
+}
+
+extern "C" int tops_gla_chunk_fwd_c16(const void* q, const void* k, const void* v, const float* g,
+                                      const float* h0, void* o, float* ht, uint16_t* h_ckpt16,
+                                      float* h_scale, const int32_t* cu_seqlens,
+                                      const int32_t* chunk_offsets, int B, int T, int H, int K,
+                                      int V, int N, int dtype, float scale, void* stream) {
+  if (!h_ckpt16 || !h_scale) return tops_set_error(TOPS_ERR_NULL, "gla_chunk_fwd_c16: null checkpoint");
+  return chunk_fwd_impl(q, k, v, g, h0, o, ht, (float*)h_ckpt16, cu_seqlens, chunk_offsets, B, T, H,
+                        K, V, N, dtype, scale, kGateK, stream, 0, 0, nullptr, 0, h_scale);
 }
 
 extern "C" int tops_simple_gla_chunk_fwd(const void* q, const void* k, const void* v,

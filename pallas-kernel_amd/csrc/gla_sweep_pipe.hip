@@ -61,6 +61,7 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t sHT[2 * BV * LH];
   __shared__ __attribute__((aligned(16))) float sTot[NSGH * KP];
   __shared__ __attribute__((aligned(16))) uint4 sDt[10 * 64];
+  __shared__ uint32_t sMx[NW];                // fp16 checkpoints: each wave's largest |S|
 
   const Plane PX{sX, sX + C * LQ, LQ};
   const Plane PZ{sZ, sZ + C * LQ, LQ};
@@ -317,20 +318,76 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
   // checkpoint: S as the state entering chunk c (stored at the start of the chunk's matrix
   // phase, which measured fastest of the placements tried: there, at the end of that phase,
   // and after the output products)
+  auto ckpt_on = [&](int c) {
+    return p.ckpt && (p.ckpt_par == 0 || ((cbase + c) & 1) == p.ckpt_par - 1);
+  };
+  // fp16 checkpoints: this wave's largest |S| into sMx (between B1 and B2; read after B2)
+  // the largest |S| of the wave as fp32 bits (non-negative floats order as their bit
+  // patterns): DPP maxima inside each 16-lane row, then the four rows' lane 0 by readlane,
+  // all on the VALU (a cross-lane shuffle would queue behind the sweep's LDS traffic)
+  auto ckpt_max = [&]() {
+    uint32_t m = 0u;
+#pragma unroll
+    for (int i = 0; i < NHT; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) m = max(m, __float_as_uint(S[i][r]) & 0x7fffffffu);
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xF, 0xF, false));
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xF, 0xF, false));
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x141, 0xF, 0xF, false));
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x140, 0xF, 0xF, false));
+    const uint32_t w = max(max((uint32_t)__builtin_amdgcn_readlane((int)m, 0),
+                               (uint32_t)__builtin_amdgcn_readlane((int)m, 16)),
+                           max((uint32_t)__builtin_amdgcn_readlane((int)m, 32),
+                               (uint32_t)__builtin_amdgcn_readlane((int)m, 48)));
+    if (lane == 0) sMx[wave] = w;
+  };
   auto store_ckpt = [&](int c) {
-    if (p.ckpt && (p.ckpt_par == 0 || ((cbase + c) & 1) == p.ckpt_par - 1)) {
-      const rsrc_t Rck = make_rsrc(p.ckpt + ((size_t)(cbase + c) * H + hh) * LDK * V,
-                                   (long long)K * V * 4);
+    if (!ckpt_on(c)) return;
+    if (p.ckpt16) {
+      // the tile's exponent: |S| < 2^(ex + 1), stored as S 2^(14 - ex), so every value is
+      // below 2^15 in fp16; the factor 2^(ex - 14) goes to ckpt_scale
+      uint32_t m = sMx[0];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) m = max(m, sMx[w]);
+      int ex = (int)((m >> 23) & 0xffu) - 127;
+      ex = ex < -100 ? -100 : ex;
+      const float sinv = __uint_as_float((uint32_t)(141 - ex) << 23);
+      if (tid == 0)
+        p.ckpt_scale[((size_t)(cbase + c) * H + hh) * p.NV + vt] = __uint_as_float((uint32_t)(113 + ex) << 23);
+      uint16_t* base = (uint16_t*)p.ckpt + ((size_t)(cbase + c) * H + hh) * LDK * V;
+      const rsrc_t Rck = make_rsrc(base, (long long)K * V * 2);
+      // each lane packs its two rows of one column; lanes (2j, 2j + 1) swap the packs (DPP
+      // quad_perm [1,0,3,2]) and v_perm picks the even lane's row r0 and the odd lane's row
+      // r1 of the column pair
+      const bool odd = l16 & 1;
+      const uint32_t sel = odd ? 0x03020706u : 0x05040100u;
 #pragma unroll
       for (int i = 0; i < NHT; ++i) {
         const int nn = (wave * NHT + i) % (BV / 16);
         const int kr = 16 * msb + 4 * lg;
-        const int vv = vt * BV + 16 * nn + l16;
-        const uint32_t vo = (vv < V) ? ((uint32_t)kr * V + vv) * 4u : kOOB;
+        const int vv = vt * BV + 16 * nn + (l16 & ~1);
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          bst32(Rck, __float_as_uint(S[i][r]), (kr + r < K) ? vo : kOOB, (uint32_t)(r * V * 4));
+        for (int rp = 0; rp < 2; ++rp) {
+          const uint32_t own = pack_f16x2(S[i][2 * rp] * sinv, S[i][2 * rp + 1] * sinv);
+          const uint32_t other = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)own, 0xB1, 0xF, 0xF, false);
+          const uint32_t w = __builtin_amdgcn_perm(other, own, sel);
+          const int row = kr + 2 * rp + (odd ? 1 : 0);
+          bst32(Rck, w, (row < K && vv < V) ? ((uint32_t)row * V + vv) * 2u : kOOB, 0);
+        }
       }
+      return;
+    }
+    const rsrc_t Rck = make_rsrc(p.ckpt + ((size_t)(cbase + c) * H + hh) * LDK * V,
+                                 (long long)K * V * 4);
+#pragma unroll
+    for (int i = 0; i < NHT; ++i) {
+      const int nn = (wave * NHT + i) % (BV / 16);
+      const int kr = 16 * msb + 4 * lg;
+      const int vv = vt * BV + 16 * nn + l16;
+      const uint32_t vo = (vv < V) ? ((uint32_t)kr * V + vv) * 4u : kOOB;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        bst32(Rck, __float_as_uint(S[i][r]), (kr + r < K) ? vo : kOOB, (uint32_t)(r * V * 4));
     }
   };
 
@@ -350,6 +407,7 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
 
     __syncthreads();  // B1: the previous chunk's planes and the totals are no longer read
     write_planes();
+    if (p.ckpt16 && ckpt_on(c)) ckpt_max();
     // the state factors of this chunk, kept for its update (stage() overwrites them)
     float cga[4], cbe[4];
 #pragma unroll
@@ -510,10 +568,12 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
 }
 
 // Whether launch_gla_sweep routes a call to the pipelined kernel: bf16, per-channel gates,
-// not the delta rule, no gate shift.  TOPS_SWEEP_SERIAL=1 in the environment keeps every call
-// on gla_sweep_kernel (the reference schedule, for A/B timing and bitwise comparisons).
+// not the delta rule, no gate shift.  TOPS_SWEEP_SERIAL=1 in the environment keeps such calls
+// on gla_sweep_kernel (the serial schedule, for A/B comparisons), except those that write
+// fp16 checkpoints, which only this kernel does.
 bool gla_pipe_eligible(const SweepParams& p) {
   if (p.gate_mode != kGateK || p.gshift) return false;
+  if (p.ckpt16) return true;   // only this kernel writes fp16 checkpoints
   const char* e = getenv("TOPS_SWEEP_SERIAL");
   return !(e && e[0] == '1');
 }

@@ -57,6 +57,9 @@ SIGNATURES = {
     "tops_chunk_bwd_dh_paired": [_vp] * 3 + [_i32] + [_vp] * 7 + [_i32] * 7 + [_f32, _vp],
     "tops_chunk_bwd_dqkg_paired": [_vp] * 4 + [_i32] + [_vp] * 10 + [_i32] * 8 + [_f32, _vp],
     "tops_chunk_reverse_fwd": [_vp] * 4 + [_i32] + [_vp] * 4 + [_i32] * 7 + [_f32, _vp],
+    "tops_gla_chunk_fwd_c16": [_vp] * 9 + [_vp] * 2 + [_i32] * 7 + [_f32, _vp],
+    "tops_gla_chunk_bwd_dh_c16": [_vp] * 9 + [_vp] * 2 + [_i32] * 7 + [_f32, _vp],
+    "tops_gla_chunk_bwd_dqkg_c16": [_vp] * 12 + [_vp] * 3 + [_i32] * 8 + [_f32, _vp],
     "tops_chunk_fwd_slice": [_vp] * 4 + [_i32] + [_vp] * 3 + [_i32] + [_vp] * 4 + [_i32] * 8
                             + [_f32, _vp],
     "tops_chunk_bwd_dh_slice": [_vp] * 3 + [_i32] + [_vp] * 5 + [_i32] + [_vp] * 3 + [_i32] * 8

@@ -4,8 +4,10 @@ from __future__ import annotations
 
 import torch
 
+from typing import NamedTuple
+
 from .. import _native as N
-from ..utils import ChunkPlan, checkpoint_layout
+from ..utils import ChunkPlan, cdiv, checkpoint_layout
 
 GATE_K, GATE_S, GATE_GAMMA, GATE_GAMMA_K = "k", "s", "gamma", "gamma_k"
 
@@ -88,6 +90,49 @@ def paired_states(q, K: int, V: int) -> bool:
 PAIRED = "paired"
 
 
+class States16(NamedTuple):
+    """fp16 state checkpoints (the GLA training path for bf16 inputs with per-channel gates):
+    h [chunks, H, K, V] fp16 times one factor per (chunk, head, 64-column tile of V), scale
+    [chunks, H, ceil(V / 64)] fp32 (include/tops_hip.h, tops_gla_chunk_fwd_c16)."""
+    h: torch.Tensor
+    scale: torch.Tensor
+
+
+def _c16(q, mode, K: int, V: int) -> bool:
+    """Whether kept states are fp16 checkpoints: bf16, per-channel gates, one tile, and
+    tops.utils.set_checkpoint_layout not "full32"."""
+    return (q.dtype == torch.bfloat16 and mode == GATE_K and K <= 128 and V <= 128
+            and checkpoint_layout() == "full")
+
+
+def _states_like(hs):
+    if isinstance(hs, States16):
+        return States16(torch.empty_like(hs.h), torch.empty_like(hs.scale))
+    return torch.empty_like(hs)
+
+
+def states_fp32(hs):
+    """Kept states as fp32 [chunks, H, K, V] (fp16 checkpoints scaled back)."""
+    if not isinstance(hs, States16):
+        return hs
+    V = hs.h.shape[-1]
+    f = hs.scale.repeat_interleave(64, dim=-1)[..., :V]
+    return hs.h.to(torch.float32) * f[:, :, None, :]
+
+
+def _sptr(hs):
+    return N.ptr(hs.h if isinstance(hs, States16) else hs)
+
+
+def pack_states(hs):
+    """(tensor, scale or None) for ctx.save_for_backward."""
+    return (hs.h, hs.scale) if isinstance(hs, States16) else (hs, None)
+
+
+def unpack_states(h, scale):
+    return h if scale is None else States16(h, scale)
+
+
 def _fwd_tile(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, keep_states):
     """Run the forward chunk sweep on one tile (K <= 128).  gate = (mode, fp32 tensor).  Returns (o, ht, h_ckpt).
     Long or few sequences sweep as concurrent segments (plan.segments).  keep_states: False,
@@ -96,8 +141,13 @@ def _fwd_tile(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, kee
     V = v.shape[-1]
     mode, gt = gate
     o = torch.empty_like(v)
-    hs = torch.empty(plan.total, H, K, V, device=q.device, dtype=torch.float32) \
-        if keep_states else None
+    c16 = keep_states is True and _c16(q, mode, K, V)
+    if c16:
+        hs = States16(torch.empty(plan.total, H, K, V, device=q.device, dtype=torch.float16),
+                      torch.empty(plan.total, H, cdiv(V, 64), device=q.device, dtype=torch.float32))
+    else:
+        hs = torch.empty(plan.total, H, K, V, device=q.device, dtype=torch.float32) \
+            if keep_states else None
     sp = plan.segments(H, V)
     if sp is None:
         ht = torch.empty(plan.N, H, K, V, device=q.device, dtype=torch.float32) \
@@ -108,9 +158,12 @@ def _fwd_tile(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, kee
         fin = torch.empty(sp.Nv, H, K, V, device=q.device, dtype=torch.float32) \
             if output_final_state else None
         cu, offs, Bx, Tx, Nx = sp.cu_dev, sp.offsets_dev, 1, B * T, sp.Nv
-    tail = (N.ptr(s0), N.ptr(o), N.ptr(fin), N.ptr(hs), N.ptr(cu), N.ptr(offs),
+    tail = (N.ptr(s0), N.ptr(o), N.ptr(fin), _sptr(hs), N.ptr(cu), N.ptr(offs),
             Bx, Tx, H, K, V, Nx, N.chunk_dtype_code(q.dtype), float(scale), N.stream())
-    if keep_states == PAIRED:
+    if c16:
+        N.call("tops_gla_chunk_fwd_c16", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gt), N.ptr(s0),
+               N.ptr(o), N.ptr(fin), N.ptr(hs.h), N.ptr(hs.scale), *tail[4:])
+    elif keep_states == PAIRED:
         N.call("tops_chunk_fwd_paired", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gt),
                _GATE_CODE[mode], *tail)
     elif mode == GATE_K:
@@ -146,7 +199,8 @@ def _bwd_tile(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool
         dg = torch.empty(B, T, H, K, device=q.device, dtype=torch.float32)
     elif mode == GATE_S:
         dg = torch.empty(B, T, H, device=q.device, dtype=torch.float32)
-    dh_work = hs if paired else torch.empty_like(hs)
+    c16 = isinstance(hs, States16)
+    dh_work = hs if paired else _states_like(hs)
     dt, st = N.chunk_dtype_code(q.dtype), N.stream()
     sp = plan.segments(H, V)
     if sp is None:
@@ -158,12 +212,18 @@ def _bwd_tile(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool
         fin = torch.empty(sp.Nv, H, K, V, device=q.device, dtype=torch.float32) \
             if want_dh0 else None
         cu, offs, Bx, Tx, Nx = sp.cu_dev, sp.offsets_dev, 1, B * T, sp.Nv
-    dh_args = (N.ptr(do), N.ptr(s0), N.ptr(dh_work), N.ptr(dv), N.ptr(fin), N.ptr(cu), N.ptr(offs),
+    dh_args = (N.ptr(do), N.ptr(s0), _sptr(dh_work), N.ptr(dv), N.ptr(fin), N.ptr(cu), N.ptr(offs),
                Bx, Tx, H, K, V, Nx, dt, float(scale), st)
-    dqkg_tail = (N.ptr(do), N.ptr(hs), N.ptr(dh_work), N.ptr(dq), N.ptr(dk), N.ptr(dg),
+    dqkg_tail = (N.ptr(do), _sptr(hs), _sptr(dh_work), N.ptr(dq), N.ptr(dk), N.ptr(dg),
                  N.ptr(plan.cu_dev), N.ptr(plan.offsets_dev), N.ptr(plan.chunk_map_dev),
                  plan.total, B, T, H, K, V, plan.N, dt, float(scale), st)
-    if paired:
+    if c16:
+        N.call("tops_gla_chunk_bwd_dh_c16", N.ptr(q), N.ptr(k), N.ptr(gt), N.ptr(do), N.ptr(s0),
+               N.ptr(dh_work.h), N.ptr(dh_work.scale), *dh_args[3:])
+        N.call("tops_gla_chunk_bwd_dqkg_c16", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gt), N.ptr(do),
+               N.ptr(hs.h), N.ptr(hs.scale), N.ptr(dh_work.h), N.ptr(dh_work.scale),
+               *dqkg_tail[3:])
+    elif paired:
         code = _GATE_CODE[mode]
         N.call("tops_chunk_bwd_dh_paired", N.ptr(q), N.ptr(k), N.ptr(gt), code, *dh_args)
         N.call("tops_chunk_bwd_dqkg_paired", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gt), code,

@@ -23,7 +23,8 @@ from __future__ import annotations
 import torch
 
 from ...utils import ChunkPlan, cdiv, inference_inputs, to_device
-from .._chunk_core import (GATE_K, GATE_GAMMA, GATE_GAMMA_K, PAIRED, check_qkv, paired_states, chunk_fwd as _core_fwd,
+from .._chunk_core import (GATE_K, GATE_GAMMA, GATE_GAMMA_K, PAIRED, check_qkv, paired_states,
+                           pack_states, states_fp32, unpack_states, chunk_fwd as _core_fwd,
                            chunk_bwd as _core_bwd)
 
 
@@ -60,7 +61,7 @@ class _ChunkGLA(torch.autograd.Function):
         o, ht, hs = _core_fwd(q, k, v, (mode, g32), h032, scale, output_final_state, plan,
                               keep_states=PAIRED if train else False)
         if train:
-            ctx.save_for_backward(q, k, v, g32, hs, h032)
+            ctx.save_for_backward(q, k, v, g32, *pack_states(hs), h032)
             ctx.paired = paired_states(q, q.shape[-1], v.shape[-1])
             ctx.plan, ctx.scale, ctx.mode = plan, scale, mode
             ctx.g_dtype = gt.dtype
@@ -69,7 +70,8 @@ class _ChunkGLA(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, do, dht):
-        q, k, v, g32, hs, h032 = ctx.saved_tensors
+        q, k, v, g32, hs, hsc, h032 = ctx.saved_tensors
+        hs = unpack_states(hs, hsc)
         do = do.contiguous().to(q.dtype)
         dht = None if dht is None else dht.contiguous().to(torch.float32)
         want_dh0 = ctx.h0_info is not None
@@ -217,7 +219,7 @@ def chunk_gla_fwd(q, k, v, g, g_gamma, g_cumsum, scale, initial_state, output_fi
     g_cumsum = g_cumsum.to(torch.float32).contiguous()
     A = chunk_gla_fwd_intra_gk(qp, kp, g_cumsum, scale, chunk_size=C)
     if C == 64:
-        h = hs.reshape(B if cu_seqlens is None else 1, -1, H, K, V)
+        h = states_fp32(hs).reshape(B if cu_seqlens is None else 1, -1, H, K, V)
     else:
         h, _ = _recurrence(kp, pad.pad(v), None, None, g_cumsum, h0, pad.cu, C, False, 1.0, 1,
                            torch.float32, False)

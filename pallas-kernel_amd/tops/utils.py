@@ -163,18 +163,19 @@ def set_sequence_split(mode=None) -> None:
 
 # Residual states of the GLA / simple-GLA training path.  "full": the forward keeps the
 # state before every chunk and the backward's reverse sweep writes dh for every chunk
-# (2 x chunks x H x K x V fp32).  "paired" (bf16 inputs): one buffer of that size holding h
-# before the even chunks and dh after the odd ones; the dq / dk / dg kernel rebuilds the
-# rest from each chunk's pair partner.  Half the memory and checkpoint bytes, but the
-# rebuild needs both chunks of a pair on one CU: at B8 T4096 H16 K=V=128 on MI355X it is
-# about 0.1 ms per step slower, so "full" is the default.
+# (2 x chunks x H x K x V).  For bf16 inputs with per-channel gates (chunk_gla, K, V <= 128)
+# these are fp16 times a power-of-two factor per (chunk, head, 64 columns of V); other
+# calls keep fp32.  "full32": fp32 everywhere.  "paired" (bf16 inputs): one fp32 buffer of
+# chunks x H x K x V holding h before the even chunks and dh after the odd ones; the dq / dk
+# / dg kernel rebuilds the rest from each chunk's pair partner.  Half the memory and
+# checkpoint bytes of "full32", but the rebuild needs both chunks of a pair on one CU.
 _CKPT = {"layout": "full"}
 
 
 def set_checkpoint_layout(layout: str = "full") -> None:
-    """"full" (default) or "paired": see the comment above."""
-    if layout not in ("full", "paired"):
-        raise ValueError("set_checkpoint_layout takes 'full' or 'paired'")
+    """"full" (default), "full32" or "paired": see the comment above."""
+    if layout not in ("full", "full32", "paired"):
+        raise ValueError("set_checkpoint_layout takes 'full', 'full32' or 'paired'")
     _CKPT["layout"] = layout
 
 

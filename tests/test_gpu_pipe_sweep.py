@@ -11,8 +11,9 @@ fp32 value, one bf16 ulp of a rounded output).  Each case runs forward + backwar
   * the two schedules against each other: relative L2 <= 1e-5 for fp32 outputs (ht, dg,
     dh0), <= 1e-3 for bf16 outputs (o, dq, dk, dv: a handful of one-ulp flips).
 Cases cover K of 32 / 64 / 128 (the kernel's three row splits), ragged T, varlen with
-one-token sequences, h0 / dht, and the paired checkpoint layout (empty sequences: the
-oracle rejects them, as tops/cpu does; other modules run them).
+one-token sequences, h0 / dht, and the fp32 and paired checkpoint layouts (empty sequences:
+the oracle rejects them, as tops/cpu does; other modules run them).  The default layout keeps
+fp16 checkpoints, which only the pipelined kernel writes: test_gpu_ckpt16.py covers it.
 """
 import os
 
@@ -41,7 +42,7 @@ def _id(c):
     return "-".join(f"{k}{v}" for k, v in c.items() if k != "seed")
 
 
-def _run(cfg, device, serial, layout="full"):
+def _run(cfg, device, serial, layout="full32"):
     from tops.ops.gla import chunk_gla
     from tops.utils import set_checkpoint_layout, checkpoint_layout
     B, T, H, K, V = (cfg[x] for x in "BTHKV")
@@ -77,7 +78,7 @@ def _run(cfg, device, serial, layout="full"):
     return d, out
 
 
-@pytest.mark.parametrize("layout", ["full", "paired"])
+@pytest.mark.parametrize("layout", ["full32", "paired"])
 @pytest.mark.parametrize("cfg", CASES, ids=_id)
 def test_pipe_vs_serial_and_oracle(cfg, layout, cuda_device):
     print(f"case {_id(cfg)} layout={layout}", flush=True)
