@@ -652,8 +652,8 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
         for (int r = 0; r < 4; ++r) gZk[rh * KH + 16 * kb + 4 * lg + r] = z[r];
       }
       if (rh == 0) {
-        hd += __shfl_xor(hd, 16, 64);
-        hd += __shfl_xor(hd, 32, 64);
+        hd += lane_xor16(hd, lane);
+        hd += lane_xor32(hd, lane);
         if (lg == 0) gHdh[kl] = hd;
       }
     }

@@ -76,6 +76,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   constexpr int NCQH = NQ / CQL;         // half-waves across the columns
   constexpr int NSGH = NSEG / SGL;       // segment groups (half-waves down the rows)
   static_assert(NQ % CQL == 0, "KP must be a multiple of 32");
+  static_assert(CQL == 8 && SGL == 4, "the segment scan takes 8 column quads x 4 segments");
   constexpr bool SIN = !In<TIn>::kExactBf16;
   constexpr bool FWD_DELTA = DELTA && !REV;
   constexpr bool REV_DELTA = DELTA && REV;
@@ -375,7 +376,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       }
     }
 
-    // ---------------- gate cumsum: thread rows, a shuffle scan over the half-wave's row
+    // ---------------- gate cumsum: thread rows, a DPP scan over the half-wave's row
     // segments, then segment-group totals through LDS
     float G[RPT][4];
     float pre[4], gam[4];
@@ -399,12 +400,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 #pragma unroll
       for (int c2 = 0; c2 < 2; ++c2) {
         const float t = gvc[YR - 1][c2];
-        float x = t;
-#pragma unroll
-        for (int d = 8; d < 32; d <<= 1) {
-          const float y = __shfl_up(x, d, 64);
-          if ((lane & 31) >= d) x += y;
-        }
+        const float x = seg8x4_scan(t, lane);   // over the row segments (lane >> 3) & 3
         prev[c2] = x - t;
         if (((lane >> 3) & 3) == 3) sGvTot[(hw >> 2) * BV + 2 * yc + c2] = x;
       }
@@ -428,12 +424,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float t = G[RPT - 1][j];
-      float x = t;
-#pragma unroll
-      for (int d = CQL; d < 32; d <<= 1) {
-        const float y = __shfl_up(x, d, 64);
-        if ((lane & 31) >= d) x += y;
-      }
+      const float x = seg8x4_scan(t, lane);   // over the row segments sgl of the half-wave
       pre[j] = x - t;                    // segments before this one, within the half-wave
       gam[j] = x;                        // inclusive; the last segment holds the group total
     }

@@ -184,12 +184,8 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
   float sga[4], sal[4], sbe[4];
   // partial gate cumsum of the raw chunk (thread rows, then the half-wave scan); the group
   // totals go to sTot.  The scan over the four row segments of a column quad (lanes cq,
-  // cq + 8, cq + 16, cq + 24 of the half-wave) runs on the VALU: DPP row_shr:8 adds the first
-  // segment of each 16-lane row to the second, row_shl:8 gives every lane of a row the row's
-  // total, and v_permlane16_swap hands the even row's total to the odd row (a cross-lane
-  // shuffle would queue behind the sweep's LDS traffic).
+  // cq + 8, cq + 16, cq + 24 of the half-wave) runs on the VALU (seg8x4_scan).
   float G[RPT][4], pre[4];
-  const bool rhi = l16 >= 8, rodd = lane & 16;
   auto cumsum = [&]() {
     float gam[4];
 #pragma unroll
@@ -202,13 +198,7 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float t = G[RPT - 1][j];
-      const float a = t + dpp_row<0x118>(t);              // row_shr:8 (0 in lanes 0..7)
-      // row_shl:8 (0 in lanes 8..15); a sum rather than a select, which the compiler may
-      // turn into a branch whose DPP read then finds its source lanes switched off
-      const float rt = dpp_row<0x108>(a) + (rhi ? a : 0.f);
-      const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(rt), __float_as_uint(rt),
-                                                       false, false);
-      const float x = a + (rodd ? __uint_as_float(sw[0]) : 0.f);
+      const float x = seg8x4_scan(t, lane);
       pre[j] = x - t;
       gam[j] = x;
     }

@@ -84,6 +84,33 @@ __device__ __forceinline__ float row16_suffix_sum(float x) {
   return x;
 }
 
+// Inclusive scan over the four 8-lane segments of each half-wave: lane l (l & 31 = 8 s + c)
+// gets the sum of t over lanes 8 s' + c (s' <= s) of its half-wave.  DPP row_shr:8 adds the
+// first segment of a 16-lane row to the second, row_shl:8 spreads the row's total over the
+// row, v_permlane16_swap hands the even row's total to the odd row: all on the VALU (a
+// cross-lane shuffle goes through the LDS queue).  Call with every lane active.
+__device__ __forceinline__ float seg8x4_scan(float t, int lane) {
+  const bool hi = (lane & 15) >= 8, odd = lane & 16;
+  const float a = t + dpp_row<0x118>(t);                // 0 from lanes 0..7 of a row
+  // a sum, not a select: the compiler may turn a select into a branch, and a DPP read in it
+  // finds its source lanes switched off
+  const float rt = dpp_row<0x108>(a) + (hi ? a : 0.f);  // 0 from lanes 8..15 of a row
+  const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(rt), __float_as_uint(rt),
+                                                   false, false);
+  return a + (odd ? __uint_as_float(sw[0]) : 0.f);
+}
+// the value of lane l ^ 16 and of lane l ^ 32 (v_permlane16_swap / v_permlane32_swap)
+__device__ __forceinline__ float lane_xor16(float x, int lane) {
+  const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return __uint_as_float((lane & 16) ? s[0] : s[1]);
+}
+__device__ __forceinline__ float lane_xor32(float x, int lane) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return __uint_as_float((lane & 32) ? s[0] : s[1]);
+}
+
 // Input element loads (bf16 stored as uint16_t, or fp32)
 template <typename T> struct In;
 template <> struct In<uint16_t> {
