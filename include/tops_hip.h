@@ -498,6 +498,31 @@ int tops_kda_chunk_bwd(const void* q, const void* k, const void* v, const float*
                        int B, int T, int H, int K, int V, int N, int dtype, float scale,
                        void* stream);
 
+/* fp16 state checkpoints for the KDA training path (bf16 inputs, K, V <= 128):
+ * tops_kda_chunk_fwd / _bwd (tops/ops/kda/chunk.py:25-190; chunk_bwd.py:655-832) with the
+ * forward's state per chunk (h_ckpt16) and the reverse sweep's dS per chunk (dh16_work)
+ * as fp16 [total,H,K,V] plus one power-of-two factor per (chunk, head, 64-column tile of V),
+ * h_scale / dh_scale [total,H,ceil(V/64)] fp32, the format of tops_gla_chunk_fwd_c16.  Half
+ * the bytes of those two intermediates.  No reference counterpart for the format (the
+ * reference recomputes the states in fp32).  The backward's WY and dq / dk / dg stages run as
+ * one kernel (bf16), so there is no dk_work / dg_work.  Other arguments as the fp32 entry
+ * points; dtype TOPS_BF16. */
+int tops_kda_chunk_fwd_c16(const void* q, const void* k, const void* v, const float* g,
+                           const float* beta, const float* h0, void* o, float* ht, float* u,
+                           float* w, float* tt, float* v_new, uint16_t* h_ckpt16, float* h_scale,
+                           const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                           const int32_t* chunk_map, int total_chunks, int B, int T, int H,
+                           int K, int V, int N, int dtype, float scale, void* stream);
+int tops_kda_chunk_bwd_c16(const void* q, const void* k, const void* v, const float* g,
+                           const float* beta, const float* w, const float* tt,
+                           const float* v_new, const uint16_t* h_ckpt16, const float* h_scale,
+                           const void* do_, const float* dht, uint16_t* dh16_work,
+                           float* dh_scale, float* dvn_work, void* dq, void* dk, void* dv,
+                           float* dbeta, float* dg, float* dh0, const int32_t* cu_seqlens,
+                           const int32_t* chunk_offsets, const int32_t* chunk_map,
+                           int total_chunks, int B, int T, int H, int K, int V, int N, int dtype,
+                           float scale, void* stream);
+
 /* KDA gate activation modes. */
 #define TOPS_KDA_GATE_NONE 0        /* gate already activated (cumsum only) */
 #define TOPS_KDA_GATE_SOFTPLUS 1    /* y = -exp(A_log[h]) * softplus(g + dt_bias[h, k]) */

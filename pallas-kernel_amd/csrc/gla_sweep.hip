@@ -113,6 +113,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
                            (GV ? (C * LE + 4 * BV) * 4 : 0);
   constexpr bool SHARED_D = !DELTA && !ST && LDS_BASE + 10 * 64 * 16 <= 160 * 1024;
   __shared__ __attribute__((aligned(16))) uint4 sDt[SHARED_D ? 10 * 64 : 1];
+  __shared__ uint32_t sMx[NW];   // fp16 checkpoints: each wave's largest |S| (fp32 bits)
   // (forward delta rule) 2^-Gm of channel c, Gm = Gamma / 2, sits in the padding columns of the
   // X hi plane (row c / 4, word c % 4): no MFMA fragment or staging write touches columns >= KP
   auto egm_at = [&](int c4) { return (float*)(sX + (c4 >> 2) * LQ + KP); };
@@ -513,7 +514,9 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     // slower (the memory counter retires in issue order, so the waits for the prefetched
     // loads at the top of the next chunk then also cover the stores).
     if constexpr (!ST) {
-      if (p.ckpt && (p.ckpt_par == 0 || ((cbase + c) & 1) == p.ckpt_par - 1)) {
+      if (p.ckpt16) {
+        state_absmax<NHT>(S, sMx, wave, lane);   // the tile maximum is read after B2
+      } else if (p.ckpt && (p.ckpt_par == 0 || ((cbase + c) & 1) == p.ckpt_par - 1)) {
         const rsrc_t Rck = make_rsrc(p.ckpt + ((size_t)(cbase + c) * H + hh) * LDK * V,
                                      (long long)K * V * 4);
 #pragma unroll
@@ -521,10 +524,10 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
           const int nn = (wave * NHT + i) % (BV / 16);
           const int kr = 16 * msb + 4 * lg;
           const int vv = vt * BV + 16 * nn + l16;
-          const uint32_t vo = (vv < V) ? ((uint32_t)kr * V + vv) * 4u : kOOB;
+          const uint32_t vo = (kr < K && vv < V) ? ((uint32_t)kr * V + vv) * 4u : kOOB;  // K % 4 == 0
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            bst32(Rck, __float_as_uint(S[i][r]), (kr + r < K) ? vo : kOOB, (uint32_t)(r * V * 4));
+            bst32(Rck, __float_as_uint(S[i][r]), vo, (uint32_t)(r * V * 4));
         }
       }
     }
@@ -606,6 +609,15 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       }
     }
     __syncthreads();  // B2: all planes visible
+
+    // fp16 checkpoint of S, from the wave maxima taken before B2 (stored ahead of the
+    // prefetch below: the memory counter retires in issue order)
+    if constexpr (!ST) {
+      if (p.ckpt16)
+        store_state16<NHT, NW>(S, sMx, (uint16_t*)p.ckpt + ((size_t)(cbase + c) * H + hh) * LDK * V,
+                               p.ckpt_scale + ((size_t)(cbase + c) * H + hh) * p.NV + vt, K, V,
+                               vt, wave, msb, lane, tid);
+    }
 
     // ---------------- prefetch the chunk PF steps ahead while this one is computed
     if (it + PF < NTs) load_chunk(cidx(it + PF), rs);
@@ -1002,7 +1014,8 @@ hipError_t launch_gla_sweep(const SweepParams& p, hipStream_t s) {
   if constexpr (std::is_same<TIn, uint16_t>::value && !DELTA) {
     if (gla_pipe_eligible(p)) return launch_gla_pipe<REV>(p, s);
   }
-  if (p.ckpt16) return hipErrorInvalidValue;   // fp16 checkpoints: the pipelined kernel only
+  // fp16 checkpoints: whole-width state rows with the plain layout (ckpt_par 0, ldk 0)
+  if (p.ckpt16 && (!p.ckpt || !p.ckpt_scale || p.ckpt_par || p.ldk)) return hipErrorInvalidValue;
   const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
   dim3 grid(p.NV * p.H * p.N);
   const bool gk = DELTA || p.gate_mode == kGateK;

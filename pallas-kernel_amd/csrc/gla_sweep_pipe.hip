@@ -319,59 +319,13 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
     return p.ckpt && (p.ckpt_par == 0 || ((cbase + c) & 1) == p.ckpt_par - 1);
   };
   // fp16 checkpoints: this wave's largest |S| into sMx (between B1 and B2; read after B2)
-  // the largest |S| of the wave as fp32 bits (non-negative floats order as their bit
-  // patterns): DPP maxima inside each 16-lane row, then the four rows' lane 0 by readlane,
-  // all on the VALU (a cross-lane shuffle would queue behind the sweep's LDS traffic)
-  auto ckpt_max = [&]() {
-    uint32_t m = 0u;
-#pragma unroll
-    for (int i = 0; i < NHT; ++i)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) m = max(m, __float_as_uint(S[i][r]) & 0x7fffffffu);
-    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xF, 0xF, false));
-    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xF, 0xF, false));
-    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x141, 0xF, 0xF, false));
-    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x140, 0xF, 0xF, false));
-    const uint32_t w = max(max((uint32_t)__builtin_amdgcn_readlane((int)m, 0),
-                               (uint32_t)__builtin_amdgcn_readlane((int)m, 16)),
-                           max((uint32_t)__builtin_amdgcn_readlane((int)m, 32),
-                               (uint32_t)__builtin_amdgcn_readlane((int)m, 48)));
-    if (lane == 0) sMx[wave] = w;
-  };
+  auto ckpt_max = [&]() { state_absmax<NHT>(S, sMx, wave, lane); };
   auto store_ckpt = [&](int c) {
     if (!ckpt_on(c)) return;
     if (p.ckpt16) {
-      // the tile's exponent: |S| < 2^(ex + 1), stored as S 2^(14 - ex), so every value is
-      // below 2^15 in fp16; the factor 2^(ex - 14) goes to ckpt_scale
-      uint32_t m = sMx[0];
-#pragma unroll
-      for (int w = 1; w < NW; ++w) m = max(m, sMx[w]);
-      int ex = (int)((m >> 23) & 0xffu) - 127;
-      ex = ex < -100 ? -100 : ex;
-      const float sinv = __uint_as_float((uint32_t)(141 - ex) << 23);
-      if (tid == 0)
-        p.ckpt_scale[((size_t)(cbase + c) * H + hh) * p.NV + vt] = __uint_as_float((uint32_t)(113 + ex) << 23);
-      uint16_t* base = (uint16_t*)p.ckpt + ((size_t)(cbase + c) * H + hh) * LDK * V;
-      const rsrc_t Rck = make_rsrc(base, (long long)K * V * 2);
-      // each lane packs its two rows of one column; lanes (2j, 2j + 1) swap the packs (DPP
-      // quad_perm [1,0,3,2]) and v_perm picks the even lane's row r0 and the odd lane's row
-      // r1 of the column pair
-      const bool odd = l16 & 1;
-      const uint32_t sel = odd ? 0x03020706u : 0x05040100u;
-#pragma unroll
-      for (int i = 0; i < NHT; ++i) {
-        const int nn = (wave * NHT + i) % (BV / 16);
-        const int kr = 16 * msb + 4 * lg;
-        const int vv = vt * BV + 16 * nn + (l16 & ~1);
-#pragma unroll
-        for (int rp = 0; rp < 2; ++rp) {
-          const uint32_t own = pack_f16x2(S[i][2 * rp] * sinv, S[i][2 * rp + 1] * sinv);
-          const uint32_t other = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)own, 0xB1, 0xF, 0xF, false);
-          const uint32_t w = __builtin_amdgcn_perm(other, own, sel);
-          const int row = kr + 2 * rp + (odd ? 1 : 0);
-          bst32(Rck, w, (row < K && vv < V) ? ((uint32_t)row * V + vv) * 2u : kOOB, 0);
-        }
-      }
+      store_state16<NHT, NW>(S, sMx, (uint16_t*)p.ckpt + ((size_t)(cbase + c) * H + hh) * LDK * V,
+                             p.ckpt_scale + ((size_t)(cbase + c) * H + hh) * p.NV + vt, K, V, vt,
+                             wave, msb, lane, tid);
       return;
     }
     const rsrc_t Rck = make_rsrc(p.ckpt + ((size_t)(cbase + c) * H + hh) * LDK * V,
@@ -381,10 +335,10 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
       const int nn = (wave * NHT + i) % (BV / 16);
       const int kr = 16 * msb + 4 * lg;
       const int vv = vt * BV + 16 * nn + l16;
-      const uint32_t vo = (vv < V) ? ((uint32_t)kr * V + vv) * 4u : kOOB;
+      const uint32_t vo = (kr < K && vv < V) ? ((uint32_t)kr * V + vv) * 4u : kOOB;  // K % 4 == 0
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        bst32(Rck, __float_as_uint(S[i][r]), (kr + r < K) ? vo : kOOB, (uint32_t)(r * V * 4));
+        bst32(Rck, __float_as_uint(S[i][r]), vo, (uint32_t)(r * V * 4));
     }
   };
 

@@ -70,6 +70,11 @@ struct KdaBwdParams {
   const int* chunk_map;
   int total, B, T, H, K, V, N;
   float scale;
+  // fp16 checkpoints (SweepParams::ckpt16): hs and dhs point at fp16 [total,H,K,V] values,
+  // scaled per (chunk, head, 64-column tile) by hs_scale / dhs_scale [total,H,ceil(V/64)]
+  int ckpt16 = 0;
+  const float* hs_scale = nullptr;
+  const float* dhs_scale = nullptr;
 };
 
 hipError_t launch_kda_bwd_fused(const KdaBwdParams& p, hipStream_t s);

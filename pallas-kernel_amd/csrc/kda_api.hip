@@ -60,17 +60,19 @@ static int kda_check(const char* who, int B, int T, int H, int K, int V, int N, 
   return TOPS_OK;
 }
 
-extern "C" int tops_kda_chunk_fwd(const void* q, const void* k, const void* v, const float* g,
-                                  const float* beta, const float* h0, void* o, float* ht, float* u,
-                                  float* w, float* tt, float* v_new, float* h_ckpt,
-                                  const int32_t* cu_seqlens, const int32_t* chunk_offsets,
-                                  const int32_t* chunk_map, int total_chunks, int B, int T, int H,
-                                  int K, int V, int N, int dtype, float scale, void* stream) {
+static int kda_fwd_impl(const void* q, const void* k, const void* v, const float* g,
+                        const float* beta, const float* h0, void* o, float* ht, float* u,
+                        float* w, float* tt, float* v_new, float* h_ckpt, float* h_scale,
+                        const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                        const int32_t* chunk_map, int total_chunks, int B, int T, int H,
+                        int K, int V, int N, int dtype, float scale, void* stream) {
   if (!q || !k || !v || !g || !beta || !o || !u || !w)
     return tops_set_error(TOPS_ERR_NULL, "kda_chunk_fwd: null tensor");
   int rc = kda_check("kda_chunk_fwd", B, T, H, K, V, N, total_chunks, cu_seqlens, chunk_offsets,
                      chunk_map, dtype);
   if (rc != TOPS_OK) return rc;
+  if (h_scale && (dtype != TOPS_BF16 || !h_ckpt))
+    return tops_set_error(TOPS_ERR_SHAPE, "kda_chunk_fwd_c16: bf16 inputs and a checkpoint buffer");
   hipStream_t s = (hipStream_t)stream;
   KdaPrepParams pp{k, v, g, beta, u, w, tt, cu_seqlens, chunk_offsets, chunk_map,
                    total_chunks, B, T, H, K, V, N};
@@ -78,21 +80,49 @@ extern "C" int tops_kda_chunk_fwd(const void* q, const void* k, const void* v, c
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   SweepParams sp{q, k, g, nullptr, h0, o, ht, h_ckpt, cu_seqlens, chunk_offsets,
                  B, T, H, K, V, N, (V + 63) / 64, scale, kGateK, u, w, v_new};
+  if (h_scale) {
+    sp.ckpt16 = 1;
+    sp.ckpt_scale = h_scale;
+  }
   e = dtype == TOPS_BF16 ? launch_gla_sweep<uint16_t, false, true>(sp, s)
                          : launch_gla_sweep<float, false, true>(sp, s);
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   return TOPS_OK;
 }
 
-extern "C" int tops_kda_chunk_bwd(const void* q, const void* k, const void* v, const float* g,
-                                  const float* beta, const float* w, const float* tt,
-                                  const float* v_new, const float* h_ckpt, const void* do_,
-                                  const float* dht, float* dh_work, float* dvn_work, float* dk_work,
-                                  float* dg_work, void* dq, void* dk, void* dv, float* dbeta,
-                                  float* dg, float* dh0, const int32_t* cu_seqlens,
-                                  const int32_t* chunk_offsets, const int32_t* chunk_map,
-                                  int total_chunks, int B, int T, int H, int K, int V, int N,
-                                  int dtype, float scale, void* stream) {
+extern "C" int tops_kda_chunk_fwd(const void* q, const void* k, const void* v, const float* g,
+                                  const float* beta, const float* h0, void* o, float* ht, float* u,
+                                  float* w, float* tt, float* v_new, float* h_ckpt,
+                                  const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                                  const int32_t* chunk_map, int total_chunks, int B, int T, int H,
+                                  int K, int V, int N, int dtype, float scale, void* stream) {
+  return kda_fwd_impl(q, k, v, g, beta, h0, o, ht, u, w, tt, v_new, h_ckpt, nullptr, cu_seqlens,
+                      chunk_offsets, chunk_map, total_chunks, B, T, H, K, V, N, dtype, scale, stream);
+}
+
+extern "C" int tops_kda_chunk_fwd_c16(const void* q, const void* k, const void* v, const float* g,
+                                      const float* beta, const float* h0, void* o, float* ht,
+                                      float* u, float* w, float* tt, float* v_new,
+                                      uint16_t* h_ckpt16, float* h_scale,
+                                      const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                                      const int32_t* chunk_map, int total_chunks, int B, int T,
+                                      int H, int K, int V, int N, int dtype, float scale,
+                                      void* stream) {
+  if (!h_ckpt16 || !h_scale) return tops_set_error(TOPS_ERR_NULL, "kda_chunk_fwd_c16: null checkpoint");
+  return kda_fwd_impl(q, k, v, g, beta, h0, o, ht, u, w, tt, v_new, (float*)h_ckpt16, h_scale,
+                      cu_seqlens, chunk_offsets, chunk_map, total_chunks, B, T, H, K, V, N, dtype,
+                      scale, stream);
+}
+
+static int kda_bwd_impl(const void* q, const void* k, const void* v, const float* g,
+                        const float* beta, const float* w, const float* tt, const float* v_new,
+                        const float* h_ckpt, const float* h_scale, const void* do_,
+                        const float* dht, float* dh_work, float* dh_scale, float* dvn_work,
+                        float* dk_work, float* dg_work, void* dq, void* dk, void* dv,
+                        float* dbeta, float* dg, float* dh0, const int32_t* cu_seqlens,
+                        const int32_t* chunk_offsets, const int32_t* chunk_map,
+                        int total_chunks, int B, int T, int H, int K, int V, int N,
+                        int dtype, float scale, void* stream) {
   if (!q || !k || !v || !g || !beta || !w || !tt || !v_new || !h_ckpt || !do_ || !dh_work ||
       !dvn_work || !dq || !dk || !dv || !dbeta || !dg)
     return tops_set_error(TOPS_ERR_NULL, "kda_chunk_bwd: null tensor");
@@ -102,17 +132,28 @@ extern "C" int tops_kda_chunk_bwd(const void* q, const void* k, const void* v, c
   int rc = kda_check("kda_chunk_bwd", B, T, H, K, V, N, total_chunks, cu_seqlens, chunk_offsets,
                      chunk_map, dtype);
   if (rc != TOPS_OK) return rc;
+  if ((h_scale || dh_scale) && (!h_scale || !dh_scale || dtype != TOPS_BF16))
+    return tops_set_error(TOPS_ERR_SHAPE, "kda_chunk_bwd_c16: bf16 inputs, both checkpoint factor arrays");
   hipStream_t s = (hipStream_t)stream;
   const bool bf = dtype == TOPS_BF16;
   // 1. reverse delta-rule sweep: dv_new (transposed per chunk), dS per chunk, dh0
   SweepParams sp{q, k, g, do_, dht, nullptr, dh0, dh_work, cu_seqlens, chunk_offsets,
                  B, T, H, K, V, N, (V + 63) / 64, scale, kGateK, nullptr, w, dvn_work};
+  if (dh_scale) {
+    sp.ckpt16 = 1;
+    sp.ckpt_scale = dh_scale;
+  }
   hipError_t e = bf ? launch_gla_sweep<uint16_t, true, true>(sp, s) : launch_gla_sweep<float, true, true>(sp, s);
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   if (bf) {
     // 2+3. the WY backward and dq, dk, dg in one kernel (the WY parts through LDS)
     KdaBwdParams fp{q, k, v, g, beta, tt, dvn_work, v_new, h_ckpt, dh_work, do_, dq, dk, dv, dbeta, dg,
                     cu_seqlens, chunk_offsets, chunk_map, total_chunks, B, T, H, K, V, N, scale};
+    if (h_scale) {
+      fp.ckpt16 = 1;
+      fp.hs_scale = h_scale;
+      fp.dhs_scale = dh_scale;
+    }
     e = launch_kda_bwd_fused(fp, s);
     if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
     return TOPS_OK;
@@ -128,6 +169,39 @@ extern "C" int tops_kda_chunk_bwd(const void* q, const void* k, const void* v, c
   e = bf ? launch_gla_dqkg<uint16_t, float>(dp, s) : launch_gla_dqkg<float, float>(dp, s);
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   return TOPS_OK;
+}
+
+extern "C" int tops_kda_chunk_bwd(const void* q, const void* k, const void* v, const float* g,
+                                  const float* beta, const float* w, const float* tt,
+                                  const float* v_new, const float* h_ckpt, const void* do_,
+                                  const float* dht, float* dh_work, float* dvn_work, float* dk_work,
+                                  float* dg_work, void* dq, void* dk, void* dv, float* dbeta,
+                                  float* dg, float* dh0, const int32_t* cu_seqlens,
+                                  const int32_t* chunk_offsets, const int32_t* chunk_map,
+                                  int total_chunks, int B, int T, int H, int K, int V, int N,
+                                  int dtype, float scale, void* stream) {
+  return kda_bwd_impl(q, k, v, g, beta, w, tt, v_new, h_ckpt, nullptr, do_, dht, dh_work, nullptr,
+                      dvn_work, dk_work, dg_work, dq, dk, dv, dbeta, dg, dh0, cu_seqlens,
+                      chunk_offsets, chunk_map, total_chunks, B, T, H, K, V, N, dtype, scale,
+                      stream);
+}
+
+extern "C" int tops_kda_chunk_bwd_c16(const void* q, const void* k, const void* v, const float* g,
+                                      const float* beta, const float* w, const float* tt,
+                                      const float* v_new, const uint16_t* h_ckpt16,
+                                      const float* h_scale, const void* do_, const float* dht,
+                                      uint16_t* dh16_work, float* dh_scale, float* dvn_work,
+                                      void* dq, void* dk, void* dv, float* dbeta, float* dg,
+                                      float* dh0, const int32_t* cu_seqlens,
+                                      const int32_t* chunk_offsets, const int32_t* chunk_map,
+                                      int total_chunks, int B, int T, int H, int K, int V, int N,
+                                      int dtype, float scale, void* stream) {
+  if (!h_ckpt16 || !h_scale || !dh16_work || !dh_scale)
+    return tops_set_error(TOPS_ERR_NULL, "kda_chunk_bwd_c16: null checkpoint");
+  return kda_bwd_impl(q, k, v, g, beta, w, tt, v_new, (const float*)h_ckpt16, h_scale, do_, dht,
+                      (float*)dh16_work, dh_scale, dvn_work, nullptr, nullptr, dq, dk, dv, dbeta,
+                      dg, dh0, cu_seqlens, chunk_offsets, chunk_map, total_chunks, B, T, H, K, V,
+                      N, dtype, scale, stream);
 }
 
 // ---------------------------------------------------------------------------------------

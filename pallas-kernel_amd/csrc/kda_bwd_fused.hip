@@ -25,7 +25,8 @@
 
 namespace tops {
 
-template <int KP, int VP>
+// C16: fp16 checkpoints (KdaBwdParams::ckpt16), 8 values per 16-byte load, scaled on the way
+template <int KP, int VP, bool C16>
 __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
   constexpr int C = kChunk;
   constexpr int KH = 32;                 // channels per pass
@@ -104,8 +105,22 @@ __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
   const rsrc_t Rq = make_rsrc_rows((const uint16_t*)p.q, e0, nrows, K);
   const rsrc_t Rk = make_rsrc_rows((const uint16_t*)p.k, e0, nrows, K);
   const rsrc_t Rg = make_rsrc_rows(p.g, e0, nrows, K);
-  const long long KVB = (long long)K * V * 4;
-  const rsrc_t Rh = make_rsrc(p.hs + ((size_t)gc * H + hh) * K * V, KVB);
+  const long long KVB = (long long)K * V * (C16 ? 2 : 4);
+  const size_t so = ((size_t)gc * H + hh) * K * V;
+  const rsrc_t Rh = C16 ? make_rsrc((const uint16_t*)p.hs + so, KVB) : make_rsrc(p.hs + so, KVB);
+  // C16: the factors of this chunk's two 64-column tiles (h and dh)
+  float hsc[2] = {1.f, 1.f}, dhsc[2] = {1.f, 1.f};
+  if constexpr (C16) {
+    const int nv = cdiv(V, 64);
+    const size_t fo = ((size_t)gc * H + hh) * nv;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if (t < nv) {
+        hsc[t] = p.hs_scale[fo + t];
+        dhsc[t] = p.dhs_scale[fo + t];
+      }
+    }
+  }
 
   // ---------------- group A's staging registers: thread = (channel ch, rows 8 sg .. 8 sg + 7)
   const int ch = tq & 31, sg = tq >> 5;
@@ -133,9 +148,21 @@ __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
 #pragma unroll
     for (int vc = 0; vc < VC; ++vc) {
       const int v0 = 32 * vc + 8 * lg;
-      const uint32_t o = (kk < K && v0 < V) ? ((uint32_t)kk * V + v0) * 4u : kOOB;
+      const uint32_t o = (kk < K && v0 < V) ? ((uint32_t)kk * V + v0) * (C16 ? 2u : 4u) : kOOB;
       raw[vc][0] = bld128(R, o, 0);
-      raw[vc][1] = bld128(R, o, 16);
+      if constexpr (!C16) raw[vc][1] = bld128(R, o, 16);
+    }
+  };
+  // the lane's 8 state values of value block vc (scaled back for fp16 checkpoints)
+  auto state8 = [&](const uint4 (&raw)[VC][2], int vc, const float* sc, float* x) {
+    if constexpr (C16) {
+      unpack8_f16(raw[vc][0], x);
+      const float f = sc[(32 * vc + 8 * lg) >> 6];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] *= f;
+    } else {
+      unpack4(raw[vc][0], x);
+      unpack4(raw[vc][1], x + 4);
     }
   };
 
@@ -150,7 +177,7 @@ __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
   // dAkk[16t + l16][16J + 4lg + r];  dac[a][J] (J >= t): beta_i dAkk[16J + 4lg + r][16t + l16]
   constexpr int NVW = (NVB + 3) / 4;     // V blocks per B wave
   // ================================================================ channel passes
-  const rsrc_t Rdh = make_rsrc(p.dhs + ((size_t)gc * H + hh) * K * V, KVB);
+  const rsrc_t Rdh = C16 ? make_rsrc((const uint16_t*)p.dhs + so, KVB) : make_rsrc(p.dhs + so, KVB);
   const rsrc_t Rdq = make_rsrc_rows((uint16_t*)p.dq, e0, nrows, K);
   const rsrc_t Rdk = make_rsrc_rows((uint16_t*)p.dk, e0, nrows, K);
   const rsrc_t Rdg = make_rsrc_rows(p.dg, e0, nrows, K);
@@ -297,8 +324,7 @@ __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
       for (int vc = 0; vc < VC; ++vc) {
         const int v0 = 32 * vc + 8 * lg;
         float hv[8];
-        unpack4(hraw[vc][0], hv);
-        unpack4(hraw[vc][1], hv + 4);
+        state8(hraw, vc, hsc, hv);
         uint32_t ah_[4], al_[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) split_bf16x2(al * hv[2 * e], al * hv[2 * e + 1], ah_[e], al_[e]);
@@ -336,10 +362,8 @@ __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
       for (int vc = 0; vc < VC; ++vc) {
         const int v0 = 32 * vc + 8 * lg;
         float hv[8], dv[8];
-        unpack4(hraw[vc][0], hv);
-        unpack4(hraw[vc][1], hv + 4);
-        unpack4(draw[vc][0], dv);
-        unpack4(draw[vc][1], dv + 4);
+        state8(hraw, vc, hsc, hv);
+        state8(draw, vc, dhsc, dv);
         if (rh == 0) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) hd += hv[e] * dv[e];
@@ -601,9 +625,9 @@ __global__ __launch_bounds__(512, 1) void kda_bwd_fused_kernel(KdaBwdParams p) {
       bf16x8 sh[VC], sl[VC];
 #pragma unroll
       for (int vc = 0; vc < VC; ++vc) {
-        float a4[4], b4[4];
-        unpack4(hraw[vc][0], a4);
-        unpack4(hraw[vc][1], b4);
+        float a4[8];
+        state8(hraw, vc, hsc, a4);
+        const float* b4 = a4 + 4;
         uint32_t h4[4], l4[4];
         split_bf16x2(a4[0], a4[1], h4[0], l4[0]);
         split_bf16x2(a4[2], a4[3], h4[1], l4[1]);
@@ -694,7 +718,10 @@ hipError_t launch_kda_bwd_fused(const KdaBwdParams& p, hipStream_t s) {
   const int vp = p.V <= 32 ? 32 : (p.V <= 64 ? 64 : 128);
   dim3 grid(p.total * p.H), block(512);
 #define TOPS_KBF(KPV, VPV) \
-  if (kp == KPV && vp == VPV) { hipLaunchKernelGGL((kda_bwd_fused_kernel<KPV, VPV>), grid, block, 0, s, p); return hipGetLastError(); }
+  if (kp == KPV && vp == VPV) { \
+    if (p.ckpt16) hipLaunchKernelGGL((kda_bwd_fused_kernel<KPV, VPV, true>), grid, block, 0, s, p); \
+    else hipLaunchKernelGGL((kda_bwd_fused_kernel<KPV, VPV, false>), grid, block, 0, s, p); \
+    return hipGetLastError(); }
   TOPS_KBF(32, 32) TOPS_KBF(32, 64) TOPS_KBF(32, 128)
   TOPS_KBF(64, 32) TOPS_KBF(64, 64) TOPS_KBF(64, 128)
   TOPS_KBF(128, 32) TOPS_KBF(128, 64) TOPS_KBF(128, 128)

@@ -453,4 +453,70 @@ __device__ __forceinline__ void acc_slice_t(const rsrc_t& Ro, const rsrc_t& Ra, 
   }
 }
 
+// ---- fp16 state checkpoints (SweepParams::ckpt16).  A sweep workgroup holds the [K, 64]
+// state tile of one (chunk, head, V tile) in MFMA accumulators: wave w's tile i covers rows
+// 16 msb + 4 (lane >> 4) + r (r = 0..3) and column 16 nn + (lane & 15), nn = (w NHT + i) % 4.
+// The checkpoint stores it as fp16 times 2^(14 - e), e the exponent of the tile's largest
+// |S| (so every stored value is below 2^15; fp16's largest normal is 65504), and the factor
+// 2^(e - 14) as one fp32.
+//
+// This wave's largest |S| as fp32 bits (non-negative floats order as their bit patterns):
+// DPP maxima inside each 16-lane row, then the four rows' lane 0 by readlane, all on the VALU
+// (a cross-lane shuffle would queue behind the sweep's LDS traffic); lane 0 writes smx[wave].
+// Call with every lane active.
+template <int NHT>
+__device__ __forceinline__ void state_absmax(const f32x4 (&S)[NHT], uint32_t* smx, int wave,
+                                             int lane) {
+  uint32_t m = 0u;
+#pragma unroll
+  for (int i = 0; i < NHT; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) m = max(m, __float_as_uint(S[i][r]) & 0x7fffffffu);
+  m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xF, 0xF, false));
+  m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xF, 0xF, false));
+  m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x141, 0xF, 0xF, false));
+  m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x140, 0xF, 0xF, false));
+  const uint32_t w = max(max((uint32_t)__builtin_amdgcn_readlane((int)m, 0),
+                             (uint32_t)__builtin_amdgcn_readlane((int)m, 16)),
+                         max((uint32_t)__builtin_amdgcn_readlane((int)m, 32),
+                             (uint32_t)__builtin_amdgcn_readlane((int)m, 48)));
+  if (lane == 0) smx[wave] = w;
+}
+// The checkpoint of this wave's fragment (smx of every wave visible), into the [K, V] fp16
+// slot `base` (row length V) and its factor into *fac (thread 0 of the workgroup).  Lanes
+// 2j, 2j + 1 hold adjacent columns of the same rows: each packs its two rows of a row pair,
+// the pair swap their packs (DPP quad_perm [1,0,3,2]) and v_perm picks the even lane's first
+// row and the odd lane's second, so every store is one 4-byte run of a row.
+template <int NHT, int NW>
+__device__ __forceinline__ void store_state16(const f32x4 (&S)[NHT], const uint32_t* smx,
+                                              uint16_t* base, float* fac, int K, int V, int vt,
+                                              int wave, int msb, int lane, int tid) {
+  uint32_t m = smx[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) m = max(m, smx[w]);
+  int ex = (int)((m >> 23) & 0xffu) - 127;
+  ex = ex < -100 ? -100 : ex;
+  const float sinv = __uint_as_float((uint32_t)(141 - ex) << 23);
+  if (tid == 0) *fac = __uint_as_float((uint32_t)(113 + ex) << 23);
+  const rsrc_t R = make_rsrc(base, (long long)K * V * 2);
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int odd = l16 & 1;
+  const uint32_t sel = odd ? 0x03020706u : 0x05040100u;
+  // rows kr + odd and kr + 2 + odd (kr + 3 < K whenever kr < K: K is a multiple of 8); the
+  // second row pair is a uniform offset of two rows
+  const int kr = 16 * msb + 4 * lg;
+#pragma unroll
+  for (int i = 0; i < NHT; ++i) {
+    const int nn = (wave * NHT + i) % 4;
+    const int vv = vt * 64 + 16 * nn + (l16 & ~1);
+    const uint32_t vo = (kr < K && vv < V) ? ((uint32_t)(kr + odd) * V + vv) * 2u : kOOB;
+#pragma unroll
+    for (int rp = 0; rp < 2; ++rp) {
+      const uint32_t own = pack_f16x2(S[i][2 * rp] * sinv, S[i][2 * rp + 1] * sinv);
+      const uint32_t other = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)own, 0xB1, 0xF, 0xF, false);
+      bst32(R, __builtin_amdgcn_perm(other, own, sel), vo, (uint32_t)(rp * 4 * V));
+    }
+  }
+}
+
 }  // namespace tops

@@ -25,8 +25,8 @@ import numpy as np
 import torch
 
 from ... import _native as N
-from ...utils import CHUNK, ChunkPlan, inference_inputs
-from .._chunk_core import check_qkv
+from ...utils import CHUNK, ChunkPlan, cdiv, checkpoint_layout, inference_inputs
+from .._chunk_core import States16, check_qkv, pack_states, unpack_states
 
 
 def _check(q, k, v, g, beta, initial_state, cu_seqlens):
@@ -39,8 +39,16 @@ def _check(q, k, v, g, beta, initial_state, cu_seqlens):
         raise NotImplementedError(f"tops-hip KDA kernels need V <= 128 (got V={V})")
 
 
+def _c16(q) -> bool:
+    """Whether the training path keeps fp16 state checkpoints (bf16 inputs; the checkpoint
+    layout not "full32"): the states per chunk and dS as fp16 times a power-of-two factor per
+    (chunk, head, 64 columns of V), half the bytes of fp32 ones."""
+    return q.dtype == torch.bfloat16 and checkpoint_layout() != "full32"
+
+
 def _fwd(q, k, v, g32, b32, h0, scale, output_final_state, plan: ChunkPlan, keep: bool):
-    """Returns (o, ht, saved) with saved = (w, tt, v_new, h_ckpt) when keep."""
+    """Returns (o, ht, saved) with saved = (w, tt, v_new, h_ckpt) when keep; h_ckpt is a
+    States16 for fp16 checkpoints."""
     B, T, H, K = q.shape
     V = v.shape[-1]
     dev, f32 = q.device, torch.float32
@@ -50,11 +58,17 @@ def _fwd(q, k, v, g32, b32, h0, scale, output_final_state, plan: ChunkPlan, keep
     w = torch.empty(B, T, H, K, device=dev, dtype=f32)
     tt = torch.empty(plan.total, H, CHUNK, CHUNK, device=dev, dtype=f32) if keep else None
     vn = torch.empty(B, T, H, V, device=dev, dtype=f32) if keep else None
-    hs = torch.empty(plan.total, H, K, V, device=dev, dtype=f32) if keep else None
-    N.call("tops_kda_chunk_fwd", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(g32), N.ptr(b32), N.ptr(h0),
-           N.ptr(o), N.ptr(ht), N.ptr(u), N.ptr(w), N.ptr(tt), N.ptr(vn), N.ptr(hs),
-           N.ptr(plan.cu_dev), N.ptr(plan.offsets_dev), N.ptr(plan.chunk_map_dev), plan.total,
-           B, T, H, K, V, plan.N, N.dtype_code(q.dtype), float(scale), N.stream())
+    tail = (N.ptr(plan.cu_dev), N.ptr(plan.offsets_dev), N.ptr(plan.chunk_map_dev), plan.total,
+            B, T, H, K, V, plan.N, N.dtype_code(q.dtype), float(scale), N.stream())
+    head = (N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(g32), N.ptr(b32), N.ptr(h0), N.ptr(o), N.ptr(ht),
+            N.ptr(u), N.ptr(w), N.ptr(tt), N.ptr(vn))
+    if keep and _c16(q):
+        hs = States16(torch.empty(plan.total, H, K, V, device=dev, dtype=torch.float16),
+                      torch.empty(plan.total, H, cdiv(V, 64), device=dev, dtype=f32))
+        N.call("tops_kda_chunk_fwd_c16", *head, N.ptr(hs.h), N.ptr(hs.scale), *tail)
+    else:
+        hs = torch.empty(plan.total, H, K, V, device=dev, dtype=f32) if keep else None
+        N.call("tops_kda_chunk_fwd", *head, N.ptr(hs), *tail)
     return o, ht, (w, tt, vn, hs)
 
 
@@ -68,8 +82,17 @@ def _bwd(q, k, v, g32, b32, do, dht, saved, scale, plan: ChunkPlan, want_dh0: bo
     dbeta = torch.empty(B, T, H, device=dev, dtype=f32)
     dg = torch.empty(B, T, H, K, device=dev, dtype=f32)
     dh0 = torch.empty(plan.N, H, K, V, device=dev, dtype=f32) if want_dh0 else None
-    dh_work = torch.empty_like(hs)
     dvn_work = torch.empty(plan.total, H, V, CHUNK, device=dev, dtype=f32)
+    tail = (N.ptr(dh0), N.ptr(plan.cu_dev), N.ptr(plan.offsets_dev), N.ptr(plan.chunk_map_dev),
+            plan.total, B, T, H, K, V, plan.N, N.dtype_code(q.dtype), float(scale), N.stream())
+    if isinstance(hs, States16):
+        dh_work = States16(torch.empty_like(hs.h), torch.empty_like(hs.scale))
+        N.call("tops_kda_chunk_bwd_c16", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(g32), N.ptr(b32),
+               N.ptr(w), N.ptr(tt), N.ptr(vn), N.ptr(hs.h), N.ptr(hs.scale), N.ptr(do), N.ptr(dht),
+               N.ptr(dh_work.h), N.ptr(dh_work.scale), N.ptr(dvn_work), N.ptr(dq), N.ptr(dk),
+               N.ptr(dv), N.ptr(dbeta), N.ptr(dg), *tail)
+        return dq, dk, dv, dbeta, dg, dh0
+    dh_work = torch.empty_like(hs)
     # bf16 keeps the WY parts of dk / dg on chip (one kernel); fp32 passes them through HBM
     split = q.dtype == torch.float32
     dk_work = torch.empty(B, T, H, K, device=dev, dtype=f32) if split else None
@@ -77,8 +100,7 @@ def _bwd(q, k, v, g32, b32, do, dht, saved, scale, plan: ChunkPlan, want_dh0: bo
     N.call("tops_kda_chunk_bwd", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(g32), N.ptr(b32), N.ptr(w),
            N.ptr(tt), N.ptr(vn), N.ptr(hs), N.ptr(do), N.ptr(dht), N.ptr(dh_work), N.ptr(dvn_work),
            N.ptr(dk_work), N.ptr(dg_work), N.ptr(dq), N.ptr(dk), N.ptr(dv), N.ptr(dbeta), N.ptr(dg),
-           N.ptr(dh0), N.ptr(plan.cu_dev), N.ptr(plan.offsets_dev), N.ptr(plan.chunk_map_dev),
-           plan.total, B, T, H, K, V, plan.N, N.dtype_code(q.dtype), float(scale), N.stream())
+           *tail)
     return dq, dk, dv, dbeta, dg, dh0
 
 
@@ -93,14 +115,15 @@ class _ChunkKDA(torch.autograd.Function):
         train = any(ctx.needs_input_grad[:5]) or (h0 is not None and ctx.needs_input_grad[6])
         o, ht, saved = _fwd(q, k, v, g32, b32, h032, scale, output_final_state, plan, keep=train)
         if train:
-            ctx.save_for_backward(q, k, v, g32, b32, *saved)
+            ctx.save_for_backward(q, k, v, g32, b32, *saved[:3], *pack_states(saved[3]))
             ctx.plan, ctx.scale = plan, scale
             ctx.dtypes = (g.dtype, beta.dtype, None if h0 is None else h0.dtype)
         return o, ht
 
     @staticmethod
     def backward(ctx, do, dht):
-        q, k, v, g32, b32, w, tt, vn, hs = ctx.saved_tensors
+        q, k, v, g32, b32, w, tt, vn, hs, hsc = ctx.saved_tensors
+        hs = unpack_states(hs, hsc)
         do = do.contiguous().to(q.dtype)
         dht = None if dht is None else dht.contiguous().to(torch.float32)
         g_dt, b_dt, h0_dt = ctx.dtypes

@@ -105,6 +105,7 @@ def test_chunk_kda_fwd_bwd(cfg, dtype, cuda_device):
 def test_kda_forward_stages(dtype, cuda_device):
     """w, T, v_new and the per-chunk states against the oracle's intermediates."""
     from tops.ops.kda.chunk import _fwd
+    from tops.ops._chunk_core import states_fp32
     from tops.utils import ChunkPlan
     B, T, H, K, V = 2, 192, 2, 128, 64
     d = kda_inputs(B, T, H, K, V, seed=5, h0=True)
@@ -113,6 +114,7 @@ def test_kda_forward_stages(dtype, cuda_device):
     scale = K ** -0.5
     plan = ChunkPlan(B, T, None, cuda_device)
     o, ht, (w, tt, vn, hs) = _fwd(q, k, v, g, beta, h0, scale, True, plan, keep=True)
+    hs = states_fp32(hs)          # bf16 inputs keep fp16 checkpoints with tile factors
     torch.cuda.synchronize()
     P = KO.chunk_kda_fwd_parts(seen(d["q"], dtype), seen(d["k"], dtype), seen(d["v"], dtype),
                                d["g"], d["beta"], scale, d["h0"])
