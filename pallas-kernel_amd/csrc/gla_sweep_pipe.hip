@@ -23,12 +23,6 @@
 
 namespace tops {
 
-// make_rsrc_rows for a pointer known to be non-null (no branch in the chunk loop)
-template <typename T>
-__device__ __forceinline__ rsrc_t rows_rsrc(const T* t, size_t e0, long long nrows, int width) {
-  return make_rsrc(t + e0 * (size_t)width, (nrows - (long long)e0) * width * (long long)sizeof(T));
-}
-
 // Keeps the computation of x at this point of the program: the compiler may otherwise sink
 // the staging arithmetic past the barriers to its first use (the plane writes of the next
 // chunk), where nothing overlaps it.
@@ -113,7 +107,6 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
     cbase = n * cdiv(p.T, C);
   }
   const int NTs = cdiv(L, C);
-  const long long nrows = (long long)p.B * p.T * p.H;
 
   // ---- staging coordinates (as gla_sweep_kernel)
   const int hw = tid >> 5;
@@ -153,29 +146,26 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
     uint32_t ry[YR];
   };
   Raw rs;
-  // (a chunk index outside the sequence loads zeros: every row is masked)
+  // The chunk's resources end at its last valid token (chunk_rsrc), so the rows past it load
+  // zeros without a mask; a chunk index outside the sequence has an empty range.
   auto load_chunk = [&](int c) {
     const bool in = c >= 0 && c < NTs;
     if (!in) c = 0;
     const int t0 = c * C;
     const int nval = in ? min(C, L - t0) : 0;
     const size_t e0 = (size_t)(row0 + t0) * H + hh;
-    const rsrc_t Rq = rows_rsrc((const uint16_t*)p.q, e0, nrows, LDK);
-    const rsrc_t Rk = rows_rsrc((const uint16_t*)p.k, e0, nrows, LDK);
-    const rsrc_t Rg = rows_rsrc(p.g, e0, nrows, LDK);
+    const rsrc_t Rq = chunk_rsrc((const uint16_t*)p.q, e0, nval, (int)rowK, LDK);
+    const rsrc_t Rk = chunk_rsrc((const uint16_t*)p.k, e0, nval, (int)rowK, LDK);
+    const rsrc_t Rg = chunk_rsrc(p.g, e0, nval, (int)rowK, LDK);
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
-      const bool ok = r0 + i < nval;
-      rs.rq[i] = bld64(Rq, ok ? offQ : kOOB, i * rowK * ES);
-      rs.rk[i] = bld64(Rk, ok ? offQ : kOOB, i * rowK * ES);
-      rs.rg[i] = bld128(Rg, ok ? offG : kOOB, i * rowK * 4);
+      rs.rq[i] = bld64(Rq, offQ, i * rowK * ES);
+      rs.rk[i] = bld64(Rk, offQ, i * rowK * ES);
+      rs.rg[i] = bld128(Rg, offG, i * rowK * 4);
     }
-    const rsrc_t Ry = rows_rsrc((const uint16_t*)p.y, e0, nrows, V);
+    const rsrc_t Ry = chunk_rsrc((const uint16_t*)p.y, e0, nval, (int)rowV, V);
 #pragma unroll
-    for (int i = 0; i < YR; ++i) {
-      const bool ok = yseg * YR + i < nval;
-      rs.ry[i] = bld32(Ry, ok ? offY : kOOB, i * rowV * ES);
-    }
+    for (int i = 0; i < YR; ++i) rs.ry[i] = bld32(Ry, offY, i * rowV * ES);
   };
   auto cidx = [&](int it) { return REV ? NTs - 1 - it : it; };
 
@@ -472,8 +462,9 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
     }
     const int tok = 16 * R + l16;
     const size_t eo = (size_t)(row0 + t0) * H + hh;
-    const rsrc_t Ro = rows_rsrc((const uint16_t*)p.out, eo, nrows, V);
-    const uint32_t oo = (tok < nval) ? ((uint32_t)tok * rowV + vt * BV + 4 * lg) * ES : kOOB;
+    // (tokens past the chunk's valid rows are outside Ro's range)
+    const rsrc_t Ro = chunk_rsrc((const uint16_t*)p.out, eo, nval, (int)rowV, V);
+    const uint32_t oo = ((uint32_t)tok * rowV + vt * BV + 4 * lg) * ES;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int nn = 2 * nh + j;
@@ -496,8 +487,8 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
         Words<uint16_t>::st4(Ro, acc, v0 < V ? oo : kOOB, (uint32_t)(16 * nn * ES));
       } else {
         // channel slices: the fp32 sum of the slices' outputs
-        const rsrc_t Ra = make_rsrc_rows(p.acc32, eo, nrows, V);
-        const uint32_t fo = (v0 < V && tok < nval) ? ((uint32_t)tok * rowV + v0) * 4u : kOOB;
+        const rsrc_t Ra = chunk_rsrc(p.acc32, eo, nval, (int)rowV, V);
+        const uint32_t fo = (v0 < V) ? ((uint32_t)tok * rowV + v0) * 4u : kOOB;
         acc_slice_t<uint16_t>(Ro, Ra, acc, fo, v0 < V ? oo : kOOB, (uint32_t)(16 * nn * ES),
                               p.acc_mode);
       }

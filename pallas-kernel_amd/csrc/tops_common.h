@@ -297,6 +297,20 @@ __device__ __forceinline__ rsrc_t make_rsrc_rows(const T* t, size_t e0, long lon
   if (t == nullptr) return make_rsrc(nullptr, 0);
   return make_rsrc(t + e0 * (size_t)width, (nrows - (long long)e0) * width * (long long)sizeof(T));
 }
+// Resource over one chunk of one head of a row tensor [.., H, width]: nval token rows of
+// `width` elements, `tstride` elements apart, from row e0 (= token_row * H + head).  The range
+// ends at the end of the last valid token's row, so the rows past the chunk's valid tokens (a
+// ragged tail, the next sequence) fail the hardware check and need no mask of their own;
+// nval <= 0 gives an empty range.
+// (32-bit sizes: a chunk spans less than 2^31 bytes, which the entry points check as
+// kChunk * H * max(K, V) * 4 < 2^31.)
+template <typename T>
+__device__ __forceinline__ rsrc_t chunk_rsrc(const T* t, size_t e0, int nval, int tstride,
+                                             int width) {
+  const int n = (t != nullptr && nval > 0) ? ((nval - 1) * tstride + width) * (int)sizeof(T) : 0;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(t + e0 * (size_t)width), (short)0, n,
+                                           kRsrcFlags);
+}
 __device__ __forceinline__ uint32_t bld32(rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
 }
