@@ -162,12 +162,14 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
   const int t0 = c * C;
   const int nval = present ? min(C, L - t0) : 0;
   const size_t e0 = (size_t)(row0 + t0) * H + hh;
-  const long long nrows = (long long)p.B * p.T * H;     // (token, head) rows of [B,T,H,.]
   const uint32_t rowK = (uint32_t)(H * LDK), rowV = (uint32_t)(H * LDV);
-  const rsrc_t Rq = make_rsrc_rows((const TIn*)p.q, e0, nrows, LDK);
-  const rsrc_t Rk = make_rsrc_rows((const TIn*)p.k, e0, nrows, LDK);
+  // chunk-bounded resources (chunk_rsrc): the tokens past nval are out of range, so the
+  // row loads and stores below carry no token mask
+  const rsrc_t Rq = chunk_rsrc((const TIn*)p.q, e0, nval, (int)rowK, LDK);
+  const rsrc_t Rk = chunk_rsrc((const TIn*)p.k, e0, nval, (int)rowK, LDK);
   const int gmode = GK ? kGateK : p.gate_mode;
-  const rsrc_t Rg = make_rsrc_rows(p.g, e0, nrows, gmode == kGateK ? LDK : 1);
+  const rsrc_t Rg = gmode == kGateK ? chunk_rsrc(p.g, e0, nval, (int)rowK, LDK)
+                                    : chunk_rsrc(p.g, e0, nval, H, 1);
   const float gam_h = gmode == kGateGamma ? p.g[hh] : 0.f;
   // kGateGammaK: this thread's constant of every pass (channel ps * KH + ch), read up front
   // through a range that is empty in the other modes.  The load is issued on every path: a
@@ -186,18 +188,18 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
 
   // ---------------- v / dO planes ([C][V], V contiguous)
   {
-    const rsrc_t Rv = make_rsrc_rows((const TV*)p.v, e0, nrows, LDV);
-    const rsrc_t Rd = make_rsrc_rows((const TIn*)p.dout, e0, nrows, LDV);
+    const rsrc_t Rv = chunk_rsrc((const TV*)p.v, e0, nval, (int)rowV, LDV);
+    const rsrc_t Rd = chunk_rsrc((const TIn*)p.dout, e0, nval, (int)rowV, LDV);
     uint4 pv[NPTV], pd[NPT];
 #pragma unroll
     for (int i = 0; i < NPTV; ++i) {
       const int pc = tq + 256 * i, row = pc / NPCV, col = (pc % NPCV) * EPV;
-      pv[i] = bld128(Rv, (row < nval && col < V) ? ((uint32_t)row * rowV + col) * ESV : kOOB, 0);
+      pv[i] = bld128(Rv, col < V ? ((uint32_t)row * rowV + col) * ESV : kOOB, 0);
     }
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
       const int pc = tq + 256 * i, row = pc / NPC, col = (pc % NPC) * EP;
-      pd[i] = bld128(Rd, (row < nval && col < V) ? ((uint32_t)row * rowV + col) * ES : kOOB, 0);
+      pd[i] = bld128(Rd, col < V ? ((uint32_t)row * rowV + col) * ES : kOOB, 0);
     }
 #pragma unroll
     for (int i = 0; i < NPTV; ++i) {
@@ -235,7 +237,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
   if constexpr (RG) {
     if (tq < C) {
       float x = 0.f;
-      if (gmode == kGateS) x = __uint_as_float(bld32(Rg, tq < nval ? (uint32_t)tq * H * 4u : kOOB, 0));
+      if (gmode == kGateS) x = __uint_as_float(bld32(Rg, (uint32_t)tq * H * 4u, 0));
       else x = tq < nval ? gam_h : 0.f;
       x *= kLog2e;
 #pragma unroll
@@ -273,7 +275,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int r = 8 * sg + i;
-      const bool v_ = ok && r < nval;
+      const bool v_ = ok;                 // rows past nval: out of the chunk's range
       const uint32_t off = (uint32_t)r * rowK + kc;
       if constexpr (SIN && !F16) {
         rq[i] = bld32(Rq, v_ ? off * 4u : kOOB, 0);
@@ -396,14 +398,16 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
       unpack4(raw[vc][1], x + 4);
     }
   };
-  const rsrc_t Rdq = make_rsrc_rows((const TIn*)p.dq, e0, nrows, LDK);
-  const rsrc_t Rdk = make_rsrc_rows((const TIn*)p.dk, e0, nrows, LDK);
-  const rsrc_t Rdka = make_rsrc_rows(p.dk_add, e0, nrows, LDK);
-  const rsrc_t Rdga = make_rsrc_rows(p.dg_add, e0, nrows, LDK);
-  const rsrc_t Rdg = make_rsrc_rows(gmode == kGateGamma ? nullptr : p.dg, e0, nrows, gmode == kGateS ? 1 : LDK);
+  const rsrc_t Rdq = chunk_rsrc((const TIn*)p.dq, e0, nval, (int)rowK, LDK);
+  const rsrc_t Rdk = chunk_rsrc((const TIn*)p.dk, e0, nval, (int)rowK, LDK);
+  const rsrc_t Rdka = chunk_rsrc(p.dk_add, e0, nval, (int)rowK, LDK);
+  const rsrc_t Rdga = chunk_rsrc(p.dg_add, e0, nval, (int)rowK, LDK);
+  const rsrc_t Rdg = gmode == kGateS ? chunk_rsrc(p.dg, e0, nval, H, 1)
+                                     : chunk_rsrc(gmode == kGateGamma ? nullptr : p.dg, e0, nval,
+                                                  (int)rowK, LDK);
   // value slices: fp32 sums of dq / dk over the slices (acc_mode 1..3)
-  const rsrc_t Rdq32 = make_rsrc_rows(p.dq32, e0, nrows, LDK);
-  const rsrc_t Rdk32 = make_rsrc_rows(p.dk32, e0, nrows, LDK);
+  const rsrc_t Rdq32 = chunk_rsrc(p.dq32, e0, nval, (int)rowK, LDK);
+  const rsrc_t Rdk32 = chunk_rsrc(p.dk32, e0, nval, (int)rowK, LDK);
   if (kScalarGate && tq < 2 * C) gDgS[tq] = 0.f;
 
   // ---- the h / dh rows of a pass: a lane's 8 values of state row kk = 32 ps + 16 kb + l16,
@@ -625,7 +629,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
       for (int a = 0; a < 2; ++a) {
         const int tok = 16 * (2 * rh + a) + l16;
         const int kc = cb + 16 * kb + 4 * lg;
-        const uint32_t o = (kc < K && tok < nval) ? ((uint32_t)tok * rowK + kc) * 4u : kOOB;
+        const uint32_t o = kc < K ? ((uint32_t)tok * rowK + kc) * 4u : kOOB;
         kadd[a] = bld128(Rdka, o, 0);
         gadd[a] = bld128(Rdga, o, 0);
       }
@@ -676,7 +680,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
 #pragma unroll
     for (int a = 0; a < 2; ++a) {
       const int tok = 16 * (2 * rh + a) + l16;
-      const bool ok = chok && tok < nval;
+      const bool ok = chok;                 // tokens past nval: out of the chunk's range
       const uint32_t off = (uint32_t)tok * rowK + kc;
       float gr[4];
       if constexpr (RG) {
@@ -749,7 +753,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
         const int tok = 16 * (2 * rh + a) + l16;
-        const bool ok = chok && tok < nval;
+        const bool ok = chok;               // tokens past nval: out of the chunk's range
         const uint32_t off = (uint32_t)tok * rowK + kc;
         float ga[4] = {0.f, 0.f, 0.f, 0.f};
         if constexpr (kEarlyAdd) unpack4(gadd[a], ga);
@@ -778,7 +782,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
     __syncthreads();
     if (tq < C) {
       float x = gDgS[tq] + gDgS[C + tq];
-      const uint32_t o = tq < nval ? (uint32_t)tq * H * 4u : kOOB;
+      const uint32_t o = (uint32_t)tq * H * 4u;   // tokens past nval: out of Rdg's range
       if (p.dg_accum) x += __uint_as_float(bld32(Rdg, o, 0));   // earlier slices
       bst32(Rdg, __float_as_uint(x), o, 0);
     }

@@ -174,7 +174,6 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     cbase = n * cdiv(p.T, C);
   }
   const int NTs = cdiv(L, C);                          // 0 for an empty sequence
-  const long long nrows = (long long)p.B * p.T * p.H;  // (token, head) rows of [B,T,H,.]
 
   // ---- staging coordinates and per-thread byte offsets within a chunk
   const int hw = tid >> 5;               // half-wave
@@ -266,26 +265,28 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     const int t0 = c * C;
     const int nval = min(C, L - t0);
     const size_t e0 = (size_t)(row0 + t0) * H + hh;     // first row of the chunk, this head
-    const rsrc_t Rq = make_rsrc_rows((const TIn*)p.q, e0, nrows, LDK);
-    const rsrc_t Rk = make_rsrc_rows((const TIn*)p.k, e0, nrows, LDK);
+    // chunk-bounded resources (chunk_rsrc): rows past the chunk's nval tokens load zeros
+    const rsrc_t Rq = chunk_rsrc((const TIn*)p.q, e0, nval, (int)rowK, LDK);
+    const rsrc_t Rk = chunk_rsrc((const TIn*)p.k, e0, nval, (int)rowK, LDK);
     // gshift: token t reads the gate row of token t - 1, so the rows start one token earlier,
     // except in the sequence's first chunk, whose row 0 reads nothing (gate 0)
     const int gadj = (gsh && t0 == 0) ? 1 : 0;
     const size_t eg = gsh && t0 > 0 ? e0 - (size_t)H : e0;
-    const rsrc_t Rg = make_rsrc_rows(p.g, eg, nrows, gk_mode ? LDK : 1);
+    const rsrc_t Rg = gk_mode ? chunk_rsrc(p.g, eg, nval, (int)rowK, LDK)
+                              : chunk_rsrc(p.g, eg, nval, H, 1);
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
-      const bool ok = r0 + i < nval;
-      rs.rq[i] = Wd::ld4(Rq, ok ? offQ : kOOB, i * rowK * ES);
-      rs.rk[i] = Wd::ld4(Rk, ok ? offQ : kOOB, i * rowK * ES);
+      rs.rq[i] = Wd::ld4(Rq, offQ, i * rowK * ES);
+      rs.rk[i] = Wd::ld4(Rk, offQ, i * rowK * ES);
       // the gate mode's transform is applied when the chunk is consumed, so the prefetch
       // never waits: four channels [.., K], or the one per-(token, head) word [.., 1]
       // (gamma: offGm is out of range, nothing is read)
-      uint32_t go = (ok && !GV) ? offGm : kOOB, gs = i * gstride;
+      uint32_t go = !GV ? offGm : kOOB, gs = i * gstride;
       if constexpr (RSH) {
         // row r0 + i - gadj (>= 0 where read), as one vector offset; masked columns and the
-        // constant gates (offGm out of range) read nothing
-        const bool rd = ok && r0 + i >= gadj && offGm != kOOB;
+        // constant gates (offGm out of range) read nothing.  The token mask stays: shifted by
+        // one row, the gate row of the first token past nval is still inside Rg's range
+        const bool rd = r0 + i < nval && r0 + i >= gadj && offGm != kOOB;
         go = rd ? offGm + (uint32_t)(i - gadj) * gstride : kOOB;
         gs = 0;
       }
@@ -295,25 +296,19 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       else rs.rg[i] = make_uint4(bld32(Rg, go, gs), 0u, 0u, 0u);
     }
     if constexpr (!FWD_DELTA) {
-      const rsrc_t Ry = make_rsrc_rows((const TIn*)p.y, e0, nrows, V);
+      const rsrc_t Ry = chunk_rsrc((const TIn*)p.y, e0, nval, (int)rowV, V);
 #pragma unroll
-      for (int i = 0; i < YR; ++i) {
-        const bool ok = yseg * YR + i < nval;
-        rs.ry[i] = Wd::ld2(Ry, ok ? offY : kOOB, i * rowV * ES);
-      }
+      for (int i = 0; i < YR; ++i) rs.ry[i] = Wd::ld2(Ry, offY, i * rowV * ES);
       if constexpr (YG == 1) {
-        const rsrc_t Rgv = make_rsrc_rows(p.g, e0, nrows, V);
+        const rsrc_t Rgv = chunk_rsrc(p.g, e0, nval, (int)rowV, V);
 #pragma unroll
-        for (int i = 0; i < YR; ++i) {
-          const bool ok = yseg * YR + i < nval;
-          rs.rgv[i] = bld64(Rgv, ok ? offYg : kOOB, i * rowV * 4);
-        }
+        for (int i = 0; i < YR; ++i) rs.rgv[i] = bld64(Rgv, offYg, i * rowV * 4);
       } else if constexpr (YG == 2) {
         // one word per row (the constant gate reads nothing: out of range)
-        const rsrc_t Rgs = make_rsrc_rows(p.g, e0, nrows, 1);
+        const rsrc_t Rgs = chunk_rsrc(p.g, e0, nval, H, 1);
 #pragma unroll
         for (int i = 0; i < YR; ++i) {
-          const bool ok = yseg * YR + i < nval && yg_s;
+          const bool ok = yg_s;
           const uint32_t w = bld32(Rgs, ok ? (uint32_t)(yseg * YR) * H * 4u : kOOB, i * H * 4);
           rs.rgv[i] = make_uint2(w, w);
         }
@@ -342,13 +337,13 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     float ur[2][4];
     auto load_wu = [&]() {
       const size_t e0 = (size_t)(row0 + t0) * H + hh;
-      const rsrc_t Rw = make_rsrc_rows(p.w, e0, nrows, LDK);
-      const rsrc_t Ru = make_rsrc_rows(p.u, e0, nrows, V);
+      const rsrc_t Rw = chunk_rsrc(p.w, e0, nval, (int)rowK, LDK);
+      const rsrc_t Ru = chunk_rsrc(p.u, e0, nval, (int)rowV, V);
       const int trow = 16 * R + l16;
 #pragma unroll
       for (int kc = 0; kc < KP / 32; ++kc) {
         const int k0 = 32 * kc + 8 * lg;
-        const uint32_t o = (trow < nval && k0 < K) ? ((uint32_t)trow * rowK + k0) * 4u : kOOB;
+        const uint32_t o = k0 < K ? ((uint32_t)trow * rowK + k0) * 4u : kOOB;
         wraw[kc][0] = bld128(Rw, o, 0);
         wraw[kc][1] = bld128(Rw, o == kOOB ? kOOB : o + 16u, 0);
       }
@@ -358,7 +353,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int tok = 16 * R + 4 * lg + r;
-          ur[j][r] = __uint_as_float(bld32(Ru, (tok < nval && vv < V) ? ((uint32_t)tok * rowV + vv) * 4u : kOOB, 0));
+          ur[j][r] = __uint_as_float(bld32(Ru, vv < V ? ((uint32_t)tok * rowV + vv) * 4u : kOOB, 0));
         }
       }
     };
@@ -368,10 +363,10 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     float4 rw[RPT];
     if constexpr (REV_DELTA) {
       const size_t e0 = (size_t)(row0 + t0) * H + hh;
-      const rsrc_t Rw = make_rsrc_rows(p.w, e0, nrows, LDK);
+      const rsrc_t Rw = chunk_rsrc(p.w, e0, nval, (int)rowK, LDK);
 #pragma unroll
       for (int i = 0; i < RPT; ++i) {
-        const uint4 x = bld128(Rw, r0 + i < nval ? offG : kOOB, i * rowK * 4);
+        const uint4 x = bld128(Rw, offG, i * rowK * 4);
         rw[i] = make_float4(__uint_as_float(x.x), __uint_as_float(x.y), __uint_as_float(x.z),
                             __uint_as_float(x.w));
       }
@@ -826,9 +821,9 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       // v_new = u - w S for (token block R, column tiles 2nh, 2nh+1).  The A operand
       // w 2^-Gm is read straight from HBM in the MFMA row layout (against H^T = 2^Gm S).
       const size_t e0 = (size_t)(row0 + t0) * H + hh;
-      const rsrc_t Rvn = make_rsrc_rows(p.y32, e0, nrows, V);
-      const rsrc_t Rw = make_rsrc_rows(p.w, e0, nrows, LDK);
-      const rsrc_t Ru = make_rsrc_rows(p.u, e0, nrows, V);
+      const rsrc_t Rvn = chunk_rsrc(p.y32, e0, nval, (int)rowV, V);
+      const rsrc_t Rw = chunk_rsrc(p.w, e0, nval, (int)rowK, LDK);
+      const rsrc_t Ru = chunk_rsrc(p.u, e0, nval, (int)rowV, V);
       bf16x8 wh[KP / 32], wl[KP / 32];
 #pragma unroll
       for (int kc = 0; kc < KP / 32; ++kc) {
@@ -839,7 +834,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
           unpack4(wraw[kc][1], a + 4);
         } else {
           const int trow = 16 * R + l16;
-          const uint32_t o = (trow < nval && k0 < K) ? ((uint32_t)trow * rowK + k0) * 4u : kOOB;
+          const uint32_t o = k0 < K ? ((uint32_t)trow * rowK + k0) * 4u : kOOB;
           unpack4(bld128(Rw, o, 0), a);
           unpack4(bld128(Rw, o == kOOB ? kOOB : o + 16u, 0), a + 4);
         }
@@ -865,7 +860,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int tok = 16 * R + 4 * lg + r;
-          const uint32_t o = (tok < nval && vv < V) ? ((uint32_t)tok * rowV + vv) * 4u : kOOB;
+          const uint32_t o = vv < V ? ((uint32_t)tok * rowV + vv) * 4u : kOOB;
           vn[r] = (HOIST ? ur[j][r] : __uint_as_float(bld32(Ru, o, 0))) - acc[r];
           bst32(Rvn, __float_as_uint(vn[r]), o, 0);
         }
@@ -929,8 +924,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
       // out^T tiles (nn, R); lane writes out[token 16R + l16][v = 16 nn + 4 lg + 0..3]
       const int tok = 16 * R + l16;
       const size_t eo = (size_t)(row0 + t0) * H + hh;
-      const rsrc_t Ro = make_rsrc_rows((const TIn*)p.out, eo, nrows, V);
-      const uint32_t oo = (tok < nval) ? ((uint32_t)tok * rowV + vt * BV + 4 * lg) * ES : kOOB;
+      const rsrc_t Ro = chunk_rsrc((const TIn*)p.out, eo, nval, (int)rowV, V);
+      const uint32_t oo = ((uint32_t)tok * rowV + vt * BV + 4 * lg) * ES;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int nn = 2 * nh + j;
@@ -964,8 +959,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
           Wd::st4(Ro, acc, v0 < V ? oo : kOOB, (uint32_t)(16 * nn * ES));
         } else {
           // channel slices: the fp32 sum of the slices' outputs (element offset as oo's)
-          const rsrc_t Ra = make_rsrc_rows(p.acc32, eo, nrows, V);
-          const uint32_t fo = (v0 < V && tok < nval) ? ((uint32_t)tok * rowV + v0) * 4u : kOOB;
+          const rsrc_t Ra = chunk_rsrc(p.acc32, eo, nval, (int)rowV, V);
+          const uint32_t fo = (v0 < V) ? ((uint32_t)tok * rowV + v0) * 4u : kOOB;
           acc_slice_t<TIn>(Ro, Ra, acc, fo, v0 < V ? oo : kOOB, (uint32_t)(16 * nn * ES), p.acc_mode);
         }
       }
