@@ -400,14 +400,17 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
   };
   const rsrc_t Rdq = chunk_rsrc((const TIn*)p.dq, e0, nval, (int)rowK, LDK);
   const rsrc_t Rdk = chunk_rsrc((const TIn*)p.dk, e0, nval, (int)rowK, LDK);
-  const rsrc_t Rdka = chunk_rsrc(p.dk_add, e0, nval, (int)rowK, LDK);
-  const rsrc_t Rdga = chunk_rsrc(p.dg_add, e0, nval, (int)rowK, LDK);
+  // C16 calls take no slices and no WY parts (the launcher checks): their instance compiles
+  // without those paths, and without the resources below
+  constexpr bool kSlices = !C16;
+  const rsrc_t Rdka = chunk_rsrc(kSlices ? p.dk_add : nullptr, e0, nval, (int)rowK, LDK);
+  const rsrc_t Rdga = chunk_rsrc(kSlices ? p.dg_add : nullptr, e0, nval, (int)rowK, LDK);
   const rsrc_t Rdg = gmode == kGateS ? chunk_rsrc(p.dg, e0, nval, H, 1)
                                      : chunk_rsrc(gmode == kGateGamma ? nullptr : p.dg, e0, nval,
                                                   (int)rowK, LDK);
   // value slices: fp32 sums of dq / dk over the slices (acc_mode 1..3)
-  const rsrc_t Rdq32 = chunk_rsrc(p.dq32, e0, nval, (int)rowK, LDK);
-  const rsrc_t Rdk32 = chunk_rsrc(p.dk32, e0, nval, (int)rowK, LDK);
+  const rsrc_t Rdq32 = chunk_rsrc(kSlices ? p.dq32 : nullptr, e0, nval, (int)rowK, LDK);
+  const rsrc_t Rdk32 = chunk_rsrc(kSlices ? p.dk32 : nullptr, e0, nval, (int)rowK, LDK);
   if (kScalarGate && tq < 2 * C) gDgS[tq] = 0.f;
 
   // ---- the h / dh rows of a pass: a lane's 8 values of state row kk = 32 ps + 16 kb + l16,
@@ -715,14 +718,14 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
           }
         }
       }
-      if (kEarlyAdd || p.dk_add) {
+      if (kEarlyAdd || (kSlices && p.dk_add)) {
         float ka[4];
         if constexpr (kEarlyAdd) unpack4(kadd[a], ka);
         else unpack4(bld128(Rdka, ok ? off * 4u : kOOB, 0), ka);
 #pragma unroll
         for (int r = 0; r < 4; ++r) dkv[r] += ka[r];
       }
-      if (p.acc_mode == 0) {
+      if (!kSlices || p.acc_mode == 0) {
         Wd::st4(Rdq, dqv, ok ? off * ES : kOOB, 0);
         Wd::st4(Rdk, dkv, ok ? off * ES : kOOB, 0);
       } else {
@@ -757,8 +760,8 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
         const uint32_t off = (uint32_t)tok * rowK + kc;
         float ga[4] = {0.f, 0.f, 0.f, 0.f};
         if constexpr (kEarlyAdd) unpack4(gadd[a], ga);
-        else if (p.dg_add) unpack4(bld128(Rdga, ok ? off * 4u : kOOB, 0), ga);
-        else if (p.dg_accum) unpack4(bld128(Rdg, ok ? off * 4u : kOOB, 0), ga);   // earlier slices
+        else if (kSlices && p.dg_add) unpack4(bld128(Rdga, ok ? off * 4u : kOOB, 0), ga);
+        else if (kSlices && p.dg_accum) unpack4(bld128(Rdg, ok ? off * 4u : kOOB, 0), ga);   // earlier slices
         bst128(Rdg, make_uint4(__float_as_uint(dgr[a][0] + add[0] + ga[0]), __float_as_uint(dgr[a][1] + add[1] + ga[1]),
                                __float_as_uint(dgr[a][2] + add[2] + ga[2]), __float_as_uint(dgr[a][3] + add[3] + ga[3])),
                ok ? off * 4u : kOOB, 0);
@@ -783,7 +786,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
     if (tq < C) {
       float x = gDgS[tq] + gDgS[C + tq];
       const uint32_t o = (uint32_t)tq * H * 4u;   // tokens past nval: out of Rdg's range
-      if (p.dg_accum) x += __uint_as_float(bld32(Rdg, o, 0));   // earlier slices
+      if (kSlices && p.dg_accum) x += __uint_as_float(bld32(Rdg, o, 0));   // earlier slices
       bst32(Rdg, __float_as_uint(x), o, 0);
     }
   }
@@ -811,7 +814,9 @@ hipError_t launch_gla_dqkg(const DqkgParams& p, hipStream_t s) {
   const bool gk = !kAllModes || p.gate_mode == kGateK;
   if (p.paired && !kPairs) return hipErrorInvalidValue;
   const dim3 pgrid(((p.total + 1) / 2) * p.H), pblock(512);
-  if (p.ckpt16 && (!kPairs || !gk || p.paired)) return hipErrorInvalidValue;
+  if (p.ckpt16 && (!kPairs || !gk || p.paired || p.acc_mode || p.dg_accum || p.dk_add || p.dg_add ||
+                   p.ldk || p.ldv))
+    return hipErrorInvalidValue;
 #define TOPS_DQKG(KPV, VPV)                                                                   \
   if (kp == KPV && vp == VPV) {                                                               \
     if constexpr (kPairs) {                                                                   \
