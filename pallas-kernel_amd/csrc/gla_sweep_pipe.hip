@@ -29,7 +29,11 @@ namespace tops {
 __device__ __forceinline__ void pin(uint32_t& x) { asm volatile("" : "+v"(x)); }
 __device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
 
-template <int KP, bool REV>
+// VAR selects the features an instance compiles: 1 = training with fp16 checkpoints (every
+// chunk, whole-width rows, no slices), 2 = no checkpoints and no slices (inference), 0 = the
+// rest (fp32 or paired checkpoints, channel slices).  Fewer live values keep the scalar
+// registers from spilling into VGPR lanes.
+template <int KP, bool REV, int VAR>
 __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
   constexpr int NW = 8;
   constexpr int NTH = 64 * NW;
@@ -93,7 +97,8 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
   }
   n = __builtin_amdgcn_readfirstlane(n);
   const int H = p.H, K = p.K, V = p.V;
-  const int LDK = p.ldk > 0 ? p.ldk : K;   // row length of q / k / g and of the state rows
+  // row length of q / k / g and of the state rows
+  const int LDK = (VAR == 0 && p.ldk > 0) ? p.ldk : K;
   const float scale = p.scale;
 
   int L, row0, cbase;
@@ -306,13 +311,15 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
   // phase, which measured fastest of the placements tried: there, at the end of that phase,
   // and after the output products)
   auto ckpt_on = [&](int c) {
+    if constexpr (VAR == 1) return true;
+    if constexpr (VAR == 2) return false;
     return p.ckpt && (p.ckpt_par == 0 || ((cbase + c) & 1) == p.ckpt_par - 1);
   };
   // fp16 checkpoints: this wave's largest |S| into sMx (between B1 and B2; read after B2)
   auto ckpt_max = [&]() { state_absmax<NHT>(S, sMx, wave, lane); };
   auto store_ckpt = [&](int c) {
     if (!ckpt_on(c)) return;
-    if (p.ckpt16) {
+    if constexpr (VAR == 1) {
       store_state16<NHT, NW>(S, sMx, (uint16_t*)p.ckpt + ((size_t)(cbase + c) * H + hh) * LDK * V,
                              p.ckpt_scale + ((size_t)(cbase + c) * H + hh) * p.NV + vt, K, V, vt,
                              wave, msb, lane, tid);
@@ -348,7 +355,7 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
 
     __syncthreads();  // B1: the previous chunk's planes and the totals are no longer read
     write_planes();
-    if (p.ckpt16 && ckpt_on(c)) ckpt_max();
+    if constexpr (VAR == 1) ckpt_max();
     // the state factors of this chunk, kept for its update (stage() overwrites them)
     float cga[4], cbe[4];
 #pragma unroll
@@ -483,7 +490,7 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
         }
       }
       const int v0 = vt * BV + 16 * nn + 4 * lg;
-      if (p.acc_mode == 0) {
+      if (VAR != 0 || p.acc_mode == 0) {
         Words<uint16_t>::st4(Ro, acc, v0 < V ? oo : kOOB, (uint32_t)(16 * nn * ES));
       } else {
         // channel slices: the fp32 sum of the slices' outputs
@@ -523,10 +530,18 @@ bool gla_pipe_eligible(const SweepParams& p) {
 template <bool REV>
 hipError_t launch_gla_pipe(const SweepParams& p, hipStream_t s) {
   const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
+  const bool plain = !p.acc_mode && !p.ldk;
+  if (p.ckpt16 && (!plain || p.ckpt_par || !p.ckpt || !p.ckpt_scale)) return hipErrorInvalidValue;
+  const int var = p.ckpt16 ? 1 : ((plain && !p.ckpt) ? 2 : 0);
   dim3 grid(p.NV * p.H * p.N);
-  if (kp == 32) hipLaunchKernelGGL((gla_pipe_kernel<32, REV>), grid, dim3(512), 0, s, p);
-  else if (kp == 64) hipLaunchKernelGGL((gla_pipe_kernel<64, REV>), grid, dim3(512), 0, s, p);
-  else hipLaunchKernelGGL((gla_pipe_kernel<128, REV>), grid, dim3(512), 0, s, p);
+#define TOPS_PIPE(KPV, VARV) hipLaunchKernelGGL((gla_pipe_kernel<KPV, REV, VARV>), grid, dim3(512), 0, s, p)
+#define TOPS_PIPE_K(KPV) \
+  if (var == 1) TOPS_PIPE(KPV, 1); else if (var == 2) TOPS_PIPE(KPV, 2); else TOPS_PIPE(KPV, 0)
+  if (kp == 32) { TOPS_PIPE_K(32); }
+  else if (kp == 64) { TOPS_PIPE_K(64); }
+  else { TOPS_PIPE_K(128); }
+#undef TOPS_PIPE_K
+#undef TOPS_PIPE
   return hipGetLastError();
 }
 

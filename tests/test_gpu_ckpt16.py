@@ -5,8 +5,10 @@ The default checkpoint layout of chunk_gla training on bf16 inputs with per-chan
 keeps h (forward) and dh (reverse sweep) as fp16 times a power-of-two factor per (chunk,
 head, 64 columns of V); set_checkpoint_layout("full32") keeps them as fp32.  Only the
 dq / dk / dg kernel reads the checkpoints, so
-  * o, ht (forward) and dv, dh0 (reverse sweep) are bitwise those of the fp32 layout: the
-    sweeps compute in fp32 either way and only the stored copies differ;
+  * o, ht (forward) and dv, dh0 (reverse sweep) equal those of the fp32 layout up to fp32
+    contraction: the sweeps compute in fp32 either way and only the stored copies differ, but
+    the two layouts run separately compiled kernel instances, whose fused multiply-adds may
+    differ (relative L2 <= 1e-5 for fp32 outputs, <= 1e-3 for bf16 ones: one-ulp flips);
   * dq, dk, dg are within the north-star bf16 tolerance of the oracle (2e-3 relative L2,
     tops/ops/gla/chunk.py:1103-1199 forward and :1447-1509 backward), and within 2e-3 of
     the fp32 layout (fp16 keeps 11 significant bits of each scaled state; the factor keeps
@@ -77,7 +79,9 @@ def test_ckpt16_vs_fp32_and_oracle(cfg, cuda_device):
     _, b = _run(cfg, cuda_device, "full32")
     for name in ("o", "ht", "dv", "dh0"):
         if a[name] is not None:
-            assert torch.equal(a[name], b[name]), f"{name}: differs from the fp32 layout"
+            lim = 1e-3 if a[name].dtype == torch.bfloat16 else 1e-5
+            e = rel(host(a[name]), host(b[name]))
+            assert e <= lim, f"{name}: differs from the fp32 layout by {e:.3e}"
     bf = torch.bfloat16
     big = cfg["T"] > 4096
     if not big:
