@@ -62,7 +62,10 @@ namespace tops {
 // GK: the per-channel gate mode only (kGateK, the GLA and KDA path), compiled on its own so
 // that the hot path carries no gate-mode branches; !GK serves the per-token and constant
 // gates (kGateS, kGateGamma, kGateGammaK) chosen at run time.
-template <typename TIn, int KP, bool REV, bool DELTA, bool ST, bool GK, int YG = 0>
+// VAR selects the features an instance compiles (as in gla_sweep_pipe.hip): 1 = fp16
+// checkpoints of every chunk, whole-width rows, no slices; 2 = no checkpoints and no slices;
+// 0 = the rest (fp32 or paired checkpoints, channel slices; no fp16 checkpoints).
+template <typename TIn, int KP, bool REV, bool DELTA, bool ST, bool GK, int YG = 0, int VAR = 0>
 __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   constexpr int NW = 8;                  // wave64s per workgroup
   constexpr int NTH = 64 * NW;
@@ -160,7 +163,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   }
   n = __builtin_amdgcn_readfirstlane(n);
   const int H = p.H, K = p.K, V = p.V;
-  const int LDK = p.ldk > 0 ? p.ldk : K;   // row length of q / k / g and of the state rows
+  // row length of q / k / g and of the state rows
+  const int LDK = (VAR == 0 && p.ldk > 0) ? p.ldk : K;
   const float scale = p.scale;
 
   int L, row0, cbase;
@@ -508,10 +512,10 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     // staging: stored after the next chunk's prefetch instead, the checkpoints measured
     // slower (the memory counter retires in issue order, so the waits for the prefetched
     // loads at the top of the next chunk then also cover the stores).
-    if constexpr (!ST) {
-      if (p.ckpt16) {
-        state_absmax<NHT>(S, sMx, wave, lane);   // the tile maximum is read after B2
-      } else if (p.ckpt && (p.ckpt_par == 0 || ((cbase + c) & 1) == p.ckpt_par - 1)) {
+    if constexpr (!ST && VAR == 1) {
+      state_absmax<NHT>(S, sMx, wave, lane);   // the tile maximum is read after B2
+    } else if constexpr (!ST && VAR == 0) {
+      if (p.ckpt && (p.ckpt_par == 0 || ((cbase + c) & 1) == p.ckpt_par - 1)) {
         const rsrc_t Rck = make_rsrc(p.ckpt + ((size_t)(cbase + c) * H + hh) * LDK * V,
                                      (long long)K * V * 4);
 #pragma unroll
@@ -607,12 +611,10 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 
     // fp16 checkpoint of S, from the wave maxima taken before B2 (stored ahead of the
     // prefetch below: the memory counter retires in issue order)
-    if constexpr (!ST) {
-      if (p.ckpt16)
-        store_state16<NHT, NW>(S, sMx, (uint16_t*)p.ckpt + ((size_t)(cbase + c) * H + hh) * LDK * V,
-                               p.ckpt_scale + ((size_t)(cbase + c) * H + hh) * p.NV + vt, K, V,
-                               vt, wave, msb, lane, tid);
-    }
+    if constexpr (!ST && VAR == 1)
+      store_state16<NHT, NW>(S, sMx, (uint16_t*)p.ckpt + ((size_t)(cbase + c) * H + hh) * LDK * V,
+                             p.ckpt_scale + ((size_t)(cbase + c) * H + hh) * p.NV + vt, K, V,
+                             vt, wave, msb, lane, tid);
 
     // ---------------- prefetch the chunk PF steps ahead while this one is computed
     if (it + PF < NTs) load_chunk(cidx(it + PF), rs);
@@ -955,7 +957,7 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
           acc[0] *= e4.x; acc[1] *= e4.y; acc[2] *= e4.z; acc[3] *= e4.w;
         }
         const int v0 = vt * BV + 16 * nn + 4 * lg;
-        if (p.acc_mode == 0) {
+        if (VAR != 0 || p.acc_mode == 0) {
           Wd::st4(Ro, acc, v0 < V ? oo : kOOB, (uint32_t)(16 * nn * ES));
         } else {
           // channel slices: the fp32 sum of the slices' outputs (element offset as oo's)
@@ -1009,17 +1011,30 @@ hipError_t launch_gla_sweep(const SweepParams& p, hipStream_t s) {
   if constexpr (std::is_same<TIn, uint16_t>::value && !DELTA) {
     if (gla_pipe_eligible(p)) return launch_gla_pipe<REV>(p, s);
   }
-  // fp16 checkpoints: whole-width state rows with the plain layout (ckpt_par 0, ldk 0)
-  if (p.ckpt16 && (!p.ckpt || !p.ckpt_scale || p.ckpt_par || p.ldk)) return hipErrorInvalidValue;
+  // fp16 checkpoints: whole-width state rows with the plain layout (ckpt_par 0, no slices)
+  const bool plain = !p.acc_mode && !p.ldk;
+  if (p.ckpt16 && (!p.ckpt || !p.ckpt_scale || p.ckpt_par || !plain)) return hipErrorInvalidValue;
+  const int var = p.ckpt16 ? 1 : ((plain && !p.ckpt) ? 2 : 0);
+  if (var == 1 && !std::is_same<TIn, uint16_t>::value) return hipErrorInvalidValue;
   const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
   dim3 grid(p.NV * p.H * p.N);
   const bool gk = DELTA || p.gate_mode == kGateK;
 #define TOPS_SWEEP(KPV, GKV) \
   hipLaunchKernelGGL((gla_sweep_kernel<TIn, KPV, REV, DELTA, false, GKV>), grid, dim3(512), 0, s, p)
+  // the delta sweeps (KDA) and the bf16 value-side-gate sweeps are compiled per feature set
+#define TOPS_SWEEP_V(KPV, GKV, YGV) \
+  if (var == 1) { \
+    if constexpr (std::is_same<TIn, uint16_t>::value) \
+      hipLaunchKernelGGL((gla_sweep_kernel<TIn, KPV, REV, DELTA, false, GKV, YGV, 1>), grid, dim3(512), 0, s, p); \
+  } else if (var == 2) hipLaunchKernelGGL((gla_sweep_kernel<TIn, KPV, REV, DELTA, false, GKV, YGV, 2>), grid, dim3(512), 0, s, p); \
+  else hipLaunchKernelGGL((gla_sweep_kernel<TIn, KPV, REV, DELTA, false, GKV, YGV, 0>), grid, dim3(512), 0, s, p)
+  // fp16 checkpoints: the delta sweeps here, the per-channel-gate bf16 sweeps in the pipelined
+  // kernel (routed above)
+  if (var == 1 && !DELTA) return hipErrorInvalidValue;
   if constexpr (DELTA) {
-    if (kp == 32) TOPS_SWEEP(32, true);
-    else if (kp == 64) TOPS_SWEEP(64, true);
-    else TOPS_SWEEP(128, true);
+    if (kp == 32) { TOPS_SWEEP_V(32, true, 0); }
+    else if (kp == 64) { TOPS_SWEEP_V(64, true, 0); }
+    else { TOPS_SWEEP_V(128, true, 0); }
   } else if (gk) {
     if (kp == 32) TOPS_SWEEP(32, true);
     else if (kp == 64) TOPS_SWEEP(64, true);
@@ -1027,12 +1042,12 @@ hipError_t launch_gla_sweep(const SweepParams& p, hipStream_t s) {
   } else if (std::is_same<TIn, uint16_t>::value && !p.gshift &&
              (p.gate_mode == kGateS || p.gate_mode == kGateGamma)) {
     // one gate per token (bf16): on the value side, q and k stay exact
-#define TOPS_SWEEP_YG(KPV) \
-  hipLaunchKernelGGL((gla_sweep_kernel<uint16_t, KPV, REV, false, false, false, 2>), grid, dim3(512), 0, s, p)
+#define TOPS_SWEEP_YG(KPV, VARV) \
+  hipLaunchKernelGGL((gla_sweep_kernel<uint16_t, KPV, REV, false, false, false, 2, VARV>), grid, dim3(512), 0, s, p)
     if constexpr (std::is_same<TIn, uint16_t>::value && !DELTA) {
-      if (kp == 32) TOPS_SWEEP_YG(32);
-      else if (kp == 64) TOPS_SWEEP_YG(64);
-      else TOPS_SWEEP_YG(128);
+      if (kp == 32) { if (var == 2) TOPS_SWEEP_YG(32, 2); else TOPS_SWEEP_YG(32, 0); }
+      else if (kp == 64) { if (var == 2) TOPS_SWEEP_YG(64, 2); else TOPS_SWEEP_YG(64, 0); }
+      else { if (var == 2) TOPS_SWEEP_YG(128, 2); else TOPS_SWEEP_YG(128, 0); }
     }
 #undef TOPS_SWEEP_YG
   } else {
@@ -1040,6 +1055,7 @@ hipError_t launch_gla_sweep(const SweepParams& p, hipStream_t s) {
     else if (kp == 64) TOPS_SWEEP(64, false);
     else TOPS_SWEEP(128, false);
   }
+#undef TOPS_SWEEP_V
 #undef TOPS_SWEEP
   return hipGetLastError();
 }
