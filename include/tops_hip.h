@@ -498,6 +498,33 @@ int tops_kda_chunk_bwd(const void* q, const void* k, const void* v, const float*
                        int B, int T, int H, int K, int V, int N, int dtype, float scale,
                        void* stream);
 
+/* fp16 state checkpoints for the simple-GLA training path (bf16 inputs, one gate per token
+ * g [B,T,H] or a scalar g_gamma [H], K, V <= 128): tops_simple_gla_chunk_fwd / _bwd_dh /
+ * _bwd_dqkg (tops/ops/simple_gla/chunk.py:464-577, 579-674) with h
+ * and dh per chunk in the format of tops_gla_chunk_fwd_c16 (fp16 [total_chunks,H,K,V] plus
+ * one power-of-two factor per (chunk, head, 64-column tile of V), fp32
+ * [total_chunks,H,ceil(V/64)]).  Pass exactly one of g, g_gamma.  No reference counterpart for
+ * the format.  Other arguments as the fp32 entry points; dtype TOPS_BF16. */
+int tops_simple_gla_chunk_fwd_c16(const void* q, const void* k, const void* v, const float* g,
+                                  const float* g_gamma, const float* h0, void* o, float* ht,
+                                  uint16_t* h_ckpt16, float* h_scale, const int32_t* cu_seqlens,
+                                  const int32_t* chunk_offsets, int B, int T, int H, int K, int V,
+                                  int N, int dtype, float scale, void* stream);
+int tops_simple_gla_chunk_bwd_dh_c16(const void* q, const void* k, const float* g,
+                                     const float* g_gamma, const void* do_, const float* dht,
+                                     uint16_t* dh16, float* dh_scale, void* dv, float* dh0,
+                                     const int32_t* cu_seqlens, const int32_t* chunk_offsets,
+                                     int B, int T, int H, int K, int V, int N, int dtype,
+                                     float scale, void* stream);
+int tops_simple_gla_chunk_bwd_dqkg_c16(const void* q, const void* k, const void* v,
+                                       const float* g, const float* g_gamma, const void* do_,
+                                       const uint16_t* h16, const float* h_scale,
+                                       const uint16_t* dh16, const float* dh_scale, void* dq,
+                                       void* dk, float* dg, const int32_t* cu_seqlens,
+                                       const int32_t* chunk_offsets, const int32_t* chunk_map,
+                                       int total_chunks, int B, int T, int H, int K, int V, int N,
+                                       int dtype, float scale, void* stream);
+
 /* fp16 state checkpoints for the KDA training path (bf16 inputs, K, V <= 128):
  * tops_kda_chunk_fwd / _bwd (tops/ops/kda/chunk.py:25-190; chunk_bwd.py:655-832) with the
  * forward's state per chunk (h_ckpt16) and the reverse sweep's dS per chunk (dh16_work)

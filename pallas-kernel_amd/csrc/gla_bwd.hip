@@ -85,8 +85,9 @@ static int bwd_dh_impl(const void* q, const void* k, const float* g, const void*
   p.acc32 = dv_sum;
   p.acc_mode = acc_mode;
   if (dh_scale) {
-    if (dtype != TOPS_BF16 || gate_mode != kGateK || V > 128 || ldk || ckpt_par)
-      return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_bwd_dh_c16: bf16, per-channel gates, V <= 128, no slices");
+    if (dtype != TOPS_BF16 || (gate_mode != kGateK && gate_mode != kGateS && gate_mode != kGateGamma) ||
+        V > 128 || ldk || ckpt_par)
+      return tops_set_error(TOPS_ERR_SHAPE, "chunk_bwd_dh_c16: bf16, per-channel or per-token gates, V <= 128, no slices");
     p.ckpt16 = 1;
     p.ckpt_scale = dh_scale;
   }
@@ -128,8 +129,9 @@ static int bwd_dqkg_impl(const void* q, const void* k, const void* v, const floa
   p.acc_mode = acc_mode;
   p.dg_accum = dg_accum;
   if (h_scale || dh_scale) {
-    if (!h_scale || !dh_scale || dtype != TOPS_BF16 || gate_mode != kGateK || paired || ldk || ldv)
-      return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_bwd_dqkg_c16: bf16, per-channel gates, both scales, unpaired, no slices");
+    if (!h_scale || !dh_scale || dtype != TOPS_BF16 ||
+        (gate_mode != kGateK && gate_mode != kGateS && gate_mode != kGateGamma) || paired || ldk || ldv)
+      return tops_set_error(TOPS_ERR_SHAPE, "chunk_bwd_dqkg_c16: bf16, per-channel or per-token gates, both scales, unpaired, no slices");
     p.ckpt16 = 1;
     p.hs_scale = h_scale;
     p.dhs_scale = dh_scale;
@@ -222,6 +224,41 @@ extern "C" int tops_simple_gla_chunk_bwd_dqkg(const void* q, const void* k, cons
   return bwd_dqkg_impl(q, k, v, g ? g : g_gamma, do_, h_ckpt, dh_work, dq, dk, g ? dg : nullptr,
                        cu_seqlens, chunk_offsets, chunk_map, total_chunks, B, T, H, K, V, N, dtype,
                        scale, g ? kGateS : kGateGamma, stream);
+}
+
+extern "C" int tops_simple_gla_chunk_bwd_dh_c16(const void* q, const void* k, const float* g,
+                                                const float* g_gamma, const void* do_,
+                                                const float* dht, uint16_t* dh16, float* dh_scale,
+                                                void* dv, float* dh0, const int32_t* cu_seqlens,
+                                                const int32_t* chunk_offsets, int B, int T, int H,
+                                                int K, int V, int N, int dtype, float scale,
+                                                void* stream) {
+  if ((g == nullptr) == (g_gamma == nullptr))
+    return tops_set_error(TOPS_ERR_NULL, "simple_gla_chunk_bwd_dh_c16: pass exactly one of g, g_gamma");
+  if (!dh16 || !dh_scale) return tops_set_error(TOPS_ERR_NULL, "simple_gla_chunk_bwd_dh_c16: null checkpoint");
+  return bwd_dh_impl(q, k, g ? g : g_gamma, do_, dht, (float*)dh16, dv, dh0, cu_seqlens, chunk_offsets,
+                     B, T, H, K, V, N, dtype, scale, g ? kGateS : kGateGamma, stream, 0, 0, nullptr, 0,
+                     dh_scale);
+}
+
+extern "C" int tops_simple_gla_chunk_bwd_dqkg_c16(const void* q, const void* k, const void* v,
+                                                  const float* g, const float* g_gamma,
+                                                  const void* do_, const uint16_t* h16,
+                                                  const float* h_scale, const uint16_t* dh16,
+                                                  const float* dh_scale, void* dq, void* dk,
+                                                  float* dg, const int32_t* cu_seqlens,
+                                                  const int32_t* chunk_offsets,
+                                                  const int32_t* chunk_map, int total_chunks,
+                                                  int B, int T, int H, int K, int V, int N,
+                                                  int dtype, float scale, void* stream) {
+  if ((g == nullptr) == (g_gamma == nullptr))
+    return tops_set_error(TOPS_ERR_NULL, "simple_gla_chunk_bwd_dqkg_c16: pass exactly one of g, g_gamma");
+  if (!h16 || !dh16 || !h_scale || !dh_scale)
+    return tops_set_error(TOPS_ERR_NULL, "simple_gla_chunk_bwd_dqkg_c16: null checkpoint");
+  return bwd_dqkg_impl(q, k, v, g ? g : g_gamma, do_, (const float*)h16, (const float*)dh16, dq, dk,
+                       g ? dg : nullptr, cu_seqlens, chunk_offsets, chunk_map, total_chunks, B, T, H,
+                       K, V, N, dtype, scale, g ? kGateS : kGateGamma, stream, nullptr, nullptr, 0,
+                       0, 0, nullptr, nullptr, 0, 0, h_scale, dh_scale);
 }
 
 extern "C" int tops_gla_chunk_bwd_dh_gamma(const void* q, const void* k, const float* g_gamma,

@@ -80,7 +80,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
   static_assert(KP % KH == 0, "KP must be 32, 64 or 128");
   static_assert(!PAIR || (!SIN && !SINV), "the paired layout takes bf16 inputs");
   static_assert(!RG || (!GK && !PAIR && !SIN && !SINV), "RG: bf16, per-token gates, unpaired");
-  static_assert(!C16 || (!PAIR && !RG), "fp16 checkpoints: the unpaired layout");
+  static_assert(!C16 || !PAIR, "fp16 checkpoints: the unpaired layout");
   typedef Words<TIn> Wd;
 
   constexpr int ZV = NPLV * C * LV, ZD = NPL * C * LV, ZT = (RG ? 1 : 2) * KH * LT;
@@ -814,14 +814,17 @@ hipError_t launch_gla_dqkg(const DqkgParams& p, hipStream_t s) {
   const bool gk = !kAllModes || p.gate_mode == kGateK;
   if (p.paired && !kPairs) return hipErrorInvalidValue;
   const dim3 pgrid(((p.total + 1) / 2) * p.H), pblock(512);
-  if (p.ckpt16 && (!kPairs || !gk || p.paired || p.acc_mode || p.dg_accum || p.dk_add || p.dg_add ||
-                   p.ldk || p.ldv))
+  // fp16 checkpoints: bf16, per-channel gates or one gate per token (RG), no pairs or slices
+  const bool rg_mode = !gk && (p.gate_mode == kGateS || p.gate_mode == kGateGamma);
+  if (p.ckpt16 && (!kPairs || !(gk || rg_mode) || p.paired || p.acc_mode || p.dg_accum ||
+                   p.dk_add || p.dg_add || p.ldk || p.ldv))
     return hipErrorInvalidValue;
 #define TOPS_DQKG(KPV, VPV)                                                                   \
   if (kp == KPV && vp == VPV) {                                                               \
     if constexpr (kPairs) {                                                                   \
       if (p.ckpt16) {                                                                         \
-        hipLaunchKernelGGL((gla_dqkg_kernel<TIn, TV, KPV, VPV, true, false, false, true>), grid, block, 0, s, p); \
+        if (gk) hipLaunchKernelGGL((gla_dqkg_kernel<TIn, TV, KPV, VPV, true, false, false, true>), grid, block, 0, s, p); \
+        else hipLaunchKernelGGL((gla_dqkg_kernel<TIn, TV, KPV, VPV, false, false, true, true>), grid, block, 0, s, p); \
         return hipGetLastError();                                                             \
       }                                                                                       \
       if (p.paired) {                                                                         \

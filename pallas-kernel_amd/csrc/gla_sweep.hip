@@ -1028,9 +1028,11 @@ hipError_t launch_gla_sweep(const SweepParams& p, hipStream_t s) {
       hipLaunchKernelGGL((gla_sweep_kernel<TIn, KPV, REV, DELTA, false, GKV, YGV, 1>), grid, dim3(512), 0, s, p); \
   } else if (var == 2) hipLaunchKernelGGL((gla_sweep_kernel<TIn, KPV, REV, DELTA, false, GKV, YGV, 2>), grid, dim3(512), 0, s, p); \
   else hipLaunchKernelGGL((gla_sweep_kernel<TIn, KPV, REV, DELTA, false, GKV, YGV, 0>), grid, dim3(512), 0, s, p)
-  // fp16 checkpoints: the delta sweeps here, the per-channel-gate bf16 sweeps in the pipelined
-  // kernel (routed above)
-  if (var == 1 && !DELTA) return hipErrorInvalidValue;
+  // fp16 checkpoints: the delta sweeps and the bf16 one-gate-per-token sweeps here, the
+  // per-channel-gate bf16 sweeps in the pipelined kernel (routed above)
+  const bool yg2 = std::is_same<TIn, uint16_t>::value && !DELTA && !gk && !p.gshift &&
+                   (p.gate_mode == kGateS || p.gate_mode == kGateGamma);
+  if (var == 1 && !DELTA && !yg2) return hipErrorInvalidValue;
   if constexpr (DELTA) {
     if (kp == 32) { TOPS_SWEEP_V(32, true, 0); }
     else if (kp == 64) { TOPS_SWEEP_V(64, true, 0); }
@@ -1045,9 +1047,12 @@ hipError_t launch_gla_sweep(const SweepParams& p, hipStream_t s) {
 #define TOPS_SWEEP_YG(KPV, VARV) \
   hipLaunchKernelGGL((gla_sweep_kernel<uint16_t, KPV, REV, false, false, false, 2, VARV>), grid, dim3(512), 0, s, p)
     if constexpr (std::is_same<TIn, uint16_t>::value && !DELTA) {
-      if (kp == 32) { if (var == 2) TOPS_SWEEP_YG(32, 2); else TOPS_SWEEP_YG(32, 0); }
-      else if (kp == 64) { if (var == 2) TOPS_SWEEP_YG(64, 2); else TOPS_SWEEP_YG(64, 0); }
-      else { if (var == 2) TOPS_SWEEP_YG(128, 2); else TOPS_SWEEP_YG(128, 0); }
+#define TOPS_SWEEP_YGV(KPV) \
+  if (var == 1) TOPS_SWEEP_YG(KPV, 1); else if (var == 2) TOPS_SWEEP_YG(KPV, 2); else TOPS_SWEEP_YG(KPV, 0)
+      if (kp == 32) { TOPS_SWEEP_YGV(32); }
+      else if (kp == 64) { TOPS_SWEEP_YGV(64); }
+      else { TOPS_SWEEP_YGV(128); }
+#undef TOPS_SWEEP_YGV
     }
 #undef TOPS_SWEEP_YG
   } else {
@@ -1142,8 +1147,9 @@ static int chunk_fwd_impl(const void* q, const void* k, const void* v, const flo
   p.acc32 = o_sum;
   p.acc_mode = acc_mode;
   if (ckpt_scale) {
-    if (dtype != TOPS_BF16 || gate_mode != kGateK || V > 128 || ldk || ckpt_par || !h_ckpt)
-      return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd_c16: bf16, per-channel gates, V <= 128, no slices");
+    if (dtype != TOPS_BF16 || (gate_mode != kGateK && gate_mode != kGateS && gate_mode != kGateGamma) ||
+        V > 128 || ldk || ckpt_par || !h_ckpt)
+      return tops_set_error(TOPS_ERR_SHAPE, "chunk_fwd_c16: bf16, per-channel or per-token gates, V <= 128, no slices");
     p.ckpt16 = 1;
     p.ckpt_scale = ckpt_scale;
   }
@@ -1186,6 +1192,22 @@ extern "C" int tops_simple_gla_chunk_fwd(const void* q, const void* k, const voi
     return tops_set_error(TOPS_ERR_NULL, "simple_gla_chunk_fwd: pass exactly one of g, g_gamma");
   return chunk_fwd_impl(q, k, v, g ? g : g_gamma, h0, o, ht, h_ckpt, cu_seqlens, chunk_offsets, B, T,
                         H, K, V, N, dtype, scale, g ? kGateS : kGateGamma, stream);
+}
+
+extern "C" int tops_simple_gla_chunk_fwd_c16(const void* q, const void* k, const void* v,
+                                             const float* g, const float* g_gamma,
+                                             const float* h0, void* o, float* ht,
+                                             uint16_t* h_ckpt16, float* h_scale,
+                                             const int32_t* cu_seqlens,
+                                             const int32_t* chunk_offsets, int B, int T, int H,
+                                             int K, int V, int N, int dtype, float scale,
+                                             void* stream) {
+  if ((g == nullptr) == (g_gamma == nullptr))
+    return tops_set_error(TOPS_ERR_NULL, "simple_gla_chunk_fwd_c16: pass exactly one of g, g_gamma");
+  if (!h_ckpt16 || !h_scale) return tops_set_error(TOPS_ERR_NULL, "simple_gla_chunk_fwd_c16: null checkpoint");
+  return chunk_fwd_impl(q, k, v, g ? g : g_gamma, h0, o, ht, (float*)h_ckpt16, cu_seqlens,
+                        chunk_offsets, B, T, H, K, V, N, dtype, scale, g ? kGateS : kGateGamma,
+                        stream, 0, 0, nullptr, 0, h_scale);
 }
 
 extern "C" int tops_gla_chunk_fwd_gamma(const void* q, const void* k, const void* v,

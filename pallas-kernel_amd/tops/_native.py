@@ -51,6 +51,9 @@ SIGNATURES = {
     "tops_kda_chunk_fwd": [_vp] * 16 + [_i32] * 8 + [_f32, _vp],
     "tops_kda_chunk_bwd": [_vp] * 24 + [_i32] * 8 + [_f32, _vp],
     "tops_kda_chunk_fwd_c16": [_vp] * 17 + [_i32] * 8 + [_f32, _vp],
+    "tops_simple_gla_chunk_fwd_c16": [_vp] * 12 + [_i32] * 7 + [_f32, _vp],
+    "tops_simple_gla_chunk_bwd_dh_c16": [_vp] * 12 + [_i32] * 7 + [_f32, _vp],
+    "tops_simple_gla_chunk_bwd_dqkg_c16": [_vp] * 16 + [_i32] * 8 + [_f32, _vp],
     "tops_kda_chunk_bwd_c16": [_vp] * 24 + [_i32] * 8 + [_f32, _vp],
     "tops_kda_chunk_fwd_noalloc": [_vp] * 11 + [_i32] * 8 + [_f32, _vp],
     "tops_simple_gla_chunk_bwd_dh": [_vp] * 11 + [_i32] * 7 + [_f32, _vp],

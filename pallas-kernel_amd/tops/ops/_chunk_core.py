@@ -99,10 +99,10 @@ class States16(NamedTuple):
 
 
 def _c16(q, mode, K: int, V: int) -> bool:
-    """Whether kept states are fp16 checkpoints: bf16, per-channel gates, one tile, and
-    tops.utils.set_checkpoint_layout not "full32"."""
-    return (q.dtype == torch.bfloat16 and mode == GATE_K and K <= 128 and V <= 128
-            and checkpoint_layout() == "full")
+    """Whether kept states are fp16 checkpoints: bf16, per-channel gates or one gate per token
+    (or a scalar g_gamma), one tile, and tops.utils.set_checkpoint_layout "full"."""
+    return (q.dtype == torch.bfloat16 and mode in (GATE_K, GATE_S, GATE_GAMMA) and K <= 128
+            and V <= 128 and checkpoint_layout() == "full")
 
 
 def _states_like(hs):
@@ -160,9 +160,12 @@ def _fwd_tile(q, k, v, gate, h0, scale, output_final_state, plan: ChunkPlan, kee
         cu, offs, Bx, Tx, Nx = sp.cu_dev, sp.offsets_dev, 1, B * T, sp.Nv
     tail = (N.ptr(s0), N.ptr(o), N.ptr(fin), _sptr(hs), N.ptr(cu), N.ptr(offs),
             Bx, Tx, H, K, V, Nx, N.chunk_dtype_code(q.dtype), float(scale), N.stream())
-    if c16:
+    if c16 and mode == GATE_K:
         N.call("tops_gla_chunk_fwd_c16", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gt), N.ptr(s0),
                N.ptr(o), N.ptr(fin), N.ptr(hs.h), N.ptr(hs.scale), *tail[4:])
+    elif c16:
+        N.call("tops_simple_gla_chunk_fwd_c16", N.ptr(q), N.ptr(k), N.ptr(v), *_gate_ptrs(gate),
+               N.ptr(s0), N.ptr(o), N.ptr(fin), N.ptr(hs.h), N.ptr(hs.scale), *tail[4:])
     elif keep_states == PAIRED:
         N.call("tops_chunk_fwd_paired", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gt),
                _GATE_CODE[mode], *tail)
@@ -217,12 +220,18 @@ def _bwd_tile(q, k, v, gate, do, dht, hs, scale, plan: ChunkPlan, want_dh0: bool
     dqkg_tail = (N.ptr(do), _sptr(hs), _sptr(dh_work), N.ptr(dq), N.ptr(dk), N.ptr(dg),
                  N.ptr(plan.cu_dev), N.ptr(plan.offsets_dev), N.ptr(plan.chunk_map_dev),
                  plan.total, B, T, H, K, V, plan.N, dt, float(scale), st)
-    if c16:
+    if c16 and mode == GATE_K:
         N.call("tops_gla_chunk_bwd_dh_c16", N.ptr(q), N.ptr(k), N.ptr(gt), N.ptr(do), N.ptr(s0),
                N.ptr(dh_work.h), N.ptr(dh_work.scale), *dh_args[3:])
         N.call("tops_gla_chunk_bwd_dqkg_c16", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gt), N.ptr(do),
                N.ptr(hs.h), N.ptr(hs.scale), N.ptr(dh_work.h), N.ptr(dh_work.scale),
                *dqkg_tail[3:])
+    elif c16:
+        N.call("tops_simple_gla_chunk_bwd_dh_c16", N.ptr(q), N.ptr(k), *_gate_ptrs(gate),
+               N.ptr(do), N.ptr(s0), N.ptr(dh_work.h), N.ptr(dh_work.scale), *dh_args[3:])
+        N.call("tops_simple_gla_chunk_bwd_dqkg_c16", N.ptr(q), N.ptr(k), N.ptr(v),
+               *_gate_ptrs(gate), N.ptr(do), N.ptr(hs.h), N.ptr(hs.scale), N.ptr(dh_work.h),
+               N.ptr(dh_work.scale), *dqkg_tail[3:])
     elif paired:
         code = _GATE_CODE[mode]
         N.call("tops_chunk_bwd_dh_paired", N.ptr(q), N.ptr(k), N.ptr(gt), code, *dh_args)

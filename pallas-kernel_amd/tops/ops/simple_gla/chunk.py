@@ -22,7 +22,8 @@ import torch
 
 from ...utils import ChunkPlan, inference_inputs
 from .._chunk_core import (GATE_S, GATE_GAMMA, PAIRED, check_qkv, chunk_fwd as _core_fwd,
-                           chunk_bwd as _core_bwd, paired_states)
+                           chunk_bwd as _core_bwd, pack_states, paired_states,
+                           unpack_states)
 
 
 def _gate(q, g, g_gamma):
@@ -51,7 +52,7 @@ class _ChunkSimpleGLA(torch.autograd.Function):
         o, ht, hs = _core_fwd(q, k, v, (mode, g32), h032, scale, output_final_state, plan,
                               keep_states=PAIRED if train else False)
         if train:
-            ctx.save_for_backward(q, k, v, g32, hs, h032)
+            ctx.save_for_backward(q, k, v, g32, *pack_states(hs), h032)
             ctx.paired = paired_states(q, q.shape[-1], v.shape[-1])
             ctx.plan, ctx.scale, ctx.mode = plan, scale, mode
             ctx.g_info = (gt.dtype, gt.shape)
@@ -60,7 +61,8 @@ class _ChunkSimpleGLA(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, do, dht):
-        q, k, v, g32, hs, h032 = ctx.saved_tensors
+        q, k, v, g32, hs, hsc, h032 = ctx.saved_tensors
+        hs = unpack_states(hs, hsc)
         do = do.contiguous().to(q.dtype)
         dht = None if dht is None else dht.contiguous().to(torch.float32)
         dq, dk, dv, dg, dh0 = _core_bwd(q, k, v, (ctx.mode, g32), do, dht, hs, ctx.scale,

@@ -13,7 +13,8 @@ import torch
 
 from ...utils import ChunkPlan, inference_inputs
 from .._chunk_core import (GATE_GAMMA, PAIRED, check_qkv, chunk_fwd as _core_fwd,
-                           chunk_bwd as _core_bwd, paired_states)
+                           chunk_bwd as _core_bwd, pack_states, paired_states,
+                           unpack_states)
 from .chunk import chunk_simple_gla_fwd, chunk_simple_gla_bwd
 
 
@@ -29,7 +30,7 @@ class _FusedChunkSimpleGLA(torch.autograd.Function):
         o, ht, hs = _core_fwd(q, k, v, (GATE_GAMMA, gg), h032, scale, output_final_state, plan,
                               keep_states=PAIRED if train else False)
         if train:
-            ctx.save_for_backward(q, k, v, gg, hs, h032)
+            ctx.save_for_backward(q, k, v, gg, *pack_states(hs), h032)
             ctx.paired = paired_states(q, q.shape[-1], v.shape[-1])
             ctx.plan, ctx.scale, ctx.has_h0 = plan, scale, h0 is not None
             ctx.g_info = (g_gamma.dtype, g_gamma.shape)
@@ -37,7 +38,8 @@ class _FusedChunkSimpleGLA(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, do, dht):
-        q, k, v, gg, hs, h032 = ctx.saved_tensors
+        q, k, v, gg, hs, hsc, h032 = ctx.saved_tensors
+        hs = unpack_states(hs, hsc)
         qkv_dtype = do.dtype
         dht = None if dht is None else dht.contiguous().to(torch.float32)
         dq, dk, dv, _, dh0 = _core_bwd(q, k, v, (GATE_GAMMA, gg), do.contiguous().to(q.dtype), dht,

@@ -4,7 +4,8 @@ import pytest
 import torch
 
 from tops import utils as U
-from tops.ops._chunk_core import (GATE_K, GATE_S, States16, _c16, pack_states, states_fp32,
+from tops.ops._chunk_core import (GATE_K, GATE_S, GATE_GAMMA, GATE_GAMMA_K, States16, _c16,
+                                  pack_states, states_fp32,
                                   unpack_states)
 
 
@@ -28,7 +29,9 @@ def test_c16_selection():
         U.set_checkpoint_layout("full")
         assert _c16(bf, GATE_K, 128, 128)
         assert not _c16(f32, GATE_K, 128, 128)          # fp32 inputs keep fp32 states
-        assert not _c16(bf, GATE_S, 128, 128)           # per-token scalar gates: fp32
+        assert _c16(bf, GATE_S, 128, 128)               # one gate per token: fp16 too
+        assert _c16(bf, GATE_GAMMA, 128, 128)
+        assert not _c16(bf, GATE_GAMMA_K, 128, 128)     # per-channel constants: fp32
         assert not _c16(bf, GATE_K, 256, 128)           # channel slices: fp32
         assert not _c16(bf, GATE_K, 128, 192)
         U.set_checkpoint_layout("full32")
