@@ -221,7 +221,9 @@ def test_chunk_gla_constant_gate_per_head_bf16(form, cuda_device, monkeypatch):
     torch.autograd.backward((o, ht), (to_dev(d["do"], bf, cuda_device),
                                       to_dev(d["dht"], torch.float32, cuda_device)))
     torch.cuda.synchronize()
-    assert "tops_simple_gla_chunk_fwd" in names and "tops_gla_chunk_fwd_gamma" not in names
+    # (training keeps fp16 checkpoints: the _c16 variant of the same entry point)
+    assert any(n.startswith("tops_simple_gla_chunk_fwd") for n in names)
+    assert not any(n.startswith("tops_gla_chunk_fwd_gamma") for n in names)
     gfull = np.zeros((B, T, H, K), np.float32) if gam is None else \
         np.broadcast_to(gam, (B, T, H, K)).astype(np.float32)
     sq, sk, sv, sdo = (seen(d[x], bf) for x in ("q", "k", "v", "do"))

@@ -4,8 +4,15 @@ against the float64 oracle (tops/cpu/ops/gla/chunk.py, tops/cpu/ops/simple_gla/c
 restated) and against the same call swept whole.  Cases cover ragged sequences, a
 one-token sequence, h0 / dht, all three gate modes and the automatic split of one long
 sequence.  Tolerance: fp32 1e-4, bf16 2e-3 (relative L2) against the oracle; 1e-4 between
-the split and unsplit runs (fp32 state rounding only).
+the split and unsplit runs (fp32 state rounding only), except dq / dk / dg of bf16 calls,
+1e-3: those read the fp16 state checkpoints, and a state that differs in its last fp32 bit
+between the two runs can round to the neighbouring fp16 value (2^-12 of that entry), which
+flips some bf16 outputs by one ulp.
 """
+
+
+def _split_bound(name, dtype):
+    return 1e-3 if dtype == torch.bfloat16 and name in ("dq", "dk", "dg") else 1e-4
 import numpy as np
 import pytest
 import torch
@@ -84,7 +91,7 @@ def test_chunk_gla_segments(cfg, dtype, cuda_device, split_mode):
     print(f"segments={sp.Nv}", " ".join(f"{x}={errs[x]:.2e}/{diffs[x]:.1e}" for x in got))
     for x in got:
         assert errs[x] < tol(dtype), (x, errs[x])
-        assert diffs[x] < 1e-4, (x, diffs[x])
+        assert diffs[x] < _split_bound(x, dtype), (x, diffs[x])
 
 
 SIMPLE_CASES = [
@@ -135,7 +142,7 @@ def test_chunk_simple_gla_segments(cfg, dtype, cuda_device, split_mode):
         e, df = rel(got[x], ref[x]), rel(got[x], whole[x])
         print(f"{x}={e:.2e}/{df:.1e}", end=" ")
         assert e < tol(dtype), (x, e)
-        assert df < 1e-4, (x, df)
+        assert df < _split_bound(x, dtype), (x, df)
 
 
 def test_automatic_split_of_one_long_sequence(cuda_device, split_mode):
