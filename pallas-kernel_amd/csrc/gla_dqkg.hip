@@ -386,18 +386,17 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
       }
     }
   }
-  // the lane's 8 state values of value block vc (scaled back for fp16 checkpoints)
-  auto state8 = [&](const uint4 (&raw)[VC][2], int vc, const float* sc, float* x) {
+  // the lane's 8 state values of value block vc as stored (fp16 checkpoints: before their
+  // tile factor, which tfac gives; the 8 values v0 .. v0 + 7 lie in 64-column tile vc / 2)
+  auto state8 = [&](const uint4 (&raw)[VC][2], int vc, float* x) {
     if constexpr (C16) {
       unpack8_f16(raw[vc][0], x);
-      const float f = sc[(32 * vc + 8 * lg) >> 6];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] *= f;
     } else {
       unpack4(raw[vc][0], x);
       unpack4(raw[vc][1], x + 4);
     }
   };
+  auto tfac = [&](const float* sc, int vc) { return C16 ? sc[vc >> 1] : 1.f; };
   const rsrc_t Rdq = chunk_rsrc((const TIn*)p.dq, e0, nval, (int)rowK, LDK);
   const rsrc_t Rdk = chunk_rsrc((const TIn*)p.dk, e0, nval, (int)rowK, LDK);
   // C16 calls take no slices and no WY parts (the launcher checks): their instance compiles
@@ -561,10 +560,11 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
     for (int vc = 0; vc < VC; ++vc) {
       const int v0 = 32 * vc + 8 * lg;
       float hv[8];
-      state8(hraw, vc, hsc, hv);
+      state8(hraw, vc, hv);
+      const float alt = al * tfac(hsc, vc);
       uint32_t ah_[4], al_[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) split_bf16x2(al * hv[2 * e], al * hv[2 * e + 1], ah_[e], al_[e]);
+      for (int e = 0; e < 4; ++e) split_bf16x2(alt * hv[2 * e], alt * hv[2 * e + 1], ah_[e], al_[e]);
       const bf16x8 Ah = __builtin_bit_cast(bf16x8, make_uint4(ah_[0], ah_[1], ah_[2], ah_[3]));
       const bf16x8 Al = __builtin_bit_cast(bf16x8, make_uint4(al_[0], al_[1], al_[2], al_[3]));
 #pragma unroll
@@ -603,15 +603,23 @@ __global__ __launch_bounds__(PAIR ? 512 : 256, 2) void gla_dqkg_kernel(DqkgParam
     for (int vc = 0; vc < VC; ++vc) {
       const int v0 = 32 * vc + 8 * lg;
       float hv[8], dv[8];
-      state8(hraw, vc, hsc, hv);
-      state8(draw, vc, dhsc, dv);
+      state8(hraw, vc, hv);
+      state8(draw, vc, dv);
       if (rh == 0) {
+        if constexpr (C16) {
+          float s = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) hd += hv[e] * dv[e];
+          for (int e = 0; e < 8; ++e) s += hv[e] * dv[e];
+          hd += s * (hsc[vc >> 1] * dhsc[vc >> 1]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) hd += hv[e] * dv[e];
+        }
       }
+      const float bet = be * tfac(dhsc, vc);
       uint32_t bh_[4], bl_[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) split_bf16x2(be * dv[2 * e], be * dv[2 * e + 1], bh_[e], bl_[e]);
+      for (int e = 0; e < 4; ++e) split_bf16x2(bet * dv[2 * e], bet * dv[2 * e + 1], bh_[e], bl_[e]);
       const bf16x8 Dh = __builtin_bit_cast(bf16x8, make_uint4(bh_[0], bh_[1], bh_[2], bh_[3]));
       const bf16x8 Dl = __builtin_bit_cast(bf16x8, make_uint4(bl_[0], bl_[1], bl_[2], bl_[3]));
 #pragma unroll

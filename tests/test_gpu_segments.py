@@ -9,10 +9,6 @@ the split and unsplit runs (fp32 state rounding only), except dq / dk / dg of bf
 between the two runs can round to the neighbouring fp16 value (2^-12 of that entry), which
 flips some bf16 outputs by one ulp.
 """
-
-
-def _split_bound(name, dtype):
-    return 1e-3 if dtype == torch.bfloat16 and name in ("dq", "dk", "dg") else 1e-4
 import numpy as np
 import pytest
 import torch
@@ -23,6 +19,10 @@ from _inputs import gla_inputs, simple_gla_inputs
 from _gpu import to_dev, seen, host, rel, tol
 
 pytestmark = pytest.mark.gpu
+
+
+def _split_bound(name, dtype):
+    return 1e-3 if dtype == torch.bfloat16 and name in ("dq", "dk", "dg") else 1e-4
 
 
 @pytest.fixture
