@@ -2,10 +2,13 @@
 // hot path: the forward of tops/ops/gla/chunk.py:1103-1199 and the state-gradient sweep of its
 // backward, chunk.py:1447-1509 with tops/ops/common/chunk_h.py:685-878).
 //
-// Same products, operand planes, thread mappings and summation order as gla_sweep_kernel
-// (gla_sweep.hip, instance TIn = bf16, DELTA = ST = false, GK = true, YG = 0); only the
-// schedule differs (the compiler may contract the fp32 state update differently, a last-bit
-// difference).  The serial kernel runs each chunk as
+// Same products, operand values, thread mappings and summation order as gla_sweep_kernel
+// (gla_sweep.hip, instance TIn = bf16, DELTA = ST = false, GK = true, YG = 0); the schedule
+// differs (the compiler may contract the fp32 state update differently, a last-bit
+// difference), and so do the planes: the state update and the intra output products read
+// Z~ and Y transposed out of their row-major planes (ds_read_b64_tr_b16) where the serial
+// kernel writes separate Z~^T / Y^T planes, 40 KB fewer LDS writes per chunk and 126 KB of
+// LDS instead of 163 KB.  The serial kernel runs each chunk as
 //   gate cumsum | B1 | VALU staging (exponentials, bf16 hi / lo splits) + plane writes | B2 |
 //   D tiles + state update (MFMA) | B3 | output products (MFMA)
 // and the VALU staging (~600 VALU instructions per wave, 4 cycles each on a 16-lane SIMD)
@@ -47,7 +50,7 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
   static_assert(NQ % CQL == 0, "KP must be a multiple of 32");
   static_assert(CQL == 8 && SGL == 4, "the segment scan takes 8 column quads x 4 segments");
   static_assert(RPT == 1 || RPT == 2 || RPT == 4, "KP must be 32, 64 or 128");
-  constexpr int LQ = KP + 8, LT = C + 8, LH = KP + 8;
+  constexpr int LQ = KP + 8, LY = BV + 8, LH = KP + 8;
   constexpr int NHT = (KP / 16) * (BV / 16) / NW;  // state tiles per wave
   constexpr int YR = C * BV / (2 * NTH);
   static_assert(YR == 4, "Y staging assumes 4 rows x 2 columns per thread");
@@ -55,8 +58,7 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
 
   __shared__ __attribute__((aligned(16))) uint16_t sX[2 * C * LQ];
   __shared__ __attribute__((aligned(16))) uint16_t sZ[2 * C * LQ];
-  __shared__ __attribute__((aligned(16))) uint16_t sZT[2 * KP * LT];
-  __shared__ __attribute__((aligned(16))) uint16_t sYT[BV * LT];
+  __shared__ __attribute__((aligned(16))) uint16_t sY[C * LY];
   __shared__ __attribute__((aligned(16))) uint16_t sHT[2 * BV * LH];
   __shared__ __attribute__((aligned(16))) float sTot[NSGH * KP];
   __shared__ __attribute__((aligned(16))) uint4 sDt[10 * 64];
@@ -64,8 +66,7 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
 
   const Plane PX{sX, sX + C * LQ, LQ};
   const Plane PZ{sZ, sZ + C * LQ, LQ};
-  const Plane PZt{sZT, sZT + KP * LT, LT};
-  const Plane PYt{sYT, sYT, LT};
+  const Plane PY{sY, sY, LY};   // Y = v (forward) or dO (reverse), [C][BV], bf16 as read
   const Plane PHt{sHT, sHT + BV * LH, LH};
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -270,41 +271,9 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
       *(uint2*)(PZ.hi + (r0 + i) * PZ.ld + c0) = make_uint2(zh[i][0], zh[i][1]);
       *(uint2*)(PZ.lo + (r0 + i) * PZ.ld + c0) = make_uint2(zl[i][0], zl[i][1]);
     }
-    if constexpr (RPT >= 2) {
+    // Y rows yseg * 4 + 0..3, columns 2 yc, 2 yc + 1
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-        uint32_t th[RPT / 2], tl[RPT / 2];
-#pragma unroll
-        for (int m = 0; m < RPT / 2; ++m) {
-          th[m] = __builtin_amdgcn_perm(zh[2 * m + 1][j >> 1], zh[2 * m][j >> 1], sel);
-          tl[m] = __builtin_amdgcn_perm(zl[2 * m + 1][j >> 1], zl[2 * m][j >> 1], sel);
-        }
-        uint16_t* ph = PZt.hi + (c0 + j) * PZt.ld + r0;
-        uint16_t* pl = PZt.lo + (c0 + j) * PZt.ld + r0;
-        if constexpr (RPT == 4) {
-          *(uint2*)ph = make_uint2(th[0], th[1]);
-          *(uint2*)pl = make_uint2(tl[0], tl[1]);
-        } else {
-          *(uint32_t*)ph = th[0];
-          *(uint32_t*)pl = tl[0];
-        }
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t w = zh[0][j >> 1], wl = zl[0][j >> 1];
-        PZt.hi[(c0 + j) * PZt.ld + r0] = (uint16_t)((j & 1) ? (w >> 16) : (w & 0xffffu));
-        PZt.lo[(c0 + j) * PZt.ld + r0] = (uint16_t)((j & 1) ? (wl >> 16) : (wl & 0xffffu));
-      }
-    }
-    // Y^T: column 2 yc (low halves) and 2 yc + 1 (high halves) of rows yseg * 4 + 0..3
-    *(uint2*)(PYt.hi + (2 * yc) * PYt.ld + yseg * YR) =
-        make_uint2(__builtin_amdgcn_perm(yw[1], yw[0], 0x05040100u),
-                   __builtin_amdgcn_perm(yw[3], yw[2], 0x05040100u));
-    *(uint2*)(PYt.hi + (2 * yc + 1) * PYt.ld + yseg * YR) =
-        make_uint2(__builtin_amdgcn_perm(yw[1], yw[0], 0x07060302u),
-                   __builtin_amdgcn_perm(yw[3], yw[2], 0x07060302u));
+    for (int i = 0; i < YR; ++i) *(uint32_t*)(PY.hi + (yseg * YR + i) * PY.ld + 2 * yc) = yw[i];
   };
 
   // checkpoint: S as the state entering chunk c (stored at the start of the chunk's matrix
@@ -419,13 +388,13 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
       for (int i = 0; i < NHT; ++i) dsu[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < C / 32; ++kc) {
-        const bf16x8 fzh = PZt.hi8(16 * msb + l16, 32 * kc + 8 * lg);
-        const bf16x8 fzl = PZt.lo8(16 * msb + l16, 32 * kc + 8 * lg);
+        const bf16x8 fzh = tr_read8(PZ.hi, PZ.ld, 32 * kc, 16 * msb, lane);
+        const bf16x8 fzl = tr_read8(PZ.lo, PZ.ld, 32 * kc, 16 * msb, lane);
         bf16x8 fyh[NHT];
 #pragma unroll
         for (int i = 0; i < NHT; ++i) {
           const int nn = (wave * NHT + i) % (BV / 16);
-          fyh[i] = PYt.hi8(16 * nn + l16, 32 * kc + 8 * lg);
+          fyh[i] = tr_read8(PY.hi, PY.ld, 32 * kc, 16 * nn, lane);
         }
 #pragma unroll
         for (int i = 0; i < NHT; ++i) dsu[i] = mfma(fzl, fyh[i], dsu[i]);
@@ -485,7 +454,7 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
         const int P0 = 2 * Pp, P1 = 2 * Pp + 1;
         const bool live = REV ? (P1 >= R) : (P0 <= R);
         if (live) {
-          const bf16x8 ah = PYt.hi44(16 * nn + l16, 16 * P0 + 4 * lg, 16 * P1 + 4 * lg);
+          const bf16x8 ah = tr_read44(PY.hi, PY.ld, 16 * P0, 16 * P1, 16 * nn, lane);
           acc = mma<false, true>(acc, ah, ah, cat44(dh[P0], dh[P1]), cat44(dl[P0], dl[P1]));
         }
       }
