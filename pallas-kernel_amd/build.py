@@ -1,9 +1,11 @@
 """Build libtops_hip.so (gfx950) from csrc/ with hipcc, in-tree.
 
-    python pallas-kernel_amd/build.py [-j N]
+    python pallas-kernel_amd/build.py [-j N] [--phase-clocks]
 
 Objects go to pallas-kernel_amd/_build/, the library to
-pallas-kernel_amd/tops/_lib/libtops_hip.so (both git-ignored).
+pallas-kernel_amd/tops/_lib/libtops_hip.so (both git-ignored).  --phase-clocks also builds
+tops/_lib/libtops_pipe_clocks.so: the pipelined sweep alone, compiled with
+TOPS_PHASE_CLOCKS (per-wave phase clocks, read by pallas-kernel_amd/phase_clocks.py).
 """
 from __future__ import annotations
 
@@ -63,12 +65,40 @@ def build(jobs: int | None = None, verbose: bool = True) -> str:
     return LIB
 
 
+CLOCKS_LIB = os.path.join(LIBDIR, "libtops_pipe_clocks.so")
+
+
+def build_phase_clocks(verbose: bool = True) -> str:
+    """The instrumented pipelined sweep (TOPS_PHASE_CLOCKS) as its own library."""
+    os.makedirs(BUILD, exist_ok=True)
+    os.makedirs(LIBDIR, exist_ok=True)
+    src = os.path.join(CSRC, "gla_sweep_pipe.hip")
+    obj = os.path.join(BUILD, "gla_sweep_pipe.clocks.o")
+    r = subprocess.run([HIPCC] + COMMON + DEVICE + ["-DTOPS_PHASE_CLOCKS", "-c", src, "-o", obj],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src} (TOPS_PHASE_CLOCKS):\n{r.stderr}")
+    tmp = CLOCKS_LIB + ".tmp"
+    r = subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, obj],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stderr}")
+    shutil.move(tmp, CLOCKS_LIB)
+    if verbose:
+        print(f"built {CLOCKS_LIB}")
+    return CLOCKS_LIB
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("-j", type=int, default=None)
+    ap.add_argument("--phase-clocks", action="store_true",
+                    help="also build the instrumented sweep library (libtops_pipe_clocks.so)")
     a = ap.parse_args()
     try:
         build(a.j)
+        if a.phase_clocks:
+            build_phase_clocks()
     except RuntimeError as e:
         print(e, file=sys.stderr)
         sys.exit(1)

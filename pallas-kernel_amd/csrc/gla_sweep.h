@@ -60,6 +60,9 @@ struct SweepParams {
   // and ckpt_scale [total, H, NV] receives the factors 2^e.
   int ckpt16 = 0;
   float* ckpt_scale = nullptr;
+  // phase clocks of the pipelined sweep, [grid, 8 waves, 8] (read only by a library built
+  // with TOPS_PHASE_CLOCKS; see gla_sweep_pipe.hip)
+  unsigned long long* clocks = nullptr;
 };
 
 // TIn = uint16_t (bf16 bits) or float; REV = reverse (state-gradient) sweep;

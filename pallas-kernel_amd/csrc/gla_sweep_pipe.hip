@@ -32,6 +32,49 @@ namespace tops {
 __device__ __forceinline__ void pin(uint32_t& x) { asm volatile("" : "+v"(x)); }
 __device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
 
+// Phase clocks (a library built with -DTOPS_PHASE_CLOCKS only; the regular build compiles
+// none of this): per wave, the shader clock (s_memtime) spent in each interval of the chunk
+// loop, summed over the chunks, slots 0 B1 wait, 1 plane writes + next gate scan, 2 B2 wait,
+// 3 matrix phase (H^T plane, checkpoint, D tiles, state update, next chunk's staging and
+// loads), 4 B3 wait, 5 output products; slot 6 the loop's s_memtime span, slot 7 its
+// s_memrealtime (100 MHz) span.  The reads sit at barriers, where the LDS counter is
+// drained anyway, and at the loop's ends.
+#ifdef TOPS_PHASE_CLOCKS
+constexpr bool kPhaseClocks = true;
+#else
+constexpr bool kPhaseClocks = false;
+#endif
+template <bool ON>
+struct PhaseClock {
+  __device__ void start() {}
+  __device__ void tick(int) {}
+  __device__ void finish(unsigned long long*, int) {}
+};
+template <>
+struct PhaseClock<true> {
+  uint64_t ph[6], t, t0, r0;
+  __device__ void start() {
+#pragma unroll
+    for (int j = 0; j < 6; ++j) ph[j] = 0;
+    t = t0 = __builtin_amdgcn_s_memtime();
+    r0 = __builtin_amdgcn_s_memrealtime();
+  }
+  __device__ void tick(int j) {
+    const uint64_t x = __builtin_amdgcn_s_memtime();
+    ph[j] += x - t;
+    t = x;
+  }
+  // slot: workgroup * 8 + wave; lane 0 writes (vector stores)
+  __device__ void finish(unsigned long long* out, int slot) {
+    const uint64_t t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    if (out == nullptr || (threadIdx.x & 63) != 0) return;
+    const rsrc_t R = make_rsrc(out + (size_t)slot * 8, 64);
+    const uint64_t v[8] = {ph[0], ph[1], ph[2], ph[3], ph[4], ph[5], t1 - t0, r1 - r0};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) bst64(R, make_uint2((uint32_t)v[j], (uint32_t)(v[j] >> 32)), 8u * j, 0);
+  }
+};
+
 // VAR selects the features an instance compiles: 1 = training with fp16 checkpoints (every
 // chunk, whole-width rows, no slices), 2 = no checkpoints and no slices (inference), 0 = the
 // rest (fp32 or paired checkpoints, channel slices).  Fewer live values keep the scalar
@@ -317,12 +360,16 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
     if (NTs > 1) load_chunk(cidx(1));
   }
 
+  PhaseClock<kPhaseClocks> clk;
+  clk.start();
   for (int it = 0; it < NTs; ++it) {
     const int c = cidx(it);
     const int t0 = c * C;
     const int nval = min(C, L - t0);
 
+    if (it > 0) clk.tick(5);
     __syncthreads();  // B1: the previous chunk's planes and the totals are no longer read
+    clk.tick(0);
     write_planes();
     if constexpr (VAR == 1) ckpt_max();
     // the state factors of this chunk, kept for its update (stage() overwrites them)
@@ -330,7 +377,9 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) { cga[r] = sga[r]; cbe[r] = sbe[r]; }
     cumsum();         // (past the last chunk: zeros, never staged into planes)
+    clk.tick(1);
     __syncthreads();  // B2: planes and the next chunk's totals visible
+    clk.tick(2);
 
     // H^T plane = alpha S (the state entering this chunk; read after B3 only)
 #pragma unroll
@@ -414,7 +463,9 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
           S[i][r] = x;
         }
     }
+    clk.tick(3);
     __syncthreads();  // B3: D tiles visible
+    clk.tick(4);
 
     // ---------------- output block: token block R, column tiles 2 nh, 2 nh + 1
     bf16x8 fxh[KP / 32], fxl[KP / 32];
@@ -471,6 +522,9 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
     }
   }
 
+  if (NTs > 0) clk.tick(5);
+  clk.finish(p.clocks, blockIdx.x * NW + wave);
+
   if (p.s_fin) {
 #pragma unroll
     for (int i = 0; i < NHT; ++i) {
@@ -516,5 +570,33 @@ hipError_t launch_gla_pipe(const SweepParams& p, hipStream_t s) {
 
 template hipError_t launch_gla_pipe<false>(const SweepParams&, hipStream_t);
 template hipError_t launch_gla_pipe<true>(const SweepParams&, hipStream_t);
+
+#ifdef TOPS_PHASE_CLOCKS
+// Instrumented build only (libtops_pipe_clocks.so, pallas-kernel_amd/phase_clocks.py): one
+// pipelined sweep over B fixed-length sequences of bf16 q, k, y (v forward, dO reverse) and
+// fp32 per-channel log gates g [B, T, H, K]; out [B, T, H, V] bf16; fp16 checkpoints when
+// ckpt16 / ckpt_scale are given (the training instance), none otherwise (inference); the
+// phase clocks of every wave into clocks [B * H * ceil(V / 64), 8, 8].
+extern "C" int tops_pipe_phase_clocks(const void* q, const void* k, const float* g, const void* y,
+                                      void* out, void* ckpt16, float* ckpt_scale,
+                                      unsigned long long* clocks, int B, int T, int H, int K,
+                                      int V, int rev, float scale, void* stream) {
+  if (!q || !k || !g || !y || !out || !clocks || (!ckpt16) != (!ckpt_scale) || B <= 0 || T <= 0 ||
+      H <= 0 || K <= 0 || K > 128 || V <= 0 || K % 4 || V % 8)
+    return (int)hipErrorInvalidValue;
+  SweepParams p{};
+  p.q = q; p.k = k; p.g = g; p.y = y; p.out = out;
+  p.ckpt = (float*)ckpt16;
+  p.ckpt16 = ckpt16 != nullptr;
+  p.ckpt_scale = ckpt_scale;
+  p.B = B; p.T = T; p.H = H; p.K = K; p.V = V; p.N = B; p.NV = (V + 63) / 64;
+  p.scale = scale;
+  p.gate_mode = kGateK;
+  p.clocks = clocks;
+  const hipError_t e = rev ? launch_gla_pipe<true>(p, (hipStream_t)stream)
+                           : launch_gla_pipe<false>(p, (hipStream_t)stream);
+  return (int)e;
+}
+#endif
 
 }  // namespace tops

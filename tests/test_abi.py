@@ -114,3 +114,22 @@ def test_decode_routing_reads_no_device_boundaries():
     assert decode_sized(8, torch.empty(3, dtype=torch.int32, device="meta"))       # mean 4
     assert not decode_sized(9, torch.empty(3, dtype=torch.int32, device="meta"))   # mean 4.5
     assert not decode_sized(0, torch.empty(1, dtype=torch.int32, device="meta"))   # no sequence
+
+
+def test_phase_clock_library_is_separate_and_checks_arguments():
+    """The instrumented sweep (phase clocks) is its own library: the regular one does not
+    export its entry, and the entry rejects missing buffers and unsupported shapes on the
+    host, before any launch."""
+    from tops import _native as N
+    assert not hasattr(N.lib(), "tops_pipe_phase_clocks")
+    path = os.path.join(ROOT, "pallas-kernel_amd", "tops", "_lib", "libtops_pipe_clocks.so")
+    if not os.path.exists(path):
+        pytest.skip("instrumented library not built (build.py --phase-clocks)")
+    f = ctypes.CDLL(path).tops_pipe_phase_clocks
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p] * 8 + [ctypes.c_int] * 6 + [ctypes.c_float, ctypes.c_void_p]
+    p = ctypes.c_void_p(8)
+    # no clock buffer; a checkpoint buffer without its factors; K over one tile
+    assert f(p, p, p, p, p, None, None, None, 1, 64, 1, 64, 64, 0, 1.0, None) != 0
+    assert f(p, p, p, p, p, p, None, p, 1, 64, 1, 64, 64, 0, 1.0, None) != 0
+    assert f(p, p, p, p, p, None, None, p, 1, 64, 1, 256, 64, 0, 1.0, None) != 0
