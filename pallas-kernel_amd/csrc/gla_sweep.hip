@@ -98,7 +98,11 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 
   __shared__ __attribute__((aligned(16))) uint16_t sX[(XL ? 2 : 1) * C * LQ];
   __shared__ __attribute__((aligned(16))) uint16_t sZ[(XL ? 2 : 1) * C * LQ];
-  __shared__ __attribute__((aligned(16))) uint16_t sZT[(XL ? 2 : 1) * KP * LT];
+  // the reverse delta rule's w^T plane [K][C]; the forward delta rule's causal D tiles
+  // (10 tiles x 64 lanes x 16 B, written after the output pass while the Z~ plane is still
+  // read by the state update).  The other sweeps read Z~ transposed out of its row-major
+  // plane and need neither.
+  __shared__ __attribute__((aligned(16))) uint16_t sZT[REV_DELTA ? 2 * KP * LT : (FWD_DELTA ? 10 * 64 * 8 : 1)];
   __shared__ __attribute__((aligned(16))) uint16_t sYT[(SY ? 2 : 1) * BV * LT];
   // (the reverse delta rule reuses sHT for the [BV][LT] dv_new^T plane: size for both)
   constexpr int NHTS = 2 * BV * (REV_DELTA && LT > LH ? LT : LH);
@@ -111,7 +115,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   // Causal D tiles of the chunk shared through LDS (bf16 hi/lo per lane, 10 tiles x 1 KB):
   // each tile is computed once instead of once per column-tile wave, and the work is spread
   // evenly over the waves.  Only where the 160 KB budget allows (not the delta sweeps).
-  constexpr int LDS_BASE = 2 * ((XL ? 2 : 1) * C * LQ) * 2 + (XL ? 2 : 1) * KP * LT * 2 +
+  constexpr int LDS_BASE = 2 * ((XL ? 2 : 1) * C * LQ) * 2 +
+                           (REV_DELTA ? 2 * KP * LT * 2 : (FWD_DELTA ? 10 * 64 * 16 : 0)) +
                            (SY ? 2 : 1) * BV * LT * 2 + NHTS * 2 + NSGH * KP * 4 +
                            (GV ? (C * LE + 4 * BV) * 4 : 0);
   constexpr bool SHARED_D = !DELTA && !ST && LDS_BASE + 10 * 64 * 16 <= 160 * 1024;
@@ -123,10 +128,9 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 
   const Plane PX{sX, XL ? sX + C * LQ : sX, LQ};
   const Plane PZ{sZ, XL ? sZ + C * LQ : sZ, LQ};
-  const Plane PZt{sZT, XL ? sZT + KP * LT : sZT, LT};
   const Plane PYt{sYT, SY ? sYT + BV * LT : sYT, LT};
   const Plane PHt{sHT, sHT + BV * LH, LH};
-  // reverse delta rule: once the output pass is done, w^T [K][C] reuses sZT and
+  // reverse delta rule: once the output pass is done, w^T [K][C] goes to sZT and
   // dv_new^T [BV][C] reuses sHT
   const Plane PWt{sZT, sZT + KP * LT, LT};
   const Plane PDt{sHT, sHT + BV * LT, LT};
@@ -530,10 +534,9 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
         }
       }
     }
-    // ---------------- gated operands for the staging rows.  Z~ is split into bf16 hi / lo once;
-    // the transposed plane reuses those halves, regrouped per channel with byte permutes.
+    // ---------------- gated operands for the staging rows (Z~ row-major: the state update
+    // reads it transposed, ds_read_b64_tr_b16)
     {
-      float zt[4][RPT];
       uint32_t zh[RPT][2], zl[RPT][2];
 #pragma unroll
       for (int i = 0; i < RPT; ++i) {
@@ -556,37 +559,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
         if constexpr (!ST) put_n<XL, 4>(PX, r0 + i, c0, xx);
         split_bf16x2(zz[0], zz[1], zh[i][0], zl[i][0]);
         split_bf16x2(zz[2], zz[3], zh[i][1], zl[i][1]);
-        if constexpr (!ST) {
-          *(uint2*)(PZ.hi + (r0 + i) * PZ.ld + c0) = make_uint2(zh[i][0], zh[i][1]);
-          if constexpr (XL) *(uint2*)(PZ.lo + (r0 + i) * PZ.ld + c0) = make_uint2(zl[i][0], zl[i][1]);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) zt[j][i] = zz[j];
-      }
-      if constexpr (RPT >= 2) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          // channel j of rows (2m, 2m + 1): the low (j even) or high (j odd) bf16 of each word
-          const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-          uint32_t th[RPT / 2], tl[RPT / 2];
-#pragma unroll
-          for (int m = 0; m < RPT / 2; ++m) {
-            th[m] = __builtin_amdgcn_perm(zh[2 * m + 1][j >> 1], zh[2 * m][j >> 1], sel);
-            tl[m] = __builtin_amdgcn_perm(zl[2 * m + 1][j >> 1], zl[2 * m][j >> 1], sel);
-          }
-          uint16_t* ph = PZt.hi + (c0 + j) * PZt.ld + r0;
-          uint16_t* pl = PZt.lo + (c0 + j) * PZt.ld + r0;
-          if constexpr (RPT == 4) {
-            *(uint2*)ph = make_uint2(th[0], th[1]);
-            if constexpr (XL) *(uint2*)pl = make_uint2(tl[0], tl[1]);
-          } else {
-            *(uint32_t*)ph = th[0];
-            if constexpr (XL) *(uint32_t*)pl = tl[0];
-          }
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) put_n<XL, RPT>(PZt, c0 + j, r0, zt[j]);
+        *(uint2*)(PZ.hi + (r0 + i) * PZ.ld + c0) = make_uint2(zh[i][0], zh[i][1]);
+        if constexpr (XL) *(uint2*)(PZ.lo + (r0 + i) * PZ.ld + c0) = make_uint2(zl[i][0], zl[i][1]);
       }
       if constexpr (!FWD_DELTA) {
         float ya[YR], yb[YR];
@@ -631,8 +605,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
           const bf16x8 bh = PYt.hi8(16 * nn + l16, 32 * kc + 8 * lg);
           bf16x8 bl = bh;
           if constexpr (SY) bl = PYt.lo8(16 * nn + l16, 32 * kc + 8 * lg);
-          d1[i] = mma<true, SY>(d1[i], PZt.hi8(16 * msb + l16, 32 * kc + 8 * lg),
-                                PZt.lo8(16 * msb + l16, 32 * kc + 8 * lg), bh, bl);
+          d1[i] = mma<true, SY>(d1[i], tr_read8(PZ.hi, PZ.ld, 32 * kc, 16 * msb, lane),
+                                tr_read8(PZ.lo, PZ.ld, 32 * kc, 16 * msb, lane), bh, bl);
         }
       }
     }
@@ -646,8 +620,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
         bf16x8 zh[C / 32], zl[C / 32], yh[NHT][C / 32], yl[NHT][C / 32];
 #pragma unroll
         for (int kc = 0; kc < C / 32; ++kc) {
-          zh[kc] = PZt.hi8(16 * msb + l16, 32 * kc + 8 * lg);
-          if constexpr (XL) zl[kc] = PZt.lo8(16 * msb + l16, 32 * kc + 8 * lg);
+          zh[kc] = tr_read8(PZ.hi, PZ.ld, 32 * kc, 16 * msb, lane);
+          if constexpr (XL) zl[kc] = tr_read8(PZ.lo, PZ.ld, 32 * kc, 16 * msb, lane);
 #pragma unroll
           for (int i = 0; i < NHT; ++i) {
             const int nn = (wave * NHT + i) % (BV / 16);
@@ -686,8 +660,10 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
             const bf16x8 bh = PYt.hi8(16 * nn + l16, 32 * kc + 8 * lg);
             bf16x8 bl = bh;
             if constexpr (SY) bl = PYt.lo8(16 * nn + l16, 32 * kc + 8 * lg);
-            d = mma<XL, SY>(d, PZt.hi8(16 * msb + l16, 32 * kc + 8 * lg),
-                            PZt.lo8(16 * msb + l16, 32 * kc + 8 * lg), bh, bl);
+            const bf16x8 zh8 = tr_read8(PZ.hi, PZ.ld, 32 * kc, 16 * msb, lane);
+            bf16x8 zl8 = zh8;
+            if constexpr (XL) zl8 = tr_read8(PZ.lo, PZ.ld, 32 * kc, 16 * msb, lane);
+            d = mma<XL, SY>(d, zh8, zl8, bh, bl);
           }
         } else {
           d = dsu[i];
@@ -868,8 +844,8 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
         }
         put_n<true, 4>(PYt, 16 * nn + l16, 16 * R + 4 * lg, vn);
       }
-      __syncthreads();  // B3: v_new^T plane complete; no wave reads the Z plane any more
-      uint4* zD = (uint4*)sZ;
+      __syncthreads();  // B3: v_new^T plane complete
+      uint4* zD = (uint4*)sZT;
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int t = wave + 8 * u;
