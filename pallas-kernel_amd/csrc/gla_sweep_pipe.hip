@@ -2,10 +2,11 @@
 // hot path: the forward of tops/ops/gla/chunk.py:1103-1199 and the state-gradient sweep of its
 // backward, chunk.py:1447-1509 with tops/ops/common/chunk_h.py:685-878).
 //
-// Same products, operand values, thread mappings and summation order as gla_sweep_kernel
-// (gla_sweep.hip, instance TIn = bf16, DELTA = ST = false, GK = true, YG = 0); the schedule
-// differs (the compiler may contract the fp32 state update differently, a last-bit
-// difference), and so do the planes: the state update and the intra output products read
+// Same products and operand values as gla_sweep_kernel (gla_sweep.hip, instance TIn = bf16,
+// DELTA = ST = false, GK = true, YG = 0); the schedule differs, the state is held transposed
+// (each lane keeps four adjacent V columns of one K row, so it needs one decay factor instead
+// of four and stores its fp16 checkpoint run directly; the state update computes S^T tiles,
+// a last-bit difference in the fp32 sums), and so do the planes: the state update and the intra output products read
 // Z~ and Y transposed out of their row-major planes (ds_read_b64_tr_b16) where the serial
 // kernel writes separate Z~^T / Y^T planes, 40 KB fewer LDS writes per chunk and 126 KB of
 // LDS instead of 163 KB.  The serial kernel runs each chunk as
@@ -93,7 +94,7 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
   static_assert(NQ % CQL == 0, "KP must be a multiple of 32");
   static_assert(CQL == 8 && SGL == 4, "the segment scan takes 8 column quads x 4 segments");
   static_assert(RPT == 1 || RPT == 2 || RPT == 4, "KP must be 32, 64 or 128");
-  constexpr int LQ = KP + 8, LY = BV + 8, LH = KP + 8;
+  constexpr int LQ = KP + 8, LY = BV + 8, LH = BV + 8;
   constexpr int NHT = (KP / 16) * (BV / 16) / NW;  // state tiles per wave
   constexpr int YR = C * BV / (2 * NTH);
   static_assert(YR == 4, "Y staging assumes 4 rows x 2 columns per thread");
@@ -102,7 +103,7 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t sX[2 * C * LQ];
   __shared__ __attribute__((aligned(16))) uint16_t sZ[2 * C * LQ];
   __shared__ __attribute__((aligned(16))) uint16_t sY[C * LY];
-  __shared__ __attribute__((aligned(16))) uint16_t sHT[2 * BV * LH];
+  __shared__ __attribute__((aligned(16))) uint16_t sH[2 * KP * LH];   // alpha S, [K][BV] hi / lo
   __shared__ __attribute__((aligned(16))) float sTot[NSGH * KP];
   __shared__ __attribute__((aligned(16))) uint4 sDt[10 * 64];
   __shared__ uint32_t sMx[NW];                // fp16 checkpoints: each wave's largest |S|
@@ -110,7 +111,7 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
   const Plane PX{sX, sX + C * LQ, LQ};
   const Plane PZ{sZ, sZ + C * LQ, LQ};
   const Plane PY{sY, sY, LY};   // Y = v (forward) or dO (reverse), [C][BV], bf16 as read
-  const Plane PHt{sHT, sHT + BV * LH, LH};
+  const Plane PH{sH, sH + KP * LH, LH};
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -172,17 +173,18 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
   const uint32_t offG = colok ? ((uint32_t)r0 * rowK + c0) * 4u : kOOB;
   const uint32_t offY = ycolok ? ((uint32_t)(yseg * YR) * rowV + yv) * ES : kOOB;
 
-  // ---- state tiles: tile i of this wave -> (msb, nn)
+  // ---- state tiles: tile i of this wave -> (msb, nn), held transposed: lane (l16, lg) has
+  // S[k = 16 msb + l16][v = 16 nn + 4 lg + r], r = 0..3 (four adjacent columns of one row)
   f32x4 S[NHT];
+  const int krow = 16 * msb + l16;
 #pragma unroll
   for (int i = 0; i < NHT; ++i) {
     const int nn = (wave * NHT + i) % (BV / 16);
-    const int vv = vt * BV + 16 * nn + l16;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int kr = 16 * msb + 4 * lg + r;
+      const int vv = vt * BV + 16 * nn + 4 * lg + r;
       float x = 0.f;
-      if (p.s0 && kr < K && vv < V) x = p.s0[((size_t)(n * H + hh) * LDK + kr) * V + vv];
+      if (p.s0 && krow < K && vv < V) x = p.s0[((size_t)(n * H + hh) * LDK + krow) * V + vv];
       S[i][r] = x;
     }
   }
@@ -220,7 +222,7 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
 
   // ---- the staged chunk: plane words and state factors, computed one chunk ahead
   uint32_t xh[RPT][2], xl[RPT][2], zh[RPT][2], zl[RPT][2], yw[YR];
-  float sga[4], sal[4], sbe[4];
+  float sga, sal, sbe;                 // factors of this lane's state row krow
   // partial gate cumsum of the raw chunk (thread rows, then the half-wave scan); the group
   // totals go to sTot.  The scan over the four row segments of a column quad (lanes cq,
   // cq + 8, cq + 16, cq + 24 of the half-wave) runs on the VALU (seg8x4_scan).
@@ -260,20 +262,14 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) gm[j] = 0.5f * gam[j];
-    float sgam[4] = {0.f, 0.f, 0.f, 0.f};
+    float sgam = 0.f;
 #pragma unroll
-    for (int s2 = 0; s2 < NSGH; ++s2) {
-      const float4 t = *(const float4*)(sTot + s2 * KP + 16 * msb + 4 * lg);
-      sgam[0] += t.x; sgam[1] += t.y; sgam[2] += t.z; sgam[3] += t.w;
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float g2 = 0.5f * sgam[r];
-      sga[r] = fast_exp2(sgam[r]);
-      sal[r] = REV ? fast_exp2(sgam[r] - g2) : scale * fast_exp2(g2);
-      sbe[r] = REV ? scale * fast_exp2(g2) : fast_exp2(sgam[r] - g2);
-      pin(sga[r]); pin(sal[r]); pin(sbe[r]);
-    }
+    for (int s2 = 0; s2 < NSGH; ++s2) sgam += sTot[s2 * KP + krow];
+    const float g2 = 0.5f * sgam;
+    sga = fast_exp2(sgam);
+    sal = REV ? fast_exp2(sgam - g2) : scale * fast_exp2(g2);
+    sbe = REV ? scale * fast_exp2(g2) : fast_exp2(sgam - g2);
+    pin(sga); pin(sal); pin(sbe);
   };
   auto stage_rows = [&](int i0, int i1) {
 #pragma unroll
@@ -332,9 +328,9 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
   auto store_ckpt = [&](int c) {
     if (!ckpt_on(c)) return;
     if constexpr (VAR == 1) {
-      store_state16<NHT, NW>(S, sMx, (uint16_t*)p.ckpt + ((size_t)(cbase + c) * H + hh) * LDK * V,
-                             p.ckpt_scale + ((size_t)(cbase + c) * H + hh) * p.NV + vt, K, V, vt,
-                             wave, msb, lane, tid);
+      store_state16_t<NHT, NW>(S, sMx, (uint16_t*)p.ckpt + ((size_t)(cbase + c) * H + hh) * LDK * V,
+                               p.ckpt_scale + ((size_t)(cbase + c) * H + hh) * p.NV + vt, K, V, vt,
+                               wave, msb, lane, tid);
       return;
     }
     const rsrc_t Rck = make_rsrc(p.ckpt + ((size_t)(cbase + c) * H + hh) * LDK * V,
@@ -342,12 +338,11 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
 #pragma unroll
     for (int i = 0; i < NHT; ++i) {
       const int nn = (wave * NHT + i) % (BV / 16);
-      const int kr = 16 * msb + 4 * lg;
-      const int vv = vt * BV + 16 * nn + l16;
-      const uint32_t vo = (kr < K && vv < V) ? ((uint32_t)kr * V + vv) * 4u : kOOB;  // K % 4 == 0
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        bst32(Rck, __float_as_uint(S[i][r]), vo, (uint32_t)(r * V * 4));
+      const int vv = vt * BV + 16 * nn + 4 * lg;
+      // (V % 8 == 0: vv < V keeps the four columns inside the row)
+      const uint32_t vo = (krow < K && vv < V) ? ((uint32_t)krow * V + vv) * 4u : kOOB;
+      bst128(Rck, make_uint4(__float_as_uint(S[i][0]), __float_as_uint(S[i][1]),
+                             __float_as_uint(S[i][2]), __float_as_uint(S[i][3])), vo, 0);
     }
   };
 
@@ -373,23 +368,20 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
     write_planes();
     if constexpr (VAR == 1) ckpt_max();
     // the state factors of this chunk, kept for its update (stage() overwrites them)
-    float cga[4], cbe[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) { cga[r] = sga[r]; cbe[r] = sbe[r]; }
+    const float cga = sga, cbe = sbe;
     cumsum();         // (past the last chunk: zeros, never staged into planes)
     clk.tick(1);
     __syncthreads();  // B2: planes and the next chunk's totals visible
     clk.tick(2);
 
-    // H^T plane = alpha S (the state entering this chunk; read after B3 only)
+    // H plane = alpha S (the state entering this chunk; read after B3 only)
 #pragma unroll
     for (int i = 0; i < NHT; ++i) {
       const int nn = (wave * NHT + i) % (BV / 16);
-      const int kr = 16 * msb + 4 * lg;
       float x[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) x[r] = sal[r] * S[i][r];
-      put_n<true, 4>(PHt, 16 * nn + l16, kr, x);
+      for (int r = 0; r < 4; ++r) x[r] = sal * S[i][r];
+      put_n<true, 4>(PH, krow, 16 * nn + 4 * lg, x);
     }
     store_ckpt(c);
 
@@ -446,9 +438,9 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
           fyh[i] = tr_read8(PY.hi, PY.ld, 32 * kc, 16 * nn, lane);
         }
 #pragma unroll
-        for (int i = 0; i < NHT; ++i) dsu[i] = mfma(fzl, fyh[i], dsu[i]);
+        for (int i = 0; i < NHT; ++i) dsu[i] = mfma(fyh[i], fzl, dsu[i]);
 #pragma unroll
-        for (int i = 0; i < NHT; ++i) dsu[i] = mfma(fzh, fyh[i], dsu[i]);
+        for (int i = 0; i < NHT; ++i) dsu[i] = mfma(fyh[i], fzh, dsu[i]);
       }
       if constexpr (RPT > 1) stage_rows(RPT / 2, RPT);
 #pragma unroll
@@ -458,7 +450,7 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
       for (int i = 0; i < NHT; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          float x = cga[r] * S[i][r] + cbe[r] * dsu[i][r];
+          float x = cga * S[i][r] + cbe * dsu[i][r];
           pin(x);
           S[i][r] = x;
         }
@@ -498,8 +490,8 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < KP / 32; ++kc)
-        acc = mma<true, true>(acc, PHt.hi8(16 * nn + l16, 32 * kc + 8 * lg),
-                              PHt.lo8(16 * nn + l16, 32 * kc + 8 * lg), fxh[kc], fxl[kc]);
+        acc = mma<true, true>(acc, tr_read8(PH.hi, PH.ld, 32 * kc, 16 * nn, lane),
+                              tr_read8(PH.lo, PH.ld, 32 * kc, 16 * nn, lane), fxh[kc], fxl[kc]);
 #pragma unroll
       for (int Pp = 0; Pp < 2; ++Pp) {
         const int P0 = 2 * Pp, P1 = 2 * Pp + 1;
@@ -529,11 +521,10 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
 #pragma unroll
     for (int i = 0; i < NHT; ++i) {
       const int nn = (wave * NHT + i) % (BV / 16);
-      const int vv = vt * BV + 16 * nn + l16;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int kr = 16 * msb + 4 * lg + r;
-        if (kr < K && vv < V) p.s_fin[((size_t)(n * H + hh) * LDK + kr) * V + vv] = S[i][r];
+        const int vv = vt * BV + 16 * nn + 4 * lg + r;
+        if (krow < K && vv < V) p.s_fin[((size_t)(n * H + hh) * LDK + krow) * V + vv] = S[i][r];
       }
     }
   }

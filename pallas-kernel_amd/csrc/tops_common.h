@@ -533,4 +533,32 @@ __device__ __forceinline__ void store_state16(const f32x4 (&S)[NHT], const uint3
   }
 }
 
+// The same checkpoint from transposed fragments (lane (l16, lg) of tile (msb, nn) holding
+// S[16 msb + l16][16 nn + 4 lg + r], r = 0..3): each lane's four values are one 8-byte run
+// of a row, stored directly.
+template <int NHT, int NW>
+__device__ __forceinline__ void store_state16_t(const f32x4 (&S)[NHT], const uint32_t* smx,
+                                                uint16_t* base, float* fac, int K, int V, int vt,
+                                                int wave, int msb, int lane, int tid) {
+  uint32_t m = smx[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) m = max(m, smx[w]);
+  int ex = (int)((m >> 23) & 0xffu) - 127;
+  ex = ex < -100 ? -100 : ex;
+  const float sinv = __uint_as_float((uint32_t)(141 - ex) << 23);
+  if (tid == 0) *fac = __uint_as_float((uint32_t)(113 + ex) << 23);
+  const rsrc_t R = make_rsrc(base, (long long)K * V * 2);
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int kr = 16 * msb + l16;
+#pragma unroll
+  for (int i = 0; i < NHT; ++i) {
+    const int nn = (wave * NHT + i) % 4;
+    const int vv = vt * 64 + 16 * nn + 4 * lg;
+    // (V % 8 == 0: vv < V keeps the run inside the row)
+    const uint32_t vo = (kr < K && vv < V) ? ((uint32_t)kr * V + vv) * 2u : kOOB;
+    bst64(R, make_uint2(pack_f16x2(S[i][0] * sinv, S[i][1] * sinv),
+                        pack_f16x2(S[i][2] * sinv, S[i][3] * sinv)), vo, 0);
+  }
+}
+
 }  // namespace tops
