@@ -93,8 +93,10 @@ def run(B, T, H, K, V, reps=5, seed=0):
         w01 = per_chunk[:, :2].mean(dim=(0, 1))
         w27 = per_chunk[:, 2:].mean(dim=(0, 1))
         loop_us = float(acc[..., 6].mean()) / mhz
+        perw = per_chunk.mean(dim=0)                       # [wave, phase]
         res[name] = dict(
-            phases={p: dict(all=float(allw[i]), waves01=float(w01[i]), waves27=float(w27[i]))
+            phases={p: dict(all=float(allw[i]), waves01=float(w01[i]), waves27=float(w27[i]),
+                            per_wave=[round(float(perw[w, i])) for w in range(NW)])
                     for i, p in enumerate(PHASES)},
             cycles_per_chunk=float(allw.sum()), clock_mhz=mhz,
             us_per_chunk=float(allw.sum()) / mhz, loop_us=loop_us,
@@ -117,6 +119,11 @@ def markdown(res, shape):
             lines.append(f"| {p} | {d['all']:.0f} | {d['waves01']:.0f} | {d['waves27']:.0f} | "
                          f"{100 * d['all'] / tot:.1f}% |")
         lines.append(f"| total | {tot:.0f} | | | |\n")
+        lines.append("| interval | " + " | ".join(f"wave {w}" for w in range(NW)) + " |")
+        lines.append("|---|" + "---|" * NW)
+        for p, d in r["phases"].items():
+            lines.append(f"| {p} | " + " | ".join(str(x) for x in d["per_wave"]) + " |")
+        lines.append("")
     return "\n".join(lines)
 
 
