@@ -177,16 +177,17 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
   // S[k = 16 msb + l16][v = 16 nn + 4 lg + r], r = 0..3 (four adjacent columns of one row)
   f32x4 S[NHT];
   const int krow = 16 * msb + l16;
+  // s0 / s_fin rows of this (sequence, head): one 16-byte run per tile and lane (V % 8 == 0
+  // keeps a run that starts inside a row inside it); no s0: an empty range loads zeros
+  const size_t s_base = (size_t)(n * H + hh) * LDK * V;
+  auto srun = [&](int i) {
+    const int vv = vt * BV + 16 * ((wave * NHT + i) % (BV / 16)) + 4 * lg;
+    return (krow < K && vv < V) ? ((uint32_t)krow * V + vv) * 4u : kOOB;
+  };
+  {
+    const rsrc_t Rs0 = make_rsrc(p.s0 ? p.s0 + s_base : nullptr, p.s0 ? (long long)LDK * V * 4 : 0);
 #pragma unroll
-  for (int i = 0; i < NHT; ++i) {
-    const int nn = (wave * NHT + i) % (BV / 16);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int vv = vt * BV + 16 * nn + 4 * lg + r;
-      float x = 0.f;
-      if (p.s0 && krow < K && vv < V) x = p.s0[((size_t)(n * H + hh) * LDK + krow) * V + vv];
-      S[i][r] = x;
-    }
+    for (int i = 0; i < NHT; ++i) S[i] = __builtin_bit_cast(f32x4, bld128(Rs0, srun(i), 0));
   }
   __builtin_amdgcn_s_waitcnt(0);
 
@@ -518,15 +519,9 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
   clk.finish(p.clocks, blockIdx.x * NW + wave);
 
   if (p.s_fin) {
+    const rsrc_t Rsf = make_rsrc(p.s_fin + s_base, (long long)LDK * V * 4);
 #pragma unroll
-    for (int i = 0; i < NHT; ++i) {
-      const int nn = (wave * NHT + i) % (BV / 16);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int vv = vt * BV + 16 * nn + 4 * lg + r;
-        if (krow < K && vv < V) p.s_fin[((size_t)(n * H + hh) * LDK + krow) * V + vv] = S[i][r];
-      }
-    }
+    for (int i = 0; i < NHT; ++i) bst128(Rsf, __builtin_bit_cast(uint4, S[i]), srun(i), 0);
   }
 }
 
