@@ -269,6 +269,15 @@ int tops_gla_chunk_fwd_gv(const void* q, const void* k, const void* v, const flo
                           const float* h0, void* o, float* ht, const int32_t* cu_seqlens, int B,
                           int T, int H, int K, int V, int N, int dtype, float scale, void* stream);
 
+/* The same recurrence with o written in fp32 (o32 [B,T,H,V]) instead of bf16.  The chunked
+ * backward of fused_recurrent_gla with gv (tops/ops/gla/fused_recurrent.py:496-619) uses it
+ * twice: for the forward output, which the gate gradient needs in fp32, and, on time-reversed
+ * inputs, for dv (the value-gated reverse recurrence of the state gradient, as a forward). */
+int tops_gla_chunk_fwd_gv32(const void* q, const void* k, const void* v, const float* gv,
+                            const float* h0, float* o32, float* ht, const int32_t* cu_seqlens,
+                            int B, int T, int H, int K, int V, int N, int dtype, float scale,
+                            void* stream);
+
 /* Simple GLA: one log-gate per (token, head) -- g [B,T,H] fp32 -- or a constant per-head
  * log-decay g_gamma [H] fp32; pass exactly one.  The state recurrence is GLA's with the
  * gate shared by all K channels.  Replaces tops.ops.simple_gla.chunk_simple_gla_fwd /

@@ -1258,11 +1258,11 @@ extern "C" int tops_chunk_reverse_fwd(const void* q, const void* k, const void* 
   return TOPS_OK;
 }
 
-extern "C" int tops_gla_chunk_fwd_gv(const void* q, const void* k, const void* v, const float* gv,
-                                     const float* h0, void* o, float* ht,
-                                     const int32_t* cu_seqlens, int B, int T, int H, int K, int V,
-                                     int N, int dtype, float scale, void* stream) {
-  if (!q || !k || !v || !gv || !o) return tops_set_error(TOPS_ERR_NULL, "gla_chunk_fwd_gv: null tensor");
+static int gla_chunk_fwd_gv_impl(const void* q, const void* k, const void* v, const float* gv,
+                                 const float* h0, void* o, float* o32, float* ht,
+                                 const int32_t* cu_seqlens, int B, int T, int H, int K, int V,
+                                 int N, int dtype, float scale, void* stream) {
+  if (!q || !k || !v || !gv || (!o && !o32)) return tops_set_error(TOPS_ERR_NULL, "gla_chunk_fwd_gv: null tensor");
   if (dtype != TOPS_BF16)
     return tops_set_error(TOPS_ERR_DTYPE, "gla_chunk_fwd_gv: the value-gate sweep takes TOPS_BF16");
   if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || N <= 0)
@@ -1273,9 +1273,32 @@ extern "C" int tops_gla_chunk_fwd_gv(const void* q, const void* k, const void* v
   if (!cu_seqlens && N != B) return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd_gv: N must equal B");
   if ((long long)kChunk * H * (K > V ? K : V) * 4 >= (1LL << 31))
     return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd_gv: H * max(K, V) too large for 32-bit chunk offsets");
-  SweepParams p{q, k, gv, v, h0, o, ht, nullptr, cu_seqlens, nullptr,
+  SweepParams p{q, k, gv, v, h0, o32 ? (void*)o32 : o, ht, nullptr, cu_seqlens, nullptr,
                 B, T, H, K, V, N, (V + 63) / 64, scale, kGateGamma};
+  if (o32) {
+    // the output in fp32 only (acc_mode 1 writes the sum buffer and not the bf16 output)
+    p.acc32 = o32;
+    p.acc_mode = 1;
+  }
   hipError_t e = launch_gla_sweep_gv(p, (hipStream_t)stream);
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   return TOPS_OK;
+}
+
+extern "C" int tops_gla_chunk_fwd_gv(const void* q, const void* k, const void* v, const float* gv,
+                                     const float* h0, void* o, float* ht,
+                                     const int32_t* cu_seqlens, int B, int T, int H, int K, int V,
+                                     int N, int dtype, float scale, void* stream) {
+  if (!o) return tops_set_error(TOPS_ERR_NULL, "gla_chunk_fwd_gv: null tensor");
+  return gla_chunk_fwd_gv_impl(q, k, v, gv, h0, o, nullptr, ht, cu_seqlens, B, T, H, K, V, N,
+                               dtype, scale, stream);
+}
+
+extern "C" int tops_gla_chunk_fwd_gv32(const void* q, const void* k, const void* v, const float* gv,
+                                       const float* h0, float* o32, float* ht,
+                                       const int32_t* cu_seqlens, int B, int T, int H, int K,
+                                       int V, int N, int dtype, float scale, void* stream) {
+  if (!o32) return tops_set_error(TOPS_ERR_NULL, "gla_chunk_fwd_gv32: null tensor");
+  return gla_chunk_fwd_gv_impl(q, k, v, gv, h0, nullptr, o32, ht, cu_seqlens, B, T, H, K, V, N,
+                               dtype, scale, stream);
 }

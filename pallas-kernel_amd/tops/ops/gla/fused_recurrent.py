@@ -18,8 +18,9 @@ cu_seqlens.  Two HIP implementations of the same recurrence are used:
     the forward recurrence on every sequence's time-reversed inputs: the inputs are reversed
     per sequence, swept forward, and the output reversed back (the reversal is part of the
     autograd graph);
-  * with gv and without gk, a forward that needs no gradient (bf16, K <= 128) runs chunkwise
-    on the forward sweep with the gate applied per V column (tops_gla_chunk_fwd_gv);
+  * with gv and without gk (bf16, K, V <= 128), the forward runs chunkwise on the forward
+    sweep with the gate applied per V column (tops_gla_chunk_fwd_gv); with gradients the
+    backward is chunked too, on kernels of the same families (_GvChunk below);
   * otherwise with gv, the per-token kernels of gla_recurrent.hip (state in registers, one
     token at a time) run the forward, a replay + reverse backward and the gate-gradient
     suffix sums.
@@ -225,6 +226,131 @@ def gv_chunk_native(q, k, v, gv, initial_state, scale, output_final_state, cu_se
     return o, ht
 
 
+def _host_cu(cu_seqlens):
+    if cu_seqlens is None:
+        return None
+    return [int(x) for x in (cu_seqlens.tolist() if isinstance(cu_seqlens, torch.Tensor) else cu_seqlens)]
+
+
+def _gv_chunk_train_ok(q, v, gk, gv, reverse, cu_seqlens):
+    """Whether a gv-only call with gradients runs on the chunk kernels (_GvChunk): bf16,
+    K, V <= 128 and multiples of 8, and no sequence-parallel split of the sweeps it uses."""
+    if gv is None or gk is not None or reverse or q.dtype != torch.bfloat16:
+        return False
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    if K > 128 or V > 128 or K % 8 or V % 8:
+        return False
+    plan = ChunkPlan(B, T, cu_seqlens, q.device)
+    return plan.segments(H, V) is None and plan.segments(H, K) is None
+
+
+def _seq_reverse_cumsum(x, T, cu):
+    """Suffix sums along time within every sequence of x [B, T, ...] (varlen: B == 1, cu
+    the host boundaries)."""
+    if cu is None:
+        return x.flip(1).cumsum(1).flip(1)
+    rev = time_reversal(T, cu, x.device)
+    xr = x.index_select(1, rev)                       # every sequence reversed in place
+    cs = xr.cumsum(1)
+    starts = torch.tensor(cu[:-1], device=x.device)
+    lens = torch.tensor([cu[i + 1] - cu[i] for i in range(len(cu) - 1)], device=x.device)
+    prev = cs.index_select(1, (starts - 1).clamp(min=0))
+    prev = prev * (starts > 0).to(x.dtype).view(1, -1, *([1] * (x.dim() - 2)))
+    cs = cs - prev.repeat_interleave(lens, dim=1)
+    return cs.index_select(1, rev)
+
+
+class _GvChunk(torch.autograd.Function):
+    """fused_recurrent_gla with gv and without gk, forward and backward on chunk kernels
+    (gradients of tops/ops/gla/fused_recurrent.py:496-619).  With S_t = S_(t-1) diag(a_t) +
+    k_t v_t^T (a_t = exp(gv_t)), o_t = scale S_t^T q_t and dS_t the gradient reaching S_t:
+      * dq_t = scale S_t dO_t.  S^T follows the key-gated recurrence S^T_t = diag(a_t) S^T_(t-1)
+        + v_t k_t^T, so dq is the key-gated chunk forward with queries dO, keys v, values k,
+        gate gv and initial state h0^T;
+      * dk_t = dS_t v_t, dS^T_t = diag(a_(t+1)) dS^T_(t+1) + scale dO_t q_t^T: the reverse
+        chunk sweep (fused_recurrent's reverse=True recurrence) with queries v, keys dO, values
+        q, the gate of the next token (0 at a sequence's last), initial state dht^T / scale and
+        output scale; its final state gives dh0 = dS_1 diag(a_1);
+      * dv_t = dS_t^T k_t: in reversed time dS is a value-gated forward recurrence, so dv is the
+        value-gate forward on every sequence reversed, with queries k, keys q, values dO, the
+        shifted gate, initial state dht / scale (fp32 output);
+      * dgv_t = sum over t' >= t of (o_t' dO_t' - v_t' dv_t') + sum_k (dht * ht)[k, :], the
+        per-column identity of the gated recurrence (o in fp32 from the forward)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, gv, h0, scale, cu_seqlens):
+        B, T, H, K = q.shape
+        V = v.shape[-1]
+        plan = ChunkPlan(B, T, cu_seqlens, q.device)
+        q, k, v = (x.contiguous() for x in (q, k, v))
+        gv32, h032 = _f32(gv), _f32(h0)
+        o32 = torch.empty(B, T, H, V, device=q.device, dtype=torch.float32)
+        ht = torch.empty(plan.N, H, K, V, device=q.device, dtype=torch.float32)
+        N.call("tops_gla_chunk_fwd_gv32", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gv32), N.ptr(h032),
+               N.ptr(o32), N.ptr(ht), N.ptr(plan.cu_dev), B, T, H, K, V, plan.N,
+               N.dtype_code(q.dtype), float(scale), N.stream())
+        ctx.save_for_backward(q, k, v, gv32, h032, o32, ht)
+        ctx.scale, ctx.cu = scale, cu_seqlens
+        ctx.dtypes = (gv.dtype, None if h0 is None else h0.dtype)
+        return o32.to(q.dtype), ht
+
+    @staticmethod
+    def backward(ctx, do, dht):
+        from .chunk import chunk_gla
+        q, k, v, gv, h0, o32, ht = ctx.saved_tensors
+        scale, cu = ctx.scale, ctx.cu
+        B, T, H, K = q.shape
+        V = v.shape[-1]
+        dev = q.device
+        plan = ChunkPlan(B, T, cu, dev)
+        cu_h = _host_cu(cu)
+        do = do.contiguous().to(q.dtype)
+        dht32 = None if dht is None else dht.to(torch.float32).contiguous()
+        # dq: the key-gated forward on the transposed state
+        h0t = None if h0 is None else h0.transpose(-1, -2).contiguous()
+        dq, _ = chunk_gla(do, v, k, gv, scale=scale, initial_state=h0t, output_final_state=False,
+                          cu_seqlens=cu)
+        # the gate of the next token, 0 at the last token of every sequence
+        gsh = torch.zeros_like(gv)
+        gsh[:, :-1] = gv[:, 1:]
+        if cu_h is not None:
+            gsh[0, torch.tensor(cu_h[1:], device=dev) - 1] = 0.0
+        # dk (and dh0): the reverse sweep on the transposed state gradient
+        s0 = None if dht32 is None else (dht32.transpose(-1, -2) / scale).contiguous()
+        r = reverse_chunk_native(v, do, q, "k", gsh, s0, scale, True, cu)
+        if r is None:
+            r = _reversed_chunk(lambda q_, k_, v_, g_, **kw: chunk_gla(q_, k_, v_, g_, **kw),
+                                v, do, q, gsh, cu, scale=scale, initial_state=s0,
+                                output_final_state=True)
+        dk, hts = r
+        dh0 = None
+        if h0 is not None:
+            first = gv[:, 0] if cu_h is None else gv[0, torch.tensor(cu_h[:-1], device=dev)]
+            dh0 = (scale * hts.transpose(-1, -2)) * torch.exp(first).unsqueeze(-2)
+        # dv: the value-gate forward in reversed time (fp32 output)
+        rev = time_reversal(T, cu, dev)
+        flip = (lambda x: x.index_select(1, rev).contiguous())
+        dv32 = torch.empty(B, T, H, V, device=dev, dtype=torch.float32)
+        s0v = None if dht32 is None else (dht32 / scale).contiguous()
+        N.call("tops_gla_chunk_fwd_gv32", N.ptr(flip(k)), N.ptr(flip(q)), N.ptr(flip(do)),
+               N.ptr(flip(gsh)), N.ptr(s0v), N.ptr(dv32), None, N.ptr(plan.cu_dev), B, T, H, K, V,
+               plan.N, N.dtype_code(q.dtype), float(scale), N.stream())
+        dv32 = dv32.index_select(1, rev)
+        # dgv: suffix sums of o dO - v dv, plus the final state's term
+        dgv = _seq_reverse_cumsum(o32 * do.to(torch.float32) - v.to(torch.float32) * dv32, T, cu_h)
+        if dht32 is not None:
+            c = (dht32 * ht).sum(-2)                                   # [N, H, V]
+            if cu_h is None:
+                dgv = dgv + c.unsqueeze(1)
+            else:
+                lens = torch.tensor([cu_h[i + 1] - cu_h[i] for i in range(len(cu_h) - 1)], device=dev)
+                dgv = dgv + c.repeat_interleave(lens, dim=0).unsqueeze(0)
+        gdt, hdt = ctx.dtypes
+        return (dq, dk, dv32.to(v.dtype), dgv.to(gdt), None if dh0 is None else dh0.to(hdt),
+                None, None)
+
+
 DECODE_MAX_TOKENS = 4    # beyond this the chunk kernels are faster (measured at K = V = 128)
 
 
@@ -305,6 +431,9 @@ def fused_recurrent_gla(q, k, v, gk=None, gv=None, scale=None, initial_state=Non
         r = gv_chunk_native(q, k, v, gv, initial_state, scale, output_final_state, cu_seqlens)
         if r is not None:
             return r
+        if _gv_chunk_train_ok(q, v, gk, gv, reverse, cu_seqlens):
+            o, ht = _GvChunk.apply(q, k, v, gv, initial_state, float(scale), cu_seqlens)
+            return o, (ht if output_final_state else None)
     if wide and not _chunked(gv, reverse, K, V):
         return _sliced(q, k, v, gk, gv, scale, initial_state, output_final_state, reverse,
                        cu_seqlens)

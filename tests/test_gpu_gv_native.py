@@ -6,8 +6,9 @@ run S_t = S_(t-1) diag(exp gv_t) + k_t v_t^T, o_t = scale S_t^T q_t
 (tops/cpu/ops/gla/fused_recurrent.py:51-167) in 64-token chunks on MFMA.  Checked against the
 oracle's per-token recurrence (oracle.gla.fused_recurrent_fwd) for h0, ragged T, T = 1, varlen
 with empty and one-token sequences, K or V not 64-aligned, V > 128 and gates up to a few
-units per token; every case checks that the chunk entry point ran.  Calls it does not take
-(gradients wanted, fp32 inputs) keep the per-token kernel, also checked.
+units per token; every case checks that the chunk entry point ran.  With gradients wanted
+(bf16) the chunked training path runs instead (tests/test_gpu_gv_train.py checks its
+gradients); fp32 inputs keep the per-token kernel, also checked.
 Tolerance: bf16 2e-3 (relative L2).
 """
 import numpy as np
@@ -103,8 +104,9 @@ def test_gv_fwd_api(cuda_device, calls):
 
 
 @pytest.mark.parametrize("case", ["grad", "fp32"])
-def test_gv_other_calls_keep_per_token_kernel(case, cuda_device, calls):
-    """With gradients wanted, or fp32 inputs, the per-token kernel runs (and matches)."""
+def test_gv_routing_with_gradients_and_fp32(case, cuda_device, calls):
+    """With gradients wanted (bf16) the chunked training path runs (its forward writes o in
+    fp32: tops_gla_chunk_fwd_gv32); fp32 inputs keep the per-token kernel.  Both match."""
     from tops.ops.gla import fused_recurrent_gla
     B, T, H, K, V = 1, 90, 2, 32, 32
     d = gla_inputs(B, T, H, K, V, seed=8, h0=True)
@@ -122,7 +124,11 @@ def test_gv_other_calls_keep_per_token_kernel(case, cuda_device, calls):
                                         initial_state=to_dev(d["h0"], torch.float32, cuda_device),
                                         output_final_state=True)
     torch.cuda.synchronize()
-    assert "tops_gla_chunk_fwd_gv" not in calls and "tops_gla_fused_recurrent_fwd" in calls
+    assert "tops_gla_chunk_fwd_gv" not in calls
+    if case == "grad":
+        assert "tops_gla_chunk_fwd_gv32" in calls and "tops_gla_fused_recurrent_fwd" not in calls
+    else:
+        assert "tops_gla_fused_recurrent_fwd" in calls
     ro, rht = O.fused_recurrent_fwd(seen(d["q"], dt), seen(d["k"], dt), seen(d["v"], dt), None, gv,
                                     initial_state=d["h0"], output_final_state=True)
     assert rel(host(o), ro) < tol(dt) and rel(host(ht), rht) < tol(dt)
