@@ -278,6 +278,39 @@ int tops_gla_chunk_fwd_gv32(const void* q, const void* k, const void* v, const f
                             int B, int T, int H, int K, int V, int N, int dtype, float scale,
                             void* stream);
 
+/* The state-gradient sweep of the value-gated recurrence (the dv of fused_recurrent_gla's
+ * backward with gv, tops/ops/gla/fused_recurrent.py:496-619): dS_t = dS_(t+1) diag(exp gv_(t+1))
+ * + scale q_t dO_t^T from dS_T = dht + scale q_T dO_T^T, dv_t = dS_t^T k_t written in fp32
+ * (dv32 [B,T,H,V]), and dh0 = dS_1 diag(exp gv_1) [N,H,K,V] fp32 or NULL.  q, k [B,T,H,K],
+ * dO [B,T,H,V] bf16 (dtype TOPS_BF16), gv [B,T,H,V] fp32 natural-log gates, dht [N,H,K,V]
+ * fp32 or NULL.  Chunked on MFMA (the reverse sweep with the gate per V column); K <= 128,
+ * K and V multiples of 8; varlen: cu_seqlens [N+1] with B == 1. */
+int tops_gla_chunk_bwd_dv_gv32(const void* q, const void* k, const void* do_, const float* gv,
+                               const float* dht, float* dv32, float* dh0,
+                               const int32_t* cu_seqlens, int B, int T, int H, int K, int V,
+                               int N, int dtype, float scale, void* stream);
+
+/* The state-gradient sweep of chunk_gla's backward (tops/ops/gla/chunk.py:1447-1509) without
+ * state checkpoints: dv [B,T,H,V] bf16 and dh0 [N,H,K,V] fp32 (or NULL) from q, k, g
+ * [B,T,H,K] (g fp32 per-channel natural-log gates), dO [B,T,H,V], dht [N,H,K,V] fp32 or
+ * NULL; bf16 (dtype TOPS_BF16), K <= 128, K and V multiples of 8; varlen: cu_seqlens [N+1]
+ * with B == 1.  The chunked backward of fused_recurrent_gla with gv uses it on the transposed
+ * state gradient, where its dv is dk. */
+int tops_gla_chunk_rev_dv(const void* q, const void* k, const float* g, const void* do_,
+                          const float* dht, void* dv, float* dh0, const int32_t* cu_seqlens, int B,
+                          int T, int H, int K, int V, int N, int dtype, float scale, void* stream);
+
+/* Gate gradient of the value-gated recurrence (the dgv of fused_recurrent_gla's backward with
+ * gv, tops/ops/gla/fused_recurrent.py:496-619; oracle tops/cpu/ops/gla/fused_recurrent.py:
+ * 171-358 keeps the same running suffix sums):
+ *     dgv[t, v] = sum over t' >= t in t's sequence of (o32 dO - v dv32)[t', v] + c[n, v],
+ * o32, dv32 [B,T,H,V] fp32; dO, v [B,T,H,V] bf16 (dtype TOPS_BF16); c [N,H,V] fp32 (the
+ * final-state term sum_k dht * ht) or NULL; dgv [B,T,H,V] fp32.  Varlen: cu_seqlens [N+1],
+ * B == 1. */
+int tops_gv_gate_grad(const float* o32, const void* dO, const void* v, const float* dv32,
+                      const float* c, float* dgv, const int32_t* cu_seqlens, int B, int T, int H,
+                      int V, int N, int dtype, void* stream);
+
 /* Simple GLA: one log-gate per (token, head) -- g [B,T,H] fp32 -- or a constant per-head
  * log-decay g_gamma [H] fp32; pass exactly one.  The state recurrence is GLA's with the
  * gate shared by all K channels.  Replaces tops.ops.simple_gla.chunk_simple_gla_fwd /

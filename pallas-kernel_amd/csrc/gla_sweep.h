@@ -77,8 +77,9 @@ bool gla_pipe_eligible(const SweepParams& p);
 template <bool REV>
 hipError_t launch_gla_pipe(const SweepParams& p, hipStream_t s);
 
-// Forward sweep with the gate on the value side (g = gv [B,T,H,V], bf16 inputs): see
-// gla_sweep.hip.
+// Sweep with the gate on the value side (g = gv [B,T,H,V], bf16 inputs), forward or (REV)
+// the state-gradient recurrence: see gla_sweep.hip.
+template <bool REV>
 hipError_t launch_gla_sweep_gv(const SweepParams& p, hipStream_t s);
 
 // State-only sweep: the end state s_fin of every sequence (from s0, usually zero) and the

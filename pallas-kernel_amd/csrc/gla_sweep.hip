@@ -87,7 +87,6 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
   constexpr bool SY = SIN || FWD_DELTA || GV;  // the Y plane carries a lo half (fp32 Y, v_new, Y~)
   constexpr bool XL = !GV;               // the X / Z planes carry a lo half (gated q / k)
   static_assert(!GV || (!DELTA && !ST && !GK && !SIN), "YG: the bf16 full sweeps only");
-  static_assert(YG != 1 || !REV, "YG = 1: forward only");
   constexpr int LQ = KP + 8, LT = C + 8, LH = KP + 8;
   constexpr int NHT = (KP / 16) * (BV / 16) / NW;  // state tiles per wave (4, 2, 1), one K block
   constexpr int ES = sizeof(TIn);
@@ -1041,11 +1040,12 @@ hipError_t launch_gla_sweep(const SweepParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <bool REV>
 hipError_t launch_gla_sweep_gv(const SweepParams& p, hipStream_t s) {
   const int kp = p.K <= 32 ? 32 : (p.K <= 64 ? 64 : 128);
   dim3 grid(p.NV * p.H * p.N);
 #define TOPS_SWEEP_GV(KPV) \
-  hipLaunchKernelGGL((gla_sweep_kernel<uint16_t, KPV, false, false, false, false, 1>), grid, dim3(512), 0, s, p)
+  hipLaunchKernelGGL((gla_sweep_kernel<uint16_t, KPV, REV, false, false, false, 1>), grid, dim3(512), 0, s, p)
   if (kp == 32) TOPS_SWEEP_GV(32);
   else if (kp == 64) TOPS_SWEEP_GV(64);
   else TOPS_SWEEP_GV(128);
@@ -1280,7 +1280,7 @@ static int gla_chunk_fwd_gv_impl(const void* q, const void* k, const void* v, co
     p.acc32 = o32;
     p.acc_mode = 1;
   }
-  hipError_t e = launch_gla_sweep_gv(p, (hipStream_t)stream);
+  hipError_t e = launch_gla_sweep_gv<false>(p, (hipStream_t)stream);
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   return TOPS_OK;
 }
@@ -1301,4 +1301,53 @@ extern "C" int tops_gla_chunk_fwd_gv32(const void* q, const void* k, const void*
   if (!o32) return tops_set_error(TOPS_ERR_NULL, "gla_chunk_fwd_gv32: null tensor");
   return gla_chunk_fwd_gv_impl(q, k, v, gv, h0, nullptr, o32, ht, cu_seqlens, B, T, H, K, V, N,
                                dtype, scale, stream);
+}
+
+// the shape checks of the chunked value-gate and reverse entries
+static int gv_shape_check(const char* who, int B, int T, int H, int K, int V, int N,
+                          const int32_t* cu_seqlens, int dtype) {
+  char msg[160];
+  if (dtype != TOPS_BF16) {
+    snprintf(msg, sizeof msg, "%s: dtype must be TOPS_BF16", who);
+    return tops_set_error(TOPS_ERR_DTYPE, msg);
+  }
+  if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || N <= 0 || K > 128 || (K % 8) || (V % 8) ||
+      (cu_seqlens && B != 1) || (!cu_seqlens && N != B) ||
+      (long long)kChunk * H * (K > V ? K : V) * 4 >= (1LL << 31)) {
+    snprintf(msg, sizeof msg, "%s: need positive sizes, K <= 128, K and V multiples of 8, "
+             "varlen with B == 1 (else N == B)", who);
+    return tops_set_error(TOPS_ERR_SHAPE, msg);
+  }
+  return TOPS_OK;
+}
+
+extern "C" int tops_gla_chunk_bwd_dv_gv32(const void* q, const void* k, const void* do_,
+                                          const float* gv, const float* dht, float* dv32,
+                                          float* dh0, const int32_t* cu_seqlens, int B, int T,
+                                          int H, int K, int V, int N, int dtype, float scale,
+                                          void* stream) {
+  if (!q || !k || !do_ || !gv || !dv32) return tops_set_error(TOPS_ERR_NULL, "gla_chunk_bwd_dv_gv32: null tensor");
+  int rc = gv_shape_check("gla_chunk_bwd_dv_gv32", B, T, H, K, V, N, cu_seqlens, dtype);
+  if (rc != TOPS_OK) return rc;
+  SweepParams p{q, k, gv, do_, dht, dv32, dh0, nullptr, cu_seqlens, nullptr,
+                B, T, H, K, V, N, (V + 63) / 64, scale, kGateGamma};
+  p.acc32 = dv32;
+  p.acc_mode = 1;
+  hipError_t e = launch_gla_sweep_gv<true>(p, (hipStream_t)stream);
+  if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
+  return TOPS_OK;
+}
+
+extern "C" int tops_gla_chunk_rev_dv(const void* q, const void* k, const float* g, const void* do_,
+                                     const float* dht, void* dv, float* dh0,
+                                     const int32_t* cu_seqlens, int B, int T, int H, int K, int V,
+                                     int N, int dtype, float scale, void* stream) {
+  if (!q || !k || !g || !do_ || !dv) return tops_set_error(TOPS_ERR_NULL, "gla_chunk_rev_dv: null tensor");
+  int rc = gv_shape_check("gla_chunk_rev_dv", B, T, H, K, V, N, cu_seqlens, dtype);
+  if (rc != TOPS_OK) return rc;
+  SweepParams p{q, k, g, do_, dht, dv, dh0, nullptr, cu_seqlens, nullptr,
+                B, T, H, K, V, N, (V + 63) / 64, scale, kGateK};
+  hipError_t e = launch_gla_sweep<uint16_t, true>(p, (hipStream_t)stream);
+  if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
+  return TOPS_OK;
 }

@@ -226,12 +226,6 @@ def gv_chunk_native(q, k, v, gv, initial_state, scale, output_final_state, cu_se
     return o, ht
 
 
-def _host_cu(cu_seqlens):
-    if cu_seqlens is None:
-        return None
-    return [int(x) for x in (cu_seqlens.tolist() if isinstance(cu_seqlens, torch.Tensor) else cu_seqlens)]
-
-
 def _gv_chunk_train_ok(q, v, gk, gv, reverse, cu_seqlens):
     """Whether a gv-only call with gradients runs on the chunk kernels (_GvChunk): bf16,
     K, V <= 128 and multiples of 8, and no sequence-parallel split of the sweeps it uses."""
@@ -245,22 +239,6 @@ def _gv_chunk_train_ok(q, v, gk, gv, reverse, cu_seqlens):
     return plan.segments(H, V) is None and plan.segments(H, K) is None
 
 
-def _seq_reverse_cumsum(x, T, cu):
-    """Suffix sums along time within every sequence of x [B, T, ...] (varlen: B == 1, cu
-    the host boundaries)."""
-    if cu is None:
-        return x.flip(1).cumsum(1).flip(1)
-    rev = time_reversal(T, cu, x.device)
-    xr = x.index_select(1, rev)                       # every sequence reversed in place
-    cs = xr.cumsum(1)
-    starts = torch.tensor(cu[:-1], device=x.device)
-    lens = torch.tensor([cu[i + 1] - cu[i] for i in range(len(cu) - 1)], device=x.device)
-    prev = cs.index_select(1, (starts - 1).clamp(min=0))
-    prev = prev * (starts > 0).to(x.dtype).view(1, -1, *([1] * (x.dim() - 2)))
-    cs = cs - prev.repeat_interleave(lens, dim=1)
-    return cs.index_select(1, rev)
-
-
 class _GvChunk(torch.autograd.Function):
     """fused_recurrent_gla with gv and without gk, forward and backward on chunk kernels
     (gradients of tops/ops/gla/fused_recurrent.py:496-619).  With S_t = S_(t-1) diag(a_t) +
@@ -268,15 +246,14 @@ class _GvChunk(torch.autograd.Function):
       * dq_t = scale S_t dO_t.  S^T follows the key-gated recurrence S^T_t = diag(a_t) S^T_(t-1)
         + v_t k_t^T, so dq is the key-gated chunk forward with queries dO, keys v, values k,
         gate gv and initial state h0^T;
-      * dk_t = dS_t v_t, dS^T_t = diag(a_(t+1)) dS^T_(t+1) + scale dO_t q_t^T: the reverse
-        chunk sweep (fused_recurrent's reverse=True recurrence) with queries v, keys dO, values
-        q, the gate of the next token (0 at a sequence's last), initial state dht^T / scale and
-        output scale; its final state gives dh0 = dS_1 diag(a_1);
-      * dv_t = dS_t^T k_t: in reversed time dS is a value-gated forward recurrence, so dv is the
-        value-gate forward on every sequence reversed, with queries k, keys q, values dO, the
-        shifted gate, initial state dht / scale (fp32 output);
+      * dk_t = dS_t v_t, dS^T_t = diag(a_(t+1)) dS^T_(t+1) + scale dO_t q_t^T: the state-gradient
+        sweep of the key-gated chunk backward (tops_gla_chunk_rev_dv) with queries dO, keys v,
+        output-gradient q and dht^T, whose dv is dk;
+      * dv_t = dS_t^T k_t and dh0 = dS_1 diag(a_1): the value-gated state-gradient sweep
+        (tops_gla_chunk_bwd_dv_gv32, dv in fp32);
       * dgv_t = sum over t' >= t of (o_t' dO_t' - v_t' dv_t') + sum_k (dht * ht)[k, :], the
-        per-column identity of the gated recurrence (o in fp32 from the forward)."""
+        per-column identity of the gated recurrence (o in fp32 from the forward), by
+        tops_gv_gate_grad."""
 
     @staticmethod
     def forward(ctx, q, k, v, gv, h0, scale, cu_seqlens):
@@ -304,48 +281,29 @@ class _GvChunk(torch.autograd.Function):
         V = v.shape[-1]
         dev = q.device
         plan = ChunkPlan(B, T, cu, dev)
-        cu_h = _host_cu(cu)
         do = do.contiguous().to(q.dtype)
         dht32 = None if dht is None else dht.to(torch.float32).contiguous()
         # dq: the key-gated forward on the transposed state
         h0t = None if h0 is None else h0.transpose(-1, -2).contiguous()
         dq, _ = chunk_gla(do, v, k, gv, scale=scale, initial_state=h0t, output_final_state=False,
                           cu_seqlens=cu)
-        # the gate of the next token, 0 at the last token of every sequence
-        gsh = torch.zeros_like(gv)
-        gsh[:, :-1] = gv[:, 1:]
-        if cu_h is not None:
-            gsh[0, torch.tensor(cu_h[1:], device=dev) - 1] = 0.0
-        # dk (and dh0): the reverse sweep on the transposed state gradient
-        s0 = None if dht32 is None else (dht32.transpose(-1, -2) / scale).contiguous()
-        r = reverse_chunk_native(v, do, q, "k", gsh, s0, scale, True, cu)
-        if r is None:
-            r = _reversed_chunk(lambda q_, k_, v_, g_, **kw: chunk_gla(q_, k_, v_, g_, **kw),
-                                v, do, q, gsh, cu, scale=scale, initial_state=s0,
-                                output_final_state=True)
-        dk, hts = r
-        dh0 = None
-        if h0 is not None:
-            first = gv[:, 0] if cu_h is None else gv[0, torch.tensor(cu_h[:-1], device=dev)]
-            dh0 = (scale * hts.transpose(-1, -2)) * torch.exp(first).unsqueeze(-2)
-        # dv: the value-gate forward in reversed time (fp32 output)
-        rev = time_reversal(T, cu, dev)
-        flip = (lambda x: x.index_select(1, rev).contiguous())
+        # dk: the key-gated state-gradient sweep on the transposed state gradient (its dv)
+        dk = torch.empty_like(q)
+        dht_t = None if dht32 is None else dht32.transpose(-1, -2).contiguous()   # [N, H, V, K]
+        N.call("tops_gla_chunk_rev_dv", N.ptr(do), N.ptr(v), N.ptr(gv), N.ptr(q), N.ptr(dht_t),
+               N.ptr(dk), None, N.ptr(plan.cu_dev), B, T, H, V, K, plan.N,
+               N.dtype_code(q.dtype), float(scale), N.stream())
+        # dv (fp32) and dh0: the value-gated state-gradient sweep
         dv32 = torch.empty(B, T, H, V, device=dev, dtype=torch.float32)
-        s0v = None if dht32 is None else (dht32 / scale).contiguous()
-        N.call("tops_gla_chunk_fwd_gv32", N.ptr(flip(k)), N.ptr(flip(q)), N.ptr(flip(do)),
-               N.ptr(flip(gsh)), N.ptr(s0v), N.ptr(dv32), None, N.ptr(plan.cu_dev), B, T, H, K, V,
-               plan.N, N.dtype_code(q.dtype), float(scale), N.stream())
-        dv32 = dv32.index_select(1, rev)
-        # dgv: suffix sums of o dO - v dv, plus the final state's term
-        dgv = _seq_reverse_cumsum(o32 * do.to(torch.float32) - v.to(torch.float32) * dv32, T, cu_h)
-        if dht32 is not None:
-            c = (dht32 * ht).sum(-2)                                   # [N, H, V]
-            if cu_h is None:
-                dgv = dgv + c.unsqueeze(1)
-            else:
-                lens = torch.tensor([cu_h[i + 1] - cu_h[i] for i in range(len(cu_h) - 1)], device=dev)
-                dgv = dgv + c.repeat_interleave(lens, dim=0).unsqueeze(0)
+        dh0 = None if h0 is None else torch.empty_like(h0)
+        N.call("tops_gla_chunk_bwd_dv_gv32", N.ptr(q), N.ptr(k), N.ptr(do), N.ptr(gv), N.ptr(dht32),
+               N.ptr(dv32), N.ptr(dh0), N.ptr(plan.cu_dev), B, T, H, K, V, plan.N,
+               N.dtype_code(q.dtype), float(scale), N.stream())
+        # dgv: suffix sums of o dO - v dv, plus the final state's term (tops_gv_gate_grad)
+        c = None if dht32 is None else (dht32 * ht).sum(-2).contiguous()      # [N, H, V]
+        dgv = torch.empty(B, T, H, V, device=dev, dtype=torch.float32)
+        N.call("tops_gv_gate_grad", N.ptr(o32), N.ptr(do), N.ptr(v), N.ptr(dv32), N.ptr(c),
+               N.ptr(dgv), N.ptr(plan.cu_dev), B, T, H, V, plan.N, N.dtype_code(q.dtype), N.stream())
         gdt, hdt = ctx.dtypes
         return (dq, dk, dv32.to(v.dtype), dgv.to(gdt), None if dh0 is None else dh0.to(hdt),
                 None, None)
