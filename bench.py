@@ -459,6 +459,18 @@ def _config2(dev, gen, iters, leg):
         sec_gv = _time(lambda: fused_recurrent_gla(q, k, v, None, gv=gk, initial_state=h0,
                                                    output_final_state=True), iters)
         o, ht = fused_recurrent_gla(q, k, v, gk, initial_state=h0, output_final_state=True)
+    # training with the gv gate (forward + backward on the chunk kernels; gk-only training is
+    # chunk_gla's step, the headline)
+    qg, kg, vg = (x.detach().clone().requires_grad_() for x in (q, k, v))
+    gvg, h0g = gk.detach().clone().requires_grad_(), h0.detach().clone().requires_grad_()
+    dog = torch.randn(B2, T2, H2, D2, device=dev, generator=gen).to(bf)
+
+    def gv_train():
+        og, _ = fused_recurrent_gla(qg, kg, vg, None, gv=gvg, initial_state=h0g,
+                                    output_final_state=True)
+        return torch.autograd.grad(og, (qg, kg, vg, gvg, h0g), dog)
+    sec_gvt = _time(gv_train, iters)
+    del qg, kg, vg, gvg, h0g, dog
     torch.cuda.synchronize()
     if leg is not None:
         hq, hk, hv, hg, hh0 = (_host(x) for x in (q, k, v, gk, h0))
@@ -474,7 +486,8 @@ def _config2(dev, gen, iters, leg):
             "tokens_per_s": round(B2 * T2 / sec, 1), "ms": round(sec * 1e3, 4),
             "algo_bytes": algo, "hbm_gbs": round(algo / sec / 1e9, 1), "hbm_frac": frac(sec),
             "reverse": {"ms": round(sec_rev * 1e3, 4), "hbm_frac": frac(sec_rev)},
-            "gv": {"ms": round(sec_gv * 1e3, 4), "hbm_frac": frac(sec_gv)}}
+            "gv": {"ms": round(sec_gv * 1e3, 4), "hbm_frac": frac(sec_gv)},
+            "gv_train_ms": round(sec_gvt * 1e3, 4)}
 
 
 def _config4(dev, gen, iters, leg):
