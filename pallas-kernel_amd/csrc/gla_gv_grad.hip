@@ -4,7 +4,7 @@
 //     dgv[t, v] = sum over t' >= t in the same sequence of (o[t', v] dO[t', v] - v[t', v] dv[t', v])
 //                 + c[n, v],
 // c[n] = sum_k (dht * ht)[n, k, :] the final-state term (or none).  One workgroup per
-// (sequence, head, 64-column tile): 8 token parts x 64 columns; each part first sums its own
+// (sequence, head, 64-column tile): 16 token parts x 64 columns; each part first sums its own
 // tokens, the parts' totals are combined through LDS, and a second walk writes the running
 // suffix sums.  HBM-bound: o and dv fp32, dO and v bf16 read twice, dgv written once.
 #include "tops_common.h"
@@ -14,7 +14,7 @@ namespace tops {
 
 namespace {
 
-constexpr int kCols = 64, kParts = 8;
+constexpr int kCols = 64, kParts = 16;
 
 __global__ __launch_bounds__(kCols * kParts) void gv_gate_grad_kernel(
     const float* o32, const uint16_t* dO, const uint16_t* v, const float* dv32, const float* c,
@@ -42,6 +42,7 @@ __global__ __launch_bounds__(kCols * kParts) void gv_gate_grad_kernel(
   };
   float s = 0.f;
   if (ok) {
+#pragma unroll 8
     for (int t = p1 - 1; t >= p0; --t) s += term(t);
   }
   __shared__ float tot[kParts][kCols];
@@ -50,6 +51,7 @@ __global__ __launch_bounds__(kCols * kParts) void gv_gate_grad_kernel(
   float run = (ok && c) ? c[((size_t)n * H + hh) * V + vv] : 0.f;
   for (int p = kParts - 1; p > part; --p) run += tot[p][col];
   if (ok) {
+#pragma unroll 8
     for (int t = p1 - 1; t >= p0; --t) {
       run += term(t);
       dgv[base + (size_t)t * rs] = run;
