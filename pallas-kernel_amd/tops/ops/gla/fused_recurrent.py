@@ -227,16 +227,15 @@ def gv_chunk_native(q, k, v, gv, initial_state, scale, output_final_state, cu_se
 
 
 def _gv_chunk_train_ok(q, v, gk, gv, reverse, cu_seqlens):
-    """Whether a gv-only call with gradients runs on the chunk kernels (_GvChunk): bf16,
-    K, V <= 128 and multiples of 8, and no sequence-parallel split of the sweeps it uses."""
+    """Whether a gv-only call with gradients runs on the chunk kernels (_GvChunk): bf16, K and
+    V <= 128 and multiples of 8.  Its value-gate and reverse sweeps take whole sequences (no
+    sequence-parallel split); for a few long sequences that leaves CUs idle, still far ahead
+    of the per-token kernels."""
     if gv is None or gk is not None or reverse or q.dtype != torch.bfloat16:
         return False
-    B, T, H, K = q.shape
+    K = q.shape[-1]
     V = v.shape[-1]
-    if K > 128 or V > 128 or K % 8 or V % 8:
-        return False
-    plan = ChunkPlan(B, T, cu_seqlens, q.device)
-    return plan.segments(H, V) is None and plan.segments(H, K) is None
+    return K <= 128 and V <= 128 and K % 8 == 0 and V % 8 == 0
 
 
 class _GvChunk(torch.autograd.Function):

@@ -4,7 +4,7 @@ forward for dq, the reverse chunk sweep for dk and dh0, the value-gate forward i
 time for dv, suffix sums for dgv) against the float64 oracle (tops/cpu/ops/gla/
 fused_recurrent.py restated), and a check that no per-token kernel ran.  Cases: fixed length
 with and without h0, varlen with a one-token sequence, K != V both ways, BASELINE config 2's
-K = V = 128 at reduced T.  Tolerance: bf16 2e-3 (relative L2) on o, ht and every gradient.
+K = V = 128 at reduced T, one long sequence.  Tolerance: bf16 2e-3 (relative L2) on o, ht and every gradient.
 """
 import numpy as np
 import pytest
@@ -22,6 +22,9 @@ CASES = [
     dict(B=1, T=150, H=2, K=64, V=32, h0=True, cu=[0, 1, 70, 150]),
     dict(B=2, T=256, H=2, K=128, V=128, h0=True),
     dict(B=1, T=333, H=3, K=48, V=96, h0=True, cu=[0, 129, 130, 333]),
+    # one long sequence on few heads (the chunk kernels' plan would split it; the gv sweeps
+    # take it whole)
+    dict(B=1, T=4096, H=1, K=64, V=64, h0=True),
 ]
 
 
