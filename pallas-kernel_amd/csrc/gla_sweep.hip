@@ -217,16 +217,22 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
 
   // ---- state tiles: tile i of this wave -> (msb, nn)
   f32x4 S[NHT];
+  // s0 / s_fin rows of this (sequence, head) through one buffer resource each: lane (l16, lg)
+  // of tile i holds rows 16 msb + 4 lg + r (K % 4 == 0: all four inside or none), column
+  // 16 nn + l16; no s0: an empty range loads zeros
+  const size_t s_base = (size_t)(n * H + hh) * LDK * V;
+  auto sel_off = [&](int i) {
+    const int kr = 16 * msb + 4 * lg;
+    const int vv = vt * BV + 16 * ((wave * NHT + i) % (BV / 16)) + l16;
+    return (kr < K && vv < V) ? ((uint32_t)kr * V + vv) * 4u : kOOB;
+  };
+  {
+    const rsrc_t Rs0 = make_rsrc(p.s0 ? p.s0 + s_base : nullptr, p.s0 ? (long long)LDK * V * 4 : 0);
 #pragma unroll
-  for (int i = 0; i < NHT; ++i) {
-    const int nn = (wave * NHT + i) % (BV / 16);
-    const int vv = vt * BV + 16 * nn + l16;
+    for (int i = 0; i < NHT; ++i) {
+      const uint32_t o = sel_off(i);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int kr = 16 * msb + 4 * lg + r;
-      float x = 0.f;
-      if (p.s0 && kr < K && vv < V) x = p.s0[((size_t)(n * H + hh) * LDK + kr) * V + vv];
-      S[i][r] = x;
+      for (int r = 0; r < 4; ++r) S[i][r] = __uint_as_float(bld32(Rs0, o, (uint32_t)(r * V * 4)));
     }
   }
   // reverse-time recurrence (gshift): the state entering the last token is h0 decayed by
@@ -968,15 +974,12 @@ __global__ __launch_bounds__(512) void gla_sweep_kernel(SweepParams p) {
     }
   }
   if (p.s_fin) {
+    const rsrc_t Rsf = make_rsrc(p.s_fin + s_base, (long long)LDK * V * 4);
 #pragma unroll
     for (int i = 0; i < NHT; ++i) {
-      const int nn = (wave * NHT + i) % (BV / 16);
-      const int vv = vt * BV + 16 * nn + l16;
+      const uint32_t o = sel_off(i);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int kr = 16 * msb + 4 * lg + r;
-        if (kr < K && vv < V) p.s_fin[((size_t)(n * H + hh) * LDK + kr) * V + vv] = S[i][r];
-      }
+      for (int r = 0; r < 4; ++r) bst32(Rsf, __float_as_uint(S[i][r]), o, (uint32_t)(r * V * 4));
     }
   }
 }
