@@ -116,7 +116,9 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lg = lane >> 4;
-  const int R = wave >> 1;
+  // output token block of the wave (the reverse sweep numbers its blocks from the end, so that
+  // in both directions a wave's first D tile lies in its output block for waves 0, 2, 4-7)
+  const int R = REV ? 3 - (wave >> 1) : (wave >> 1);
   const int nh = wave & 1;
   const int msb = (wave * NHT) / (BV / 16);
   const int wg = xcd_remap(blockIdx.x, gridDim.x, p.NV);
@@ -387,6 +389,10 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
     store_ckpt(c);
 
     // ---------------- D tiles of this chunk (shared through LDS), staging of the next
+    // the output block's X~ fragments: kept from the wave's first D tile when that tile lies in
+    // the output block (wave w: tile w, row block Rc(w) = w / 2 for w = 0, 2, 4..7)
+    bf16x8 fxh[KP / 32], fxl[KP / 32];
+    const bool xkeep = (wave == 0 || wave == 2 || wave >= 4);
     auto dtile = [&](int t) -> uint4 {
       const int Rc = t >= 6 ? 3 : (t >= 3 ? 2 : (t >= 1 ? 1 : 0));
       const int Pc = t - Rc * (Rc + 1) / 2;
@@ -398,6 +404,10 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
         const bf16x8 xh8 = PX.hi8(16 * Rt + l16, 32 * kc + 8 * lg);
         const bf16x8 zl8 = PZ.lo8(16 * Pt + l16, 32 * kc + 8 * lg);
         const bf16x8 xl8 = PX.lo8(16 * Rt + l16, 32 * kc + 8 * lg);
+        if (t == wave) {
+          fxh[kc] = xh8;
+          fxl[kc] = xl8;
+        }
         a0 = mfma(zl8, xh8, a0);
         a1 = mfma(zh8, xl8, a1);
         a2 = mfma(zh8, xh8, a2);
@@ -461,11 +471,12 @@ __global__ __launch_bounds__(512) void gla_pipe_kernel(SweepParams p) {
     clk.tick(4);
 
     // ---------------- output block: token block R, column tiles 2 nh, 2 nh + 1
-    bf16x8 fxh[KP / 32], fxl[KP / 32];
+    if (!xkeep) {
 #pragma unroll
-    for (int kc = 0; kc < KP / 32; ++kc) {
-      fxh[kc] = PX.hi8(16 * R + l16, 32 * kc + 8 * lg);
-      fxl[kc] = PX.lo8(16 * R + l16, 32 * kc + 8 * lg);
+      for (int kc = 0; kc < KP / 32; ++kc) {
+        fxh[kc] = PX.hi8(16 * R + l16, 32 * kc + 8 * lg);
+        fxl[kc] = PX.lo8(16 * R + l16, 32 * kc + 8 * lg);
+      }
     }
     uint2 dh[4], dl[4];
 #pragma unroll
