@@ -4,9 +4,12 @@
 //     dgv[t, v] = sum over t' >= t in the same sequence of (o[t', v] dO[t', v] - v[t', v] dv[t', v])
 //                 + c[n, v],
 // c[n] = sum_k (dht * ht)[n, k, :] the final-state term (or none).  One workgroup per
-// (sequence, head, 64-column tile): 16 token parts x 64 columns; each part first sums its own
-// tokens, the parts' totals are combined through LDS, and a second walk writes the running
-// suffix sums.  HBM-bound: o and dv fp32, dO and v bf16 read twice, dgv written once.
+// (sequence, head, 64-column tile) walks the sequence from its end in blocks of 16 runs x 8
+// tokens: each thread holds one run of one column in registers, forms the run's own suffix
+// sums, the 16 run totals are combined through LDS (double-buffered, one barrier per block)
+// and the carry from the later blocks is added.  The next block's inputs are fetched before
+// the current block is scanned.  Each input is read once and dgv written once: HBM-bound at
+// 16 bytes per (token, column) with o and dv fp32 and dO and v bf16.
 #include "tops_common.h"
 #include "tops_hip.h"
 
@@ -14,12 +17,12 @@ namespace tops {
 
 namespace {
 
-constexpr int kCols = 64, kParts = 16;
+constexpr int kCols = 64, kRuns = 16, kRun = 8, kBlock = kRuns * kRun;
 
-__global__ __launch_bounds__(kCols * kParts) void gv_gate_grad_kernel(
+__global__ __launch_bounds__(kCols * kRuns) void gv_gate_grad_kernel(
     const float* o32, const uint16_t* dO, const uint16_t* v, const float* dv32, const float* c,
     float* dgv, const int32_t* cu_seqlens, int T, int H, int V, int NVT) {
-  const int col = threadIdx.x % kCols, part = threadIdx.x / kCols;
+  const int col = threadIdx.x % kCols, run = threadIdx.x / kCols;
   const int vt = blockIdx.x % NVT, hh = (blockIdx.x / NVT) % H, n = blockIdx.x / (NVT * H);
   const int vv = vt * kCols + col;
   int t0, L;
@@ -30,32 +33,60 @@ __global__ __launch_bounds__(kCols * kParts) void gv_gate_grad_kernel(
     t0 = n * T;
     L = T;
   }
-  // this part's tokens [p0, p1) of the sequence
-  const int per = (L + kParts - 1) / kParts;
-  const int p0 = min(L, part * per), p1 = min(L, p0 + per);
   const bool ok = vv < V;
   const size_t rs = (size_t)H * V;                       // elements between tokens
   const size_t base = ((size_t)t0 * H + hh) * V + vv;
-  auto term = [&](int t) {
-    const size_t e = base + (size_t)t * rs;
-    return o32[e] * bf16_to_f32(dO[e]) - bf16_to_f32(v[e]) * dv32[e];
-  };
-  float s = 0.f;
-  if (ok) {
-#pragma unroll 8
-    for (int t = p1 - 1; t >= p0; --t) s += term(t);
-  }
-  __shared__ float tot[kParts][kCols];
-  tot[part][col] = s;
-  __syncthreads();
-  float run = (ok && c) ? c[((size_t)n * H + hh) * V + vv] : 0.f;
-  for (int p = kParts - 1; p > part; --p) run += tot[p][col];
-  if (ok) {
-#pragma unroll 8
-    for (int t = p1 - 1; t >= p0; --t) {
-      run += term(t);
-      dgv[base + (size_t)t * rs] = run;
+  // block b (counted from the sequence's end) holds tokens [L - (b + 1) kBlock, L - b kBlock);
+  // this thread's run of it starts at first(b); tokens before the sequence's start are zeros
+  auto first = [&](int b) { return L - (b + 1) * kBlock + run * kRun; };
+  float xo[kRun], xd[kRun];
+  uint16_t xg[kRun], xv[kRun];
+  auto fetch = [&](int b) {
+    const int tb = first(b);
+#pragma unroll
+    for (int j = 0; j < kRun; ++j) {
+      const int t = tb + j;
+      if (ok && t >= 0) {
+        const size_t e = base + (size_t)t * rs;
+        xo[j] = o32[e];
+        xd[j] = dv32[e];
+        xg[j] = dO[e];
+        xv[j] = v[e];
+      } else {
+        xo[j] = xd[j] = 0.f;
+        xg[j] = xv[j] = 0;
+      }
     }
+  };
+  __shared__ float tot[2][kRuns][kCols];
+  float carry = (ok && c) ? c[((size_t)n * H + hh) * V + vv] : 0.f;
+  const int nblk = (L + kBlock - 1) / kBlock;
+  fetch(0);
+  for (int b = 0; b < nblk; ++b) {
+    float s[kRun];
+#pragma unroll
+    for (int j = 0; j < kRun; ++j) s[j] = xo[j] * bf16_to_f32(xg[j]) - bf16_to_f32(xv[j]) * xd[j];
+    if (b + 1 < nblk) fetch(b + 1);
+#pragma unroll
+    for (int j = kRun - 2; j >= 0; --j) s[j] += s[j + 1];
+    float(*tt)[kCols] = tot[b & 1];
+    tt[run][col] = s[0];
+    __syncthreads();
+    // every thread of the column adds the run totals in the same order, so all of them carry
+    // the same value into the next block; off is the carry plus the totals of the later runs
+    float acc = carry, off = carry;
+#pragma unroll
+    for (int r = kRuns - 1; r >= 0; --r) {
+      if (r == run) off = acc;
+      acc += tt[r][col];
+    }
+    const int tb = first(b);
+    if (ok) {
+#pragma unroll
+      for (int j = 0; j < kRun; ++j)
+        if (tb + j >= 0) dgv[base + (size_t)(tb + j) * rs] = off + s[j];
+    }
+    carry = acc;
   }
 }
 
@@ -74,7 +105,7 @@ extern "C" int tops_gv_gate_grad(const float* o32, const void* dO, const void* v
   if (cu_seqlens && B != 1) return tops_set_error(TOPS_ERR_SHAPE, "gv_gate_grad: varlen needs B == 1");
   if (!cu_seqlens && N != B) return tops_set_error(TOPS_ERR_SHAPE, "gv_gate_grad: N must equal B");
   const int NVT = (V + kCols - 1) / kCols;
-  hipLaunchKernelGGL(gv_gate_grad_kernel, dim3(N * H * NVT), dim3(kCols * kParts), 0,
+  hipLaunchKernelGGL(gv_gate_grad_kernel, dim3(N * H * NVT), dim3(kCols * kRuns), 0,
                      (hipStream_t)stream, o32, (const uint16_t*)dO, (const uint16_t*)v, dv32, c,
                      dgv, cu_seqlens, T, H, V, NVT);
   const hipError_t e = hipGetLastError();
