@@ -166,10 +166,11 @@ def cpu_summary(res, threads):
             "configs": {k: {x: y for x, y in v.items() if x != "parity"} for k, v in res.items()}}
 
 
-def _time(fn, iters, warmup=2, settle_s=0.04):
+def _time(fn, iters, warmup=2, settle_s=0.2):
     """Mean wall time of iters calls, after untimed calls that settle the GPU clock (at least
     warmup of them, and at least settle_s of wall time: the clock ramps up over the first
-    ~30 ms of work after an idle period)."""
+    ~30 ms of busy work after an idle period, and calls of ~0.15 ms with host waits between
+    them keep it lower for longer)."""
     import torch
     fn()                       # the first call may load code objects and allocate
     torch.cuda.synchronize()
@@ -177,7 +178,7 @@ def _time(fn, iters, warmup=2, settle_s=0.04):
     while n < warmup or time.perf_counter() - t_s < settle_s:
         fn()
         n += 1
-        if n % 4 == 0:
+        if n % 16 == 0:
             torch.cuda.synchronize()
     torch.cuda.synchronize()
     t0 = time.perf_counter()

@@ -305,11 +305,12 @@ int tops_gla_chunk_rev_dv(const void* q, const void* k, const float* g, const vo
  * 171-358 keeps the same running suffix sums):
  *     dgv[t, v] = sum over t' >= t in t's sequence of (o32 dO - v dv32)[t', v] + c[n, v],
  * o32, dv32 [B,T,H,V] fp32; dO, v [B,T,H,V] bf16 (dtype TOPS_BF16); c [N,H,V] fp32 (the
- * final-state term sum_k dht * ht) or NULL; dgv [B,T,H,V] fp32.  Varlen: cu_seqlens [N+1],
+ * final-state term sum_k dht * ht) or NULL; dgv [B,T,H,V] fp32; dv_out [B,T,H,V] bf16 receives
+ * dv32 rounded to bf16 (the gradient handed back for v), or NULL.  Varlen: cu_seqlens [N+1],
  * B == 1. */
 int tops_gv_gate_grad(const float* o32, const void* dO, const void* v, const float* dv32,
-                      const float* c, float* dgv, const int32_t* cu_seqlens, int B, int T, int H,
-                      int V, int N, int dtype, void* stream);
+                      const float* c, float* dgv, void* dv_out, const int32_t* cu_seqlens, int B,
+                      int T, int H, int V, int N, int dtype, void* stream);
 
 /* Simple GLA: one log-gate per (token, head) -- g [B,T,H] fp32 -- or a constant per-head
  * log-decay g_gamma [H] fp32; pass exactly one.  The state recurrence is GLA's with the

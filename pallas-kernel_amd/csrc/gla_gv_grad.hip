@@ -9,7 +9,8 @@
 // sums, the 16 run totals are combined through LDS (double-buffered, one barrier per block)
 // and the carry from the later blocks is added.  The next block's inputs are fetched before
 // the current block is scanned.  Each input is read once and dgv written once: HBM-bound at
-// 16 bytes per (token, column) with o and dv fp32 and dO and v bf16.
+// 16 bytes per (token, column) with o and dv fp32 and dO and v bf16, 2 more when the bf16 copy
+// of dv is written on the way.
 #include "tops_common.h"
 #include "tops_hip.h"
 
@@ -21,7 +22,7 @@ constexpr int kCols = 64, kRuns = 16, kRun = 8, kBlock = kRuns * kRun;
 
 __global__ __launch_bounds__(kCols * kRuns) void gv_gate_grad_kernel(
     const float* o32, const uint16_t* dO, const uint16_t* v, const float* dv32, const float* c,
-    float* dgv, const int32_t* cu_seqlens, int T, int H, int V, int NVT) {
+    float* dgv, uint16_t* dv_out, const int32_t* cu_seqlens, int T, int H, int V, int NVT) {
   const int col = threadIdx.x % kCols, run = threadIdx.x / kCols;
   const int vt = blockIdx.x % NVT, hh = (blockIdx.x / NVT) % H, n = blockIdx.x / (NVT * H);
   const int vv = vt * kCols + col;
@@ -63,9 +64,15 @@ __global__ __launch_bounds__(kCols * kRuns) void gv_gate_grad_kernel(
   const int nblk = (L + kBlock - 1) / kBlock;
   fetch(0);
   for (int b = 0; b < nblk; ++b) {
+    const int tb = first(b);
     float s[kRun];
 #pragma unroll
     for (int j = 0; j < kRun; ++j) s[j] = xo[j] * bf16_to_f32(xg[j]) - bf16_to_f32(xv[j]) * xd[j];
+    if (dv_out && ok) {
+#pragma unroll
+      for (int j = 0; j < kRun; ++j)
+        if (tb + j >= 0) dv_out[base + (size_t)(tb + j) * rs] = f32_to_bf16(xd[j]);
+    }
     if (b + 1 < nblk) fetch(b + 1);
 #pragma unroll
     for (int j = kRun - 2; j >= 0; --j) s[j] += s[j + 1];
@@ -80,7 +87,6 @@ __global__ __launch_bounds__(kCols * kRuns) void gv_gate_grad_kernel(
       if (r == run) off = acc;
       acc += tt[r][col];
     }
-    const int tb = first(b);
     if (ok) {
 #pragma unroll
       for (int j = 0; j < kRun; ++j)
@@ -95,8 +101,9 @@ __global__ __launch_bounds__(kCols * kRuns) void gv_gate_grad_kernel(
 }  // namespace tops
 
 extern "C" int tops_gv_gate_grad(const float* o32, const void* dO, const void* v, const float* dv32,
-                                 const float* c, float* dgv, const int32_t* cu_seqlens, int B,
-                                 int T, int H, int V, int N, int dtype, void* stream) {
+                                 const float* c, float* dgv, void* dv_out,
+                                 const int32_t* cu_seqlens, int B, int T, int H, int V, int N,
+                                 int dtype, void* stream) {
   using namespace tops;
   if (!o32 || !dO || !v || !dv32 || !dgv) return tops_set_error(TOPS_ERR_NULL, "gv_gate_grad: null tensor");
   if (dtype != TOPS_BF16) return tops_set_error(TOPS_ERR_DTYPE, "gv_gate_grad: dO and v must be TOPS_BF16");
@@ -107,7 +114,7 @@ extern "C" int tops_gv_gate_grad(const float* o32, const void* dO, const void* v
   const int NVT = (V + kCols - 1) / kCols;
   hipLaunchKernelGGL(gv_gate_grad_kernel, dim3(N * H * NVT), dim3(kCols * kRuns), 0,
                      (hipStream_t)stream, o32, (const uint16_t*)dO, (const uint16_t*)v, dv32, c,
-                     dgv, cu_seqlens, T, H, V, NVT);
+                     dgv, (uint16_t*)dv_out, cu_seqlens, T, H, V, NVT);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
   return TOPS_OK;

@@ -73,7 +73,7 @@ SIGNATURES = {
                                  + [_i32] * 10 + [_f32, _vp],
     "tops_gla_chunk_fwd_gv": [_vp] * 8 + [_i32] * 7 + [_f32, _vp],
     "tops_gla_chunk_fwd_gv32": [_vp] * 8 + [_i32] * 7 + [_f32, _vp],
-    "tops_gv_gate_grad": [_vp] * 7 + [_i32] * 6 + [_vp],
+    "tops_gv_gate_grad": [_vp] * 8 + [_i32] * 6 + [_vp],
     "tops_gla_chunk_bwd_dv_gv32": [_vp] * 8 + [_i32] * 7 + [_f32, _vp],
     "tops_gla_chunk_rev_dv": [_vp] * 8 + [_i32] * 7 + [_f32, _vp],
     "tops_kda_stage_intra_fwd": [_vp] * 6 + [_i32] + [_vp] * 6 + [_i32] * 6 + [_f32, _vp],

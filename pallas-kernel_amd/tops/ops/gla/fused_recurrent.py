@@ -300,11 +300,14 @@ class _GvChunk(torch.autograd.Function):
                N.dtype_code(q.dtype), float(scale), N.stream())
         # dgv: suffix sums of o dO - v dv, plus the final state's term (tops_gv_gate_grad)
         c = None if dht32 is None else (dht32 * ht).sum(-2).contiguous()      # [N, H, V]
+        # and the bf16 dv, rounded from dv32 on the same walk
         dgv = torch.empty(B, T, H, V, device=dev, dtype=torch.float32)
+        dv = torch.empty(B, T, H, V, device=dev, dtype=v.dtype)
         N.call("tops_gv_gate_grad", N.ptr(o32), N.ptr(do), N.ptr(v), N.ptr(dv32), N.ptr(c),
-               N.ptr(dgv), N.ptr(plan.cu_dev), B, T, H, V, plan.N, N.dtype_code(q.dtype), N.stream())
+               N.ptr(dgv), N.ptr(dv), N.ptr(plan.cu_dev), B, T, H, V, plan.N,
+               N.dtype_code(q.dtype), N.stream())
         gdt, hdt = ctx.dtypes
-        return (dq, dk, dv32.to(v.dtype), dgv.to(gdt), None if dh0 is None else dh0.to(hdt),
+        return (dq, dk, dv, dgv.to(gdt), None if dh0 is None else dh0.to(hdt),
                 None, None)
 
 
