@@ -269,6 +269,9 @@ class _GvChunk(torch.autograd.Function):
         ctx.save_for_backward(q, k, v, gv32, h032, o32, ht)
         ctx.scale, ctx.cu = scale, cu_seqlens
         ctx.dtypes = (gv.dtype, None if h0 is None else h0.dtype)
+        # an unused output hands backward None instead of zeros: no final-state term to form
+        # when ht takes no part in the loss
+        ctx.set_materialize_grads(False)
         return o32.to(q.dtype), ht
 
     @staticmethod
@@ -280,6 +283,8 @@ class _GvChunk(torch.autograd.Function):
         V = v.shape[-1]
         dev = q.device
         plan = ChunkPlan(B, T, cu, dev)
+        if do is None:
+            do = torch.zeros(B, T, H, V, device=dev, dtype=q.dtype)
         do = do.contiguous().to(q.dtype)
         dht32 = None if dht is None else dht.to(torch.float32).contiguous()
         # dq: the key-gated forward on the transposed state

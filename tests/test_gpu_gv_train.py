@@ -71,3 +71,37 @@ def test_gv_training_on_chunk_kernels(cfg, cuda_device, monkeypatch):
     print(" ".join(f"{x}={e:.2e}" for x, e in errs.items()))
     for x, e in errs.items():
         assert e < tol(bf), (x, e)
+
+
+@pytest.mark.parametrize("used", ["o", "ht"])
+def test_gv_training_with_one_output_unused(used, cuda_device):
+    """A loss on o alone (backward gets no dht: no final-state term) or on ht alone (no dO):
+    the same gradients as the oracle's with the missing one zero."""
+    from tops.ops.gla import fused_recurrent_gla
+    B, T, H, K, V = 2, 200, 2, 64, 64
+    d = gla_inputs(B, T, H, K, V, seed=11, gate_div=4.0, h0=True, N=B, grads=True)
+    rng = np.random.default_rng(5)
+    gvn = (-np.abs(rng.standard_normal((B, T, H, V))) * 0.2).astype(np.float32)
+    bf = torch.bfloat16
+    q, k, v = (to_dev(d[x], bf, cuda_device).requires_grad_() for x in "qkv")
+    gv = to_dev(gvn, torch.float32, cuda_device).requires_grad_()
+    h0 = to_dev(d["h0"], torch.float32, cuda_device).requires_grad_()
+    o, ht = fused_recurrent_gla(q, k, v, None, gv, initial_state=h0, output_final_state=True)
+    if used == "o":
+        o.backward(to_dev(d["do"], bf, cuda_device))
+        do, dht = d["do"], np.zeros_like(d["dht"])
+    else:
+        ht.backward(to_dev(d["dht"], torch.float32, cuda_device))
+        do, dht = np.zeros_like(d["do"]), d["dht"]
+    torch.cuda.synchronize()
+    sq, sk, sv, sdo = (seen(x, bf) for x in (d["q"], d["k"], d["v"], do))
+    ro, _ = O.fused_recurrent_fwd(sq, sk, sv, None, gvn, initial_state=d["h0"],
+                                  output_final_state=True)
+    rq, rk, rv, _, rgv, rh0 = O.fused_recurrent_bwd(sq, sk, sv, None, gvn, ro, sdo, dht,
+                                                    initial_state=d["h0"])
+    got = dict(dq=q.grad, dk=k.grad, dv=v.grad, dgv=gv.grad, dh0=h0.grad)
+    ref = dict(dq=rq, dk=rk, dv=rv, dgv=rgv, dh0=rh0)
+    errs = {x: rel(host(got[x]), ref[x]) for x in got}
+    print(" ".join(f"{x}={e:.2e}" for x, e in errs.items()))
+    for x, e in errs.items():
+        assert e < tol(bf), (x, e)
