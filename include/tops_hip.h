@@ -269,14 +269,14 @@ int tops_gla_chunk_fwd_gv(const void* q, const void* k, const void* v, const flo
                           const float* h0, void* o, float* ht, const int32_t* cu_seqlens, int B,
                           int T, int H, int K, int V, int N, int dtype, float scale, void* stream);
 
-/* The same recurrence with o written in fp32 (o32 [B,T,H,V]) instead of bf16.  The chunked
- * backward of fused_recurrent_gla with gv (tops/ops/gla/fused_recurrent.py:496-619) uses it
- * twice: for the forward output, which the gate gradient needs in fp32, and, on time-reversed
- * inputs, for dv (the value-gated reverse recurrence of the state gradient, as a forward). */
+/* The same recurrence with o written in fp32 (o32 [B,T,H,V]) and, when o [B,T,H,V] bf16 is
+ * not NULL, in bf16 as well (both rounded from the same fp32 value).  The training forward of
+ * fused_recurrent_gla with gv (tops/ops/gla/fused_recurrent.py:496-619) takes both: the bf16
+ * output is returned, the fp32 one kept for the gate gradient of the backward. */
 int tops_gla_chunk_fwd_gv32(const void* q, const void* k, const void* v, const float* gv,
-                            const float* h0, float* o32, float* ht, const int32_t* cu_seqlens,
-                            int B, int T, int H, int K, int V, int N, int dtype, float scale,
-                            void* stream);
+                            const float* h0, float* o32, void* o, float* ht,
+                            const int32_t* cu_seqlens, int B, int T, int H, int K, int V, int N,
+                            int dtype, float scale, void* stream);
 
 /* The state-gradient sweep of the value-gated recurrence (the dv of fused_recurrent_gla's
  * backward with gv, tops/ops/gla/fused_recurrent.py:496-619): dS_t = dS_(t+1) diag(exp gv_(t+1))

@@ -1276,12 +1276,13 @@ static int gla_chunk_fwd_gv_impl(const void* q, const void* k, const void* v, co
   if (!cu_seqlens && N != B) return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd_gv: N must equal B");
   if ((long long)kChunk * H * (K > V ? K : V) * 4 >= (1LL << 31))
     return tops_set_error(TOPS_ERR_SHAPE, "gla_chunk_fwd_gv: H * max(K, V) too large for 32-bit chunk offsets");
-  SweepParams p{q, k, gv, v, h0, o32 ? (void*)o32 : o, ht, nullptr, cu_seqlens, nullptr,
+  SweepParams p{q, k, gv, v, h0, o ? o : (void*)o32, ht, nullptr, cu_seqlens, nullptr,
                 B, T, H, K, V, N, (V + 63) / 64, scale, kGateGamma};
   if (o32) {
-    // the output in fp32 only (acc_mode 1 writes the sum buffer and not the bf16 output)
+    // the output in fp32 (acc_mode 1 writes the sum buffer only), and in bf16 as well when o
+    // is given (acc_mode 4, both from the same accumulator)
     p.acc32 = o32;
-    p.acc_mode = 1;
+    p.acc_mode = o ? 4 : 1;
   }
   hipError_t e = launch_gla_sweep_gv<false>(p, (hipStream_t)stream);
   if (e != hipSuccess) return tops_set_error(TOPS_ERR_LAUNCH, hipGetErrorString(e));
@@ -1298,11 +1299,11 @@ extern "C" int tops_gla_chunk_fwd_gv(const void* q, const void* k, const void* v
 }
 
 extern "C" int tops_gla_chunk_fwd_gv32(const void* q, const void* k, const void* v, const float* gv,
-                                       const float* h0, float* o32, float* ht,
+                                       const float* h0, float* o32, void* o, float* ht,
                                        const int32_t* cu_seqlens, int B, int T, int H, int K,
                                        int V, int N, int dtype, float scale, void* stream) {
   if (!o32) return tops_set_error(TOPS_ERR_NULL, "gla_chunk_fwd_gv32: null tensor");
-  return gla_chunk_fwd_gv_impl(q, k, v, gv, h0, nullptr, o32, ht, cu_seqlens, B, T, H, K, V, N,
+  return gla_chunk_fwd_gv_impl(q, k, v, gv, h0, o, o32, ht, cu_seqlens, B, T, H, K, V, N,
                                dtype, scale, stream);
 }
 

@@ -448,23 +448,22 @@ __device__ __forceinline__ void put_n(const Plane& P, int r, int c, const float*
 
 // Four outputs of one channel slice of a sliced call, summed over the slices in fp32: mode 1
 // writes the sum buffer (Ra, byte offset fo), 2 adds into it, 3 writes the final value to the
-// output (Ro, offsets oo / so).
+// output (Ro, offsets oo / so); 4 (an unsliced call that wants both) writes the value to the
+// sum buffer and to the output.
 template <typename TIn>
 __device__ __forceinline__ void acc_slice_t(const rsrc_t& Ro, const rsrc_t& Ra, f32x4 acc,
                                             uint32_t fo, uint32_t oo, uint32_t so, int mode) {
-  if (mode >= 2) {
+  if (mode == 2 || mode == 3) {
     const uint4 prev = bld128(Ra, fo, 0);
     acc[0] += __uint_as_float(prev.x);
     acc[1] += __uint_as_float(prev.y);
     acc[2] += __uint_as_float(prev.z);
     acc[3] += __uint_as_float(prev.w);
   }
-  if (mode == 3) {
-    Words<TIn>::st4(Ro, acc, oo, so);
-  } else {
+  if (mode == 3 || mode == 4) Words<TIn>::st4(Ro, acc, oo, so);
+  if (mode != 3)
     bst128(Ra, make_uint4(__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]),
                           __float_as_uint(acc[3])), fo, 0);
-  }
 }
 
 // ---- fp16 state checkpoints (SweepParams::ckpt16).  A sweep workgroup holds the [K, 64]

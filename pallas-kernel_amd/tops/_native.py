@@ -72,7 +72,7 @@ SIGNATURES = {
     "tops_chunk_bwd_dqkg_slice": [_vp] * 4 + [_i32] + [_vp] * 8 + [_i32] * 2 + [_vp] * 3
                                  + [_i32] * 10 + [_f32, _vp],
     "tops_gla_chunk_fwd_gv": [_vp] * 8 + [_i32] * 7 + [_f32, _vp],
-    "tops_gla_chunk_fwd_gv32": [_vp] * 8 + [_i32] * 7 + [_f32, _vp],
+    "tops_gla_chunk_fwd_gv32": [_vp] * 9 + [_i32] * 7 + [_f32, _vp],
     "tops_gv_gate_grad": [_vp] * 8 + [_i32] * 6 + [_vp],
     "tops_gla_chunk_bwd_dv_gv32": [_vp] * 8 + [_i32] * 7 + [_f32, _vp],
     "tops_gla_chunk_rev_dv": [_vp] * 8 + [_i32] * 7 + [_f32, _vp],

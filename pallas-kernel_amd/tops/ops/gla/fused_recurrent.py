@@ -262,9 +262,10 @@ class _GvChunk(torch.autograd.Function):
         q, k, v = (x.contiguous() for x in (q, k, v))
         gv32, h032 = _f32(gv), _f32(h0)
         o32 = torch.empty(B, T, H, V, device=q.device, dtype=torch.float32)
+        o = torch.empty(B, T, H, V, device=q.device, dtype=q.dtype)
         ht = torch.empty(plan.N, H, K, V, device=q.device, dtype=torch.float32)
         N.call("tops_gla_chunk_fwd_gv32", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gv32), N.ptr(h032),
-               N.ptr(o32), N.ptr(ht), N.ptr(plan.cu_dev), B, T, H, K, V, plan.N,
+               N.ptr(o32), N.ptr(o), N.ptr(ht), N.ptr(plan.cu_dev), B, T, H, K, V, plan.N,
                N.dtype_code(q.dtype), float(scale), N.stream())
         ctx.save_for_backward(q, k, v, gv32, h032, o32, ht)
         ctx.scale, ctx.cu = scale, cu_seqlens
@@ -272,7 +273,7 @@ class _GvChunk(torch.autograd.Function):
         # an unused output hands backward None instead of zeros: no final-state term to form
         # when ht takes no part in the loss
         ctx.set_materialize_grads(False)
-        return o32.to(q.dtype), ht
+        return o, ht
 
     @staticmethod
     def backward(ctx, do, dht):

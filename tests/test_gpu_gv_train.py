@@ -1,10 +1,12 @@
 """fused_recurrent_gla with a value-side gate gv (no gk) and gradients, bf16: forward and
-backward on the chunk kernels (the value-gate forward with fp32 output, the key-gated chunk
-forward for dq, the reverse chunk sweep for dk and dh0, the value-gate forward in reversed
-time for dv, suffix sums for dgv) against the float64 oracle (tops/cpu/ops/gla/
-fused_recurrent.py restated), and a check that no per-token kernel ran.  Cases: fixed length
-with and without h0, varlen with a one-token sequence, K != V both ways, BASELINE config 2's
-K = V = 128 at reduced T, one long sequence.  Tolerance: bf16 2e-3 (relative L2) on o, ht and every gradient.
+backward on the chunk kernels (the value-gate forward with fp32 and bf16 output, the
+key-gated chunk forward on the transposed state for dq, the key-gated state-gradient sweep
+on the transposed problem for dk, the value-gated state-gradient sweep for dv and dh0,
+suffix sums for dgv) against the float64 oracle (tops/cpu/ops/gla/fused_recurrent.py
+restated), and a check that no per-token kernel ran.  Cases: fixed length with and without
+h0, varlen with a one-token sequence, K != V both ways, BASELINE config 2's K = V = 128 at
+reduced T, one long sequence, a loss on o alone and on ht alone.  Tolerance: bf16 2e-3
+(relative L2) on o, ht and every gradient; the forward's two outputs bitwise.
 """
 import numpy as np
 import pytest
@@ -105,3 +107,32 @@ def test_gv_training_with_one_output_unused(used, cuda_device):
     print(" ".join(f"{x}={e:.2e}" for x, e in errs.items()))
     for x, e in errs.items():
         assert e < tol(bf), (x, e)
+
+
+def test_gv32_forward_writes_the_bf16_output_from_the_same_sum(cuda_device):
+    """tops_gla_chunk_fwd_gv32 with the optional bf16 o: o32 is bitwise the same as without
+    it, and o is o32 rounded to bf16 (torch's round-to-nearest-even), on a varlen call whose
+    V is not a multiple of 64."""
+    from tops import _native as N
+    B, T, H, K, V = 1, 300, 2, 64, 72
+    cu = [0, 1, 130, 300]
+    d = gla_inputs(B, T, H, K, V, seed=23, gate_div=4.0, h0=True, N=3)
+    rng = np.random.default_rng(9)
+    gv = to_dev((-np.abs(rng.standard_normal((B, T, H, V))) * 0.2).astype(np.float32),
+                torch.float32, cuda_device)
+    q, k, v = (to_dev(d[x], torch.bfloat16, cuda_device) for x in "qkv")
+    h0 = to_dev(d["h0"], torch.float32, cuda_device)
+    cut = torch.tensor(cu, dtype=torch.int32, device=cuda_device)
+    outs = []
+    for with_o in (False, True):
+        o32 = torch.full((B, T, H, V), float("nan"), device=cuda_device)
+        o = torch.zeros(B, T, H, V, device=cuda_device, dtype=torch.bfloat16) if with_o else None
+        ht = torch.empty(3, H, K, V, device=cuda_device)
+        N.call("tops_gla_chunk_fwd_gv32", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gv), N.ptr(h0),
+               N.ptr(o32), N.ptr(o), N.ptr(ht), N.ptr(cut), B, T, H, K, V, 3,
+               N.dtype_code(torch.bfloat16), K ** -0.5, N.stream())
+        torch.cuda.synchronize()
+        outs.append((o32, o))
+    assert not outs[0][0].isnan().any()
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[1][1].view(torch.int16), outs[1][0].to(torch.bfloat16).view(torch.int16))
