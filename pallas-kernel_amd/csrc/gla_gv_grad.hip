@@ -8,9 +8,10 @@
 // tokens: each thread holds one run of one column in registers, forms the run's own suffix
 // sums, the 16 run totals are combined through LDS (double-buffered, one barrier per block)
 // and the carry from the later blocks is added.  The next block's inputs are fetched before
-// the current block is scanned.  Each input is read once and dgv written once: HBM-bound at
-// 16 bytes per (token, column) with o and dv fp32 and dO and v bf16, 2 more when the bf16 copy
-// of dv is written on the way.
+// the current block is scanned; loads and stores are non-temporal, as nothing is touched
+// twice (159 against 179 us at B16 T2048 H8 V128).  Each input is read once and dgv written
+// once: HBM-bound at 16 bytes per (token, column) with o and dv fp32 and dO and v bf16, 2
+// more when the bf16 copy of dv is written on the way.
 #include "tops_common.h"
 #include "tops_hip.h"
 
@@ -49,10 +50,10 @@ __global__ __launch_bounds__(kCols * kRuns) void gv_gate_grad_kernel(
       const int t = tb + j;
       if (ok && t >= 0) {
         const size_t e = base + (size_t)t * rs;
-        xo[j] = o32[e];
-        xd[j] = dv32[e];
-        xg[j] = dO[e];
-        xv[j] = v[e];
+        xo[j] = __builtin_nontemporal_load(o32 + e);
+        xd[j] = __builtin_nontemporal_load(dv32 + e);
+        xg[j] = __builtin_nontemporal_load(dO + e);
+        xv[j] = __builtin_nontemporal_load(v + e);
       } else {
         xo[j] = xd[j] = 0.f;
         xg[j] = xv[j] = 0;
@@ -71,7 +72,7 @@ __global__ __launch_bounds__(kCols * kRuns) void gv_gate_grad_kernel(
     if (dv_out && ok) {
 #pragma unroll
       for (int j = 0; j < kRun; ++j)
-        if (tb + j >= 0) dv_out[base + (size_t)(tb + j) * rs] = f32_to_bf16(xd[j]);
+        if (tb + j >= 0) __builtin_nontemporal_store(f32_to_bf16(xd[j]), dv_out + base + (size_t)(tb + j) * rs);
     }
     if (b + 1 < nblk) fetch(b + 1);
 #pragma unroll
@@ -90,7 +91,7 @@ __global__ __launch_bounds__(kCols * kRuns) void gv_gate_grad_kernel(
     if (ok) {
 #pragma unroll
       for (int j = 0; j < kRun; ++j)
-        if (tb + j >= 0) dgv[base + (size_t)(tb + j) * rs] = off + s[j];
+        if (tb + j >= 0) __builtin_nontemporal_store(off + s[j], dgv + base + (size_t)(tb + j) * rs);
     }
     carry = acc;
   }
